@@ -1,0 +1,246 @@
+"""Benchmark of the tbn float x binary path on one MI355X.
+
+A "step" is one float x binary GEMM at the headline shape M = N = K = 4096
+(fp32 activations ~ N(0,1) resident in HBM, +-1 weights pre-packed in the
+reference's BinaryMatrix layout, per-column fp32 scale ~ U[0.5, 1.5]).  The
+JSON line reports GFLOP/s-equivalent (2*M*N*K / t), the roofline of the GEMM
+kernel, the config-4 binary Conv2D time per batch of 64, and the reference's
+portable CPU path (restated in oracle/) timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+import argparse
+import json
+import os
+import pathlib
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "fast-arm-tbcnn_amd" / "python"))
+
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (the unit the kernel runs on)
+FP32_PEAK_TFLOPS = 157.3    # MI355X fp32 (the north_star's "relevant roofline")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_stream(fn, stream, steps, warmup, torch):
+    """Runs fn() warmup times, then times `steps` calls with HIP events on
+    the stream the kernels are launched on; returns ms per call."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def gemm_workload(torch, tbn_hip, M, N, K, seed):
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    A = torch.randn((M, K), generator=g, device=dev, dtype=torch.float32)
+    binw = (torch.rand((K, N), generator=g, device=dev) < 0.5).to(torch.uint8)
+    scale = torch.rand(N, generator=g, device=dev, dtype=torch.float32) + 0.5
+    K_pad, N_pad = tbn_hip.padded_dims(K, N)
+    packed = torch.empty(N_pad * K_pad // 8, dtype=torch.uint8, device=dev)
+    tbn_hip.call("tbn_hip_pack_binary", binw.data_ptr(), K, N, tbn_hip.LAYOUT_KN, K_pad, N_pad,
+                 packed.data_ptr(), None)
+    C = torch.empty((M, N), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+    return A, packed, K_pad, N_pad, scale, C
+
+
+def conv_workload(torch, tbn_hip, seed):
+    """Config 4: x[64,64,14,14] ~ N(0,1), W[128,64,3,3] +-1, per-channel scale,
+    bias ~ N(0, 0.01), stride 1, pad 1, ReLU."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    x = torch.randn((64, 64, 14, 14), generator=g, device=dev)
+    wb = (torch.rand((128, 64 * 9), generator=g, device=dev) < 0.5).to(torch.uint8)
+    scale = torch.rand(128, generator=g, device=dev) + 0.5
+    bias = torch.randn(128, generator=g, device=dev) * 0.01
+    K_pad, N_pad = tbn_hip.padded_dims(576, 128)
+    packed = torch.empty(N_pad * K_pad // 8, dtype=torch.uint8, device=dev)
+    tbn_hip.call("tbn_hip_pack_binary", wb.data_ptr(), 576, 128, tbn_hip.LAYOUT_NK, K_pad, N_pad,
+                 packed.data_ptr(), None)
+    y = torch.empty((64, 128, 14, 14), device=dev)
+    desc = tbn_hip.conv_desc(64, 64, 14, 14, 128, 3, 3, 1, 1, 1, 1)
+    torch.cuda.synchronize()
+    return x, packed, K_pad, N_pad, scale, bias, y, desc
+
+
+def cpu_baseline(M, N, K, budget_s):
+    """The reference's portable CPU path for qlinear_matmul_binary (ternarized
+    activations, BinaryMatrix re-pack, scalar popcount GemmEngine), restated in
+    oracle/tbn_oracle.c, one thread, on a bounded sample of the workload."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_api as orc
+
+    rng = np.random.default_rng(7)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    binw = (rng.random((K, N)) < 0.5).astype(np.uint8)
+    tiling = (128, 256, 256, 16, 8)  # the reference's fastest portable tiling (gemm.cpp:323-329)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while not times or (time.perf_counter() < t_end and len(times) < 5):
+        t0 = time.perf_counter()
+        rc, _ = orc.qlinear_matmul_binary_tbn(A, binw, 1.0, tiling)
+        times.append(time.perf_counter() - t0)
+        assert rc == 0, rc
+    best = min(times)
+    # the true fp32-activation reference loop (qlinear_matmul_binary_naive), on 64 rows
+    rows = 64
+    t0 = time.perf_counter()
+    orc.qlinear_matmul_binary_naive(A[:rows], binw, 1.0)
+    naive_s = time.perf_counter() - t0
+    cpu = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(2.0 * M * N * K / best / 1e9, 2),
+        "unit": "GFLOP/s-equiv",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"{M}x{K}x{N} qlinear_matmul_binary, mode TBN (reference portable path: pack_from_float, "
+                   f"BinaryMatrix::pack, scalar popcount GemmEngine, tiling 128/256/256/16/8), best of "
+                   f"{len(times)} runs, 1 thread, gcc -O3 -march=x86-64-v3, host {cpu}"),
+        "fp32_naive_gflops": round(2.0 * rows * N * K / naive_s / 1e9, 3),
+        "fp32_naive_sample": f"{rows}x{K}x{N} qlinear_matmul_binary_naive (true fp32 x binary), 1 thread",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a 1 GiB device copy (known bytes) for counter calibration")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the path has no multi-GPU component in this build "
+              "(batch/M sharding with replicated packed weights needs no exchange); run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import tbn_hip
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    tbn_hip.call("tbn_hip_device_check")
+    stream = torch.cuda.Stream()
+    sh = stream.cuda_stream
+
+    M = N = K = 4096
+    A, packed, K_pad, N_pad, scale, C = gemm_workload(torch, tbn_hip, M, N, K, seed=1)
+
+    def gemm_step():
+        tbn_hip.call("tbn_hip_gemm_f32_binary", A.data_ptr(), K, M, N, K, packed.data_ptr(), K_pad, N_pad,
+                     scale.data_ptr(), 1.0, 0, 0, C.data_ptr(), N, sh)
+
+    with torch.cuda.stream(stream):
+        ms = time_stream(gemm_step, stream, args.steps, args.warmup, torch)
+    flops = 2.0 * M * N * K
+    gflops = flops / (ms * 1e-3) / 1e9
+    log(f"gemm 4096^3 float x binary: {ms * 1e3:.1f} us/launch, {gflops / 1e3:.1f} TFLOP/s-equiv")
+
+    # config-4 binary conv, batch 64
+    x, cpk, cK_pad, cN_pad, cs, cb, y, desc = conv_workload(torch, tbn_hip, seed=2)
+
+    def conv_step():
+        tbn_hip.call("tbn_hip_conv2d_f32_binary", x.data_ptr(), desc, cpk.data_ptr(), cK_pad, cN_pad,
+                     cs.data_ptr(), 1.0, cb.data_ptr(), tbn_hip.EPI_RELU, y.data_ptr(), sh)
+
+    with torch.cuda.stream(stream):
+        conv_ms = time_stream(conv_step, stream, args.steps, args.warmup, torch)
+    conv_flops = 2.0 * 64 * 196 * 576 * 128
+    log(f"conv 64x64x14x14 -> 128, 3x3, batch 64: {conv_ms * 1e3:.1f} us/batch, "
+        f"{conv_flops / conv_ms / 1e9:.1f} TFLOP/s-equiv")
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 1 GiB device-to-device copies")
+
+    algo_bytes = 4.0 * M * K + K_pad * N_pad / 8 + 4.0 * N + 4.0 * M * N
+    achieved_tflops = flops / (ms * 1e-3) / 1e12
+    roofline = {
+        "bound": "mfma",
+        "achieved": round(achieved_tflops, 2),
+        "peak": BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved_tflops / BF16_PEAK_TFLOPS, 4),
+        "traffic": None,
+        "kernel": "mfma_tile_kernel<128x128, SplitMatrix, SignPacked<binary>, GemmEpi>",
+        "issued_bf16_frac": round(3.0 * achieved_tflops / BF16_PEAK_TFLOPS, 4),
+        "fp32_roofline_frac": round(achieved_tflops / FP32_PEAK_TFLOPS, 4),
+        "algorithmic_bytes": int(algo_bytes),
+        "hbm_gbs_algorithmic": round(algo_bytes / (ms * 1e-3) / 1e9, 1),
+    }
+    traffic_file = ROOT / "profiles" / "traffic.json"
+    if traffic_file.exists():
+        tr = json.loads(traffic_file.read_text()).get("gemm_f32_binary_4096")
+        if tr:
+            roofline["traffic"] = tr.get("bytes_per_launch")
+
+    result = {
+        "metric": "float×binary GEMM GFLOP/s-equiv @4096³; Conv2D 64→128 14×14 µs/batch",
+        "value": round(gflops, 1),
+        "unit": "GFLOP/s-equiv",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "strong",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (A ~ N(0,1), W +-1 p=0.5, scale ~ U[0.5,1.5]; generated on device, seeded)",
+        "config": {
+            "workload": "float x binary GEMM M=N=K=4096, fp32 activations, BinaryMatrix-packed +-1 weights, "
+                        "per-column fp32 scale (mode F32: exact products, fp32 accumulation)",
+            "M": M, "N": N, "K": K, "K_pad": K_pad, "N_pad": N_pad,
+            "conv_workload": "binary Conv2D 64x14x14 -> 128x14x14, 3x3, s1 p1, batch 64, per-channel scale, "
+                             "bias, ReLU (config 4)",
+        },
+        "conv_us_per_batch": round(conv_ms * 1e3, 2),
+        "conv_gflops_equiv": round(conv_flops / (conv_ms * 1e-3) / 1e9, 1),
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline ...")
+        result["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_budget)
+    else:
+        result["cpu_baseline"] = None
+    result["host"] = platform.node()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,38 @@
+// Shared host-side plumbing of libtbn_hip: error reporting, argument checks,
+// device validation and launch checking.  Device code lives in the .hip files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "tbn_hip.h"
+
+namespace tbn_hip {
+
+// Records `msg` as this thread's last error and returns `code`.
+int fail(int code, const std::string& msg);
+// Clears the thread's last error and returns TBN_SUCCESS.
+int ok();
+// Verifies the current device is a gfx950 (cached per device id).
+int ensure_device();
+// Maps the result of hipGetLastError() after a launch to a status.
+int check_launch(const char* what);
+
+inline hipStream_t stream_of(tbn_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace tbn_hip
+
+#define TBN_REQUIRE(cond, code, msg)                         \
+    do {                                                     \
+        if (!(cond)) return ::tbn_hip::fail((code), (msg));  \
+    } while (0)
+
+#define TBN_DEVICE_GUARD()                             \
+    do {                                               \
+        int _rc = ::tbn_hip::ensure_device();          \
+        if (_rc != TBN_SUCCESS) return _rc;            \
+    } while (0)

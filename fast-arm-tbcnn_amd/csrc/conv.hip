@@ -1,0 +1,336 @@
+// Implicit-GEMM Conv2D (north_star subsystem 3): the im2col matrix is never
+// materialised.  Each K step gathers the [positions x 32] slice of it from the
+// NCHW input straight into LDS (as three bf16 planes), so the convolution is
+// the same MFMA tile engine as the GEMM with
+//   MFMA rows    = output channels (packed +-1 / ternary weights, or fp32
+//                  weights for the unquantized layers), and
+//   MFMA columns = output positions (n, oh, ow),
+// which makes every result register row 32 consecutive output pixels of one
+// channel: coalesced NCHW stores.  With TBN_EPI_MAXPOOL2X2 the positions are
+// enumerated window by window (n, ph, pw, dy, dx), so the four pixels of a
+// 2x2 pooling window sit in four neighbouring lanes and are reduced with two
+// lane shuffles before one store; pixels outside the pooled area (odd last
+// row / column, floor mode) are never computed.
+//
+// Reference behaviour replaced: conv2d_binary (conv2d.cpp:220-316: im2col,
+// weight transpose, qlinear_matmul_binary, reshape, bias),
+// conv2d_binary_with_scales (conv2d.cpp:319-369), conv2d (conv2d.cpp:78-192)
+// and the Session's cached binary conv (model.hpp:414-559).
+#include <string>
+
+#include "common.hpp"
+#include "mfma_core.hpp"
+
+namespace {
+
+using namespace tbnk;
+
+struct ConvGeom {
+    int C, H, W;
+    int kh, kw, sh, sw, ph, pw, dh, dw;
+    int K;      // C * kh * kw
+    int Q;      // number of computed output positions
+    int OW, OHW;  // unpooled output plane
+    int pool;   // positions enumerated by 2x2 window
+    int PW, PHW;  // pooled output plane
+};
+
+// Decomposes a position index into (n, oh, ow) of the conv output.
+__device__ __forceinline__ void position_coords(const ConvGeom& g, int q, int& n, int& oh, int& ow) {
+    if (g.pool) {
+        const int per_image = g.PHW * 4;
+        n = q / per_image;
+        const int rem = q - n * per_image;
+        const int win = rem >> 2;
+        const int ph = win / g.PW;
+        const int pw = win - ph * g.PW;
+        oh = 2 * ph + ((rem >> 1) & 1);
+        ow = 2 * pw + (rem & 1);
+    } else {
+        n = q / g.OHW;
+        const int rem = q - n * g.OHW;
+        oh = rem / g.OW;
+        ow = rem - oh * g.OW;
+    }
+}
+
+// im2col column operand: row = output position, k = (c, r, s).  Work item =
+// (position, 4 consecutive k); consecutive threads take consecutive positions
+// so the gathered reads run along the image rows.
+template <int ROWS, int NT>
+struct Im2col {
+    static constexpr int PIECES = 3;
+    static constexpr int ITEMS = ROWS * (BK / 4);
+    static constexpr int PER_THREAD = (ITEMS + NT - 1) / NT;
+    const float* x;
+    ConvGeom g;
+    FastDiv div_khkw, div_kw;
+
+    struct Regs {
+        float v[PER_THREAD][4];
+        int64_t base[PER_THREAD];  // n*C*H*W, or -1 for positions past the end
+        int ih0[PER_THREAD], iw0[PER_THREAD];
+    };
+
+    __device__ __forceinline__ void init(Regs& rg, int c0, int tid) const {
+#pragma unroll
+        for (int it = 0; it < PER_THREAD; ++it) {
+            const int item = tid + it * NT;
+            const int q = c0 + item % ROWS;
+            rg.base[it] = -1;
+            rg.ih0[it] = 0;
+            rg.iw0[it] = 0;
+            if ((ITEMS % NT == 0 || item < ITEMS) && q < g.Q) {
+                int n, oh, ow;
+                position_coords(g, q, n, oh, ow);
+                rg.base[it] = static_cast<int64_t>(n) * g.C * g.H * g.W;
+                rg.ih0[it] = oh * g.sh - g.ph;
+                rg.iw0[it] = ow * g.sw - g.pw;
+            }
+        }
+    }
+
+    __device__ __forceinline__ void load(Regs& rg, int, int k0, int tid) const {
+#pragma unroll
+        for (int it = 0; it < PER_THREAD; ++it) {
+            const int item = tid + it * NT;
+            const int kc = item / ROWS;
+            float v[4] = {0.f, 0.f, 0.f, 0.f};
+            if (rg.base[it] >= 0) {
+                int k = k0 + kc * 4;
+                uint32_t c = div_khkw.div(static_cast<uint32_t>(k));
+                uint32_t rs = static_cast<uint32_t>(k) - c * div_khkw.d;
+                uint32_t r = div_kw.div(rs);
+                uint32_t s = rs - r * div_kw.d;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (k + e < g.K) {
+                        const int ih = rg.ih0[it] + static_cast<int>(r) * g.dh;
+                        const int iw = rg.iw0[it] + static_cast<int>(s) * g.dw;
+                        if (static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
+                            static_cast<unsigned>(iw) < static_cast<unsigned>(g.W))
+                            v[e] = x[rg.base[it] + (static_cast<int64_t>(c) * g.H + ih) * g.W + iw];
+                    }
+                    if (++s == div_kw.d) {
+                        s = 0;
+                        if (++r == static_cast<uint32_t>(g.kh)) { r = 0; ++c; }
+                    }
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) rg.v[it][e] = v[e];
+        }
+    }
+
+    __device__ __forceinline__ void store(const Regs& rg, uint16_t* lds, int tid) const {
+#pragma unroll
+        for (int it = 0; it < PER_THREAD; ++it) {
+            const int item = tid + it * NT;
+            if (ITEMS % NT == 0 || item < ITEMS) {
+                const int r = item % ROWS, kc = item / ROWS;
+                const Split4 s = split4(rg.v[it][0], rg.v[it][1], rg.v[it][2], rg.v[it][3]);
+                uint16_t* dst = lds + r * LDS_ROW + kc * 4;
+                *reinterpret_cast<uint2*>(dst) = make_uint2(s.hi[0], s.hi[1]);
+                *reinterpret_cast<uint2*>(dst + ROWS * LDS_ROW) = make_uint2(s.mid[0], s.mid[1]);
+                *reinterpret_cast<uint2*>(dst + 2 * ROWS * LDS_ROW) = make_uint2(s.lo[0], s.lo[1]);
+            }
+        }
+    }
+};
+
+// y[n, m, oh, ow] = relu?( acc*alpha*s[m] + b[m] ) (or (acc + b[m])*alpha*s[m]),
+// optionally max-pooled over 2x2 windows held by lanes 4t .. 4t+3.
+struct ConvEpi {
+    float* y;
+    int M;  // output channels
+    ConvGeom g;
+    const float* scale;
+    float alpha;
+    const float* bias;
+    int flags;
+
+    template <class Cfg>
+    __device__ __forceinline__ void apply(f32x16_t (&acc)[Cfg::FR][Cfg::FC], int row0, int col0,
+                                          int lane) const {
+        const bool pool = g.pool != 0;
+        const int plane = pool ? g.PHW : g.OHW;
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j) {
+            const int q = col0 + frag_out_col(j, lane);
+            const bool valid_q = q < g.Q;
+            int64_t out_base = 0;
+            if (valid_q) {
+                if (pool) {
+                    const int per_image = g.PHW * 4;
+                    const int n = q / per_image;
+                    const int win = (q - n * per_image) >> 2;
+                    out_base = static_cast<int64_t>(n) * M * plane + win;
+                } else {
+                    const int n = q / g.OHW;
+                    out_base = static_cast<int64_t>(n) * M * plane + (q - n * g.OHW);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int m = row0 + frag_out_row(i, e, lane);
+                    float v = acc[i][j][e];
+                    if (m < M) {
+                        const float mult = scale ? alpha * scale[m] : alpha;
+                        const float b = bias ? bias[m] : 0.0f;
+                        v = (flags & TBN_EPI_BIAS_THEN_SCALE) ? (v + b) * mult : v * mult + b;
+                        if (flags & TBN_EPI_RELU) v = v > 0.0f ? v : 0.0f;
+                    }
+                    if (pool) {
+                        v = fmaxf(v, __shfl_xor(v, 1));
+                        v = fmaxf(v, __shfl_xor(v, 2));
+                    }
+                    if (m < M && valid_q && (!pool || (lane & 3) == 0))
+                        y[out_base + static_cast<int64_t>(m) * plane] = v;
+                }
+        }
+    }
+};
+
+using CfgM128 = TileCfg<128, 64, 64, 32>;  // >= 128 output channels
+using CfgM64 = TileCfg<64, 64, 32, 32>;    // 33..64 output channels, or few positions
+using CfgM32 = TileCfg<32, 128, 32, 32>;   // <= 32 output channels
+
+template <class Cfg, class RowL>
+int launch_conv_impl(const RowL& rowl, const float* x, const ConvGeom& g, const ConvEpi& epi,
+                     hipStream_t stream, const char* what) {
+    Im2col<Cfg::BC, Cfg::NT> coll;
+    coll.x = x;
+    coll.g = g;
+    coll.div_khkw = make_fastdiv(static_cast<uint32_t>(g.kh * g.kw));
+    coll.div_kw = make_fastdiv(static_cast<uint32_t>(g.kw));
+    const int tiles_r = static_cast<int>(tbn_hip::ceil_div(epi.M, Cfg::BR));
+    const int tiles_c = static_cast<int>(tbn_hip::ceil_div(g.Q, Cfg::BC));
+    hipLaunchKernelGGL((mfma_tile_kernel<Cfg, RowL, Im2col<Cfg::BC, Cfg::NT>, ConvEpi>),
+                       dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, stream, rowl, coll, epi, g.K,
+                       tiles_r, tiles_c);
+    return tbn_hip::check_launch(what);
+}
+
+int make_geom(const tbn_conv2d_desc* d, int flags, ConvGeom& g) {
+    TBN_REQUIRE(d != nullptr, TBN_INVALID_ARGUMENT, "conv descriptor is null");
+    TBN_REQUIRE(d->n >= 0 && d->c > 0 && d->h > 0 && d->w > 0 && d->m > 0, TBN_INVALID_SHAPE,
+                "conv input/output dimensions must be positive");
+    TBN_REQUIRE(d->kh > 0 && d->kw > 0 && d->sh > 0 && d->sw > 0 && d->dh > 0 && d->dw > 0 &&
+                    d->ph >= 0 && d->pw >= 0,
+                TBN_INVALID_ARGUMENT, "invalid kernel/stride/padding/dilation");
+    const int64_t OH = (d->h + 2 * d->ph - d->dh * (d->kh - 1) - 1) / d->sh + 1;
+    const int64_t OW = (d->w + 2 * d->pw - d->dw * (d->kw - 1) - 1) / d->sw + 1;
+    TBN_REQUIRE(OH > 0 && OW > 0, TBN_INVALID_SHAPE,
+                "invalid output dimensions: " + std::to_string(OH) + "x" + std::to_string(OW));
+    const int64_t K = d->c * d->kh * d->kw;
+    const int64_t xsize = d->n * d->c * d->h * d->w;
+    TBN_REQUIRE(K * d->kh * d->kw < (1LL << 32) && xsize < (1LL << 40) && d->h < (1 << 30) &&
+                    d->w < (1 << 30),
+                TBN_INVALID_SHAPE, "convolution too large");
+    g.C = int(d->c); g.H = int(d->h); g.W = int(d->w);
+    g.kh = int(d->kh); g.kw = int(d->kw); g.sh = int(d->sh); g.sw = int(d->sw);
+    g.ph = int(d->ph); g.pw = int(d->pw); g.dh = int(d->dh); g.dw = int(d->dw);
+    g.K = int(K);
+    g.OW = int(OW);
+    g.OHW = int(OH * OW);
+    g.pool = (flags & TBN_EPI_MAXPOOL2X2) ? 1 : 0;
+    if (g.pool) {
+        const int64_t PH = OH / 2, PW = OW / 2;
+        TBN_REQUIRE(PH > 0 && PW > 0, TBN_INVALID_SHAPE, "2x2 max pool needs an output of at least 2x2");
+        g.PW = int(PW);
+        g.PHW = int(PH * PW);
+        TBN_REQUIRE(d->n * PH * PW * 4 < (1LL << 31), TBN_INVALID_SHAPE, "too many output positions");
+        g.Q = int(d->n * PH * PW * 4);
+    } else {
+        g.PW = 0;
+        g.PHW = 0;
+        TBN_REQUIRE(d->n * OH * OW < (1LL << 31), TBN_INVALID_SHAPE, "too many output positions");
+        g.Q = int(d->n * OH * OW);
+    }
+    return TBN_SUCCESS;
+}
+
+template <bool TERNARY>
+int conv_quant(const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed, int64_t K_pad,
+               int64_t N_pad, const float* scale, float alpha, const float* bias, int flags,
+               float* y, tbn_stream_t stream) {
+    const char* what = TERNARY ? "conv2d_f32_ternary" : "conv2d_f32_binary";
+    ConvGeom g;
+    int rc = make_geom(desc, flags, g);
+    if (rc) return rc;
+    TBN_REQUIRE((flags & ~(TBN_EPI_RELU | TBN_EPI_BIAS_THEN_SCALE | TBN_EPI_MAXPOOL2X2)) == 0,
+                TBN_INVALID_ARGUMENT, "unknown epilogue flags");
+    TBN_REQUIRE(K_pad >= g.K && K_pad % 32 == 0, TBN_INVALID_SHAPE,
+                "K_pad must be >= C*kh*kw and a multiple of 32");
+    TBN_REQUIRE(N_pad >= desc->m, TBN_INVALID_SHAPE, "N_pad must be >= output channels");
+    if (g.Q == 0) return tbn_hip::ok();
+    TBN_REQUIRE(x && packed && y, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    ConvEpi epi{y, int(desc->m), g, scale, alpha, bias, flags};
+    const int64_t col_bytes = TERNARY ? K_pad / 4 : K_pad / 8;
+    hipStream_t s = tbn_hip::stream_of(stream);
+    const int m = int(desc->m);
+    if (m <= 32) {
+        SignPacked<CfgM32::BR, CfgM32::NT, TERNARY> rowl{packed, col_bytes, int(N_pad)};
+        return launch_conv_impl<CfgM32>(rowl, x, g, epi, s, what);
+    }
+    const int64_t big_tiles = tbn_hip::ceil_div(m, 128) * tbn_hip::ceil_div(g.Q, 64);
+    if (m <= 64 || big_tiles < 256) {
+        SignPacked<CfgM64::BR, CfgM64::NT, TERNARY> rowl{packed, col_bytes, int(N_pad)};
+        return launch_conv_impl<CfgM64>(rowl, x, g, epi, s, what);
+    }
+    SignPacked<CfgM128::BR, CfgM128::NT, TERNARY> rowl{packed, col_bytes, int(N_pad)};
+    return launch_conv_impl<CfgM128>(rowl, x, g, epi, s, what);
+}
+
+}  // namespace
+
+extern "C" {
+
+int tbn_hip_conv2d_f32_binary(const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed,
+                              int64_t K_pad, int64_t N_pad, const float* scale, float alpha,
+                              const float* bias, int flags, float* y, tbn_stream_t stream) {
+    return conv_quant<false>(x, desc, packed, K_pad, N_pad, scale, alpha, bias, flags, y, stream);
+}
+
+int tbn_hip_conv2d_f32_ternary(const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed,
+                               int64_t K_pad, int64_t N_pad, const float* scale, float alpha,
+                               const float* bias, int flags, float* y, tbn_stream_t stream) {
+    return conv_quant<true>(x, desc, packed, K_pad, N_pad, scale, alpha, bias, flags, y, stream);
+}
+
+int tbn_hip_conv2d_f32(const float* x, const tbn_conv2d_desc* desc, const float* w,
+                       const float* bias, int flags, float* y, tbn_stream_t stream) {
+    ConvGeom g;
+    int rc = make_geom(desc, flags, g);
+    if (rc) return rc;
+    TBN_REQUIRE((flags & ~(TBN_EPI_RELU | TBN_EPI_MAXPOOL2X2)) == 0, TBN_INVALID_ARGUMENT,
+                "unsupported epilogue flags for conv2d_f32");
+    if (g.Q == 0) return tbn_hip::ok();
+    TBN_REQUIRE(x && w && y, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    ConvEpi epi{y, int(desc->m), g, nullptr, 1.0f, bias, flags};
+    hipStream_t s = tbn_hip::stream_of(stream);
+    const int m = int(desc->m);
+    auto make_rows = [&](auto& rowl) {
+        rowl.base = w;
+        rowl.s_row = g.K;
+        rowl.s_k = 1;
+        rowl.rows_valid = m;
+        rowl.K = g.K;
+        rowl.vec = (g.K % 4 == 0) && (reinterpret_cast<uintptr_t>(w) % 16 == 0);
+        rowl.row_fast = 0;
+    };
+    if (m <= 32) {
+        SplitMatrix<CfgM32::BR, CfgM32::NT> rowl;
+        make_rows(rowl);
+        return launch_conv_impl<CfgM32>(rowl, x, g, epi, s, "conv2d_f32");
+    }
+    SplitMatrix<CfgM64::BR, CfgM64::NT> rowl;
+    make_rows(rowl);
+    return launch_conv_impl<CfgM64>(rowl, x, g, epi, s, "conv2d_f32");
+}
+
+}  // extern "C"

@@ -1,0 +1,368 @@
+// Weight quantization and bit-packing kernels (north_star subsystem 1).
+//
+// Every kernel writes the reference's packed formats bit for bit:
+//   BinaryMatrix   column n = K_pad/8 bytes, bit (k&7) of byte k>>3, 1 = -1,
+//                  padding +1 (GeMM/05-final/GeMM.cpp:114-151)
+//   ternary 2-bit  00=-1, 01=0, 10=+1, 11 decodes to 0
+//                  (tbn-runtime/include/tbn/memory/packed_weights.hpp:35-71)
+// The packers work on 32-bit output words (32 binary or 16 ternary weights of
+// one column) so each thread issues one aligned store.  Weight packing runs
+// once per Session, so these kernels favour simple coalesced reads over
+// tiling.
+#include "common.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+
+inline int grid_for(int64_t work) {
+    const int64_t blocks = tbn_hip::ceil_div(work, kThreads);
+    return static_cast<int>(blocks < 16384 ? (blocks > 0 ? blocks : 1) : 16384);
+}
+
+// ---- elementwise quantizers ------------------------------------------------
+
+__global__ void quantize_binary_f32_kernel(const float* __restrict__ w, int64_t n, float thr,
+                                           uint8_t* __restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = (w[i] > thr) ? 1 : 0;
+}
+
+__global__ void quantize_binary_i8_kernel(const int8_t* __restrict__ w, int64_t n,
+                                          uint8_t* __restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = (w[i] > 0) ? 1 : 0;
+}
+
+__global__ void quantize_ternary_f32_kernel(const float* __restrict__ w, int64_t n, float lo,
+                                            float hi, int8_t* __restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float v = w[i];
+        out[i] = (v < lo) ? int8_t(-1) : ((v > hi) ? int8_t(1) : int8_t(0));
+    }
+}
+
+__global__ void sign_ge0_kernel(const float* __restrict__ w, int64_t n, uint8_t* __restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = (w[i] >= 0.0f) ? 1 : 0;
+}
+
+// One thread per channel, summing in the same sequential order as the
+// Session (model.hpp:388-394) so the scale is bit-identical.
+__global__ void channel_mean_abs_kernel(const float* __restrict__ w, int64_t channels,
+                                        int64_t per_channel, float* __restrict__ scale) {
+    const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (c >= channels) return;
+    const float* row = w + c * per_channel;
+    float acc = 0.0f;
+    for (int64_t i = 0; i < per_channel; ++i) acc += fabsf(row[i]);
+    scale[c] = acc / (float)per_channel;
+}
+
+// ---- BinaryMatrix packing ---------------------------------------------------
+
+// Source of the sign of weight (k, n): a BINARY byte tensor or fp32 weights
+// under one of the reference's sign rules.  Returns true when the weight is -1.
+struct BinaryBytes {
+    const uint8_t* p;
+    __device__ bool neg(int64_t idx) const { return p[idx] != 1; }
+};
+struct FloatGT {
+    const float* p;
+    float thr;
+    __device__ bool neg(int64_t idx) const { return !(p[idx] > thr); }
+};
+struct FloatGE0 {
+    const float* p;
+    __device__ bool neg(int64_t idx) const { return !(p[idx] >= 0.0f); }
+};
+
+// Word (n, wi) holds k = 32*wi .. 32*wi+31 of column n.  For layout KN the
+// thread index runs fastest over n so reads of W[k, :] coalesce; for NK it
+// runs fastest over wi so each thread reads 32 contiguous weights of row n.
+template <class Src>
+__global__ void pack_binary_kernel(Src src, int64_t K, int64_t N, int layout, int64_t K_pad,
+                                   int64_t N_pad, uint32_t* __restrict__ packed) {
+    const int64_t words_per_col = K_pad / 32;
+    const int64_t total = N_pad * words_per_col;
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        int64_t n, wi;
+        if (layout == TBN_LAYOUT_KN) { n = t % N_pad; wi = t / N_pad; }
+        else { wi = t % words_per_col; n = t / words_per_col; }
+        uint32_t word = 0;
+        if (n < N) {
+            const int64_t k0 = wi * 32;
+#pragma unroll 4
+            for (int j = 0; j < 32; ++j) {
+                const int64_t k = k0 + j;
+                if (k < K) {
+                    const int64_t idx = (layout == TBN_LAYOUT_KN) ? k * N + n : n * K + k;
+                    word |= (src.neg(idx) ? 1u : 0u) << j;
+                }
+            }
+        }
+        packed[n * words_per_col + wi] = word;
+    }
+}
+
+__global__ void unpack_binary_kernel(const uint8_t* __restrict__ packed, int64_t K, int64_t N,
+                                     int layout, int64_t K_pad, int8_t* __restrict__ out) {
+    const int64_t total = K * N;
+    const int64_t col_bytes = K_pad / 8;
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        int64_t k, n;
+        if (layout == TBN_LAYOUT_KN) { k = t / N; n = t % N; }
+        else { n = t / K; k = t % K; }
+        const uint32_t bit = (packed[n * col_bytes + (k >> 3)] >> (k & 7)) & 1u;
+        out[t] = bit ? int8_t(-1) : int8_t(1);
+    }
+}
+
+// ---- 2-bit ternary packing ---------------------------------------------------
+
+__device__ __forceinline__ uint32_t ternary_code(int8_t v) {
+    return (v == -1) ? 0u : ((v == 1) ? 2u : 1u);
+}
+
+__global__ void pack_ternary2_kernel(const int8_t* __restrict__ t, int64_t n,
+                                     uint8_t* __restrict__ packed) {
+    const int64_t bytes = (n + 3) / 4;
+    for (int64_t b = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; b < bytes;
+         b += (int64_t)gridDim.x * blockDim.x) {
+        uint32_t v = 0;  // a fresh TernaryPackedWeights buffer is zero (code 00)
+        for (int j = 0; j < 4; ++j) {
+            const int64_t i = b * 4 + j;
+            if (i < n) v |= ternary_code(t[i]) << (2 * j);
+        }
+        packed[b] = static_cast<uint8_t>(v);
+    }
+}
+
+__global__ void unpack_ternary2_kernel(const uint8_t* __restrict__ packed, int64_t n,
+                                       int8_t* __restrict__ out) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const uint32_t code = (packed[i >> 2] >> ((i & 3) * 2)) & 3u;
+        out[i] = (code == 0u) ? int8_t(-1) : ((code == 2u) ? int8_t(1) : int8_t(0));
+    }
+}
+
+struct TernaryBytes {
+    const int8_t* p;
+    __device__ uint32_t code(int64_t idx) const { return ternary_code(p[idx]); }
+};
+struct TernaryFloat {
+    const float* p;
+    float lo, hi;
+    __device__ uint32_t code(int64_t idx) const {
+        const float v = p[idx];
+        return (v < lo) ? 0u : ((v > hi) ? 2u : 1u);
+    }
+};
+
+// GEMM layout: flat 2-bit codes of W^T[N_pad, K_pad]; word (n, wi) holds
+// k = 16*wi .. 16*wi+15 of column n, padding encodes 0 (code 01).
+template <class Src>
+__global__ void pack_ternary_kernel(Src src, int64_t K, int64_t N, int layout, int64_t K_pad,
+                                    int64_t N_pad, uint32_t* __restrict__ packed) {
+    const int64_t words_per_col = K_pad / 16;
+    const int64_t total = N_pad * words_per_col;
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        int64_t n, wi;
+        if (layout == TBN_LAYOUT_KN) { n = t % N_pad; wi = t / N_pad; }
+        else { wi = t % words_per_col; n = t / words_per_col; }
+        uint32_t word = 0x55555555u;  // all zeros (code 01)
+        if (n < N) {
+            word = 0;
+            const int64_t k0 = wi * 16;
+#pragma unroll 4
+            for (int j = 0; j < 16; ++j) {
+                const int64_t k = k0 + j;
+                uint32_t c = 1u;
+                if (k < K) c = src.code((layout == TBN_LAYOUT_KN) ? k * N + n : n * K + k);
+                word |= c << (2 * j);
+            }
+        }
+        packed[n * words_per_col + wi] = word;
+    }
+}
+
+int check_pack_dims(int64_t K, int64_t N, int layout, int64_t K_pad, int64_t N_pad,
+                    int k_multiple) {
+    TBN_REQUIRE(K >= 0 && N >= 0, TBN_INVALID_SHAPE, "K and N must be non-negative");
+    TBN_REQUIRE(layout == TBN_LAYOUT_KN || layout == TBN_LAYOUT_NK, TBN_INVALID_ARGUMENT,
+                "layout must be TBN_LAYOUT_KN or TBN_LAYOUT_NK");
+    TBN_REQUIRE(K_pad >= K && N_pad >= N, TBN_INVALID_SHAPE, "K_pad/N_pad smaller than K/N");
+    TBN_REQUIRE(K_pad % k_multiple == 0, TBN_INVALID_SHAPE,
+                "K_pad must be a multiple of " + std::to_string(k_multiple));
+    return TBN_SUCCESS;
+}
+
+}  // namespace
+
+using tbn_hip::check_launch;
+using tbn_hip::stream_of;
+
+extern "C" {
+
+int tbn_hip_quantize_to_binary_f32(const float* w, int64_t n, float threshold, uint8_t* out,
+                                   tbn_stream_t stream) {
+    TBN_REQUIRE(n >= 0, TBN_INVALID_SHAPE, "n must be non-negative");
+    TBN_REQUIRE(n == 0 || (w && out), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    if (n == 0) return tbn_hip::ok();
+    hipLaunchKernelGGL(quantize_binary_f32_kernel, dim3(grid_for(n)), dim3(kThreads), 0,
+                       stream_of(stream), w, n, threshold, out);
+    return check_launch("quantize_to_binary_f32");
+}
+
+int tbn_hip_quantize_to_binary_i8(const int8_t* w, int64_t n, uint8_t* out, tbn_stream_t stream) {
+    TBN_REQUIRE(n >= 0, TBN_INVALID_SHAPE, "n must be non-negative");
+    TBN_REQUIRE(n == 0 || (w && out), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    if (n == 0) return tbn_hip::ok();
+    hipLaunchKernelGGL(quantize_binary_i8_kernel, dim3(grid_for(n)), dim3(kThreads), 0,
+                       stream_of(stream), w, n, out);
+    return check_launch("quantize_to_binary_i8");
+}
+
+int tbn_hip_quantize_to_ternary_f32(const float* w, int64_t n, float lo, float hi, int8_t* out,
+                                    tbn_stream_t stream) {
+    TBN_REQUIRE(n >= 0, TBN_INVALID_SHAPE, "n must be non-negative");
+    TBN_REQUIRE(n == 0 || (w && out), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    if (n == 0) return tbn_hip::ok();
+    hipLaunchKernelGGL(quantize_ternary_f32_kernel, dim3(grid_for(n)), dim3(kThreads), 0,
+                       stream_of(stream), w, n, lo, hi, out);
+    return check_launch("quantize_to_ternary_f32");
+}
+
+int tbn_hip_sign_ge0_f32(const float* w, int64_t n, uint8_t* out, tbn_stream_t stream) {
+    TBN_REQUIRE(n >= 0, TBN_INVALID_SHAPE, "n must be non-negative");
+    TBN_REQUIRE(n == 0 || (w && out), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    if (n == 0) return tbn_hip::ok();
+    hipLaunchKernelGGL(sign_ge0_kernel, dim3(grid_for(n)), dim3(kThreads), 0, stream_of(stream),
+                       w, n, out);
+    return check_launch("sign_ge0_f32");
+}
+
+int tbn_hip_channel_mean_abs(const float* w, int64_t channels, int64_t per_channel, float* scale,
+                             tbn_stream_t stream) {
+    TBN_REQUIRE(channels >= 0 && per_channel > 0, TBN_INVALID_SHAPE,
+                "channels must be >= 0 and per_channel > 0");
+    TBN_REQUIRE(channels == 0 || (w && scale), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    if (channels == 0) return tbn_hip::ok();
+    hipLaunchKernelGGL(channel_mean_abs_kernel, dim3(tbn_hip::ceil_div(channels, 64)), dim3(64),
+                       0, stream_of(stream), w, channels, per_channel, scale);
+    return check_launch("channel_mean_abs");
+}
+
+int tbn_hip_pack_binary(const uint8_t* bin, int64_t K, int64_t N, int layout, int64_t K_pad,
+                        int64_t N_pad, uint8_t* packed, tbn_stream_t stream) {
+    int rc = check_pack_dims(K, N, layout, K_pad, N_pad, 64);
+    if (rc) return rc;
+    TBN_REQUIRE(N_pad % 8 == 0, TBN_INVALID_SHAPE, "N_pad must be a multiple of 8");
+    TBN_REQUIRE(packed && (K * N == 0 || bin), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    const int64_t words = N_pad * (K_pad / 32);
+    if (words == 0) return tbn_hip::ok();
+    hipLaunchKernelGGL(pack_binary_kernel<BinaryBytes>, dim3(grid_for(words)), dim3(kThreads), 0,
+                       stream_of(stream), BinaryBytes{bin}, K, N, layout, K_pad, N_pad,
+                       reinterpret_cast<uint32_t*>(packed));
+    return check_launch("pack_binary");
+}
+
+int tbn_hip_quantize_pack_binary_f32(const float* w, int64_t K, int64_t N, int layout,
+                                     int sign_rule, float threshold, int64_t K_pad,
+                                     int64_t N_pad, uint8_t* packed, tbn_stream_t stream) {
+    int rc = check_pack_dims(K, N, layout, K_pad, N_pad, 64);
+    if (rc) return rc;
+    TBN_REQUIRE(N_pad % 8 == 0, TBN_INVALID_SHAPE, "N_pad must be a multiple of 8");
+    TBN_REQUIRE(sign_rule == TBN_SIGN_GT_THRESHOLD || sign_rule == TBN_SIGN_GE_ZERO,
+                TBN_INVALID_ARGUMENT, "unknown sign rule");
+    TBN_REQUIRE(packed && (K * N == 0 || w), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    const int64_t words = N_pad * (K_pad / 32);
+    if (words == 0) return tbn_hip::ok();
+    uint32_t* out = reinterpret_cast<uint32_t*>(packed);
+    if (sign_rule == TBN_SIGN_GT_THRESHOLD)
+        hipLaunchKernelGGL(pack_binary_kernel<FloatGT>, dim3(grid_for(words)), dim3(kThreads), 0,
+                           stream_of(stream), FloatGT{w, threshold}, K, N, layout, K_pad, N_pad,
+                           out);
+    else
+        hipLaunchKernelGGL(pack_binary_kernel<FloatGE0>, dim3(grid_for(words)), dim3(kThreads), 0,
+                           stream_of(stream), FloatGE0{w}, K, N, layout, K_pad, N_pad, out);
+    return check_launch("quantize_pack_binary_f32");
+}
+
+int tbn_hip_unpack_binary(const uint8_t* packed, int64_t K, int64_t N, int layout, int64_t K_pad,
+                          int8_t* out, tbn_stream_t stream) {
+    int rc = check_pack_dims(K, N, layout, K_pad, N, 8);
+    if (rc) return rc;
+    TBN_REQUIRE(K * N == 0 || (packed && out), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    if (K * N == 0) return tbn_hip::ok();
+    hipLaunchKernelGGL(unpack_binary_kernel, dim3(grid_for(K * N)), dim3(kThreads), 0,
+                       stream_of(stream), packed, K, N, layout, K_pad, out);
+    return check_launch("unpack_binary");
+}
+
+int tbn_hip_pack_ternary2(const int8_t* t, int64_t n, uint8_t* packed, tbn_stream_t stream) {
+    TBN_REQUIRE(n >= 0, TBN_INVALID_SHAPE, "n must be non-negative");
+    TBN_REQUIRE(n == 0 || (t && packed), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    if (n == 0) return tbn_hip::ok();
+    hipLaunchKernelGGL(pack_ternary2_kernel, dim3(grid_for((n + 3) / 4)), dim3(kThreads), 0,
+                       stream_of(stream), t, n, packed);
+    return check_launch("pack_ternary2");
+}
+
+int tbn_hip_unpack_ternary2(const uint8_t* packed, int64_t n, int8_t* out, tbn_stream_t stream) {
+    TBN_REQUIRE(n >= 0, TBN_INVALID_SHAPE, "n must be non-negative");
+    TBN_REQUIRE(n == 0 || (packed && out), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    if (n == 0) return tbn_hip::ok();
+    hipLaunchKernelGGL(unpack_ternary2_kernel, dim3(grid_for(n)), dim3(kThreads), 0,
+                       stream_of(stream), packed, n, out);
+    return check_launch("unpack_ternary2");
+}
+
+int tbn_hip_pack_ternary(const int8_t* t, int64_t K, int64_t N, int layout, int64_t K_pad,
+                         int64_t N_pad, uint8_t* packed, tbn_stream_t stream) {
+    int rc = check_pack_dims(K, N, layout, K_pad, N_pad, 32);
+    if (rc) return rc;
+    TBN_REQUIRE(packed && (K * N == 0 || t), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    const int64_t words = N_pad * (K_pad / 16);
+    if (words == 0) return tbn_hip::ok();
+    hipLaunchKernelGGL(pack_ternary_kernel<TernaryBytes>, dim3(grid_for(words)), dim3(kThreads),
+                       0, stream_of(stream), TernaryBytes{t}, K, N, layout, K_pad, N_pad,
+                       reinterpret_cast<uint32_t*>(packed));
+    return check_launch("pack_ternary");
+}
+
+int tbn_hip_quantize_pack_ternary_f32(const float* w, int64_t K, int64_t N, int layout, float lo,
+                                      float hi, int64_t K_pad, int64_t N_pad, uint8_t* packed,
+                                      tbn_stream_t stream) {
+    int rc = check_pack_dims(K, N, layout, K_pad, N_pad, 32);
+    if (rc) return rc;
+    TBN_REQUIRE(packed && (K * N == 0 || w), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    const int64_t words = N_pad * (K_pad / 16);
+    if (words == 0) return tbn_hip::ok();
+    hipLaunchKernelGGL(pack_ternary_kernel<TernaryFloat>, dim3(grid_for(words)), dim3(kThreads),
+                       0, stream_of(stream), TernaryFloat{w, lo, hi}, K, N, layout, K_pad, N_pad,
+                       reinterpret_cast<uint32_t*>(packed));
+    return check_launch("quantize_pack_ternary_f32");
+}
+
+}  // extern "C"

@@ -1,0 +1,239 @@
+/*
+ * tbn_hip.h -- C ABI of the MI355X (gfx950) quantized compute path of tbn.
+ *
+ * This is the drop-in boundary: plain pointers and sizes, int status codes,
+ * one explicit HIP stream per call.  Every tensor pointer is a DEVICE pointer
+ * (HBM); the library never copies through the host.  All calls are
+ * asynchronous on `stream` (NULL = the default stream) unless stated.
+ *
+ * Status codes are the values of tbn::ErrorCode
+ * (tbn-runtime/include/tbn/utils/errors.hpp:10-22).  On failure the message
+ * of the most recent error on the calling thread is available from
+ * tbn_hip_last_error().  Argument errors are detected on the host before any
+ * work is queued.
+ *
+ * Packed formats (bit-exact with the reference):
+ *   BINARY tensor      1 byte per weight, byte 1 = +1, any other byte = -1
+ *                      (tbn-runtime/include/tbn/runtime/types.hpp:86-87;
+ *                       tbn-runtime/src/operators/quantized_gemm_neon.cpp:205).
+ *   BinaryMatrix       weight matrix W[K,N] packed column by column: column n
+ *                      occupies K_pad/8 bytes at packed + n*K_pad/8, the value
+ *                      at row k is bit (k&7) of byte (k>>3), bit 1 = -1, and
+ *                      padding rows/columns are +1 (bit 0)
+ *                      (GeMM/05-final/GeMM.cpp:114-151).  The runtime pads
+ *                      K_pad = ceil128(K), N_pad = ceil8(N)
+ *                      (tbn-runtime/src/operators/quantized_gemm_neon.cpp:38-58).
+ *   Ternary 2-bit      flat element i -> byte i>>2, bits (i&3)*2..+1,
+ *                      00 = -1, 01 = 0, 10 = +1, 11 decodes to 0
+ *                      (tbn-runtime/include/tbn/memory/packed_weights.hpp:35-71).
+ *                      For the GEMM/conv kernels the 2-bit codes are applied
+ *                      to the transposed zero-padded matrix W^T[N_pad, K_pad],
+ *                      so column n occupies K_pad/4 bytes at packed + n*K_pad/4.
+ *
+ * Arithmetic ("mode F32"): activations stay fp32, weights are the exact
+ * values +-1 (or 0) times an fp32 scale, accumulation is fp32.  Every product
+ * a*w is formed exactly (a is split into three bf16 parts whose sum is a, and
+ * each part is multiplied by the +-1/0 weight on the bf16 matrix cores);
+ * only the accumulation order differs from a sequential fp32 loop.
+ */
+#ifndef TBN_HIP_H
+#define TBN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* tbn::ErrorCode values (tbn-runtime/include/tbn/utils/errors.hpp:10-22). */
+enum tbn_status {
+    TBN_SUCCESS = 0,
+    TBN_INVALID_ARGUMENT = -1,
+    TBN_OUT_OF_MEMORY = -2,
+    TBN_NOT_IMPLEMENTED = -3,
+    TBN_INVALID_MODEL = -4,
+    TBN_RUNTIME_ERROR = -5,
+    TBN_QUANTIZATION_ERROR = -6,
+    TBN_INVALID_SHAPE = -7,
+    TBN_DEVICE_NOT_SUPPORTED = -8,
+    TBN_ONNX_PARSE_ERROR = -9,
+    TBN_OPERATOR_NOT_SUPPORTED = -10
+};
+
+typedef void* tbn_stream_t; /* a hipStream_t */
+
+/* Row-major layout of a weight matrix handed to the packers:
+ *   TBN_LAYOUT_KN  W[K,N]  (qlinear_matmul_binary's B, Gemm's B with transB=0)
+ *   TBN_LAYOUT_NK  W[N,K]  (Conv weights [M_out, C, kh, kw] seen as [M_out, C*kh*kw]) */
+enum tbn_layout { TBN_LAYOUT_KN = 0, TBN_LAYOUT_NK = 1 };
+
+/* Float -> binary sign rules (the reference uses both):
+ *   TBN_SIGN_GT_THRESHOLD  +1 iff w > threshold; 0, -0.0, NaN -> -1
+ *                          (quantize_to_binary, quantized_gemm_neon.cpp:553)
+ *   TBN_SIGN_GE_ZERO       +1 iff w >= 0; 0, -0.0 -> +1, NaN -> -1
+ *                          (Session sign extraction, model.hpp:433,803) */
+enum tbn_sign_rule { TBN_SIGN_GT_THRESHOLD = 0, TBN_SIGN_GE_ZERO = 1 };
+
+/* Epilogue flags for the GEMM / conv entry points. */
+enum tbn_epilogue {
+    TBN_EPI_NONE = 0,
+    TBN_EPI_RELU = 1,            /* y = max(y, 0) after scale and bias        */
+    TBN_EPI_BIAS_THEN_SCALE = 2, /* y = (acc + b) * s  (Session cached conv,  */
+                                 /*  model.hpp:523-557); default y = acc*s + b */
+                                 /*  (conv2d_binary_with_scales, conv2d.cpp:319-369) */
+    TBN_EPI_MAXPOOL2X2 = 4       /* conv only: fused 2x2 stride-2 max pool      */
+};
+
+/* Convolution geometry (NCHW input, [M, C, kh, kw] weights, groups = 1),
+ * mirroring tbn::Conv2DParams (tbn-runtime/include/tbn/operators/conv2d.hpp:12-37). */
+typedef struct tbn_conv2d_desc {
+    int64_t n, c, h, w;   /* input  [n, c, h, w]                 */
+    int64_t m;            /* output channels                     */
+    int64_t kh, kw;       /* kernel                              */
+    int64_t sh, sw;       /* stride                              */
+    int64_t ph, pw;       /* symmetric zero padding              */
+    int64_t dh, dw;       /* dilation                            */
+} tbn_conv2d_desc;
+
+/* ---- library -------------------------------------------------------------- */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* tbn_hip_last_error(void);
+/* Library version, major*10000 + minor*100 + patch. */
+int tbn_hip_version(void);
+/* Checks that the current HIP device is a gfx950 (MI355X); returns
+ * TBN_DEVICE_NOT_SUPPORTED otherwise. */
+int tbn_hip_device_check(void);
+/* Waits for `stream` and reports any asynchronous device error. */
+int tbn_hip_synchronize(tbn_stream_t stream);
+
+/* ---- quantization (north_star subsystem 1) --------------------------------- */
+
+/* quantize_to_binary(W, threshold), FLOAT32 input: out[i] = w[i] > threshold.
+ * Replaces tbn::quantize_to_binary (tbn-runtime/src/operators/quantized_gemm_neon.cpp:544-565). */
+int tbn_hip_quantize_to_binary_f32(const float* w, int64_t n, float threshold,
+                                   uint8_t* out, tbn_stream_t stream);
+/* quantize_to_binary, INT8 input: out[i] = w[i] > 0 (same reference lines 555-559). */
+int tbn_hip_quantize_to_binary_i8(const int8_t* w, int64_t n, uint8_t* out, tbn_stream_t stream);
+/* quantize_to_ternary(W, lo, hi): -1 if w < lo, +1 if w > hi, else 0.
+ * Replaces tbn::quantize_to_ternary (quantized_gemm_neon.cpp:570-597). */
+int tbn_hip_quantize_to_ternary_f32(const float* w, int64_t n, float lo, float hi,
+                                    int8_t* out, tbn_stream_t stream);
+/* Session sign extraction, out[i] = w[i] >= 0 (model.hpp:423-438,797-807). */
+int tbn_hip_sign_ge0_f32(const float* w, int64_t n, uint8_t* out, tbn_stream_t stream);
+/* Per-channel scale = mean |w| over `per_channel` contiguous elements, summed
+ * sequentially in fp32 as the Session does (model.hpp:388-394): bit-exact. */
+int tbn_hip_channel_mean_abs(const float* w, int64_t channels, int64_t per_channel,
+                             float* scale, tbn_stream_t stream);
+
+/* ---- packing (north_star subsystem 1) -------------------------------------- */
+
+/* BINARY byte tensor (layout KN or NK) -> BinaryMatrix bits [N_pad][K_pad/8].
+ * Requires K_pad >= K, N_pad >= N, K_pad % 64 == 0, N_pad % 8 == 0.
+ * Replaces the transpose+pad+BinaryMatrix::pack sequence of
+ * quantized_gemm_neon.cpp:197-214, model.hpp:456-480 and model.hpp:809-833. */
+int tbn_hip_pack_binary(const uint8_t* bin, int64_t K, int64_t N, int layout,
+                        int64_t K_pad, int64_t N_pad, uint8_t* packed, tbn_stream_t stream);
+/* Fused float -> sign -> BinaryMatrix bits in one pass (same layout rules);
+ * `sign_rule` picks the reference rule, `threshold` applies to GT_THRESHOLD. */
+int tbn_hip_quantize_pack_binary_f32(const float* w, int64_t K, int64_t N, int layout,
+                                     int sign_rule, float threshold,
+                                     int64_t K_pad, int64_t N_pad, uint8_t* packed,
+                                     tbn_stream_t stream);
+/* BinaryMatrix bits -> int8 +-1 in layout KN or NK (the sign decode). */
+int tbn_hip_unpack_binary(const uint8_t* packed, int64_t K, int64_t N, int layout,
+                          int64_t K_pad, int8_t* out, tbn_stream_t stream);
+/* Flat 2-bit encoding of n ternary values (TernaryPackedWeights::set_weight
+ * over a fresh buffer, packed_weights.hpp:52-71); values other than -1,0,+1
+ * encode as 0.  packed holds ceil(n/4) bytes. */
+int tbn_hip_pack_ternary2(const int8_t* t, int64_t n, uint8_t* packed, tbn_stream_t stream);
+/* Flat 2-bit decode (TernaryPackedWeights::get_weight, packed_weights.hpp:35-49). */
+int tbn_hip_unpack_ternary2(const uint8_t* packed, int64_t n, int8_t* out, tbn_stream_t stream);
+/* Ternary weights (layout KN or NK) -> GEMM 2-bit layout W^T[N_pad][K_pad],
+ * zero padded.  Requires K_pad >= K, N_pad >= N, K_pad % 32 == 0. */
+int tbn_hip_pack_ternary(const int8_t* t, int64_t K, int64_t N, int layout,
+                         int64_t K_pad, int64_t N_pad, uint8_t* packed, tbn_stream_t stream);
+/* Fused float -> ternary (lo/hi thresholds) -> GEMM 2-bit layout. */
+int tbn_hip_quantize_pack_ternary_f32(const float* w, int64_t K, int64_t N, int layout,
+                                      float lo, float hi, int64_t K_pad, int64_t N_pad,
+                                      uint8_t* packed, tbn_stream_t stream);
+
+/* ---- float x binary / float x ternary GEMM (north_star subsystem 2) -------- */
+
+/* C[m,n] = acc[m,n] * alpha * s[n] + b[n]   (optionally ReLU), with
+ *   acc[m,n] = sum_k A[m,k] * w[k,n],  w = +-1 decoded from BinaryMatrix bits.
+ * A: fp32 [M, K] row-major, leading dimension lda >= K.
+ * scale: per-column fp32 [N] or NULL (then s = 1); alpha: scalar multiplier
+ * (the reference's scalar `scale` argument); bias: [N] or NULL.
+ * C: fp32 [M, N], ldc >= N.  Requires K_pad % 32 == 0, K_pad >= K, N_pad >= N.
+ * Replaces tbn::qlinear_matmul_binary / _blocked_packed / _naive
+ * (quantized_gemm_neon.cpp:63-90,249-309,380-430), computing the fp32-activation
+ * product of qlinear_matmul_binary_naive. */
+int tbn_hip_gemm_f32_binary(const float* A, int64_t lda, int64_t M, int64_t N, int64_t K,
+                            const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                            const float* scale, float alpha, const float* bias, int flags,
+                            float* C, int64_t ldc, tbn_stream_t stream);
+/* Same with w in {-1, 0, +1} from the GEMM 2-bit layout.  Replaces
+ * tbn::qlinear_matmul_ternary (quantized_gemm_neon.cpp:506-538) with the true
+ * float x ternary product its own test expects (test_quantized_operators.cpp:151-155). */
+int tbn_hip_gemm_f32_ternary(const float* A, int64_t lda, int64_t M, int64_t N, int64_t K,
+                             const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                             const float* scale, float alpha, const float* bias, int flags,
+                             float* C, int64_t ldc, tbn_stream_t stream);
+
+/* ---- binary / ternary Conv2D (north_star subsystem 3) ---------------------- */
+
+/* Implicit-GEMM convolution, im2col formed on the fly (no column buffer):
+ *   y[n,m,oh,ow] = epi( sum_{c,r,s} x[n,c,ih,iw] * w[m,(c,r,s)] )
+ * with w = +-1 from BinaryMatrix bits packed from the [M, C*kh*kw] weights
+ * (layout NK, K_pad >= C*kh*kw, K_pad % 32 == 0, N_pad >= M).
+ * epi: default acc*alpha*s[m] + b[m]; TBN_EPI_BIAS_THEN_SCALE gives
+ * (acc + b[m]) * alpha*s[m]; then TBN_EPI_RELU; then TBN_EPI_MAXPOOL2X2
+ * (floor mode, output [n, m, OH/2, OW/2]).
+ * Replaces tbn::conv2d_binary / conv2d_binary_with_scales and the Session's
+ * cached binary conv (conv2d.cpp:220-369; model.hpp:414-559). */
+int tbn_hip_conv2d_f32_binary(const float* x, const tbn_conv2d_desc* desc,
+                              const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                              const float* scale, float alpha, const float* bias, int flags,
+                              float* y, tbn_stream_t stream);
+/* Same with ternary weights in the GEMM 2-bit layout (tbn::conv2d_ternary,
+ * conv2d.cpp:195-217, with true ternary values). */
+int tbn_hip_conv2d_f32_ternary(const float* x, const tbn_conv2d_desc* desc,
+                               const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                               const float* scale, float alpha, const float* bias, int flags,
+                               float* y, tbn_stream_t stream);
+
+/* ---- fp32 layers and epilogue operators (Session support) ------------------ */
+
+/* fp32 Conv2D (tbn::conv2d, conv2d.cpp:78-192), weights fp32 [M, C, kh, kw];
+ * flags: TBN_EPI_RELU, TBN_EPI_MAXPOOL2X2. */
+int tbn_hip_conv2d_f32(const float* x, const tbn_conv2d_desc* desc, const float* w,
+                       const float* bias, int flags, float* y, tbn_stream_t stream);
+/* fp32 GEMM (tbn::gemm, gemm.cpp:349-360): out = alpha*op(A)*op(B) + beta*C,
+ * C NULL, [N] (c_is_1d) or [M, N]; flags: TBN_EPI_RELU. */
+int tbn_hip_gemm_f32(const float* A, const float* B, const float* Cin, int c_is_1d,
+                     int64_t M, int64_t K, int64_t N, float alpha, float beta,
+                     int transA, int transB, int flags, float* out, tbn_stream_t stream);
+/* MaxPool2D (tbn::maxpool2d, pooling.cpp:10-80).  out_hw (host, may be NULL)
+ * receives the output height and width; y may be NULL to query only. */
+int tbn_hip_maxpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w,
+                      int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                      int64_t dh, int64_t dw, int ceil_mode, float* y, int64_t* out_hw,
+                      tbn_stream_t stream);
+/* GlobalAvgPool2D (tbn::global_avgpool2d, pooling.cpp:184-216), y [n, c]. */
+int tbn_hip_global_avgpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w,
+                             float* y, tbn_stream_t stream);
+/* Elementwise y = a + b (+ReLU) with b broadcast over an [outer, inner, rest]
+ * view: b has `outer_b * inner` elements indexed by (i_outer % outer_b, i_inner).
+ * Covers the Session's Add cases (model.hpp:905-1037): same shape
+ * (inner = n, rest = 1), [M,N]+[N], [N,C,H,W]+[C] / [C,1,1]. */
+int tbn_hip_add(const float* a, const float* b, int64_t outer, int64_t inner, int64_t rest,
+                int64_t outer_b, int flags, float* y, tbn_stream_t stream);
+/* y = max(x, 0) (model.hpp:1166-1171). */
+int tbn_hip_relu(const float* x, int64_t n, float* y, tbn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TBN_HIP_H */

@@ -1,0 +1,44 @@
+"""The C-ABI library loads and exports every symbol include/tbn_hip.h declares;
+host-side argument validation returns tbn::ErrorCode values before any device
+work (no compute calls here, so this runs on the CPU)."""
+import ctypes
+
+import tbn_hip
+
+
+def test_library_exports_every_declared_symbol():
+    lib = tbn_hip.lib()
+    declared = tbn_hip.header_symbols()
+    assert len(declared) >= 25
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(tbn_hip._SIGNATURES), "ctypes signatures out of sync with the header"
+
+
+def test_version_and_error_string():
+    assert tbn_hip.lib().tbn_hip_version() == 100
+    assert isinstance(tbn_hip.last_error(), str)
+
+
+def test_argument_errors_are_reported_before_device_use():
+    lib = tbn_hip.lib()
+    # negative sizes -> INVALID_SHAPE, no device touched
+    assert lib.tbn_hip_quantize_to_binary_f32(None, -1, 0.0, None, None) == tbn_hip.INVALID_SHAPE
+    assert "non-negative" in tbn_hip.last_error()
+    # K_pad not a multiple of 32 -> INVALID_SHAPE
+    rc = lib.tbn_hip_gemm_f32_binary(None, 64, 4, 4, 64, None, 40, 8, None, 1.0, None, 0, None, 4, None)
+    assert rc == tbn_hip.INVALID_SHAPE
+    # lda < K -> INVALID_ARGUMENT
+    rc = lib.tbn_hip_gemm_f32_binary(None, 10, 4, 4, 64, None, 64, 8, None, 1.0, None, 0, None, 4, None)
+    assert rc == tbn_hip.INVALID_ARGUMENT
+    # unknown layout / sign rule
+    assert lib.tbn_hip_pack_binary(None, 64, 8, 7, 64, 8, None, None) == tbn_hip.INVALID_ARGUMENT
+    assert lib.tbn_hip_quantize_pack_binary_f32(None, 64, 8, 0, 9, 0.0, 64, 8, None, None) == tbn_hip.INVALID_ARGUMENT
+    # conv with an empty output
+    d = tbn_hip.conv_desc(1, 1, 2, 2, 1, 5, 5)
+    rc = lib.tbn_hip_conv2d_f32_binary(None, ctypes.byref(d), None, 32, 8, None, 1.0, None, 0, None, None)
+    assert rc == tbn_hip.INVALID_SHAPE
+    # maxpool shape query is host-only
+    hw = (ctypes.c_int64 * 2)()
+    assert lib.tbn_hip_maxpool2d(None, 1, 1, 112, 112, 3, 3, 2, 2, 1, 1, 1, 1, 0, None, hw, None) == 0
+    assert list(hw) == [56, 56]

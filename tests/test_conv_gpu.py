@@ -1,0 +1,116 @@
+"""Implicit-GEMM Conv2D on the GPU vs the oracle (north_star subsystem 3).
+
+Reference semantics (mode F32): the reference's fp32 conv2d (conv2d.cpp:78-192)
+applied to the dequantized weights s[m]*sign(w), i.e. y = s*acc + b
+(conv2d_binary_with_scales order, conv2d.cpp:319-369), then ReLU / MaxPool.
+Tolerance: rel-L2 <= 1e-5, max-abs <= 1e-4*sqrt(K)*max|x|*max|s|."""
+import numpy as np
+import pytest
+import torch
+
+import refmath as rm
+import tbn_hip
+from gpu_util import P, empty, host, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def pack_conv_weights(w_sign_bytes, M, K):
+    K_pad, N_pad = tbn_hip.padded_dims(K, M)
+    packed = empty(N_pad * K_pad // 8, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_binary", P(to_dev(w_sign_bytes)), K, M, tbn_hip.LAYOUT_NK, K_pad, N_pad,
+                 P(packed), None)
+    return packed, K_pad, N_pad
+
+
+def conv_ref(x, wsign, scale, alpha, bias, stride, pad, dil, flags):
+    acc = rm.f64_conv(x, wsign, None, stride, pad, dil)
+    mult = (np.float32(alpha) * scale.astype(np.float32)).astype(np.float64)[None, :, None, None]
+    b = bias.astype(np.float64)[None, :, None, None]
+    y = (acc + b) * mult if flags & tbn_hip.EPI_BIAS_THEN_SCALE else acc * mult + b
+    if flags & tbn_hip.EPI_RELU:
+        y = np.maximum(y, 0.0)
+    if flags & tbn_hip.EPI_MAXPOOL2X2:
+        N, M, OH, OW = y.shape
+        y = y[:, :, :OH // 2 * 2, :OW // 2 * 2].reshape(N, M, OH // 2, 2, OW // 2, 2).max(axis=(3, 5))
+    return y
+
+
+CASES = [
+    # N, C, H, W, M, kh, kw, stride, pad, dil, flags
+    (64, 64, 14, 14, 128, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_RELU),        # config 4
+    (1, 1, 28, 28, 6, 5, 5, (1, 1), (0, 0), (1, 1), tbn_hip.EPI_RELU | tbn_hip.EPI_MAXPOOL2X2),  # LeNet conv1
+    (1, 6, 12, 12, 16, 5, 5, (1, 1), (0, 0), (1, 1), tbn_hip.EPI_RELU | tbn_hip.EPI_MAXPOOL2X2),  # LeNet conv2
+    (4, 64, 56, 56, 128, 3, 3, (2, 2), (1, 1), (1, 1), tbn_hip.EPI_RELU),          # ResNet downsample
+    (4, 64, 56, 56, 128, 1, 1, (2, 2), (0, 0), (1, 1), 0),                          # 1x1 projection
+    (2, 128, 28, 28, 128, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_BIAS_THEN_SCALE),
+    (2, 5, 13, 11, 40, 3, 2, (2, 1), (1, 0), (2, 2), tbn_hip.EPI_RELU),            # odd everything
+    (3, 7, 9, 9, 70, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_MAXPOOL2X2),        # odd output, floor pool
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[:7])))
+def test_conv_binary(dev, orc, case):
+    N, C, H, W, M, kh, kw, stride, pad, dil, flags = case
+    rng = np.random.default_rng(N * 131 + C * 7 + M)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    wbytes = (rng.random((M, C, kh, kw)) < 0.5).astype(np.uint8)
+    wsign = np.where(wbytes == 1, 1.0, -1.0).astype(np.float32)
+    scale = rng.uniform(0.5, 1.5, M).astype(np.float32)
+    bias = (rng.standard_normal(M) * 0.01).astype(np.float32)
+    K = C * kh * kw
+    packed, K_pad, N_pad = pack_conv_weights(wbytes, M, K)
+    d = tbn_hip.conv_desc(N, C, H, W, M, kh, kw, *stride, *pad, *dil)
+    OH, OW = tbn_hip.conv_out_hw(d)
+    oshape = (N, M, OH // 2, OW // 2) if flags & tbn_hip.EPI_MAXPOOL2X2 else (N, M, OH, OW)
+    y = empty(oshape, torch.float32)
+    y.fill_(np.nan)
+    tbn_hip.call("tbn_hip_conv2d_f32_binary", P(to_dev(x)), d, P(packed), K_pad, N_pad, P(to_dev(scale)), 1.0,
+                 P(to_dev(bias)), flags, P(y), None)
+    ref = conv_ref(x, wsign, scale, 1.0, bias, stride, pad, dil, flags)
+    rm.assert_within_tolerance(host(y), ref, K, np.abs(x).max() * 1.5)
+    if case[0] == 64:
+        # fp32 reference operator on dequantized weights (conv2d.cpp:78-192) is within the same bound
+        y32 = orc.conv2d_f32(x[:2], wsign * scale[:, None, None, None], bias, stride, pad, dil)
+        rm.assert_within_tolerance(host(y)[:2], np.maximum(y32, 0), K, np.abs(x).max() * 1.5)
+
+
+def test_conv_ternary(dev, orc):
+    rng = np.random.default_rng(77)
+    N, C, H, W, M, kh, kw = 2, 16, 10, 10, 48, 3, 3
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    t = rng.choice(np.array([-1, 0, 1], np.int8), size=(M, C, kh, kw), p=[0.3, 0.4, 0.3])
+    scale = rng.uniform(0.5, 1.5, M).astype(np.float32)
+    bias = (rng.standard_normal(M) * 0.01).astype(np.float32)
+    K = C * kh * kw
+    K_pad = (K + 31) // 32 * 32
+    packed = empty(M * K_pad // 4, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(t)), K, M, tbn_hip.LAYOUT_NK, K_pad, M, P(packed), None)
+    d = tbn_hip.conv_desc(N, C, H, W, M, kh, kw, 1, 1, 1, 1)
+    y = empty((N, M, H, W), torch.float32)
+    tbn_hip.call("tbn_hip_conv2d_f32_ternary", P(to_dev(x)), d, P(packed), K_pad, M, P(to_dev(scale)), 1.0,
+                 P(to_dev(bias)), tbn_hip.EPI_RELU, P(y), None)
+    ref = conv_ref(x, t.astype(np.float32), scale, 1.0, bias, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_RELU)
+    rm.assert_within_tolerance(host(y), ref, K, np.abs(x).max() * 1.5)
+
+
+@pytest.mark.parametrize("case", [(2, 3, 64, 64, 64, 7, 7, 2, 3, 0), (1, 1, 28, 28, 6, 5, 5, 1, 0, 4),
+                                  (2, 8, 9, 9, 40, 3, 3, 1, 1, 1)])
+def test_conv_f32(dev, orc, case):
+    """fp32 layers (ResNet stem 7x7/2, LeNet with quantization off)."""
+    N, C, H, W, M, kh, kw, s, p, flags = case
+    rng = np.random.default_rng(M + C)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    w = (rng.standard_normal((M, C, kh, kw)) * np.sqrt(2.0 / (C * kh * kw))).astype(np.float32)
+    b = (rng.standard_normal(M) * 0.01).astype(np.float32)
+    d = tbn_hip.conv_desc(N, C, H, W, M, kh, kw, s, s, p, p)
+    OH, OW = tbn_hip.conv_out_hw(d)
+    pool = flags & tbn_hip.EPI_MAXPOOL2X2
+    y = empty((N, M, OH // 2, OW // 2) if pool else (N, M, OH, OW), torch.float32)
+    tbn_hip.call("tbn_hip_conv2d_f32", P(to_dev(x)), d, P(to_dev(w)), P(to_dev(b)), flags, P(y), None)
+    ref = orc.conv2d_f64(x, w, b, (s, s), (p, p))
+    if flags & tbn_hip.EPI_RELU:
+        ref = np.maximum(ref, 0.0)
+    if pool:
+        ref = ref[:, :, :OH // 2 * 2, :OW // 2 * 2].reshape(N, M, OH // 2, 2, OW // 2, 2).max(axis=(3, 5))
+    rm.assert_within_tolerance(host(y), ref, C * kh * kw, np.abs(x).max() * np.abs(w).max())

@@ -1,0 +1,210 @@
+"""float x binary / float x ternary GEMM on the GPU vs the oracle (north_star
+subsystem 2).  Tolerance (north_star): rel-L2 <= 1e-5 and max-abs <=
+1e-4*sqrt(K)*max|x| (x = activations times the largest column multiplier)
+against the float64 oracle; the fp32 sequential oracle is checked the same way.
+Full-size shapes (4096^3) are checked through size-independent properties:
+exact row spot checks, column checksums and linearity."""
+import numpy as np
+import pytest
+import torch
+
+import refmath as rm
+import gpu_util
+import tbn_hip
+from gpu_util import P, empty, host, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def make_binary_problem(M, K, N, seed, lda=None):
+    rng = np.random.default_rng(seed)
+    lda = lda or K
+    A = rng.standard_normal((M, lda)).astype(np.float32)
+    binw = (rng.random((K, N)) < 0.5).astype(np.uint8)
+    scale = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    return A, binw, scale, bias
+
+
+def gpu_pack_binary(binw, K, N):
+    K_pad, N_pad = tbn_hip.padded_dims(K, N)
+    packed = empty(N_pad * K_pad // 8, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_binary", P(to_dev(binw)), K, N, tbn_hip.LAYOUT_KN, K_pad, N_pad, P(packed), None)
+    return packed, K_pad, N_pad
+
+
+def run_gemm(kind, A, lda, M, N, K, packed, K_pad, N_pad, scale=None, alpha=1.0, bias=None, flags=0, ldc=None):
+    ldc = ldc or N
+    dA = A if isinstance(A, torch.Tensor) else to_dev(A)
+    gpu_util._KEEP.append(dA)
+    C = empty((M, ldc), torch.float32)
+    C.fill_(np.nan)
+    ds = None if scale is None else to_dev(scale)
+    db = None if bias is None else to_dev(bias)
+    tbn_hip.call(f"tbn_hip_gemm_f32_{kind}", P(dA), lda, M, N, K, P(packed), K_pad, N_pad, P(ds), alpha, P(db),
+                 flags, P(C), ldc, None)
+    return C
+
+
+@pytest.mark.parametrize("M,K,N,lda", [(1, 25, 6, 25), (1, 256, 10, 256), (7, 300, 13, 301), (64, 64, 64, 64),
+                                       (130, 257, 70, 260), (33, 1000, 129, 1000), (200, 576, 128, 576)])
+def test_gemm_binary_small_shapes(dev, orc, M, K, N, lda):
+    A, binw, scale, bias = make_binary_problem(M, K, N, seed=M * 1000 + K, lda=lda)
+    packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+    Ak = np.ascontiguousarray(A[:, :K])
+    hp = host(packed)
+    for flags, alpha in [(0, 1.0), (tbn_hip.EPI_RELU, 0.7), (tbn_hip.EPI_BIAS_THEN_SCALE, 1.3)]:
+        out = host(run_gemm("binary", A, lda, M, N, K, packed, K_pad, N_pad, scale, alpha, bias, flags))
+        ref = orc.gemm_f64_binary(Ak, hp, K_pad, N, scale, alpha, bias, bool(flags & 1)) \
+            if not flags & tbn_hip.EPI_BIAS_THEN_SCALE else \
+            rm.f64_gemm(Ak, rm.np_unpack_binary(hp, K, N, K_pad), scale, alpha, bias, bias_then_scale=True)
+        rm.assert_within_tolerance(out, ref, K, np.abs(A).max() * alpha * 1.5)
+    # the sequential-fp32 reference loop (qlinear_matmul_binary_naive) is within the same bound
+    out = host(run_gemm("binary", A, lda, M, N, K, packed, K_pad, N_pad))
+    rm.assert_within_tolerance(out, orc.qlinear_matmul_binary_naive(Ak, binw, 1.0), K, np.abs(A).max())
+
+
+def test_gemm_binary_no_scale_no_bias_and_ldc(dev, orc):
+    M, K, N = 50, 128, 40
+    A, binw, _, _ = make_binary_problem(M, K, N, seed=5)
+    packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+    C = host(run_gemm("binary", A, K, M, N, K, packed, K_pad, N_pad, ldc=48))
+    ref = orc.gemm_f64_binary(A, host(packed), K_pad, N)
+    rm.assert_within_tolerance(C[:, :N], ref, K, np.abs(A).max())
+    assert np.isnan(C[:, N:]).all()  # columns past N untouched
+
+
+def test_gemm_binary_cfg2_1024(dev, orc):
+    """Config 2: M=N=K=1024, A ~ N(0,1), W +-1 p=0.5, per-column scale U[0.5,1.5]."""
+    M = N = K = 1024
+    A, binw, scale, _ = make_binary_problem(M, K, N, seed=2)
+    packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+    out = host(run_gemm("binary", A, K, M, N, K, packed, K_pad, N_pad, scale))
+    ref = orc.gemm_f64_binary(A, host(packed), K_pad, N, scale)
+    r, m = rm.assert_within_tolerance(out, ref, K, np.abs(A).max() * 1.5)
+    assert r < 1e-6  # exact products, fp32 accumulation
+
+
+def test_gemm_headline_4096_properties(dev, orc):
+    """4096^3 float x binary: exact oracle rows, column checksum, linearity."""
+    M = N = K = 4096
+    rng = np.random.default_rng(42)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    binw = (rng.random((K, N)) < 0.5).astype(np.uint8)
+    scale = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+    dA = to_dev(A)
+    C = run_gemm("binary", dA, K, M, N, K, packed, K_pad, N_pad, scale)
+    hp = host(packed)
+    rows = rng.choice(M, 24, replace=False)
+    rows = np.concatenate([[0, M - 1], rows])
+    Cr = host(C)[rows]
+    ref_rows = orc.gemm_f64_binary(A[rows], hp, K_pad, N, scale)
+    rm.assert_within_tolerance(Cr, ref_rows, K, np.abs(A).max() * 1.5)
+    # column checksum: sum_m C[m, :] == (sum_m A[m, :]) W diag(s)
+    colsum = host(C).astype(np.float64).sum(axis=0)
+    asum = A.astype(np.float64).sum(axis=0)
+    W = rm.np_unpack_binary(hp, K, N, K_pad).astype(np.float64)
+    expect = (asum @ W) * scale.astype(np.float64)
+    assert rm.rel_l2(colsum, expect) < 1e-5
+    # linearity: C(A1 + A2) == C(A1) + C(A2) within fp32 accumulation error
+    A2 = rng.standard_normal((M, K)).astype(np.float32)
+    C2 = run_gemm("binary", to_dev(A2), K, M, N, K, packed, K_pad, N_pad, scale)
+    C12 = run_gemm("binary", dA + to_dev(A2), K, M, N, K, packed, K_pad, N_pad, scale)
+    lhs = host(C12).astype(np.float64)
+    rhs = host(C).astype(np.float64) + host(C2)
+    assert rm.rel_l2(lhs, rhs) < 1e-5
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 2, 2), (9, 260, 17), (64, 512, 96)])
+def test_gemm_ternary_small(dev, orc, M, K, N):
+    rng = np.random.default_rng(M + K + N)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    t = rng.choice([-1, 0, 1], size=(K, N), p=[0.3, 0.4, 0.3]).astype(np.int8)
+    scale = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    K_pad = (K + 31) // 32 * 32
+    packed = empty(N * K_pad // 4, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(t)), K, N, tbn_hip.LAYOUT_KN, K_pad, N, P(packed), None)
+    out = host(run_gemm("ternary", A, K, M, N, K, packed, K_pad, N, scale, 0.5))
+    ref = orc.gemm_f64_ternary(A, host(packed), K_pad, N, scale, 0.5)
+    rm.assert_within_tolerance(out, ref, K, np.abs(A).max() * 0.75)
+
+
+def test_gemm_ternary_known_answer(dev):
+    # tbn-runtime/tests/test_quantized_operators.cpp:151-155
+    A = np.array([[1.0, 2.0], [3.0, 4.0]], np.float32)
+    t = np.array([[1, -1], [0, 1]], np.int8)
+    packed = empty(2 * 32 // 4, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(t)), 2, 2, tbn_hip.LAYOUT_KN, 32, 2, P(packed), None)
+    out = host(run_gemm("ternary", A, 2, 2, 2, 2, packed, 32, 2, alpha=0.5))
+    assert out.reshape(-1).tolist() == [0.5, 0.5, 1.5, 0.5]
+
+
+def test_gemm_binary_known_answer(dev):
+    # test_quantized_operators.cpp:165-179 inputs, true float x binary
+    A = np.array([[1.0, -2.0], [3.0, -4.0]], np.float32)
+    packed, K_pad, N_pad = gpu_pack_binary(np.array([[1, 0], [0, 1]], np.uint8), 2, 2)
+    out = host(run_gemm("binary", A, 2, 2, 2, 2, packed, K_pad, N_pad, alpha=0.7))
+    np.testing.assert_allclose(out.reshape(-1), [2.1, -2.1, 4.9, -4.9], rtol=1e-6)
+
+
+def test_gemm_ternary_cfg3(dev, orc):
+    """Config 3: M=256, N=K=4096, T in {-1,0,1} p={.3,.4,.3}, 2-bit packed, scale U[0.5,1.5]."""
+    M, N, K = 256, 4096, 4096
+    rng = np.random.default_rng(3)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    t = rng.choice(np.array([-1, 0, 1], np.int8), size=(K, N), p=[0.3, 0.4, 0.3])
+    scale = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    packed = empty(N * K // 4, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(t)), K, N, tbn_hip.LAYOUT_KN, K, N, P(packed), None)
+    out = host(run_gemm("ternary", A, K, M, N, K, packed, K, N, scale))
+    rows = np.arange(0, M, 4)
+    ref = orc.gemm_f64_ternary(A[rows], host(packed), K, N, scale)
+    rm.assert_within_tolerance(out[rows], ref, K, np.abs(A).max() * 1.5)
+
+
+def test_gemm_special_values(dev, orc):
+    M, K, N = 4, 64, 8
+    A = np.zeros((M, K), np.float32)
+    A[0, 0] = np.inf
+    A[1, 3] = -np.inf
+    A[2, 5] = np.nan
+    A[3, :] = np.float32(1e-30)
+    A[3, 1] = -0.0
+    binw = np.ones((K, N), np.uint8)
+    binw[0, 1] = 0
+    packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+    out = host(run_gemm("binary", A, K, M, N, K, packed, K_pad, N_pad))
+    ref = orc.gemm_f32_binary(A, host(packed), K_pad, N)
+    assert np.array_equal(np.isinf(out), np.isinf(ref)) and np.array_equal(np.sign(out[:2]), np.sign(ref[:2]))
+    assert np.isnan(out[2]).all() and np.isnan(ref[2]).all()
+    np.testing.assert_allclose(out[3], ref[3], rtol=1e-6)
+
+
+def test_gemm_f32_matches_blocked_reference(dev, orc):
+    rng = np.random.default_rng(21)
+    for (M, K, N, ta, tb) in [(32, 512, 1000, False, False), (1, 256, 10, False, True), (70, 130, 90, True, False)]:
+        A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+        B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+        c1 = rng.standard_normal(N).astype(np.float32)
+        out = empty((M, N), torch.float32)
+        tbn_hip.call("tbn_hip_gemm_f32", P(to_dev(A)), P(to_dev(B)), P(to_dev(c1)), 1, M, K, N, 0.5, 2.0,
+                     int(ta), int(tb), 0, P(out), None)
+        ref = 0.5 * ((A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)) + 2.0 * c1
+        rm.assert_within_tolerance(host(out), ref, K, np.abs(A).max() * np.abs(B).max())
+        rm.assert_within_tolerance(orc.gemm_f32_blocked(A, B, c1, 0.5, 2.0, ta, tb), ref, K,
+                                   np.abs(A).max() * np.abs(B).max())
+
+
+def test_gemm_error_codes(dev):
+    packed = empty(64, torch.uint8)
+    A = empty((4, 64), torch.float32)
+    C = empty((4, 8), torch.float32)
+    with pytest.raises(tbn_hip.TbnError) as e:
+        tbn_hip.call("tbn_hip_gemm_f32_binary", P(A), 64, 4, 8, 64, P(packed), 40, 8, None, 1.0, None, 0, P(C), 8, None)
+    assert e.value.code == tbn_hip.INVALID_SHAPE
+    with pytest.raises(tbn_hip.TbnError) as e:
+        tbn_hip.call("tbn_hip_gemm_f32_binary", P(A), 64, 4, 8, 64, None, 64, 8, None, 1.0, None, 0, P(C), 8, None)
+    assert e.value.code == tbn_hip.INVALID_ARGUMENT
+    # empty problems are no-ops
+    tbn_hip.call("tbn_hip_gemm_f32_binary", None, 0, 0, 8, 64, None, 64, 8, None, 1.0, None, 0, None, 8, None)

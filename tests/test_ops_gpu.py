@@ -1,0 +1,76 @@
+"""Pooling / elementwise operators on the GPU vs the oracle.  Max, ReLU and
+the sequential-sum GlobalAvgPool are exact, so these compare bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+import refmath as rm
+import tbn_hip
+from gpu_util import P, empty, host, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_maxpool(x, k, s, p=(0, 0), ceil_mode=False):
+    N, C, H, W = x.shape
+    import ctypes
+    hw = (ctypes.c_int64 * 2)()
+    args = [N, C, H, W, k[0], k[1], s[0], s[1], p[0], p[1], 1, 1, int(ceil_mode)]
+    tbn_hip.call("tbn_hip_maxpool2d", None, *args, None, hw, None)
+    y = empty((N, C, hw[0], hw[1]), torch.float32)
+    tbn_hip.call("tbn_hip_maxpool2d", P(to_dev(x)), *args, P(y), hw, None)
+    return host(y)
+
+
+@pytest.mark.parametrize("k,s,p,ceil_mode", [((2, 2), (2, 2), (0, 0), False), ((3, 3), (2, 2), (1, 1), False),
+                                             ((3, 3), (2, 2), (0, 0), True), ((2, 3), (1, 2), (1, 1), False)])
+def test_maxpool_bit_exact(dev, orc, k, s, p, ceil_mode):
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((2, 3, 9, 8)).astype(np.float32)
+    x[0, 0, 0, 0] = np.nan  # ignored by the running max, as in the reference
+    assert np.array_equal(gpu_maxpool(x, k, s, p, ceil_mode), orc.maxpool2d(x, k, s, p, ceil_mode=ceil_mode))
+
+
+def test_maxpool_known_answer_and_resnet_shape(dev, orc):
+    x = (np.arange(32) % 10).astype(np.float32).reshape(1, 2, 4, 4)
+    assert gpu_maxpool(x, (2, 2), (2, 2)).reshape(-1)[:2].tolist() == [5.0, 7.0]
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((2, 64, 112, 112)).astype(np.float32)
+    assert np.array_equal(gpu_maxpool(x, (3, 3), (2, 2), (1, 1)), orc.maxpool2d(x, (3, 3), (2, 2), (1, 1)))
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 4, 4), (32, 512, 7, 7), (3, 5, 1, 1)])
+def test_global_avgpool_bit_exact(dev, orc, shape):
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(shape).astype(np.float32)
+    y = empty(shape[:2], torch.float32)
+    tbn_hip.call("tbn_hip_global_avgpool2d", P(to_dev(x)), *shape, P(y), None)
+    assert np.array_equal(host(y), orc.global_avgpool2d(x))
+
+
+def test_add_broadcasts_and_relu(dev):
+    rng = np.random.default_rng(4)
+    a = rng.standard_normal((2, 6, 5, 5)).astype(np.float32)
+    same = rng.standard_normal(a.shape).astype(np.float32)
+    ch = rng.standard_normal(6).astype(np.float32)
+    y = empty(a.shape, torch.float32)
+    tbn_hip.call("tbn_hip_add", P(to_dev(a)), P(to_dev(same)), 1, a.size, 1, 1, 0, P(y), None)
+    assert np.array_equal(host(y), a + same)
+    tbn_hip.call("tbn_hip_add", P(to_dev(a)), P(to_dev(same)), 1, a.size, 1, 1, tbn_hip.EPI_RELU, P(y), None)
+    assert np.array_equal(host(y), np.maximum(a + same, 0))
+    tbn_hip.call("tbn_hip_add", P(to_dev(a)), P(to_dev(ch)), 2, 6, 25, 1, 0, P(y), None)
+    assert np.array_equal(host(y), a + ch[None, :, None, None])
+    m2 = rng.standard_normal((7, 10)).astype(np.float32)
+    b1 = rng.standard_normal(10).astype(np.float32)
+    y2 = empty((7, 10), torch.float32)
+    tbn_hip.call("tbn_hip_add", P(to_dev(m2)), P(to_dev(b1)), 7, 10, 1, 1, 0, P(y2), None)
+    assert np.array_equal(host(y2), m2 + b1)
+
+
+def test_relu(dev):
+    x = np.array([-1.0, 0.0, -0.0, 2.5, np.nan, -np.inf, np.inf], np.float32)
+    y = empty(x.size, torch.float32)
+    tbn_hip.call("tbn_hip_relu", P(to_dev(x)), x.size, P(y), None)
+    out = host(y)
+    assert out.tolist() == [0.0, 0.0, 0.0, 2.5, 0.0, 0.0, np.inf]
+    assert not np.signbit(out[2])
