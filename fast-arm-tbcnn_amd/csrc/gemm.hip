@@ -51,7 +51,7 @@ struct GemmEpi {
     }
 };
 
-using CfgBig = TileCfg<128, 128, 64, 64>;
+using CfgBig = TileCfg<128, 256, 64, 128, 2>;
 using CfgSmall = TileCfg<64, 64, 32, 32>;
 
 template <class Cfg, class ColL>
@@ -95,8 +95,8 @@ int gemm_quant(const float* A, int64_t lda, int64_t M, int64_t N, int64_t K, con
     GemmEpi epi{C, ldc, static_cast<int>(M), static_cast<int>(N), scale, alpha, bias,
                 nullptr, 0.0f, 0, flags};
     const int64_t col_bytes = TERNARY ? K_pad / 4 : K_pad / 8;
-    const int64_t big_tiles = tbn_hip::ceil_div(M, 128) * tbn_hip::ceil_div(N, 128);
-    if (big_tiles >= 512) {
+    const int64_t big_tiles = tbn_hip::ceil_div(M, CfgBig::BR) * tbn_hip::ceil_div(N, CfgBig::BC);
+    if (big_tiles >= 256) {
         SignPacked<CfgBig::BC, CfgBig::NT, TERNARY> coll{packed, col_bytes, static_cast<int>(N_pad)};
         return launch_gemm<CfgBig>(A, lda, int(M), int(N), int(K), coll, epi,
                                    tbn_hip::stream_of(stream), what);

@@ -36,9 +36,10 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int BK = 32;           // K elements staged per LDS round
 constexpr int LDS_ROW = BK + 8;  // bf16 per LDS row (80 bytes)
 
-template <int BR_, int BC_, int WR_, int WC_>
+template <int BR_, int BC_, int WR_, int WC_, int WAVES_PER_SIMD_ = 1>
 struct TileCfg {
     static constexpr int BR = BR_, BC = BC_, WR = WR_, WC = WC_;
+    static constexpr int WAVES_PER_SIMD = WAVES_PER_SIMD_;  // occupancy the registers must allow
     static constexpr int WAVES_R = BR / WR, WAVES_C = BC / WC;
     static constexpr int NT = 64 * WAVES_R * WAVES_C;
     static constexpr int FR = WR / 32, FC = WC / 32;
@@ -308,7 +309,7 @@ __device__ __forceinline__ void tile_coords(int tiles_r, int tiles_c, int& tr, i
 }
 
 template <class Cfg, class RowL, class ColL, class Epi>
-__global__ void __launch_bounds__(Cfg::NT)
+__global__ void __launch_bounds__(Cfg::NT, Cfg::WAVES_PER_SIMD)
 mfma_tile_kernel(RowL rowl, ColL coll, Epi epi, int K, int tiles_r, int tiles_c) {
     __shared__ __attribute__((aligned(16))) uint16_t lds_r[RowL::PIECES * Cfg::BR * LDS_ROW];
     __shared__ __attribute__((aligned(16))) uint16_t lds_c[ColL::PIECES * Cfg::BC * LDS_ROW];
