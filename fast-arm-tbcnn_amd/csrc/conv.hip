@@ -147,6 +147,7 @@ struct ConvEpi {
     const float* scale;
     float alpha;
     const float* bias;
+    const float* residual;  // same layout as y (unpooled only), may be null
     int flags;
 
     template <class Cfg>
@@ -180,6 +181,7 @@ struct ConvEpi {
                         const float mult = scale ? alpha * scale[m] : alpha;
                         const float b = bias ? bias[m] : 0.0f;
                         v = (flags & TBN_EPI_BIAS_THEN_SCALE) ? (v + b) * mult : v * mult + b;
+                        if (residual && valid_q) v += residual[out_base + static_cast<int64_t>(m) * plane];
                         if (flags & TBN_EPI_RELU) v = v > 0.0f ? v : 0.0f;
                     }
                     if (pool) {
@@ -254,8 +256,8 @@ int make_geom(const tbn_conv2d_desc* d, int flags, ConvGeom& g) {
 
 template <bool TERNARY>
 int conv_quant(const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed, int64_t K_pad,
-               int64_t N_pad, const float* scale, float alpha, const float* bias, int flags,
-               float* y, tbn_stream_t stream) {
+               int64_t N_pad, const float* scale, float alpha, const float* bias,
+               const float* residual, int flags, float* y, tbn_stream_t stream) {
     const char* what = TERNARY ? "conv2d_f32_ternary" : "conv2d_f32_binary";
     ConvGeom g;
     int rc = make_geom(desc, flags, g);
@@ -265,10 +267,12 @@ int conv_quant(const float* x, const tbn_conv2d_desc* desc, const uint8_t* packe
     TBN_REQUIRE(K_pad >= g.K && K_pad % 32 == 0, TBN_INVALID_SHAPE,
                 "K_pad must be >= C*kh*kw and a multiple of 32");
     TBN_REQUIRE(N_pad >= desc->m, TBN_INVALID_SHAPE, "N_pad must be >= output channels");
+    TBN_REQUIRE(!(residual && g.pool), TBN_INVALID_ARGUMENT,
+                "a residual input cannot be combined with the fused max pool");
     if (g.Q == 0) return tbn_hip::ok();
     TBN_REQUIRE(x && packed && y, TBN_INVALID_ARGUMENT, "null pointer");
     TBN_DEVICE_GUARD();
-    ConvEpi epi{y, int(desc->m), g, scale, alpha, bias, flags};
+    ConvEpi epi{y, int(desc->m), g, scale, alpha, bias, residual, flags};
     const int64_t col_bytes = TERNARY ? K_pad / 4 : K_pad / 8;
     hipStream_t s = tbn_hip::stream_of(stream);
     const int m = int(desc->m);
@@ -292,13 +296,28 @@ extern "C" {
 int tbn_hip_conv2d_f32_binary(const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed,
                               int64_t K_pad, int64_t N_pad, const float* scale, float alpha,
                               const float* bias, int flags, float* y, tbn_stream_t stream) {
-    return conv_quant<false>(x, desc, packed, K_pad, N_pad, scale, alpha, bias, flags, y, stream);
+    return conv_quant<false>(x, desc, packed, K_pad, N_pad, scale, alpha, bias, nullptr, flags, y,
+                             stream);
 }
 
 int tbn_hip_conv2d_f32_ternary(const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed,
                                int64_t K_pad, int64_t N_pad, const float* scale, float alpha,
                                const float* bias, int flags, float* y, tbn_stream_t stream) {
-    return conv_quant<true>(x, desc, packed, K_pad, N_pad, scale, alpha, bias, flags, y, stream);
+    return conv_quant<true>(x, desc, packed, K_pad, N_pad, scale, alpha, bias, nullptr, flags, y,
+                            stream);
+}
+
+int tbn_hip_conv2d_f32_quantized(int weights, const float* x, const tbn_conv2d_desc* desc,
+                                 const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                                 const float* scale, float alpha, const float* bias,
+                                 const float* residual, int flags, float* y, tbn_stream_t stream) {
+    if (weights == TBN_WEIGHTS_BINARY)
+        return conv_quant<false>(x, desc, packed, K_pad, N_pad, scale, alpha, bias, residual, flags,
+                                 y, stream);
+    if (weights == TBN_WEIGHTS_TERNARY)
+        return conv_quant<true>(x, desc, packed, K_pad, N_pad, scale, alpha, bias, residual, flags,
+                                y, stream);
+    return tbn_hip::fail(TBN_INVALID_ARGUMENT, "unknown weights kind");
 }
 
 int tbn_hip_conv2d_f32(const float* x, const tbn_conv2d_desc* desc, const float* w,
@@ -311,7 +330,7 @@ int tbn_hip_conv2d_f32(const float* x, const tbn_conv2d_desc* desc, const float*
     if (g.Q == 0) return tbn_hip::ok();
     TBN_REQUIRE(x && w && y, TBN_INVALID_ARGUMENT, "null pointer");
     TBN_DEVICE_GUARD();
-    ConvEpi epi{y, int(desc->m), g, nullptr, 1.0f, bias, flags};
+    ConvEpi epi{y, int(desc->m), g, nullptr, 1.0f, bias, nullptr, flags};
     hipStream_t s = tbn_hip::stream_of(stream);
     const int m = int(desc->m);
     auto make_rows = [&](auto& rowl) {

@@ -76,7 +76,8 @@ int launch_gemm(const float* A, int64_t lda, int M, int N, int K, const ColL& co
 template <bool TERNARY>
 int gemm_quant(const float* A, int64_t lda, int64_t M, int64_t N, int64_t K, const uint8_t* packed,
                int64_t K_pad, int64_t N_pad, const float* scale, float alpha, const float* bias,
-               int flags, float* C, int64_t ldc, tbn_stream_t stream) {
+               const float* cin, int cin_1d, float beta, int flags, float* C, int64_t ldc,
+               tbn_stream_t stream) {
     const char* what = TERNARY ? "gemm_f32_ternary" : "gemm_f32_binary";
     TBN_REQUIRE(M >= 0 && N >= 0 && K >= 0, TBN_INVALID_SHAPE, "M, N, K must be non-negative");
     TBN_REQUIRE(M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31), TBN_INVALID_SHAPE,
@@ -93,7 +94,7 @@ int gemm_quant(const float* A, int64_t lda, int64_t M, int64_t N, int64_t K, con
     TBN_DEVICE_GUARD();
 
     GemmEpi epi{C, ldc, static_cast<int>(M), static_cast<int>(N), scale, alpha, bias,
-                nullptr, 0.0f, 0, flags};
+                (cin && beta != 0.0f) ? cin : nullptr, beta, cin_1d, flags};
     const int64_t col_bytes = TERNARY ? K_pad / 4 : K_pad / 8;
     const int64_t big_tiles = tbn_hip::ceil_div(M, CfgBig::BR) * tbn_hip::ceil_div(N, CfgBig::BC);
     if (big_tiles >= 256) {
@@ -114,16 +115,30 @@ int tbn_hip_gemm_f32_binary(const float* A, int64_t lda, int64_t M, int64_t N, i
                             const uint8_t* packed, int64_t K_pad, int64_t N_pad,
                             const float* scale, float alpha, const float* bias, int flags,
                             float* C, int64_t ldc, tbn_stream_t stream) {
-    return gemm_quant<false>(A, lda, M, N, K, packed, K_pad, N_pad, scale, alpha, bias, flags, C,
-                             ldc, stream);
+    return gemm_quant<false>(A, lda, M, N, K, packed, K_pad, N_pad, scale, alpha, bias, nullptr, 0,
+                             0.0f, flags, C, ldc, stream);
 }
 
 int tbn_hip_gemm_f32_ternary(const float* A, int64_t lda, int64_t M, int64_t N, int64_t K,
                              const uint8_t* packed, int64_t K_pad, int64_t N_pad,
                              const float* scale, float alpha, const float* bias, int flags,
                              float* C, int64_t ldc, tbn_stream_t stream) {
-    return gemm_quant<true>(A, lda, M, N, K, packed, K_pad, N_pad, scale, alpha, bias, flags, C,
-                            ldc, stream);
+    return gemm_quant<true>(A, lda, M, N, K, packed, K_pad, N_pad, scale, alpha, bias, nullptr, 0,
+                            0.0f, flags, C, ldc, stream);
+}
+
+int tbn_hip_gemm_f32_quantized(int weights, const float* A, int64_t lda, int64_t M, int64_t N,
+                               int64_t K, const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                               const float* scale, float alpha, const float* bias, const float* cin,
+                               int cin_1d, float beta, int flags, float* C, int64_t ldc,
+                               tbn_stream_t stream) {
+    if (weights == TBN_WEIGHTS_BINARY)
+        return gemm_quant<false>(A, lda, M, N, K, packed, K_pad, N_pad, scale, alpha, bias, cin,
+                                 cin_1d, beta, flags, C, ldc, stream);
+    if (weights == TBN_WEIGHTS_TERNARY)
+        return gemm_quant<true>(A, lda, M, N, K, packed, K_pad, N_pad, scale, alpha, bias, cin,
+                                cin_1d, beta, flags, C, ldc, stream);
+    return tbn_hip::fail(TBN_INVALID_ARGUMENT, "unknown weights kind");
 }
 
 int tbn_hip_gemm_f32(const float* A, const float* B, const float* Cin, int c_is_1d, int64_t M,

@@ -1,5 +1,6 @@
 // Pooling and elementwise operators used between the GEMM/conv layers of a
-// Session (MaxPool, GlobalAveragePool, Add, Relu).  All are HBM-bound; they
+// Session (MaxPool, GlobalAveragePool, Add, Relu, Sub/Greater/Less and the
+// ternary Relu replacement).  All are HBM-bound; they
 // keep the reference's arithmetic order where it fixes the rounding
 // (GlobalAveragePool sums each plane sequentially, as pooling.cpp:200-212).
 #include <string>
@@ -77,9 +78,61 @@ __global__ void relu_kernel(const float* __restrict__ x, int64_t n, float* __res
     }
 }
 
+// Sub / Greater / Less of the Session (model.hpp:1176-1300): the right
+// operand is b[i % nb] when b is given, else the scalar.
+__global__ void elementwise_kernel(int op, const float* __restrict__ a, int64_t n,
+                                   const float* __restrict__ b, int64_t nb, float scalar,
+                                   float* __restrict__ y) {
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < n;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const float r = b ? b[t % nb] : scalar;
+        const float l = a[t];
+        float v;
+        if (op == TBN_OP_SUB) v = l - r;
+        else if (op == TBN_OP_GREATER) v = (l > r) ? 1.0f : 0.0f;
+        else v = (l < r) ? 1.0f : 0.0f;
+        y[t] = v;
+    }
+}
+
+// The Session's ternary Relu replacement (model.hpp:1144-1165):
+// x > t -> 1, x < -t -> -1, else 0 (NaN -> 0).
+__global__ void ternary_activation_kernel(const float* __restrict__ x, int64_t n, float t,
+                                          float* __restrict__ y) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float v = x[i];
+        y[i] = (v > t) ? 1.0f : ((v < -t) ? -1.0f : 0.0f);
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+int tbn_hip_elementwise(int op, const float* a, int64_t n, const float* b, int64_t nb, float scalar,
+                        float* y, tbn_stream_t stream) {
+    TBN_REQUIRE(op == TBN_OP_SUB || op == TBN_OP_GREATER || op == TBN_OP_LESS, TBN_INVALID_ARGUMENT,
+                "unknown elementwise op");
+    TBN_REQUIRE(n >= 0 && (b == nullptr || nb > 0), TBN_INVALID_SHAPE, "invalid sizes");
+    if (n == 0) return tbn_hip::ok();
+    TBN_REQUIRE(a && y, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    hipLaunchKernelGGL(elementwise_kernel, dim3(grid_for(n)), dim3(kThreads), 0,
+                       tbn_hip::stream_of(stream), op, a, n, b, nb, scalar, y);
+    return tbn_hip::check_launch("elementwise");
+}
+
+int tbn_hip_ternary_activation(const float* x, int64_t n, float threshold, float* y,
+                               tbn_stream_t stream) {
+    TBN_REQUIRE(n >= 0, TBN_INVALID_SHAPE, "n must be non-negative");
+    if (n == 0) return tbn_hip::ok();
+    TBN_REQUIRE(x && y, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    hipLaunchKernelGGL(ternary_activation_kernel, dim3(grid_for(n)), dim3(kThreads), 0,
+                       tbn_hip::stream_of(stream), x, n, threshold, y);
+    return tbn_hip::check_launch("ternary_activation");
+}
 
 int tbn_hip_maxpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, int64_t kh,
                       int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh,

@@ -32,6 +32,11 @@ EPI_NONE = 0
 EPI_RELU = 1
 EPI_BIAS_THEN_SCALE = 2
 EPI_MAXPOOL2X2 = 4
+WEIGHTS_BINARY = 0
+WEIGHTS_TERNARY = 1
+OP_SUB = 0
+OP_GREATER = 1
+OP_LESS = 2
 
 
 class TbnError(RuntimeError):
@@ -79,6 +84,12 @@ _SIGNATURES = {
     "tbn_hip_global_avgpool2d": ([_P, _I64, _I64, _I64, _I64, _P, _P], _I32),
     "tbn_hip_add": ([_P, _P, _I64, _I64, _I64, _I64, _I32, _P, _P], _I32),
     "tbn_hip_relu": ([_P, _I64, _P, _P], _I32),
+    "tbn_hip_gemm_f32_quantized": ([_I32, _P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _F32, _P, _P, _I32,
+                                    _F32, _I32, _P, _I64, _P], _I32),
+    "tbn_hip_conv2d_f32_quantized": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _I64, _I64, _P, _F32, _P, _P,
+                                      _I32, _P, _P], _I32),
+    "tbn_hip_elementwise": ([_I32, _P, _I64, _P, _I64, _F32, _P, _P], _I32),
+    "tbn_hip_ternary_activation": ([_P, _I64, _F32, _P, _P], _I32),
 }
 
 _lib = None

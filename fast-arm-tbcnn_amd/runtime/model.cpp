@@ -1,0 +1,1114 @@
+// TBNModel and the device-resident TBNModel::Session.
+//
+// The Session compiles the graph once per (quantization flag, input shapes):
+//   1. lowering   every node becomes an Op with resolved value ids, output
+//                 shapes and, for quantized layers, packed device weights
+//                 (computed once and cached by initializer name for the
+//                 Session's lifetime);
+//   2. fusion     Relu into the preceding Conv/Gemm/Add, a 2x2/2 MaxPool into
+//                 the preceding Conv, and a residual Add (+ Relu) into the
+//                 preceding quantized Conv, each only when the intermediate
+//                 value has no other reader and is not a graph output;
+//   3. memory     every activation gets an offset in one device arena, chosen
+//                 greedily so values with overlapping lifetimes never share
+//                 bytes; Reshape / Flatten / Cast are views (no copy);
+//   4. launch     the ops become a list of C ABI calls on the current stream,
+//                 optionally recorded once into a HIP graph and replayed.
+// The arithmetic of each op follows the reference's execute_* functions
+// (tbn-runtime/include/tbn/runtime/model.hpp:277-1300) in mode F32.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <functional>
+#include <map>
+#include <set>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "internal.hpp"
+#include "tbn/device.hpp"
+#include "tbn/model.hpp"
+#include "tbn/session.hpp"
+#include "tbn_hip.h"
+
+namespace tbn {
+
+// ===========================================================================
+// TBNModel
+// ===========================================================================
+
+TBNModel::TBNModel() : graph_(std::make_shared<ModelGraph>()) {}
+TBNModel::TBNModel(std::shared_ptr<ModelGraph> graph) : graph_(std::move(graph)) {
+    TBN_CHECK(graph_ != nullptr, InvalidArgumentError, "graph is null");
+}
+
+bool TBNModel::has_input(const std::string& name) const {
+    return std::find(graph_->inputs.begin(), graph_->inputs.end(), name) != graph_->inputs.end();
+}
+
+bool TBNModel::has_output(const std::string& name) const {
+    return std::find(graph_->outputs.begin(), graph_->outputs.end(), name) != graph_->outputs.end();
+}
+
+const Shape& TBNModel::get_input_shape(const std::string& name) const {
+    auto it = graph_->value_info.find(name);
+    TBN_CHECK(it != graph_->value_info.end(), InvalidArgumentError, "Input '" + name + "' not found in model");
+    return it->second;
+}
+
+const Shape& TBNModel::get_output_shape(const std::string& name) const {
+    auto it = graph_->value_info.find(name);
+    TBN_CHECK(it != graph_->value_info.end(), InvalidArgumentError, "Output '" + name + "' not found in model");
+    return it->second;
+}
+
+void TBNModel::validate() const {
+    TBN_CHECK(!graph_->inputs.empty(), InvalidModelError, "Model has no inputs");
+    TBN_CHECK(!graph_->outputs.empty(), InvalidModelError, "Model has no outputs");
+    TBN_CHECK(!graph_->nodes.empty(), InvalidModelError, "Model has no computation nodes");
+    for (const auto& in : graph_->inputs)
+        TBN_CHECK(graph_->value_info.count(in) > 0, InvalidModelError, "Input '" + in + "' shape not defined");
+    for (const auto& out : graph_->outputs)
+        TBN_CHECK(graph_->value_info.count(out) > 0, InvalidModelError, "Output '" + out + "' shape not defined");
+    for (const auto& node : graph_->nodes) {
+        for (const auto& in : node.inputs)
+            TBN_CHECK(graph_->value_info.count(in) > 0 || graph_->initializers.count(in) > 0, InvalidModelError,
+                      "Node input '" + in + "' not defined");
+        for (const auto& out : node.outputs)
+            TBN_CHECK(graph_->value_info.count(out) > 0, InvalidModelError,
+                      "Node output '" + out + "' shape not defined");
+    }
+}
+
+TBNModel load_model(const std::string& path) {
+    throw NotImplementedError("load_model('" + path +
+                              "'): the ONNX loader is not part of this library; build a ModelGraph instead");
+}
+
+const char* get_version() { return "0.1.0"; }
+
+// ===========================================================================
+// Session internals
+// ===========================================================================
+
+namespace {
+
+tbn_stream_t cur_stream() { return device::current_stream(); }
+
+// ---- attribute helpers ------------------------------------------------------
+
+const AttributeValue* find_attr(const ModelNode& n, const char* key) {
+    auto it = n.attributes.find(key);
+    return it == n.attributes.end() ? nullptr : &it->second;
+}
+
+bool quantize_allowed(const ModelNode& n) {
+    const AttributeValue* a = find_attr(n, "tbn_quantize");
+    return !(a && a->is_int() && a->as_int() == 0);
+}
+
+// Conv2DParams from ONNX attributes as execute_conv reads them (model.hpp:296-352).
+Conv2DParams conv_params(const ModelNode& node, const Shape& w) {
+    Conv2DParams p;
+    p.kernel_h = w.dims[2];
+    p.kernel_w = w.dims[3];
+    if (auto a = find_attr(node, "strides"); a && a->is_ints() && a->as_ints().size() >= 2) {
+        p.stride_h = a->as_ints()[0];
+        p.stride_w = a->as_ints()[1];
+    }
+    if (auto a = find_attr(node, "pads"); a && a->is_ints() && a->as_ints().size() >= 4) {
+        p.pad_h = a->as_ints()[0];
+        p.pad_w = a->as_ints()[1];
+    }
+    if (auto a = find_attr(node, "auto_pad"); a && a->is_string() &&
+        (a->as_string() == "SAME_UPPER" || a->as_string() == "SAME_LOWER")) {
+        p.pad_h = (p.kernel_h - 1) * p.dilation_h / 2;
+        p.pad_w = (p.kernel_w - 1) * p.dilation_w / 2;
+    }
+    if (auto a = find_attr(node, "dilations"); a && a->is_ints() && a->as_ints().size() >= 2) {
+        p.dilation_h = a->as_ints()[0];
+        p.dilation_w = a->as_ints()[1];
+    }
+    if (auto a = find_attr(node, "group"); a && a->is_int()) p.groups = a->as_int();
+    return p;
+}
+
+// Pool2DParams as execute_maxpool reads them (model.hpp:577-628): strides
+// default to the kernel size.
+Pool2DParams pool_params(const ModelNode& node) {
+    Pool2DParams p;
+    if (auto a = find_attr(node, "kernel_shape"); a && a->is_ints() && a->as_ints().size() >= 2) {
+        p.kernel_h = a->as_ints()[0];
+        p.kernel_w = a->as_ints()[1];
+    }
+    if (auto a = find_attr(node, "strides"); a && a->is_ints()) {
+        if (a->as_ints().size() >= 2) {
+            p.stride_h = a->as_ints()[0];
+            p.stride_w = a->as_ints()[1];
+        }
+    } else {
+        p.stride_h = p.kernel_h;
+        p.stride_w = p.kernel_w;
+    }
+    if (auto a = find_attr(node, "pads"); a && a->is_ints() && a->as_ints().size() >= 4) {
+        p.pad_h = a->as_ints()[0];
+        p.pad_w = a->as_ints()[1];
+    }
+    if (auto a = find_attr(node, "ceil_mode"); a && a->is_int()) p.ceil_mode = a->as_int() != 0;
+    return p;
+}
+
+// ---- the lowered program ---------------------------------------------------
+
+enum class OpKind {
+    ConvF32,
+    ConvQuant,
+    GemmF32,
+    GemmQuant,
+    Add,
+    Relu,
+    TernaryAct,
+    MaxPool,
+    GlobalAvgPool,
+    Elementwise,
+    View,
+};
+
+struct Op {
+    OpKind kind;
+    std::string node;        // node name (for error messages)
+    std::vector<int> in;     // value ids read
+    int out = -1;            // value id written
+    bool dead = false;       // removed by fusion
+    // conv
+    tbn_conv2d_desc desc{};
+    int flags = 0;
+    int residual = -1;       // value id of a fused residual addend
+    const PackedWeights* pw = nullptr;
+    const float* scale = nullptr;  // per-channel scale (device)
+    const float* w = nullptr;      // fp32 weights (device)
+    const float* bias = nullptr;   // device
+    // gemm
+    int64_t M = 0, K = 0, N = 0;
+    float alpha = 1.0f, beta = 0.0f;
+    bool transA = false, transB = false;
+    const float* cin = nullptr;    // constant addend (device) or null
+    int cin_value = -1;            // or an activation addend
+    int cin_1d = 0;
+    // pooling / elementwise
+    Pool2DParams pool;
+    int64_t outer = 0, inner = 0, rest = 0;
+    int elem_op = 0;
+    float scalar = 0.0f;
+    int rhs_value = -1;
+    int64_t rhs_n = 0;
+    const float* rhs_const = nullptr;
+};
+
+struct Value {
+    std::string name;
+    Shape shape;
+    DataType dtype = DataType::FLOAT32;
+    bool is_const = false;   // initializer: lives in the weight cache
+    bool is_input = false;
+    int view_of = -1;        // storage shared with another value
+    const void* const_ptr = nullptr;
+    int64_t offset = -1;     // arena offset (bytes)
+    int def = -1, last = -1; // op index of definition and last use
+};
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+
+struct TBNModel::Session::Impl {
+    std::shared_ptr<ModelGraph> graph;
+    TilingParams tiling;
+    bool quant = false;
+    bool graph_replay = false;
+    std::unordered_map<std::string, Tensor> inputs;
+
+    // ---- caches that live as long as the Session ----
+    std::unordered_map<std::string, Tensor> dev_init;          // uploaded initializers
+    std::unordered_map<std::string, std::vector<float>> channel_scales;  // host copy of mean|w|
+    std::unordered_map<std::string, Tensor> dev_scales;        // device per-channel scales
+    std::unordered_map<std::string, bool> conv_already_binary;
+    std::unordered_map<std::string, PackedWeights> packed;      // key: name + "#" + variant
+    std::unordered_map<std::string, Tensor> scaled_addends;     // beta * C of quantized Gemms
+
+    // ---- the compiled plan ----
+    bool planned = false;
+    bool plan_quant = false;
+    std::map<std::string, Shape> plan_shapes;
+    std::vector<Value> values;
+    std::unordered_map<std::string, int> value_id;
+    std::vector<Op> ops;
+    Tensor arena;
+    size_t launches = 0;
+    hipStream_t replay_stream = nullptr;
+    hipGraph_t hip_graph = nullptr;
+    hipGraphExec_t hip_graph_exec = nullptr;
+    int eager_runs = 0;
+
+    ~Impl() { drop_graph(); if (replay_stream) (void)hipStreamDestroy(replay_stream); }
+
+    void drop_graph() {
+        if (hip_graph_exec) (void)hipGraphExecDestroy(hip_graph_exec);
+        if (hip_graph) (void)hipGraphDestroy(hip_graph);
+        hip_graph_exec = nullptr;
+        hip_graph = nullptr;
+    }
+
+    // ---- weight helpers ------------------------------------------------------
+
+    const Tensor& initializer(const std::string& name) const {
+        auto it = graph->initializers.find(name);
+        TBN_CHECK(it != graph->initializers.end(), RuntimeError, "initializer '" + name + "' not found");
+        return it->second;
+    }
+
+    const Tensor& device_init(const std::string& name) {
+        auto it = dev_init.find(name);
+        if (it != dev_init.end()) return it->second;
+        const Tensor& t = initializer(name);
+        return dev_init.emplace(name, t.on_device() ? t : t.to_device(DeviceType::HIP)).first->second;
+    }
+
+    std::vector<float> host_floats(const std::string& name) const {
+        return initializer(name).to_vector<float>();
+    }
+
+    // Per-channel mean|w| computed on the device with the Session's sequential
+    // fp32 sum (model.hpp:383-395), plus the "already binary" test
+    // (model.hpp:396-410) on the host copy of the weights.
+    void conv_scales(const std::string& wname) {
+        if (conv_already_binary.count(wname)) return;
+        const Tensor& w = device_init(wname);
+        const int64_t ch = w.shape().dims[0];
+        const int64_t per = w.num_elements() / ch;
+        Tensor s = Tensor::empty({ch}, DataType::FLOAT32, DeviceType::HIP);
+        check_status(tbn_hip_channel_mean_abs(w.typed_data<float>(), ch, per, s.typed_data<float>(), cur_stream()),
+                     "channel_mean_abs");
+        std::vector<float> hs = s.to_vector<float>();
+        const std::vector<float> hw = host_floats(wname);
+        bool already = true;
+        for (int64_t c = 0; c < ch && already; ++c) {
+            const float scale = hs[c];
+            int64_t near = 0;
+            for (int64_t i = 0; i < per; ++i) {
+                const float v = hw[c * per + i];
+                const float expected = (v >= 0) ? scale : -scale;
+                if (std::abs(v - expected) < 0.01f * scale || std::abs(v) < 0.01f) ++near;
+            }
+            if (near < per * 0.9f) already = false;
+        }
+        channel_scales[wname] = hs;
+        dev_scales[wname] = s;
+        conv_already_binary[wname] = already;
+    }
+
+    const PackedWeights& packed_binary(const std::string& wname, bool nk, int rule) {
+        // rule: 0 = BINARY bytes, 1 = float w > 0, 2 = float w >= 0
+        const std::string key = wname + "#b" + std::to_string(nk) + std::to_string(rule);
+        auto it = packed.find(key);
+        if (it != packed.end()) return it->second;
+        return packed.emplace(key, pack_binary_weights(device_init(wname), nk, rule == 2)).first->second;
+    }
+
+    const PackedWeights& packed_ternary(const std::string& wname, bool nk) {
+        const std::string key = wname + "#t" + std::to_string(nk);
+        auto it = packed.find(key);
+        if (it != packed.end()) return it->second;
+        return packed.emplace(key, pack_ternary_weights(device_init(wname), nk)).first->second;
+    }
+
+    // The quantized Gemm's "already binary" test samples about 1000 values for
+    // exact -1, 1, 0, 0.999, -0.999 (model.hpp:765-786).
+    bool gemm_already_binary(const std::string& bname) {
+        const std::vector<float> b = host_floats(bname);
+        const int64_t n = static_cast<int64_t>(b.size());
+        const int64_t step = std::max<int64_t>(1, n / 1000);
+        for (int64_t i = 0; i < n; i += step) {
+            const float v = b[i];
+            if (v != -1.0f && v != 1.0f && v != 0.0f && v != 0.999f && v != -0.999f) return false;
+        }
+        return true;
+    }
+
+    // ---- compilation ---------------------------------------------------------------
+
+    int new_value(const std::string& name, const Shape& shape, DataType dt) {
+        Value v;
+        v.name = name;
+        v.shape = shape;
+        v.dtype = dt;
+        values.push_back(v);
+        value_id[name] = static_cast<int>(values.size()) - 1;
+        return value_id[name];
+    }
+
+    int lookup(const std::string& name, const std::string& node) {
+        auto it = value_id.find(name);
+        if (it != value_id.end()) return it->second;
+        auto init = graph->initializers.find(name);
+        TBN_CHECK(init != graph->initializers.end(), RuntimeError,
+                  "node '" + node + "': input '" + name + "' not found");
+        int id = new_value(name, init->second.shape(), init->second.dtype());
+        values[id].is_const = true;
+        values[id].const_ptr = device_init(name).data();
+        return id;
+    }
+
+    const float* const_f32(int id) const { return static_cast<const float*>(values[id].const_ptr); }
+
+    void lower_conv(const ModelNode& node) {
+        TBN_CHECK(node.inputs.size() >= 2, InvalidArgumentError, "Conv expects at least 2 inputs");
+        TBN_CHECK(node.outputs.size() == 1, InvalidArgumentError, "Conv expects 1 output");
+        const int xi = lookup(node.inputs[0], node.name);
+        const std::string& wname = node.inputs[1];
+        TBN_CHECK(graph->initializers.count(wname), NotImplementedError,
+                  "Conv '" + node.name + "': weights must be an initializer");
+        const int wi = lookup(wname, node.name);
+        const Shape& xs = values[xi].shape;
+        const Shape& ws = values[wi].shape;
+        TBN_CHECK(xs.rank() == 4, InvalidShapeError, "Conv input must be 4D (NCHW), got " + shape_to_string(xs));
+        TBN_CHECK(ws.rank() == 4, InvalidShapeError, "Conv weights must be 4D, got " + shape_to_string(ws));
+        const Conv2DParams p = conv_params(node, ws);
+        TBN_CHECK(p.groups == 1, NotImplementedError, "Conv '" + node.name + "': grouped convolution is not supported");
+        TBN_CHECK(xs.dims[1] == ws.dims[1], InvalidShapeError, "Conv '" + node.name + "': channel mismatch");
+        Op op;
+        op.node = node.name;
+        op.in.push_back(xi);
+        op.desc = tbn_conv2d_desc{xs.dims[0], xs.dims[1], xs.dims[2], xs.dims[3], ws.dims[0], ws.dims[2],
+                                  ws.dims[3], p.stride_h, p.stride_w, p.pad_h, p.pad_w, p.dilation_h, p.dilation_w};
+        const int64_t OH = (xs.dims[2] + 2 * p.pad_h - p.dilation_h * (ws.dims[2] - 1) - 1) / p.stride_h + 1;
+        const int64_t OW = (xs.dims[3] + 2 * p.pad_w - p.dilation_w * (ws.dims[3] - 1) - 1) / p.stride_w + 1;
+        TBN_CHECK(OH > 0 && OW > 0, InvalidShapeError, "Conv '" + node.name + "': invalid output dimensions");
+        if (node.inputs.size() >= 3 && !node.inputs[2].empty()) {
+            const int bi = lookup(node.inputs[2], node.name);
+            TBN_CHECK(values[bi].is_const, NotImplementedError, "Conv '" + node.name + "': bias must be an initializer");
+            TBN_CHECK(values[bi].shape.size() == ws.dims[0], InvalidShapeError,
+                      "Conv '" + node.name + "': bias size must equal the output channels");
+            op.bias = const_f32(bi);
+        }
+        const DataType wt = values[wi].dtype;
+        if (wt == DataType::BINARY) {
+            op.kind = OpKind::ConvQuant;
+            op.pw = &packed_binary(wname, true, 0);
+        } else if (wt == DataType::TERNARY) {
+            op.kind = OpKind::ConvQuant;
+            op.pw = &packed_ternary(wname, true);
+        } else if (wt == DataType::FLOAT32 && quant && quantize_allowed(node)) {
+            op.kind = OpKind::ConvQuant;
+            conv_scales(wname);
+            if (conv_already_binary[wname]) {
+                // cached path: signs w >= 0, y = (acc + b) * s[m] (model.hpp:414-559)
+                op.pw = &packed_binary(wname, true, 2);
+                op.scale = dev_scales[wname].typed_data<float>();
+                op.flags |= TBN_EPI_BIAS_THEN_SCALE;
+            } else {
+                // quantize_to_binary(W) (w > 0) then conv2d_binary, no scale (model.hpp:560-564)
+                op.pw = &packed_binary(wname, true, 1);
+            }
+        } else {
+            TBN_CHECK(wt == DataType::FLOAT32, InvalidArgumentError, "Conv '" + node.name + "': unsupported weight type");
+            op.kind = OpKind::ConvF32;
+            op.w = const_f32(wi);
+        }
+        op.out = new_value(node.outputs[0], Shape{xs.dims[0], ws.dims[0], OH, OW}, DataType::FLOAT32);
+        ops.push_back(op);
+    }
+
+    void lower_gemm(const ModelNode& node, bool matmul) {
+        TBN_CHECK(node.inputs.size() >= 2, InvalidArgumentError, "Gemm expects at least 2 inputs");
+        TBN_CHECK(node.outputs.size() == 1, InvalidArgumentError, "Gemm expects 1 output");
+        Op op;
+        op.node = node.name;
+        if (!matmul) {
+            if (auto a = find_attr(node, "alpha"); a && a->is_float()) op.alpha = a->as_float();
+            op.beta = 1.0f;
+            if (auto a = find_attr(node, "beta"); a && a->is_float()) op.beta = a->as_float();
+            if (auto a = find_attr(node, "transA"); a && a->is_int()) op.transA = a->as_int() != 0;
+            if (auto a = find_attr(node, "transB"); a && a->is_int()) op.transB = a->as_int() != 0;
+        }
+        const int ai = lookup(node.inputs[0], node.name);
+        const int bi = lookup(node.inputs[1], node.name);
+        const Shape& as = values[ai].shape;
+        const Shape& bs = values[bi].shape;
+        if (as.rank() != 2 || bs.rank() != 2) {
+            if (matmul) throw NotImplementedError("MatMul for non-2D tensors not implemented");
+            throw InvalidShapeError("Gemm '" + node.name + "': inputs must be 2-D");
+        }
+        op.M = op.transA ? as.dims[1] : as.dims[0];
+        op.K = op.transA ? as.dims[0] : as.dims[1];
+        const int64_t Kb = op.transB ? bs.dims[1] : bs.dims[0];
+        op.N = op.transB ? bs.dims[0] : bs.dims[1];
+        TBN_CHECK(op.K == Kb, InvalidShapeError, "Gemm '" + node.name + "': inner dimensions differ");
+        op.in = {ai};
+        int ci = -1;
+        if (!matmul && node.inputs.size() >= 3 && !node.inputs[2].empty()) {
+            ci = lookup(node.inputs[2], node.name);
+            const int64_t cn = values[ci].shape.size();
+            op.cin_1d = values[ci].shape.rank() == 1 ? 1 : 0;
+            TBN_CHECK(op.cin_1d ? cn == op.N : cn == op.M * op.N, InvalidShapeError,
+                      "Gemm '" + node.name + "': C must be [N] or [M, N]");
+        }
+        const bool quantized = quant && quantize_allowed(node) && !matmul && values[bi].dtype == DataType::FLOAT32 &&
+                               !op.transA && !op.transB;
+        if (quantized) {
+            TBN_CHECK(values[bi].is_const, NotImplementedError, "Gemm '" + node.name + "': B must be an initializer");
+            op.kind = OpKind::GemmQuant;
+            const std::string& bname = node.inputs[1];
+            // already binary: signs w >= 0 (model.hpp:790-841); otherwise
+            // quantize_to_binary (w > 0) (model.hpp:842-845); scale 1 either way.
+            op.pw = &packed_binary(bname, false, gemm_already_binary(bname) ? 2 : 1);
+            // then result * alpha + beta * C (model.hpp:847-870)
+        } else {
+            op.kind = OpKind::GemmF32;
+            op.in.push_back(bi);
+            TBN_CHECK(values[bi].dtype == DataType::FLOAT32 && values[ai].dtype == DataType::FLOAT32,
+                      InvalidArgumentError, "gemm requires float32 inputs");
+        }
+        if (ci >= 0 && op.beta != 0.0f) {
+            if (values[ci].is_const) op.cin = const_f32(ci);
+            else { op.cin_value = ci; op.in.push_back(ci); }
+        }
+        op.out = new_value(node.outputs[0], Shape{op.M, op.N}, DataType::FLOAT32);
+        ops.push_back(op);
+    }
+
+    void lower_unary(const ModelNode& node, OpKind kind) {
+        TBN_CHECK(node.inputs.size() >= 1 && node.outputs.size() >= 1, InvalidArgumentError,
+                  node.op_type + " expects 1 input and 1 output");
+        const int xi = lookup(node.inputs[0], node.name);
+        Op op;
+        op.kind = kind;
+        op.node = node.name;
+        op.in = {xi};
+        Shape out = values[xi].shape;
+        if (kind == OpKind::MaxPool || kind == OpKind::GlobalAvgPool) {
+            TBN_CHECK(out.rank() == 4, InvalidShapeError, node.op_type + " input must be 4D (NCHW)");
+        }
+        if (kind == OpKind::MaxPool) {
+            op.pool = pool_params(node);
+            const auto& d = out.dims;
+            int64_t hw[2];
+            check_status(tbn_hip_maxpool2d(nullptr, d[0], d[1], d[2], d[3], op.pool.kernel_h, op.pool.kernel_w,
+                                           op.pool.stride_h, op.pool.stride_w, op.pool.pad_h, op.pool.pad_w, 1, 1,
+                                           op.pool.ceil_mode, nullptr, hw, nullptr),
+                         ("MaxPool '" + node.name + "'").c_str());
+            out = Shape{d[0], d[1], hw[0], hw[1]};
+        } else if (kind == OpKind::GlobalAvgPool) {
+            out = Shape{out.dims[0], out.dims[1], 1, 1};
+        } else if (kind == OpKind::TernaryAct) {
+            op.scalar = 0.5f;
+        }
+        op.out = new_value(node.outputs[0], out, DataType::FLOAT32);
+        ops.push_back(op);
+    }
+
+    void lower_view(const ModelNode& node, const Shape& shape) {
+        const int xi = lookup(node.inputs[0], node.name);
+        TBN_CHECK(shape.size() == values[xi].shape.size(), InvalidShapeError,
+                  node.op_type + " '" + node.name + "' changes the element count");
+        Op op;
+        op.kind = OpKind::View;
+        op.node = node.name;
+        op.in = {xi};
+        op.out = new_value(node.outputs[0], shape, values[xi].dtype);
+        values[op.out].view_of = xi;
+        ops.push_back(op);
+    }
+
+    void lower_add(const ModelNode& node) {
+        TBN_CHECK(node.inputs.size() == 2, InvalidArgumentError, "Add expects 2 inputs");
+        TBN_CHECK(node.outputs.size() == 1, InvalidArgumentError, "Add expects 1 output");
+        int ai = lookup(node.inputs[0], node.name);
+        int bi = lookup(node.inputs[1], node.name);
+        if (values[ai].shape.rank() == 1 && values[bi].shape.rank() == 2) std::swap(ai, bi);
+        Op op;
+        op.kind = OpKind::Add;
+        op.node = node.name;
+        op.in = {ai, bi};
+        detail::add_view(values[ai].shape, values[bi].shape, op.outer, op.inner, op.rest);
+        op.out = new_value(node.outputs[0], values[ai].shape, DataType::FLOAT32);
+        ops.push_back(op);
+    }
+
+    void lower_elementwise(const ModelNode& node, int elem_op) {
+        TBN_CHECK(node.inputs.size() == 2 && node.outputs.size() == 1, InvalidArgumentError,
+                  node.op_type + " expects 2 inputs and 1 output");
+        const int ai = lookup(node.inputs[0], node.name);
+        Op op;
+        op.kind = OpKind::Elementwise;
+        op.node = node.name;
+        op.elem_op = elem_op;
+        op.in = {ai};
+        const bool have_rhs = value_id.count(node.inputs[1]) || graph->initializers.count(node.inputs[1]);
+        if (have_rhs) {
+            const int bi = lookup(node.inputs[1], node.name);
+            op.rhs_n = values[bi].shape.size();
+            TBN_CHECK(op.rhs_n > 0, InvalidShapeError, node.op_type + " right operand is empty");
+            if (values[bi].is_const) op.rhs_const = const_f32(bi);
+            else { op.rhs_value = bi; op.in.push_back(bi); }
+        } else {
+            TBN_CHECK(elem_op != TBN_OP_SUB, RuntimeError, "Sub rhs not found");
+            auto a = find_attr(node, "value");
+            op.scalar = a ? a->as_float() : 0.0f;
+        }
+        op.out = new_value(node.outputs[0], values[ai].shape, DataType::FLOAT32);
+        ops.push_back(op);
+    }
+
+    void lower(const ModelNode& node) {
+        const std::string& t = node.op_type;
+        if (t == "Conv") return lower_conv(node);
+        if (t == "Gemm") return lower_gemm(node, false);
+        if (t == "MatMul") return lower_gemm(node, true);
+        if (t == "Add") return lower_add(node);
+        if (t == "Relu") {
+            // the reference turns Relu into a ternary activation (threshold 0.5)
+            // when quantization is on and the input name matches (model.hpp:1144-1165)
+            const bool ternary = quant && (node.inputs[0].find("conv2d_1") != std::string::npos ||
+                                           node.inputs[0].find("conv2_out") != std::string::npos);
+            return lower_unary(node, ternary ? OpKind::TernaryAct : OpKind::Relu);
+        }
+        if (t == "MaxPool") return lower_unary(node, OpKind::MaxPool);
+        if (t == "GlobalAveragePool" || t == "GlobalAvgPool") return lower_unary(node, OpKind::GlobalAvgPool);
+        if (t == "Flatten") {
+            const int xi = lookup(node.inputs[0], node.name);
+            int64_t axis = 1;
+            if (auto a = find_attr(node, "axis"); a && a->is_int()) axis = a->as_int();
+            const auto& d = values[xi].shape.dims;
+            TBN_CHECK(axis >= 0 && axis <= static_cast<int64_t>(d.size()), InvalidArgumentError, "Flatten axis out of range");
+            int64_t outer = 1, inner = 1;
+            for (int64_t i = 0; i < axis; ++i) outer *= d[i];
+            for (size_t i = axis; i < d.size(); ++i) inner *= d[i];
+            return lower_view(node, Shape{outer, inner});
+        }
+        if (t == "Reshape") {
+            const int xi = lookup(node.inputs[0], node.name);
+            Shape s;
+            if (node.inputs.size() >= 2) {
+                auto it = graph->initializers.find(node.inputs[1]);
+                TBN_CHECK(it != graph->initializers.end(), NotImplementedError,
+                          "Reshape '" + node.name + "': the shape must be an initializer");
+                const std::vector<int64_t> dims = it->second.to_vector<int64_t>();
+                s.dims = dims;
+            }
+            int64_t known = 1;
+            int unknown = -1;
+            for (size_t i = 0; i < s.dims.size(); ++i) {
+                if (s.dims[i] == -1) unknown = static_cast<int>(i);
+                else known *= s.dims[i];
+            }
+            if (unknown >= 0) s.dims[unknown] = known ? values[xi].shape.size() / known : 0;
+            return lower_view(node, s);
+        }
+        if (t == "Cast") return lower_view(node, values[lookup(node.inputs[0], node.name)].shape);
+        if (t == "Sub") return lower_elementwise(node, TBN_OP_SUB);
+        if (t == "Greater") return lower_elementwise(node, TBN_OP_GREATER);
+        if (t == "Less") return lower_elementwise(node, TBN_OP_LESS);
+        throw NotImplementedError("Operator '" + t + "' not implemented");
+    }
+
+    // ---- fusion -------------------------------------------------------------------
+
+    std::vector<int> readers(int v) const {
+        std::vector<int> r;
+        for (size_t i = 0; i < ops.size(); ++i)
+            if (!ops[i].dead && std::find(ops[i].in.begin(), ops[i].in.end(), v) != ops[i].in.end())
+                r.push_back(static_cast<int>(i));
+        return r;
+    }
+
+    bool is_output(int v) const {
+        for (const auto& o : graph->outputs)
+            if (value_id.count(o) && value_id.at(o) == v) return true;
+        return false;
+    }
+
+    // The single op reading value v, or -1 when v has several readers, a view
+    // reading it, or is a graph output.
+    int sole_reader(int v) const {
+        if (is_output(v)) return -1;
+        auto r = readers(v);
+        if (r.size() != 1) return -1;
+        return r[0];
+    }
+
+    // Op `victim` is absorbed into op `host`: its output becomes host's output.
+    void absorb(int host, int victim) {
+        ops[victim].dead = true;
+        const int old_out = ops[host].out;
+        ops[host].out = ops[victim].out;
+        (void)old_out;
+    }
+
+    // For Add(conv_out, other) where `other` is produced after the conv but
+    // from values that exist before it (a ResNet projection shortcut in
+    // export order), move other's producer in front of the conv so the add
+    // can be fused into the conv's epilogue.
+    void hoist_residual_producers() {
+        for (size_t a = 0; a < ops.size(); ++a) {
+            if (ops[a].dead || ops[a].kind != OpKind::Add || ops[a].in.size() != 2) continue;
+            for (int side = 0; side < 2; ++side) {
+                const int i = producer(ops[a].in[side]);
+                const int p = producer(ops[a].in[1 - side]);
+                if (i < 0 || p < 0 || ops[i].kind != OpKind::ConvQuant || p < i || p > static_cast<int>(a)) continue;
+                bool ready = true;
+                for (int in : ops[p].in) {
+                    const int q = producer(in);
+                    if (q >= i) ready = false;
+                }
+                if (!ready) continue;
+                Op moved = ops[p];
+                ops.erase(ops.begin() + p);
+                ops.insert(ops.begin() + i, moved);
+                break;
+            }
+        }
+    }
+
+    void fuse() {
+        hoist_residual_producers();
+        for (size_t i = 0; i < ops.size(); ++i) {
+            Op& op = ops[i];
+            if (op.dead) continue;
+            const bool conv = op.kind == OpKind::ConvQuant || op.kind == OpKind::ConvF32;
+            const bool gemm = op.kind == OpKind::GemmQuant || op.kind == OpKind::GemmF32;
+            // residual Add (+Relu) into a quantized conv whose addend is ready
+            if (op.kind == OpKind::ConvQuant && !(op.flags & (TBN_EPI_RELU | TBN_EPI_MAXPOOL2X2))) {
+                int r = sole_reader(op.out);
+                if (r >= 0 && ops[r].kind == OpKind::Add) {
+                    const int other = ops[r].in[0] == op.out ? ops[r].in[1] : ops[r].in[0];
+                    const Value& ov = values[other];
+                    const bool ready = ov.is_const || ov.is_input || producer(other) < static_cast<int>(i);
+                    if (ops[r].in[0] != ops[r].in[1] && ov.shape == values[op.out].shape && ready &&
+                        !ov.is_const) {
+                        op.residual = other;
+                        op.in.push_back(other);
+                        absorb(static_cast<int>(i), r);
+                    }
+                }
+            }
+            // Relu into Conv / Gemm / Add
+            if ((conv || gemm || op.kind == OpKind::Add) && !(op.flags & TBN_EPI_MAXPOOL2X2)) {
+                int r = sole_reader(op.out);
+                if (r >= 0 && ops[r].kind == OpKind::Relu) {
+                    op.flags |= TBN_EPI_RELU;
+                    absorb(static_cast<int>(i), r);
+                }
+            }
+            // 2x2/2 floor MaxPool (with or without a Relu either side) into Conv
+            if (conv && op.residual < 0) {
+                int r = sole_reader(op.out);
+                if (r >= 0 && ops[r].kind == OpKind::MaxPool) {
+                    const Pool2DParams& p = ops[r].pool;
+                    const Shape& s = values[op.out].shape;
+                    if (p.kernel_h == 2 && p.kernel_w == 2 && p.stride_h == 2 && p.stride_w == 2 && p.pad_h == 0 &&
+                        p.pad_w == 0 && s.dims[2] >= 2 && s.dims[3] >= 2) {
+                        op.flags |= TBN_EPI_MAXPOOL2X2;
+                        absorb(static_cast<int>(i), r);
+                        int r2 = sole_reader(op.out);
+                        if (r2 >= 0 && ops[r2].kind == OpKind::Relu && !(op.flags & TBN_EPI_RELU)) {
+                            op.flags |= TBN_EPI_RELU;  // relu(max(x)) = max(relu(x))
+                            absorb(static_cast<int>(i), r2);
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    int producer(int v) const {
+        for (size_t i = 0; i < ops.size(); ++i)
+            if (!ops[i].dead && ops[i].out == v) return static_cast<int>(i);
+        return -1;
+    }
+
+    // ---- memory planning -------------------------------------------------------------
+
+    int root(int v) const {
+        while (values[v].view_of >= 0) v = values[v].view_of;
+        return v;
+    }
+
+    void plan_memory() {
+        const int nops = static_cast<int>(ops.size());
+        for (auto& v : values) { v.def = -1; v.last = -1; v.offset = -1; }
+        for (int i = 0; i < nops; ++i) {
+            if (ops[i].dead) continue;
+            const int o = root(ops[i].out);
+            if (values[o].def < 0) values[o].def = i;
+            values[o].last = std::max(values[o].last, i);
+            for (int in : ops[i].in) values[root(in)].last = std::max(values[root(in)].last, i);
+        }
+        for (const auto& name : graph->outputs) {
+            auto it = value_id.find(name);
+            TBN_CHECK(it != value_id.end(), RuntimeError, "Output '" + name + "' was not produced");
+            values[root(it->second)].last = nops;  // live until the next run
+        }
+        for (auto& v : values)
+            if (v.is_input) { v.def = -1; v.last = std::max(v.last, 0); }
+        // greedy placement, largest first
+        std::vector<int> order;
+        for (size_t i = 0; i < values.size(); ++i) {
+            const Value& v = values[i];
+            if (v.is_const || v.view_of >= 0) continue;
+            if (!v.is_input && v.def < 0) continue;  // never produced (dead)
+            order.push_back(static_cast<int>(i));
+        }
+        auto bytes = [&](int i) { return round_up(values[i].shape.size() * element_size(values[i].dtype), 256); };
+        std::sort(order.begin(), order.end(), [&](int a, int b) { return bytes(a) > bytes(b); });
+        std::vector<int> placed;
+        size_t total = 0;
+        for (int i : order) {
+            const size_t sz = std::max<size_t>(bytes(i), 256);
+            const int d0 = values[i].def, d1 = values[i].last;
+            std::vector<std::pair<size_t, size_t>> busy;
+            for (int j : placed) {
+                const int e0 = values[j].def, e1 = values[j].last;
+                if (d0 <= e1 && e0 <= d1) busy.push_back({static_cast<size_t>(values[j].offset),
+                                                          static_cast<size_t>(values[j].offset) + std::max<size_t>(bytes(j), 256)});
+            }
+            std::sort(busy.begin(), busy.end());
+            size_t off = 0;
+            for (auto& b : busy) {
+                if (off + sz <= b.first) break;
+                off = std::max(off, b.second);
+            }
+            values[i].offset = static_cast<int64_t>(off);
+            total = std::max(total, off + sz);
+            placed.push_back(i);
+        }
+        arena = Tensor::empty({static_cast<int64_t>(std::max<size_t>(total, 256))}, DataType::UINT8, DeviceType::HIP);
+    }
+
+    void* ptr(int v) {
+        const Value& val = values[v];
+        if (val.is_const) return const_cast<void*>(val.const_ptr);
+        const int r = root(v);
+        if (values[r].is_const) return const_cast<void*>(values[r].const_ptr);
+        return static_cast<uint8_t*>(arena.data()) + values[r].offset;
+    }
+    float* fp(int v) { return static_cast<float*>(ptr(v)); }
+
+    void compile() {
+        drop_graph();
+        eager_runs = 0;
+        values.clear();
+        value_id.clear();
+        ops.clear();
+        arena = Tensor();
+        for (const auto& name : graph->inputs) {
+            if (graph->initializers.count(name)) continue;
+            auto it = inputs.find(name);
+            TBN_CHECK(it != inputs.end(), InvalidArgumentError, "Input '" + name + "' not set");
+            int id = new_value(name, it->second.shape(), it->second.dtype());
+            values[id].is_input = true;
+        }
+        for (const auto& node : graph->nodes) lower(node);
+        fuse();
+        plan_memory();
+        launches = 0;
+        for (const auto& op : ops)
+            if (!op.dead && op.kind != OpKind::View) ++launches;
+        planned = true;
+        plan_quant = quant;
+        plan_shapes.clear();
+        for (auto& kv : inputs) plan_shapes[kv.first] = kv.second.shape();
+    }
+
+    bool plan_valid() const {
+        if (!planned || plan_quant != quant) return false;
+        if (plan_shapes.size() != inputs.size()) return false;
+        for (auto& kv : inputs) {
+            auto it = plan_shapes.find(kv.first);
+            if (it == plan_shapes.end() || it->second != kv.second.shape()) return false;
+        }
+        return true;
+    }
+
+    // ---- execution ---------------------------------------------------------------------
+
+    void launch(Op& op, tbn_stream_t s) {
+        const std::string what = "node '" + op.node + "'";
+        switch (op.kind) {
+            case OpKind::View:
+                return;
+            case OpKind::ConvF32:
+                check_status(tbn_hip_conv2d_f32(fp(op.in[0]), &op.desc, op.w, op.bias, op.flags, fp(op.out), s),
+                             what.c_str());
+                return;
+            case OpKind::ConvQuant:
+                check_status(tbn_hip_conv2d_f32_quantized(
+                                 op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY : TBN_WEIGHTS_TERNARY,
+                                 fp(op.in[0]), &op.desc, op.pw->bits.typed_data<uint8_t>(), op.pw->K_pad,
+                                 op.pw->N_pad, op.scale, 1.0f, op.bias, op.residual >= 0 ? fp(op.residual) : nullptr,
+                                 op.flags, fp(op.out), s),
+                             what.c_str());
+                return;
+            case OpKind::GemmQuant: {
+                const float* cin = op.cin ? op.cin : (op.cin_value >= 0 ? fp(op.cin_value) : nullptr);
+                check_status(tbn_hip_gemm_f32_quantized(
+                                 op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY : TBN_WEIGHTS_TERNARY,
+                                 fp(op.in[0]), op.K, op.M, op.N, op.K, op.pw->bits.typed_data<uint8_t>(),
+                                 op.pw->K_pad, op.pw->N_pad, nullptr, op.alpha, nullptr, cin, op.cin_1d, op.beta,
+                                 op.flags, fp(op.out), op.N, s),
+                             what.c_str());
+                return;
+            }
+            case OpKind::GemmF32: {
+                const float* cin = op.cin ? op.cin : (op.cin_value >= 0 ? fp(op.cin_value) : nullptr);
+                check_status(tbn_hip_gemm_f32(fp(op.in[0]), fp(op.in[1]), cin, op.cin_1d, op.M, op.K, op.N, op.alpha,
+                                              cin ? op.beta : 0.0f, op.transA, op.transB, op.flags, fp(op.out), s),
+                             what.c_str());
+                return;
+            }
+            case OpKind::Add:
+                check_status(tbn_hip_add(fp(op.in[0]), fp(op.in[1]), op.outer, op.inner, op.rest, 1, op.flags,
+                                         fp(op.out), s),
+                             what.c_str());
+                return;
+            case OpKind::Relu:
+                check_status(tbn_hip_relu(fp(op.in[0]), values[op.out].shape.size(), fp(op.out), s), what.c_str());
+                return;
+            case OpKind::TernaryAct:
+                check_status(tbn_hip_ternary_activation(fp(op.in[0]), values[op.out].shape.size(), op.scalar,
+                                                        fp(op.out), s),
+                             what.c_str());
+                return;
+            case OpKind::MaxPool: {
+                const auto& d = values[op.in[0]].shape.dims;
+                const Pool2DParams& p = op.pool;
+                check_status(tbn_hip_maxpool2d(fp(op.in[0]), d[0], d[1], d[2], d[3], p.kernel_h, p.kernel_w,
+                                               p.stride_h, p.stride_w, p.pad_h, p.pad_w, 1, 1, p.ceil_mode,
+                                               fp(op.out), nullptr, s),
+                             what.c_str());
+                return;
+            }
+            case OpKind::GlobalAvgPool: {
+                const auto& d = values[op.in[0]].shape.dims;
+                check_status(tbn_hip_global_avgpool2d(fp(op.in[0]), d[0], d[1], d[2], d[3], fp(op.out), s),
+                             what.c_str());
+                return;
+            }
+            case OpKind::Elementwise: {
+                const float* rhs = op.rhs_const ? op.rhs_const : (op.rhs_value >= 0 ? fp(op.rhs_value) : nullptr);
+                check_status(tbn_hip_elementwise(op.elem_op, fp(op.in[0]), values[op.out].shape.size(), rhs,
+                                                 op.rhs_n, op.scalar, fp(op.out), s),
+                             what.c_str());
+                return;
+            }
+        }
+    }
+
+    void upload_inputs(tbn_stream_t s) {
+        for (auto& kv : inputs) {
+            const int id = value_id.at(kv.first);
+            const Tensor& t = kv.second;
+            if (t.on_device()) {
+                if (hipMemcpyAsync(ptr(id), t.data(), t.data_size(), hipMemcpyDeviceToDevice,
+                                   static_cast<hipStream_t>(s)) != hipSuccess)
+                    throw RuntimeError("input copy failed for '" + kv.first + "'");
+            } else {
+                if (hipMemcpyAsync(ptr(id), t.data(), t.data_size(), hipMemcpyHostToDevice,
+                                   static_cast<hipStream_t>(s)) != hipSuccess)
+                    throw RuntimeError("input upload failed for '" + kv.first + "'");
+                if (hipStreamSynchronize(static_cast<hipStream_t>(s)) != hipSuccess)
+                    throw RuntimeError("input upload failed for '" + kv.first + "'");
+            }
+        }
+    }
+
+    void run_ops(tbn_stream_t s) {
+        for (auto& op : ops)
+            if (!op.dead) launch(op, s);
+    }
+
+    void run() {
+        size_t user_inputs = 0;
+        for (const auto& name : graph->inputs)
+            if (!graph->initializers.count(name)) ++user_inputs;
+        TBN_CHECK(inputs.size() == user_inputs, InvalidArgumentError,
+                  "Not all inputs provided (expected " + std::to_string(user_inputs) + ", got " +
+                      std::to_string(inputs.size()) + ")");
+        if (!plan_valid()) compile();
+        tbn_stream_t s = cur_stream();
+        if (!graph_replay) {
+            upload_inputs(s);
+            run_ops(s);
+            return;
+        }
+        // HIP graph replay: the first run is eager (warms every cache), the
+        // second records the ops on a private stream, later runs replay.
+        if (!replay_stream) {
+            if (hipStreamCreate(&replay_stream) != hipSuccess) throw RuntimeError("hipStreamCreate failed");
+        }
+        hipStream_t rs = replay_stream;
+        hipEvent_t ev;
+        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) throw RuntimeError("hipEventCreate failed");
+        // the private stream starts after everything queued on the current stream
+        (void)hipEventRecord(ev, static_cast<hipStream_t>(s));
+        (void)hipStreamWaitEvent(rs, ev, 0);
+        upload_inputs(rs);
+        if (eager_runs < 1) {
+            run_ops(rs);
+            ++eager_runs;
+        } else {
+            if (!hip_graph_exec) {
+                if (hipStreamBeginCapture(rs, hipStreamCaptureModeThreadLocal) != hipSuccess)
+                    throw RuntimeError("hipStreamBeginCapture failed");
+                try {
+                    run_ops(rs);
+                } catch (...) {
+                    hipGraph_t g = nullptr;
+                    (void)hipStreamEndCapture(rs, &g);
+                    if (g) (void)hipGraphDestroy(g);
+                    throw;
+                }
+                if (hipStreamEndCapture(rs, &hip_graph) != hipSuccess) throw RuntimeError("hipStreamEndCapture failed");
+                if (hipGraphInstantiate(&hip_graph_exec, hip_graph, nullptr, nullptr, 0) != hipSuccess)
+                    throw RuntimeError("hipGraphInstantiate failed");
+            }
+            if (hipGraphLaunch(hip_graph_exec, rs) != hipSuccess) throw RuntimeError("hipGraphLaunch failed");
+        }
+        // the current stream continues after the replay
+        (void)hipEventRecord(ev, rs);
+        (void)hipStreamWaitEvent(static_cast<hipStream_t>(s), ev, 0);
+        (void)hipEventDestroy(ev);
+    }
+
+    Tensor output_device(const std::string& name) {
+        TBN_CHECK(planned, InvalidArgumentError, "Output '" + name + "' not available");
+        TBN_CHECK(std::find(graph->outputs.begin(), graph->outputs.end(), name) != graph->outputs.end(),
+                  InvalidArgumentError, "Output '" + name + "' not available");
+        auto it = value_id.find(name);
+        TBN_CHECK(it != value_id.end(), RuntimeError, "Output '" + name + "' was not produced");
+        const Value& v = values[it->second];
+        Tensor view = Tensor::wrap(v.shape, v.dtype, ptr(it->second), DeviceType::HIP);
+        return view;
+    }
+
+    size_t bytes_held() const {
+        size_t b = arena.data_size();
+        for (auto& kv : dev_init) b += kv.second.data_size();
+        for (auto& kv : packed) b += kv.second.bits.data_size();
+        for (auto& kv : dev_scales) b += kv.second.data_size();
+        return b;
+    }
+};
+
+// ===========================================================================
+// Session public interface
+// ===========================================================================
+
+TBNModel::Session::Session(std::shared_ptr<ModelGraph> graph, TilingParams tiling) : impl_(new Impl()) {
+    TBN_CHECK(graph != nullptr, InvalidArgumentError, "graph is null");
+    impl_->graph = std::move(graph);
+    impl_->tiling = tiling;
+}
+
+TBNModel::Session::~Session() = default;
+TBNModel::Session::Session(Session&&) noexcept = default;
+TBNModel::Session& TBNModel::Session::operator=(Session&&) noexcept = default;
+
+void TBNModel::Session::set_quantization(bool enable) { impl_->quant = enable; }
+bool TBNModel::Session::is_quantization_enabled() const { return impl_->quant; }
+void TBNModel::Session::set_tiling(const TilingParams& p) { impl_->tiling = p; }
+const TilingParams& TBNModel::Session::get_tiling() const { return impl_->tiling; }
+
+void TBNModel::Session::set_input(const std::string& name, const Tensor& tensor) {
+    const auto& vi = impl_->graph->value_info;
+    TBN_CHECK(vi.count(name) > 0, InvalidArgumentError, "Input '" + name + "' not found in model");
+    TBN_CHECK(tensor.shape() == vi.at(name), InvalidShapeError, "Input shape mismatch for '" + name + "'");
+    impl_->inputs[name] = tensor;
+}
+
+Tensor TBNModel::Session::get_input(const std::string& name) const {
+    auto it = impl_->inputs.find(name);
+    TBN_CHECK(it != impl_->inputs.end(), InvalidArgumentError, "Input '" + name + "' not set");
+    return it->second;
+}
+
+void TBNModel::Session::run() { impl_->run(); }
+
+Tensor TBNModel::Session::get_output(const std::string& name) const {
+    return impl_->output_device(name).to_device(DeviceType::CPU);
+}
+
+Tensor TBNModel::Session::get_output_device(const std::string& name) const { return impl_->output_device(name); }
+
+void TBNModel::Session::set_graph_replay(bool enable) {
+    if (enable == impl_->graph_replay) return;
+    impl_->graph_replay = enable;
+    impl_->drop_graph();
+    impl_->eager_runs = 0;
+}
+
+void TBNModel::Session::synchronize() const { device::synchronize(); }
+size_t TBNModel::Session::planned_launches() const { return impl_->planned ? impl_->launches : 0; }
+size_t TBNModel::Session::device_bytes() const { return impl_->bytes_held(); }
+
+// ===========================================================================
+// InferenceSession
+// ===========================================================================
+
+InferenceSession::InferenceSession(std::shared_ptr<TBNModel> model, const Options& options)
+    : model_(std::move(model)), options_(options) {}
+
+void InferenceSession::initialize() {
+    TBN_CHECK(model_ != nullptr, InvalidArgumentError, "Model is null");
+    model_->validate();
+    session_ = std::make_unique<TBNModel::Session>(model_->create_session());
+    session_->set_quantization(options_.use_quantization);
+    initialized_ = true;
+}
+
+void InferenceSession::set_input(const std::string& name, const Tensor& tensor) {
+    TBN_CHECK(initialized_, RuntimeError, "Session not initialized");
+    TBN_CHECK(model_->has_input(name), InvalidArgumentError, "Input '" + name + "' not found in model");
+    TBN_CHECK(tensor.shape() == model_->get_input_shape(name), InvalidShapeError,
+              "Input shape mismatch for '" + name + "'");
+    inputs_[name] = tensor;
+}
+
+Tensor InferenceSession::get_input(const std::string& name) const {
+    auto it = inputs_.find(name);
+    TBN_CHECK(it != inputs_.end(), InvalidArgumentError, "Input '" + name + "' not set");
+    return it->second;
+}
+
+void InferenceSession::run() {
+    TBN_CHECK(initialized_, RuntimeError, "Session not initialized");
+    TBN_CHECK(inputs_.size() == model_->inputs().size(), InvalidArgumentError, "Not all inputs provided");
+    const auto t0 = std::chrono::high_resolution_clock::now();
+    for (const auto& kv : inputs_) session_->set_input(kv.first, kv.second);
+    session_->run();
+    outputs_.clear();
+    for (const auto& name : model_->outputs()) outputs_[name] = session_->get_output(name);
+    const auto t1 = std::chrono::high_resolution_clock::now();
+    last_run_us_ = std::chrono::duration<double, std::micro>(t1 - t0).count();
+    if (options_.enable_profiling)
+        std::fprintf(stderr, "[tbn] Inference completed in %.1f us\n", last_run_us_);
+}
+
+Tensor InferenceSession::get_output(const std::string& name) const {
+    auto it = outputs_.find(name);
+    TBN_CHECK(it != outputs_.end(), InvalidArgumentError, "Output '" + name + "' not available");
+    return it->second;
+}
+
+std::unique_ptr<InferenceSession> create_inference_session(std::shared_ptr<TBNModel> model,
+                                                           const InferenceSession::Options& options) {
+    auto s = std::make_unique<InferenceSession>(std::move(model), options);
+    s->initialize();
+    return s;
+}
+
+}  // namespace tbn

@@ -182,6 +182,19 @@ int tbn_hip_gemm_f32_ternary(const float* A, int64_t lda, int64_t M, int64_t N, 
                              const float* scale, float alpha, const float* bias, int flags,
                              float* C, int64_t ldc, tbn_stream_t stream);
 
+/* Weight kinds of the general entry points below. */
+enum tbn_weights_kind { TBN_WEIGHTS_BINARY = 0, TBN_WEIGHTS_TERNARY = 1 };
+
+/* General quantized GEMM used by the Session's quantized Gemm node
+ * (model.hpp:763-870): weights binary or ternary as above, and
+ *   C[m,n] = epi(acc[m,n]) + beta * Cin,  Cin NULL, [N] (cin_1d) or [M, N]
+ * with epi as in tbn_hip_gemm_f32_binary (ReLU, if requested, applies last). */
+int tbn_hip_gemm_f32_quantized(int weights, const float* A, int64_t lda, int64_t M, int64_t N,
+                               int64_t K, const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                               const float* scale, float alpha, const float* bias, const float* cin,
+                               int cin_1d, float beta, int flags, float* C, int64_t ldc,
+                               tbn_stream_t stream);
+
 /* ---- binary / ternary Conv2D (north_star subsystem 3) ---------------------- */
 
 /* Implicit-GEMM convolution, im2col formed on the fly (no column buffer):
@@ -203,6 +216,16 @@ int tbn_hip_conv2d_f32_ternary(const float* x, const tbn_conv2d_desc* desc,
                                const uint8_t* packed, int64_t K_pad, int64_t N_pad,
                                const float* scale, float alpha, const float* bias, int flags,
                                float* y, tbn_stream_t stream);
+
+/* General quantized conv used by the Session: weights binary or ternary, and
+ * an optional `residual` tensor (same [n, m, OH, OW] layout as y) added after
+ * scale and bias and before ReLU -- a Conv followed by a residual Add and Relu
+ * (model.hpp:905-1037,1127-1174) in one pass.  residual excludes
+ * TBN_EPI_MAXPOOL2X2. */
+int tbn_hip_conv2d_f32_quantized(int weights, const float* x, const tbn_conv2d_desc* desc,
+                                 const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                                 const float* scale, float alpha, const float* bias,
+                                 const float* residual, int flags, float* y, tbn_stream_t stream);
 
 /* ---- fp32 layers and epilogue operators (Session support) ------------------ */
 
@@ -232,6 +255,16 @@ int tbn_hip_add(const float* a, const float* b, int64_t outer, int64_t inner, in
                 int64_t outer_b, int flags, float* y, tbn_stream_t stream);
 /* y = max(x, 0) (model.hpp:1166-1171). */
 int tbn_hip_relu(const float* x, int64_t n, float* y, tbn_stream_t stream);
+
+/* Session elementwise ops (model.hpp:1176-1300), r = b ? b[i % nb] : scalar:
+ *   TBN_OP_SUB y = a - r;  TBN_OP_GREATER y = a > r;  TBN_OP_LESS y = a < r (1.0 / 0.0). */
+enum tbn_elementwise_op { TBN_OP_SUB = 0, TBN_OP_GREATER = 1, TBN_OP_LESS = 2 };
+int tbn_hip_elementwise(int op, const float* a, int64_t n, const float* b, int64_t nb, float scalar,
+                        float* y, tbn_stream_t stream);
+/* The Session's ternary replacement of Relu (model.hpp:1144-1165):
+ * y = x > t ? 1 : (x < -t ? -1 : 0). */
+int tbn_hip_ternary_activation(const float* x, int64_t n, float threshold, float* y,
+                               tbn_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -5,6 +5,7 @@ import pytest
 
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 sys.path.insert(0, str(ROOT / "fast-arm-tbcnn_amd" / "python"))
+sys.path.insert(0, str(ROOT / "fast-arm-tbcnn_amd" / "lib"))
 sys.path.insert(0, str(ROOT / "tests"))
 
 
@@ -16,6 +17,13 @@ def pytest_configure(config):
 def orc():
     import oracle_api
     return oracle_api
+
+
+@pytest.fixture(scope="session")
+def tbn():
+    """The C++ runtime's Python module (fast-arm-tbcnn_amd/lib/_tbn*.so)."""
+    import _tbn
+    return _tbn
 
 
 @pytest.fixture(scope="session")

@@ -1,0 +1,232 @@
+"""Device-resident Session (TBNModel::Session through the _tbn module) against
+the CPU reference executor in tests/models.py.
+
+Configs 1 (LeNet) and 5 (ResNet-18) of BASELINE.json; tolerance as the
+north_star states: rel-L2 <= 1e-5 and max-abs <= 1e-4 * sqrt(K) * max|x|
+for the last layer's K and input."""
+import numpy as np
+import pytest
+
+import models
+import refmath as rm
+
+pytestmark = pytest.mark.gpu
+
+
+def _session(tbn, spec, quant, replay=False):
+    model = tbn.TBNModel(models.build_graph(spec, tbn))
+    model.validate()
+    s = model.create_session()
+    s.set_quantization(quant)
+    if replay:
+        s.set_graph_replay(True)
+    return model, s
+
+
+def _check(out, ref, K, xmax):
+    assert np.all(np.isfinite(out))
+    return rm.assert_within_tolerance(out, ref, K, xmax)
+
+
+@pytest.mark.parametrize("prebinarized", [True, False])
+def test_lenet_quantized(dev, tbn, orc, prebinarized):
+    spec = models.lenet(seed=1, prebinarized=prebinarized)
+    x = models.lenet_input(1)
+    _, s = _session(tbn, spec, quant=True)
+    s.set_input("input", x)
+    s.run()
+    out = s.get_output("output")
+    rec = {}
+    ref = models.run_oracle(spec, {"input": x}, True, orc, record=rec)["output"]
+    print("lenet quantized prebinarized=%s: out[:4]=%s" % (prebinarized, out.ravel()[:4]))
+    _check(out, ref, 256, np.abs(rec["flat"]).max())
+    # conv+relu+pool fused twice, then the Gemm: three launches
+    assert s.planned_launches() == 3
+
+
+def test_lenet_fp32(dev, tbn, orc):
+    spec = models.lenet(seed=2, prebinarized=False)
+    x = models.lenet_input(2)
+    _, s = _session(tbn, spec, quant=False)
+    s.set_input("input", x)
+    s.run()
+    rec = {}
+    ref = models.run_oracle(spec, {"input": x}, False, orc, record=rec)["output"]
+    _check(s.get_output("output"), ref, 256, np.abs(rec["flat"]).max())
+
+
+def test_lenet_repeat_runs_and_new_input(dev, tbn, orc):
+    spec = models.lenet(seed=3)
+    _, s = _session(tbn, spec, quant=True)
+    outs = []
+    for seed in (3, 4, 3):
+        s.set_input("input", models.lenet_input(seed))
+        s.run()
+        outs.append(s.get_output("output"))
+    assert np.array_equal(outs[0], outs[2])
+    assert not np.array_equal(outs[0], outs[1])
+
+
+def test_lenet_graph_replay_matches_eager(dev, tbn):
+    import torch
+    spec = models.lenet(seed=6)
+    x = models.lenet_input(6)
+    _, eager = _session(tbn, spec, quant=True)
+    eager.set_input("input", x)
+    eager.run()
+    want = eager.get_output("output")
+    stream = torch.cuda.Stream()
+    tbn.set_current_stream(stream.cuda_stream)
+    try:
+        _, rs = _session(tbn, spec, quant=True, replay=True)
+        rs.set_input("input", x)
+        for i in range(6):  # eager, capture, then replays
+            rs.run()
+            got = rs.get_output("output")
+            assert np.array_equal(got, want), f"replay {i} differs"
+            torch.zeros(1000, device="cuda").sum().item()  # unrelated eager work between replays
+    finally:
+        tbn.set_current_stream(0)
+
+
+def test_session_device_input(dev, tbn):
+    import torch
+    spec = models.lenet(seed=7)
+    x = models.lenet_input(7)
+    _, s = _session(tbn, spec, quant=True)
+    s.set_input("input", x)
+    s.run()
+    want = s.get_output("output")
+    xd = torch.from_numpy(x).cuda()
+    s.set_input("input", tbn.Tensor.wrap(xd.data_ptr(), list(x.shape), "float32", "hip"))
+    s.run()
+    torch.cuda.synchronize()
+    assert np.array_equal(s.get_output("output"), want)
+    dev_out = s.get_output_device("output")
+    assert dev_out.device == "hip" and dev_out.shape == [1, 10]
+    assert np.array_equal(dev_out.numpy(), want)
+
+
+def test_relu_ternary_replacement(dev, tbn, orc):
+    """The reference turns Relu into a ternary activation when quantization is
+    on and the input name contains conv2d_1 (model.hpp:1144-1165)."""
+    rng = np.random.default_rng(11)
+    w = models.prebinarize(rng.standard_normal((8, 4, 3, 3)).astype(np.float32))
+    spec = models.Spec(
+        nodes=[models.Node("c", "Conv", ["input", "w"], ["conv2d_1"], {"pads": [1, 1, 1, 1]}),
+               models.Node("r", "Relu", ["conv2d_1"], ["out"])],
+        inits={"w": w}, init_dtypes={"w": "float32"}, inputs={"input": (2, 4, 9, 9)},
+        outputs={"out": (2, 8, 9, 9)}, value_info={"conv2d_1": (2, 8, 9, 9), "out": (2, 8, 9, 9), "input": (2, 4, 9, 9)})
+    x = rng.standard_normal((2, 4, 9, 9)).astype(np.float32) * 0.3
+    for quant in (True, False):
+        _, s = _session(tbn, spec, quant=quant)
+        s.set_input("input", x)
+        s.run()
+        out = s.get_output("out")
+        ref = models.run_oracle(spec, {"input": x}, quant, orc)["out"]
+        if quant:
+            assert set(np.unique(out).tolist()) <= {-1.0, 0.0, 1.0}
+            # values away from the +-0.5 thresholds must agree exactly
+            pre = models.run_oracle(models.Spec(spec.nodes[:1], spec.inits, spec.init_dtypes, spec.inputs,
+                                                {"conv2d_1": (2, 8, 9, 9)}, spec.value_info), {"input": x}, True, orc)
+            far = np.abs(np.abs(pre["conv2d_1"]) - 0.5) > 1e-4
+            assert np.array_equal(out[far], ref[far])
+        else:
+            _check(out, ref, 36, np.abs(x).max())
+
+
+def test_binary_and_ternary_initializers(dev, tbn, orc):
+    """BINARY / TERNARY weight initializers take conv2d_binary / conv2d_ternary."""
+    rng = np.random.default_rng(12)
+    wb = (rng.random((16, 8, 3, 3)) < 0.5).astype(np.uint8)
+    wt = rng.choice(np.array([-1, 0, 1], np.int8), size=(16, 16, 3, 3), p=[0.3, 0.4, 0.3])
+    b = (rng.standard_normal(16) * 0.01).astype(np.float32)
+    spec = models.Spec(
+        nodes=[models.Node("c1", "Conv", ["input", "wb", "b"], ["y1"], {"pads": [1, 1, 1, 1]}),
+               models.Node("r1", "Relu", ["y1"], ["a1"]),
+               models.Node("c2", "Conv", ["a1", "wt", "b"], ["out"], {"strides": [2, 2]})],
+        inits={"wb": wb, "wt": wt, "b": b}, init_dtypes={"wb": "binary", "wt": "ternary", "b": "float32"},
+        inputs={"input": (3, 8, 15, 15)}, outputs={"out": (3, 16, 7, 7)},
+        value_info={"y1": (3, 16, 15, 15), "a1": (3, 16, 15, 15), "out": (3, 16, 7, 7), "input": (3, 8, 15, 15)})
+    x = rng.standard_normal((3, 8, 15, 15)).astype(np.float32)
+    _, s = _session(tbn, spec, quant=False)
+    s.set_input("input", x)
+    s.run()
+    rec = {}
+    ref = models.run_oracle(spec, {"input": x}, False, orc, record=rec)["out"]
+    _check(s.get_output("out"), ref, 144, np.abs(rec["a1"]).max())
+
+
+@pytest.mark.parametrize("batch", [2])
+def test_resnet18_parity(dev, tbn, orc, batch):
+    spec = models.resnet18(batch=batch, seed=5)
+    x = models.resnet_input(batch, seed=5)
+    _, s = _session(tbn, spec, quant=True)
+    s.set_input("input", x)
+    s.run()
+    out = s.get_output("logits")
+    rec = {}
+    ref = models.run_oracle(spec, {"input": x}, True, orc, record=rec)["logits"]
+    r, m = _check(out, ref, 512, np.abs(rec["flat"]).max())
+    print(f"resnet18 batch {batch}: rel-L2 {r:.2e}, max-abs {m:.2e}, launches {s.planned_launches()}")
+    # stem(+relu), pool, 16 binary convs with relu or residual fused, 3 projections, gap, fc
+    assert s.planned_launches() == 1 + 1 + 16 + 3 + 1 + 1
+
+
+def test_resnet18_batch32_batch_invariant(dev, tbn):
+    """Config 5 at its full batch of 32: every sample's logits are bit-identical
+    to the same sample run in a batch of 2 (each output element accumulates
+    over K in the same order whatever the batch)."""
+    spec32 = models.resnet18(batch=32, seed=5)
+    x32 = models.resnet_input(32, seed=5)
+    _, s32 = _session(tbn, spec32, quant=True)
+    s32.set_input("input", x32)
+    s32.run()
+    out32 = s32.get_output("logits")
+    assert out32.shape == (32, 1000) and np.all(np.isfinite(out32))
+    spec2 = models.resnet18(batch=2, seed=5)
+    _, s2 = _session(tbn, spec2, quant=True)
+    for i0 in (0, 30):
+        s2.set_input("input", x32[i0:i0 + 2].copy())
+        s2.run()
+        assert np.array_equal(s2.get_output("logits"), out32[i0:i0 + 2]), f"samples {i0}..{i0 + 1}"
+
+
+def test_inference_session_and_model_wrappers(dev, tbn, orc):
+    spec = models.lenet(seed=8)
+    x = models.lenet_input(8)
+    ref = models.run_oracle(spec, {"input": x}, True, orc)["output"]
+    opts = tbn.InferenceSessionOptions()
+    opts.use_quantization = True
+    sess = tbn.InferenceSession(tbn.TBNModel(models.build_graph(spec, tbn)), opts)
+    sess.initialize()
+    sess.set_input("input", x)
+    sess.run()
+    a = sess.get_output("output")
+    m = tbn.Model(models.build_graph(spec, tbn))
+    b = m.run_quantized(x)
+    assert np.array_equal(a, b)
+    _check(a, ref, 256, 10.0)
+    assert m.input_names() == ["input"] and m.output_names() == ["output"]
+
+
+def test_session_errors(dev, tbn):
+    spec = models.lenet(seed=9)
+    _, s = _session(tbn, spec, quant=True)
+    with pytest.raises(tbn.TBNError) as e:
+        s.run()  # no input
+    assert e.value.code == -1
+    with pytest.raises(tbn.TBNError) as e:
+        s.set_input("input", np.zeros((1, 1, 28, 27), np.float32))
+    assert e.value.code == -7
+    with pytest.raises(tbn.TBNError) as e:
+        s.set_input("nope", np.zeros((1, 1, 28, 28), np.float32))
+    assert e.value.code == -1
+    g = models.build_graph(spec, tbn)
+    g.add_node("bad", "Softmax", ["output"], ["sm"], {})
+    g.set_value_info("sm", [1, 10])
+    s2 = tbn.TBNModel(g).create_session()
+    s2.set_input("input", models.lenet_input(9))
+    with pytest.raises(tbn.TBNError) as e:
+        s2.run()
+    assert e.value.code == -3
