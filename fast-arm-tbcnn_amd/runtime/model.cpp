@@ -22,6 +22,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <deque>
 #include <functional>
 #include <map>
 #include <set>
@@ -244,7 +245,7 @@ struct TBNModel::Session::Impl {
     bool planned = false;
     bool plan_quant = false;
     std::map<std::string, Shape> plan_shapes;
-    std::vector<Value> values;
+    std::deque<Value> values;  // deque: references stay valid as values are added
     std::unordered_map<std::string, int> value_id;
     std::vector<Op> ops;
     Tensor arena;
@@ -373,8 +374,8 @@ struct TBNModel::Session::Impl {
         TBN_CHECK(graph->initializers.count(wname), NotImplementedError,
                   "Conv '" + node.name + "': weights must be an initializer");
         const int wi = lookup(wname, node.name);
-        const Shape& xs = values[xi].shape;
-        const Shape& ws = values[wi].shape;
+        const Shape xs = values[xi].shape;
+        const Shape ws = values[wi].shape;
         TBN_CHECK(xs.rank() == 4, InvalidShapeError, "Conv input must be 4D (NCHW), got " + shape_to_string(xs));
         TBN_CHECK(ws.rank() == 4, InvalidShapeError, "Conv weights must be 4D, got " + shape_to_string(ws));
         const Conv2DParams p = conv_params(node, ws);
@@ -437,8 +438,8 @@ struct TBNModel::Session::Impl {
         }
         const int ai = lookup(node.inputs[0], node.name);
         const int bi = lookup(node.inputs[1], node.name);
-        const Shape& as = values[ai].shape;
-        const Shape& bs = values[bi].shape;
+        const Shape as = values[ai].shape;
+        const Shape bs = values[bi].shape;
         if (as.rank() != 2 || bs.rank() != 2) {
             if (matmul) throw NotImplementedError("MatMul for non-2D tensors not implemented");
             throw InvalidShapeError("Gemm '" + node.name + "': inputs must be 2-D");
