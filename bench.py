@@ -1,13 +1,17 @@
-"""Benchmark of the tbn float x binary path on one MI355X.
+"""Benchmark of the tbn quantized compute path on one MI355X.
 
 A "step" is one float x binary GEMM at the headline shape M = N = K = 4096
 (fp32 activations ~ N(0,1) resident in HBM, +-1 weights pre-packed in the
-reference's BinaryMatrix layout, per-column fp32 scale ~ U[0.5, 1.5]).  The
-JSON line reports GFLOP/s-equivalent (2*M*N*K / t), the roofline of the GEMM
-kernel, the config-4 binary Conv2D time per batch of 64, and the reference's
-portable CPU path (restated in oracle/) timed on this host.
+reference's BinaryMatrix layout, per-column fp32 scale ~ U[0.5, 1.5]):
+`value` is its GFLOP/s-equivalent (2*M*N*K / t).  The same JSON line carries
+the other BASELINE.json configs as secondary figures -- config-4 binary
+Conv2D (us per batch of 64), config-3 float x ternary GEMM, config-2 1024^3
+GEMM, config-1 LeNet and config-5 ResNet-18 through the device-resident
+Session -- the roofline of the GEMM kernel, and the reference's portable CPU
+path (restated in oracle/) timed on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+                       [--only gemm|conv|ternary|gemm1024|lenet|resnet]
 """
 import argparse
 import json
@@ -21,10 +25,12 @@ import numpy as np
 
 ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "fast-arm-tbcnn_amd" / "python"))
+sys.path.insert(0, str(ROOT / "fast-arm-tbcnn_amd" / "lib"))
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (the unit the kernel runs on)
 FP32_PEAK_TFLOPS = 157.3    # MI355X fp32 (the north_star's "relevant roofline")
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 
 
 def log(*a):
@@ -32,8 +38,8 @@ def log(*a):
 
 
 def time_stream(fn, stream, steps, warmup, torch):
-    """Runs fn() warmup times, then times `steps` calls with HIP events on
-    the stream the kernels are launched on; returns ms per call."""
+    """Runs fn() `warmup` times, then times `steps` calls with HIP events
+    recorded on the stream the kernels are launched on; returns ms per call."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -47,23 +53,38 @@ def time_stream(fn, stream, steps, warmup, torch):
     return start.elapsed_time(end) / steps
 
 
-def gemm_workload(torch, tbn_hip, M, N, K, seed):
+# ---- workloads --------------------------------------------------------------------------
+
+def packed_gemm(torch, tbn_hip, M, N, K, seed, ternary=False):
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     A = torch.randn((M, K), generator=g, device=dev, dtype=torch.float32)
-    binw = (torch.rand((K, N), generator=g, device=dev) < 0.5).to(torch.uint8)
-    scale = torch.rand(N, generator=g, device=dev, dtype=torch.float32) + 0.5
     K_pad, N_pad = tbn_hip.padded_dims(K, N)
-    packed = torch.empty(N_pad * K_pad // 8, dtype=torch.uint8, device=dev)
-    tbn_hip.call("tbn_hip_pack_binary", binw.data_ptr(), K, N, tbn_hip.LAYOUT_KN, K_pad, N_pad,
-                 packed.data_ptr(), None)
+    if ternary:
+        u = torch.rand((K, N), generator=g, device=dev)
+        t = torch.where(u < 0.3, -1, torch.where(u < 0.7, 0, 1)).to(torch.int8)  # p = 0.3/0.4/0.3
+        packed = torch.empty(N_pad * K_pad // 4, dtype=torch.uint8, device=dev)
+        tbn_hip.call("tbn_hip_pack_ternary", t.data_ptr(), K, N, tbn_hip.LAYOUT_KN, K_pad, N_pad,
+                     packed.data_ptr(), None)
+    else:
+        binw = (torch.rand((K, N), generator=g, device=dev) < 0.5).to(torch.uint8)
+        packed = torch.empty(N_pad * K_pad // 8, dtype=torch.uint8, device=dev)
+        tbn_hip.call("tbn_hip_pack_binary", binw.data_ptr(), K, N, tbn_hip.LAYOUT_KN, K_pad, N_pad,
+                     packed.data_ptr(), None)
+    scale = torch.rand(N, generator=g, device=dev, dtype=torch.float32) + 0.5
     C = torch.empty((M, N), dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
-    return A, packed, K_pad, N_pad, scale, C
+    fn_name = "tbn_hip_gemm_f32_ternary" if ternary else "tbn_hip_gemm_f32_binary"
+
+    def step(sh):
+        tbn_hip.call(fn_name, A.data_ptr(), K, M, N, K, packed.data_ptr(), K_pad, N_pad,
+                     scale.data_ptr(), 1.0, 0, 0, C.data_ptr(), N, sh)
+    keep = (A, packed, scale, C)
+    return step, keep, K_pad, N_pad
 
 
-def conv_workload(torch, tbn_hip, seed):
+def conv_cfg4(torch, tbn_hip, seed):
     """Config 4: x[64,64,14,14] ~ N(0,1), W[128,64,3,3] +-1, per-channel scale,
     bias ~ N(0, 0.01), stride 1, pad 1, ReLU."""
     dev = torch.device("cuda:0")
@@ -80,7 +101,36 @@ def conv_workload(torch, tbn_hip, seed):
     y = torch.empty((64, 128, 14, 14), device=dev)
     desc = tbn_hip.conv_desc(64, 64, 14, 14, 128, 3, 3, 1, 1, 1, 1)
     torch.cuda.synchronize()
-    return x, packed, K_pad, N_pad, scale, bias, y, desc
+
+    def step(sh):
+        tbn_hip.call("tbn_hip_conv2d_f32_binary", x.data_ptr(), desc, packed.data_ptr(), K_pad, N_pad,
+                     scale.data_ptr(), 1.0, bias.data_ptr(), tbn_hip.EPI_RELU, y.data_ptr(), sh)
+    return step, (x, packed, scale, bias, y, desc)
+
+
+def session_workload(torch, _tbn, which, stream):
+    """Config 1 (LeNet, batch 1, HIP-graph replay) or config 5 (ResNet-18,
+    batch 32) through TBNModel::Session with quantization on; the input is
+    already in HBM, the output stays there (get_output_device)."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import models
+    if which == "lenet":
+        spec, x = models.lenet(seed=1), models.lenet_input(1)
+    else:
+        spec, x = models.resnet18(batch=32, seed=5), models.resnet_input(32, seed=5)
+    model = _tbn.TBNModel(models.build_graph(spec, _tbn))
+    sess = model.create_session()
+    sess.set_quantization(True)
+    xd = torch.from_numpy(x).cuda()
+    torch.cuda.synchronize()
+    _tbn.set_current_stream(stream.cuda_stream)
+    sess.set_input("input", _tbn.Tensor.wrap(xd.data_ptr(), list(x.shape), "float32", "hip"))
+    if which == "lenet":
+        sess.set_graph_replay(True)
+
+    def step(sh):
+        sess.run()
+    return step, (model, sess, xd)
 
 
 def cpu_baseline(M, N, K, budget_s):
@@ -102,8 +152,7 @@ def cpu_baseline(M, N, K, budget_s):
         times.append(time.perf_counter() - t0)
         assert rc == 0, rc
     best = min(times)
-    # the true fp32-activation reference loop (qlinear_matmul_binary_naive), on 64 rows
-    rows = 64
+    rows = 64  # the true fp32-activation reference loop (qlinear_matmul_binary_naive), on 64 rows
     t0 = time.perf_counter()
     orc.qlinear_matmul_binary_naive(A[:rows], binw, 1.0)
     naive_s = time.perf_counter() - t0
@@ -135,59 +184,89 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
+    ap.add_argument("--only", choices=["gemm", "conv", "ternary", "gemm1024", "lenet", "resnet"],
+                    help="run one workload only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
-                    help="also run a 1 GiB device copy (known bytes) for counter calibration")
+                    help="also run 3 device copies of 1 GiB (known bytes) for counter calibration")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one MI355X: the path has no multi-GPU component in this build "
-              "(batch/M sharding with replicated packed weights needs no exchange); run with --gpus 1.",
-              file=sys.stderr)
+        print("bench.py measures one MI355X: this build runs on a single GPU (batch/M sharding with "
+              "replicated packed weights needs no exchange); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
     import tbn_hip
+    import _tbn
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     tbn_hip.call("tbn_hip_device_check")
     stream = torch.cuda.Stream()
     sh = stream.cuda_stream
+    want = (lambda name: args.only is None or args.only == name)
 
+    def timed(step):
+        with torch.cuda.stream(stream):
+            return time_stream(lambda: step(sh), stream, args.steps, args.warmup, torch)
+
+    extra = {}
     M = N = K = 4096
-    A, packed, K_pad, N_pad, scale, C = gemm_workload(torch, tbn_hip, M, N, K, seed=1)
-
-    def gemm_step():
-        tbn_hip.call("tbn_hip_gemm_f32_binary", A.data_ptr(), K, M, N, K, packed.data_ptr(), K_pad, N_pad,
-                     scale.data_ptr(), 1.0, 0, 0, C.data_ptr(), N, sh)
-
-    with torch.cuda.stream(stream):
-        ms = time_stream(gemm_step, stream, args.steps, args.warmup, torch)
-    flops = 2.0 * M * N * K
-    gflops = flops / (ms * 1e-3) / 1e9
-    log(f"gemm 4096^3 float x binary: {ms * 1e3:.1f} us/launch, {gflops / 1e3:.1f} TFLOP/s-equiv")
-
-    # config-4 binary conv, batch 64
-    x, cpk, cK_pad, cN_pad, cs, cb, y, desc = conv_workload(torch, tbn_hip, seed=2)
-
-    def conv_step():
-        tbn_hip.call("tbn_hip_conv2d_f32_binary", x.data_ptr(), desc, cpk.data_ptr(), cK_pad, cN_pad,
-                     cs.data_ptr(), 1.0, cb.data_ptr(), tbn_hip.EPI_RELU, y.data_ptr(), sh)
-
-    with torch.cuda.stream(stream):
-        conv_ms = time_stream(conv_step, stream, args.steps, args.warmup, torch)
-    conv_flops = 2.0 * 64 * 196 * 576 * 128
-    log(f"conv 64x64x14x14 -> 128, 3x3, batch 64: {conv_ms * 1e3:.1f} us/batch, "
-        f"{conv_flops / conv_ms / 1e9:.1f} TFLOP/s-equiv")
+    ms = None
+    K_pad = N_pad = None
+    if want("gemm"):
+        step, keep, K_pad, N_pad = packed_gemm(torch, tbn_hip, M, N, K, seed=1)
+        ms = timed(step)
+        log(f"gemm 4096^3 float x binary: {ms * 1e3:.1f} us/launch, {2.0 * M * N * K / ms / 1e9:.1f} TFLOP/s-eq")
+        del keep
+    if want("conv"):
+        step, keep = conv_cfg4(torch, tbn_hip, seed=2)
+        conv_ms = timed(step)
+        conv_flops = 2.0 * 64 * 196 * 576 * 128
+        extra["conv_us_per_batch"] = round(conv_ms * 1e3, 2)
+        extra["conv_gflops_equiv"] = round(conv_flops / (conv_ms * 1e-3) / 1e9, 1)
+        log(f"conv cfg4 batch 64: {conv_ms * 1e3:.1f} us/batch")
+        del keep
+    if want("ternary"):
+        step, keep, _, _ = packed_gemm(torch, tbn_hip, 256, 4096, 4096, seed=3, ternary=True)
+        t_ms = timed(step)
+        extra["ternary_cfg3_us"] = round(t_ms * 1e3, 2)
+        extra["ternary_cfg3_gflops_equiv"] = round(2.0 * 256 * 4096 * 4096 / (t_ms * 1e-3) / 1e9, 1)
+        log(f"ternary cfg3 256x4096x4096: {t_ms * 1e3:.1f} us")
+        del keep
+    if want("gemm1024"):
+        step, keep, _, _ = packed_gemm(torch, tbn_hip, 1024, 1024, 1024, seed=4)
+        g_ms = timed(step)
+        extra["gemm_cfg2_us"] = round(g_ms * 1e3, 2)
+        extra["gemm_cfg2_gflops_equiv"] = round(2.0 * 1024 ** 3 / (g_ms * 1e-3) / 1e9, 1)
+        log(f"binary cfg2 1024^3: {g_ms * 1e3:.1f} us")
+        del keep
+    for which, key in (("lenet", "lenet_session_us_per_forward"), ("resnet", "resnet18_session_ms_per_batch32")):
+        if not want(which):
+            continue
+        step, keep = session_workload(torch, _tbn, which, stream)
+        s_ms = timed(step)
+        extra[key] = round(s_ms * (1e3 if which == "lenet" else 1.0), 3)
+        extra[which + "_session_launches"] = keep[1].planned_launches()
+        log(f"{which} session: {s_ms * 1e3:.1f} us per forward ({keep[1].planned_launches()} launches)")
+        _tbn.set_current_stream(0)
+        del keep
 
     if args.copy_calibration:
-        src = torch.empty(1 << 28, dtype=torch.float32, device="cuda:0")
+        # an elementwise kernel that reads 1 GiB and writes 1 GiB (known bytes)
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda:0")
         dst = torch.empty_like(src)
         with torch.cuda.stream(stream):
             for _ in range(3):
-                dst.copy_(src)
+                torch.mul(src, 1.0, out=dst)
         torch.cuda.synchronize()
-        log("copy calibration: 3 x 1 GiB device-to-device copies")
+        log("copy calibration: 3 x (read 1 GiB, write 1 GiB) elementwise kernels")
 
+    if ms is None:
+        print(json.dumps({"only": args.only, **extra}), flush=True)
+        return
+
+    flops = 2.0 * M * N * K
+    gflops = flops / (ms * 1e-3) / 1e9
     algo_bytes = 4.0 * M * K + K_pad * N_pad / 8 + 4.0 * N + 4.0 * M * N
     achieved_tflops = flops / (ms * 1e-3) / 1e12
     roofline = {
@@ -197,15 +276,14 @@ def main():
         "unit": "TFLOP/s",
         "frac": round(achieved_tflops / BF16_PEAK_TFLOPS, 4),
         "traffic": None,
-        "kernel": "mfma_tile_kernel<128x128, SplitMatrix, SignPacked<binary>, GemmEpi>",
+        "kernel": "mfma_tile_kernel<TileCfg<128,256,64,128,2>, SplitMatrix, SignPacked<binary>, GemmEpi>",
         "issued_bf16_frac": round(3.0 * achieved_tflops / BF16_PEAK_TFLOPS, 4),
         "fp32_roofline_frac": round(achieved_tflops / FP32_PEAK_TFLOPS, 4),
         "algorithmic_bytes": int(algo_bytes),
         "hbm_gbs_algorithmic": round(algo_bytes / (ms * 1e-3) / 1e9, 1),
     }
-    traffic_file = ROOT / "profiles" / "traffic.json"
-    if traffic_file.exists():
-        tr = json.loads(traffic_file.read_text()).get("gemm_f32_binary_4096")
+    if TRAFFIC_FILE.exists():
+        tr = json.loads(TRAFFIC_FILE.read_text()).get("gemm_f32_binary_4096")
         if tr:
             roofline["traffic"] = tr.get("bytes_per_launch")
 
@@ -229,11 +307,10 @@ def main():
             "conv_workload": "binary Conv2D 64x14x14 -> 128x14x14, 3x3, s1 p1, batch 64, per-channel scale, "
                              "bias, ReLU (config 4)",
         },
-        "conv_us_per_batch": round(conv_ms * 1e3, 2),
-        "conv_gflops_equiv": round(conv_flops / (conv_ms * 1e-3) / 1e9, 1),
+        **extra,
         "roofline": roofline,
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.only is None:
         log("timing the CPU baseline ...")
         result["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_budget)
     else:
