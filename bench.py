@@ -100,12 +100,23 @@ def conv_cfg4(torch, tbn_hip, seed):
                  packed.data_ptr(), None)
     y = torch.empty((64, 128, 14, 14), device=dev)
     desc = tbn_hip.conv_desc(64, 64, 14, 14, 128, 3, 3, 1, 1, 1, 1)
+    # weights re-ordered once into the conv layout, as a Session does at init
+    import ctypes
+    wbytes = ctypes.c_int64()
+    tbn_hip.call("tbn_hip_conv_weights_bytes", tbn_hip.WEIGHTS_BINARY, desc, ctypes.byref(wbytes))
+    conv_w = torch.empty(wbytes.value, dtype=torch.uint8, device=dev)
+    tbn_hip.call("tbn_hip_pack_conv_weights", tbn_hip.WEIGHTS_BINARY, packed.data_ptr(), K_pad, N_pad, desc,
+                 conv_w.data_ptr(), None)
     torch.cuda.synchronize()
 
     def step(sh):
+        tbn_hip.call("tbn_hip_conv2d_f32_prepacked", tbn_hip.WEIGHTS_BINARY, x.data_ptr(), desc, conv_w.data_ptr(),
+                     scale.data_ptr(), 1.0, bias.data_ptr(), None, tbn_hip.EPI_RELU, y.data_ptr(), sh)
+
+    def step_reference_layout(sh):
         tbn_hip.call("tbn_hip_conv2d_f32_binary", x.data_ptr(), desc, packed.data_ptr(), K_pad, N_pad,
                      scale.data_ptr(), 1.0, bias.data_ptr(), tbn_hip.EPI_RELU, y.data_ptr(), sh)
-    return step, (x, packed, scale, bias, y, desc)
+    return step, step_reference_layout, (x, packed, conv_w, scale, bias, y, desc)
 
 
 def session_workload(torch, _tbn, which, stream):
@@ -219,12 +230,15 @@ def main():
         log(f"gemm 4096^3 float x binary: {ms * 1e3:.1f} us/launch, {2.0 * M * N * K / ms / 1e9:.1f} TFLOP/s-eq")
         del keep
     if want("conv"):
-        step, keep = conv_cfg4(torch, tbn_hip, seed=2)
+        step, step_ref, keep = conv_cfg4(torch, tbn_hip, seed=2)
         conv_ms = timed(step)
         conv_flops = 2.0 * 64 * 196 * 576 * 128
         extra["conv_us_per_batch"] = round(conv_ms * 1e3, 2)
         extra["conv_gflops_equiv"] = round(conv_flops / (conv_ms * 1e-3) / 1e9, 1)
-        log(f"conv cfg4 batch 64: {conv_ms * 1e3:.1f} us/batch")
+        ref_ms = timed(step_ref)
+        extra["conv_reference_layout_us_per_batch"] = round(ref_ms * 1e3, 2)
+        log(f"conv cfg4 batch 64: {conv_ms * 1e3:.1f} us/batch pre-packed, {ref_ms * 1e3:.1f} us with the "
+            f"per-call weight re-order of the reference-layout entry point")
         del keep
     if want("ternary"):
         step, keep, _, _ = packed_gemm(torch, tbn_hip, 256, 4096, 4096, seed=3, ternary=True)

@@ -1,0 +1,745 @@
+// Binary / ternary Conv2D, patch form (inputs of 16 or more channels).
+//
+// A block owns BM output channels x one spatial tile of TH x TW output pixels
+// of one image.  The K loop runs over channel chunks of 32: for each chunk
+// the block stages the input patch the tile needs -- ((TH-1)*sh + (kh-1)*dh + 1)
+// x ((TW-1)*sw + (kw-1)*dw + 1) pixels x 32 channels -- from the NCHW fp32
+// input into LDS, split on the way into three bf16 planes (hi + mid + lo = x
+// exactly), zero outside the image.  Every tap of the chunk is then one K step
+// of 32 read from the same patch, so each input element is loaded and split
+// once per block instead of once per tap, and the chunk's global loads are in
+// flight during the previous chunk's kh*kw K steps of MFMAs.
+//
+// Weights use the conv layout k' = ((c / 32) * taps + tap) * 32 + c % 32 (taps =
+// kh*kw), made once from the reference's packed columns by
+// tbn_hip_pack_conv_weights; the block stages the chunk's 32-bit (binary) or
+// 64-bit (ternary) words [tap][channel] into LDS next to the patch, and each
+// lane decodes its channel's word to bf16 +-1 / 0 in registers.  The inner
+// loop touches only LDS.  Output channels are the MFMA rows, tile pixels the columns; with
+// the fused 2x2 max pool the pixels are enumerated window by window so a window
+// sits in four neighbouring lanes.
+#include <algorithm>
+#include <cstdlib>
+#include <string>
+
+#include "conv_common.hpp"
+
+namespace {
+
+using namespace tbnk;
+
+constexpr int kChunk = 32;               // channels per K chunk
+constexpr int kPix = kChunk + 8;         // bf16 per staged pixel (80 bytes: conflict-free 16-byte reads)
+constexpr int kMaxLds = 160 * 1024;      // gfx950 LDS per workgroup
+
+struct PatchGeom {
+    int N, C, H, W, M;
+    int kh, kw, sh, sw, ph, pw, dh, dw;
+    int OH, OW;
+    int taps, chunks;      // kh*kw, ceil(C / 32)
+    int PHi, PWi;          // staged patch rows / cols
+    int tiles_h, tiles_w;  // 2-D tiles per image (linear == 0)
+    int pool, PH, PW;      // fused 2x2 pool and its output size
+    int VH, VW;            // extent of computed pixels (2*PH x 2*PW when pooling)
+    int linear;            // 1: a tile is QT consecutive pixels (QT/4 pool windows) of one image
+    int tiles_img;         // tiles per image
+};
+
+// Output pixel of the tile-local index ql and its patch index.  Linear tiles
+// run along the flattened image (pool windows when pooling), so a fragment's
+// 32 lanes hold 32 consecutive pixels (or 8 windows) of one channel;
+// 2-D tiles are TH x TW blocks.  Pixels past the image are flagged invalid
+// and mapped to patch index 0 (their results are never stored).
+template <class Cfg>
+__device__ __forceinline__ bool tile_pixel(const PatchGeom& g, int q0, int row0, int col0, int ql, int& oh,
+                                           int& ow, int& patch_index) {
+    bool valid;
+    if (g.linear) {
+        if (g.pool) {
+            const int w = q0 + (ql >> 2);
+            const int pr = w / g.PW;
+            oh = 2 * pr + ((ql >> 1) & 1);
+            ow = 2 * (w - pr * g.PW) + (ql & 1);
+            valid = w < g.PH * g.PW;
+        } else {
+            const int q = q0 + ql;
+            oh = q / g.OW;
+            ow = q - oh * g.OW;
+            valid = q < g.OH * g.OW;
+        }
+    } else {
+        int i, j;
+        if (g.pool) {
+            const int win = ql >> 2;
+            i = 2 * (win / (Cfg::TW / 2)) + ((ql >> 1) & 1);
+            j = 2 * (win % (Cfg::TW / 2)) + (ql & 1);
+        } else {
+            i = ql / Cfg::TW;
+            j = ql - i * Cfg::TW;
+        }
+        oh = row0 + i;
+        ow = col0 + j;
+        valid = oh < g.VH && ow < g.VW;
+    }
+    patch_index = valid ? ((oh - row0) * g.sh * g.PWi + (ow - col0) * g.sw) : 0;
+    return valid;
+}
+
+template <int BM_, int TH_, int TW_, int WM_, int WQ_>
+struct PatchCfg {
+    static constexpr int BM = BM_, TH = TH_, TW = TW_, WM = WM_, WQ = WQ_;
+    static constexpr int QT = TH * TW;
+    static constexpr int WAVES_M = BM / WM, WAVES_Q = QT / WQ;
+    static constexpr int NT = 64 * WAVES_M * WAVES_Q;
+    static constexpr int FR = WM / 32, FC = WQ / 32;
+    static_assert(QT % WQ == 0 && BM % WM == 0 && WM % 32 == 0 && WQ % 32 == 0, "bad tile");
+    static_assert(TH % 2 == 0 && TW % 2 == 0, "tiles must hold whole 2x2 pool windows");
+};
+
+template <bool TERNARY>
+__device__ __forceinline__ u32x4_t weight_frag(uint2 w, int kk, int kg) {
+    if (TERNARY) {
+        const uint32_t word = kk ? w.y : w.x;
+        return decode_ternary8((word >> (16 * kg)) & 0xFFFFu);
+    }
+    return decode_binary8((w.x >> (8 * (2 * kk + kg))) & 0xFFu);
+}
+
+struct PatchEpi {
+    float* y;
+    const float* scale;
+    float alpha;
+    const float* bias;
+    const float* residual;
+    int flags;
+};
+
+template <class Cfg, bool TERNARY>
+__global__ void __launch_bounds__(Cfg::NT)
+conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __restrict__ wbits, int64_t col_bytes,
+                  int m_alloc, PatchEpi epi) {
+    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+    // one LDS buffer = the patch (3 planes x pixels x kPix bf16) followed by the
+    // chunk's weight words [tap][channel] (uint32, or uint2 for ternary); two buffers
+    constexpr int kWordHalves = TERNARY ? 4 : 2;       // uint16 per channel word
+    const int patch = g.PHi * g.PWi;
+    const int plane_elems = patch * kPix;
+    const int wofs = 3 * plane_elems;                  // weight words after the planes
+    const int buf_elems = wofs + kWordHalves * Cfg::BM * g.taps;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave / Cfg::WAVES_Q;
+    const int wq = wave % Cfg::WAVES_Q;
+
+    // block -> (channel tile, image, spatial tile); channel tiles of one pixel
+    // tile are neighbours so the patch is shared through L2
+    const int tiles_m = (g.M + Cfg::BM - 1) / Cfg::BM;
+    const int mt = blockIdx.x % tiles_m;
+    int st = blockIdx.x / tiles_m;
+    const int n = st / g.tiles_img;
+    st -= n * g.tiles_img;
+    const int m0 = mt * Cfg::BM;
+    int q0 = 0, oh0, ow0;  // first pixel / window of a linear tile; first row / col of the patch
+    if (g.linear) {
+        q0 = st * (g.pool ? Cfg::QT / 4 : Cfg::QT);
+        oh0 = g.pool ? 2 * (q0 / g.PW) : q0 / g.OW;
+        ow0 = 0;
+    } else {
+        const int th = st / g.tiles_w;
+        oh0 = th * Cfg::TH;
+        ow0 = (st - th * g.tiles_w) * Cfg::TW;
+    }
+    const int ih0 = oh0 * g.sh - g.ph, iw0 = ow0 * g.sw - g.pw;
+
+    // ---- staging of one chunk: patch items = (8-channel group, pixel) and
+    //      weight items = (tap, channel) ----
+    const int items = 4 * patch;
+    const int per_thread = (items + Cfg::NT - 1) / Cfg::NT;  // <= kMaxItems (host-checked)
+    constexpr int kMaxItems = 8;
+    const int witems = Cfg::BM * g.taps;
+    const int wper_thread = (witems + Cfg::NT - 1) / Cfg::NT;  // <= kMaxWItems (host-checked)
+    constexpr int kMaxWItems = 8;
+    const int64_t img = static_cast<int64_t>(n) * g.C * g.H * g.W;
+    const int64_t HW = static_cast<int64_t>(g.H) * g.W;
+    float stage[kMaxItems][8];
+    uint2 wstage[kMaxWItems];
+
+    auto load_chunk = [&](int ch) {
+#pragma unroll
+        for (int it = 0; it < kMaxItems; ++it) {
+            if (it >= per_thread) break;
+            const int item = tid + it * Cfg::NT;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) stage[it][e] = 0.0f;
+            if (item < items) {
+                const int grp = item / patch;
+                const int pp = item - grp * patch;
+                const int pr = pp / g.PWi;
+                const int ih = ih0 + pr;
+                const int iw = iw0 + (pp - pr * g.PWi);
+                const int c0 = ch * kChunk + grp * 8;
+                if (static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
+                    static_cast<unsigned>(iw) < static_cast<unsigned>(g.W) && c0 < g.C) {
+                    const float* src = x + img + static_cast<int64_t>(c0) * HW + static_cast<int64_t>(ih) * g.W + iw;
+                    // channels past C (last chunk) re-read channel c0 and are zeroed
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const bool in = c0 + e < g.C;
+                        const float v = src[in ? e * HW : 0];
+                        stage[it][e] = in ? v : 0.0f;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kMaxWItems; ++it) {
+            if (it >= wper_thread) break;
+            const int item = tid + it * Cfg::NT;
+            wstage[it] = make_uint2(0, 0);
+            if (item < witems) {
+                const int ml = item % Cfg::BM;
+                const int tap = item / Cfg::BM;
+                const int m = m0 + ml;
+                if (m < m_alloc) {
+                    const uint8_t* col = wbits + static_cast<int64_t>(m) * col_bytes;
+                    const int64_t t = static_cast<int64_t>(ch) * g.taps + tap;
+                    if (TERNARY) wstage[it] = *reinterpret_cast<const uint2*>(col + 8 * t);
+                    else wstage[it].x = *reinterpret_cast<const uint32_t*>(col + 4 * t);
+                }
+            }
+        }
+    };
+    auto store_chunk = [&](int b) {
+        uint16_t* dst = lds + b * buf_elems;
+#pragma unroll
+        for (int it = 0; it < kMaxItems; ++it) {
+            if (it >= per_thread) break;
+            const int item = tid + it * Cfg::NT;
+            if (item < items) {
+                const int grp = item / patch;
+                const int pp = item - grp * patch;
+                const Split4 a = split4(stage[it][0], stage[it][1], stage[it][2], stage[it][3]);
+                const Split4 c = split4(stage[it][4], stage[it][5], stage[it][6], stage[it][7]);
+                uint16_t* d = dst + pp * kPix + grp * 8;
+                *reinterpret_cast<uint4*>(d) = make_uint4(a.hi[0], a.hi[1], c.hi[0], c.hi[1]);
+                *reinterpret_cast<uint4*>(d + plane_elems) = make_uint4(a.mid[0], a.mid[1], c.mid[0], c.mid[1]);
+                *reinterpret_cast<uint4*>(d + 2 * plane_elems) = make_uint4(a.lo[0], a.lo[1], c.lo[0], c.lo[1]);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kMaxWItems; ++it) {
+            if (it >= wper_thread) break;
+            const int item = tid + it * Cfg::NT;
+            if (item < witems) {
+                uint16_t* d = dst + wofs + item * kWordHalves;  // item = tap * BM + channel
+                if (TERNARY) *reinterpret_cast<uint2*>(d) = wstage[it];
+                else *reinterpret_cast<uint32_t*>(d) = wstage[it].x;
+            }
+        }
+    };
+
+    // ---- this lane's pixels (fragment columns) inside the patch ----
+    int pbase[Cfg::FC];
+#pragma unroll
+    for (int j = 0; j < Cfg::FC; ++j) {
+        int oh, ow, pi;
+        tile_pixel<Cfg>(g, q0, oh0, ow0, wq * Cfg::WQ + j * 32 + (lane & 31), oh, ow, pi);
+        pbase[j] = pi * kPix;
+    }
+    // this lane's weight rows (fragment rows) inside the chunk's word table
+    const int wrow = wm * Cfg::WM + (lane & 31);
+
+    f32x16_t acc[Cfg::FR][Cfg::FC];
+#pragma unroll
+    for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    load_chunk(0);
+    store_chunk(0);
+    if (g.chunks > 1) load_chunk(1);
+    __syncthreads();
+
+    const int kg = lane >> 5;
+    // patch offset of tap (r, s): (r*dh*PWi + s*dw) * kPix, advanced incrementally
+    const int tap_ds = g.dw * kPix;
+    const int tap_dr = g.dh * g.PWi * kPix - (g.kw - 1) * g.dw * kPix;
+    for (int ch = 0; ch < g.chunks; ++ch) {
+        const uint16_t* cur = lds + (ch & 1) * buf_elems;
+        // steps = (tap, kk) pairs; the B fragments of step t+1 are read from LDS
+        // while the MFMAs of step t run
+        u32x4_t bcur[3][Cfg::FC], bnext[3][Cfg::FC];
+        auto read_b = [&](int toff, int kk, u32x4_t (&b)[3][Cfg::FC]) {
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+#pragma unroll
+                for (int j = 0; j < Cfg::FC; ++j)
+                    b[p][j] = *reinterpret_cast<const u32x4_t*>(cur + p * plane_elems + pbase[j] + toff + kk * 16 +
+                                                                 kg * 8);
+        };
+        read_b(0, 0, bcur);
+        int toff = 0, s = 0;
+        uint2 w[Cfg::FR];
+        for (int tap = 0; tap < g.taps; ++tap) {
+#pragma unroll
+            for (int f = 0; f < Cfg::FR; ++f) {
+                const uint16_t* src = cur + wofs + (tap * Cfg::BM + wrow + f * 32) * kWordHalves;
+                if (TERNARY) w[f] = *reinterpret_cast<const uint2*>(src);
+                else w[f] = make_uint2(*reinterpret_cast<const uint32_t*>(src), 0u);
+            }
+            // next tap's patch offset
+            int next_toff = toff + tap_ds, next_s = s + 1;
+            if (next_s == g.kw) {
+                next_s = 0;
+                next_toff = toff + tap_dr;
+            }
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                if (kk == 0) read_b(toff, 1, bnext);
+                else if (tap + 1 < g.taps) read_b(next_toff, 0, bnext);
+                u32x4_t a[Cfg::FR];
+#pragma unroll
+                for (int f = 0; f < Cfg::FR; ++f) a[f] = weight_frag<TERNARY>(w[f], kk, kg);
+#pragma unroll
+                for (int p = 0; p < 3; ++p)
+#pragma unroll
+                    for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+                        for (int j = 0; j < Cfg::FC; ++j) acc[f][j] = mfma32(a[f], bcur[p][j], acc[f][j]);
+#pragma unroll
+                for (int p = 0; p < 3; ++p)
+#pragma unroll
+                    for (int j = 0; j < Cfg::FC; ++j) bcur[p][j] = bnext[p][j];
+            }
+            toff = next_toff;
+            s = next_s;
+        }
+        if (ch + 1 < g.chunks) {
+            store_chunk((ch + 1) & 1);
+            if (ch + 2 < g.chunks) load_chunk(ch + 2);
+        }
+        __syncthreads();
+    }
+
+    // ---- epilogue: scale, bias, residual, ReLU, optional 2x2 max pool ----
+    // Every value is computed (all loads issued together) before the first
+    // store: y may alias nothing, but the compiler cannot know, and loads
+    // interleaved with stores would each wait a full memory round trip.
+    const bool pool = g.pool != 0;
+    const int64_t plane = pool ? static_cast<int64_t>(g.PH) * g.PW : static_cast<int64_t>(g.OH) * g.OW;
+    float mult[Cfg::FR][16], badd[Cfg::FR][16];
+#pragma unroll
+    for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int m = min(m0 + wm * Cfg::WM + frag_out_row(f, e, lane), g.M - 1);
+            mult[f][e] = epi.scale ? epi.alpha * epi.scale[m] : epi.alpha;
+            badd[f][e] = epi.bias ? epi.bias[m] : 0.0f;
+        }
+    int64_t out_base[Cfg::FC];
+    bool valid[Cfg::FC];
+#pragma unroll
+    for (int j = 0; j < Cfg::FC; ++j) {
+        int oh, ow, pi;
+        valid[j] = tile_pixel<Cfg>(g, q0, oh0, ow0, wq * Cfg::WQ + j * 32 + (lane & 31), oh, ow, pi);
+        if (!valid[j]) oh = ow = 0;
+        out_base[j] = pool ? (static_cast<int64_t>(n) * g.M * g.PH + (oh >> 1)) * g.PW + (ow >> 1)
+                           : (static_cast<int64_t>(n) * g.M * g.OH + oh) * g.OW + ow;
+    }
+#pragma unroll
+    for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+        for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                float v = acc[f][j][e];
+                v = (epi.flags & TBN_EPI_BIAS_THEN_SCALE) ? (v + badd[f][e]) * mult[f][e] : v * mult[f][e] + badd[f][e];
+                acc[f][j][e] = v;
+            }
+    if (epi.residual) {
+        // residual only without pooling (host-checked): same index as the output
+        float res[Cfg::FC][Cfg::FR][16];
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int m = m0 + wm * Cfg::WM + frag_out_row(f, e, lane);
+                    res[j][f][e] = (m < g.M && valid[j]) ? epi.residual[out_base[j] + static_cast<int64_t>(m) * plane]
+                                                         : 0.0f;
+                }
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[f][j][e] += res[j][f][e];
+    }
+#pragma unroll
+    for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+        for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                float v = acc[f][j][e];
+                if (epi.flags & TBN_EPI_RELU) v = v > 0.0f ? v : 0.0f;
+                if (pool) {
+                    v = fmaxf(v, __shfl_xor(v, 1));
+                    v = fmaxf(v, __shfl_xor(v, 2));
+                }
+                const int m = m0 + wm * Cfg::WM + frag_out_row(f, e, lane);
+                if (m < g.M && valid[j] && (!pool || (lane & 3) == 0))
+                    epi.y[out_base[j] + static_cast<int64_t>(m) * plane] = v;
+            }
+}
+
+// ---------------------------------------------------------------------------
+// Weight re-order: reference k = c*taps + tap  ->  k' = ((c/32)*taps + tap)*32 + c%32
+// ---------------------------------------------------------------------------
+
+struct ConvWeightDims {
+    int M, C, taps, chunks;
+    int64_t K_pad;   // reference layout column: K_pad/8 bytes (binary) or K_pad/4 (ternary)
+    int64_t Kc;      // conv layout k' count: chunks * taps * 32
+    int M_alloc;     // columns written: ceil8(M)
+};
+
+__device__ __forceinline__ bool conv_k_to_ref(const ConvWeightDims& d, int64_t kp, int64_t& k) {
+    const int64_t step = kp / kChunk;
+    const int cl = static_cast<int>(kp - step * kChunk);
+    const int ch = static_cast<int>(step / d.taps);
+    const int tap = static_cast<int>(step - static_cast<int64_t>(ch) * d.taps);
+    const int c = ch * kChunk + cl;
+    if (c >= d.C) return false;
+    k = static_cast<int64_t>(c) * d.taps + tap;
+    return true;
+}
+
+// One thread per output byte; padding channels and columns get +1 (bit 0),
+// which meets zero activations.
+__global__ void reorder_conv_binary_kernel(const uint8_t* __restrict__ ref, ConvWeightDims d,
+                                           uint8_t* __restrict__ out) {
+    const int64_t bpc = d.Kc / 8;
+    const int64_t total = static_cast<int64_t>(d.M_alloc) * bpc;
+    for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
+         t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int m = static_cast<int>(t / bpc);
+        const int64_t kb = t - m * bpc;
+        uint32_t byte = 0;
+        if (m < d.M) {
+            const uint8_t* col = ref + m * (d.K_pad / 8);
+            for (int e = 0; e < 8; ++e) {
+                int64_t k;
+                if (conv_k_to_ref(d, kb * 8 + e, k)) byte |= ((col[k >> 3] >> (k & 7)) & 1u) << e;
+            }
+        }
+        out[t] = static_cast<uint8_t>(byte);
+    }
+}
+
+// Ternary: four codes per byte; padding code 01 (0).
+__global__ void reorder_conv_ternary_kernel(const uint8_t* __restrict__ ref, ConvWeightDims d,
+                                            uint8_t* __restrict__ out) {
+    const int64_t bpc = d.Kc / 4;
+    const int64_t total = static_cast<int64_t>(d.M_alloc) * bpc;
+    for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
+         t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int m = static_cast<int>(t / bpc);
+        const int64_t kb = t - m * bpc;
+        uint32_t byte = 0x55u;
+        if (m < d.M) {
+            const uint8_t* col = ref + m * (d.K_pad / 4);
+            byte = 0;
+            for (int e = 0; e < 4; ++e) {
+                int64_t k;
+                uint32_t code = 1u;
+                if (conv_k_to_ref(d, kb * 4 + e, k)) code = (col[k >> 2] >> ((k & 3) * 2)) & 3u;
+                byte |= code << (2 * e);
+            }
+        }
+        out[t] = static_cast<uint8_t>(byte);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+
+int64_t conv_weight_bytes(int weights, const tbn_conv2d_desc* d) {
+    const int64_t Kc = (d->c + kChunk - 1) / kChunk * d->kh * d->kw * kChunk;
+    return (d->m + 7) / 8 * 8 * Kc / (weights == TBN_WEIGHTS_BINARY ? 8 : 4);
+}
+
+struct TileChoice {
+    int cfg;     // index into the PatchCfg menu
+    int linear;  // 1: linear tiles, 0: 2-D tiles
+    int TH, TW, BM, NT;
+};
+
+size_t lds_bytes(const PatchGeom& g, int BM, bool ternary) {
+    const size_t patch = static_cast<size_t>(3) * g.PHi * g.PWi * kPix * 2;
+    const size_t words = static_cast<size_t>(BM) * g.taps * (ternary ? 8 : 4);
+    return 2 * (patch + words);
+}
+
+void fill_patch(PatchGeom& g, const TileChoice& c) {
+    g.linear = c.linear;
+    int rows;  // output rows one tile's pixels span (at most)
+    if (c.linear) {
+        const int per = g.pool ? c.TH * c.TW / 4 : c.TH * c.TW;
+        const int total = g.pool ? g.PH * g.PW : g.OH * g.OW;
+        const int rowlen = g.pool ? g.PW : g.OW;
+        g.tiles_img = (total + per - 1) / per;
+        int span = 1;
+        for (int t = 0; t < g.tiles_img; ++t) {
+            const int first = t * per / rowlen;
+            const int last = (std::min((t + 1) * per, total) - 1) / rowlen;
+            span = std::max(span, last - first + 1);
+        }
+        rows = g.pool ? 2 * span : span;
+        g.PWi = (g.OW - 1) * g.sw + (g.kw - 1) * g.dw + 1;
+        g.tiles_h = g.tiles_w = 0;
+    } else {
+        rows = c.TH;
+        g.PWi = (c.TW - 1) * g.sw + (g.kw - 1) * g.dw + 1;
+        g.tiles_h = (g.VH + c.TH - 1) / c.TH;
+        g.tiles_w = (g.VW + c.TW - 1) / c.TW;
+        g.tiles_img = g.tiles_h * g.tiles_w;
+    }
+    g.PHi = (rows - 1) * g.sh + (g.kh - 1) * g.dh + 1;
+}
+
+// Tile menu: (BM, TH, TW, wave tile); TH x TW is also the pixel count of a
+// linear tile.
+using P0 = PatchCfg<128, 8, 16, 64, 64>;  // 24 MFMA per wave per K step
+using P1 = PatchCfg<128, 8, 8, 64, 32>;
+using P2 = PatchCfg<64, 8, 16, 32, 64>;
+using P3 = PatchCfg<64, 8, 8, 32, 32>;
+using P4 = PatchCfg<32, 8, 8, 32, 32>;    // <= 32 output channels
+using P5 = PatchCfg<128, 4, 8, 64, 32>;   // small 2-D patches (strided / large kernels)
+using P6 = PatchCfg<64, 4, 8, 32, 32>;
+
+template <class Cfg>
+constexpr TileChoice choice(int cfg, int linear) {
+    return TileChoice{cfg, linear, Cfg::TH, Cfg::TW, Cfg::BM, Cfg::NT};
+}
+
+// TBN_CONV_TILE=<id> forces a tile (tuning only): id = cfg for linear tiles,
+// 10 + cfg for 2-D tiles.
+int tile_override() {
+    static const int v = [] {
+        const char* e = std::getenv("TBN_CONV_TILE");
+        return e ? std::atoi(e) : -1;
+    }();
+    return v;
+}
+
+// In preference order (linear tiles store whole 128-byte pixel runs; larger
+// tiles do more MFMA per decoded weight word), the first tile whose patch fits
+// the LDS and the staging registers and that gives >= 240 blocks; otherwise
+// the feasible tile with the most blocks.
+bool choose_tile(PatchGeom& g, TileChoice& out) {
+    const TileChoice menu[] = {choice<P0>(0, 1),  choice<P1>(1, 1),  choice<P2>(2, 1),  choice<P3>(3, 1),
+                               choice<P4>(4, 1),  choice<P0>(0, 0),  choice<P1>(1, 0),  choice<P2>(2, 0),
+                               choice<P3>(3, 0),  choice<P4>(4, 0),  choice<P5>(5, 0),  choice<P6>(6, 0)};
+    const TileChoice* best = nullptr;
+    int64_t best_blocks = -1;
+    const int forced = tile_override();
+    for (const auto& c : menu) {
+        const int id = c.linear ? c.cfg : 10 + c.cfg;
+        if (forced >= 0 && id != forced) continue;
+        if (forced < 0) {
+            if (g.M <= 32 && c.BM != 32) continue;
+            if (g.M > 32 && c.BM == 32) continue;
+            if (g.M <= 64 && c.BM == 128) continue;
+        }
+        PatchGeom t = g;
+        fill_patch(t, c);
+        if (lds_bytes(t, c.BM, true) > static_cast<size_t>(kMaxLds)) continue;
+        if (4 * t.PHi * t.PWi > 8 * c.NT) continue;  // patch staging registers per thread
+        if (c.BM * t.taps > 8 * c.NT) continue;      // weight staging registers per thread
+        const int64_t blocks = static_cast<int64_t>(t.N) * t.tiles_img * ((g.M + c.BM - 1) / c.BM);
+        if (forced >= 0 || blocks >= 240) {
+            out = c;
+            g = t;
+            return true;
+        }
+        if (blocks > best_blocks) {
+            best_blocks = blocks;
+            best = &c;
+        }
+    }
+    if (!best) return false;
+    out = *best;
+    fill_patch(g, out);
+    return true;
+}
+
+template <class Cfg, bool TERNARY>
+int launch_patch(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
+                 const PatchEpi& epi, hipStream_t s) {
+    const size_t lds = lds_bytes(g, Cfg::BM, TERNARY);
+    const int items = 4 * g.PHi * g.PWi;
+    if ((items + Cfg::NT - 1) / Cfg::NT > 8 || (Cfg::BM * g.taps + Cfg::NT - 1) / Cfg::NT > 8)
+        return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for the staging registers");
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_patch_kernel<Cfg, TERNARY>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
+        if (e != hipSuccess) return tbn_hip::fail(TBN_RUNTIME_ERROR, std::string("hipFuncSetAttribute: ") +
+                                                                         hipGetErrorString(e));
+        attr_set = true;
+    }
+    const int64_t blocks = static_cast<int64_t>(g.N) * g.tiles_img * ((g.M + Cfg::BM - 1) / Cfg::BM);
+    hipLaunchKernelGGL((conv_patch_kernel<Cfg, TERNARY>), dim3(static_cast<unsigned>(blocks)), dim3(Cfg::NT), lds, s,
+                       x, g, w, col_bytes, m_alloc, epi);
+    return tbn_hip::check_launch(TERNARY ? "conv2d_f32_ternary (patch)" : "conv2d_f32_binary (patch)");
+}
+
+template <bool TERNARY>
+int dispatch_patch(int id, const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
+                   const PatchEpi& epi, hipStream_t s) {
+    switch (id) {
+        case 0: return launch_patch<P0, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 1: return launch_patch<P1, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 2: return launch_patch<P2, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 3: return launch_patch<P3, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 4: return launch_patch<P4, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 5: return launch_patch<P5, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        default: return launch_patch<P6, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+    }
+}
+
+int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
+    ConvGeom cg;
+    int rc = make_geom(d, flags, cg);
+    if (rc) return rc;
+    g.N = int(d->n); g.C = int(d->c); g.H = int(d->h); g.W = int(d->w); g.M = int(d->m);
+    g.kh = int(d->kh); g.kw = int(d->kw); g.sh = int(d->sh); g.sw = int(d->sw);
+    g.ph = int(d->ph); g.pw = int(d->pw); g.dh = int(d->dh); g.dw = int(d->dw);
+    g.OH = cg.OHW / cg.OW;
+    g.OW = cg.OW;
+    g.taps = g.kh * g.kw;
+    g.chunks = (g.C + kChunk - 1) / kChunk;
+    g.pool = cg.pool;
+    g.PH = g.pool ? g.OH / 2 : 0;
+    g.PW = g.pool ? g.OW / 2 : 0;
+    g.VH = g.pool ? 2 * g.PH : g.OH;
+    g.VW = g.pool ? 2 * g.PW : g.OW;
+    return TBN_SUCCESS;
+}
+
+int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, const uint8_t* conv_weights,
+                   const float* scale, float alpha, const float* bias, const float* residual, int flags, float* y,
+                   hipStream_t s) {
+    TBN_REQUIRE(weights == TBN_WEIGHTS_BINARY || weights == TBN_WEIGHTS_TERNARY, TBN_INVALID_ARGUMENT,
+                "unknown weights kind");
+    TBN_REQUIRE((flags & ~(TBN_EPI_RELU | TBN_EPI_BIAS_THEN_SCALE | TBN_EPI_MAXPOOL2X2)) == 0,
+                TBN_INVALID_ARGUMENT, "unknown epilogue flags");
+    PatchGeom g;
+    int rc = make_patch_geom(desc, flags, g);
+    if (rc) return rc;
+    TBN_REQUIRE(!(residual && g.pool), TBN_INVALID_ARGUMENT,
+                "a residual input cannot be combined with the fused max pool");
+    TileChoice tc;
+    TBN_REQUIRE(choose_tile(g, tc), TBN_INVALID_SHAPE, "no conv tile fits this kernel size / stride / dilation");
+    if (g.VH == 0 || g.VW == 0 || g.N == 0) return tbn_hip::ok();
+    TBN_REQUIRE(x && conv_weights && y, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_REQUIRE(reinterpret_cast<uintptr_t>(conv_weights) % 8 == 0, TBN_INVALID_ARGUMENT,
+                "conv weights must be 8-byte aligned");
+    TBN_DEVICE_GUARD();
+    const int64_t Kc = static_cast<int64_t>(g.chunks) * g.taps * kChunk;
+    const int64_t col_bytes = Kc / (weights == TBN_WEIGHTS_BINARY ? 8 : 4);
+    const int m_alloc = int((desc->m + 7) / 8 * 8);
+    PatchEpi epi{y, scale, alpha, bias, residual, flags};
+    if (weights == TBN_WEIGHTS_TERNARY) return dispatch_patch<true>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, epi, s);
+    return dispatch_patch<false>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, epi, s);
+}
+
+}  // namespace
+
+namespace tbn_hip {
+
+bool conv_patch_supported(const tbn_conv2d_desc* desc) {
+    PatchGeom g;
+    if (make_patch_geom(desc, 0, g) != TBN_SUCCESS) return false;
+    TileChoice tc;
+    return choose_tile(g, tc);
+}
+
+int conv_patch_from_reference(int weights, const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed,
+                              int64_t K_pad, int64_t N_pad, const float* scale, float alpha, const float* bias,
+                              const float* residual, int flags, float* y, hipStream_t s) {
+    const int64_t wbytes = conv_weight_bytes(weights, desc);
+    void* buf = nullptr;
+    hipError_t e = hipMallocAsync(&buf, static_cast<size_t>(wbytes), s);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(e == hipErrorOutOfMemory ? TBN_OUT_OF_MEMORY : TBN_RUNTIME_ERROR,
+                    std::string("conv weight buffer allocation failed: ") + hipGetErrorString(e));
+    }
+    int rc = tbn_hip_pack_conv_weights(weights, packed, K_pad, N_pad, desc, static_cast<uint8_t*>(buf), s);
+    if (rc == TBN_SUCCESS)
+        rc = conv_patch_run(weights, x, desc, static_cast<const uint8_t*>(buf), scale, alpha, bias, residual, flags,
+                            y, s);
+    (void)hipFreeAsync(buf, s);
+    return rc;
+}
+
+}  // namespace tbn_hip
+
+extern "C" {
+
+int tbn_hip_conv_weights_bytes(int weights, const tbn_conv2d_desc* desc, int64_t* bytes) {
+    TBN_REQUIRE(weights == TBN_WEIGHTS_BINARY || weights == TBN_WEIGHTS_TERNARY, TBN_INVALID_ARGUMENT,
+                "unknown weights kind");
+    PatchGeom g;
+    int rc = make_patch_geom(desc, 0, g);
+    if (rc) return rc;
+    TileChoice tc;
+    TBN_REQUIRE(choose_tile(g, tc), TBN_INVALID_SHAPE,
+                "no conv tile fits this kernel size / stride / dilation (use the reference-layout entry points)");
+    TBN_REQUIRE(bytes != nullptr, TBN_INVALID_ARGUMENT, "null pointer");
+    *bytes = conv_weight_bytes(weights, desc);
+    return tbn_hip::ok();
+}
+
+int tbn_hip_pack_conv_weights(int weights, const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                              const tbn_conv2d_desc* desc, uint8_t* conv_weights, tbn_stream_t stream) {
+    TBN_REQUIRE(weights == TBN_WEIGHTS_BINARY || weights == TBN_WEIGHTS_TERNARY, TBN_INVALID_ARGUMENT,
+                "unknown weights kind");
+    ConvGeom g;
+    int rc = make_geom(desc, 0, g);
+    if (rc) return rc;
+    const int64_t K = desc->c * desc->kh * desc->kw;
+    TBN_REQUIRE(K_pad >= K && K_pad % 32 == 0, TBN_INVALID_SHAPE, "K_pad must be >= C*kh*kw and a multiple of 32");
+    TBN_REQUIRE(N_pad >= desc->m, TBN_INVALID_SHAPE, "N_pad must be >= output channels");
+    TBN_REQUIRE(packed && conv_weights, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    const int chunks = int((desc->c + kChunk - 1) / kChunk);
+    ConvWeightDims d{int(desc->m), int(desc->c), int(desc->kh * desc->kw), chunks, K_pad,
+                     static_cast<int64_t>(chunks) * desc->kh * desc->kw * kChunk, int((desc->m + 7) / 8 * 8)};
+    const int64_t bytes = conv_weight_bytes(weights, desc);
+    const int blocks = static_cast<int>(std::min<int64_t>(tbn_hip::ceil_div(bytes, 256), 4096));
+    if (weights == TBN_WEIGHTS_TERNARY)
+        hipLaunchKernelGGL(reorder_conv_ternary_kernel, dim3(blocks), dim3(256), 0, tbn_hip::stream_of(stream),
+                           packed, d, conv_weights);
+    else
+        hipLaunchKernelGGL(reorder_conv_binary_kernel, dim3(blocks), dim3(256), 0, tbn_hip::stream_of(stream),
+                           packed, d, conv_weights);
+    return tbn_hip::check_launch("pack_conv_weights");
+}
+
+int tbn_hip_conv2d_f32_prepacked(int weights, const float* x, const tbn_conv2d_desc* desc,
+                                 const uint8_t* conv_weights, const float* scale, float alpha, const float* bias,
+                                 const float* residual, int flags, float* y, tbn_stream_t stream) {
+    return conv_patch_run(weights, x, desc, conv_weights, scale, alpha, bias, residual, flags, y,
+                          tbn_hip::stream_of(stream));
+}
+
+}  // extern "C"

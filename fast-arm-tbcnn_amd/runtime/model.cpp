@@ -190,6 +190,8 @@ struct Op {
     int flags = 0;
     int residual = -1;       // value id of a fused residual addend
     const PackedWeights* pw = nullptr;
+    const Tensor* conv_w = nullptr;  // conv-layout weights of the patch conv path
+    int workspace = -1;              // value id of the op's transient workspace (none yet)
     const float* scale = nullptr;  // per-channel scale (device)
     const float* w = nullptr;      // fp32 weights (device)
     const float* bias = nullptr;   // device
@@ -239,6 +241,7 @@ struct TBNModel::Session::Impl {
     std::unordered_map<std::string, Tensor> dev_scales;        // device per-channel scales
     std::unordered_map<std::string, bool> conv_already_binary;
     std::unordered_map<std::string, PackedWeights> packed;      // key: name + "#" + variant
+    std::unordered_map<std::string, Tensor> conv_packed;        // conv-layout copies of `packed` entries
     std::unordered_map<std::string, Tensor> scaled_addends;     // beta * C of quantized Gemms
 
     // ---- the compiled plan ----
@@ -419,6 +422,24 @@ struct TBNModel::Session::Impl {
             TBN_CHECK(wt == DataType::FLOAT32, InvalidArgumentError, "Conv '" + node.name + "': unsupported weight type");
             op.kind = OpKind::ConvF32;
             op.w = const_f32(wi);
+        }
+        const int kind = op.pw && op.pw->kind == PackedWeights::Kind::Ternary ? TBN_WEIGHTS_TERNARY
+                                                                              : TBN_WEIGHTS_BINARY;
+        int64_t wbytes = 0;
+        if (op.kind == OpKind::ConvQuant && op.desc.c >= 16 &&
+            tbn_hip_conv_weights_bytes(kind, &op.desc, &wbytes) == TBN_SUCCESS) {
+            // patch conv: conv-layout weights once per Session, then no
+            // allocation and no re-ordering per run
+            const std::string key = wname + "#conv" + std::to_string(reinterpret_cast<uintptr_t>(op.pw));
+            auto it = conv_packed.find(key);
+            if (it == conv_packed.end()) {
+                Tensor cw = Tensor::empty({wbytes}, DataType::UINT8, DeviceType::HIP);
+                check_status(tbn_hip_pack_conv_weights(kind, op.pw->bits.typed_data<uint8_t>(), op.pw->K_pad,
+                                                       op.pw->N_pad, &op.desc, cw.typed_data<uint8_t>(), cur_stream()),
+                             ("Conv '" + node.name + "'").c_str());
+                it = conv_packed.emplace(key, cw).first;
+            }
+            op.conv_w = &it->second;
         }
         op.out = new_value(node.outputs[0], Shape{xs.dims[0], ws.dims[0], OH, OW}, DataType::FLOAT32);
         ops.push_back(op);
@@ -748,6 +769,10 @@ struct TBNModel::Session::Impl {
             if (values[o].def < 0) values[o].def = i;
             values[o].last = std::max(values[o].last, i);
             for (int in : ops[i].in) values[root(in)].last = std::max(values[root(in)].last, i);
+            if (ops[i].workspace >= 0) {
+                values[ops[i].workspace].def = i;
+                values[ops[i].workspace].last = i;
+            }
         }
         for (const auto& name : graph->outputs) {
             auto it = value_id.find(name);
@@ -847,6 +872,16 @@ struct TBNModel::Session::Impl {
                              what.c_str());
                 return;
             case OpKind::ConvQuant:
+                if (op.conv_w) {
+                    check_status(tbn_hip_conv2d_f32_prepacked(
+                                     op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY
+                                                                                : TBN_WEIGHTS_TERNARY,
+                                     fp(op.in[0]), &op.desc, op.conv_w->typed_data<uint8_t>(), op.scale, 1.0f,
+                                     op.bias, op.residual >= 0 ? fp(op.residual) : nullptr, op.flags, fp(op.out),
+                                     s),
+                                 what.c_str());
+                    return;
+                }
                 check_status(tbn_hip_conv2d_f32_quantized(
                                  op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY : TBN_WEIGHTS_TERNARY,
                                  fp(op.in[0]), &op.desc, op.pw->bits.typed_data<uint8_t>(), op.pw->K_pad,
@@ -1000,6 +1035,7 @@ struct TBNModel::Session::Impl {
         size_t b = arena.data_size();
         for (auto& kv : dev_init) b += kv.second.data_size();
         for (auto& kv : packed) b += kv.second.bits.data_size();
+        for (auto& kv : conv_packed) b += kv.second.data_size();
         for (auto& kv : dev_scales) b += kv.second.data_size();
         return b;
     }

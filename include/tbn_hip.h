@@ -227,6 +227,33 @@ int tbn_hip_conv2d_f32_quantized(int weights, const float* x, const tbn_conv2d_d
                                  const float* scale, float alpha, const float* bias,
                                  const float* residual, int flags, float* y, tbn_stream_t stream);
 
+/* ---- binary / ternary Conv2D on pre-packed conv-layout weights ------------
+ * For inputs of 16 or more channels the conv kernels behind the entry points
+ * above stage each block's input patch (32 channels at a time, split into the
+ * three bf16 parts) in LDS and run every tap from it.  Their weights use the
+ * "conv layout": column m holds Kc = ceil(C/32) * kh*kw * 32 values in the
+ * order k' = ((c / 32) * kh*kw + r*kw + s) * 32 + c % 32, in the reference's
+ * encoding (bit 1 = -1, or the 2-bit code); channels >= C are +1 / 0 and meet
+ * zero activations.  The entry points above re-order the reference layout
+ * into a stream-ordered temporary (hipMallocAsync) on every call; a caller
+ * that runs a layer many times (the Session) packs once and calls
+ * tbn_hip_conv2d_f32_prepacked, which allocates nothing. */
+
+/* Bytes of the conv-layout weights for `desc` (weights: TBN_WEIGHTS_BINARY or
+ * TBN_WEIGHTS_TERNARY): ceil8(M) * Kc / 8 (binary) or / 4 (ternary). */
+int tbn_hip_conv_weights_bytes(int weights, const tbn_conv2d_desc* desc, int64_t* bytes);
+/* Re-orders packed weights from the reference layout (BinaryMatrix bits or the
+ * 2-bit GEMM layout of the [M, C*kh*kw] matrix, as tbn_hip_conv2d_f32_binary /
+ * _ternary take them) into the conv layout (8-byte aligned output). */
+int tbn_hip_pack_conv_weights(int weights, const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                              const tbn_conv2d_desc* desc, uint8_t* conv_weights, tbn_stream_t stream);
+/* tbn_hip_conv2d_f32_quantized on conv-layout weights: same arithmetic and
+ * epilogue, no allocation.  Returns TBN_INVALID_SHAPE for geometries whose
+ * patch does not fit (very large kernels or dilations). */
+int tbn_hip_conv2d_f32_prepacked(int weights, const float* x, const tbn_conv2d_desc* desc,
+                                 const uint8_t* conv_weights, const float* scale, float alpha, const float* bias,
+                                 const float* residual, int flags, float* y, tbn_stream_t stream);
+
 /* ---- fp32 layers and epilogue operators (Session support) ------------------ */
 
 /* fp32 Conv2D (tbn::conv2d, conv2d.cpp:78-192), weights fp32 [M, C, kh, kw];

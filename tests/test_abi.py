@@ -42,3 +42,16 @@ def test_argument_errors_are_reported_before_device_use():
     hw = (ctypes.c_int64 * 2)()
     assert lib.tbn_hip_maxpool2d(None, 1, 1, 112, 112, 3, 3, 2, 2, 1, 1, 1, 1, 0, None, hw, None) == 0
     assert list(hw) == [56, 56]
+
+
+def test_conv_weight_sizes_are_host_only():
+    wb = ctypes.c_int64()
+    lib = tbn_hip.lib()
+    d = tbn_hip.conv_desc(64, 64, 14, 14, 128, 3, 3, 1, 1, 1, 1)
+    assert lib.tbn_hip_conv_weights_bytes(0, ctypes.byref(d), ctypes.byref(wb)) == 0
+    assert wb.value == 128 * 2 * 9 * 32 // 8          # two 32-channel chunks x 9 taps
+    assert lib.tbn_hip_conv_weights_bytes(1, ctypes.byref(d), ctypes.byref(wb)) == 0
+    assert wb.value == 128 * 2 * 9 * 32 // 4
+    assert lib.tbn_hip_conv_weights_bytes(5, ctypes.byref(d), ctypes.byref(wb)) == tbn_hip.INVALID_ARGUMENT
+    big = tbn_hip.conv_desc(1, 64, 200, 200, 8, 15, 15, 1, 1, 28, 28, 4, 4)  # patch cannot fit the LDS
+    assert lib.tbn_hip_conv_weights_bytes(0, ctypes.byref(big), ctypes.byref(wb)) == tbn_hip.INVALID_SHAPE

@@ -114,3 +114,81 @@ def test_conv_f32(dev, orc, case):
     if pool:
         ref = ref[:, :, :OH // 2 * 2, :OW // 2 * 2].reshape(N, M, OH // 2, 2, OW // 2, 2).max(axis=(3, 5))
     rm.assert_within_tolerance(host(y), ref, C * kh * kw, np.abs(x).max() * np.abs(w).max())
+
+
+def _np_conv_layout_bits(wbytes, M_alloc):
+    """Closed form of the conv weight layout: column m, bit
+    k' = ((c // 32) * kh*kw + r*kw + s) * 32 + c % 32 set iff -1."""
+    M, C, kh, kw = wbytes.shape
+    chunks = (C + 31) // 32
+    full = np.zeros((M_alloc, chunks, 32, kh * kw), np.uint8)  # [m, chunk, c%32, tap]
+    t = (wbytes != 1).reshape(M, C, kh * kw)
+    padded = np.zeros((M, chunks * 32, kh * kw), np.uint8)
+    padded[:, :C] = t
+    full[:M] = padded.reshape(M, chunks, 32, kh * kw)
+    neg = full.transpose(0, 1, 3, 2).reshape(M_alloc, -1)  # [m, chunk, tap, c%32]
+    return np.packbits(neg, axis=1, bitorder="little").reshape(-1)
+
+
+@pytest.mark.parametrize("case", [(2, 16, 9, 9, 40, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_RELU),
+                                  (3, 40, 10, 7, 33, 3, 3, (2, 2), (1, 1), (1, 1), tbn_hip.EPI_MAXPOOL2X2),
+                                  (2, 64, 8, 8, 200, 1, 1, (1, 1), (0, 0), (1, 1), 0),
+                                  (1, 32, 12, 12, 16, 3, 3, (1, 1), (2, 2), (2, 2), tbn_hip.EPI_BIAS_THEN_SCALE),
+                                  (2, 96, 19, 23, 72, 5, 5, (1, 2), (2, 2), (1, 1), tbn_hip.EPI_RELU)])
+def test_conv_prepacked_entry_point(dev, orc, case):
+    """Pre-packed conv-layout weights: tbn_hip_pack_conv_weights matches the
+    closed form bit for bit, and tbn_hip_conv2d_f32_prepacked equals
+    tbn_hip_conv2d_f32_binary bitwise (same kernel) and the float64 oracle
+    within tolerance."""
+    import ctypes
+    N, C, H, W, M, kh, kw, stride, pad, dil, flags = case
+    rng = np.random.default_rng(C * 1000 + M)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    wbytes = (rng.random((M, C, kh, kw)) < 0.5).astype(np.uint8)
+    scale = rng.uniform(0.5, 1.5, M).astype(np.float32)
+    bias = (rng.standard_normal(M) * 0.01).astype(np.float32)
+    K = C * kh * kw
+    packed, K_pad, N_pad = pack_conv_weights(wbytes, M, K)
+    d = tbn_hip.conv_desc(N, C, H, W, M, kh, kw, *stride, *pad, *dil)
+    wb = ctypes.c_int64()
+    tbn_hip.call("tbn_hip_conv_weights_bytes", tbn_hip.WEIGHTS_BINARY, d, ctypes.byref(wb))
+    M_alloc = (M + 7) // 8 * 8
+    assert wb.value == M_alloc * ((C + 31) // 32) * kh * kw * 32 // 8
+    cw = empty(wb.value, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_conv_weights", tbn_hip.WEIGHTS_BINARY, P(packed), K_pad, N_pad, d, P(cw), None)
+    assert np.array_equal(host(cw), _np_conv_layout_bits(wbytes, M_alloc))
+    OH, OW = tbn_hip.conv_out_hw(d)
+    oshape = (N, M, OH // 2, OW // 2) if flags & tbn_hip.EPI_MAXPOOL2X2 else (N, M, OH, OW)
+    dx, ds, db = to_dev(x), to_dev(scale), to_dev(bias)
+    y1 = empty(oshape, torch.float32)
+    y2 = empty(oshape, torch.float32)
+    y1.fill_(np.nan)
+    tbn_hip.call("tbn_hip_conv2d_f32_prepacked", tbn_hip.WEIGHTS_BINARY, P(dx), d, P(cw), P(ds), 1.0, P(db), None,
+                 flags, P(y1), None)
+    tbn_hip.call("tbn_hip_conv2d_f32_binary", P(dx), d, P(packed), K_pad, N_pad, P(ds), 1.0, P(db), flags, P(y2), None)
+    assert np.array_equal(host(y1), host(y2))
+    wsign = np.where(wbytes == 1, 1.0, -1.0).astype(np.float32)
+    ref = conv_ref(x, wsign, scale, 1.0, bias, stride, pad, dil, flags)
+    rm.assert_within_tolerance(host(y1), ref, K, np.abs(x).max() * 1.5)
+
+
+def test_conv_patch_residual_epilogue(dev, orc):
+    """Residual add fused after scale/bias and before ReLU (the Session's Conv + Add + Relu)."""
+    rng = np.random.default_rng(5)
+    N, C, H, W, M = 2, 32, 10, 10, 32
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    res = rng.standard_normal((N, M, H, W)).astype(np.float32)
+    wbytes = (rng.random((M, C, 3, 3)) < 0.5).astype(np.uint8)
+    scale = rng.uniform(0.5, 1.5, M).astype(np.float32)
+    bias = (rng.standard_normal(M) * 0.01).astype(np.float32)
+    K = C * 9
+    packed, K_pad, N_pad = pack_conv_weights(wbytes, M, K)
+    d = tbn_hip.conv_desc(N, C, H, W, M, 3, 3, 1, 1, 1, 1)
+    y = empty((N, M, H, W), torch.float32)
+    flags = tbn_hip.EPI_RELU | tbn_hip.EPI_BIAS_THEN_SCALE
+    tbn_hip.call("tbn_hip_conv2d_f32_quantized", tbn_hip.WEIGHTS_BINARY, P(to_dev(x)), d, P(packed), K_pad, N_pad,
+                 P(to_dev(scale)), 1.0, P(to_dev(bias)), P(to_dev(res)), flags, P(y), None)
+    wsign = np.where(wbytes == 1, 1.0, -1.0).astype(np.float32)
+    ref = conv_ref(x, wsign, scale, 1.0, bias, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_BIAS_THEN_SCALE)
+    ref = np.maximum(ref + res, 0.0)
+    rm.assert_within_tolerance(host(y), ref, K, np.abs(x).max() * 1.5)
