@@ -94,6 +94,7 @@ struct PatchCfg {
     static constexpr int FR = WM / 32, FC = WQ / 32;
     static_assert(QT % WQ == 0 && BM % WM == 0 && WM % 32 == 0 && WQ % 32 == 0, "bad tile");
     static_assert(TH % 2 == 0 && TW % 2 == 0, "tiles must hold whole 2x2 pool windows");
+    static_assert(NT >= BM, "one thread per channel stages the epilogue factors");
 };
 
 template <bool TERNARY>
@@ -152,6 +153,16 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
         ow0 = (st - th * g.tiles_w) * Cfg::TW;
     }
     const int ih0 = oh0 * g.sh - g.ph, iw0 = ow0 * g.sw - g.pw;
+
+    // per-channel epilogue factors of the block's BM channels: loaded now (the
+    // load latency hides behind the first chunk), written to LDS after the
+    // patch buffers with the first chunk, read back as float4 by the epilogue
+    float raw_scale = 1.0f, raw_bias = 0.0f;
+    if (tid < Cfg::BM) {
+        const int m = min(m0 + tid, g.M - 1);
+        if (epi.scale) raw_scale = epi.scale[m];
+        if (epi.bias) raw_bias = epi.bias[m];
+    }
 
     // ---- staging of one chunk: patch items = (8-channel group, pixel) and
     //      weight items = (tap, channel) ----
@@ -261,6 +272,11 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
 
     load_chunk(0);
     store_chunk(0);
+    float* epi_lds = reinterpret_cast<float*>(lds + 2 * buf_elems);  // [BM] multipliers, [BM] addends
+    if (tid < Cfg::BM) {
+        epi_lds[tid] = epi.alpha * raw_scale;
+        epi_lds[Cfg::BM + tid] = raw_bias;
+    }
     if (g.chunks > 1) load_chunk(1);
     __syncthreads();
 
@@ -331,14 +347,17 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     // interleaved with stores would each wait a full memory round trip.
     const bool pool = g.pool != 0;
     const int64_t plane = pool ? static_cast<int64_t>(g.PH) * g.PW : static_cast<int64_t>(g.OH) * g.OW;
+    // rows of register e: f*32 + 8*(e/4) + 4*(lane/32) + e%4, four consecutive per float4
     float mult[Cfg::FR][16], badd[Cfg::FR][16];
 #pragma unroll
     for (int f = 0; f < Cfg::FR; ++f)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int m = min(m0 + wm * Cfg::WM + frag_out_row(f, e, lane), g.M - 1);
-            mult[f][e] = epi.scale ? epi.alpha * epi.scale[m] : epi.alpha;
-            badd[f][e] = epi.bias ? epi.bias[m] : 0.0f;
+        for (int e4 = 0; e4 < 4; ++e4) {
+            const int r = wm * Cfg::WM + f * 32 + 8 * e4 + 4 * (lane >> 5);
+            const float4 mv = *reinterpret_cast<const float4*>(epi_lds + r);
+            const float4 bv = *reinterpret_cast<const float4*>(epi_lds + Cfg::BM + r);
+            mult[f][4 * e4] = mv.x, mult[f][4 * e4 + 1] = mv.y, mult[f][4 * e4 + 2] = mv.z, mult[f][4 * e4 + 3] = mv.w;
+            badd[f][4 * e4] = bv.x, badd[f][4 * e4 + 1] = bv.y, badd[f][4 * e4 + 2] = bv.z, badd[f][4 * e4 + 3] = bv.w;
         }
     int64_t out_base[Cfg::FC];
     bool valid[Cfg::FC];
@@ -361,7 +380,9 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                 acc[f][j][e] = v;
             }
     if (epi.residual) {
-        // residual only without pooling (host-checked): same index as the output
+        // residual only without pooling (host-checked): same index as the output.
+        // Out-of-range rows and pixels read an in-range element (channel M-1,
+        // pixel 0 of the image) unconditionally; their results are never stored.
         float res[Cfg::FC][Cfg::FR][16];
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j)
@@ -369,9 +390,8 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
             for (int f = 0; f < Cfg::FR; ++f)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
-                    const int m = m0 + wm * Cfg::WM + frag_out_row(f, e, lane);
-                    res[j][f][e] = (m < g.M && valid[j]) ? epi.residual[out_base[j] + static_cast<int64_t>(m) * plane]
-                                                         : 0.0f;
+                    const int m = min(m0 + wm * Cfg::WM + frag_out_row(f, e, lane), g.M - 1);
+                    res[j][f][e] = epi.residual[out_base[j] + static_cast<int64_t>(m) * plane];
                 }
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j)
@@ -484,7 +504,7 @@ struct TileChoice {
 size_t lds_bytes(const PatchGeom& g, int BM, bool ternary) {
     const size_t patch = static_cast<size_t>(3) * g.PHi * g.PWi * kPix * 2;
     const size_t words = static_cast<size_t>(BM) * g.taps * (ternary ? 8 : 4);
-    return 2 * (patch + words);
+    return 2 * (patch + words) + 2 * sizeof(float) * BM;  // two buffers + epilogue factors
 }
 
 void fill_patch(PatchGeom& g, const TileChoice& c) {
