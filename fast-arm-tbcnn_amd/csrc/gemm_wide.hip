@@ -1,0 +1,370 @@
+// Wide-tile float x binary GEMM: C = epilogue(A * W), A fp32 [M, K] row-major,
+// W the reference's BinaryMatrix (column n = K_pad bits, bit 1 = -1).
+//
+// A block owns BR = 128 rows of A x BC = 512 columns of W; its 8 waves each
+// own all 128 rows x 64 columns (4 x 2 MFMA fragments of 32 x 32), so every
+// packed weight column belongs to exactly one wave and is decoded once per
+// block, in registers, straight from global memory.  The A tile of a K step
+// (128 x 32 fp32) is split by the block into three bf16 planes in LDS (hi +
+// mid + lo = a exactly) and shared by all 8 waves; LDS holds two steps so one
+// barrier per step suffices.  Per step and wave: 48 v_mfma_f32_32x32x16_bf16
+// against ~100 VALU (split 8 elements, decode 4 weight bytes).
+//
+// Memory: A and W are read with buffer loads whose resource covers the
+// block's rows / columns to the end of the matrix: rows >= M and columns >=
+// N_pad read as zero, and the voffsets are fixed per lane (the K position is
+// the scalar offset), so the steady-state loop issues no address arithmetic.
+// A K step past K (K % 32 != 0) is zeroed before the split.  Global loads run
+// two steps ahead of their split; W words are fetched 16 bytes (128 k) at a
+// time, one quad of steps ahead.
+//
+// Blocks are dealt round-robin over the 8 XCDs; the tile order puts the
+// BC-column tiles of one 128-row band of A on the same XCD, so the band is
+// fetched from HBM once into that XCD's L2 and read there by its tiles.
+#include <type_traits>
+
+#include "gemm_wide.hpp"
+#include "mfma_core.hpp"
+
+namespace {
+
+using namespace tbnk;
+
+constexpr int kStep = 32;           // K per LDS buffer
+constexpr int kRowHalves = kStep + 8;  // bf16 per LDS row: 80 bytes, conflict-free fragment reads
+
+template <int BR_, int BC_, int WR_, int WC_>
+struct WideCfg {
+    static constexpr int BR = BR_, BC = BC_, WR = WR_, WC = WC_;
+    static constexpr int WAVES_R = BR / WR, WAVES_C = BC / WC;
+    static constexpr int NT = 64 * WAVES_R * WAVES_C;
+    static constexpr int FR = WR / 32, FC = WC / 32;
+    static_assert(BR * kStep == 8 * NT, "each thread stages 8 consecutive k of one row per step");
+    static_assert(WR % 32 == 0 && WC % 32 == 0 && BR % WR == 0 && BC % WC == 0, "bad tile");
+};
+
+using Wide = WideCfg<128, 512, 128, 64>;
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer resource word 3 for gfx9: 32-bit dword data format, raw addressing.
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+    const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : static_cast<uint32_t>(bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(n),
+                                             kRsrcWord3);
+}
+
+// 8 BinaryMatrix bits (bit e = weight k0 + e, 1 means -1) -> 8 bf16 +-1.0.
+// Bits 16 and up of x must be zero; bits 8..15 are ignored.  y holds bit e at
+// e and at e + 15, so one shift puts bit 2d at 15 and bit 2d+1 at 31.
+__device__ __forceinline__ u32x4_t decode_binary8_y(uint32_t x) {
+    const uint32_t y = x | (x << 15);
+    u32x4_t r;
+    r[0] = ((y << 15) & 0x80008000u) | 0x3F803F80u;
+    r[1] = ((y << 13) & 0x80008000u) | 0x3F803F80u;
+    r[2] = ((y << 11) & 0x80008000u) | 0x3F803F80u;
+    r[3] = ((y << 9) & 0x80008000u) | 0x3F803F80u;
+    return r;
+}
+
+// Exact three-way bf16 split of 8 fp32 values (hi + mid + lo = x), branch
+// free: r1 = x - hi is forced to 0 where x == hi, which covers +-inf (whose
+// plain difference is NaN); a NaN input keeps a NaN in hi or r1.
+__device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& mid, uint4& lo) {
+    uint32_t hb[8], mb[8], lb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t u = __float_as_uint(x[e]);
+        const float h = __uint_as_float(u & 0xFFFF0000u);
+        const float r1 = (x[e] == h) ? 0.0f : x[e] - h;
+        const uint32_t m = __float_as_uint(r1);
+        const float r2 = r1 - __uint_as_float(m & 0xFFFF0000u);
+        hb[e] = u;
+        mb[e] = m;
+        lb[e] = __float_as_uint(r2);
+    }
+    hi = make_uint4(upper_halves(hb[0], hb[1]), upper_halves(hb[2], hb[3]), upper_halves(hb[4], hb[5]),
+                    upper_halves(hb[6], hb[7]));
+    mid = make_uint4(upper_halves(mb[0], mb[1]), upper_halves(mb[2], mb[3]), upper_halves(mb[4], mb[5]),
+                     upper_halves(mb[6], mb[7]));
+    lo = make_uint4(upper_halves(lb[0], lb[1]), upper_halves(lb[2], lb[3]), upper_halves(lb[4], lb[5]),
+                    upper_halves(lb[6], lb[7]));
+}
+
+template <bool B>
+using bool_c = std::integral_constant<bool, B>;
+
+template <class Cfg>
+__global__ void __launch_bounds__(Cfg::NT)
+gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 3 * Cfg::BR * kRowHalves];
+    constexpr int kPlane = Cfg::BR * kRowHalves;  // bf16 per plane
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wr = wave / Cfg::WAVES_C;
+    const int wc = wave % Cfg::WAVES_C;
+    const int h = lane >> 5;
+
+    // tile order: the tiles of one XCD (blockIdx % 8) are consecutive in t,
+    // and consecutive t share a row band of A
+    const int total = tiles_r * tiles_c;
+    int t = blockIdx.x;
+    if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
+    const int tr = t / tiles_c;
+    const int tc = t - tr * tiles_c;
+    const int r0 = tr * Cfg::BR;
+    const int c0 = tc * Cfg::BC;
+
+    // A staging: thread -> row ar, k-group ag (8 consecutive k)
+    const int ar = tid >> 2, ag = tid & 3;
+    const __amdgpu_buffer_rsrc_t a_rs =
+        make_rsrc(p.A + static_cast<int64_t>(r0) * p.lda, static_cast<uint64_t>(p.M - r0) * p.lda * 4);
+    const int a_voff = (ar * static_cast<int>(p.lda) + ag * 8) * 4;
+    // W: lane's columns c0 + wc*WC + j*32 + lane%32
+    const __amdgpu_buffer_rsrc_t b_rs =
+        make_rsrc(p.packed + static_cast<int64_t>(c0) * p.col_bytes,
+                  static_cast<uint64_t>(p.N_pad - c0) * static_cast<uint64_t>(p.col_bytes));
+    int b_voff[Cfg::FC];
+#pragma unroll
+    for (int j = 0; j < Cfg::FC; ++j)
+        b_voff[j] = (wc * Cfg::WC + j * 32 + (lane & 31)) * static_cast<int>(p.col_bytes);
+
+    const int steps = (p.K + kStep - 1) / kStep;
+    const int quads = (steps + 3) / 4;
+
+    float areg[2][8];
+    uint32_t bw[Cfg::FC][4], bwn[Cfg::FC][4];
+    u32x4_t bcur[2][Cfg::FC], bnext[2][Cfg::FC];  // decoded W fragments [kk][j]
+
+    // loads past the end of A / W return zeros or data of later rows / columns
+    // that no result uses, so they need no guard
+    auto load_a = [&](int s, float (&v)[8]) {
+        const int soff = s * kStep * 4;
+        const f32x4_t x0 = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff, soff, 0));
+        const f32x4_t x1 =
+            __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16, soff, 0));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[e] = x0[e];
+            v[4 + e] = x1[e];
+        }
+    };
+    auto load_b = [&](int q, uint32_t (&w)[Cfg::FC][4]) {
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j) {
+            const u32x4_t x =
+                __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], q * 16, 0));
+#pragma unroll
+            for (int d = 0; d < 4; ++d) w[j][d] = x[d];
+        }
+    };
+    auto decode_b = [&](const uint32_t (&word)[Cfg::FC], u32x4_t (&bf)[2][Cfg::FC]) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+                bf[kk][j] = decode_binary8_y(__builtin_amdgcn_ubfe(word[j], 16 * kk + 8 * h, 16));
+    };
+    // split the step's 8 values into the three planes of LDS buffer b; with
+    // MASK, values at k >= K (last step) are zeroed first
+    const int a_store = ar * kRowHalves + ag * 8;
+    auto store_a = [&](int b, int s, float (&v)[8], auto mask) {
+        if constexpr (decltype(mask)::value) {
+            const int kbase = s * kStep + ag * 8;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                if (kbase + e >= p.K) v[e] = 0.0f;
+        }
+        uint4 hi, mid, lo;
+        split8(v, hi, mid, lo);
+        uint16_t* d = lds + b * 3 * kPlane + a_store;
+        *reinterpret_cast<uint4*>(d) = hi;
+        *reinterpret_cast<uint4*>(d + kPlane) = mid;
+        *reinterpret_cast<uint4*>(d + 2 * kPlane) = lo;
+    };
+
+    f32x16_t acc[Cfg::FR][Cfg::FC];
+#pragma unroll
+    for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    // fragment read base: row wr*WR + lane%32, k offset 8*(lane/32)
+    const int a_frag = (wr * Cfg::WR + (lane & 31)) * kRowHalves + h * 8;
+
+    // one K step s = 4q + u on LDS buffer u & 1: 48 MFMAs on the step's A
+    // fragments and the W fragments decoded by the previous step; meanwhile
+    // decode W for step s+1, split step s+1's A into the other buffer and
+    // fetch step s+3's A.  FULL steps (s + 3 < steps) need no guards.
+    auto step = [&](int q, auto uc, auto full) {
+        constexpr int u = decltype(uc)::value;
+        constexpr bool FULL = decltype(full)::value;
+        constexpr int b = u & 1;
+        const int s = 4 * q + u;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                u32x4_t af[Cfg::FR];
+#pragma unroll
+                for (int i = 0; i < Cfg::FR; ++i)
+                    af[i] = *reinterpret_cast<const u32x4_t*>(lds + (b * 3 + pl) * kPlane + i * 32 * kRowHalves +
+                                                             a_frag + kk * 16);
+#pragma unroll
+                for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+                    for (int j = 0; j < Cfg::FC; ++j) acc[i][j] = mfma32(af[i], bcur[kk][j], acc[i][j]);
+            }
+        {
+            uint32_t word[Cfg::FC];
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j) word[j] = u < 3 ? bw[j][(u + 1) & 3] : bwn[j][0];
+            decode_b(word, bnext);
+        }
+        if constexpr (FULL) {
+            store_a(b ^ 1, s + 1, areg[b ^ 1], bool_c<false>{});
+            load_a(s + 3, areg[b ^ 1]);
+        } else {
+            if (s + 1 < steps) store_a(b ^ 1, s + 1, areg[b ^ 1], bool_c<true>{});
+            if (s + 3 < steps) load_a(s + 3, areg[b ^ 1]);
+        }
+        if constexpr (u == 3) {
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int d = 0; d < 4; ++d) bw[j][d] = bwn[j][d];
+            load_b(q + 2, bwn);
+        }
+        if constexpr (FULL) {
+            // 4 fragment reads ahead, then per fragment: 2 MFMAs, the next read, VALU
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+            for (int g = 0; g < 20; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+            }
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j) bcur[kk][j] = bnext[kk][j];
+    };
+
+    // prologue: A steps 0 and 1 in registers, step 0 split into buffer 0,
+    // step 2 in flight; W quads 0 and 1; W fragments of step 0 decoded
+    load_a(0, areg[0]);
+    load_a(1, areg[1]);
+    load_b(0, bw);
+    load_b(1, bwn);
+    store_a(0, 0, areg[0], bool_c<true>{});
+    load_a(2, areg[0]);
+    {
+        uint32_t word[Cfg::FC];
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j) word[j] = bw[j][0];
+        decode_b(word, bcur);
+    }
+    __syncthreads();
+
+    int q = 0;
+    for (; 4 * q + 6 < steps; ++q) {
+        step(q, std::integral_constant<int, 0>{}, bool_c<true>{});
+        step(q, std::integral_constant<int, 1>{}, bool_c<true>{});
+        step(q, std::integral_constant<int, 2>{}, bool_c<true>{});
+        step(q, std::integral_constant<int, 3>{}, bool_c<true>{});
+    }
+    for (; q < quads; ++q) {
+        if (4 * q + 0 < steps) step(q, std::integral_constant<int, 0>{}, bool_c<false>{});
+        if (4 * q + 1 < steps) step(q, std::integral_constant<int, 1>{}, bool_c<false>{});
+        if (4 * q + 2 < steps) step(q, std::integral_constant<int, 2>{}, bool_c<false>{});
+        if (4 * q + 3 < steps) step(q, std::integral_constant<int, 3>{}, bool_c<false>{});
+    }
+
+    // ---- epilogue: C[m, n] = relu?(acc * alpha * scale[n] + bias[n] (+ beta * cin)) ----
+    float mult[Cfg::FC], badd[Cfg::FC];
+    int ncol[Cfg::FC];
+#pragma unroll
+    for (int j = 0; j < Cfg::FC; ++j) {
+        ncol[j] = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
+        const int nc = min(ncol[j], p.N - 1);
+        mult[j] = p.alpha;
+        badd[j] = 0.0f;
+        if (p.scale) mult[j] = p.alpha * p.scale[nc];
+        if (p.bias) badd[j] = p.bias[nc];
+    }
+    const bool bias_then_scale = (p.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
+    const bool relu = (p.flags & TBN_EPI_RELU) != 0;
+#pragma unroll
+    for (int i = 0; i < Cfg::FR; ++i) {
+        const int mrow = r0 + wr * Cfg::WR + i * 32 + 4 * h;
+        float v[Cfg::FC][16];
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float a = acc[i][j][e];
+                v[j][e] = bias_then_scale ? (a + badd[j]) * mult[j] : a * mult[j] + badd[j];
+            }
+        if (p.cin) {
+            float cv[Cfg::FC][16];
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int m = min(mrow + 8 * (e >> 2) + (e & 3), p.M - 1);
+                    const int nc = min(ncol[j], p.N - 1);
+                    cv[j][e] = p.cin_1d ? p.cin[nc] : p.cin[static_cast<int64_t>(m) * p.N + nc];
+                }
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) v[j][e] += p.beta * cv[j][e];
+        }
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = mrow + 8 * (e >> 2) + (e & 3);
+                float x = v[j][e];
+                if (relu) x = x > 0.0f ? x : 0.0f;
+                if (m < p.M && ncol[j] < p.N) p.C[static_cast<int64_t>(m) * p.ldc + ncol[j]] = x;
+            }
+    }
+}
+
+}  // namespace
+
+namespace tbn_hip {
+
+bool gemm_wide_binary_fits(const WideGemmArgs& a) {
+    using Cfg = Wide;
+    const int64_t tiles = ceil_div(a.M, Cfg::BR) * ceil_div(a.N, Cfg::BC);
+    return a.M >= 1024 && a.N >= 1024 && a.K >= kStep && tiles >= 128 && a.lda % 4 == 0 &&
+           reinterpret_cast<uintptr_t>(a.A) % 16 == 0 && a.col_bytes % 16 == 0 &&
+           reinterpret_cast<uintptr_t>(a.packed) % 16 == 0 && a.lda <= (1 << 22) &&
+           static_cast<int64_t>(Cfg::BC) * a.col_bytes < (1LL << 31);
+}
+
+int gemm_wide_binary(const WideGemmArgs& a, hipStream_t stream) {
+    using Cfg = Wide;
+    const int tiles_r = static_cast<int>(ceil_div(a.M, Cfg::BR));
+    const int tiles_c = static_cast<int>(ceil_div(a.N, Cfg::BC));
+    hipLaunchKernelGGL((gemm_wide_binary_kernel<Cfg>), dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, stream, a,
+                       tiles_r, tiles_c);
+    return check_launch("gemm_f32_binary (wide)");
+}
+
+}  // namespace tbn_hip

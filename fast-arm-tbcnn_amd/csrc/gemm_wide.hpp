@@ -1,0 +1,32 @@
+// Wide-tile float x binary GEMM for large shapes (gemm_wide.hip), used by the
+// quantized GEMM entry points when the shape fills the chip with its tiles.
+#pragma once
+
+#include "common.hpp"
+
+namespace tbn_hip {
+
+struct WideGemmArgs {
+    const float* A;
+    int64_t lda;
+    int M, N, K;
+    const uint8_t* packed;  // BinaryMatrix columns, col_bytes each
+    int64_t col_bytes;
+    int N_pad;
+    float* C;
+    int64_t ldc;
+    const float* scale;  // per column, may be null
+    float alpha;
+    const float* bias;   // per column, may be null
+    const float* cin;    // null, [N] (cin_1d) or [M, N]
+    int cin_1d;
+    float beta;
+    int flags;
+};
+
+// True when the wide kernel takes this GEMM: enough tiles to fill the chip,
+// 16-byte aligned fp32 rows and 16-byte multiple packed columns.
+bool gemm_wide_binary_fits(const WideGemmArgs& a);
+int gemm_wide_binary(const WideGemmArgs& a, hipStream_t stream);
+
+}  // namespace tbn_hip

@@ -116,6 +116,73 @@ def test_gemm_headline_4096_properties(dev, orc):
     assert rm.rel_l2(lhs, rhs) < 1e-5
 
 
+def _f64_dev_gemm(A, binw, scale, alpha=1.0, bias=None, cin=None, beta=0.0, relu=False, bias_then_scale=False):
+    """float64 A @ W on the GPU (binw 1 -> +1, 0 -> -1, as tbn_hip_pack_binary reads it), then the epilogue."""
+    dA = torch.as_tensor(A, dtype=torch.float64, device="cuda")
+    dW = 2.0 * torch.as_tensor(binw, dtype=torch.float64, device="cuda") - 1.0
+    acc = dA @ dW
+    s = torch.as_tensor(scale, dtype=torch.float64, device="cuda") * alpha
+    b = 0.0 if bias is None else torch.as_tensor(bias, dtype=torch.float64, device="cuda")
+    out = (acc + b) * s if bias_then_scale else acc * s + b
+    if cin is not None:
+        out = out + beta * torch.as_tensor(cin, dtype=torch.float64, device="cuda")
+    if relu:
+        out = out.clamp_min(0.0)
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,K,N,lda", [(2048, 4096, 4096, 4096), (2000, 1000, 4000, 1004), (1500, 1064, 5000, 1064)])
+def test_gemm_binary_wide_tiles(dev, orc, M, K, N, lda):
+    """Shapes taken by the wide-tile kernel (128 x 512 block tiles): ragged M / N,
+    a K tail (K % 32 != 0), padded rows (lda > K); every element checked against
+    float64, sampled rows against the oracle, all epilogue variants."""
+    A, binw, scale, bias = make_binary_problem(M, K, N, seed=M + K + N, lda=lda)
+    packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+    Ak = np.ascontiguousarray(A[:, :K])
+    dA = to_dev(A)
+    xmax = np.abs(A).max() * 1.5
+    for flags, alpha in [(0, 1.0), (tbn_hip.EPI_RELU, 0.7), (tbn_hip.EPI_BIAS_THEN_SCALE, 1.3)]:
+        out = host(run_gemm("binary", dA, lda, M, N, K, packed, K_pad, N_pad, scale, alpha, bias, flags))
+        ref = _f64_dev_gemm(Ak, binw, scale, alpha, bias, relu=bool(flags & tbn_hip.EPI_RELU),
+                            bias_then_scale=bool(flags & tbn_hip.EPI_BIAS_THEN_SCALE))
+        r, _ = rm.assert_within_tolerance(out, ref, K, xmax * alpha)
+        assert r < 1e-6
+    rows = np.array([0, 1, M // 2, M - 1])
+    out = host(run_gemm("binary", dA, lda, M, N, K, packed, K_pad, N_pad, scale, 1.0, bias))
+    ref = orc.gemm_f64_binary(Ak[rows], host(packed), K_pad, N, scale, 1.0, bias, False)
+    rm.assert_within_tolerance(out[rows], ref, K, xmax)
+    # GEMM with an fp32 addend (ONNX Gemm C): [M, N] and [N]
+    rng = np.random.default_rng(7)
+    cin = rng.standard_normal((M, N)).astype(np.float32)
+    c1 = rng.standard_normal(N).astype(np.float32)
+    for c, is1d in [(cin, 1), (c1, 1), (cin, 0)]:
+        if is1d and c.ndim == 2:
+            continue
+        dc = to_dev(c)
+        C = empty((M, N), torch.float32)
+        tbn_hip.call("tbn_hip_gemm_f32_quantized", tbn_hip.WEIGHTS_BINARY, P(dA), lda, M, N, K, P(packed), K_pad,
+                     N_pad, P(to_dev(scale)), 0.5, None, P(dc), is1d, 2.0, 0, P(C), N, None)
+        ref = _f64_dev_gemm(Ak, binw, scale, 0.5, None, cin=c, beta=2.0)
+        rm.assert_within_tolerance(host(C), ref, K, xmax)
+
+
+def test_gemm_binary_wide_special_values(dev):
+    """inf / nan rows through the wide kernel: +-inf per column sign, nan rows stay nan."""
+    M, K, N = 2048, 512, 4096
+    A, binw, scale, _ = make_binary_problem(M, K, N, seed=11)
+    A[0, 5] = np.inf
+    A[1, 7] = -np.inf
+    A[2, 9] = np.nan
+    packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+    out = host(run_gemm("binary", A, K, M, N, K, packed, K_pad, N_pad, scale))
+    sign = 2.0 * binw - 1.0
+    assert np.array_equal(out[0], np.where(sign[5] > 0, np.inf, -np.inf).astype(np.float32))
+    assert np.array_equal(out[1], np.where(sign[7] > 0, -np.inf, np.inf).astype(np.float32))
+    assert np.isnan(out[2]).all()
+    ref = _f64_dev_gemm(A[3:], binw, scale)
+    rm.assert_within_tolerance(out[3:], ref, K, np.abs(A[3:]).max() * 1.5)
+
+
 @pytest.mark.parametrize("M,K,N", [(1, 2, 2), (9, 260, 17), (64, 512, 96)])
 def test_gemm_ternary_small(dev, orc, M, K, N):
     rng = np.random.default_rng(M + K + N)
