@@ -30,20 +30,25 @@ namespace {
 
 using namespace tbnk;
 
-constexpr int kStep = 32;           // K per LDS buffer
-constexpr int kRowHalves = kStep + 8;  // bf16 per LDS row: 80 bytes, conflict-free fragment reads
-
-template <int BR_, int BC_, int WR_, int WC_>
+template <int BR_, int BC_, int WR_, int WC_, int KS_>
 struct WideCfg {
     static constexpr int BR = BR_, BC = BC_, WR = WR_, WC = WC_;
+    static constexpr int KS = KS_;                 // K per step (one LDS buffer, one barrier)
+    static constexpr int KROW = KS + 8;            // bf16 per LDS row: conflict-free 16-byte fragment reads
     static constexpr int WAVES_R = BR / WR, WAVES_C = BC / WC;
     static constexpr int NT = 64 * WAVES_R * WAVES_C;
     static constexpr int FR = WR / 32, FC = WC / 32;
-    static_assert(BR * kStep == 8 * NT, "each thread stages 8 consecutive k of one row per step");
+    static constexpr int KK = KS / 16;             // MFMA k-slices per step
+    static constexpr int EPT = BR * KS / NT;       // A elements a thread stages per step
+    static constexpr int TPR = KS / EPT;           // threads per A row
+    static constexpr int WPS = KS / 32;            // 32-bit W words per column per step
+    static constexpr int SPG = 4 / WPS;            // steps per 16-byte W load
+    static_assert(EPT % 8 == 0 && KS % EPT == 0, "a thread stages whole 8-element groups of one row");
     static_assert(WR % 32 == 0 && WC % 32 == 0 && BR % WR == 0 && BC % WC == 0, "bad tile");
+    static_assert(KK % 2 == 0 && SPG % 2 == 0, "double buffers alternate with even periods");
 };
 
-using Wide = WideCfg<128, 512, 128, 64>;
+using Wide = WideCfg<128, 512, 128, 64, 64>;
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -58,21 +63,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 // 8 BinaryMatrix bits (bit e = weight k0 + e, 1 means -1) -> 8 bf16 +-1.0.
 // Bits 16 and up of x must be zero; bits 8..15 are ignored.  y holds bit e at
-// e and at e + 15, so one shift puts bit 2d at 15 and bit 2d+1 at 31.
-__device__ __forceinline__ u32x4_t decode_binary8_y(uint32_t x) {
+// e and at e + 15, so one shift puts bit 2d at 15 and bit 2d+1 at 31, and one
+// v_and_or_b32 (mask in an SGPR, +1.0 pair in `ones`, a VGPR) finishes a dword.
+__device__ __forceinline__ u32x4_t decode_binary8_y(uint32_t x, uint32_t ones) {
     const uint32_t y = x | (x << 15);
     u32x4_t r;
-    r[0] = ((y << 15) & 0x80008000u) | 0x3F803F80u;
-    r[1] = ((y << 13) & 0x80008000u) | 0x3F803F80u;
-    r[2] = ((y << 11) & 0x80008000u) | 0x3F803F80u;
-    r[3] = ((y << 9) & 0x80008000u) | 0x3F803F80u;
+    r[0] = ((y << 15) & 0x80008000u) | ones;
+    r[1] = ((y << 13) & 0x80008000u) | ones;
+    r[2] = ((y << 11) & 0x80008000u) | ones;
+    r[3] = ((y << 9) & 0x80008000u) | ones;
     return r;
 }
 
 // Exact three-way bf16 split of 8 fp32 values (hi + mid + lo = x), branch
 // free: r1 = x - hi is forced to 0 where x == hi, which covers +-inf (whose
 // plain difference is NaN); a NaN input keeps a NaN in hi or r1.
-__device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& mid, uint4& lo) {
+__device__ __forceinline__ void split8(const float* x, uint4& hi, uint4& mid, uint4& lo) {
     uint32_t hb[8], mb[8], lb[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -95,12 +101,15 @@ __device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& mi
 
 template <bool B>
 using bool_c = std::integral_constant<bool, B>;
+template <int I>
+using int_c = std::integral_constant<int, I>;
 
 template <class Cfg>
 __global__ void __launch_bounds__(Cfg::NT)
 gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 3 * Cfg::BR * kRowHalves];
-    constexpr int kPlane = Cfg::BR * kRowHalves;  // bf16 per plane
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 3 * Cfg::BR * Cfg::KROW];
+    constexpr int kPlane = Cfg::BR * Cfg::KROW;  // bf16 per plane
+    constexpr int KS = Cfg::KS;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -108,6 +117,9 @@ gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
     const int wr = wave / Cfg::WAVES_C;
     const int wc = wave % Cfg::WAVES_C;
     const int h = lane >> 5;
+    // +1.0 bf16 pair kept in a VGPR so each decoded dword is one v_and_or_b32
+    uint32_t ones;
+    asm volatile("v_mov_b32 %0, 0x3f803f80" : "=v"(ones));
 
     // tile order: the tiles of one XCD (blockIdx % 8) are consecutive in t,
     // and consecutive t share a row band of A
@@ -119,11 +131,11 @@ gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
     const int r0 = tr * Cfg::BR;
     const int c0 = tc * Cfg::BC;
 
-    // A staging: thread -> row ar, k-group ag (8 consecutive k)
-    const int ar = tid >> 2, ag = tid & 3;
+    // A staging: thread -> row ar, EPT consecutive k from ag * EPT
+    const int ar = tid / Cfg::TPR, ag = tid % Cfg::TPR;
     const __amdgpu_buffer_rsrc_t a_rs =
         make_rsrc(p.A + static_cast<int64_t>(r0) * p.lda, static_cast<uint64_t>(p.M - r0) * p.lda * 4);
-    const int a_voff = (ar * static_cast<int>(p.lda) + ag * 8) * 4;
+    const int a_voff = (ar * static_cast<int>(p.lda) + ag * Cfg::EPT) * 4;
     // W: lane's columns c0 + wc*WC + j*32 + lane%32
     const __amdgpu_buffer_rsrc_t b_rs =
         make_rsrc(p.packed + static_cast<int64_t>(c0) * p.col_bytes,
@@ -133,58 +145,59 @@ gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
     for (int j = 0; j < Cfg::FC; ++j)
         b_voff[j] = (wc * Cfg::WC + j * 32 + (lane & 31)) * static_cast<int>(p.col_bytes);
 
-    const int steps = (p.K + kStep - 1) / kStep;
-    const int quads = (steps + 3) / 4;
+    const int steps = (p.K + KS - 1) / KS;
+    const int groups = (steps + Cfg::SPG - 1) / Cfg::SPG;
 
-    float areg[2][8];
-    uint32_t bw[Cfg::FC][4], bwn[Cfg::FC][4];
-    u32x4_t bcur[2][Cfg::FC], bnext[2][Cfg::FC];  // decoded W fragments [kk][j]
+    float areg[Cfg::EPT];                          // A of the next step, in flight
+    uint32_t bw[Cfg::FC][4], bwn[Cfg::FC][4];      // W words of the current / next group
+    u32x4_t bfr[2][Cfg::FC];                       // decoded W fragments, alternating k-slices
 
     // loads past the end of A / W return zeros or data of later rows / columns
     // that no result uses, so they need no guard
-    auto load_a = [&](int s, float (&v)[8]) {
-        const int soff = s * kStep * 4;
-        const f32x4_t x0 = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff, soff, 0));
-        const f32x4_t x1 =
-            __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16, soff, 0));
+    auto load_a = [&](int s) {
+        const int soff = s * KS * 4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[e] = x0[e];
-            v[4 + e] = x1[e];
+        for (int v = 0; v < Cfg::EPT / 4; ++v) {
+            const f32x4_t x =
+                __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16 * v, soff, 0));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) areg[4 * v + e] = x[e];
         }
     };
-    auto load_b = [&](int q, uint32_t (&w)[Cfg::FC][4]) {
+    auto load_b = [&](int g, uint32_t (&w)[Cfg::FC][4]) {
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             const u32x4_t x =
-                __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], q * 16, 0));
+                __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], g * 16, 0));
 #pragma unroll
             for (int d = 0; d < 4; ++d) w[j][d] = x[d];
         }
     };
-    auto decode_b = [&](const uint32_t (&word)[Cfg::FC], u32x4_t (&bf)[2][Cfg::FC]) {
+    // k-slice kk of a step whose words start at w[.][wofs]
+    auto decode_b = [&](const uint32_t (&w)[Cfg::FC][4], int wofs, int kk, u32x4_t (&bf)[Cfg::FC]) {
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-            for (int j = 0; j < Cfg::FC; ++j)
-                bf[kk][j] = decode_binary8_y(__builtin_amdgcn_ubfe(word[j], 16 * kk + 8 * h, 16));
+        for (int j = 0; j < Cfg::FC; ++j)
+            bf[j] = decode_binary8_y(__builtin_amdgcn_ubfe(w[j][wofs + kk / 2], 16 * (kk & 1) + 8 * h, 16), ones);
     };
-    // split the step's 8 values into the three planes of LDS buffer b; with
+    // split the staged step into the three planes of LDS buffer b; with
     // MASK, values at k >= K (last step) are zeroed first
-    const int a_store = ar * kRowHalves + ag * 8;
-    auto store_a = [&](int b, int s, float (&v)[8], auto mask) {
+    const int a_store = ar * Cfg::KROW + ag * Cfg::EPT;
+    auto store_a = [&](int b, int s, auto mask) {
         if constexpr (decltype(mask)::value) {
-            const int kbase = s * kStep + ag * 8;
+            const int kbase = s * KS + ag * Cfg::EPT;
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
-                if (kbase + e >= p.K) v[e] = 0.0f;
+            for (int e = 0; e < Cfg::EPT; ++e)
+                if (kbase + e >= p.K) areg[e] = 0.0f;
         }
-        uint4 hi, mid, lo;
-        split8(v, hi, mid, lo);
-        uint16_t* d = lds + b * 3 * kPlane + a_store;
-        *reinterpret_cast<uint4*>(d) = hi;
-        *reinterpret_cast<uint4*>(d + kPlane) = mid;
-        *reinterpret_cast<uint4*>(d + 2 * kPlane) = lo;
+#pragma unroll
+        for (int v = 0; v < Cfg::EPT / 8; ++v) {
+            uint4 hi, mid, lo;
+            split8(areg + 8 * v, hi, mid, lo);
+            uint16_t* d = lds + b * 3 * kPlane + a_store + 8 * v;
+            *reinterpret_cast<uint4*>(d) = hi;
+            *reinterpret_cast<uint4*>(d + kPlane) = mid;
+            *reinterpret_cast<uint4*>(d + 2 * kPlane) = lo;
+        }
     };
 
     f32x16_t acc[Cfg::FR][Cfg::FC];
@@ -196,101 +209,96 @@ gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
     // fragment read base: row wr*WR + lane%32, k offset 8*(lane/32)
-    const int a_frag = (wr * Cfg::WR + (lane & 31)) * kRowHalves + h * 8;
+    const int a_frag = (wr * Cfg::WR + (lane & 31)) * Cfg::KROW + h * 8;
 
-    // one K step s = 4q + u on LDS buffer u & 1: 48 MFMAs on the step's A
-    // fragments and the W fragments decoded by the previous step; meanwhile
-    // decode W for step s+1, split step s+1's A into the other buffer and
-    // fetch step s+3's A.  FULL steps (s + 3 < steps) need no guards.
-    auto step = [&](int q, auto uc, auto full) {
+    // One K step s = SPG*g + u on LDS buffer u & 1: per k-slice kk, 3 planes x
+    // FR x FC MFMAs with the W fragments decoded one slice ahead; meanwhile
+    // split step s+1's A (in registers) into the other buffer and fetch step
+    // s+2's A.  FULL steps (s + 2 < steps) need no guards.
+    auto step = [&](int g, auto uc, auto full) {
         constexpr int u = decltype(uc)::value;
         constexpr bool FULL = decltype(full)::value;
         constexpr int b = u & 1;
-        const int s = 4 * q + u;
+        const int s = Cfg::SPG * g + u;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
+        for (int kk = 0; kk < Cfg::KK; ++kk) {
+            // next slice's W fragments (the next step's first slice after the last)
+            if (kk + 1 < Cfg::KK) decode_b(bw, u * Cfg::WPS, kk + 1, bfr[(kk + 1) & 1]);
+            else if (u + 1 < Cfg::SPG) decode_b(bw, (u + 1) * Cfg::WPS, 0, bfr[0]);
+            else decode_b(bwn, 0, 0, bfr[0]);
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl) {
                 u32x4_t af[Cfg::FR];
 #pragma unroll
                 for (int i = 0; i < Cfg::FR; ++i)
-                    af[i] = *reinterpret_cast<const u32x4_t*>(lds + (b * 3 + pl) * kPlane + i * 32 * kRowHalves +
+                    af[i] = *reinterpret_cast<const u32x4_t*>(lds + (b * 3 + pl) * kPlane + i * 32 * Cfg::KROW +
                                                              a_frag + kk * 16);
 #pragma unroll
                 for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
-                    for (int j = 0; j < Cfg::FC; ++j) acc[i][j] = mfma32(af[i], bcur[kk][j], acc[i][j]);
+                    for (int j = 0; j < Cfg::FC; ++j) acc[i][j] = mfma32(af[i], bfr[kk & 1][j], acc[i][j]);
             }
-        {
-            uint32_t word[Cfg::FC];
-#pragma unroll
-            for (int j = 0; j < Cfg::FC; ++j) word[j] = u < 3 ? bw[j][(u + 1) & 3] : bwn[j][0];
-            decode_b(word, bnext);
         }
         if constexpr (FULL) {
-            store_a(b ^ 1, s + 1, areg[b ^ 1], bool_c<false>{});
-            load_a(s + 3, areg[b ^ 1]);
+            store_a(b ^ 1, s + 1, bool_c<false>{});
+            load_a(s + 2);
         } else {
-            if (s + 1 < steps) store_a(b ^ 1, s + 1, areg[b ^ 1], bool_c<true>{});
-            if (s + 3 < steps) load_a(s + 3, areg[b ^ 1]);
+            if (s + 1 < steps) store_a(b ^ 1, s + 1, bool_c<true>{});
+            if (s + 2 < steps) load_a(s + 2);
         }
-        if constexpr (u == 3) {
+        if constexpr (u + 1 == Cfg::SPG) {
 #pragma unroll
             for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
                 for (int d = 0; d < 4; ++d) bw[j][d] = bwn[j][d];
-            load_b(q + 2, bwn);
+            load_b(g + 2, bwn);
         }
         if constexpr (FULL) {
             // 4 fragment reads ahead, then per fragment: 2 MFMAs, the next read, VALU
+            constexpr int kReads = Cfg::KK * 3 * Cfg::FR;
+            constexpr int kPairs = Cfg::KK * 3 * Cfg::FR * Cfg::FC / 2;
             __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-            for (int g = 0; g < 20; ++g) {
+            for (int q = 0; q < kReads - 4; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
             }
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
+            for (int q = kReads - 4; q < kPairs; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
                 __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
             }
         }
         __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-            for (int j = 0; j < Cfg::FC; ++j) bcur[kk][j] = bnext[kk][j];
     };
 
-    // prologue: A steps 0 and 1 in registers, step 0 split into buffer 0,
-    // step 2 in flight; W quads 0 and 1; W fragments of step 0 decoded
-    load_a(0, areg[0]);
-    load_a(1, areg[1]);
+    // prologue: step 0 split into buffer 0, step 1 in flight, W groups 0 and 1,
+    // W fragments of step 0's first slice decoded
+    load_a(0);
     load_b(0, bw);
     load_b(1, bwn);
-    store_a(0, 0, areg[0], bool_c<true>{});
-    load_a(2, areg[0]);
-    {
-        uint32_t word[Cfg::FC];
-#pragma unroll
-        for (int j = 0; j < Cfg::FC; ++j) word[j] = bw[j][0];
-        decode_b(word, bcur);
-    }
+    store_a(0, 0, bool_c<true>{});
+    load_a(1);
+    decode_b(bw, 0, 0, bfr[0]);
     __syncthreads();
 
-    int q = 0;
-    for (; 4 * q + 6 < steps; ++q) {
-        step(q, std::integral_constant<int, 0>{}, bool_c<true>{});
-        step(q, std::integral_constant<int, 1>{}, bool_c<true>{});
-        step(q, std::integral_constant<int, 2>{}, bool_c<true>{});
-        step(q, std::integral_constant<int, 3>{}, bool_c<true>{});
+    int g = 0;
+    for (; Cfg::SPG * g + Cfg::SPG + 1 < steps; ++g) {
+        step(g, int_c<0>{}, bool_c<true>{});
+        step(g, int_c<1>{}, bool_c<true>{});
+        if constexpr (Cfg::SPG == 4) {
+            step(g, int_c<2 % Cfg::SPG>{}, bool_c<true>{});
+            step(g, int_c<3 % Cfg::SPG>{}, bool_c<true>{});
+        }
     }
-    for (; q < quads; ++q) {
-        if (4 * q + 0 < steps) step(q, std::integral_constant<int, 0>{}, bool_c<false>{});
-        if (4 * q + 1 < steps) step(q, std::integral_constant<int, 1>{}, bool_c<false>{});
-        if (4 * q + 2 < steps) step(q, std::integral_constant<int, 2>{}, bool_c<false>{});
-        if (4 * q + 3 < steps) step(q, std::integral_constant<int, 3>{}, bool_c<false>{});
+    for (; g < groups; ++g) {
+        if (Cfg::SPG * g + 0 < steps) step(g, int_c<0>{}, bool_c<false>{});
+        if (Cfg::SPG * g + 1 < steps) step(g, int_c<1>{}, bool_c<false>{});
+        if constexpr (Cfg::SPG == 4) {
+            if (Cfg::SPG * g + 2 < steps) step(g, int_c<2 % Cfg::SPG>{}, bool_c<false>{});
+            if (Cfg::SPG * g + 3 < steps) step(g, int_c<3 % Cfg::SPG>{}, bool_c<false>{});
+        }
     }
 
     // ---- epilogue: C[m, n] = relu?(acc * alpha * scale[n] + bias[n] (+ beta * cin)) ----
@@ -352,7 +360,7 @@ namespace tbn_hip {
 bool gemm_wide_binary_fits(const WideGemmArgs& a) {
     using Cfg = Wide;
     const int64_t tiles = ceil_div(a.M, Cfg::BR) * ceil_div(a.N, Cfg::BC);
-    return a.M >= 1024 && a.N >= 1024 && a.K >= kStep && tiles >= 128 && a.lda % 4 == 0 &&
+    return a.M >= 1024 && a.N >= 1024 && a.K >= Cfg::KS && tiles >= 128 && a.lda % 4 == 0 &&
            reinterpret_cast<uintptr_t>(a.A) % 16 == 0 && a.col_bytes % 16 == 0 &&
            reinterpret_cast<uintptr_t>(a.packed) % 16 == 0 && a.lda <= (1 << 22) &&
            static_cast<int64_t>(Cfg::BC) * a.col_bytes < (1LL << 31);
