@@ -11,7 +11,7 @@ Session -- the roofline of the GEMM kernel, and the reference's portable CPU
 path (restated in oracle/) timed on this host.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-                       [--only gemm|conv|ternary|gemm1024|lenet|resnet]
+                       [--only gemm|conv|ternary|tbn|gemm1024|lenet|resnet]
 """
 import argparse
 import json
@@ -195,7 +195,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
-    ap.add_argument("--only", choices=["gemm", "conv", "ternary", "gemm1024", "lenet", "resnet"],
+    ap.add_argument("--only", choices=["gemm", "conv", "ternary", "tbn", "gemm1024", "lenet", "resnet"],
                     help="run one workload only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 device copies of 1 GiB (known bytes) for counter calibration")
@@ -247,6 +247,27 @@ def main():
         extra["ternary_cfg3_gflops_equiv"] = round(2.0 * 256 * 4096 * 4096 / (t_ms * 1e-3) / 1e9, 1)
         log(f"ternary cfg3 256x4096x4096: {t_ms * 1e3:.1f} us")
         del keep
+    if want("tbn"):
+        # TBN mode (the reference's production arithmetic): activations
+        # ternarized at +-0.1, integer ternary x binary GEMM, float(C) * scale
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev)
+        g.manual_seed(6)
+        A = torch.randn((M, K), generator=g, device=dev)
+        binw = (torch.rand((K, N), generator=g, device=dev) < 0.5).to(torch.uint8)
+        Kp, Np = tbn_hip.padded_dims(K, N)
+        packed = torch.empty(Np * Kp // 8, dtype=torch.uint8, device=dev)
+        tbn_hip.call("tbn_hip_pack_binary", binw.data_ptr(), K, N, tbn_hip.LAYOUT_KN, Kp, Np, packed.data_ptr(), None)
+        out = torch.empty((M, N), device=dev)
+
+        def tbn_step(sh):
+            tbn_hip.call("tbn_hip_qlinear_matmul_binary_tbn", A.data_ptr(), K, M, K, packed.data_ptr(), Kp, N, Np,
+                         1.0, -0.1, 0.1, out.data_ptr(), N, sh)
+        tb_ms = timed(tbn_step)
+        extra["tbn_mode_4096_us"] = round(tb_ms * 1e3, 2)
+        extra["tbn_mode_4096_gops"] = round(2.0 * M * N * K / (tb_ms * 1e-3) / 1e9, 1)
+        log(f"TBN mode qlinear_matmul_binary 4096^3: {tb_ms * 1e3:.1f} us")
+        del A, binw, packed, out
     if want("gemm1024"):
         step, keep, _, _ = packed_gemm(torch, tbn_hip, 1024, 1024, 1024, seed=4)
         g_ms = timed(step)

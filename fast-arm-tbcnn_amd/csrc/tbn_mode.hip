@@ -1,0 +1,494 @@
+// TBN mode: the reference's production arithmetic for qlinear_matmul_binary
+// and the Session's cached convolutions.  Activations are ternarized at
+// (lo, hi) -- v < lo -> -1, v > hi -> +1, else 0 -- and multiplied by the +-1
+// BinaryMatrix weights in exact integer arithmetic.
+//
+//   * tbn_hip_ternary_pack_f32 / tbn_hip_im2col_ternary_packed produce the
+//     reference's two row-major bit planes (TernaryMatrix::pack_from_float,
+//     im2col_ternary_packed), bit for bit.
+//   * The GEMM runs on v_mfma_i32_32x32x32_i8.  The ternary activations are
+//     expanded once per call into int8 rows T (-1 / 0 / +1, zero padded) with
+//     their row sums; the weights stay packed and each wave expands its own
+//     columns' bits to 0/1 bytes b in registers (3 VALU per 4 weights).  With
+//     w = 1 - 2b the exact result is C = rowsum(T) - 2 * (T . b), accumulated
+//     in int32 -- the value the reference forms as popcount(pos) -
+//     popcount(neg) per 64-bit word (GeMM/05-final/GeMM.cpp:160-252).
+//   * Block tile 128 rows x 512 columns, 8 waves of 128 x 64 (4 x 2 fragments),
+//     64 k per LDS buffer (two int8 MFMA slices), one barrier per step; rows
+//     of T and packed columns are read with buffer loads (out-of-range rows /
+//     columns read as zero).
+#include <type_traits>
+
+#include "common.hpp"
+#include "conv_common.hpp"
+#include "mfma_core.hpp"
+
+namespace {
+
+using namespace tbnk;
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kRsrcWord3 = 0x00020000;  // gfx9 buffer resource: raw dword addressing
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+    const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : static_cast<uint32_t>(bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(n),
+                                             kRsrcWord3);
+}
+
+// ---------------------------------------------------------------------------
+// Activation packing
+// ---------------------------------------------------------------------------
+
+// Two bit planes [rows, cols / 8] of A [M, K] (zero padded): bit c of row r is
+// set in neg when a < lo, in pos when a > hi.  One thread per 32-bit word.
+// GeMM/05-final/GeMM.cpp:71-112; tbn-runtime/src/operators/quantized_gemm_neon.cpp:118-141
+__global__ void ternary_planes_kernel(const float* __restrict__ A, int64_t lda, int64_t M, int64_t K,
+                                      int64_t rows, int64_t wpr, float lo, float hi, uint32_t* __restrict__ pos,
+                                      uint32_t* __restrict__ neg) {
+    const int64_t total = rows * wpr;
+    for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
+         t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t row = t / wpr;
+        const int64_t c0 = (t - row * wpr) * 32;
+        uint32_t p = 0, m = 0;
+        if (row < M) {
+            const float* src = A + row * lda;
+#pragma unroll 8
+            for (int e = 0; e < 32; ++e) {
+                const float v = (c0 + e < K) ? src[c0 + e] : 0.0f;
+                m |= (v < lo ? 1u : 0u) << e;
+                p |= (!(v < lo) && v > hi ? 1u : 0u) << e;
+            }
+        }
+        pos[t] = p;
+        neg[t] = m;
+    }
+}
+
+// The im2col matrix [N*OH*OW, C*kh*kw] (k = (c*kh + r)*kw + s) ternarized into
+// two bit planes [m_pad, k_pad / 8]; taps outside the image and padding are 0.
+// tbn-runtime/src/operators/conv2d.cpp:511-601
+struct Im2colDims {
+    int C, H, W, kh, kw, sh, sw, ph, pw, dh, dw, OH, OW;
+    int64_t positions;  // N * OH * OW
+    int K;              // C * kh * kw
+};
+
+__global__ void im2col_ternary_kernel(const float* __restrict__ x, Im2colDims d, int64_t m_pad, int64_t wpr,
+                                      float lo, float hi, uint32_t* __restrict__ pos, uint32_t* __restrict__ neg) {
+    const int64_t total = m_pad * wpr;
+    const int taps = d.kh * d.kw;
+    for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
+         t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int64_t row = t / wpr;
+        const int c0 = static_cast<int>((t - row * wpr) * 32);
+        uint32_t p = 0, m = 0;
+        if (row < d.positions) {
+            const int64_t plane = static_cast<int64_t>(d.OH) * d.OW;
+            const int64_t n = row / plane;
+            const int rem = static_cast<int>(row - n * plane);
+            const int oh = rem / d.OW, ow = rem - (rem / d.OW) * d.OW;
+            const float* img = x + n * d.C * static_cast<int64_t>(d.H) * d.W;
+            for (int e = 0; e < 32; ++e) {
+                const int col = c0 + e;
+                if (col >= d.K) break;
+                const int c = col / taps;
+                const int tap = col - c * taps;
+                const int r = tap / d.kw, s = tap - (tap / d.kw) * d.kw;
+                const int ih = oh * d.sh - d.ph + r * d.dh;
+                const int iw = ow * d.sw - d.pw + s * d.dw;
+                if (static_cast<unsigned>(ih) >= static_cast<unsigned>(d.H) ||
+                    static_cast<unsigned>(iw) >= static_cast<unsigned>(d.W))
+                    continue;
+                const float v = img[(static_cast<int64_t>(c) * d.H + ih) * d.W + iw];
+                if (v < lo) m |= 1u << e;
+                else if (v > hi) p |= 1u << e;
+            }
+        }
+        pos[t] = p;
+        neg[t] = m;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Expansion to int8 rows + row sums (the GEMM's activation operand)
+// ---------------------------------------------------------------------------
+
+// Block-wide int32 sum (blockDim.x a multiple of 64, at most 1024).
+__device__ __forceinline__ int block_sum(int v, int* red) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    int s = 0;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) s += red[w];
+    return s;
+}
+
+// int8 byte of one ternary value from its plane bits.
+__device__ __forceinline__ uint32_t tern_byte(bool p, bool m) { return m ? 0xFFu : (p ? 0x01u : 0x00u); }
+
+// fp32 rows -> int8 T[row, 0..ldt) and rowsum[row]; one block per row.
+__global__ void ternarize_rows_kernel(const float* __restrict__ A, int64_t lda, int M, int K, int64_t ldt, float lo,
+                                      float hi, int8_t* __restrict__ T, int* __restrict__ rowsum) {
+    __shared__ int red[16];
+    for (int row = blockIdx.x; row < M; row += gridDim.x) {
+        const float* src = A + static_cast<int64_t>(row) * lda;
+        uint32_t* dst = reinterpret_cast<uint32_t*>(T + static_cast<int64_t>(row) * ldt);
+        int sum = 0;
+        for (int64_t w = threadIdx.x; w < ldt / 4; w += blockDim.x) {
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int64_t c = 4 * w + e;
+                const float v = c < K ? src[c] : 0.0f;
+                const bool m = v < lo, p = !m && v > hi;
+                sum += (p ? 1 : 0) - (m ? 1 : 0);
+                word |= tern_byte(p, m) << (8 * e);
+            }
+            dst[w] = word;
+        }
+        sum = block_sum(sum, red);
+        if (threadIdx.x == 0) rowsum[row] = sum;
+    }
+}
+
+// Bit planes [M, n / 8] -> int8 T[row, 0..n) and rowsum[row]; one block per row.
+__global__ void planes_to_rows_kernel(const uint8_t* __restrict__ pos, const uint8_t* __restrict__ neg, int M,
+                                      int64_t n, int8_t* __restrict__ T, int* __restrict__ rowsum) {
+    __shared__ int red[16];
+    for (int row = blockIdx.x; row < M; row += gridDim.x) {
+        const uint8_t* rp = pos + static_cast<int64_t>(row) * (n / 8);
+        const uint8_t* rm = neg + static_cast<int64_t>(row) * (n / 8);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(T + static_cast<int64_t>(row) * n);
+        int sum = 0;
+        for (int64_t w = threadIdx.x; w < n / 4; w += blockDim.x) {
+            const uint32_t pb = (rp[w >> 1] >> (4 * (w & 1))) & 0xFu;
+            const uint32_t mb = (rm[w >> 1] >> (4 * (w & 1))) & 0xFu;
+            uint32_t word = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool p = (pb >> e) & 1u, m = (mb >> e) & 1u;
+                // both bits set contributes 0 in the reference's formula
+                const bool pp = p && !m, mm = m && !p;
+                sum += (pp ? 1 : 0) - (mm ? 1 : 0);
+                word |= tern_byte(pp, mm) << (8 * e);
+            }
+            dst[w] = word;
+        }
+        sum = block_sum(sum, red);
+        if (threadIdx.x == 0) rowsum[row] = sum;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The int8 GEMM
+// ---------------------------------------------------------------------------
+
+struct TbnGemmArgs {
+    const int8_t* T;      // [M, ldt] ternary activations, zero beyond K
+    int64_t ldt;          // bytes per row (>= K, multiple of 16)
+    const int* rowsum;    // [M]
+    int M, N, K;          // K = shared dimension, a multiple of 64
+    const uint8_t* bits;  // BinaryMatrix columns (col_bytes each, bit 1 = -1)
+    int64_t col_bytes;
+    int N_pad;            // columns present in bits
+    void* out;            // int32 or float [M, ldo]
+    int64_t ldo;
+    float scale;          // float output: out = float(C) * scale
+};
+
+template <int BR_, int BC_, int WR_, int WC_>
+struct I8Cfg {
+    static constexpr int BR = BR_, BC = BC_, WR = WR_, WC = WC_;
+    static constexpr int KS = 64;         // k per step
+    static constexpr int KROW = KS + 16;  // bytes per LDS row: conflict-free 16-byte fragment reads
+    static constexpr int WAVES_R = BR / WR, WAVES_C = BC / WC;
+    static constexpr int NT = 64 * WAVES_R * WAVES_C;
+    static constexpr int FR = WR / 32, FC = WC / 32;
+    static constexpr int TPR = NT / BR;   // threads per A row (16 bytes each)
+    static_assert(TPR * 16 == KS, "a step's A tile is one 16-byte load per thread");
+};
+
+using I8Wide = I8Cfg<128, 512, 128, 64>;
+
+// 4 weight bits (bit i = weight k0 + i, 1 means -1) -> 4 bytes b_i in {0, 1}:
+// the multiply copies bit i to bit 8i without carries.
+__device__ __forceinline__ uint32_t spread4(uint32_t nib) { return __umul24(nib, 0x204081u) & 0x01010101u; }
+
+template <class Cfg, bool FLOAT_OUT>
+__global__ void __launch_bounds__(Cfg::NT)
+tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * Cfg::BR * Cfg::KROW];
+    __shared__ __attribute__((aligned(16))) int rs_lds[Cfg::BR];
+    constexpr int KS = Cfg::KS;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wr = wave / Cfg::WAVES_C;
+    const int wc = wave % Cfg::WAVES_C;
+    const int h = lane >> 5;
+
+    const int total = tiles_r * tiles_c;
+    int t = blockIdx.x;
+    if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
+    const int tr = t / tiles_c;
+    const int tc = t - tr * tiles_c;
+    const int r0 = tr * Cfg::BR;
+    const int c0 = tc * Cfg::BC;
+
+    if (tid < Cfg::BR) rs_lds[tid] = (r0 + tid < p.M) ? p.rowsum[r0 + tid] : 0;
+
+    const int ar = tid / Cfg::TPR, ag = tid % Cfg::TPR;
+    const __amdgpu_buffer_rsrc_t a_rs =
+        make_rsrc(p.T + static_cast<int64_t>(r0) * p.ldt, static_cast<uint64_t>(p.M - r0) * p.ldt);
+    const int a_voff = ar * static_cast<int>(p.ldt) + ag * 16;
+    const __amdgpu_buffer_rsrc_t b_rs =
+        make_rsrc(p.bits + static_cast<int64_t>(c0) * p.col_bytes,
+                  static_cast<uint64_t>(p.N_pad - c0) * static_cast<uint64_t>(p.col_bytes));
+    int b_voff[Cfg::FC];
+#pragma unroll
+    for (int j = 0; j < Cfg::FC; ++j)
+        b_voff[j] = (wc * Cfg::WC + j * 32 + (lane & 31)) * static_cast<int>(p.col_bytes);
+
+    const int steps = p.K / KS;
+    const int pairs = (steps + 1) / 2;  // W words: 16 bytes = two steps
+
+    i32x4_t areg;
+    uint32_t bw[Cfg::FC][4], bwn[Cfg::FC][4];
+    auto load_a = [&](int s) { areg = __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff, s * KS, 0); };
+    auto load_b = [&](int q, uint32_t (&w)[Cfg::FC][4]) {
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j) {
+            const u32x4_t x =
+                __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], q * 16, 0));
+#pragma unroll
+            for (int d = 0; d < 4; ++d) w[j][d] = x[d];
+        }
+    };
+    const int a_store = ar * Cfg::KROW + ag * 16;
+    auto store_a = [&](int b) { *reinterpret_cast<i32x4_t*>(lds + b * Cfg::BR * Cfg::KROW + a_store) = areg; };
+
+    i32x16_t acc[Cfg::FR][Cfg::FC];
+#pragma unroll
+    for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+
+    const int a_frag = (wr * Cfg::WR + (lane & 31)) * Cfg::KROW + h * 16;
+
+    // one step s = 2q + u: two MFMA slices of 32 k on LDS buffer u; meanwhile
+    // step s+1's A goes to the other buffer and step s+2's A is fetched
+    auto step = [&](int q, auto uc) {
+        constexpr int u = decltype(uc)::value;
+        const int s = 2 * q + u;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            i32x4_t bf[Cfg::FC];
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j) {
+                const uint32_t word = bw[j][2 * u + kk];
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+                    bf[j][d] = static_cast<int>(spread4(__builtin_amdgcn_ubfe(word, 16 * h + 4 * d, 4)));
+            }
+#pragma unroll
+            for (int i = 0; i < Cfg::FR; ++i) {
+                const i32x4_t af = *reinterpret_cast<const i32x4_t*>(lds + u * Cfg::BR * Cfg::KROW + i * 32 * Cfg::KROW +
+                                                                    a_frag + kk * 32);
+#pragma unroll
+                for (int j = 0; j < Cfg::FC; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[j], acc[i][j], 0, 0, 0);
+            }
+        }
+        if (s + 1 < steps) store_a(u ^ 1);
+        if (s + 2 < steps) load_a(s + 2);
+        if constexpr (u == 1) {
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int d = 0; d < 4; ++d) bw[j][d] = bwn[j][d];
+            if (q + 2 < pairs) load_b(q + 2, bwn);
+        }
+        __syncthreads();
+    };
+
+    load_a(0);
+    load_b(0, bw);
+    if (pairs > 1) load_b(1, bwn);
+    store_a(0);
+    if (steps > 1) load_a(1);
+    __syncthreads();
+    for (int q = 0; q < pairs; ++q) {
+        step(q, std::integral_constant<int, 0>{});
+        if (2 * q + 1 < steps) step(q, std::integral_constant<int, 1>{});
+    }
+
+    // epilogue: C = rowsum - 2 * acc; rows of register e: i*32 + 8*(e/4) + 4*h + e%4
+#pragma unroll
+    for (int i = 0; i < Cfg::FR; ++i) {
+        int rsum[16];
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+            const i32x4_t r = *reinterpret_cast<const i32x4_t*>(rs_lds + wr * Cfg::WR + i * 32 + 8 * e4 + 4 * h);
+            rsum[4 * e4] = r[0], rsum[4 * e4 + 1] = r[1], rsum[4 * e4 + 2] = r[2], rsum[4 * e4 + 3] = r[3];
+        }
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j) {
+            const int n = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = r0 + wr * Cfg::WR + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+                const int c = rsum[e] - 2 * acc[i][j][e];
+                if (m < p.M && n < p.N) {
+                    if (FLOAT_OUT)
+                        static_cast<float*>(p.out)[static_cast<int64_t>(m) * p.ldo + n] = static_cast<float>(c) * p.scale;
+                    else
+                        static_cast<int*>(p.out)[static_cast<int64_t>(m) * p.ldo + n] = c;
+                }
+            }
+        }
+    }
+}
+
+int launch_i8_gemm(const TbnGemmArgs& a, bool float_out, hipStream_t stream) {
+    using Cfg = I8Wide;
+    const int tiles_r = static_cast<int>(tbn_hip::ceil_div(a.M, Cfg::BR));
+    const int tiles_c = static_cast<int>(tbn_hip::ceil_div(a.N, Cfg::BC));
+    if (float_out)
+        hipLaunchKernelGGL((tbn_i8_gemm_kernel<Cfg, true>), dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, stream, a,
+                           tiles_r, tiles_c);
+    else
+        hipLaunchKernelGGL((tbn_i8_gemm_kernel<Cfg, false>), dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, stream, a,
+                           tiles_r, tiles_c);
+    return tbn_hip::check_launch("tbn_gemm");
+}
+
+int grid_for(int64_t items, int threads) {
+    return static_cast<int>(std::min<int64_t>(tbn_hip::ceil_div(std::max<int64_t>(items, 1), threads), 65536));
+}
+
+// Stream-ordered scratch for the int8 rows and row sums.
+struct Scratch {
+    void* ptr = nullptr;
+    hipStream_t stream = nullptr;
+    ~Scratch() {
+        if (ptr) (void)hipFreeAsync(ptr, stream);
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+int tbn_hip_ternary_pack_f32(const float* A, int64_t lda, int64_t M, int64_t K, int64_t rows, int64_t cols, float lo,
+                             float hi, uint8_t* pos, uint8_t* neg, tbn_stream_t stream) {
+    TBN_REQUIRE(M >= 0 && K >= 0 && rows >= M && cols >= K, TBN_INVALID_ARGUMENT,
+                "padded dimensions must cover the matrix");
+    TBN_REQUIRE(rows % 8 == 0 && cols % 64 == 0, TBN_INVALID_ARGUMENT,
+                "ternary matrix rows must be a multiple of 8 and columns a multiple of 64");
+    TBN_REQUIRE(M == 0 || lda >= K, TBN_INVALID_ARGUMENT, "lda must be >= K");
+    if (rows == 0 || cols == 0) return tbn_hip::ok();
+    TBN_REQUIRE(pos && neg && (M == 0 || K == 0 || A), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    const int64_t wpr = cols / 32;
+    hipLaunchKernelGGL(ternary_planes_kernel, dim3(grid_for(rows * wpr, 256)), dim3(256), 0,
+                       tbn_hip::stream_of(stream), A, lda, M, K, rows, wpr, lo, hi,
+                       reinterpret_cast<uint32_t*>(pos), reinterpret_cast<uint32_t*>(neg));
+    return tbn_hip::check_launch("ternary_pack_f32");
+}
+
+int tbn_hip_im2col_ternary_packed(const float* x, const tbn_conv2d_desc* desc, int64_t m_pad, int64_t k_pad,
+                                  float lo, float hi, uint8_t* pos, uint8_t* neg, tbn_stream_t stream) {
+    ConvGeom g;
+    const int rc = make_geom(desc, 0, g);
+    if (rc != TBN_SUCCESS) return rc;
+    const int64_t OH = (desc->h + 2 * desc->ph - desc->dh * (desc->kh - 1) - 1) / desc->sh + 1;
+    Im2colDims d{g.C, g.H, g.W, g.kh, g.kw, g.sh, g.sw, g.ph, g.pw, g.dh, g.dw, static_cast<int>(OH), g.OW,
+                 desc->n * OH * g.OW, g.K};
+    TBN_REQUIRE(m_pad >= d.positions && k_pad >= d.K && k_pad % 32 == 0, TBN_INVALID_ARGUMENT,
+                "m_pad / k_pad must cover the im2col matrix and k_pad be a multiple of 32");
+    if (m_pad == 0) return tbn_hip::ok();
+    TBN_REQUIRE(pos && neg && (d.positions == 0 || x), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    const int64_t wpr = k_pad / 32;
+    hipLaunchKernelGGL(im2col_ternary_kernel, dim3(grid_for(m_pad * wpr, 256)), dim3(256), 0,
+                       tbn_hip::stream_of(stream), x, d, m_pad, wpr, lo, hi, reinterpret_cast<uint32_t*>(pos),
+                       reinterpret_cast<uint32_t*>(neg));
+    return tbn_hip::check_launch("im2col_ternary_packed");
+}
+
+int tbn_hip_tbn_gemm(const uint8_t* pos, const uint8_t* neg, const uint8_t* bits, int64_t m, int64_t n, int64_t k,
+                     int32_t* C, tbn_stream_t stream) {
+    TBN_REQUIRE(m >= 0 && n >= 0 && k >= 0 && m < (1LL << 31) && k < (1LL << 31) && n < (1LL << 24),
+                TBN_INVALID_SHAPE, "m, n, k out of range");
+    TBN_REQUIRE(n % 64 == 0, TBN_INVALID_ARGUMENT, "the shared dimension n must be a multiple of 64");
+    if (m == 0 || k == 0) return tbn_hip::ok();
+    TBN_REQUIRE(C && (n == 0 || (pos && neg && bits)), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    hipStream_t s = tbn_hip::stream_of(stream);
+    if (n == 0) {
+        if (hipMemsetAsync(C, 0, static_cast<size_t>(m) * k * sizeof(int32_t), s) != hipSuccess)
+            return tbn_hip::fail(TBN_RUNTIME_ERROR, "hipMemsetAsync failed");
+        return tbn_hip::ok();
+    }
+    Scratch scr;
+    scr.stream = s;
+    const size_t tbytes = static_cast<size_t>(m) * n;
+    if (hipMallocAsync(&scr.ptr, tbytes + static_cast<size_t>(m) * 4 + 16, s) != hipSuccess)
+        return tbn_hip::fail(TBN_OUT_OF_MEMORY, "tbn_gemm: scratch allocation failed");
+    int8_t* T = static_cast<int8_t*>(scr.ptr);
+    int* rowsum = reinterpret_cast<int*>(static_cast<uint8_t*>(scr.ptr) + ((tbytes + 15) / 16) * 16);
+    hipLaunchKernelGGL(planes_to_rows_kernel, dim3(static_cast<int>(std::min<int64_t>(m, 65536))), dim3(256), 0, s,
+                       pos, neg, static_cast<int>(m), n, T, rowsum);
+    int rc = tbn_hip::check_launch("tbn_gemm (planes)");
+    if (rc != TBN_SUCCESS) return rc;
+    TbnGemmArgs a{T, n, rowsum, static_cast<int>(m), static_cast<int>(k), static_cast<int>(n), bits, n / 8,
+                  static_cast<int>(k), C, k, 1.0f};
+    return launch_i8_gemm(a, false, s);
+}
+
+int tbn_hip_qlinear_matmul_binary_tbn(const float* A, int64_t lda, int64_t M, int64_t K, const uint8_t* packed,
+                                      int64_t K_pad, int64_t N, int64_t N_pad, float scale, float lo, float hi,
+                                      float* out, int64_t ldo, tbn_stream_t stream) {
+    TBN_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M < (1LL << 31) && N < (1LL << 31) && K_pad < (1LL << 24),
+                TBN_INVALID_SHAPE, "M, N, K out of range");
+    TBN_REQUIRE(K_pad >= K && K_pad % 64 == 0, TBN_INVALID_SHAPE, "K_pad must be >= K and a multiple of 64");
+    TBN_REQUIRE(N_pad >= N, TBN_INVALID_SHAPE, "N_pad must be >= N");
+    TBN_REQUIRE(M == 0 || lda >= K, TBN_INVALID_ARGUMENT, "lda must be >= K");
+    TBN_REQUIRE(ldo >= N, TBN_INVALID_ARGUMENT, "ldo must be >= N");
+    if (M == 0 || N == 0) return tbn_hip::ok();
+    TBN_REQUIRE(out && (K == 0 || (A && packed)), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    hipStream_t s = tbn_hip::stream_of(stream);
+    if (K_pad == 0) {
+        if (hipMemset2DAsync(out, ldo * sizeof(float), 0, N * sizeof(float), M, s) != hipSuccess)
+            return tbn_hip::fail(TBN_RUNTIME_ERROR, "hipMemset2DAsync failed");
+        return tbn_hip::ok();
+    }
+    Scratch scr;
+    scr.stream = s;
+    const size_t tbytes = static_cast<size_t>(M) * K_pad;
+    if (hipMallocAsync(&scr.ptr, tbytes + static_cast<size_t>(M) * 4 + 16, s) != hipSuccess)
+        return tbn_hip::fail(TBN_OUT_OF_MEMORY, "qlinear_matmul_binary_tbn: scratch allocation failed");
+    int8_t* T = static_cast<int8_t*>(scr.ptr);
+    int* rowsum = reinterpret_cast<int*>(static_cast<uint8_t*>(scr.ptr) + ((tbytes + 15) / 16) * 16);
+    hipLaunchKernelGGL(ternarize_rows_kernel, dim3(static_cast<int>(std::min<int64_t>(M, 65536))), dim3(256), 0, s,
+                       A, lda, static_cast<int>(M), static_cast<int>(K), K_pad, lo, hi, T, rowsum);
+    int rc = tbn_hip::check_launch("qlinear_matmul_binary_tbn (ternarize)");
+    if (rc != TBN_SUCCESS) return rc;
+    TbnGemmArgs a{T, K_pad, rowsum, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K_pad), packed,
+                  K_pad / 8, static_cast<int>(N_pad), out, ldo, scale};
+    return launch_i8_gemm(a, true, s);
+}
+
+}  // extern "C"

@@ -93,6 +93,11 @@ _SIGNATURES = {
     "tbn_hip_conv2d_f32_prepacked": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P, _P], _I32),
     "tbn_hip_elementwise": ([_I32, _P, _I64, _P, _I64, _F32, _P, _P], _I32),
     "tbn_hip_ternary_activation": ([_P, _I64, _F32, _P, _P], _I32),
+    "tbn_hip_ternary_pack_f32": ([_P, _I64, _I64, _I64, _I64, _I64, _F32, _F32, _P, _P, _P], _I32),
+    "tbn_hip_im2col_ternary_packed": ([_P, ctypes.POINTER(ConvDesc), _I64, _I64, _F32, _F32, _P, _P, _P], _I32),
+    "tbn_hip_tbn_gemm": ([_P, _P, _P, _I64, _I64, _I64, _P, _P], _I32),
+    "tbn_hip_qlinear_matmul_binary_tbn": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _F32, _F32, _F32, _P, _I64,
+                                           _P], _I32),
 }
 
 _lib = None

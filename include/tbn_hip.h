@@ -293,6 +293,45 @@ int tbn_hip_elementwise(int op, const float* a, int64_t n, const float* b, int64
 int tbn_hip_ternary_activation(const float* x, int64_t n, float threshold, float* y,
                                tbn_stream_t stream);
 
+/* ---- TBN mode: ternary activations x binary weights, integer arithmetic ----
+ * The reference's production arithmetic for qlinear_matmul_binary and the
+ * Session's cached convolutions: activations ternarized at (lo, hi) (v < lo ->
+ * -1, v > hi -> +1, else 0; the reference uses -0.1 / 0.1), multiplied by the
+ * +-1 BinaryMatrix weights with exact int32 accumulation.  Results are bit
+ * identical to the reference's. */
+
+/* TernaryMatrix::pack_from_float after pad_float_matrix (GeMM/05-final/
+ * GeMM.cpp:71-112, quantized_gemm_neon.cpp:118-141): two row-major bit planes
+ * pos / neg of rows x cols/8 bytes (bit j&7 of byte j>>3 of a row), A [M, K]
+ * zero padded to [rows, cols]; rows % 8 == 0 and cols % 64 == 0 as the
+ * reference requires (else TBN_INVALID_ARGUMENT). */
+int tbn_hip_ternary_pack_f32(const float* A, int64_t lda, int64_t M, int64_t K, int64_t rows,
+                             int64_t cols, float lo, float hi, uint8_t* pos, uint8_t* neg,
+                             tbn_stream_t stream);
+/* impl::im2col_ternary_packed (conv2d.cpp:511-601): the im2col matrix
+ * [n*OH*OW, c*kh*kw] of x, column (c*kh + r)*kw + s, ternarized into bit
+ * planes of m_pad rows x k_pad/8 bytes; taps outside the image and padding
+ * are 0.  k_pad % 32 == 0. */
+int tbn_hip_im2col_ternary_packed(const float* x, const tbn_conv2d_desc* desc, int64_t m_pad,
+                                  int64_t k_pad, float lo, float hi, uint8_t* pos, uint8_t* neg,
+                                  tbn_stream_t stream);
+/* GemmEngine::compute (GeMM/05-final/GeMM.cpp:303-363), reference naming:
+ * C[m, k] (int32, row-major) = sum over the shared dimension n of the
+ * ternary rows (pos / neg planes, m x n/8 bytes) times the BinaryMatrix
+ * columns `bits` (k columns of n/8 bytes).  n % 64 == 0 (the reference needs
+ * n % 128 == 0 and m, k multiples of its micro tiles; no tiling constraint
+ * here).  Uses a stream-ordered temporary of m*(n+4) bytes. */
+int tbn_hip_tbn_gemm(const uint8_t* pos, const uint8_t* neg, const uint8_t* bits, int64_t m,
+                     int64_t n, int64_t k, int32_t* C, tbn_stream_t stream);
+/* qlinear_matmul_binary as the reference computes it (quantized_gemm_neon.cpp:
+ * 160-243,380-430): out[M, N] = float(sum_k t(A[m,k]) * w[k,n]) * scale with
+ * t the ternarization at (lo, hi) and w the packed BinaryMatrix (K_pad % 64
+ * == 0, N_pad >= N).  Uses a stream-ordered temporary of M*(K_pad+4) bytes. */
+int tbn_hip_qlinear_matmul_binary_tbn(const float* A, int64_t lda, int64_t M, int64_t K,
+                                      const uint8_t* packed, int64_t K_pad, int64_t N,
+                                      int64_t N_pad, float scale, float lo, float hi, float* out,
+                                      int64_t ldo, tbn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
