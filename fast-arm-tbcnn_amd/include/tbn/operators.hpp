@@ -107,6 +107,17 @@ Tensor qlinear_matmul_ternary(const Tensor& a, const Tensor& b_ternary, float b_
 // B FLOAT32 with values in {-1, 0, +1}; w >= 0 -> +1.
 Tensor qlinear_matmul_binary_float(const Tensor& a, const Tensor& b_binary_float, float b_scale,
                                    const TilingParams& params = TilingParams::default_128x128());
+// TBN mode, the reference's own arithmetic for qlinear_matmul_binary
+// (quantized_gemm_neon.cpp:160-243,380-430): A ternarized at (lo, hi) (v < lo
+// -> -1, v > hi -> +1, else 0), exact integer product with the +-1 weights,
+// out = float(C) * b_scale.  Bit-identical to the reference's operator;
+// TilingParams is ignored (no shape is rejected for tiling reasons).
+Tensor qlinear_matmul_binary_tbn(const Tensor& a, const Tensor& b_binary, float b_scale,
+                                 const TilingParams& params = TilingParams::default_128x128(),
+                                 float lo = -0.1f, float hi = 0.1f);
+// TBN mode on pre-packed binary weights.
+Tensor qlinear_matmul_packed_tbn(const Tensor& a, const PackedWeights& w, float scale, float lo = -0.1f,
+                                 float hi = 0.1f);
 // GEMM on pre-packed weights (qlinear_matmul_binary_blocked_packed,
 // quantized_gemm_neon.cpp:249-309): out = act(acc * scale * s[n] + bias[n]),
 // channel_scales and bias FLOAT32 [N] or null.

@@ -247,6 +247,18 @@ PYBIND11_MODULE(_tbn, m) {
               return qlinear_matmul_binary(as_tensor(a), as_tensor(b), s);
           },
           py::arg("a"), py::arg("b_binary"), py::arg("b_scale") = 1.0f);
+    m.def("qlinear_matmul_binary_tbn",
+          [](const py::object& a, const py::object& b, float s, float lo, float hi) {
+              return qlinear_matmul_binary_tbn(as_tensor(a), as_tensor(b), s, TilingParams{}, lo, hi);
+          },
+          py::arg("a"), py::arg("b_binary"), py::arg("b_scale") = 1.0f, py::arg("threshold_low") = -0.1f,
+          py::arg("threshold_high") = 0.1f);
+    m.def("qlinear_matmul_packed_tbn",
+          [](const py::object& a, const PackedWeights& w, float s, float lo, float hi) {
+              return qlinear_matmul_packed_tbn(as_tensor(a), w, s, lo, hi);
+          },
+          py::arg("a"), py::arg("weights"), py::arg("scale") = 1.0f, py::arg("threshold_low") = -0.1f,
+          py::arg("threshold_high") = 0.1f);
     m.def("qlinear_matmul_ternary",
           [](const py::object& a, const py::object& b, float s) {
               return qlinear_matmul_ternary(as_tensor(a), as_tensor(b), s);

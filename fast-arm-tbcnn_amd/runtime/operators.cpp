@@ -229,6 +229,30 @@ Tensor qlinear_matmul_binary(const Tensor& a, const Tensor& b, float b_scale, co
     return qlinear_matmul_packed(a, pack_binary_weights(b, false), b_scale);
 }
 
+Tensor qlinear_matmul_packed_tbn(const Tensor& a, const PackedWeights& w, float scale, float lo, float hi) {
+    require_float(a, "Input A");
+    TBN_CHECK(w.kind == PackedWeights::Kind::Binary, InvalidArgumentError, "TBN mode needs binary weights");
+    TBN_CHECK(a.shape().rank() == 2, InvalidShapeError, "Both inputs must be 2D matrices");
+    const int64_t M = a.shape().dims[0], K = a.shape().dims[1];
+    TBN_CHECK(K == w.K, InvalidShapeError,
+              "Matrix dimensions incompatible: A cols (" + std::to_string(K) + ") != B rows (" +
+                  std::to_string(w.K) + ")");
+    Tensor ad = on_device(a);
+    Tensor out = Tensor::empty({M, w.N}, DataType::FLOAT32, DeviceType::HIP);
+    check_status(tbn_hip_qlinear_matmul_binary_tbn(ad.typed_data<float>(), K, M, K, w.bits.typed_data<uint8_t>(),
+                                                   w.K_pad, w.N, w.N_pad, scale, lo, hi, out.typed_data<float>(),
+                                                   w.N, stream()),
+                 "qlinear_matmul_binary (TBN mode)");
+    return deliver(out, a);
+}
+
+Tensor qlinear_matmul_binary_tbn(const Tensor& a, const Tensor& b, float b_scale, const TilingParams&, float lo,
+                                 float hi) {
+    check_matmul_operands(a, b);
+    TBN_CHECK(b.dtype() == DataType::BINARY, InvalidArgumentError, "Input B must be BINARY");
+    return qlinear_matmul_packed_tbn(a, pack_binary_weights(b, false), b_scale, lo, hi);
+}
+
 Tensor qlinear_matmul_ternary(const Tensor& a, const Tensor& b, float b_scale, const TilingParams&) {
     check_matmul_operands(a, b);
     TBN_CHECK(b.dtype() == DataType::TERNARY, InvalidArgumentError, "Input B must be TERNARY");

@@ -206,3 +206,21 @@ def test_tbn_error_codes(dev):
     assert e.value.code == tbn_hip.INVALID_SHAPE  # K_pad % 64
     # empty problems are no-ops
     tbn_hip.call("tbn_hip_tbn_gemm", None, None, None, 0, 64, 4, None, None)
+
+
+def test_runtime_qlinear_matmul_binary_tbn(dev, tbn, orc):
+    """tbn::qlinear_matmul_binary_tbn (C++ runtime, host tensors in and out)
+    is the reference operator bit for bit; the packed variant agrees."""
+    rng = np.random.default_rng(12)
+    M, K, N = 64, 300, 50
+    A = special_matrix(M, K, seed=12)
+    binw = (rng.random((K, N)) < 0.5).astype(np.uint8)
+    out = tbn.qlinear_matmul_binary_tbn(tbn.Tensor(A), tbn.Tensor(binw, "binary"), 0.5).numpy()
+    rc, ref = orc.qlinear_matmul_binary_tbn(A, binw, 0.5, TILING)
+    assert rc == 0
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    w = tbn.pack_binary_weights(tbn.Tensor(binw, "binary"))
+    out2 = tbn.qlinear_matmul_packed_tbn(tbn.Tensor(A), w, 0.5).numpy()
+    assert np.array_equal(out2.view(np.uint32), ref.view(np.uint32))
+    with pytest.raises(tbn.TBNError):
+        tbn.qlinear_matmul_binary_tbn(tbn.Tensor(A), tbn.Tensor(np.zeros((K, N), np.float32)), 1.0)
