@@ -20,6 +20,8 @@
 // sits in four neighbouring lanes.
 #include <algorithm>
 #include <cstdlib>
+#include <map>
+#include <mutex>
 #include <string>
 
 #include "conv_common.hpp"
@@ -43,7 +45,28 @@ struct PatchGeom {
     int VH, VW;            // extent of computed pixels (2*PH x 2*PW when pooling)
     int linear;            // 1: a tile is QT consecutive pixels (QT/4 pool windows) of one image
     int tiles_img;         // tiles per image
+    uint32_t mul_patch;    // ceil(2^32 / (PHi*PWi)): staging item -> channel group by multiply-high
+    uint32_t mul_pwi;      // ceil(2^32 / PWi), or 0 when PWi == 1
+    // patch sampling: patch pixel (pr, pc) is input (ih0 + pr*psh, iw0 + pc*psw);
+    // output (oh, ow) reads patch pixel ((oh-row0)*poh, (ow-col0)*pow).  1x1
+    // kernels stage only the pixels they use (psh = sh, poh = 1); others stage
+    // the dense rectangle (psh = 1, poh = sh)
+    int psh, psw, poh, pow_;
 };
+
+// Buffer resource (gfx9 word 3: raw dword addressing) over `bytes` from base;
+// loads at offsets past the end return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {
+    const uint32_t n = bytes > 0xFFFFFFF0ull ? 0xFFFFFFF0u : static_cast<uint32_t>(bytes);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(n),
+                                             0x00020000);
+}
+
+// n / d for the staging coordinates (n * d < 2^32): multiply-high by the
+// host's ceil(2^32 / d); mul == 0 stands for d == 1.
+__device__ __forceinline__ int div_by(int n, uint32_t mul) {
+    return mul ? static_cast<int>(__umulhi(static_cast<uint32_t>(n), mul)) : n;
+}
 
 // Output pixel of the tile-local index ql and its patch index.  Linear tiles
 // run along the flattened image (pool windows when pooling), so a fragment's
@@ -81,7 +104,7 @@ __device__ __forceinline__ bool tile_pixel(const PatchGeom& g, int q0, int row0,
         ow = col0 + j;
         valid = oh < g.VH && ow < g.VW;
     }
-    patch_index = valid ? ((oh - row0) * g.sh * g.PWi + (ow - col0) * g.sw) : 0;
+    patch_index = valid ? ((oh - row0) * g.poh * g.PWi + (ow - col0) * g.pow_) : 0;
     return valid;
 }
 
@@ -97,13 +120,26 @@ struct PatchCfg {
     static_assert(NT >= BM, "one thread per channel stages the epilogue factors");
 };
 
+// 8 binary weight bits (bit e = weight e, 1 means -1) -> 8 bf16 +-1.0.  Bits
+// 16 and up of x must be zero (bits 8..15 are ignored): y holds bit e at e and
+// e + 15, so one shift puts bit 2d at 15 and bit 2d+1 at 31.
+__device__ __forceinline__ u32x4_t decode_binary8_fast(uint32_t x) {
+    const uint32_t y = x | (x << 15);
+    u32x4_t r;
+    r[0] = ((y << 15) & 0x80008000u) | 0x3F803F80u;
+    r[1] = ((y << 13) & 0x80008000u) | 0x3F803F80u;
+    r[2] = ((y << 11) & 0x80008000u) | 0x3F803F80u;
+    r[3] = ((y << 9) & 0x80008000u) | 0x3F803F80u;
+    return r;
+}
+
 template <bool TERNARY>
 __device__ __forceinline__ u32x4_t weight_frag(uint2 w, int kk, int kg) {
     if (TERNARY) {
         const uint32_t word = kk ? w.y : w.x;
         return decode_ternary8((word >> (16 * kg)) & 0xFFFFu);
     }
-    return decode_binary8((w.x >> (8 * (2 * kk + kg))) & 0xFFu);
+    return decode_binary8_fast(__builtin_amdgcn_ubfe(w.x, 8 * (2 * kk + kg), 16));
 }
 
 struct PatchEpi {
@@ -115,7 +151,9 @@ struct PatchEpi {
     int flags;
 };
 
-template <class Cfg, bool TERNARY>
+// TAPS = 9: 3x3 kernels, taps unrolled and the chunk's weight words held in
+// registers; TAPS = 0: any kernel size, words read per tap.
+template <class Cfg, bool TERNARY, int TAPS>
 __global__ void __launch_bounds__(Cfg::NT)
 conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __restrict__ wbits, int64_t col_bytes,
                   int m_alloc, PatchEpi epi) {
@@ -174,6 +212,12 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     constexpr int kMaxWItems = 8;
     const int64_t img = static_cast<int64_t>(n) * g.C * g.H * g.W;
     const int64_t HW = static_cast<int64_t>(g.H) * g.W;
+    // staging loads are buffer loads: an element outside the image, past C
+    // or past the weight columns gets an offset beyond the resource and reads
+    // 0, so no branch or select waits on a load before it is stored
+    const __amdgpu_buffer_rsrc_t x_rs = make_rsrc(x + img, static_cast<uint64_t>(g.C) * HW * 4);
+    const __amdgpu_buffer_rsrc_t w_rs = make_rsrc(wbits, static_cast<uint64_t>(m_alloc) * col_bytes);
+    constexpr uint32_t kOutside = 0xFFFFFFF0u;
     float stage[kMaxItems][8];
     uint2 wstage[kMaxWItems];
 
@@ -182,43 +226,39 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
         for (int it = 0; it < kMaxItems; ++it) {
             if (it >= per_thread) break;
             const int item = tid + it * Cfg::NT;
+            const int grp = div_by(item, g.mul_patch);
+            const int pp = item - grp * patch;
+            const int pr = div_by(pp, g.mul_pwi);
+            const int ih = ih0 + pr * g.psh;
+            const int iw = iw0 + (pp - pr * g.PWi) * g.psw;
+            const int c0 = ch * kChunk + grp * 8;
+            const bool ok = item < items && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
+                            static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
+            const uint32_t base = static_cast<uint32_t>((static_cast<int64_t>(c0) * HW + ih * g.W + iw) * 4);
+            const uint32_t step = static_cast<uint32_t>(HW * 4);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) stage[it][e] = 0.0f;
-            if (item < items) {
-                const int grp = item / patch;
-                const int pp = item - grp * patch;
-                const int pr = pp / g.PWi;
-                const int ih = ih0 + pr;
-                const int iw = iw0 + (pp - pr * g.PWi);
-                const int c0 = ch * kChunk + grp * 8;
-                if (static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
-                    static_cast<unsigned>(iw) < static_cast<unsigned>(g.W) && c0 < g.C) {
-                    const float* src = x + img + static_cast<int64_t>(c0) * HW + static_cast<int64_t>(ih) * g.W + iw;
-                    // channels past C (last chunk) re-read channel c0 and are zeroed
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const bool in = c0 + e < g.C;
-                        const float v = src[in ? e * HW : 0];
-                        stage[it][e] = in ? v : 0.0f;
-                    }
-                }
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t off = (ok && c0 + e < g.C) ? base + e * step : kOutside;
+                stage[it][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x_rs, off, 0, 0));
             }
         }
 #pragma unroll
         for (int it = 0; it < kMaxWItems; ++it) {
             if (it >= wper_thread) break;
             const int item = tid + it * Cfg::NT;
-            wstage[it] = make_uint2(0, 0);
-            if (item < witems) {
-                const int ml = item % Cfg::BM;
-                const int tap = item / Cfg::BM;
-                const int m = m0 + ml;
-                if (m < m_alloc) {
-                    const uint8_t* col = wbits + static_cast<int64_t>(m) * col_bytes;
-                    const int64_t t = static_cast<int64_t>(ch) * g.taps + tap;
-                    if (TERNARY) wstage[it] = *reinterpret_cast<const uint2*>(col + 8 * t);
-                    else wstage[it].x = *reinterpret_cast<const uint32_t*>(col + 4 * t);
-                }
+            const int ml = item % Cfg::BM;
+            const int tap = item / Cfg::BM;
+            const int m = m0 + ml;
+            const bool ok = item < witems && m < m_alloc;
+            const int64_t t = static_cast<int64_t>(ch) * g.taps + tap;
+            const uint32_t off = ok ? static_cast<uint32_t>(static_cast<int64_t>(m) * col_bytes + (TERNARY ? 8 : 4) * t)
+                                    : kOutside;
+            if (TERNARY) {
+                const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(w_rs, off, 0, 0);
+                const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(w_rs, ok ? off + 4 : kOutside, 0, 0);
+                wstage[it] = make_uint2(lo, hi);
+            } else {
+                wstage[it] = make_uint2(__builtin_amdgcn_raw_buffer_load_b32(w_rs, off, 0, 0), 0u);
             }
         }
     };
@@ -229,7 +269,7 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
             if (it >= per_thread) break;
             const int item = tid + it * Cfg::NT;
             if (item < items) {
-                const int grp = item / patch;
+                const int grp = div_by(item, g.mul_patch);
                 const int pp = item - grp * patch;
                 const Split4 a = split4(stage[it][0], stage[it][1], stage[it][2], stage[it][3]);
                 const Split4 c = split4(stage[it][4], stage[it][5], stage[it][6], stage[it][7]);
@@ -281,14 +321,11 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     __syncthreads();
 
     const int kg = lane >> 5;
-    // patch offset of tap (r, s): (r*dh*PWi + s*dw) * kPix, advanced incrementally
+    // patch offset of tap (r, s): (r*dh*PWi + s*dw) * kPix
     const int tap_ds = g.dw * kPix;
-    const int tap_dr = g.dh * g.PWi * kPix - (g.kw - 1) * g.dw * kPix;
+    const int tap_dr = g.dh * g.PWi * kPix;
     for (int ch = 0; ch < g.chunks; ++ch) {
         const uint16_t* cur = lds + (ch & 1) * buf_elems;
-        // steps = (tap, kk) pairs; the B fragments of step t+1 are read from LDS
-        // while the MFMAs of step t run
-        u32x4_t bcur[3][Cfg::FC], bnext[3][Cfg::FC];
         auto read_b = [&](int toff, int kk, u32x4_t (&b)[3][Cfg::FC]) {
 #pragma unroll
             for (int p = 0; p < 3; ++p)
@@ -297,42 +334,96 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                     b[p][j] = *reinterpret_cast<const u32x4_t*>(cur + p * plane_elems + pbase[j] + toff + kk * 16 +
                                                                  kg * 8);
         };
-        read_b(0, 0, bcur);
-        int toff = 0, s = 0;
-        uint2 w[Cfg::FR];
-        for (int tap = 0; tap < g.taps; ++tap) {
+        auto mfma_step = [&](const u32x4_t (&a)[Cfg::FR], const u32x4_t (&b)[3][Cfg::FC]) {
 #pragma unroll
-            for (int f = 0; f < Cfg::FR; ++f) {
-                const uint16_t* src = cur + wofs + (tap * Cfg::BM + wrow + f * 32) * kWordHalves;
-                if (TERNARY) w[f] = *reinterpret_cast<const uint2*>(src);
-                else w[f] = make_uint2(*reinterpret_cast<const uint32_t*>(src), 0u);
+            for (int p = 0; p < 3; ++p)
+#pragma unroll
+                for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+                    for (int j = 0; j < Cfg::FC; ++j) acc[f][j] = mfma32(a[f], b[p][j], acc[f][j]);
+        };
+        if constexpr (TAPS > 0) {
+            // the chunk's words for this lane's rows, every tap, in registers
+            // (read before the first pixel fragments so no wait covers both)
+            uint2 wr[Cfg::FR][TAPS];
+#pragma unroll
+            for (int tap = 0; tap < TAPS; ++tap)
+#pragma unroll
+                for (int f = 0; f < Cfg::FR; ++f) {
+                    const uint16_t* src = cur + wofs + (tap * Cfg::BM + wrow + f * 32) * kWordHalves;
+                    if (TERNARY) wr[f][tap] = *reinterpret_cast<const uint2*>(src);
+                    else wr[f][tap] = make_uint2(*reinterpret_cast<const uint32_t*>(src), 0u);
+                }
+            // software pipeline over the 2*TAPS steps (tap, kk): step t+1's
+            // pixel fragments are read from LDS and its weight fragments decoded
+            // while step t's MFMAs run; the scheduling barriers keep each
+            // step's reads ahead of its MFMAs so no LDS wait lands in the chain
+            u32x4_t bcur[3][Cfg::FC], acur[Cfg::FR];
+            read_b(0, 0, bcur);
+#pragma unroll
+            for (int f = 0; f < Cfg::FR; ++f) acur[f] = weight_frag<TERNARY>(wr[f][0], 0, kg);
+#pragma unroll
+            for (int t = 0; t < 2 * TAPS; ++t) {
+                const int nt = (t + 1) >> 1, nk = (t + 1) & 1;
+                u32x4_t bnext[3][Cfg::FC], anext[Cfg::FR];
+                if (t + 1 < 2 * TAPS) read_b((nt / 3) * tap_dr + (nt % 3) * tap_ds, nk, bnext);
+                __builtin_amdgcn_sched_barrier(0);
+                mfma_step(acur, bcur);
+                if (t + 1 < 2 * TAPS) {
+#pragma unroll
+                    for (int f = 0; f < Cfg::FR; ++f) anext[f] = weight_frag<TERNARY>(wr[f][nt], nk, kg);
+                }
+#pragma unroll
+                for (int q = 0; q < 3 * Cfg::FR * Cfg::FC; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                if (t + 1 < 2 * TAPS) {
+#pragma unroll
+                    for (int p = 0; p < 3; ++p)
+#pragma unroll
+                        for (int j = 0; j < Cfg::FC; ++j) bcur[p][j] = bnext[p][j];
+#pragma unroll
+                    for (int f = 0; f < Cfg::FR; ++f) acur[f] = anext[f];
+                }
             }
-            // next tap's patch offset
-            int next_toff = toff + tap_ds, next_s = s + 1;
-            if (next_s == g.kw) {
-                next_s = 0;
-                next_toff = toff + tap_dr;
+        } else {
+            // steps = (tap, kk) pairs; the B fragments of step t+1 are read from
+            // LDS while the MFMAs of step t run
+            u32x4_t bcur[3][Cfg::FC], bnext[3][Cfg::FC];
+            read_b(0, 0, bcur);
+            int toff = 0, s = 0;
+            uint2 w[Cfg::FR];
+            for (int tap = 0; tap < g.taps; ++tap) {
+#pragma unroll
+                for (int f = 0; f < Cfg::FR; ++f) {
+                    const uint16_t* src = cur + wofs + (tap * Cfg::BM + wrow + f * 32) * kWordHalves;
+                    if (TERNARY) w[f] = *reinterpret_cast<const uint2*>(src);
+                    else w[f] = make_uint2(*reinterpret_cast<const uint32_t*>(src), 0u);
+                }
+                // next tap's patch offset
+                int next_toff = toff + tap_ds, next_s = s + 1;
+                if (next_s == g.kw) {
+                    next_s = 0;
+                    next_toff = toff + tap_dr - (g.kw - 1) * tap_ds;
+                }
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk) {
+                    if (kk == 0) read_b(toff, 1, bnext);
+                    else if (tap + 1 < g.taps) read_b(next_toff, 0, bnext);
+                    u32x4_t a[Cfg::FR];
+#pragma unroll
+                    for (int f = 0; f < Cfg::FR; ++f) a[f] = weight_frag<TERNARY>(w[f], kk, kg);
+                    mfma_step(a, bcur);
+#pragma unroll
+                    for (int p = 0; p < 3; ++p)
+#pragma unroll
+                        for (int j = 0; j < Cfg::FC; ++j) bcur[p][j] = bnext[p][j];
+                }
+                toff = next_toff;
+                s = next_s;
             }
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk) {
-                if (kk == 0) read_b(toff, 1, bnext);
-                else if (tap + 1 < g.taps) read_b(next_toff, 0, bnext);
-                u32x4_t a[Cfg::FR];
-#pragma unroll
-                for (int f = 0; f < Cfg::FR; ++f) a[f] = weight_frag<TERNARY>(w[f], kk, kg);
-#pragma unroll
-                for (int p = 0; p < 3; ++p)
-#pragma unroll
-                    for (int f = 0; f < Cfg::FR; ++f)
-#pragma unroll
-                        for (int j = 0; j < Cfg::FC; ++j) acc[f][j] = mfma32(a[f], bcur[p][j], acc[f][j]);
-#pragma unroll
-                for (int p = 0; p < 3; ++p)
-#pragma unroll
-                    for (int j = 0; j < Cfg::FC; ++j) bcur[p][j] = bnext[p][j];
-            }
-            toff = next_toff;
-            s = next_s;
         }
         if (ch + 1 < g.chunks) {
             store_chunk((ch + 1) & 1);
@@ -509,7 +600,7 @@ size_t lds_bytes(const PatchGeom& g, int BM, bool ternary) {
 
 void fill_patch(PatchGeom& g, const TileChoice& c) {
     g.linear = c.linear;
-    int rows;  // output rows one tile's pixels span (at most)
+    int rows, cols;  // output rows / columns one tile's pixels span (at most)
     if (c.linear) {
         const int per = g.pool ? c.TH * c.TW / 4 : c.TH * c.TW;
         const int total = g.pool ? g.PH * g.PW : g.OH * g.OW;
@@ -522,16 +613,27 @@ void fill_patch(PatchGeom& g, const TileChoice& c) {
             span = std::max(span, last - first + 1);
         }
         rows = g.pool ? 2 * span : span;
-        g.PWi = (g.OW - 1) * g.sw + (g.kw - 1) * g.dw + 1;
+        cols = g.OW;
         g.tiles_h = g.tiles_w = 0;
     } else {
         rows = c.TH;
-        g.PWi = (c.TW - 1) * g.sw + (g.kw - 1) * g.dw + 1;
+        cols = c.TW;
         g.tiles_h = (g.VH + c.TH - 1) / c.TH;
         g.tiles_w = (g.VW + c.TW - 1) / c.TW;
         g.tiles_img = g.tiles_h * g.tiles_w;
     }
-    g.PHi = (rows - 1) * g.sh + (g.kh - 1) * g.dh + 1;
+    const bool compact = g.kh == 1 && g.kw == 1;
+    g.psh = compact ? g.sh : 1;
+    g.psw = compact ? g.sw : 1;
+    g.poh = compact ? 1 : g.sh;
+    g.pow_ = compact ? 1 : g.sw;
+    g.PHi = compact ? rows : (rows - 1) * g.sh + (g.kh - 1) * g.dh + 1;
+    g.PWi = compact ? cols : (cols - 1) * g.sw + (g.kw - 1) * g.dw + 1;
+    const auto magic = [](int64_t d) -> uint32_t {
+        return d <= 1 ? 0u : static_cast<uint32_t>(((int64_t(1) << 32) + d - 1) / d);
+    };
+    g.mul_patch = magic(static_cast<int64_t>(g.PHi) * g.PWi);
+    g.mul_pwi = magic(g.PWi);
 }
 
 // Tile menu: (BM, TH, TW, wave tile); TH x TW is also the pixel count of a
@@ -543,6 +645,8 @@ using P3 = PatchCfg<64, 8, 8, 32, 32>;
 using P4 = PatchCfg<32, 8, 8, 32, 32>;    // <= 32 output channels
 using P5 = PatchCfg<128, 4, 8, 64, 32>;   // small 2-D patches (strided / large kernels)
 using P6 = PatchCfg<64, 4, 8, 32, 32>;
+using P7 = PatchCfg<64, 8, 8, 64, 32>;    // 64 channels per wave: each pixel fragment feeds 2 MFMAs
+using P8 = PatchCfg<64, 8, 16, 64, 32>;
 
 template <class Cfg>
 constexpr TileChoice choice(int cfg, int linear) {
@@ -551,26 +655,36 @@ constexpr TileChoice choice(int cfg, int linear) {
 
 // TBN_CONV_TILE=<id> forces a tile (tuning only): id = cfg for linear tiles,
 // 10 + cfg for 2-D tiles.
+// TBN_CONV_TILE=<id> forces one tile (id = menu index for linear tiles,
+// 10 + index for 2-D tiles): a tuning aid, read on every call.
 int tile_override() {
-    static const int v = [] {
-        const char* e = std::getenv("TBN_CONV_TILE");
-        return e ? std::atoi(e) : -1;
-    }();
-    return v;
+    const char* e = std::getenv("TBN_CONV_TILE");
+    return e ? std::atoi(e) : -1;
 }
 
 // In preference order (linear tiles store whole 128-byte pixel runs; larger
 // tiles do more MFMA per decoded weight word), the first tile whose patch fits
 // the LDS and the staging registers and that gives >= 240 blocks; otherwise
 // the feasible tile with the most blocks.
+constexpr TileChoice kMenu[] = {choice<P0>(0, 1), choice<P1>(1, 1), choice<P2>(2, 1), choice<P3>(3, 1),
+                                choice<P4>(4, 1), choice<P7>(7, 1), choice<P8>(8, 1), choice<P0>(0, 0),
+                                choice<P1>(1, 0), choice<P2>(2, 0), choice<P3>(3, 0), choice<P4>(4, 0),
+                                choice<P5>(5, 0), choice<P6>(6, 0), choice<P7>(7, 0), choice<P8>(8, 0)};
+
+// A tile can run this geometry: its patch fits the LDS and the staging
+// registers (8 items per thread for the patch and for the weight words).
+bool tile_fits(const PatchGeom& g, const TileChoice& c, PatchGeom& t) {
+    t = g;
+    fill_patch(t, c);
+    return lds_bytes(t, c.BM, true) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= 8 * c.NT &&
+           c.BM * t.taps <= 8 * c.NT;
+}
+
 bool choose_tile(PatchGeom& g, TileChoice& out) {
-    const TileChoice menu[] = {choice<P0>(0, 1),  choice<P1>(1, 1),  choice<P2>(2, 1),  choice<P3>(3, 1),
-                               choice<P4>(4, 1),  choice<P0>(0, 0),  choice<P1>(1, 0),  choice<P2>(2, 0),
-                               choice<P3>(3, 0),  choice<P4>(4, 0),  choice<P5>(5, 0),  choice<P6>(6, 0)};
     const TileChoice* best = nullptr;
     int64_t best_blocks = -1;
     const int forced = tile_override();
-    for (const auto& c : menu) {
+    for (const auto& c : kMenu) {
         const int id = c.linear ? c.cfg : 10 + c.cfg;
         if (forced >= 0 && id != forced) continue;
         if (forced < 0) {
@@ -578,11 +692,8 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
             if (g.M > 32 && c.BM == 32) continue;
             if (g.M <= 64 && c.BM == 128) continue;
         }
-        PatchGeom t = g;
-        fill_patch(t, c);
-        if (lds_bytes(t, c.BM, true) > static_cast<size_t>(kMaxLds)) continue;
-        if (4 * t.PHi * t.PWi > 8 * c.NT) continue;  // patch staging registers per thread
-        if (c.BM * t.taps > 8 * c.NT) continue;      // weight staging registers per thread
+        PatchGeom t;
+        if (!tile_fits(g, c, t)) continue;
         const int64_t blocks = static_cast<int64_t>(t.N) * t.tiles_img * ((g.M + c.BM - 1) / c.BM);
         if (forced >= 0 || blocks >= 240) {
             out = c;
@@ -600,25 +711,32 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
     return true;
 }
 
-template <class Cfg, bool TERNARY>
-int launch_patch(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
-                 const PatchEpi& epi, hipStream_t s) {
+template <class Cfg, bool TERNARY, int TAPS>
+int launch_patch_taps(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
+                      const PatchEpi& epi, hipStream_t s) {
     const size_t lds = lds_bytes(g, Cfg::BM, TERNARY);
     const int items = 4 * g.PHi * g.PWi;
     if ((items + Cfg::NT - 1) / Cfg::NT > 8 || (Cfg::BM * g.taps + Cfg::NT - 1) / Cfg::NT > 8)
         return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for the staging registers");
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_patch_kernel<Cfg, TERNARY>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_patch_kernel<Cfg, TERNARY, TAPS>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
         if (e != hipSuccess) return tbn_hip::fail(TBN_RUNTIME_ERROR, std::string("hipFuncSetAttribute: ") +
                                                                          hipGetErrorString(e));
         attr_set = true;
     }
     const int64_t blocks = static_cast<int64_t>(g.N) * g.tiles_img * ((g.M + Cfg::BM - 1) / Cfg::BM);
-    hipLaunchKernelGGL((conv_patch_kernel<Cfg, TERNARY>), dim3(static_cast<unsigned>(blocks)), dim3(Cfg::NT), lds, s,
-                       x, g, w, col_bytes, m_alloc, epi);
+    hipLaunchKernelGGL((conv_patch_kernel<Cfg, TERNARY, TAPS>), dim3(static_cast<unsigned>(blocks)), dim3(Cfg::NT),
+                       lds, s, x, g, w, col_bytes, m_alloc, epi);
     return tbn_hip::check_launch(TERNARY ? "conv2d_f32_ternary (patch)" : "conv2d_f32_binary (patch)");
+}
+
+template <class Cfg, bool TERNARY>
+int launch_patch(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
+                 const PatchEpi& epi, hipStream_t s) {
+    if (g.kh == 3 && g.kw == 3) return launch_patch_taps<Cfg, TERNARY, 9>(x, g, w, col_bytes, m_alloc, epi, s);
+    return launch_patch_taps<Cfg, TERNARY, 0>(x, g, w, col_bytes, m_alloc, epi, s);
 }
 
 template <bool TERNARY>
@@ -631,8 +749,114 @@ int dispatch_patch(int id, const float* x, const PatchGeom& g, const uint8_t* w,
         case 3: return launch_patch<P3, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
         case 4: return launch_patch<P4, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
         case 5: return launch_patch<P5, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
-        default: return launch_patch<P6, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 6: return launch_patch<P6, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 7: return launch_patch<P7, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        default: return launch_patch<P8, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
     }
+}
+
+// ---- tile selection by measurement ------------------------------------------
+// Which tile is fastest depends on image size, channel counts and stride in
+// ways a static rule gets wrong by up to 1.6x.  The first call for a shape
+// times every feasible tile (into a temporary output) and caches the winner
+// for the process; every tile accumulates each output in the same order
+// (chunk, tap, k-slice, hi/mid/lo), so the choice never changes results.
+// Calls under stream capture, TBN_CONV_TUNE=0 or a forced tile use the
+// static rule.
+
+struct PlanKey {
+    int64_t v[16];
+    bool operator<(const PlanKey& o) const { return std::lexicographical_compare(v, v + 16, o.v, o.v + 16); }
+};
+
+std::mutex& plan_mutex() {
+    static std::mutex m;
+    return m;
+}
+std::map<PlanKey, int>& plan_cache() {
+    static std::map<PlanKey, int> m;
+    return m;
+}
+
+bool tuning_allowed(hipStream_t s) {
+    const char* e = std::getenv("TBN_CONV_TUNE");
+    if (e && e[0] == '0') return false;
+    if (tile_override() >= 0) return false;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(s, &st) == hipSuccess && st == hipStreamCaptureStatusNone;
+}
+
+template <bool TERNARY>
+int dispatch_patch(int id, const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
+                   const PatchEpi& epi, hipStream_t s);
+
+template <bool TERNARY>
+int select_tile(const tbn_conv2d_desc* d, PatchGeom& g, const float* x, const uint8_t* w, int64_t col_bytes,
+                int m_alloc, const PatchEpi& epi, hipStream_t s, TileChoice& out) {
+    const PlanKey key{{d->n, d->c, d->h, d->w, d->m, d->kh, d->kw, d->sh, d->sw, d->ph, d->pw, d->dh, d->dw,
+                       TERNARY ? 1 : 0, epi.flags, epi.residual ? 1 : 0}};
+    if (tile_override() < 0) {
+        std::lock_guard<std::mutex> lock(plan_mutex());
+        auto it = plan_cache().find(key);
+        if (it != plan_cache().end()) {
+            out = kMenu[it->second];
+            fill_patch(g, out);
+            return TBN_SUCCESS;
+        }
+    }
+    if (!choose_tile(g, out)) return tbn_hip::fail(TBN_INVALID_SHAPE, "no conv tile fits this geometry");
+    if (!tuning_allowed(s)) return TBN_SUCCESS;
+    const int ceil_m = (g.M + 31) / 32 * 32;
+    int cands[sizeof(kMenu) / sizeof(kMenu[0])];
+    int ncand = 0;
+    for (int i = 0; i < static_cast<int>(sizeof(kMenu) / sizeof(kMenu[0])); ++i) {
+        PatchGeom t;
+        if (kMenu[i].BM > ceil_m || !tile_fits(g, kMenu[i], t)) continue;
+        cands[ncand++] = i;
+    }
+    if (ncand <= 1) return TBN_SUCCESS;
+    const int64_t plane = g.pool ? static_cast<int64_t>(g.PH) * g.PW : static_cast<int64_t>(g.OH) * g.OW;
+    const size_t ybytes = static_cast<size_t>(g.N) * g.M * plane * sizeof(float);
+    void* tmp = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipMallocAsync(&tmp, ybytes, s) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
+        hipEventCreate(&e1) != hipSuccess) {
+        (void)hipGetLastError();
+        if (tmp) (void)hipFreeAsync(tmp, s);
+        if (e0) (void)hipEventDestroy(e0);
+        return TBN_SUCCESS;  // keep the static choice
+    }
+    PatchEpi te = epi;
+    te.y = static_cast<float*>(tmp);
+    int best = -1;
+    float best_ms = 0.0f;
+    for (int k = 0; k < ncand; ++k) {
+        const TileChoice& c = kMenu[cands[k]];
+        PatchGeom t;
+        tile_fits(g, c, t);
+        if (dispatch_patch<TERNARY>(c.cfg, x, t, w, col_bytes, m_alloc, te, s) != TBN_SUCCESS) continue;
+        (void)hipEventRecord(e0, s);
+        bool ok = true;
+        for (int r = 0; r < 2 && ok; ++r) ok = dispatch_patch<TERNARY>(c.cfg, x, t, w, col_bytes, m_alloc, te, s) == TBN_SUCCESS;
+        (void)hipEventRecord(e1, s);
+        float ms = 0.0f;
+        if (!ok || hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) continue;
+        if (best < 0 || ms < best_ms) {
+            best = cands[k];
+            best_ms = ms;
+        }
+    }
+    (void)hipFreeAsync(tmp, s);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    (void)hipGetLastError();
+    tbn_hip::ok();
+    if (best < 0) return TBN_SUCCESS;
+    out = kMenu[best];
+    fill_patch(g, out);
+    std::lock_guard<std::mutex> lock(plan_mutex());
+    plan_cache()[key] = best;
+    return TBN_SUCCESS;
 }
 
 int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
@@ -651,6 +875,11 @@ int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
     g.PW = g.pool ? g.OW / 2 : 0;
     g.VH = g.pool ? 2 * g.PH : g.OH;
     g.VW = g.pool ? 2 * g.PW : g.OW;
+    // staging loads address one image and the conv-layout weights with 32-bit offsets
+    const int64_t image_bytes = static_cast<int64_t>(g.C) * g.H * g.W * 4;
+    const int64_t weight_bytes = (d->m + 7) / 8 * 8 * static_cast<int64_t>(g.chunks) * g.taps * 8;
+    if (image_bytes >= 0xFFFFFFF0LL || weight_bytes >= 0xFFFFFFF0LL)
+        return tbn_hip::fail(TBN_INVALID_SHAPE, "conv image or weights too large for the patch kernel");
     return TBN_SUCCESS;
 }
 
@@ -667,7 +896,10 @@ int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, con
     TBN_REQUIRE(!(residual && g.pool), TBN_INVALID_ARGUMENT,
                 "a residual input cannot be combined with the fused max pool");
     TileChoice tc;
-    TBN_REQUIRE(choose_tile(g, tc), TBN_INVALID_SHAPE, "no conv tile fits this kernel size / stride / dilation");
+    {
+        PatchGeom t = g;
+        TBN_REQUIRE(choose_tile(t, tc), TBN_INVALID_SHAPE, "no conv tile fits this kernel size / stride / dilation");
+    }
     if (g.VH == 0 || g.VW == 0 || g.N == 0) return tbn_hip::ok();
     TBN_REQUIRE(x && conv_weights && y, TBN_INVALID_ARGUMENT, "null pointer");
     TBN_REQUIRE(reinterpret_cast<uintptr_t>(conv_weights) % 8 == 0, TBN_INVALID_ARGUMENT,
@@ -677,7 +909,13 @@ int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, con
     const int64_t col_bytes = Kc / (weights == TBN_WEIGHTS_BINARY ? 8 : 4);
     const int m_alloc = int((desc->m + 7) / 8 * 8);
     PatchEpi epi{y, scale, alpha, bias, residual, flags};
-    if (weights == TBN_WEIGHTS_TERNARY) return dispatch_patch<true>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, epi, s);
+    if (weights == TBN_WEIGHTS_TERNARY) {
+        rc = select_tile<true>(desc, g, x, conv_weights, col_bytes, m_alloc, epi, s, tc);
+        if (rc) return rc;
+        return dispatch_patch<true>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, epi, s);
+    }
+    rc = select_tile<false>(desc, g, x, conv_weights, col_bytes, m_alloc, epi, s, tc);
+    if (rc) return rc;
     return dispatch_patch<false>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, epi, s);
 }
 
