@@ -123,23 +123,25 @@ struct PatchCfg {
 // 8 binary weight bits (bit e = weight e, 1 means -1) -> 8 bf16 +-1.0.  Bits
 // 16 and up of x must be zero (bits 8..15 are ignored): y holds bit e at e and
 // e + 15, so one shift puts bit 2d at 15 and bit 2d+1 at 31.
-__device__ __forceinline__ u32x4_t decode_binary8_fast(uint32_t x) {
+// `ones` is the +1.0 bf16 pair 0x3F803F80 held in a VGPR, so each dword is one
+// shift and one v_and_or_b32.
+__device__ __forceinline__ u32x4_t decode_binary8_fast(uint32_t x, uint32_t ones) {
     const uint32_t y = x | (x << 15);
     u32x4_t r;
-    r[0] = ((y << 15) & 0x80008000u) | 0x3F803F80u;
-    r[1] = ((y << 13) & 0x80008000u) | 0x3F803F80u;
-    r[2] = ((y << 11) & 0x80008000u) | 0x3F803F80u;
-    r[3] = ((y << 9) & 0x80008000u) | 0x3F803F80u;
+    r[0] = ((y << 15) & 0x80008000u) | ones;
+    r[1] = ((y << 13) & 0x80008000u) | ones;
+    r[2] = ((y << 11) & 0x80008000u) | ones;
+    r[3] = ((y << 9) & 0x80008000u) | ones;
     return r;
 }
 
 template <bool TERNARY>
-__device__ __forceinline__ u32x4_t weight_frag(uint2 w, int kk, int kg) {
+__device__ __forceinline__ u32x4_t weight_frag(uint2 w, int kk, int kg, uint32_t ones) {
     if (TERNARY) {
         const uint32_t word = kk ? w.y : w.x;
         return decode_ternary8((word >> (16 * kg)) & 0xFFFFu);
     }
-    return decode_binary8_fast(__builtin_amdgcn_ubfe(w.x, 8 * (2 * kk + kg), 16));
+    return decode_binary8_fast(__builtin_amdgcn_ubfe(w.x, 8 * (2 * kk + kg), 16), ones);
 }
 
 struct PatchEpi {
@@ -321,6 +323,8 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     __syncthreads();
 
     const int kg = lane >> 5;
+    uint32_t ones;
+    asm volatile("v_mov_b32 %0, 0x3f803f80" : "=v"(ones));
     // patch offset of tap (r, s): (r*dh*PWi + s*dw) * kPix
     const int tap_ds = g.dw * kPix;
     const int tap_dr = g.dh * g.PWi * kPix;
@@ -361,7 +365,7 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
             u32x4_t bcur[3][Cfg::FC], acur[Cfg::FR];
             read_b(0, 0, bcur);
 #pragma unroll
-            for (int f = 0; f < Cfg::FR; ++f) acur[f] = weight_frag<TERNARY>(wr[f][0], 0, kg);
+            for (int f = 0; f < Cfg::FR; ++f) acur[f] = weight_frag<TERNARY>(wr[f][0], 0, kg, ones);
 #pragma unroll
             for (int t = 0; t < 2 * TAPS; ++t) {
                 const int nt = (t + 1) >> 1, nk = (t + 1) & 1;
@@ -371,7 +375,7 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                 mfma_step(acur, bcur);
                 if (t + 1 < 2 * TAPS) {
 #pragma unroll
-                    for (int f = 0; f < Cfg::FR; ++f) anext[f] = weight_frag<TERNARY>(wr[f][nt], nk, kg);
+                    for (int f = 0; f < Cfg::FR; ++f) anext[f] = weight_frag<TERNARY>(wr[f][nt], nk, kg, ones);
                 }
 #pragma unroll
                 for (int q = 0; q < 3 * Cfg::FR * Cfg::FC; ++q) {
@@ -414,7 +418,7 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                     else if (tap + 1 < g.taps) read_b(next_toff, 0, bnext);
                     u32x4_t a[Cfg::FR];
 #pragma unroll
-                    for (int f = 0; f < Cfg::FR; ++f) a[f] = weight_frag<TERNARY>(w[f], kk, kg);
+                    for (int f = 0; f < Cfg::FR; ++f) a[f] = weight_frag<TERNARY>(w[f], kk, kg, ones);
                     mfma_step(a, bcur);
 #pragma unroll
                     for (int p = 0; p < 3; ++p)
