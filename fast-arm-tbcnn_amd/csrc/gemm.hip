@@ -97,10 +97,10 @@ int gemm_quant(const float* A, int64_t lda, int64_t M, int64_t N, int64_t K, con
     GemmEpi epi{C, ldc, static_cast<int>(M), static_cast<int>(N), scale, alpha, bias,
                 (cin && beta != 0.0f) ? cin : nullptr, beta, cin_1d, flags};
     const int64_t col_bytes = TERNARY ? K_pad / 4 : K_pad / 8;
-    if (!TERNARY) {
+    {
         const tbn_hip::WideGemmArgs wa{A, lda, int(M), int(N), int(K), packed, col_bytes, int(N_pad), C, ldc,
                                        scale, alpha, bias, epi.cin, cin_1d, beta, flags};
-        if (tbn_hip::gemm_wide_binary_fits(wa)) return tbn_hip::gemm_wide_binary(wa, tbn_hip::stream_of(stream));
+        if (tbn_hip::gemm_wide_fits(wa, TERNARY)) return tbn_hip::gemm_wide(wa, TERNARY, tbn_hip::stream_of(stream));
     }
     const int64_t big_tiles = tbn_hip::ceil_div(M, CfgBig::BR) * tbn_hip::ceil_div(N, CfgBig::BC);
     if (big_tiles >= 256) {

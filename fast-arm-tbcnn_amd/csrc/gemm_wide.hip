@@ -21,6 +21,9 @@
 // Blocks are dealt round-robin over the 8 XCDs; the tile order puts the
 // BC-column tiles of one 128-row band of A on the same XCD, so the band is
 // fetched from HBM once into that XCD's L2 and read there by its tiles.
+#include <algorithm>
+#include <cstdlib>
+#include <string>
 #include <type_traits>
 
 #include "gemm_wide.hpp"
@@ -41,16 +44,15 @@ struct WideCfg {
     static constexpr int KK = KS / 16;             // MFMA k-slices per step
     static constexpr int EPT = BR * KS / NT;       // A elements a thread stages per step
     static constexpr int TPR = KS / EPT;           // threads per A row
-    static constexpr int WPS = KS / 32;            // 32-bit W words per column per step
-    static constexpr int SPG = 4 / WPS;            // steps per 16-byte W load
     static_assert(EPT % 8 == 0 && KS % EPT == 0, "a thread stages whole 8-element groups of one row");
     static_assert(WR % 32 == 0 && WC % 32 == 0 && BR % WR == 0 && BC % WC == 0, "bad tile");
-    static_assert(KK % 2 == 0 && SPG % 2 == 0, "double buffers alternate with even periods");
+    static_assert(KK % 2 == 0 && KS == 64, "two k-slice fragment buffers; 8 / 16 weight bytes per step");
 };
 
 using Wide = WideCfg<128, 512, 128, 64, 64>;
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x2_t __attribute__((ext_vector_type(2)));
 
 // Buffer resource word 3 for gfx9: 32-bit dword data format, raw addressing.
 constexpr int kRsrcWord3 = 0x00020000;
@@ -72,6 +74,25 @@ __device__ __forceinline__ u32x4_t decode_binary8_y(uint32_t x, uint32_t ones) {
     r[1] = ((y << 13) & 0x80008000u) | ones;
     r[2] = ((y << 11) & 0x80008000u) | ones;
     r[3] = ((y << 9) & 0x80008000u) | ones;
+    return r;
+}
+
+// 8 two-bit ternary codes (code i in bits 2i, 2i+1: 00 -> -1, 10 -> +1, 01 and
+// 11 -> 0) -> 8 bf16.  With u = ~x, bit 2i+1 of u is the sign and bit 2i says
+// "nonzero"; v holds u at i and i + 14, so one shift places code 2d's bits at
+// 15 and code 2d+1's at 31.  The +-1 pair is built like the binary decode and
+// the zero codes are masked with a packed 16-bit arithmetic shift.
+__device__ __forceinline__ u32x4_t decode_ternary8_y(uint32_t x, uint32_t ones) {
+    const uint32_t u = x ^ 0xFFFFu;
+    const uint32_t v = u | (u << 14);
+    u32x4_t r;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t sg = v << (14 - 4 * d);  // bit 15 <- u[4d+1], bit 31 <- u[4d+3]
+        const uint32_t val = (sg & 0x80008000u) | ones;
+        const i16x2_t nz = __builtin_bit_cast(i16x2_t, sg << 1) >> 15;  // halves: -1 where nonzero
+        r[d] = val & __builtin_bit_cast(uint32_t, nz);
+    }
     return r;
 }
 
@@ -104,12 +125,15 @@ using bool_c = std::integral_constant<bool, B>;
 template <int I>
 using int_c = std::integral_constant<int, I>;
 
-template <class Cfg>
+// One block: a BR x BC tile of C over the K steps [s0, s0 + ns).  SPLIT
+// blocks (split-K) write their raw sums to `partial` for splitk_reduce_kernel.
+template <class Cfg, bool TERNARY, bool SPLIT>
 __global__ void __launch_bounds__(Cfg::NT)
-gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
+gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per_split, float* partial) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 3 * Cfg::BR * Cfg::KROW];
     constexpr int kPlane = Cfg::BR * Cfg::KROW;  // bf16 per plane
     constexpr int KS = Cfg::KS;
+    constexpr int WPS = TERNARY ? 4 : 2;        // 32-bit weight words per column per step
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -122,14 +146,18 @@ gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
     asm volatile("v_mov_b32 %0, 0x3f803f80" : "=v"(ones));
 
     // tile order: the tiles of one XCD (blockIdx % 8) are consecutive in t,
-    // and consecutive t share a row band of A
+    // and consecutive t share a row band of A; split-K blocks are split-major
     const int total = tiles_r * tiles_c;
-    int t = blockIdx.x;
+    const int split = SPLIT ? static_cast<int>(blockIdx.x) / total : 0;
+    int t = static_cast<int>(blockIdx.x) - split * total;
     if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
     const int tr = t / tiles_c;
     const int tc = t - tr * tiles_c;
     const int r0 = tr * Cfg::BR;
     const int c0 = tc * Cfg::BC;
+    const int all_steps = (p.K + KS - 1) / KS;
+    const int s0 = SPLIT ? split * steps_per_split : 0;
+    const int ns = SPLIT ? min(steps_per_split, all_steps - s0) : all_steps;
 
     // A staging: thread -> row ar, EPT consecutive k from ag * EPT
     const int ar = tid / Cfg::TPR, ag = tid % Cfg::TPR;
@@ -145,15 +173,12 @@ gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
     for (int j = 0; j < Cfg::FC; ++j)
         b_voff[j] = (wc * Cfg::WC + j * 32 + (lane & 31)) * static_cast<int>(p.col_bytes);
 
-    const int steps = (p.K + KS - 1) / KS;
-    const int groups = (steps + Cfg::SPG - 1) / Cfg::SPG;
-
-    float areg[Cfg::EPT];                          // A of the next step, in flight
-    uint32_t bw[Cfg::FC][4], bwn[Cfg::FC][4];      // W words of the current / next group
-    u32x4_t bfr[2][Cfg::FC];                       // decoded W fragments, alternating k-slices
+    float areg[Cfg::EPT];                              // A of the next step, in flight
+    uint32_t bw[Cfg::FC][WPS], bwn[Cfg::FC][WPS];      // W words of the current / next step
+    u32x4_t bfr[2][Cfg::FC];                           // decoded W fragments, alternating k-slices
 
     // loads past the end of A / W return zeros or data of later rows / columns
-    // that no result uses, so they need no guard
+    // that no result uses, so they need no guard; s is an absolute step
     auto load_a = [&](int s) {
         const int soff = s * KS * 4;
 #pragma unroll
@@ -164,20 +189,31 @@ gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
             for (int e = 0; e < 4; ++e) areg[4 * v + e] = x[e];
         }
     };
-    auto load_b = [&](int g, uint32_t (&w)[Cfg::FC][4]) {
+    auto load_b = [&](int s, uint32_t (&w)[Cfg::FC][WPS]) {
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
-            const u32x4_t x =
-                __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], g * 16, 0));
+            if constexpr (TERNARY) {
+                const u32x4_t x = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], s * 4 * WPS, 0));
 #pragma unroll
-            for (int d = 0; d < 4; ++d) w[j][d] = x[d];
+                for (int d = 0; d < WPS; ++d) w[j][d] = x[d];
+            } else {
+                const uint64_t x = __builtin_bit_cast(
+                    uint64_t, __builtin_amdgcn_raw_buffer_load_b64(b_rs, b_voff[j], s * 4 * WPS, 0));
+                w[j][0] = static_cast<uint32_t>(x);
+                w[j][1] = static_cast<uint32_t>(x >> 32);
+            }
         }
     };
-    // k-slice kk of a step whose words start at w[.][wofs]
-    auto decode_b = [&](const uint32_t (&w)[Cfg::FC][4], int wofs, int kk, u32x4_t (&bf)[Cfg::FC]) {
+    // k-slice kk (16 k) of a step's words: binary 8 bits, ternary 16 bits per lane half
+    auto decode_b = [&](const uint32_t (&w)[Cfg::FC][WPS], int kk, u32x4_t (&bf)[Cfg::FC]) {
 #pragma unroll
-        for (int j = 0; j < Cfg::FC; ++j)
-            bf[j] = decode_binary8_y(__builtin_amdgcn_ubfe(w[j][wofs + kk / 2], 16 * (kk & 1) + 8 * h, 16), ones);
+        for (int j = 0; j < Cfg::FC; ++j) {
+            if constexpr (TERNARY)
+                bf[j] = decode_ternary8_y(__builtin_amdgcn_ubfe(w[j][kk], 16 * h, 16), ones);
+            else
+                bf[j] = decode_binary8_y(__builtin_amdgcn_ubfe(w[j][kk / 2], 16 * (kk & 1) + 8 * h, 16), ones);
+        }
     };
     // split the staged step into the three planes of LDS buffer b; with
     // MASK, values at k >= K (last step) are zeroed first
@@ -211,27 +247,26 @@ gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
     // fragment read base: row wr*WR + lane%32, k offset 8*(lane/32)
     const int a_frag = (wr * Cfg::WR + (lane & 31)) * Cfg::KROW + h * 8;
 
-    // One K step s = SPG*g + u on LDS buffer u & 1: per k-slice kk, 3 planes x
-    // FR x FC MFMAs with the W fragments decoded one slice ahead; meanwhile
-    // split step s+1's A (in registers) into the other buffer and fetch step
-    // s+2's A.  FULL steps (s + 2 < steps) need no guards.
-    auto step = [&](int g, auto uc, auto full) {
+    // Local step l = 2q + u on LDS buffer u: per k-slice kk, 3 planes x FR x FC
+    // MFMAs with the W fragments decoded one slice ahead; meanwhile split step
+    // l+1's A (in registers) into the other buffer and fetch step l+2's A and
+    // W words.  FULL steps (l + 2 < ns) need no guards.
+    auto step = [&](int q, auto uc, auto full) {
         constexpr int u = decltype(uc)::value;
         constexpr bool FULL = decltype(full)::value;
-        constexpr int b = u & 1;
-        const int s = Cfg::SPG * g + u;
+        const int l = 2 * q + u;
+        const int s = s0 + l;
 #pragma unroll
         for (int kk = 0; kk < Cfg::KK; ++kk) {
             // next slice's W fragments (the next step's first slice after the last)
-            if (kk + 1 < Cfg::KK) decode_b(bw, u * Cfg::WPS, kk + 1, bfr[(kk + 1) & 1]);
-            else if (u + 1 < Cfg::SPG) decode_b(bw, (u + 1) * Cfg::WPS, 0, bfr[0]);
-            else decode_b(bwn, 0, 0, bfr[0]);
+            if (kk + 1 < Cfg::KK) decode_b(bw, kk + 1, bfr[(kk + 1) & 1]);
+            else decode_b(bwn, 0, bfr[0]);
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl) {
                 u32x4_t af[Cfg::FR];
 #pragma unroll
                 for (int i = 0; i < Cfg::FR; ++i)
-                    af[i] = *reinterpret_cast<const u32x4_t*>(lds + (b * 3 + pl) * kPlane + i * 32 * Cfg::KROW +
+                    af[i] = *reinterpret_cast<const u32x4_t*>(lds + (u * 3 + pl) * kPlane + i * 32 * Cfg::KROW +
                                                              a_frag + kk * 16);
 #pragma unroll
                 for (int i = 0; i < Cfg::FR; ++i)
@@ -240,65 +275,76 @@ gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
             }
         }
         if constexpr (FULL) {
-            store_a(b ^ 1, s + 1, bool_c<false>{});
+            store_a(u ^ 1, s + 1, bool_c<false>{});
             load_a(s + 2);
         } else {
-            if (s + 1 < steps) store_a(b ^ 1, s + 1, bool_c<true>{});
-            if (s + 2 < steps) load_a(s + 2);
+            if (l + 1 < ns) store_a(u ^ 1, s + 1, bool_c<true>{});
+            if (l + 2 < ns) load_a(s + 2);
         }
-        if constexpr (u + 1 == Cfg::SPG) {
 #pragma unroll
-            for (int j = 0; j < Cfg::FC; ++j)
+        for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
-                for (int d = 0; d < 4; ++d) bw[j][d] = bwn[j][d];
-            load_b(g + 2, bwn);
-        }
+            for (int d = 0; d < WPS; ++d) bw[j][d] = bwn[j][d];
+        load_b(s + 2, bwn);
         if constexpr (FULL) {
             // 4 fragment reads ahead, then per fragment: 2 MFMAs, the next read, VALU
             constexpr int kReads = Cfg::KK * 3 * Cfg::FR;
             constexpr int kPairs = Cfg::KK * 3 * Cfg::FR * Cfg::FC / 2;
+            constexpr int kValu = TERNARY ? 7 : 5;
             __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-            for (int q = 0; q < kReads - 4; ++q) {
+            for (int r = 0; r < kReads - 4; ++r) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
             }
 #pragma unroll
-            for (int q = kReads - 4; q < kPairs; ++q) {
+            for (int r = kReads - 4; r < kPairs; ++r) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
             }
         }
         __syncthreads();
     };
 
-    // prologue: step 0 split into buffer 0, step 1 in flight, W groups 0 and 1,
-    // W fragments of step 0's first slice decoded
-    load_a(0);
-    load_b(0, bw);
-    load_b(1, bwn);
-    store_a(0, 0, bool_c<true>{});
-    load_a(1);
-    decode_b(bw, 0, 0, bfr[0]);
+    // prologue: step s0 split into buffer 0, step s0+1 in flight, W words of
+    // steps s0 and s0+1, W fragments of step s0's first slice decoded
+    load_a(s0);
+    load_b(s0, bw);
+    load_b(s0 + 1, bwn);
+    store_a(0, s0, bool_c<true>{});
+    load_a(s0 + 1);
+    decode_b(bw, 0, bfr[0]);
     __syncthreads();
 
-    int g = 0;
-    for (; Cfg::SPG * g + Cfg::SPG + 1 < steps; ++g) {
-        step(g, int_c<0>{}, bool_c<true>{});
-        step(g, int_c<1>{}, bool_c<true>{});
-        if constexpr (Cfg::SPG == 4) {
-            step(g, int_c<2 % Cfg::SPG>{}, bool_c<true>{});
-            step(g, int_c<3 % Cfg::SPG>{}, bool_c<true>{});
-        }
+    const int pairs = (ns + 1) / 2;
+    int q = 0;
+    for (; 2 * q + 3 < ns; ++q) {
+        step(q, int_c<0>{}, bool_c<true>{});
+        step(q, int_c<1>{}, bool_c<true>{});
     }
-    for (; g < groups; ++g) {
-        if (Cfg::SPG * g + 0 < steps) step(g, int_c<0>{}, bool_c<false>{});
-        if (Cfg::SPG * g + 1 < steps) step(g, int_c<1>{}, bool_c<false>{});
-        if constexpr (Cfg::SPG == 4) {
-            if (Cfg::SPG * g + 2 < steps) step(g, int_c<2 % Cfg::SPG>{}, bool_c<false>{});
-            if (Cfg::SPG * g + 3 < steps) step(g, int_c<3 % Cfg::SPG>{}, bool_c<false>{});
+    for (; q < pairs; ++q) {
+        step(q, int_c<0>{}, bool_c<false>{});
+        if (2 * q + 1 < ns) step(q, int_c<1>{}, bool_c<false>{});
+    }
+
+    if constexpr (SPLIT) {
+        // raw sums of this split: partial[split][m][n]
+        float* part = partial + static_cast<int64_t>(split) * p.M * p.N;
+#pragma unroll
+        for (int i = 0; i < Cfg::FR; ++i) {
+            const int mrow = r0 + wr * Cfg::WR + i * 32 + 4 * h;
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j) {
+                const int n = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int m = mrow + 8 * (e >> 2) + (e & 3);
+                    if (m < p.M && n < p.N) part[static_cast<int64_t>(m) * p.N + n] = acc[i][j][e];
+                }
+            }
         }
+        return;
     }
 
     // ---- epilogue: C[m, n] = relu?(acc * alpha * scale[n] + bias[n] (+ beta * cin)) ----
@@ -353,26 +399,122 @@ gemm_wide_binary_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c) {
     }
 }
 
+// C = epilogue(sum over splits of partial[s]) with the sums taken in split
+// order, so the result is the same on every run.  Rows are grid-strided over
+// blockIdx.y; each thread takes 4 consecutive columns (float4 when N % 4 == 0).
+__global__ void splitk_reduce_kernel(tbn_hip::WideGemmArgs p, const float* __restrict__ partial, int splits) {
+    const int64_t MN = static_cast<int64_t>(p.M) * p.N;
+    const bool bias_then_scale = (p.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
+    const bool relu = (p.flags & TBN_EPI_RELU) != 0;
+    const bool vec = (p.N % 4) == 0;
+    const int n0 = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
+    if (n0 >= p.N) return;
+    const int cnt = min(4, p.N - n0);
+    float mult[4], badd[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int n = min(n0 + e, p.N - 1);
+        mult[e] = p.scale ? p.alpha * p.scale[n] : p.alpha;
+        badd[e] = p.bias ? p.bias[n] : 0.0f;
+    }
+    for (int m = blockIdx.y; m < p.M; m += gridDim.y) {
+        const int64_t row = static_cast<int64_t>(m) * p.N + n0;
+        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int sp = 0; sp < splits; ++sp) {
+            const float* src = partial + sp * MN + row;
+            if (vec) {
+                const float4 v = *reinterpret_cast<const float4*>(src);
+                acc[0] += v.x, acc[1] += v.y, acc[2] += v.z, acc[3] += v.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (e < cnt) acc[e] += src[e];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (e >= cnt) break;
+            float v = bias_then_scale ? (acc[e] + badd[e]) * mult[e] : acc[e] * mult[e] + badd[e];
+            if (p.cin) v += p.beta * (p.cin_1d ? p.cin[n0 + e] : p.cin[row + e]);
+            if (relu) v = v > 0.0f ? v : 0.0f;
+            p.C[static_cast<int64_t>(m) * p.ldc + n0 + e] = v;
+        }
+    }
+}
+
+// K-split count: 1 when the tiles fill the chip; otherwise enough splits for
+// ~1024 waves, at least 4 K steps each and at most 8 (each split adds M*N*8
+// bytes of partial traffic).
+int split_count(int64_t tiles, int steps) {
+    if (const char* e = std::getenv("TBN_GEMM_SPLITS")) {  // tuning aid
+        const int forced = std::atoi(e);
+        if (forced >= 1) return std::min(forced, std::max(steps, 1));
+    }
+    if (tiles >= 128) return 1;
+    int sp = static_cast<int>((128 + tiles - 1) / tiles);
+    sp = std::min(sp, 8);
+    sp = std::min(sp, steps / 4);
+    return std::max(sp, 1);
+}
+
+template <bool TERNARY, bool SPLIT>
+void launch_wide(const tbn_hip::WideGemmArgs& a, int tiles_r, int tiles_c, int splits, int per, float* part,
+                 hipStream_t stream) {
+    using Cfg = Wide;
+    hipLaunchKernelGGL((gemm_wide_kernel<Cfg, TERNARY, SPLIT>), dim3(tiles_r * tiles_c * splits), dim3(Cfg::NT), 0,
+                       stream, a, tiles_r, tiles_c, per, part);
+}
+
 }  // namespace
 
 namespace tbn_hip {
 
-bool gemm_wide_binary_fits(const WideGemmArgs& a) {
+bool gemm_wide_fits(const WideGemmArgs& a, bool ternary) {
     using Cfg = Wide;
     const int64_t tiles = ceil_div(a.M, Cfg::BR) * ceil_div(a.N, Cfg::BC);
-    return a.M >= 1024 && a.N >= 1024 && a.K >= Cfg::KS && tiles >= 128 && a.lda % 4 == 0 &&
+    const int steps = static_cast<int>(ceil_div(a.K, Cfg::KS));
+    const int64_t blocks = tiles * split_count(tiles, steps);
+    // shapes whose tiles (with K splits) fill at least half the chip
+    return a.K >= Cfg::KS && blocks >= 128 && a.M >= 128 && a.N >= 512 && a.lda % 4 == 0 &&
            reinterpret_cast<uintptr_t>(a.A) % 16 == 0 && a.col_bytes % 16 == 0 &&
            reinterpret_cast<uintptr_t>(a.packed) % 16 == 0 && a.lda <= (1 << 22) &&
-           static_cast<int64_t>(Cfg::BC) * a.col_bytes < (1LL << 31);
+           static_cast<int64_t>(Cfg::BC) * a.col_bytes < (1LL << 31) && (ternary || a.col_bytes % 16 == 0);
 }
 
-int gemm_wide_binary(const WideGemmArgs& a, hipStream_t stream) {
+int gemm_wide(const WideGemmArgs& a, bool ternary, hipStream_t stream) {
     using Cfg = Wide;
     const int tiles_r = static_cast<int>(ceil_div(a.M, Cfg::BR));
     const int tiles_c = static_cast<int>(ceil_div(a.N, Cfg::BC));
-    hipLaunchKernelGGL((gemm_wide_binary_kernel<Cfg>), dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, stream, a,
-                       tiles_r, tiles_c);
-    return check_launch("gemm_f32_binary (wide)");
+    const int steps = static_cast<int>(ceil_div(a.K, Cfg::KS));
+    const int splits = split_count(static_cast<int64_t>(tiles_r) * tiles_c, steps);
+    const char* what = ternary ? "gemm_f32_ternary (wide)" : "gemm_f32_binary (wide)";
+    if (splits == 1) {
+        if (ternary) launch_wide<true, false>(a, tiles_r, tiles_c, 1, steps, nullptr, stream);
+        else launch_wide<false, false>(a, tiles_r, tiles_c, 1, steps, nullptr, stream);
+        return check_launch(what);
+    }
+    const int per = (steps + splits - 1) / splits;
+    const int used = (steps + per - 1) / per;  // splits that own at least one step
+    void* part = nullptr;
+    const size_t bytes = static_cast<size_t>(used) * a.M * a.N * sizeof(float);
+    hipError_t e = hipMallocAsync(&part, bytes, stream);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(e == hipErrorOutOfMemory ? TBN_OUT_OF_MEMORY : TBN_RUNTIME_ERROR,
+                    std::string("split-K partial buffer: ") + hipGetErrorString(e));
+    }
+    if (ternary) launch_wide<true, true>(a, tiles_r, tiles_c, used, per, static_cast<float*>(part), stream);
+    else launch_wide<false, true>(a, tiles_r, tiles_c, used, per, static_cast<float*>(part), stream);
+    int rc = check_launch(what);
+    if (rc == TBN_SUCCESS) {
+        const int gx = static_cast<int>(ceil_div(ceil_div(a.N, 4), 256));
+        const int gy = static_cast<int>(std::min<int64_t>(a.M, 65535));
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(gx, gy), dim3(256), 0, stream, a,
+                           static_cast<const float*>(part), used);
+        rc = check_launch("gemm split-K reduce");
+    }
+    (void)hipFreeAsync(part, stream);
+    return rc;
 }
 
 }  // namespace tbn_hip

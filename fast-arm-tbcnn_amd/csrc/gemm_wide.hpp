@@ -24,9 +24,12 @@ struct WideGemmArgs {
     int flags;
 };
 
-// True when the wide kernel takes this GEMM: enough tiles to fill the chip,
-// 16-byte aligned fp32 rows and 16-byte multiple packed columns.
-bool gemm_wide_binary_fits(const WideGemmArgs& a);
-int gemm_wide_binary(const WideGemmArgs& a, hipStream_t stream);
+// True when the wide kernel takes this GEMM: enough tiles (with K splits) to
+// fill the chip, 16-byte aligned fp32 rows and 16-byte multiple packed columns.
+// `packed` holds BinaryMatrix columns, or 2-bit ternary columns when ternary.
+bool gemm_wide_fits(const WideGemmArgs& a, bool ternary);
+// Runs it; shapes with few tiles split K and sum the splits in a second,
+// deterministic pass (stream-ordered temporary of splits * M * N floats).
+int gemm_wide(const WideGemmArgs& a, bool ternary, hipStream_t stream);
 
 }  // namespace tbn_hip

@@ -166,6 +166,72 @@ def test_gemm_binary_wide_tiles(dev, orc, M, K, N, lda):
         rm.assert_within_tolerance(host(C), ref, K, xmax)
 
 
+def _f64_dev_ternary(A, t, scale, alpha=1.0, bias=None, relu=False, bias_then_scale=False, cin=None, beta=0.0):
+    dA = torch.as_tensor(A, dtype=torch.float64, device="cuda")
+    dT = torch.as_tensor(t, dtype=torch.float64, device="cuda")
+    acc = dA @ dT
+    s = torch.as_tensor(scale, dtype=torch.float64, device="cuda") * alpha
+    b = 0.0 if bias is None else torch.as_tensor(bias, dtype=torch.float64, device="cuda")
+    out = (acc + b) * s if bias_then_scale else acc * s + b
+    if cin is not None:
+        out = out + beta * torch.as_tensor(cin, dtype=torch.float64, device="cuda")
+    if relu:
+        out = out.clamp_min(0.0)
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 4096, 4096), (384, 2600, 2600), (2048, 1024, 4096), (130, 1000, 700)])
+def test_gemm_ternary_wide_and_split(dev, orc, M, K, N):
+    """Ternary weights through the wide kernel: split-K for few tiles (the
+    first two shapes), one pass for many (the third); the last shape stays on
+    the small-tile engine.  Every element against float64, all epilogues."""
+    rng = np.random.default_rng(M + K + N)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    t = rng.choice(np.array([-1, 0, 1], np.int8), size=(K, N), p=[0.3, 0.4, 0.3])
+    scale = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    K_pad = (K + 63) // 64 * 64
+    packed = empty(N * K_pad // 4, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(t)), K, N, tbn_hip.LAYOUT_KN, K_pad, N, P(packed), None)
+    dA = to_dev(A)
+    xmax = np.abs(A).max() * 1.5
+    for flags, alpha in [(0, 1.0), (tbn_hip.EPI_RELU, 0.7), (tbn_hip.EPI_BIAS_THEN_SCALE, 1.3)]:
+        out = host(run_gemm("ternary", dA, K, M, N, K, packed, K_pad, N, scale, alpha, bias, flags))
+        ref = _f64_dev_ternary(A, t, scale, alpha, bias, relu=bool(flags & tbn_hip.EPI_RELU),
+                               bias_then_scale=bool(flags & tbn_hip.EPI_BIAS_THEN_SCALE))
+        r, _ = rm.assert_within_tolerance(out, ref, K, xmax * alpha)
+        assert r < 1e-6
+    rows = np.array([0, M // 3, M - 1])
+    out = host(run_gemm("ternary", dA, K, M, N, K, packed, K_pad, N, scale, 0.5))
+    ref = orc.gemm_f64_ternary(A[rows], host(packed), K_pad, N, scale, 0.5)
+    rm.assert_within_tolerance(out[rows], ref, K, xmax)
+    # deterministic: a second launch gives identical bits
+    out2 = host(run_gemm("ternary", dA, K, M, N, K, packed, K_pad, N, scale, 0.5))
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+
+
+@pytest.mark.parametrize("M,K,N", [(640, 2000, 2048), (256, 4096, 4096), (512, 777, 4000)])
+def test_gemm_binary_split_k(dev, orc, M, K, N):
+    """Binary GEMMs with few wide tiles split K and reduce in a second pass:
+    ragged M / N / K, the fp32 addend, bit-for-bit repeatable."""
+    A, binw, scale, bias = make_binary_problem(M, K, N, seed=M * 3 + K)
+    packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+    dA = to_dev(A)
+    xmax = np.abs(A).max() * 1.5
+    out = host(run_gemm("binary", dA, K, M, N, K, packed, K_pad, N_pad, scale, 0.9, bias, tbn_hip.EPI_RELU))
+    ref = _f64_dev_gemm(A, binw, scale, 0.9, bias, relu=True)
+    r, _ = rm.assert_within_tolerance(out, ref, K, xmax)
+    assert r < 1e-6
+    out2 = host(run_gemm("binary", dA, K, M, N, K, packed, K_pad, N_pad, scale, 0.9, bias, tbn_hip.EPI_RELU))
+    assert np.array_equal(out.view(np.uint32), out2.view(np.uint32))
+    cin = np.random.default_rng(1).standard_normal((M, N)).astype(np.float32)
+    C = empty((M, N), torch.float32)
+    tbn_hip.call("tbn_hip_gemm_f32_quantized", tbn_hip.WEIGHTS_BINARY, P(dA), K, M, N, K, P(packed), K_pad, N_pad,
+                 P(to_dev(scale)), 1.0, None, P(to_dev(cin)), 0, -1.5, 0, P(C), N, None)
+    ref = _f64_dev_gemm(A, binw, scale, 1.0, None, cin=cin, beta=-1.5)
+    rm.assert_within_tolerance(host(C), ref, K, xmax)
+
+
 def test_gemm_binary_wide_special_values(dev):
     """inf / nan rows through the wide kernel: +-inf per column sign, nan rows stay nan."""
     M, K, N = 2048, 512, 4096
