@@ -53,6 +53,33 @@ def time_stream(fn, stream, steps, warmup, torch):
     return start.elapsed_time(end) / steps
 
 
+def time_graph(step, steps, warmup, torch):
+    """Device time of one launch for microsecond-scale kernels: `steps`
+    launches captured into a HIP graph and replayed, timed with HIP events, so
+    the Python launch overhead (about 10 us per ctypes call) is not counted.
+    Only for entry points that allocate nothing."""
+    for _ in range(warmup):
+        step(None)
+    torch.cuda.synchronize()
+    cap = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        sh = torch.cuda.current_stream().cuda_stream
+        for _ in range(steps):
+            step(sh)
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    reps = 3
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (reps * steps)
+
+
 # ---- workloads --------------------------------------------------------------------------
 
 def packed_gemm(torch, tbn_hip, M, N, K, seed, ternary=False):
@@ -231,7 +258,7 @@ def main():
         del keep
     if want("conv"):
         step, step_ref, keep = conv_cfg4(torch, tbn_hip, seed=2)
-        conv_ms = timed(step)
+        conv_ms = time_graph(step, args.steps, args.warmup, torch)
         conv_flops = 2.0 * 64 * 196 * 576 * 128
         extra["conv_us_per_batch"] = round(conv_ms * 1e3, 2)
         extra["conv_gflops_equiv"] = round(conv_flops / (conv_ms * 1e-3) / 1e9, 1)
@@ -270,7 +297,7 @@ def main():
         del A, binw, packed, out
     if want("gemm1024"):
         step, keep, _, _ = packed_gemm(torch, tbn_hip, 1024, 1024, 1024, seed=4)
-        g_ms = timed(step)
+        g_ms = time_graph(step, args.steps, args.warmup, torch)
         extra["gemm_cfg2_us"] = round(g_ms * 1e3, 2)
         extra["gemm_cfg2_gflops_equiv"] = round(2.0 * 1024 ** 3 / (g_ms * 1e-3) / 1e9, 1)
         log(f"binary cfg2 1024^3: {g_ms * 1e3:.1f} us")

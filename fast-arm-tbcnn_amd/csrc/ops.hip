@@ -5,6 +5,8 @@
 // (GlobalAveragePool sums each plane sequentially, as pooling.cpp:200-212).
 #include <string>
 
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace {
@@ -21,25 +23,28 @@ inline int grid_for(int64_t work) {
 __global__ void maxpool2d_kernel(const float* __restrict__ x, int64_t planes, int H, int W,
                                  int OH, int OW, int kh, int kw, int sh, int sw, int ph, int pw,
                                  int dh, int dw, float* __restrict__ y) {
-    const int64_t total = planes * OH * OW;
-    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
-         t += (int64_t)gridDim.x * blockDim.x) {
-        const int ow = static_cast<int>(t % OW);
-        const int oh = static_cast<int>((t / OW) % OH);
-        const int64_t plane = t / ((int64_t)OH * OW);
+    // blockIdx.y (grid-strided) walks the planes, x-threads the plane's
+    // outputs: 32-bit index math only
+    const int per_plane = OH * OW;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= per_plane) return;
+    const int oh = i / OW;
+    const int ow = i - oh * OW;
+    const int ih0 = oh * sh - ph, iw0 = ow * sw - pw;
+    for (int64_t plane = blockIdx.y; plane < planes; plane += gridDim.y) {
         const float* src = x + plane * H * W;
         float mx = -INFINITY;
         for (int r = 0; r < kh; ++r) {
-            const int ih = oh * sh - ph + r * dh;
+            const int ih = ih0 + r * dh;
             if (ih < 0 || ih >= H) continue;
             for (int s = 0; s < kw; ++s) {
-                const int iw = ow * sw - pw + s * dw;
+                const int iw = iw0 + s * dw;
                 if (iw < 0 || iw >= W) continue;
-                const float v = src[(int64_t)ih * W + iw];
+                const float v = src[ih * W + iw];
                 if (mx < v) mx = v;
             }
         }
-        y[t] = mx;
+        y[plane * per_plane + i] = mx;
     }
 }
 
@@ -153,7 +158,11 @@ int tbn_hip_maxpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w
     if (!y || n * c == 0) return tbn_hip::ok();
     TBN_REQUIRE(x != nullptr, TBN_INVALID_ARGUMENT, "null pointer");
     TBN_DEVICE_GUARD();
-    hipLaunchKernelGGL(maxpool2d_kernel, dim3(grid_for(n * c * OH * OW)), dim3(kThreads), 0,
+    TBN_REQUIRE(h * w < (1LL << 31) && OH * OW < (1LL << 31), TBN_INVALID_SHAPE, "pooling plane too large");
+    hipLaunchKernelGGL(maxpool2d_kernel,
+                       dim3(static_cast<unsigned>(tbn_hip::ceil_div(OH * OW, kThreads)),
+                            static_cast<unsigned>(std::min<int64_t>(n * c, 65535))),
+                       dim3(kThreads), 0,
                        tbn_hip::stream_of(stream), x, n * c, int(h), int(w), int(OH), int(OW),
                        int(kh), int(kw), int(sh), int(sw), int(ph), int(pw), int(dh), int(dw), y);
     return tbn_hip::check_launch("maxpool2d");
