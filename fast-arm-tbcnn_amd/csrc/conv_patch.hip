@@ -23,6 +23,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <type_traits>
 
 #include "conv_common.hpp"
 
@@ -144,6 +145,12 @@ __device__ __forceinline__ u32x4_t weight_frag(uint2 w, int kk, int kg, uint32_t
     return decode_binary8_fast(__builtin_amdgcn_ubfe(w.x, 8 * (2 * kk + kg), 16), ones);
 }
 
+// v from lane (lane & ~3) | perm[lane & 3] of the same quad (DPP quad_perm).
+template <int CTRL>
+__device__ __forceinline__ float quad_perm(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
 struct PatchEpi {
     float* y;
     const float* scale;
@@ -153,20 +160,31 @@ struct PatchEpi {
     int flags;
 };
 
+// bf16 elements of one LDS buffer: three planes of patch + 1 pixel records
+// (the spare record takes the stores of items past the patch), the weight
+// words plus a spare one; rounded to 16 bytes so both buffers stay aligned.
+__host__ __device__ inline int patch_buffer_elems(int patch, int words, int word_halves) {
+    return (3 * (patch + 1) * kPix + word_halves * (words + 1) + 7) / 8 * 8;
+}
+
 // TAPS = 9: 3x3 kernels, taps unrolled and the chunk's weight words held in
-// registers; TAPS = 0: any kernel size, words read per tap.
-template <class Cfg, bool TERNARY, int TAPS>
+// registers; TAPS = 0: any kernel size, words read per tap.  MAXI bounds the
+// patch items a thread stages per chunk (4 or 8, the launch picks the smaller
+// that fits): the staging registers live through the whole K loop, and 8
+// items (64 VGPRs) would cost a wave per SIMD on shapes that need 2.
+template <class Cfg, bool TERNARY, int TAPS, int MAXI>
 __global__ void __launch_bounds__(Cfg::NT)
 conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __restrict__ wbits, int64_t col_bytes,
                   int m_alloc, PatchEpi epi) {
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-    // one LDS buffer = the patch (3 planes x pixels x kPix bf16) followed by the
-    // chunk's weight words [tap][channel] (uint32, or uint2 for ternary); two buffers
+    // one LDS buffer = the patch (3 planes x (pixels + 1 spare) x kPix bf16)
+    // followed by the chunk's weight words [tap][channel] (uint32, or uint2 for
+    // ternary) and one spare word; two buffers
     constexpr int kWordHalves = TERNARY ? 4 : 2;       // uint16 per channel word
     const int patch = g.PHi * g.PWi;
-    const int plane_elems = patch * kPix;
+    const int plane_elems = (patch + 1) * kPix;
     const int wofs = 3 * plane_elems;                  // weight words after the planes
-    const int buf_elems = wofs + kWordHalves * Cfg::BM * g.taps;
+    const int buf_elems = patch_buffer_elems(patch, Cfg::BM * g.taps, kWordHalves);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -208,59 +226,75 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     //      weight items = (tap, channel) ----
     const int items = 4 * patch;
     const int per_thread = (items + Cfg::NT - 1) / Cfg::NT;  // <= kMaxItems (host-checked)
-    constexpr int kMaxItems = 8;
+    constexpr int kMaxItems = MAXI;
     const int witems = Cfg::BM * g.taps;
     const int wper_thread = (witems + Cfg::NT - 1) / Cfg::NT;  // <= kMaxWItems (host-checked)
-    constexpr int kMaxWItems = 8;
+    constexpr int kMaxWItems = TAPS > 0 ? std::min(8, (Cfg::BM * TAPS + Cfg::NT - 1) / Cfg::NT) : 8;
     const int64_t img = static_cast<int64_t>(n) * g.C * g.H * g.W;
-    const int64_t HW = static_cast<int64_t>(g.H) * g.W;
-    // staging loads are buffer loads: an element outside the image, past C
-    // or past the weight columns gets an offset beyond the resource and reads
-    // 0, so no branch or select waits on a load before it is stored
-    const __amdgpu_buffer_rsrc_t x_rs = make_rsrc(x + img, static_cast<uint64_t>(g.C) * HW * 4);
+    const uint32_t HW4 = static_cast<uint32_t>(g.H) * g.W * 4;
+    constexpr uint32_t kWordBytes = TERNARY ? 8 : 4;
+    // Staging loads are buffer loads at 32-bit byte offsets (host-checked: the
+    // image with its channels padded to whole chunks, and the weight columns,
+    // stay under 2^31 bytes).  An item outside the image or past the patch
+    // gets an offset of at least kOutside, and a channel past C lands past the
+    // image's C planes: the range check returns 0 for both, so no load waits
+    // on a branch or a select.
+    const __amdgpu_buffer_rsrc_t x_rs = make_rsrc(x + img, static_cast<uint64_t>(g.C) * HW4);
     const __amdgpu_buffer_rsrc_t w_rs = make_rsrc(wbits, static_cast<uint64_t>(m_alloc) * col_bytes);
-    constexpr uint32_t kOutside = 0xFFFFFFF0u;
+    constexpr uint32_t kOutside = 0x80000000u;
+    // per item, computed once: chunk-0 byte offset and LDS slot (an item past
+    // the patch / the word table writes the spare record after it)
+    uint32_t xoff[kMaxItems], woff[kMaxWItems];
+    int xslot[kMaxItems], wslot[kMaxWItems];
+#pragma unroll
+    for (int it = 0; it < kMaxItems; ++it) {
+        const int item = tid + it * Cfg::NT;
+        const int grp = div_by(item, g.mul_patch);
+        const int pp = item - grp * patch;
+        const int pr = div_by(pp, g.mul_pwi);
+        const int ih = ih0 + pr * g.psh;
+        const int iw = iw0 + (pp - pr * g.PWi) * g.psw;
+        const bool in_patch = item < items;
+        const bool ok = in_patch && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
+                        static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
+        xoff[it] = ok ? static_cast<uint32_t>(grp * 8) * HW4 + static_cast<uint32_t>(ih * g.W + iw) * 4 : kOutside;
+        xslot[it] = in_patch ? pp * kPix + grp * 8 : patch * kPix;
+    }
+#pragma unroll
+    for (int it = 0; it < kMaxWItems; ++it) {
+        const int item = tid + it * Cfg::NT;
+        const int ml = item % Cfg::BM;
+        const int tap = item / Cfg::BM;
+        const bool ok = item < witems;
+        woff[it] = ok ? static_cast<uint32_t>(m0 + ml) * static_cast<uint32_t>(col_bytes) + tap * kWordBytes
+                      : kOutside;
+        wslot[it] = (ok ? item : witems) * kWordHalves;
+    }
     float stage[kMaxItems][8];
     uint2 wstage[kMaxWItems];
 
     auto load_chunk = [&](int ch) {
+        const uint32_t cofs = static_cast<uint32_t>(ch * kChunk) * HW4;
+        const uint32_t wofs_ch = static_cast<uint32_t>(ch * g.taps) * kWordBytes;
 #pragma unroll
         for (int it = 0; it < kMaxItems; ++it) {
-            if (it >= per_thread) break;
-            const int item = tid + it * Cfg::NT;
-            const int grp = div_by(item, g.mul_patch);
-            const int pp = item - grp * patch;
-            const int pr = div_by(pp, g.mul_pwi);
-            const int ih = ih0 + pr * g.psh;
-            const int iw = iw0 + (pp - pr * g.PWi) * g.psw;
-            const int c0 = ch * kChunk + grp * 8;
-            const bool ok = item < items && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
-                            static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
-            const uint32_t base = static_cast<uint32_t>((static_cast<int64_t>(c0) * HW + ih * g.W + iw) * 4);
-            const uint32_t step = static_cast<uint32_t>(HW * 4);
+            if (it < per_thread) {
+                const uint32_t o = xoff[it] + cofs;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint32_t off = (ok && c0 + e < g.C) ? base + e * step : kOutside;
-                stage[it][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x_rs, off, 0, 0));
+                for (int e = 0; e < 8; ++e)
+                    stage[it][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x_rs, o + e * HW4, 0, 0));
             }
         }
 #pragma unroll
         for (int it = 0; it < kMaxWItems; ++it) {
-            if (it >= wper_thread) break;
-            const int item = tid + it * Cfg::NT;
-            const int ml = item % Cfg::BM;
-            const int tap = item / Cfg::BM;
-            const int m = m0 + ml;
-            const bool ok = item < witems && m < m_alloc;
-            const int64_t t = static_cast<int64_t>(ch) * g.taps + tap;
-            const uint32_t off = ok ? static_cast<uint32_t>(static_cast<int64_t>(m) * col_bytes + (TERNARY ? 8 : 4) * t)
-                                    : kOutside;
-            if (TERNARY) {
-                const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(w_rs, off, 0, 0);
-                const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b32(w_rs, ok ? off + 4 : kOutside, 0, 0);
-                wstage[it] = make_uint2(lo, hi);
-            } else {
-                wstage[it] = make_uint2(__builtin_amdgcn_raw_buffer_load_b32(w_rs, off, 0, 0), 0u);
+            if (it < wper_thread) {
+                const uint32_t o = woff[it] + wofs_ch;
+                if (TERNARY) {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b64(w_rs, o, 0, 0);
+                    wstage[it] = make_uint2(v[0], v[1]);
+                } else {
+                    wstage[it] = make_uint2(__builtin_amdgcn_raw_buffer_load_b32(w_rs, o, 0, 0), 0u);
+                }
             }
         }
     };
@@ -268,25 +302,19 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
         uint16_t* dst = lds + b * buf_elems;
 #pragma unroll
         for (int it = 0; it < kMaxItems; ++it) {
-            if (it >= per_thread) break;
-            const int item = tid + it * Cfg::NT;
-            if (item < items) {
-                const int grp = div_by(item, g.mul_patch);
-                const int pp = item - grp * patch;
-                const Split4 a = split4(stage[it][0], stage[it][1], stage[it][2], stage[it][3]);
-                const Split4 c = split4(stage[it][4], stage[it][5], stage[it][6], stage[it][7]);
-                uint16_t* d = dst + pp * kPix + grp * 8;
-                *reinterpret_cast<uint4*>(d) = make_uint4(a.hi[0], a.hi[1], c.hi[0], c.hi[1]);
-                *reinterpret_cast<uint4*>(d + plane_elems) = make_uint4(a.mid[0], a.mid[1], c.mid[0], c.mid[1]);
-                *reinterpret_cast<uint4*>(d + 2 * plane_elems) = make_uint4(a.lo[0], a.lo[1], c.lo[0], c.lo[1]);
+            if (it < per_thread) {
+                uint4 hi, mid, lo;
+                split8(stage[it], hi, mid, lo);
+                uint16_t* d = dst + xslot[it];
+                *reinterpret_cast<uint4*>(d) = hi;
+                *reinterpret_cast<uint4*>(d + plane_elems) = mid;
+                *reinterpret_cast<uint4*>(d + 2 * plane_elems) = lo;
             }
         }
 #pragma unroll
         for (int it = 0; it < kMaxWItems; ++it) {
-            if (it >= wper_thread) break;
-            const int item = tid + it * Cfg::NT;
-            if (item < witems) {
-                uint16_t* d = dst + wofs + item * kWordHalves;  // item = tap * BM + channel
+            if (it < wper_thread) {
+                uint16_t* d = dst + wofs + wslot[it];
                 if (TERNARY) *reinterpret_cast<uint2*>(d) = wstage[it];
                 else *reinterpret_cast<uint32_t*>(d) = wstage[it].x;
             }
@@ -437,80 +465,87 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     }
 
     // ---- epilogue: scale, bias, residual, ReLU, optional 2x2 max pool ----
-    // Every value is computed (all loads issued together) before the first
-    // store: y may alias nothing, but the compiler cannot know, and loads
-    // interleaved with stores would each wait a full memory round trip.
+    // Outputs go out as buffer stores at 32-bit offsets into image n's planes
+    // from channel m0 on (host-checked: M + 128 planes stay under 2^31
+    // bytes): rows past M fall beyond the resource and lanes without a pixel
+    // to store carry kOutside, so the range check drops both with no branch.
     const bool pool = g.pool != 0;
-    const int64_t plane = pool ? static_cast<int64_t>(g.PH) * g.PW : static_cast<int64_t>(g.OH) * g.OW;
-    // rows of register e: f*32 + 8*(e/4) + 4*(lane/32) + e%4, four consecutive per float4
-    float mult[Cfg::FR][16], badd[Cfg::FR][16];
-#pragma unroll
-    for (int f = 0; f < Cfg::FR; ++f)
-#pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {
-            const int r = wm * Cfg::WM + f * 32 + 8 * e4 + 4 * (lane >> 5);
-            const float4 mv = *reinterpret_cast<const float4*>(epi_lds + r);
-            const float4 bv = *reinterpret_cast<const float4*>(epi_lds + Cfg::BM + r);
-            mult[f][4 * e4] = mv.x, mult[f][4 * e4 + 1] = mv.y, mult[f][4 * e4 + 2] = mv.z, mult[f][4 * e4 + 3] = mv.w;
-            badd[f][4 * e4] = bv.x, badd[f][4 * e4 + 1] = bv.y, badd[f][4 * e4 + 2] = bv.z, badd[f][4 * e4 + 3] = bv.w;
-        }
-    int64_t out_base[Cfg::FC];
-    bool valid[Cfg::FC];
+    const uint32_t plane = pool ? static_cast<uint32_t>(g.PH * g.PW) : static_cast<uint32_t>(g.OH * g.OW);
+    const uint32_t plane4 = plane * 4;
+    const int64_t obase = (static_cast<int64_t>(n) * g.M + m0) * plane;
+    const uint32_t obytes = static_cast<uint32_t>(g.M - m0) * plane4;
+    const __amdgpu_buffer_rsrc_t y_rs = make_rsrc(epi.y + obase, obytes);
+    const int rlane = wm * Cfg::WM + 4 * (lane >> 5);  // row of register 0 of fragment 0, from m0
+    uint32_t voff[Cfg::FC];
 #pragma unroll
     for (int j = 0; j < Cfg::FC; ++j) {
         int oh, ow, pi;
-        valid[j] = tile_pixel<Cfg>(g, q0, oh0, ow0, wq * Cfg::WQ + j * 32 + (lane & 31), oh, ow, pi);
-        if (!valid[j]) oh = ow = 0;
-        out_base[j] = pool ? (static_cast<int64_t>(n) * g.M * g.PH + (oh >> 1)) * g.PW + (ow >> 1)
-                           : (static_cast<int64_t>(n) * g.M * g.OH + oh) * g.OW + ow;
+        const bool valid = tile_pixel<Cfg>(g, q0, oh0, ow0, wq * Cfg::WQ + j * 32 + (lane & 31), oh, ow, pi);
+        const uint32_t pix = pool ? static_cast<uint32_t>((oh >> 1) * g.PW + (ow >> 1))
+                                  : static_cast<uint32_t>(oh * g.OW + ow);
+        const bool keep = valid && (!pool || (lane & 3) == 0);
+        voff[j] = keep ? static_cast<uint32_t>(rlane) * plane4 + pix * 4 : kOutside;
     }
-#pragma unroll
-    for (int j = 0; j < Cfg::FC; ++j)
-#pragma unroll
-        for (int f = 0; f < Cfg::FR; ++f)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                float v = acc[f][j][e];
-                v = (epi.flags & TBN_EPI_BIAS_THEN_SCALE) ? (v + badd[f][e]) * mult[f][e] : v * mult[f][e] + badd[f][e];
-                acc[f][j][e] = v;
-            }
-    if (epi.residual) {
-        // residual only without pooling (host-checked): same index as the output.
-        // Out-of-range rows and pixels read an in-range element (channel M-1,
-        // pixel 0 of the image) unconditionally; their results are never stored.
-        float res[Cfg::FC][Cfg::FR][16];
-#pragma unroll
-        for (int j = 0; j < Cfg::FC; ++j)
+    // v' = (v + a) * s + b with (a, b) = (bias, 0) for bias-then-scale, else (0, bias)
+    const bool bts = (epi.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
+    auto finish = [&](auto relu_c, auto pool_c, auto res_c) {
+        constexpr bool RELU = decltype(relu_c)::value, POOL = decltype(pool_c)::value, RES = decltype(res_c)::value;
+        // residual (never with the pool, host-checked): all loads issued before
+        // the first store, which the compiler could not move them across
+        float res[Cfg::FR][Cfg::FC][16];
+        if constexpr (RES) {
+            const __amdgpu_buffer_rsrc_t r_rs = make_rsrc(epi.residual + obase, obytes);
 #pragma unroll
             for (int f = 0; f < Cfg::FR; ++f)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int m = min(m0 + wm * Cfg::WM + frag_out_row(f, e, lane), g.M - 1);
-                    res[j][f][e] = epi.residual[out_base[j] + static_cast<int64_t>(m) * plane];
-                }
+                for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
-        for (int j = 0; j < Cfg::FC; ++j)
-#pragma unroll
-            for (int f = 0; f < Cfg::FR; ++f)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[f][j][e] += res[j][f][e];
-    }
-#pragma unroll
-    for (int j = 0; j < Cfg::FC; ++j)
+                    for (int e = 0; e < 16; ++e)
+                        res[f][j][e] = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(
+                                       r_rs, voff[j] + (f * 32 + 8 * (e >> 2) + (e & 3)) * plane4, 0, 0));
+        }
 #pragma unroll
         for (int f = 0; f < Cfg::FR; ++f)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                float v = acc[f][j][e];
-                if (epi.flags & TBN_EPI_RELU) v = v > 0.0f ? v : 0.0f;
-                if (pool) {
-                    v = fmaxf(v, __shfl_xor(v, 1));
-                    v = fmaxf(v, __shfl_xor(v, 2));
-                }
-                const int m = m0 + wm * Cfg::WM + frag_out_row(f, e, lane);
-                if (m < g.M && valid[j] && (!pool || (lane & 3) == 0))
-                    epi.y[out_base[j] + static_cast<int64_t>(m) * plane] = v;
+            for (int e4 = 0; e4 < 4; ++e4) {
+                // rows of registers 4*e4 .. 4*e4+3: four consecutive channels
+                const int r = wm * Cfg::WM + f * 32 + 8 * e4 + 4 * (lane >> 5);
+                const float4 mv = *reinterpret_cast<const float4*>(epi_lds + r);
+                const float4 bv = *reinterpret_cast<const float4*>(epi_lds + Cfg::BM + r);
+                const float mm[4] = {mv.x, mv.y, mv.z, mv.w};
+                const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
+#pragma unroll
+                for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int e = 4 * e4 + i;
+                        const float a = bts ? bb[i] : 0.0f, b = bts ? 0.0f : bb[i];
+                        float v = (acc[f][j][e] + a) * mm[i] + b;
+                        if constexpr (RES) v += res[f][j][e];
+                        if constexpr (RELU) v = v > 0.0f ? v : 0.0f;
+                        if constexpr (POOL) {
+                            v = fmaxf(v, quad_perm<0xB1>(v));  // partner across the window's columns
+                            v = fmaxf(v, quad_perm<0x4E>(v));  // and rows
+                        }
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), y_rs,
+                                                              voff[j] + (f * 32 + 8 * e4 + i) * plane4, 0, 0);
+                    }
             }
+    };
+    using T = std::true_type;
+    using F = std::false_type;
+    const bool relu = (epi.flags & TBN_EPI_RELU) != 0;
+    if (pool) {
+        if (relu) finish(T{}, T{}, F{});
+        else finish(F{}, T{}, F{});
+    } else if (epi.residual) {
+        if (relu) finish(T{}, F{}, T{});
+        else finish(F{}, F{}, T{});
+    } else {
+        if (relu) finish(T{}, F{}, F{});
+        else finish(F{}, F{}, F{});
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -597,9 +632,8 @@ struct TileChoice {
 };
 
 size_t lds_bytes(const PatchGeom& g, int BM, bool ternary) {
-    const size_t patch = static_cast<size_t>(3) * g.PHi * g.PWi * kPix * 2;
-    const size_t words = static_cast<size_t>(BM) * g.taps * (ternary ? 8 : 4);
-    return 2 * (patch + words) + 2 * sizeof(float) * BM;  // two buffers + epilogue factors
+    const size_t buf = static_cast<size_t>(patch_buffer_elems(g.PHi * g.PWi, BM * g.taps, ternary ? 4 : 2)) * 2;
+    return 2 * buf + 2 * sizeof(float) * BM;  // two buffers + epilogue factors
 }
 
 void fill_patch(PatchGeom& g, const TileChoice& c) {
@@ -715,32 +749,40 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
     return true;
 }
 
-template <class Cfg, bool TERNARY, int TAPS>
+template <class Cfg, bool TERNARY, int TAPS, int MAXI>
 int launch_patch_taps(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
                       const PatchEpi& epi, hipStream_t s) {
     const size_t lds = lds_bytes(g, Cfg::BM, TERNARY);
-    const int items = 4 * g.PHi * g.PWi;
-    if ((items + Cfg::NT - 1) / Cfg::NT > 8 || (Cfg::BM * g.taps + Cfg::NT - 1) / Cfg::NT > 8)
-        return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for the staging registers");
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_patch_kernel<Cfg, TERNARY, TAPS>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
         if (e != hipSuccess) return tbn_hip::fail(TBN_RUNTIME_ERROR, std::string("hipFuncSetAttribute: ") +
                                                                          hipGetErrorString(e));
         attr_set = true;
     }
     const int64_t blocks = static_cast<int64_t>(g.N) * g.tiles_img * ((g.M + Cfg::BM - 1) / Cfg::BM);
-    hipLaunchKernelGGL((conv_patch_kernel<Cfg, TERNARY, TAPS>), dim3(static_cast<unsigned>(blocks)), dim3(Cfg::NT),
-                       lds, s, x, g, w, col_bytes, m_alloc, epi);
+    hipLaunchKernelGGL((conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI>), dim3(static_cast<unsigned>(blocks)),
+                       dim3(Cfg::NT), lds, s, x, g, w, col_bytes, m_alloc, epi);
     return tbn_hip::check_launch(TERNARY ? "conv2d_f32_ternary (patch)" : "conv2d_f32_binary (patch)");
+}
+
+template <class Cfg, bool TERNARY, int TAPS>
+int launch_patch_items(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
+                       const PatchEpi& epi, hipStream_t s) {
+    const int per_thread = (4 * g.PHi * g.PWi + Cfg::NT - 1) / Cfg::NT;
+    const int wper_thread = (Cfg::BM * g.taps + Cfg::NT - 1) / Cfg::NT;
+    if (per_thread > 8 || wper_thread > 8)
+        return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for the staging registers");
+    if (per_thread <= 4) return launch_patch_taps<Cfg, TERNARY, TAPS, 4>(x, g, w, col_bytes, m_alloc, epi, s);
+    return launch_patch_taps<Cfg, TERNARY, TAPS, 8>(x, g, w, col_bytes, m_alloc, epi, s);
 }
 
 template <class Cfg, bool TERNARY>
 int launch_patch(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
                  const PatchEpi& epi, hipStream_t s) {
-    if (g.kh == 3 && g.kw == 3) return launch_patch_taps<Cfg, TERNARY, 9>(x, g, w, col_bytes, m_alloc, epi, s);
-    return launch_patch_taps<Cfg, TERNARY, 0>(x, g, w, col_bytes, m_alloc, epi, s);
+    if (g.kh == 3 && g.kw == 3) return launch_patch_items<Cfg, TERNARY, 9>(x, g, w, col_bytes, m_alloc, epi, s);
+    return launch_patch_items<Cfg, TERNARY, 0>(x, g, w, col_bytes, m_alloc, epi, s);
 }
 
 template <bool TERNARY>
@@ -879,11 +921,15 @@ int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
     g.PW = g.pool ? g.OW / 2 : 0;
     g.VH = g.pool ? 2 * g.PH : g.OH;
     g.VW = g.pool ? 2 * g.PW : g.OW;
-    // staging loads address one image and the conv-layout weights with 32-bit offsets
-    const int64_t image_bytes = static_cast<int64_t>(g.C) * g.H * g.W * 4;
-    const int64_t weight_bytes = (d->m + 7) / 8 * 8 * static_cast<int64_t>(g.chunks) * g.taps * 8;
-    if (image_bytes >= 0xFFFFFFF0LL || weight_bytes >= 0xFFFFFFF0LL)
-        return tbn_hip::fail(TBN_INVALID_SHAPE, "conv image or weights too large for the patch kernel");
+    // the kernel addresses one image (channels padded to whole chunks), the
+    // conv-layout weights (rows padded by a channel tile) and one image's
+    // output planes (likewise) with 32-bit offsets below 2^31, the bit that
+    // marks a masked element
+    const int64_t image_bytes = static_cast<int64_t>(g.chunks) * kChunk * g.H * g.W * 4;
+    const int64_t weight_bytes = ((d->m + 7) / 8 * 8 + 128) * static_cast<int64_t>(g.chunks) * g.taps * 8;
+    const int64_t out_bytes = (d->m + 128) * static_cast<int64_t>(g.pool ? g.PH * g.PW : g.OH * g.OW) * 4;
+    if (image_bytes >= (1LL << 31) || weight_bytes >= (1LL << 31) || out_bytes >= (1LL << 31))
+        return tbn_hip::fail(TBN_INVALID_SHAPE, "conv image, weights or output too large for the patch kernel");
     return TBN_SUCCESS;
 }
 

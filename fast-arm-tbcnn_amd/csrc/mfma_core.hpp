@@ -56,6 +56,30 @@ __device__ __forceinline__ uint32_t upper_halves(uint32_t a, uint32_t b) {
     return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
+// Exact three-way bf16 split of 8 fp32 values (hi + mid + lo = x), branch
+// free: r1 = x - hi is forced to 0 where x == hi, which covers +-inf (whose
+// plain difference is NaN); a NaN input keeps a NaN in hi or r1.
+__device__ __forceinline__ void split8(const float* x, uint4& hi, uint4& mid, uint4& lo) {
+    uint32_t hb[8], mb[8], lb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const uint32_t u = __float_as_uint(x[e]);
+        const float h = __uint_as_float(u & 0xFFFF0000u);
+        const float r1 = (x[e] == h) ? 0.0f : x[e] - h;
+        const uint32_t m = __float_as_uint(r1);
+        const float r2 = r1 - __uint_as_float(m & 0xFFFF0000u);
+        hb[e] = u;
+        mb[e] = m;
+        lb[e] = __float_as_uint(r2);
+    }
+    hi = make_uint4(upper_halves(hb[0], hb[1]), upper_halves(hb[2], hb[3]), upper_halves(hb[4], hb[5]),
+                    upper_halves(hb[6], hb[7]));
+    mid = make_uint4(upper_halves(mb[0], mb[1]), upper_halves(mb[2], mb[3]), upper_halves(mb[4], mb[5]),
+                     upper_halves(mb[6], mb[7]));
+    lo = make_uint4(upper_halves(lb[0], lb[1]), upper_halves(lb[2], lb[3]), upper_halves(lb[4], lb[5]),
+                    upper_halves(lb[6], lb[7]));
+}
+
 struct Split4 {
     uint32_t hi[2], mid[2], lo[2];
 };

@@ -192,3 +192,32 @@ def test_conv_patch_residual_epilogue(dev, orc):
     ref = conv_ref(x, wsign, scale, 1.0, bias, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_BIAS_THEN_SCALE)
     ref = np.maximum(ref + res, 0.0)
     rm.assert_within_tolerance(host(y), ref, K, np.abs(x).max() * 1.5)
+
+
+@pytest.mark.parametrize("case", [(3, 40, 10, 7, 33, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_RELU),
+                                  (2, 40, 11, 9, 70, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_MAXPOOL2X2),
+                                  (2, 64, 8, 8, 200, 1, 1, (2, 2), (0, 0), (1, 1), 0)])
+def test_conv_patch_writes_only_its_output(dev, orc, case):
+    """Masked lanes (rows past M, pixels past the image, pooled-away lanes)
+    store nothing: a guard region after the output keeps its sentinel, and
+    every output element is written (NaN fill replaced)."""
+    import ctypes
+    N, C, H, W, M, kh, kw, stride, pad, dil, flags = case
+    rng = np.random.default_rng(M)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    wbytes = (rng.random((M, C, kh, kw)) < 0.5).astype(np.uint8)
+    scale = rng.uniform(0.5, 1.5, M).astype(np.float32)
+    packed, K_pad, N_pad = pack_conv_weights(wbytes, M, C * kh * kw)
+    d = tbn_hip.conv_desc(N, C, H, W, M, kh, kw, *stride, *pad, *dil)
+    OH, OW = tbn_hip.conv_out_hw(d)
+    oshape = (N, M, OH // 2, OW // 2) if flags & tbn_hip.EPI_MAXPOOL2X2 else (N, M, OH, OW)
+    n_out = int(np.prod(oshape))
+    guard = 1 << 16
+    buf = empty(n_out + guard, torch.float32)
+    buf.fill_(np.nan)
+    buf[n_out:].fill_(-12345.0)
+    tbn_hip.call("tbn_hip_conv2d_f32_binary", P(to_dev(x)), d, P(packed), K_pad, N_pad, P(to_dev(scale)), 1.0, None,
+                 flags, P(buf), None)
+    out = host(buf)
+    assert np.all(out[n_out:] == -12345.0)
+    assert not np.isnan(out[:n_out]).any()
