@@ -4,6 +4,7 @@
 // MFMA rows are the M rows of A (split operand), MFMA columns the N output
 // columns (packed weights, or the fp32 B matrix for tbn::gemm), so each
 // result register row is 32 consecutive columns of C: 128-byte stores.
+#include <algorithm>
 #include <string>
 
 #include "common.hpp"
@@ -54,6 +55,74 @@ struct GemmEpi {
 
 using CfgBig = TileCfg<128, 256, 64, 128, 2>;
 using CfgSmall = TileCfg<64, 64, 32, 32>;
+
+// Raw sums of one K split of the fp32 GEMM: P[m, n].
+struct PartialEpi {
+    float* P;
+    int M, N;
+
+    template <class Cfg>
+    __device__ __forceinline__ void apply(f32x16_t (&acc)[Cfg::FR][Cfg::FC], int row0, int col0,
+                                          int lane) const {
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j) {
+            const int n = col0 + frag_out_col(j, lane);
+            if (n >= N) continue;
+#pragma unroll
+            for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int m = row0 + frag_out_row(i, e, lane);
+                    if (m < M) P[static_cast<int64_t>(m) * N + n] = acc[i][j][e];
+                }
+        }
+    }
+};
+
+// fp32 GEMM with K split over `splits` blocks per tile (shapes with few
+// tiles, e.g. a classifier layer at small batch): block = (split, tile), split
+// s covers k in [s * ksplit, min(K, (s + 1) * ksplit)).
+template <class Cfg>
+__global__ void __launch_bounds__(Cfg::NT, Cfg::WAVES_PER_SIMD)
+gemm_f32_split_kernel(SplitMatrix<Cfg::BR, Cfg::NT> rowl, SplitMatrix<Cfg::BC, Cfg::NT> coll, float* partial,
+                      int M, int N, int K, int ksplit, int tiles_r, int tiles_c) {
+    const int total = tiles_r * tiles_c;
+    const int sp = static_cast<int>(blockIdx.x) / total;
+    int tr, tc;
+    tile_coords_of(static_cast<int>(blockIdx.x) - sp * total, tiles_r, tiles_c, tr, tc);
+    const int k0 = sp * ksplit;
+    const int klen = min(ksplit, K - k0);
+    rowl.base += static_cast<int64_t>(k0) * rowl.s_k;
+    rowl.K = klen;
+    coll.base += static_cast<int64_t>(k0) * coll.s_k;
+    coll.K = klen;
+    const PartialEpi epi{partial + static_cast<int64_t>(sp) * M * N, M, N};
+    mfma_tile_body<Cfg>(rowl, coll, epi, klen, tr, tc);
+}
+
+// C = epilogue(sum of the splits, in split order): the GemmEpi arithmetic
+// with no scale and no bias.
+__global__ void gemm_f32_reduce_kernel(const float* __restrict__ partial, int splits, int M, int N, float alpha,
+                                       const float* __restrict__ cin, int cin_1d, float beta, int flags,
+                                       float* __restrict__ C) {
+    const int64_t total = static_cast<int64_t>(M) * N;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+        float v = partial[i];
+        for (int s = 1; s < splits; ++s) v += partial[static_cast<int64_t>(s) * total + i];
+        v = v * alpha + 0.0f;
+        if (cin) v += beta * (cin_1d ? cin[i % N] : cin[i]);
+        if (flags & TBN_EPI_RELU) v = v > 0.0f ? v : 0.0f;
+        C[i] = v;
+    }
+}
+
+// K splits of the fp32 GEMM: a function of N and K only, so a row's result
+// does not depend on how many rows (the batch) the call has.
+int f32_gemm_splits(int64_t N, int64_t K) {
+    if (K < 512 || N > 4096) return 1;
+    return static_cast<int>(std::min<int64_t>(8, K / 64));
+}
 
 template <class Cfg, class ColL>
 int launch_gemm(const float* A, int64_t lda, int M, int N, int K, const ColL& coll,
@@ -180,6 +249,34 @@ int tbn_hip_gemm_f32(const float* A, const float* B, const float* Cin, int c_is_
                 (Cin && beta != 0.0f) ? Cin : nullptr, beta, c_is_1d, flags};
     const int tiles_r = static_cast<int>(tbn_hip::ceil_div(M, Cfg::BR));
     const int tiles_c = static_cast<int>(tbn_hip::ceil_div(N, Cfg::BC));
+    const int splits = f32_gemm_splits(N, K);
+    if (splits > 1) {
+        // ksplit: a multiple of the K step; the last split may be shorter
+        const int ksplit = static_cast<int>(tbn_hip::ceil_div(tbn_hip::ceil_div(K, splits), 32) * 32);
+        const int used = static_cast<int>(tbn_hip::ceil_div(K, ksplit));
+        hipStream_t s = tbn_hip::stream_of(stream);
+        void* part = nullptr;
+        const size_t bytes = static_cast<size_t>(used) * M * N * sizeof(float);
+        hipError_t e = hipMallocAsync(&part, bytes, s);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            return tbn_hip::fail(e == hipErrorOutOfMemory ? TBN_OUT_OF_MEMORY : TBN_RUNTIME_ERROR,
+                                 std::string("gemm_f32 split-K buffer: ") + hipGetErrorString(e));
+        }
+        hipLaunchKernelGGL((gemm_f32_split_kernel<Cfg>), dim3(used * tiles_r * tiles_c), dim3(Cfg::NT), 0, s, rowl,
+                           coll, static_cast<float*>(part), static_cast<int>(M), static_cast<int>(N),
+                           static_cast<int>(K), ksplit, tiles_r, tiles_c);
+        int rc = tbn_hip::check_launch("gemm_f32 (split)");
+        if (rc == TBN_SUCCESS) {
+            const int blocks = static_cast<int>(std::min<int64_t>(tbn_hip::ceil_div(M * N, 256), 2048));
+            hipLaunchKernelGGL(gemm_f32_reduce_kernel, dim3(blocks), dim3(256), 0, s,
+                               static_cast<const float*>(part), used, static_cast<int>(M), static_cast<int>(N),
+                               alpha, epi.cin, c_is_1d, beta, flags, out);
+            rc = tbn_hip::check_launch("gemm_f32 (split reduce)");
+        }
+        (void)hipFreeAsync(part, s);
+        return rc;
+    }
     hipLaunchKernelGGL((mfma_tile_kernel<Cfg, SplitMatrix<Cfg::BR, Cfg::NT>,
                                          SplitMatrix<Cfg::BC, Cfg::NT>, GemmEpi>),
                        dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, tbn_hip::stream_of(stream), rowl,

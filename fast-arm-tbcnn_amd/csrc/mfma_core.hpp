@@ -318,9 +318,8 @@ struct ProductSchedule<3, 3> {  // split x split: hi*hi, hi*mid, mid*hi, hi*lo, 
 // Maps a linear workgroup id to (tile_r, tile_c): consecutive ids on one XCD
 // (workgroups are dealt round-robin over the 8 XCDs) get neighbouring tiles,
 // walked in groups of 8 tile-rows so operand tiles are reused from L2.
-__device__ __forceinline__ void tile_coords(int tiles_r, int tiles_c, int& tr, int& tc) {
+__device__ __forceinline__ void tile_coords_of(int pid, int tiles_r, int tiles_c, int& tr, int& tc) {
     const int total = tiles_r * tiles_c;
-    int pid = blockIdx.x;
     if (total % 8 == 0) pid = (pid % 8) * (total / 8) + pid / 8;
     constexpr int GROUP = 8;
     const int per_group = GROUP * tiles_c;
@@ -331,10 +330,14 @@ __device__ __forceinline__ void tile_coords(int tiles_r, int tiles_c, int& tr, i
     tr = first + in % rows_in_group;
     tc = in / rows_in_group;
 }
+__device__ __forceinline__ void tile_coords(int tiles_r, int tiles_c, int& tr, int& tc) {
+    tile_coords_of(static_cast<int>(blockIdx.x), tiles_r, tiles_c, tr, tc);
+}
 
+// One block's tile (tr, tc) over K: operands staged through LDS in BK steps.
 template <class Cfg, class RowL, class ColL, class Epi>
-__global__ void __launch_bounds__(Cfg::NT, Cfg::WAVES_PER_SIMD)
-mfma_tile_kernel(RowL rowl, ColL coll, Epi epi, int K, int tiles_r, int tiles_c) {
+__device__ __forceinline__ void mfma_tile_body(const RowL& rowl, const ColL& coll, const Epi& epi, int K, int tr,
+                                               int tc) {
     __shared__ __attribute__((aligned(16))) uint16_t lds_r[RowL::PIECES * Cfg::BR * LDS_ROW];
     __shared__ __attribute__((aligned(16))) uint16_t lds_c[ColL::PIECES * Cfg::BC * LDS_ROW];
     using Sched = ProductSchedule<RowL::PIECES, ColL::PIECES>;
@@ -344,8 +347,6 @@ mfma_tile_kernel(RowL rowl, ColL coll, Epi epi, int K, int tiles_r, int tiles_c)
     const int wave = tid >> 6;
     const int wr = wave / Cfg::WAVES_C;
     const int wc = wave % Cfg::WAVES_C;
-    int tr, tc;
-    tile_coords(tiles_r, tiles_c, tr, tc);
     const int r0 = tr * Cfg::BR;
     const int c0 = tc * Cfg::BC;
 
@@ -405,6 +406,14 @@ mfma_tile_kernel(RowL rowl, ColL coll, Epi epi, int K, int tiles_r, int tiles_c)
     }
 
     epi.template apply<Cfg>(acc, r0 + wr * Cfg::WR, c0 + wc * Cfg::WC, lane);
+}
+
+template <class Cfg, class RowL, class ColL, class Epi>
+__global__ void __launch_bounds__(Cfg::NT, Cfg::WAVES_PER_SIMD)
+mfma_tile_kernel(RowL rowl, ColL coll, Epi epi, int K, int tiles_r, int tiles_c) {
+    int tr, tc;
+    tile_coords(tiles_r, tiles_c, tr, tc);
+    mfma_tile_body<Cfg>(rowl, coll, epi, K, tr, tc);
 }
 
 // Row / column of register e of fragment (i, j) relative to the wave tile.

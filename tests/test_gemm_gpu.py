@@ -329,6 +329,31 @@ def test_gemm_f32_matches_blocked_reference(dev, orc):
                                    np.abs(A).max() * np.abs(B).max())
 
 
+def test_gemm_f32_split_k(dev, orc):
+    """K split over blocks (K >= 512, N <= 4096): 2-D addend, ReLU, transposed
+    operands and a K that leaves a short last split; rows are bit-identical
+    whatever the number of rows (the split count depends on N and K only)."""
+    rng = np.random.default_rng(22)
+    for (M, K, N, ta, tb, relu) in [(33, 600, 70, True, False, True), (5, 1030, 257, False, True, False),
+                                     (64, 512, 1000, False, True, True)]:
+        A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
+        B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
+        c2 = rng.standard_normal((M, N)).astype(np.float32)
+        out = empty((M, N), torch.float32)
+        flags = tbn_hip.EPI_RELU if relu else 0
+        tbn_hip.call("tbn_hip_gemm_f32", P(to_dev(A)), P(to_dev(B)), P(to_dev(c2)), 0, M, K, N, 1.5, -0.5,
+                     int(ta), int(tb), flags, P(out), None)
+        ref = 1.5 * ((A.T if ta else A).astype(np.float64) @ (B.T if tb else B).astype(np.float64)) - 0.5 * c2
+        if relu:
+            ref = np.maximum(ref, 0.0)
+        rm.assert_within_tolerance(host(out), ref, K, np.abs(A).max() * np.abs(B).max())
+        if not ta:
+            few = empty((2, N), torch.float32)
+            tbn_hip.call("tbn_hip_gemm_f32", P(to_dev(A[3:5].copy())), P(to_dev(B)), P(to_dev(c2[3:5].copy())), 0,
+                         2, K, N, 1.5, -0.5, 0, int(tb), flags, P(few), None)
+            assert np.array_equal(host(few), host(out)[3:5])
+
+
 def test_gemm_error_codes(dev):
     packed = empty(64, torch.uint8)
     A = empty((4, 64), torch.float32)
