@@ -48,16 +48,76 @@ __global__ void maxpool2d_kernel(const float* __restrict__ x, int64_t planes, in
     }
 }
 
+// The 3x3 / stride 2 / pad 1 pool (ResNet stems): a thread walks one output
+// column down a band of rows.  Each input row's 3-wide maximum (a float2 at
+// 2*ow and a float at 2*ow - 1) serves the two output rows that share it.
+// Taking the running maximum of the row maxima in row order, each one a
+// running maximum in column order, keeps the reference's first-wins result
+// (which of -0 / +0 is kept, NaN ignored).
+__device__ __forceinline__ float first_max(float m, float v) { return m < v ? v : m; }
+
+template <bool VEC2>
+__global__ void __launch_bounds__(256) maxpool3x3s2_kernel(const float* __restrict__ x, int H, int W, int OH, int OW,
+                                                           int band, float* __restrict__ y) {
+    const int64_t plane = blockIdx.x;
+    const int ow = static_cast<int>(blockIdx.y) * 64 + (threadIdx.x & 63);
+    const int oh0 = (static_cast<int>(blockIdx.z) * 4 + (threadIdx.x >> 6)) * band;
+    if (ow >= OW || oh0 >= OH) return;
+    const int oh1 = min(OH, oh0 + band);
+    const float* src = x + plane * H * W;
+    float* dst = y + plane * OH * OW + ow;
+    const int c = 2 * ow;
+    auto row_max = [&](int ih) {
+        float m = -INFINITY;
+        if (ih < 0 || ih >= H) return m;
+        const float* r = src + ih * W;
+        if (c >= 1) m = first_max(m, r[c - 1]);
+        if (VEC2 && c + 1 < W) {
+            const float2 v = *reinterpret_cast<const float2*>(r + c);
+            m = first_max(m, v.x);
+            m = first_max(m, v.y);
+        } else {
+            if (c < W) m = first_max(m, r[c]);
+            if (c + 1 < W) m = first_max(m, r[c + 1]);
+        }
+        return m;
+    };
+    float top = row_max(2 * oh0 - 1);
+    for (int oh = oh0; oh < oh1; ++oh) {
+        const float mid = row_max(2 * oh);
+        const float bot = row_max(2 * oh + 1);
+        float m = first_max(-INFINITY, top);
+        m = first_max(m, mid);
+        m = first_max(m, bot);
+        dst[static_cast<int64_t>(oh) * OW] = m;
+        top = bot;
+    }
+}
+
 // tbn::global_avgpool2d (pooling.cpp:184-216): one thread per plane, summing
 // in memory order so the result matches the sequential reference bit for bit.
-__global__ void global_avgpool_kernel(const float* __restrict__ x, int64_t planes, int64_t hw,
-                                      float* __restrict__ y) {
-    const int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (p >= planes) return;
-    const float* src = x + p * hw;
+__global__ void __launch_bounds__(256) global_avgpool_kernel(const float* __restrict__ x, int64_t planes,
+                                                              int64_t hw, float* __restrict__ y) {
+    // a block owns 64 consecutive planes (contiguous in memory); each chunk
+    // of 64 positions of all 64 planes is staged through LDS with coalesced
+    // loads, then thread p adds its plane's values in memory order
+    __shared__ float tile[64][65];
+    const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int np = static_cast<int>(planes - p0 < 64 ? planes - p0 : 64);
+    const int tid = threadIdx.x;
     float sum = 0.0f;
-    for (int64_t i = 0; i < hw; ++i) sum += src[i];
-    y[p] = sum / static_cast<float>(hw);
+    for (int64_t c0 = 0; c0 < hw; c0 += 64) {
+        const int cl = static_cast<int>(hw - c0 < 64 ? hw - c0 : 64);
+        for (int idx = tid; idx < np * 64; idx += 256) {
+            const int pl = idx >> 6, i = idx & 63;
+            if (i < cl) tile[pl][i] = x[(p0 + pl) * hw + c0 + i];
+        }
+        __syncthreads();
+        if (tid < np)
+            for (int i = 0; i < cl; ++i) sum += tile[tid][i];
+        __syncthreads();
+    }
+    if (tid < np) y[p0 + tid] = sum / static_cast<float>(hw);
 }
 
 __global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, int64_t outer,
@@ -159,6 +219,21 @@ int tbn_hip_maxpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w
     TBN_REQUIRE(x != nullptr, TBN_INVALID_ARGUMENT, "null pointer");
     TBN_DEVICE_GUARD();
     TBN_REQUIRE(h * w < (1LL << 31) && OH * OW < (1LL << 31), TBN_INVALID_SHAPE, "pooling plane too large");
+    if (kh == 3 && kw == 3 && sh == 2 && sw == 2 && ph == 1 && pw == 1 && dh == 1 && dw == 1 &&
+        n * c < (1LL << 31) && tbn_hip::ceil_div(OW, 64) <= 65535) {
+        const int64_t band = std::min<int64_t>(16, tbn_hip::ceil_div(OH, 4));
+        const dim3 grid(static_cast<unsigned>(n * c), static_cast<unsigned>(tbn_hip::ceil_div(OW, 64)),
+                        static_cast<unsigned>(tbn_hip::ceil_div(OH, 4 * band)));
+        TBN_REQUIRE(grid.z <= 65535, TBN_INVALID_SHAPE, "pooling input too large");
+        const bool vec2 = (w % 2 == 0) && (reinterpret_cast<uintptr_t>(x) % 8 == 0);
+        if (vec2)
+            hipLaunchKernelGGL(maxpool3x3s2_kernel<true>, grid, dim3(256), 0, tbn_hip::stream_of(stream), x, int(h),
+                               int(w), int(OH), int(OW), int(band), y);
+        else
+            hipLaunchKernelGGL(maxpool3x3s2_kernel<false>, grid, dim3(256), 0, tbn_hip::stream_of(stream), x, int(h),
+                               int(w), int(OH), int(OW), int(band), y);
+        return tbn_hip::check_launch("maxpool2d");
+    }
     hipLaunchKernelGGL(maxpool2d_kernel,
                        dim3(static_cast<unsigned>(tbn_hip::ceil_div(OH * OW, kThreads)),
                             static_cast<unsigned>(std::min<int64_t>(n * c, 65535))),
@@ -174,7 +249,7 @@ int tbn_hip_global_avgpool2d(const float* x, int64_t n, int64_t c, int64_t h, in
     if (n * c == 0) return tbn_hip::ok();
     TBN_REQUIRE(x && y, TBN_INVALID_ARGUMENT, "null pointer");
     TBN_DEVICE_GUARD();
-    hipLaunchKernelGGL(global_avgpool_kernel, dim3(tbn_hip::ceil_div(n * c, 64)), dim3(64), 0,
+    hipLaunchKernelGGL(global_avgpool_kernel, dim3(tbn_hip::ceil_div(n * c, 64)), dim3(256), 0,
                        tbn_hip::stream_of(stream), x, n * c, h * w, y);
     return tbn_hip::check_launch("global_avgpool2d");
 }

@@ -39,6 +39,26 @@ def test_maxpool_known_answer_and_resnet_shape(dev, orc):
     assert np.array_equal(gpu_maxpool(x, (3, 3), (2, 2), (1, 1)), orc.maxpool2d(x, (3, 3), (2, 2), (1, 1)))
 
 
+@pytest.mark.parametrize("shape,ceil_mode", [((2, 3, 9, 7), False), ((1, 2, 8, 8), True), ((1, 2, 200, 300), False),
+                                              ((2, 2, 5, 130), True)])
+def test_maxpool_3x3_stride2_bitwise(dev, orc, shape, ceil_mode):
+    """The specialised 3x3 / stride 2 / pad 1 path (row maxima shared by
+    neighbouring output rows): bit-identical to the reference's first-wins
+    running max, including which zero sign survives, NaN taps, infinities,
+    odd widths, ceil mode and planes wider than 64 outputs / taller than 64."""
+    rng = np.random.default_rng(shape[3])
+    x = rng.standard_normal(shape).astype(np.float32)
+    x[..., ::3, 1::4] = 0.0
+    x[..., 1::3, ::4] = -0.0
+    x[..., 2::5, 2::3] = np.nan
+    x[0, 0, 0, :3] = np.inf
+    x[0, -1, -1, -3:] = -np.inf
+    x[-1, -1, :, :] = np.nan
+    got = gpu_maxpool(x, (3, 3), (2, 2), (1, 1), ceil_mode)
+    ref = orc.maxpool2d(x, (3, 3), (2, 2), (1, 1), ceil_mode=ceil_mode)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 @pytest.mark.parametrize("shape", [(1, 2, 4, 4), (32, 512, 7, 7), (3, 5, 1, 1)])
 def test_global_avgpool_bit_exact(dev, orc, shape):
     rng = np.random.default_rng(3)
