@@ -215,6 +215,8 @@ int tbn_hip_conv2d_f32(const float* x, const tbn_conv2d_desc* desc, const float*
     if (g.Q == 0) return tbn_hip::ok();
     TBN_REQUIRE(x && w && y, TBN_INVALID_ARGUMENT, "null pointer");
     TBN_DEVICE_GUARD();
+    if (tbn_hip::conv_stem_supported(desc, flags))
+        return tbn_hip::conv_stem_run(x, desc, w, bias, flags, y, tbn_hip::stream_of(stream));
     ConvEpi epi{y, int(desc->m), g, nullptr, 1.0f, bias, nullptr, flags};
     hipStream_t s = tbn_hip::stream_of(stream);
     const int m = int(desc->m);

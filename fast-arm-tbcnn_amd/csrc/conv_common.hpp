@@ -147,4 +147,9 @@ bool conv_patch_supported(const tbn_conv2d_desc* desc);
 int conv_patch_from_reference(int weights, const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed,
                               int64_t K_pad, int64_t N_pad, const float* scale, float alpha, const float* bias,
                               const float* residual, int flags, float* y, hipStream_t s);
+// The fp32 stem path (conv_stem.hip): few input channels, 7-wide kernels,
+// stride 2 along W, <= 64 output channels, bias + optional ReLU.
+bool conv_stem_supported(const tbn_conv2d_desc* desc, int flags);
+int conv_stem_run(const float* x, const tbn_conv2d_desc* desc, const float* w, const float* bias, int flags,
+                  float* y, hipStream_t s);
 }  // namespace tbn_hip

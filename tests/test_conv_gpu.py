@@ -95,7 +95,10 @@ def test_conv_ternary(dev, orc):
 
 
 @pytest.mark.parametrize("case", [(2, 3, 64, 64, 64, 7, 7, 2, 3, 0), (1, 1, 28, 28, 6, 5, 5, 1, 0, 4),
-                                  (2, 8, 9, 9, 40, 3, 3, 1, 1, 1)])
+                                  (2, 8, 9, 9, 40, 3, 3, 1, 1, 1),
+                                  # the stem kernel: partial tiles, M < 64, ReLU
+                                  (3, 3, 70, 50, 64, 7, 7, 2, 3, 1), (1, 3, 33, 37, 40, 7, 7, 2, 3, 0),
+                                  (2, 3, 224, 224, 64, 7, 7, 2, 3, 1)])
 def test_conv_f32(dev, orc, case):
     """fp32 layers (ResNet stem 7x7/2, LeNet with quantization off)."""
     N, C, H, W, M, kh, kw, s, p, flags = case
@@ -221,3 +224,31 @@ def test_conv_patch_writes_only_its_output(dev, orc, case):
     out = host(buf)
     assert np.all(out[n_out:] == -12345.0)
     assert not np.isnan(out[:n_out]).any()
+
+
+def test_conv_f32_stem_inf_stays_local(dev, orc):
+    """An infinite input pixel reaches only the outputs whose 7x7 window
+    holds it: the stem kernel's padded tap columns (kw = 7 of 8) and padded
+    k rows carry zero weights and zero inputs, never inf * 0."""
+    N, C, H, W, M = 1, 3, 40, 40, 64
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    w = (rng.standard_normal((M, C, 7, 7)) * 0.1).astype(np.float32)
+    b = np.zeros(M, np.float32)
+    ih, iw = 21, 18
+    x[0, 1, ih, iw] = np.inf
+    d = tbn_hip.conv_desc(N, C, H, W, M, 7, 7, 2, 2, 3, 3)
+    OH, OW = tbn_hip.conv_out_hw(d)
+    y = empty((N, M, OH, OW), torch.float32)
+    tbn_hip.call("tbn_hip_conv2d_f32", P(to_dev(x)), d, P(to_dev(w)), P(to_dev(b)), 0, P(y), None)
+    out = host(y)
+    oh = np.arange(OH)[:, None]
+    ow = np.arange(OW)[None, :]
+    touched = (np.abs(2 * oh - 3 + 3 - ih) <= 3) & (np.abs(2 * ow - 3 + 3 - iw) <= 3)
+    assert np.all(np.isfinite(out[:, :, ~touched]))
+    assert not np.any(np.isfinite(out[:, :, touched]))
+    x0 = x.copy()
+    x0[0, 1, ih, iw] = 0.0
+    ref = orc.conv2d_f64(x0, w, b, (2, 2), (3, 3))
+    rm.assert_within_tolerance(np.where(touched, 0.0, out), np.where(touched, 0.0, ref), C * 49,
+                               np.abs(x0).max() * np.abs(w).max())
