@@ -1,23 +1,27 @@
 // fp32 convolution for few input channels and wide kernels: the ResNet stem
 // (3 -> 64 channels, 7x7, stride 2).  The im2col engine of conv.hip gathers
-// every (pixel, tap) element from global memory and splits it anew; here a
-// block stages the input patch of a 16 x 16 output tile in LDS once and
-// builds each MFMA column fragment from it.
+// every (pixel, tap) element from global memory and splits it anew; here each
+// wave stages the input patch of its output tile in LDS once, split on the
+// way into three bf16 planes (hi + mid + lo = x exactly), and reads every
+// column fragment from those planes.
 //
 // K is ordered k = (r * C + c) * 8 + s: tap row r, channel c, tap column s
 // padded from kw to 8.  A lane's 8 consecutive k of a k-slice are then 8
-// consecutive input columns of one row of one channel, i.e. four float2
-// reads from the patch, split into three bf16 planes in registers (hi + mid +
-// lo = x exactly).  The weights are split the same way once per call into a
-// [plane][64 rows][K_pad] bf16 table (zero outside M, kh, kw) that each block
-// keeps in LDS for all the tiles it takes (the grid is persistent, one block
-// per CU).  Products per k-slice: w_hi x_hi, w_hi x_mid, w_mid x_hi,
-// w_hi x_lo, w_mid x_mid, w_lo x_hi (the terms below 2^-24 relative dropped),
-// accumulated in fp32.
+// consecutive input columns of one row of one channel: four dword reads per
+// plane (the run starts at an even column).  Column 8 of the run (s = kw)
+// and k past kh * C have zero weights; their inputs are zeroed too, so an
+// infinite pixel there cannot turn into NaN.  Products per k-slice: w_hi x_hi,
+// w_hi x_mid, w_mid x_hi, w_hi x_lo, w_mid x_mid, w_lo x_hi (the terms below
+// 2^-24 relative dropped), accumulated in fp32.
 //
-// Block: 4 waves, all 64 output channels x a 16 x 16 tile of output pixels;
-// wave w owns tile rows 4w .. 4w+3 (two 32-pixel column fragments).  The next
-// tile's patch is loaded into registers while the current one is computed.
+// A block (persistent, one per CU) splits the weights into a [plane][64
+// rows][K_pad] bf16 table in LDS once; after that its 8 waves work without
+// barriers: each wave takes output tiles of all 64 channels x 4 rows x 16
+// columns (two 32-pixel column fragments) with a patch buffer of its own, and
+// loads its next tile's patch into registers while computing the current
+// one.  Tiles are dealt wave-major across blocks (wave w of every block
+// before wave w + 1 of any), so the tiles beyond a whole round land on
+// different SIMDs.
 #include <algorithm>
 #include <mutex>
 #include <string>
@@ -28,19 +32,16 @@ namespace {
 
 using namespace tbnk;
 
-constexpr int kRows = 64;        // output channels per block (M <= 64)
-constexpr int kTile = 16;        // output tile: 16 x 16 pixels
-constexpr int kMaxPatch = 6144;  // floats of the staged input patch
-constexpr int kStage = kMaxPatch / 256;
+constexpr int kRows = 64;    // output channels per tile (M <= 64)
+constexpr int kTileH = 4;    // output tile: 4 rows x 16 columns (one wave)
+constexpr int kTileW = 16;
+constexpr int kWaves = 8;    // waves per block
 constexpr uint32_t kOutside = 0x80000000u;
 
 struct StemGeom {
-    int N, C, H, W, M;
-    int kh, kw, sh, sw, ph, pw, dh;
+    int N, H, W, M;
+    int ph, pw;
     int OH, OW;
-    int K_pad;         // 16 * slices
-    int prows, pitch;  // staged patch: rows, row pitch in floats (a multiple of 4)
-    int patch;         // C * prows * pitch
     int tiles_w, tiles_img, tiles;
     int relu;
 };
@@ -50,121 +51,204 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                              0x00020000);
 }
 
-// w [M, C, kh, kw] fp32 -> [3][64][K_pad] bf16 planes in the kernel's K order.
-__global__ void stem_weights_kernel(const float* __restrict__ w, StemGeom g, uint16_t* __restrict__ out) {
-    const int idx = blockIdx.x * 256 + threadIdx.x;
-    if (idx >= kRows * g.K_pad) return;
-    const int m = idx / g.K_pad, k = idx - m * g.K_pad;
-    const int k8 = k >> 3, s = k & 7;
-    const int r = k8 / g.C, c = k8 - r * g.C;
-    float v = 0.0f;
-    if (m < g.M && r < g.kh && s < g.kw) v = w[((static_cast<int64_t>(m) * g.C + c) * g.kh + r) * g.kw + s];
-    const uint32_t u = __float_as_uint(v);
-    const float h = __uint_as_float(u & 0xFFFF0000u);
-    const float r1 = (v == h) ? 0.0f : v - h;
-    const uint32_t mb = __float_as_uint(r1);
-    const float r2 = r1 - __uint_as_float(mb & 0xFFFF0000u);
-    const int64_t plane = static_cast<int64_t>(kRows) * g.K_pad;
-    out[idx] = static_cast<uint16_t>(u >> 16);
-    out[plane + idx] = static_cast<uint16_t>(mb >> 16);
-    out[2 * plane + idx] = static_cast<uint16_t>(__float_as_uint(r2) >> 16);
+// Exact three-way bf16 split of two values, packed as (x0, x1) bf16 pairs.
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+    float x[2] = {x0, x1};
+    uint32_t hb[2], mb[2], lb[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const uint32_t u = __float_as_uint(x[e]);
+        const float h = __uint_as_float(u & 0xFFFF0000u);
+        const float r1 = (x[e] == h) ? 0.0f : x[e] - h;
+        const uint32_t m = __float_as_uint(r1);
+        hb[e] = u;
+        mb[e] = m;
+        lb[e] = __float_as_uint(r1 - __uint_as_float(m & 0xFFFF0000u));
+    }
+    hi = upper_halves(hb[0], hb[1]);
+    mid = upper_halves(mb[0], mb[1]);
+    lo = upper_halves(lb[0], lb[1]);
 }
 
-template <int KW, int SLICES>
-__global__ void __launch_bounds__(256) stem_conv_kernel(const float* __restrict__ x, StemGeom g,
-                                                        const uint16_t* __restrict__ wsplit,
-                                                        const float* __restrict__ bias, float* __restrict__ y) {
-    constexpr int K_PAD = 16 * SLICES;
-    constexpr int KROW = K_PAD + 8;  // bf16 per LDS weight row: conflict-free 16-byte reads
+// Compile-time geometry: C channels, KH x KW taps, stride SH x SW, no
+// dilation (pads, image size, batch and M <= 64 are runtime).
+template <int C_, int KH_, int KW_, int SH_, int SW_>
+struct StemShape {
+    static constexpr int C = C_, KH = KH_, KW = KW_, SH = SH_, SW = SW_;
+    static constexpr int SLICES = (KH * C + 1) / 2;                    // k8 groups: KH * C, two per slice
+    static constexpr int K_PAD = 16 * SLICES;
+    static constexpr int KROW = K_PAD + 8;                             // LDS weight row: conflict-free reads
+    static constexpr int PROWS = (kTileH - 1) * SH + KH;               // a wave's patch rows
+    static constexpr int PITCH = ((kTileW - 1) * SW + 8 + 3) / 4 * 4;  // row pitch (elements)
+    static constexpr int PATCH = C * PROWS * PITCH;
+    static constexpr int PAIRS = PATCH / 2;                            // dwords per plane
+    static constexpr int PER = (PAIRS + 63) / 64;                      // pairs staged per lane
+    static constexpr size_t LDS = static_cast<size_t>(3) * kRows * KROW * 2 + kRows * 4 +
+                                  static_cast<size_t>(kWaves) * 3 * PAIRS * 4;
+    static_assert(KW <= 8 && SW % 2 == 0 && PITCH % 4 == 0, "a lane's run: 8 columns from an even one");
+    static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+template <class S>
+__global__ void __launch_bounds__(64 * kWaves) stem_conv_kernel(const float* __restrict__ x, StemGeom g,
+                                                                const float* __restrict__ w,
+                                                                const float* __restrict__ bias,
+                                                                float* __restrict__ y) {
+    constexpr int SLICES = S::SLICES, KW = S::KW, KROW = S::KROW, K_PAD = S::K_PAD;
     extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
     uint16_t* wl = lds;                                             // [3][64][KROW]
     float* bl = reinterpret_cast<float*>(lds + 3 * kRows * KROW);  // [64] bias
-    float* patch = bl + kRows;                                      // [C][prows][pitch]
+    const int tid_all = threadIdx.x;
+    const int lane = tid_all & 63;
+    // wave-uniform (an SGPR), so the tiles, and with them the buffer
+    // resources, are too: a resource in VGPRs would loop every load and store
+    const int wave = __builtin_amdgcn_readfirstlane(tid_all >> 6);
+    constexpr int pplane = S::PAIRS;
+    uint32_t* pl = reinterpret_cast<uint32_t*>(bl + kRows) + wave * 3 * pplane;  // [3 planes][C][PROWS][PITCH]
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-
-    // ---- weights and bias, once per block ----
-    constexpr int kChunks = 3 * kRows * (K_PAD / 8);  // 16-byte pieces
-#pragma unroll 8
-    for (int i = tid; i < kChunks; i += 256) {
-        const int row = i / (K_PAD / 8), q = i - row * (K_PAD / 8);
-        *reinterpret_cast<uint4*>(wl + row * KROW + q * 8) =
-            *reinterpret_cast<const uint4*>(wsplit + static_cast<int64_t>(row) * K_PAD + q * 8);
-    }
-    if (tid < kRows) bl[tid] = (bias && tid < g.M) ? bias[tid] : 0.0f;
-
-    // ---- patch staging: element e = tid + 256 i of [C][prows][pitch] ----
-    // (c, row, col) of each element is the same for every tile: packed once
-    uint32_t coord[kStage];
+    // ---- weights, once per block: item = (row m, k8 = r * C + c), the run
+    //      w[m, c, r, 0..kw) split into the three planes (zero past M, KH, KW) ----
+    {
+        constexpr int kGroups = K_PAD / 8;
+        constexpr int kItems = kRows * kGroups;
+        constexpr int kPer = (kItems + 64 * kWaves - 1) / (64 * kWaves);
+        float v[kPer][8];
 #pragma unroll
-    for (int i = 0; i < kStage; ++i) {
-        const int e = tid + 256 * i;
-        const int c = e / (g.prows * g.pitch);
-        const int rem = e - c * g.prows * g.pitch;
-        const int pr = rem / g.pitch;
-        const int pc = rem - pr * g.pitch;
-        coord[i] = (e < g.patch) ? (static_cast<uint32_t>(c) << 24) | (static_cast<uint32_t>(pr) << 12) | pc
-                                 : 0xFFFFFFFFu;
+        for (int i = 0; i < kPer; ++i) {
+            const int item = tid_all + i * 64 * kWaves;
+            const int m = item / kGroups, k8 = item - m * kGroups;
+            const int r = k8 / S::C, c = k8 - r * S::C;
+            const bool ok = item < kItems && m < g.M && r < S::KH;
+            const float* src =
+                w + ((static_cast<int64_t>(ok ? m : 0) * S::C + (ok ? c : 0)) * S::KH + (ok ? r : 0)) * KW;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) v[i][q] = (ok && q < KW) ? src[q] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            const int item = tid_all + i * 64 * kWaves;
+            if (item < kItems) {
+                const int m = item / kGroups, k8 = item - m * kGroups;
+                uint4 hi, mid, lo;
+                split8(v[i], hi, mid, lo);
+                uint16_t* d = wl + m * KROW + k8 * 8;
+                *reinterpret_cast<uint4*>(d) = hi;
+                *reinterpret_cast<uint4*>(d + kRows * KROW) = mid;
+                *reinterpret_cast<uint4*>(d + 2 * kRows * KROW) = lo;
+            }
+        }
     }
+    if (tid_all < kRows) bl[tid_all] = (bias && tid_all < g.M) ? bias[tid_all] : 0.0f;
+    __syncthreads();  // the only block-wide barrier
+
+    // ---- patch staging: pair p = lane + 64 i = elements 2p, 2p + 1 of
+    //      [C][PROWS][PITCH] (the pitch is even: both in one row) ----
     const uint32_t HW = static_cast<uint32_t>(g.H) * g.W;
-    float stage[kStage];
+    float stage[S::PER][2];
     auto tile_origin = [&](int t, int& n, int& oh0, int& ow0) {
         n = t / g.tiles_img;
         const int r = t - n * g.tiles_img;
         const int th = r / g.tiles_w;
-        oh0 = th * kTile;
-        ow0 = (r - th * g.tiles_w) * kTile;
+        oh0 = th * kTileH;
+        ow0 = (r - th * g.tiles_w) * kTileW;
     };
     auto load_patch = [&](int t) {
         int n, oh0, ow0;
         tile_origin(t, n, oh0, ow0);
-        const int ih0 = oh0 * g.sh - g.ph, iw0 = ow0 * g.sw - g.pw;
+        const int ih0 = oh0 * S::SH - g.ph, iw0 = ow0 * S::SW - g.pw;
         // image n: C * H * W floats (host-checked below 2^31 bytes); outside -> 0
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(x + static_cast<int64_t>(n) * g.C * HW, g.C * HW * 4);
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(x + static_cast<int64_t>(n) * S::C * HW, S::C * HW * 4);
 #pragma unroll
-        for (int i = 0; i < kStage; ++i) {
-            const uint32_t cd = coord[i];
-            const int c = cd >> 24, pr = (cd >> 12) & 0xFFF, pc = cd & 0xFFF;
+        for (int i = 0; i < S::PER; ++i) {
+            const int e = 2 * (lane + 64 * i);
+            const int c = e / (S::PROWS * S::PITCH);
+            const int rem = e - c * (S::PROWS * S::PITCH);
+            const int pr = rem / S::PITCH;
+            const int pc = rem - pr * S::PITCH;
             const int ih = ih0 + pr, iw = iw0 + pc;
-            const bool ok = cd != 0xFFFFFFFFu && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
-                            static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
-            const uint32_t off = ok ? (static_cast<uint32_t>(c) * HW + ih * g.W + iw) * 4 : kOutside;
-            stage[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+            const bool row_ok = e < S::PATCH && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H);
+            const uint32_t base = (static_cast<uint32_t>(c) * HW + ih * g.W + iw) * 4;
+            const bool ok0 = row_ok && static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
+            const bool ok1 = row_ok && static_cast<unsigned>(iw + 1) < static_cast<unsigned>(g.W);
+            stage[i][0] =
+                __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, ok0 ? base : kOutside, 0, 0));
+            stage[i][1] =
+                __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, ok1 ? base + 4 : kOutside, 0, 0));
         }
     };
     auto store_patch = [&]() {
 #pragma unroll
-        for (int i = 0; i < kStage; ++i)
-            if (tid + 256 * i < g.patch) patch[tid + 256 * i] = stage[i];
+        for (int i = 0; i < S::PER; ++i) {
+            const int p = lane + 64 * i;
+            if (p < S::PAIRS) {
+                uint32_t hi, mid, lo;
+                split2(stage[i][0], stage[i][1], hi, mid, lo);
+                pl[p] = hi;
+                pl[pplane + p] = mid;
+                pl[2 * pplane + p] = lo;
+            }
+        }
     };
 
-    // ---- this lane's fragment pixels and k-slice offsets ----
+    // ---- this lane's fragment pixels (in dwords of a plane) ----
     const int kg = lane >> 5;
-    int pix[2];  // patch offset of the lane's pixel in fragment j (tap (0, 0), channel 0)
+    int pix[2];  // fragment j: tile rows 2j (lanes 0-15) and 2j + 1 (lanes 16-31)
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int tr = 4 * wave + 2 * j + ((lane & 31) >> 4);
+        const int tr = 2 * j + ((lane & 31) >> 4);
         const int tc = lane & 15;
-        pix[j] = tr * g.sh * g.pitch + tc * g.sw;
+        pix[j] = (tr * S::SH * S::PITCH + tc * S::SW) / 2;
     }
-    int koff[SLICES];  // patch offset of k8 = 2 t + kg: row r * dh of channel c; -1 past kh * C
-#pragma unroll
-    for (int t = 0; t < SLICES; ++t) {
-        const int k8 = 2 * t + kg;
-        const int r = k8 / g.C, c = k8 - r * g.C;
-        koff[t] = (r < g.kh) ? (c * g.prows + r * g.dh) * g.pitch : -1;
-    }
+    // k8 = 2 sl + kg: tap row r, channel c at dword offset koff(sl, kg) of the patch
+    auto koff = [&](int sl, int k) {
+        const int k8 = 2 * sl + k;
+        const int r = k8 / S::C, c = k8 - r * S::C;
+        return (c * S::PROWS + r) * S::PITCH / 2;
+    };
     const int wrow = lane & 31;
 
-    int t = blockIdx.x;
+    // Fragments of slice sl: weights a[plane][f] and inputs b[plane][j]; past
+    // KH * C (the last slice, kg = 1 when KH * C is odd) the inputs are zeroed.
+    auto read_slice = [&](int sl, u32x4_t (&a)[3][2], u32x4_t (&b)[3][2]) {
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int f = 0; f < 2; ++f)
+                a[p][f] = *reinterpret_cast<const u32x4_t*>(wl + (p * kRows + f * 32 + wrow) * KROW + sl * 16 +
+                                                            kg * 8);
+        const bool last_odd = (2 * sl + 1 >= S::KH * S::C);
+        const int ko0 = koff(sl, 0);
+        const int ko1 = last_odd ? ko0 : koff(sl, 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t* src = pl + pix[j] + (kg ? ko1 : ko0);
+#pragma unroll
+            for (int p = 0; p < 3; ++p) {
+                u32x4_t v;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) v[q] = src[p * pplane + q];
+                if (KW == 7) v[3] &= 0x0000FFFFu;  // s = 7
+                if (last_odd) {
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) v[q] = kg ? 0u : v[q];
+                }
+                b[p][j] = v;
+            }
+        }
+    };
+
+    // tiles wave-major: wave w of block b takes w * gridDim.x + b, then steps
+    // by all the waves of the grid
+    const int stride = kWaves * static_cast<int>(gridDim.x);
+    int t = wave * static_cast<int>(gridDim.x) + static_cast<int>(blockIdx.x);
     if (t < g.tiles) load_patch(t);
-    for (; t < g.tiles; t += gridDim.x) {
+    for (; t < g.tiles; t += stride) {
         store_patch();
-        __syncthreads();
-        const int tn = t + gridDim.x;
-        if (tn < g.tiles) load_patch(tn);
+        // a wave's own LDS operations complete in order; the fences keep the
+        // compiler from moving the fragment reads above these writes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (t + stride < g.tiles) load_patch(t + stride);
 
         f32x16_t acc[2][2];
 #pragma unroll
@@ -173,53 +257,24 @@ __global__ void __launch_bounds__(256) stem_conv_kernel(const float* __restrict_
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[f][j][e] = 0.0f;
+        // per slice: 6 weight and 6 input fragments, 24 MFMAs (products
+        // outermost, so consecutive MFMAs go to the four accumulators); the
+        // other wave on the SIMD covers the LDS latency
 #pragma unroll
         for (int sl = 0; sl < SLICES; ++sl) {
-            u32x4_t a[3][2];
+            u32x4_t a[3][2], b[3][2];
+            read_slice(sl, a, b);
+            constexpr int pa[6] = {0, 0, 1, 0, 1, 2}, pb[6] = {0, 1, 0, 2, 1, 0};
 #pragma unroll
-            for (int p = 0; p < 3; ++p)
+            for (int q = 0; q < 6; ++q)
 #pragma unroll
                 for (int f = 0; f < 2; ++f)
-                    a[p][f] = *reinterpret_cast<const u32x4_t*>(wl + (p * kRows + f * 32 + wrow) * KROW + sl * 16 +
-                                                                kg * 8);
-            u32x4_t b[3][2];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int ko = koff[sl];
-                const float* src = patch + pix[j] + (ko < 0 ? 0 : ko);
-                float v[8];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const float2 w2 = *reinterpret_cast<const float2*>(src + 2 * q);
-                    v[2 * q] = w2.x;
-                    v[2 * q + 1] = w2.y;
-                }
-                // columns past the kernel and rows past kh carry zero weights;
-                // zero their inputs too so an inf there cannot make a NaN
-#pragma unroll
-                for (int q = KW; q < 8; ++q) v[q] = 0.0f;
-                if (ko < 0) {
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) v[q] = 0.0f;
-                }
-                uint4 hi, mid, lo;
-                split8(v, hi, mid, lo);
-                b[0][j] = u32x4_t{hi.x, hi.y, hi.z, hi.w};
-                b[1][j] = u32x4_t{mid.x, mid.y, mid.z, mid.w};
-                b[2][j] = u32x4_t{lo.x, lo.y, lo.z, lo.w};
-            }
-#pragma unroll
-            for (int f = 0; f < 2; ++f)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    acc[f][j] = mfma32(a[0][f], b[0][j], acc[f][j]);
-                    acc[f][j] = mfma32(a[0][f], b[1][j], acc[f][j]);
-                    acc[f][j] = mfma32(a[1][f], b[0][j], acc[f][j]);
-                    acc[f][j] = mfma32(a[0][f], b[2][j], acc[f][j]);
-                    acc[f][j] = mfma32(a[1][f], b[1][j], acc[f][j]);
-                    acc[f][j] = mfma32(a[2][f], b[0][j], acc[f][j]);
-                }
+                    for (int j = 0; j < 2; ++j) acc[f][j] = mfma32(a[pa[q]][f], b[pb[q]][j], acc[f][j]);
         }
+        // the next tile's store overwrites the patch: these reads come first
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
         // ---- epilogue: + bias, ReLU; buffer stores into image n's output
         //      (rows past M and pixels past the image carry kOutside) ----
@@ -230,11 +285,10 @@ __global__ void __launch_bounds__(256) stem_conv_kernel(const float* __restrict_
             make_rsrc(y + static_cast<int64_t>(n) * g.M * plane, static_cast<uint32_t>(g.M) * plane * 4);
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int oh = oh0 + 4 * wave + 2 * j + ((lane & 31) >> 4);
+            const int oh = oh0 + 2 * j + ((lane & 31) >> 4);
             const int ow = ow0 + (lane & 15);
-            const uint32_t base = (oh < g.OH && ow < g.OW)
-                                      ? (static_cast<uint32_t>(4 * kg) * plane + oh * g.OW + ow) * 4
-                                      : kOutside;
+            const uint32_t base =
+                (oh < g.OH && ow < g.OW) ? (static_cast<uint32_t>(4 * kg) * plane + oh * g.OW + ow) * 4 : kOutside;
 #pragma unroll
             for (int f = 0; f < 2; ++f)
 #pragma unroll
@@ -246,7 +300,6 @@ __global__ void __launch_bounds__(256) stem_conv_kernel(const float* __restrict_
                                                           base + static_cast<uint32_t>(row) * plane * 4, 0, 0);
                 }
         }
-        __syncthreads();
     }
 }
 
@@ -265,27 +318,22 @@ int stem_cu_count() {
     return cached[dev];
 }
 
-constexpr int kStemKW = 7, kStemSlices = 11;
+using Stem7x7 = StemShape<3, 7, 7, 2, 2>;  // the ResNet stem
 
 bool stem_geom(const tbn_conv2d_desc* d, int flags, StemGeom& g) {
+    using S = Stem7x7;
     if (!d || flags & ~TBN_EPI_RELU) return false;
-    if (d->kw != kStemKW || d->dw != 1 || d->m > kRows || d->sw % 2 != 0) return false;
-    if ((d->kh * d->c + 1) / 2 != kStemSlices) return false;
-    const int64_t OH = (d->h + 2 * d->ph - d->dh * (d->kh - 1) - 1) / d->sh + 1;
+    if (d->c != S::C || d->kh != S::KH || d->kw != S::KW || d->sh != S::SH || d->sw != S::SW || d->dh != 1 ||
+        d->dw != 1 || d->m > kRows || d->m <= 0)
+        return false;
+    const int64_t OH = (d->h + 2 * d->ph - (d->kh - 1) - 1) / d->sh + 1;
     const int64_t OW = (d->w + 2 * d->pw - (d->kw - 1) - 1) / d->sw + 1;
     if (OH <= 0 || OW <= 0) return false;
-    g.N = int(d->n); g.C = int(d->c); g.H = int(d->h); g.W = int(d->w); g.M = int(d->m);
-    g.kh = int(d->kh); g.kw = int(d->kw); g.sh = int(d->sh); g.sw = int(d->sw);
-    g.ph = int(d->ph); g.pw = int(d->pw); g.dh = int(d->dh);
+    g.N = int(d->n); g.H = int(d->h); g.W = int(d->w); g.M = int(d->m);
+    g.ph = int(d->ph); g.pw = int(d->pw);
     g.OH = int(OH); g.OW = int(OW);
-    g.K_pad = 16 * kStemSlices;
-    g.prows = (kTile - 1) * g.sh + (g.kh - 1) * g.dh + 1;
-    // a fragment reads columns tc * sw + 0..7 of each patch row
-    g.pitch = ((kTile - 1) * g.sw + 8 + 3) / 4 * 4;
-    g.patch = g.C * g.prows * g.pitch;
-    if (g.patch > kMaxPatch || g.prows >= 4096 || g.C >= 256) return false;
-    g.tiles_w = (g.OW + kTile - 1) / kTile;
-    g.tiles_img = ((g.OH + kTile - 1) / kTile) * g.tiles_w;
+    g.tiles_w = (g.OW + kTileW - 1) / kTileW;
+    g.tiles_img = ((g.OH + kTileH - 1) / kTileH) * g.tiles_w;
     const int64_t tiles = static_cast<int64_t>(d->n) * g.tiles_img;
     // 32-bit offsets below 2^31: one input image, one output image (all 64
     // rows of a tile, also past M)
@@ -310,36 +358,17 @@ int conv_stem_run(const float* x, const tbn_conv2d_desc* desc, const float* w, c
     StemGeom g;
     TBN_REQUIRE(stem_geom(desc, flags, g), TBN_INVALID_SHAPE, "shape not handled by the stem conv kernel");
     if (g.tiles == 0) return ok();
-    void* wsplit = nullptr;
-    const size_t wbytes = static_cast<size_t>(3) * kRows * g.K_pad * sizeof(uint16_t);
-    hipError_t e = hipMallocAsync(&wsplit, wbytes, s);
-    if (e != hipSuccess) {
-        (void)hipGetLastError();
-        return fail(e == hipErrorOutOfMemory ? TBN_OUT_OF_MEMORY : TBN_RUNTIME_ERROR,
-                    std::string("stem conv weight buffer: ") + hipGetErrorString(e));
+    using S = Stem7x7;
+    static bool attr_set = false;
+    if (!attr_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&stem_conv_kernel<S>),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return fail(TBN_RUNTIME_ERROR, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
+        attr_set = true;
     }
-    hipLaunchKernelGGL(stem_weights_kernel, dim3(static_cast<unsigned>(ceil_div(kRows * g.K_pad, 256))), dim3(256), 0,
-                       s, w, g, static_cast<uint16_t*>(wsplit));
-    int rc = check_launch("conv2d_f32 (stem weights)");
-    if (rc == TBN_SUCCESS) {
-        constexpr int KROW = 16 * kStemSlices + 8;
-        const size_t lds = static_cast<size_t>(3) * kRows * KROW * 2 + kRows * 4 + static_cast<size_t>(g.patch) * 4;
-        static bool attr_set = false;
-        if (!attr_set) {
-            e = hipFuncSetAttribute(reinterpret_cast<const void*>(&stem_conv_kernel<kStemKW, kStemSlices>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-            if (e != hipSuccess) rc = fail(TBN_RUNTIME_ERROR, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
-            else attr_set = true;
-        }
-        if (rc == TBN_SUCCESS) {
-            const int blocks = std::min(g.tiles, stem_cu_count());
-            hipLaunchKernelGGL((stem_conv_kernel<kStemKW, kStemSlices>), dim3(blocks), dim3(256), lds, s, x, g,
-                               static_cast<const uint16_t*>(wsplit), bias, y);
-            rc = check_launch("conv2d_f32 (stem)");
-        }
-    }
-    (void)hipFreeAsync(wsplit, s);
-    return rc;
+    const int blocks = static_cast<int>(std::min<int64_t>(ceil_div(g.tiles, kWaves), stem_cu_count()));
+    hipLaunchKernelGGL((stem_conv_kernel<S>), dim3(blocks), dim3(64 * kWaves), S::LDS, s, x, g, w, bias, y);
+    return check_launch("conv2d_f32 (stem)");
 }
 
 }  // namespace tbn_hip
