@@ -146,10 +146,11 @@ def conv_cfg4(torch, tbn_hip, seed):
     return step, step_reference_layout, (x, packed, conv_w, scale, bias, y, desc)
 
 
-def session_workload(torch, _tbn, which, stream):
-    """Config 1 (LeNet, batch 1, HIP-graph replay) or config 5 (ResNet-18,
-    batch 32) through TBNModel::Session with quantization on; the input is
-    already in HBM, the output stays there (get_output_device)."""
+def session_workload(torch, _tbn, which, stream, replay):
+    """Config 1 (LeNet, batch 1) or config 5 (ResNet-18, batch 32) through
+    TBNModel::Session with quantization on, eager or replaying the Session's
+    HIP graph of the forward (the same kernels, launched without the host);
+    the input is already in HBM, the output stays there."""
     sys.path.insert(0, str(ROOT / "tests"))
     import models
     if which == "lenet":
@@ -163,7 +164,7 @@ def session_workload(torch, _tbn, which, stream):
     torch.cuda.synchronize()
     _tbn.set_current_stream(stream.cuda_stream)
     sess.set_input("input", _tbn.Tensor.wrap(xd.data_ptr(), list(x.shape), "float32", "hip"))
-    if which == "lenet":
+    if replay:
         sess.set_graph_replay(True)
 
     def step(sh):
@@ -302,14 +303,16 @@ def main():
         extra["gemm_cfg2_gflops_equiv"] = round(2.0 * 1024 ** 3 / (g_ms * 1e-3) / 1e9, 1)
         log(f"binary cfg2 1024^3: {g_ms * 1e3:.1f} us")
         del keep
-    for which, key in (("lenet", "lenet_session_us_per_forward"), ("resnet", "resnet18_session_ms_per_batch32")):
+    for which, key, replay in (("lenet", "lenet_session_us_per_forward", True),
+                               ("resnet", "resnet18_session_ms_per_batch32", False)):
         if not want(which):
             continue
-        step, keep = session_workload(torch, _tbn, which, stream)
+        step, keep = session_workload(torch, _tbn, which, stream, replay)
         s_ms = timed(step)
         extra[key] = round(s_ms * (1e3 if which == "lenet" else 1.0), 3)
         extra[which + "_session_launches"] = keep[1].planned_launches()
-        log(f"{which} session: {s_ms * 1e3:.1f} us per forward ({keep[1].planned_launches()} launches)")
+        log(f"{which} session ({'graph replay' if replay else 'eager'}): {s_ms * 1e3:.1f} us per forward "
+            f"({keep[1].planned_launches()} launches)")
         _tbn.set_current_stream(0)
         del keep
 

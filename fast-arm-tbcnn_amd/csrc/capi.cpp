@@ -23,6 +23,64 @@ int ok() {
     return TBN_SUCCESS;
 }
 
+// Stream workspace for split-K partial sums.  A free followed by a new
+// allocation on a stream makes the GPU wait on the allocator between kernels
+// (about 6 us per call), so each device keeps one buffer for the stream that
+// last used it, grown as needed; consecutive users on that stream are
+// ordered by the stream.  Calls on another stream, or under stream capture
+// (where an allocation belongs to the graph), get a stream-ordered temporary.
+namespace {
+struct Workspace {
+    hipStream_t stream = nullptr;
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+Workspace g_ws[64];
+
+int alloc_async(void*& ptr, size_t bytes, hipStream_t s) {
+    const hipError_t e = hipMallocAsync(&ptr, bytes, s);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        ptr = nullptr;
+        return fail(e == hipErrorOutOfMemory ? TBN_OUT_OF_MEMORY : TBN_RUNTIME_ERROR,
+                    std::string("workspace allocation failed: ") + hipGetErrorString(e));
+    }
+    return TBN_SUCCESS;
+}
+}  // namespace
+
+int stream_workspace(hipStream_t s, size_t bytes, void*& ptr, bool& temporary) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone;
+    int dev = 0;
+    if (!capturing && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+        std::lock_guard<std::mutex> lock(g_ws_mutex);
+        Workspace& w = g_ws[dev];
+        if (w.ptr && w.stream == s && w.bytes >= bytes) {
+            ptr = w.ptr;
+            temporary = false;
+            return TBN_SUCCESS;
+        }
+        if (!w.ptr || w.stream == s) {
+            if (w.ptr) (void)hipFreeAsync(w.ptr, w.stream);
+            w = Workspace{};
+            const size_t grown = bytes + bytes / 4;
+            const int rc = alloc_async(ptr, grown, s);
+            if (rc) return rc;
+            w = Workspace{s, ptr, grown};
+            temporary = false;
+            return TBN_SUCCESS;
+        }
+    }
+    temporary = true;
+    return alloc_async(ptr, bytes, s);
+}
+
+void release_workspace(void* ptr, bool temporary, hipStream_t s) {
+    if (temporary && ptr) (void)hipFreeAsync(ptr, s);
+}
+
 int ensure_device() {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);

@@ -22,6 +22,12 @@ int check_launch(const char* what);
 
 inline hipStream_t stream_of(tbn_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Device scratch for split-K partial sums on stream s: a per-device buffer
+// reused by consecutive calls on one stream, else (another stream, stream
+// capture) a stream-ordered temporary; release_workspace frees only the latter.
+int stream_workspace(hipStream_t s, size_t bytes, void*& ptr, bool& temporary);
+void release_workspace(void* ptr, bool temporary, hipStream_t s);
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace tbn_hip

@@ -53,6 +53,9 @@ struct PatchGeom {
     // kernels stage only the pixels they use (psh = sh, poh = 1); others stage
     // the dense rectangle (psh = 1, poh = sh)
     int psh, psw, poh, pow_;
+    // split-K over blocks: split s takes chunks [s * cps, min(chunks, (s + 1) * cps))
+    // and writes raw sums; blocks_split = blocks of one split
+    int splits, cps, blocks_split;
 };
 
 // Buffer resource (gfx9 word 3: raw dword addressing) over `bytes` from base;
@@ -158,6 +161,7 @@ struct PatchEpi {
     const float* bias;
     const float* residual;
     int flags;
+    float* partial;  // split-K: raw sums [split][N][M][OH * OW] instead of y (null: no split)
 };
 
 // bf16 elements of one LDS buffer: three planes of patch + 1 pixel records
@@ -195,8 +199,16 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     // block -> (channel tile, image, spatial tile); channel tiles of one pixel
     // tile are neighbours so the patch is shared through L2
     const int tiles_m = (g.M + Cfg::BM - 1) / Cfg::BM;
-    const int mt = blockIdx.x % tiles_m;
-    int st = blockIdx.x / tiles_m;
+    int bid = static_cast<int>(blockIdx.x);
+    int sp = 0;  // K split of this block
+    if (g.splits > 1) {
+        sp = bid / g.blocks_split;
+        bid -= sp * g.blocks_split;
+    }
+    const int cb = sp * g.cps;                        // the block's chunks [cb, ce)
+    const int ce = min(g.chunks, cb + g.cps);
+    const int mt = bid % tiles_m;
+    int st = bid / tiles_m;
     const int n = st / g.tiles_img;
     st -= n * g.tiles_img;
     const int m0 = mt * Cfg::BM;
@@ -340,14 +352,14 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    load_chunk(0);
+    load_chunk(cb);
     store_chunk(0);
     float* epi_lds = reinterpret_cast<float*>(lds + 2 * buf_elems);  // [BM] multipliers, [BM] addends
     if (tid < Cfg::BM) {
         epi_lds[tid] = epi.alpha * raw_scale;
         epi_lds[Cfg::BM + tid] = raw_bias;
     }
-    if (g.chunks > 1) load_chunk(1);
+    if (cb + 1 < ce) load_chunk(cb + 1);
     __syncthreads();
 
     const int kg = lane >> 5;
@@ -356,8 +368,8 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     // patch offset of tap (r, s): (r*dh*PWi + s*dw) * kPix
     const int tap_ds = g.dw * kPix;
     const int tap_dr = g.dh * g.PWi * kPix;
-    for (int ch = 0; ch < g.chunks; ++ch) {
-        const uint16_t* cur = lds + (ch & 1) * buf_elems;
+    for (int ch = cb; ch < ce; ++ch) {
+        const uint16_t* cur = lds + ((ch - cb) & 1) * buf_elems;
         auto read_b = [&](int toff, int kk, u32x4_t (&b)[3][Cfg::FC]) {
 #pragma unroll
             for (int p = 0; p < 3; ++p)
@@ -457,9 +469,9 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                 s = next_s;
             }
         }
-        if (ch + 1 < g.chunks) {
-            store_chunk((ch + 1) & 1);
-            if (ch + 2 < g.chunks) load_chunk(ch + 2);
+        if (ch + 1 < ce) {
+            store_chunk((ch + 1 - cb) & 1);
+            if (ch + 2 < ce) load_chunk(ch + 2);
         }
         __syncthreads();
     }
@@ -485,6 +497,26 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                                   : static_cast<uint32_t>(oh * g.OW + ow);
         const bool keep = valid && (!pool || (lane & 3) == 0);
         voff[j] = keep ? static_cast<uint32_t>(rlane) * plane4 + pix * 4 : kOutside;
+    }
+    if (epi.partial) {
+        // split-K (never with the pool, host-checked): raw sums of this
+        // block's chunks into split sp's plane set
+        const __amdgpu_buffer_rsrc_t p_rs =
+            make_rsrc(epi.partial + static_cast<int64_t>(sp) * g.N * g.M * plane + obase, obytes);
+#pragma unroll
+        for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    // through a VGPR: stored straight from the accumulator
+                    // registers, hipcc put one register's value in all 16 stores
+                    uint32_t v;
+                    asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "v"(acc[f][j][e]));
+                    __builtin_amdgcn_raw_buffer_store_b32(v, p_rs, voff[j] + (f * 32 + 8 * (e >> 2) + (e & 3)) * plane4,
+                                                          0, 0);
+                }
+        return;
     }
     // v' = (v + a) * s + b with (a, b) = (bias, 0) for bias-then-scale, else (0, bias)
     const bool bts = (epi.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
@@ -545,6 +577,26 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     } else {
         if (relu) finish(T{}, F{}, F{});
         else finish(F{}, F{}, F{});
+    }
+}
+
+// Split-K sum and epilogue: y = the kernel's epilogue applied to the splits'
+// raw sums added in split order (element i of the [N][M][OH * OW] output).
+__global__ void __launch_bounds__(256) conv_splitk_reduce_kernel(const float* __restrict__ partial, int splits,
+                                                                 int64_t total, int M, int plane, PatchEpi epi) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    const bool bts = (epi.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+        float v = partial[i];
+        for (int sp = 1; sp < splits; ++sp) v += partial[static_cast<int64_t>(sp) * total + i];
+        const int m = static_cast<int>((i / plane) % M);
+        const float mm = epi.alpha * (epi.scale ? epi.scale[m] : 1.0f);
+        const float bb = epi.bias ? epi.bias[m] : 0.0f;
+        const float a = bts ? bb : 0.0f, b = bts ? 0.0f : bb;
+        v = (v + a) * mm + b;
+        if (epi.residual) v += epi.residual[i];
+        if (epi.flags & TBN_EPI_RELU) v = v > 0.0f ? v : 0.0f;
+        epi.y[i] = v;
     }
 }
 
@@ -761,9 +813,11 @@ int launch_patch_taps(const float* x, const PatchGeom& g, const uint8_t* w, int6
                                                                          hipGetErrorString(e));
         attr_set = true;
     }
-    const int64_t blocks = static_cast<int64_t>(g.N) * g.tiles_img * ((g.M + Cfg::BM - 1) / Cfg::BM);
+    PatchGeom gl = g;
+    gl.blocks_split = static_cast<int>(static_cast<int64_t>(g.N) * g.tiles_img * ((g.M + Cfg::BM - 1) / Cfg::BM));
+    const int64_t blocks = static_cast<int64_t>(gl.blocks_split) * g.splits;
     hipLaunchKernelGGL((conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI>), dim3(static_cast<unsigned>(blocks)),
-                       dim3(Cfg::NT), lds, s, x, g, w, col_bytes, m_alloc, epi);
+                       dim3(Cfg::NT), lds, s, x, gl, w, col_bytes, m_alloc, epi);
     return tbn_hip::check_launch(TERNARY ? "conv2d_f32_ternary (patch)" : "conv2d_f32_binary (patch)");
 }
 
@@ -930,8 +984,29 @@ int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
     const int64_t out_bytes = (d->m + 128) * static_cast<int64_t>(g.pool ? g.PH * g.PW : g.OH * g.OW) * 4;
     if (image_bytes >= (1LL << 31) || weight_bytes >= (1LL << 31) || out_bytes >= (1LL << 31))
         return tbn_hip::fail(TBN_INVALID_SHAPE, "conv image, weights or output too large for the patch kernel");
+    // K splits over blocks for the smallest feature maps with many chunks
+    // (ResNet's last stage, whose tiles alone leave SIMDs with one wave):
+    // 2^16 outputs per image and split, at least 36 K steps of 32 per split
+    // (a split's saving must pay for the reduce launch).  The
+    // rule reads one image's shape, not the batch, so a sample's result does
+    // not depend on the batch it runs in; the tile choice never changes it.
+    const int64_t outputs_img = static_cast<int64_t>(g.M) * g.OH * g.OW;
+    int splits = 1;
+    if (!g.pool) {
+        while (splits < 4 && outputs_img * splits * 2 <= (int64_t(1) << 16) &&
+               g.chunks * g.taps / (splits * 2) >= 36)
+            splits *= 2;
+    }
+    if (const char* e = std::getenv("TBN_CONV_SPLITS")) splits = std::max(1, std::atoi(e));  // tuning aid
+    g.cps = (g.chunks + splits - 1) / splits;
+    g.splits = (g.chunks + g.cps - 1) / g.cps;
+    g.blocks_split = 0;
     return TBN_SUCCESS;
 }
+
+int conv_patch_dispatch(int weights, const float* x, const tbn_conv2d_desc* desc, PatchGeom& g,
+                        const uint8_t* conv_weights, int64_t col_bytes, int m_alloc, const PatchEpi& epi,
+                        hipStream_t s);
 
 int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, const uint8_t* conv_weights,
                    const float* scale, float alpha, const float* bias, const float* residual, int flags, float* y,
@@ -958,7 +1033,36 @@ int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, con
     const int64_t Kc = static_cast<int64_t>(g.chunks) * g.taps * kChunk;
     const int64_t col_bytes = Kc / (weights == TBN_WEIGHTS_BINARY ? 8 : 4);
     const int m_alloc = int((desc->m + 7) / 8 * 8);
-    PatchEpi epi{y, scale, alpha, bias, residual, flags};
+    PatchEpi epi{y, scale, alpha, bias, residual, flags, nullptr};
+    void* part = nullptr;
+    bool temporary = false;
+    if (g.splits > 1) {
+        const int64_t total = static_cast<int64_t>(g.N) * g.M * g.OH * g.OW;
+        rc = tbn_hip::stream_workspace(s, static_cast<size_t>(total) * g.splits * sizeof(float), part, temporary);
+        if (rc) return rc;
+        epi.partial = static_cast<float*>(part);
+    }
+    rc = conv_patch_dispatch(weights, x, desc, g, conv_weights, col_bytes, m_alloc, epi, s);
+    if (part) {
+        if (rc == TBN_SUCCESS) {
+            const int64_t total = static_cast<int64_t>(g.N) * g.M * g.OH * g.OW;
+            const int blocks = static_cast<int>(std::min<int64_t>(tbn_hip::ceil_div(total, 256), 4096));
+            PatchEpi fin = epi;
+            fin.partial = nullptr;
+            hipLaunchKernelGGL(conv_splitk_reduce_kernel, dim3(blocks), dim3(256), 0, s,
+                               static_cast<const float*>(part), g.splits, total, g.M, g.OH * g.OW, fin);
+            rc = tbn_hip::check_launch("conv2d (split-K reduce)");
+        }
+        tbn_hip::release_workspace(part, temporary, s);
+    }
+    return rc;
+}
+
+int conv_patch_dispatch(int weights, const float* x, const tbn_conv2d_desc* desc, PatchGeom& g,
+                        const uint8_t* conv_weights, int64_t col_bytes, int m_alloc, const PatchEpi& epi,
+                        hipStream_t s) {
+    int rc;
+    TileChoice tc;
     if (weights == TBN_WEIGHTS_TERNARY) {
         rc = select_tile<true>(desc, g, x, conv_weights, col_bytes, m_alloc, epi, s, tc);
         if (rc) return rc;

@@ -256,17 +256,13 @@ int tbn_hip_gemm_f32(const float* A, const float* B, const float* Cin, int c_is_
         const int used = static_cast<int>(tbn_hip::ceil_div(K, ksplit));
         hipStream_t s = tbn_hip::stream_of(stream);
         void* part = nullptr;
-        const size_t bytes = static_cast<size_t>(used) * M * N * sizeof(float);
-        hipError_t e = hipMallocAsync(&part, bytes, s);
-        if (e != hipSuccess) {
-            (void)hipGetLastError();
-            return tbn_hip::fail(e == hipErrorOutOfMemory ? TBN_OUT_OF_MEMORY : TBN_RUNTIME_ERROR,
-                                 std::string("gemm_f32 split-K buffer: ") + hipGetErrorString(e));
-        }
+        bool temporary = false;
+        int rc = tbn_hip::stream_workspace(s, static_cast<size_t>(used) * M * N * sizeof(float), part, temporary);
+        if (rc) return rc;
         hipLaunchKernelGGL((gemm_f32_split_kernel<Cfg>), dim3(used * tiles_r * tiles_c), dim3(Cfg::NT), 0, s, rowl,
                            coll, static_cast<float*>(part), static_cast<int>(M), static_cast<int>(N),
                            static_cast<int>(K), ksplit, tiles_r, tiles_c);
-        int rc = tbn_hip::check_launch("gemm_f32 (split)");
+        rc = tbn_hip::check_launch("gemm_f32 (split)");
         if (rc == TBN_SUCCESS) {
             const int blocks = static_cast<int>(std::min<int64_t>(tbn_hip::ceil_div(M * N, 256), 2048));
             hipLaunchKernelGGL(gemm_f32_reduce_kernel, dim3(blocks), dim3(256), 0, s,
@@ -274,7 +270,7 @@ int tbn_hip_gemm_f32(const float* A, const float* B, const float* Cin, int c_is_
                                alpha, epi.cin, c_is_1d, beta, flags, out);
             rc = tbn_hip::check_launch("gemm_f32 (split reduce)");
         }
-        (void)hipFreeAsync(part, s);
+        tbn_hip::release_workspace(part, temporary, s);
         return rc;
     }
     hipLaunchKernelGGL((mfma_tile_kernel<Cfg, SplitMatrix<Cfg::BR, Cfg::NT>,

@@ -473,12 +473,9 @@ int gemm_wide(const WideGemmArgs& a, bool ternary, hipStream_t stream) {
     const int used = (steps + per - 1) / per;  // splits that own at least one step
     void* part = nullptr;
     const size_t bytes = static_cast<size_t>(used) * a.M * a.N * sizeof(float);
-    hipError_t e = hipMallocAsync(&part, bytes, stream);
-    if (e != hipSuccess) {
-        (void)hipGetLastError();
-        return fail(e == hipErrorOutOfMemory ? TBN_OUT_OF_MEMORY : TBN_RUNTIME_ERROR,
-                    std::string("split-K partial buffer: ") + hipGetErrorString(e));
-    }
+    bool temporary = false;
+    const int wrc = stream_workspace(stream, bytes, part, temporary);
+    if (wrc) return wrc;
     if (ternary) launch_wide<true, true>(a, tiles_r, tiles_c, used, per, static_cast<float*>(part), stream);
     else launch_wide<false, true>(a, tiles_r, tiles_c, used, per, static_cast<float*>(part), stream);
     int rc = check_launch(what);
@@ -489,7 +486,7 @@ int gemm_wide(const WideGemmArgs& a, bool ternary, hipStream_t stream) {
                            static_cast<const float*>(part), used);
         rc = check_launch("gemm split-K reduce");
     }
-    (void)hipFreeAsync(part, stream);
+    release_workspace(part, temporary, stream);
     return rc;
 }
 

@@ -378,12 +378,13 @@ int grid_for(int64_t items, int threads) {
 }
 
 // Stream-ordered scratch for the int8 rows and row sums.
+// Device scratch of one call (the stream workspace, see common.hpp).
 struct Scratch {
     void* ptr = nullptr;
+    bool temporary = false;
     hipStream_t stream = nullptr;
-    ~Scratch() {
-        if (ptr) (void)hipFreeAsync(ptr, stream);
-    }
+    int get(size_t bytes) { return tbn_hip::stream_workspace(stream, bytes, ptr, temporary); }
+    ~Scratch() { tbn_hip::release_workspace(ptr, temporary, stream); }
 };
 
 }  // namespace
@@ -444,8 +445,7 @@ int tbn_hip_tbn_gemm(const uint8_t* pos, const uint8_t* neg, const uint8_t* bits
     Scratch scr;
     scr.stream = s;
     const size_t tbytes = static_cast<size_t>(m) * n;
-    if (hipMallocAsync(&scr.ptr, tbytes + static_cast<size_t>(m) * 4 + 16, s) != hipSuccess)
-        return tbn_hip::fail(TBN_OUT_OF_MEMORY, "tbn_gemm: scratch allocation failed");
+    if (int rc = scr.get(tbytes + static_cast<size_t>(m) * 4 + 16)) return rc;
     int8_t* T = static_cast<int8_t*>(scr.ptr);
     int* rowsum = reinterpret_cast<int*>(static_cast<uint8_t*>(scr.ptr) + ((tbytes + 15) / 16) * 16);
     hipLaunchKernelGGL(planes_to_rows_kernel, dim3(static_cast<int>(std::min<int64_t>(m, 65536))), dim3(256), 0, s,
@@ -478,8 +478,7 @@ int tbn_hip_qlinear_matmul_binary_tbn(const float* A, int64_t lda, int64_t M, in
     Scratch scr;
     scr.stream = s;
     const size_t tbytes = static_cast<size_t>(M) * K_pad;
-    if (hipMallocAsync(&scr.ptr, tbytes + static_cast<size_t>(M) * 4 + 16, s) != hipSuccess)
-        return tbn_hip::fail(TBN_OUT_OF_MEMORY, "qlinear_matmul_binary_tbn: scratch allocation failed");
+    if (int rc = scr.get(tbytes + static_cast<size_t>(M) * 4 + 16)) return rc;
     int8_t* T = static_cast<int8_t*>(scr.ptr);
     int* rowsum = reinterpret_cast<int*>(static_cast<uint8_t*>(scr.ptr) + ((tbytes + 15) / 16) * 16);
     hipLaunchKernelGGL(ternarize_rows_kernel, dim3(static_cast<int>(std::min<int64_t>(M, 65536))), dim3(256), 0, s,

@@ -46,6 +46,10 @@ CASES = [
     (2, 128, 28, 28, 128, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_BIAS_THEN_SCALE),
     (2, 5, 13, 11, 40, 3, 2, (2, 1), (1, 0), (2, 2), tbn_hip.EPI_RELU),            # odd everything
     (3, 7, 9, 9, 70, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_MAXPOOL2X2),        # odd output, floor pool
+    # K split over blocks (deep layers): 8 chunks -> 2 splits, 16 chunks -> 4
+    (3, 256, 7, 7, 96, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_RELU),
+    (2, 512, 7, 7, 72, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_BIAS_THEN_SCALE),
+    (2, 300, 9, 8, 40, 3, 3, (2, 2), (1, 1), (1, 1), 0),                            # ragged last split
 ]
 
 
@@ -252,3 +256,34 @@ def test_conv_f32_stem_inf_stays_local(dev, orc):
     ref = orc.conv2d_f64(x0, w, b, (2, 2), (3, 3))
     rm.assert_within_tolerance(np.where(touched, 0.0, out), np.where(touched, 0.0, ref), C * 49,
                                np.abs(x0).max() * np.abs(w).max())
+
+
+def test_conv_patch_split_k_residual_and_ternary(dev, orc):
+    """Split-K with the residual epilogue (binary) and with ternary weights:
+    the reduce applies scale, bias, residual and ReLU after adding the splits."""
+    rng = np.random.default_rng(11)
+    N, C, H, W, M = 2, 512, 7, 7, 64
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    res = rng.standard_normal((N, M, H, W)).astype(np.float32)
+    wbytes = (rng.random((M, C, 3, 3)) < 0.5).astype(np.uint8)
+    scale = rng.uniform(0.5, 1.5, M).astype(np.float32)
+    bias = (rng.standard_normal(M) * 0.01).astype(np.float32)
+    K = C * 9
+    packed, K_pad, N_pad = pack_conv_weights(wbytes, M, K)
+    d = tbn_hip.conv_desc(N, C, H, W, M, 3, 3, 1, 1, 1, 1)
+    y = empty((N, M, H, W), torch.float32)
+    tbn_hip.call("tbn_hip_conv2d_f32_quantized", tbn_hip.WEIGHTS_BINARY, P(to_dev(x)), d, P(packed), K_pad, N_pad,
+                 P(to_dev(scale)), 1.0, P(to_dev(bias)), P(to_dev(res)), tbn_hip.EPI_RELU, P(y), None)
+    wsign = np.where(wbytes == 1, 1.0, -1.0).astype(np.float32)
+    ref = conv_ref(x, wsign, scale, 1.0, bias, (1, 1), (1, 1), (1, 1), 0)
+    rm.assert_within_tolerance(host(y), np.maximum(ref + res, 0.0), K, np.abs(x).max() * 1.5)
+    # ternary weights through the same split path
+    t = rng.integers(-1, 2, (M, C * 9)).astype(np.int8)
+    K_pad = (K + 31) // 32 * 32
+    tp = empty(M * K_pad // 4, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(t)), K, M, tbn_hip.LAYOUT_NK, K_pad, M, P(tp), None)
+    y2 = empty((N, M, H, W), torch.float32)
+    tbn_hip.call("tbn_hip_conv2d_f32_ternary", P(to_dev(x)), d, P(tp), K_pad, M, P(to_dev(scale)), 1.0,
+                 P(to_dev(bias)), 0, P(y2), None)
+    ref2 = conv_ref(x, t.reshape(M, C, 3, 3).astype(np.float32), scale, 1.0, bias, (1, 1), (1, 1), (1, 1), 0)
+    rm.assert_within_tolerance(host(y2), ref2, K, np.abs(x).max() * 1.5)

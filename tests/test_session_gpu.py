@@ -89,6 +89,30 @@ def test_lenet_graph_replay_matches_eager(dev, tbn):
         tbn.set_current_stream(0)
 
 
+def test_resnet18_graph_replay_matches_eager(dev, tbn):
+    """Config 5 captured into a HIP graph (the split-K temporaries become
+    graph allocations): every replay equals the eager run bit for bit."""
+    import torch
+    spec = models.resnet18(batch=4, seed=5)
+    x = models.resnet_input(4, seed=5)
+    _, eager = _session(tbn, spec, quant=True)
+    eager.set_input("input", x)
+    eager.run()
+    want = eager.get_output("logits")
+    stream = torch.cuda.Stream()
+    tbn.set_current_stream(stream.cuda_stream)
+    try:
+        _, rs = _session(tbn, spec, quant=True, replay=True)
+        rs.set_input("input", x)
+        for i in range(5):  # eager, capture, then replays
+            rs.run()
+            got = rs.get_output("logits")
+            assert np.array_equal(got, want), f"replay {i} differs"
+            torch.zeros(1000, device="cuda").sum().item()  # unrelated eager work between replays
+    finally:
+        tbn.set_current_stream(0)
+
+
 def test_session_device_input(dev, tbn):
     import torch
     spec = models.lenet(seed=7)
