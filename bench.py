@@ -345,7 +345,7 @@ def main():
         "unit": "TFLOP/s",
         "frac": round(achieved_tflops / FP32_PEAK_TFLOPS, 4),
         "traffic": None,
-        "kernel": "gemm_wide_binary_kernel<WideCfg<128,512,128,64,64>>",
+        "kernel": "gemm_wide_kernel<WideCfg<128,512,128,64,64>,false,false>",
         "mfma_issued": {
             "dtype": "bf16",
             "tflops": round(3.0 * achieved_tflops, 1),
