@@ -161,8 +161,10 @@ private:
     std::string producer_version_;
 };
 
-// The ONNX loader is not part of this library: it throws NotImplementedError.
+// Read an ONNX model (model.hpp:1328-1329 of the reference); the reader is in
+// onnx_parser.hpp.
 TBNModel load_model(const std::string& path);
+TBNModel load_model_from_buffer(const void* data, size_t size);
 const char* get_version();
 
 }  // namespace tbn

@@ -5,6 +5,7 @@
 #include "device.hpp"
 #include "errors.hpp"
 #include "model.hpp"
+#include "onnx_parser.hpp"
 #include "operators.hpp"
 #include "session.hpp"
 #include "tensor.hpp"

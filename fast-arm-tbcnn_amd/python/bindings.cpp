@@ -41,6 +41,12 @@ std::string dtype_name(DataType d) {
         case DataType::INT32: return "int32";
         case DataType::INT64: return "int64";
         case DataType::BOOL: return "bool";
+        case DataType::FLOAT16: return "float16";
+        case DataType::BFLOAT16: return "bfloat16";
+        case DataType::INT16: return "int16";
+        case DataType::UINT16: return "uint16";
+        case DataType::UINT32: return "uint32";
+        case DataType::UINT64: return "uint64";
         default: return "other";
     }
 }
@@ -59,6 +65,11 @@ py::dtype np_dtype(DataType d) {
         case DataType::TERNARY: case DataType::INT8: return py::dtype::of<int8_t>();
         case DataType::INT32: return py::dtype::of<int32_t>();
         case DataType::INT64: return py::dtype::of<int64_t>();
+        case DataType::UINT16: case DataType::BFLOAT16: return py::dtype::of<uint16_t>();  // bf16 as its bits
+        case DataType::INT16: return py::dtype::of<int16_t>();
+        case DataType::FLOAT16: return py::dtype("float16");
+        case DataType::UINT32: return py::dtype::of<uint32_t>();
+        case DataType::UINT64: return py::dtype::of<uint64_t>();
         default: throw InvalidArgumentError("dtype has no numpy equivalent");
     }
 }
@@ -118,6 +129,16 @@ AttributeValue to_attr(const py::handle& v) {
     throw InvalidArgumentError("unsupported attribute value");
 }
 
+py::object from_attr(const AttributeValue& a) {
+    if (a.is_int()) return py::int_(a.as_int());
+    if (a.is_float()) return py::float_(a.as_float());
+    if (a.is_string()) return py::str(a.as_string());
+    if (a.is_tensor()) return to_numpy(a.as_tensor());
+    if (a.is_ints()) return py::cast(a.as_ints());
+    if (a.is_floats()) return py::cast(a.as_floats());
+    return py::cast(a.as_strings());
+}
+
 Conv2DParams conv_params(const Tensor& w, std::vector<int64_t> stride, std::vector<int64_t> pad,
                          std::vector<int64_t> dilation, int64_t groups) {
     Conv2DParams p;
@@ -132,12 +153,12 @@ Conv2DParams conv_params(const Tensor& w, std::vector<int64_t> stride, std::vect
     return p;
 }
 
-// The reference's PyModel (bindings.cpp:53-110) over a graph instead of an ONNX path.
+// The reference's PyModel (bindings.cpp:53-110): an ONNX file (or a graph)
+// with one Session reused by every run().
 class PyModel {
 public:
-    PyModel(std::shared_ptr<ModelGraph> graph, uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk,
-            uint32_t nmk)
-        : model_(std::move(graph)) {
+    PyModel(TBNModel model, uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk, uint32_t nmk)
+        : model_(std::move(model)) {
         TilingParams t{mblk, nblk, kblk, mmk, nmk};
         session_ = std::make_unique<TBNModel::Session>(model_.create_session(t));
     }
@@ -158,6 +179,7 @@ public:
         if (it == model_.graph().value_info.end()) throw std::runtime_error("Input not found: " + name);
         return it->second;
     }
+    const TBNModel& model() const { return model_; }
     TBNModel::Session& session() { return *session_; }
 
 private:
@@ -358,7 +380,37 @@ PYBIND11_MODULE(_tbn, m) {
              py::arg("name"), py::arg("op_type"), py::arg("inputs"), py::arg("outputs"), py::arg("attributes") = py::dict())
         .def_property_readonly("inputs", [](const ModelGraph& g) { return g.inputs; })
         .def_property_readonly("outputs", [](const ModelGraph& g) { return g.outputs; })
-        .def("num_nodes", [](const ModelGraph& g) { return g.nodes.size(); });
+        .def("num_nodes", [](const ModelGraph& g) { return g.nodes.size(); })
+        .def_property_readonly("value_info",
+                               [](const ModelGraph& g) {
+                                   py::dict d;
+                                   for (const auto& [n, s] : g.value_info) d[py::str(n)] = py::cast(s.dims);
+                                   return d;
+                               })
+        .def("initializer_names",
+             [](const ModelGraph& g) {
+                 std::vector<std::string> v;
+                 for (const auto& kv : g.initializers) v.push_back(kv.first);
+                 return v;
+             })
+        .def("initializer", [](const ModelGraph& g, const std::string& n) { return to_numpy(g.initializers.at(n)); })
+        .def("initializer_dtype",
+             [](const ModelGraph& g, const std::string& n) { return dtype_name(g.initializers.at(n).dtype()); })
+        .def("nodes", [](const ModelGraph& g) {
+            py::list out;
+            for (const auto& nd : g.nodes) {
+                py::dict attrs;
+                for (const auto& [k, v] : nd.attributes) attrs[py::str(k)] = from_attr(v);
+                py::dict d;
+                d["name"] = nd.name;
+                d["op_type"] = nd.op_type;
+                d["inputs"] = nd.inputs;
+                d["outputs"] = nd.outputs;
+                d["attributes"] = attrs;
+                out.append(d);
+            }
+            return out;
+        });
 
     py::class_<TBNModel::Session>(m, "Session")
         .def("set_quantization", &TBNModel::Session::set_quantization)
@@ -377,7 +429,12 @@ PYBIND11_MODULE(_tbn, m) {
         .def("validate", &TBNModel::validate)
         .def("inputs", &TBNModel::inputs)
         .def("outputs", &TBNModel::outputs)
-        .def("create_session", [](TBNModel& mdl) { return mdl.create_session(); });
+        .def("create_session", [](TBNModel& mdl) { return mdl.create_session(); })
+        .def("graph", &TBNModel::graph_ptr)
+        .def("producer_name", &TBNModel::producer_name)
+        .def("producer_version", &TBNModel::producer_version)
+        .def("get_input_shape", [](const TBNModel& mdl, const std::string& n) { return mdl.get_input_shape(n).dims; })
+        .def("get_output_shape", [](const TBNModel& mdl, const std::string& n) { return mdl.get_output_shape(n).dims; });
 
     py::class_<InferenceSessionOptions>(m, "InferenceSessionOptions")
         .def(py::init<>())
@@ -399,7 +456,13 @@ PYBIND11_MODULE(_tbn, m) {
         .def("last_run_us", &InferenceSession::last_run_us);
 
     py::class_<PyModel>(m, "Model")
-        .def(py::init<std::shared_ptr<ModelGraph>, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t>(),
+        .def(py::init([](const std::string& path, uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk,
+                         uint32_t nmk) { return new PyModel(load_onnx_model(path), mblk, nblk, kblk, mmk, nmk); }),
+             py::arg("path"), py::arg("mblk") = 64, py::arg("nblk") = 64, py::arg("kblk") = 128,
+             py::arg("mmk") = 32, py::arg("nmk") = 32,
+             "Load an ONNX model; the tiling arguments are accepted for compatibility.")
+        .def(py::init([](std::shared_ptr<ModelGraph> g, uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk,
+                         uint32_t nmk) { return new PyModel(TBNModel(std::move(g)), mblk, nblk, kblk, mmk, nmk); }),
              py::arg("graph"), py::arg("mblk") = 64, py::arg("nblk") = 64, py::arg("kblk") = 128,
              py::arg("mmk") = 32, py::arg("nmk") = 32)
         .def("run", &PyModel::run, py::arg("input"), py::arg("use_quantization") = false)
@@ -407,7 +470,33 @@ PYBIND11_MODULE(_tbn, m) {
         .def("input_names", &PyModel::input_names)
         .def("output_names", &PyModel::output_names)
         .def("input_shape", &PyModel::input_shape, py::arg("name"))
+        .def("producer", [](const PyModel& p) { return py::make_tuple(p.model().producer_name(), p.model().producer_version()); })
         .def("session", &PyModel::session, py::return_value_policy::reference_internal);
 
-    m.def("load_model", [](const std::string& path) { return load_model(path); }, py::arg("path"));
+    // bindings.cpp:154-167 of the reference: load_model returns a Model.
+    m.def("load_model",
+          [](const std::string& path, uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk, uint32_t nmk) {
+              return new PyModel(load_onnx_model(path), mblk, nblk, kblk, mmk, nmk);
+          },
+          py::arg("path"), py::arg("mblk") = 64, py::arg("nblk") = 64, py::arg("kblk") = 128, py::arg("mmk") = 32,
+          py::arg("nmk") = 32, py::return_value_policy::take_ownership);
+
+    // The C++ reader itself, for inspecting a model without a Session.
+    py::class_<OnnxParser>(m, "OnnxParser")
+        .def(py::init<>())
+        .def("parse_from_file", &OnnxParser::parse_from_file, py::arg("path"))
+        .def("parse_from_buffer",
+             [](OnnxParser& p, const py::bytes& b, const std::string& base_dir) {
+                 const std::string s = b;
+                 p.parse_from_buffer(s.data(), s.size(), base_dir);
+             },
+             py::arg("data"), py::arg("base_dir") = "")
+        .def("get_graph", &OnnxParser::get_graph)
+        .def("get_producer_name", &OnnxParser::get_producer_name)
+        .def("get_producer_version", &OnnxParser::get_producer_version)
+        .def("ir_version", &OnnxParser::ir_version)
+        .def("opset_version", &OnnxParser::opset_version, py::arg("domain") = "")
+        .def("warnings", &OnnxParser::warnings);
+    m.def("load_onnx_model", [](const std::string& path) { return std::make_shared<TBNModel>(load_onnx_model(path)); },
+          py::arg("path"));
 }

@@ -33,6 +33,7 @@
 #include "internal.hpp"
 #include "tbn/device.hpp"
 #include "tbn/model.hpp"
+#include "tbn/onnx_parser.hpp"
 #include "tbn/session.hpp"
 #include "tbn_hip.h"
 
@@ -85,10 +86,10 @@ void TBNModel::validate() const {
     }
 }
 
-TBNModel load_model(const std::string& path) {
-    throw NotImplementedError("load_model('" + path +
-                              "'): the ONNX loader is not part of this library; build a ModelGraph instead");
-}
+// model.cpp:10-21 of the reference: both go through the ONNX reader.
+TBNModel load_model(const std::string& path) { return load_onnx_model(path); }
+
+TBNModel load_model_from_buffer(const void* data, size_t size) { return load_onnx_model_from_buffer(data, size); }
 
 const char* get_version() { return "0.1.0"; }
 

@@ -173,6 +173,17 @@ def build_graph(spec, _tbn):
     return g
 
 
+def spec_from_onnx(m):
+    """Spec of a model decoded by onnx_proto.decode_model (initializers as
+    stored: float32, or int64 for shapes)."""
+    nodes = [Node(n["name"], n["op_type"], list(n["inputs"]), list(n["outputs"]), dict(n["attributes"]))
+             for n in m["nodes"]]
+    inits = dict(m["inits"])
+    dtypes = {k: str(v.dtype) for k, v in inits.items()}
+    return Spec(nodes, inits, dtypes, {k: m["value_info"][k] for k in m["inputs"]},
+                {k: m["value_info"][k] for k in m["outputs"]}, dict(m["value_info"]))
+
+
 # ---- the CPU reference executor ------------------------------------------------------
 
 def _conv_attrs(attrs):
@@ -258,6 +269,16 @@ def run_oracle(spec, feeds, quant, orc, record=None):
             x = env[n.inputs[0]]
             ax = a.get("axis", 1)
             y = x.reshape(int(np.prod(x.shape[:ax])), -1)
+        elif n.op == "Reshape":
+            # model.hpp:1039-1090: the shape input, one -1 inferred
+            y = env[n.inputs[0]].reshape([int(d) for d in env[n.inputs[1]].reshape(-1)])
+        elif n.op == "Cast":
+            y = env[n.inputs[0]]  # model.hpp:1272-1287: values pass through as fp32
+        elif n.op in ("Greater", "Less", "Sub"):
+            # model.hpp:1176-1300: the right operand is read at i % its size
+            x = env[n.inputs[0]].astype(np.float32)
+            r = np.resize(env[n.inputs[1]].astype(np.float32).reshape(-1), x.size).reshape(x.shape)
+            y = x > r if n.op == "Greater" else (x < r if n.op == "Less" else x - r)
         elif n.op == "Add":
             xa, xb = env[n.inputs[0]].astype(np.float64), env[n.inputs[1]].astype(np.float64)
             if xa.ndim == 4 and xb.ndim in (1, 3):

@@ -43,12 +43,6 @@ def test_graph_validation_errors(tbn):
     assert e.value.code == -4 and "missing" in str(e.value)
 
 
-def test_load_model_is_not_implemented(tbn):
-    with pytest.raises(tbn.TBNError) as e:
-        tbn.load_model("tests/models/cnn/onnx/simple_cnn.onnx")
-    assert e.value.code == -3
-
-
 def test_session_input_checks_before_device_use(tbn):
     spec = models.lenet(seed=1)
     s = tbn.TBNModel(models.build_graph(spec, tbn)).create_session()
