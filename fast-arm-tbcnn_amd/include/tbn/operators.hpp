@@ -127,7 +127,8 @@ Tensor qlinear_matmul_packed(const Tensor& a, const PackedWeights& w, float scal
 
 // ---- convolution -----------------------------------------------------------------
 
-// fp32 Conv2D (conv2d.cpp:78-192): y = conv(x, w) + b.  groups must be 1.
+// fp32 Conv2D (conv2d.cpp:78-192): y = conv(x, w) + b.  params.groups > 1 is
+// conv2d_grouped.
 Tensor conv2d(const Tensor& input, const Tensor& weights, const Tensor* bias = nullptr,
               const Conv2DParams& params = Conv2DParams());
 // Binary Conv2D (conv2d.cpp:220-316): y = conv(x, +-1) + b, weights BINARY
@@ -141,6 +142,22 @@ Tensor conv2d_ternary(const Tensor& input, const Tensor& ternary_weights, const 
 // y = s[m] * conv(x, +-1) + b[m] (conv2d.cpp:319-369).
 Tensor conv2d_binary_with_scales(const Tensor& input, const Tensor& binary_weights, const Tensor* bias,
                                  const Conv2DParams& params, const std::vector<float>& channel_scales);
+
+// Grouped fp32 Conv2D, weights [M, C/groups, kh, kw] (conv2d.cpp:372-384, which
+// throws for groups > 1): groups == C runs the depthwise kernel, otherwise one
+// dense conv per group on channel slices.
+Tensor conv2d_grouped(const Tensor& input, const Tensor& weights, const Tensor* bias = nullptr,
+                      int64_t groups = 1, const Conv2DParams& params = Conv2DParams());
+// groups = input channels (conv2d.cpp:386-393).
+Tensor depthwise_conv2d(const Tensor& input, const Tensor& weights, const Tensor* bias = nullptr,
+                        const Conv2DParams& params = Conv2DParams());
+// conv2d with dilation on both axes (conv2d.cpp:396-403).
+Tensor dilated_conv2d(const Tensor& input, const Tensor& weights, const Tensor* bias = nullptr,
+                      int64_t dilation = 1, const Conv2DParams& params = Conv2DParams());
+// Inference BatchNormalization over dim 1 (not in the reference):
+// y = (x - mean) / sqrt(var + eps) * scale + B, computed as x * k + t.
+Tensor batch_norm(const Tensor& input, const Tensor& scale, const Tensor& B, const Tensor& mean,
+                  const Tensor& var, float epsilon = 1e-5f);
 
 // ---- fp32 GEMM, pooling, elementwise ---------------------------------------------
 

@@ -319,6 +319,25 @@ PYBIND11_MODULE(_tbn, m) {
     conv_def("conv2d", &conv2d);
     conv_def("conv2d_binary", &conv2d_binary);
     conv_def("conv2d_ternary", &conv2d_ternary);
+    conv_def("depthwise_conv2d", &depthwise_conv2d);
+    m.def("conv2d_grouped",
+          [](const py::object& x, const py::object& w, const py::object& bias, int64_t groups,
+             std::vector<int64_t> stride, std::vector<int64_t> pad, std::vector<int64_t> dilation) {
+              Tensor hb;
+              Tensor wt = as_tensor(w);
+              return conv2d_grouped(as_tensor(x), wt, opt_tensor(bias, hb), groups,
+                                    conv_params(wt, stride, pad, dilation, groups));
+          },
+          py::arg("input"), py::arg("weights"), py::arg("bias") = py::none(), py::arg("groups") = 1,
+          py::arg("stride") = std::vector<int64_t>{1, 1}, py::arg("pad") = std::vector<int64_t>{0, 0},
+          py::arg("dilation") = std::vector<int64_t>{1, 1});
+    m.def("batch_norm",
+          [](const py::object& x, const py::object& scale, const py::object& B, const py::object& mean,
+             const py::object& var, float eps) {
+              return batch_norm(as_tensor(x), as_tensor(scale), as_tensor(B), as_tensor(mean), as_tensor(var), eps);
+          },
+          py::arg("input"), py::arg("scale"), py::arg("B"), py::arg("mean"), py::arg("var"),
+          py::arg("epsilon") = 1e-5f);
     m.def("conv2d_binary_with_scales",
           [](const py::object& x, const py::object& w, const py::object& bias, std::vector<float> scales,
              std::vector<int64_t> stride, std::vector<int64_t> pad, std::vector<int64_t> dilation) {

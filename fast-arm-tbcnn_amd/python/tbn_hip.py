@@ -84,6 +84,9 @@ _SIGNATURES = {
     "tbn_hip_global_avgpool2d": ([_P, _I64, _I64, _I64, _I64, _P, _P], _I32),
     "tbn_hip_add": ([_P, _P, _I64, _I64, _I64, _I64, _I32, _P, _P], _I32),
     "tbn_hip_relu": ([_P, _I64, _P, _P], _I32),
+    "tbn_hip_conv2d_depthwise": ([_P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P, _P], _I32),
+    "tbn_hip_copy_channels": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P], _I32),
+    "tbn_hip_channel_affine": ([_P, _I64, _I64, _I64, _P, _P, _I32, _P, _P], _I32),
     "tbn_hip_gemm_f32_quantized": ([_I32, _P, _I64, _I64, _I64, _I64, _P, _I64, _I64, _P, _F32, _P, _P, _I32,
                                     _F32, _I32, _P, _I64, _P], _I32),
     "tbn_hip_conv2d_f32_quantized": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _I64, _I64, _P, _F32, _P, _P,

@@ -22,6 +22,7 @@
 #include <chrono>
 #include <cmath>
 #include <cstdio>
+#include <cstring>
 #include <deque>
 #include <functional>
 #include <map>
@@ -169,6 +170,8 @@ Pool2DParams pool_params(const ModelNode& node) {
 enum class OpKind {
     ConvF32,
     ConvQuant,
+    ConvDepthwise,  // one input channel per group: fp32 weights (exact +-1 / ternary when quantized)
+    ChannelAffine,  // BatchNormalization not folded into a conv
     GemmF32,
     GemmQuant,
     Add,
@@ -192,7 +195,11 @@ struct Op {
     int residual = -1;       // value id of a fused residual addend
     const PackedWeights* pw = nullptr;
     const Tensor* conv_w = nullptr;  // conv-layout weights of the patch conv path
-    int workspace = -1;              // value id of the op's transient workspace (none yet)
+    int64_t groups = 1;              // > 1: one dense conv per group on channel slices
+    std::string weight_name, scale_name, bias_name;  // initializers behind w / scale / bias
+    std::vector<float> bn_k, bn_t;   // ChannelAffine: y = x * k + t per channel (host copy)
+    std::vector<const Tensor*> group_conv_w;  // per-group conv-layout weights (grouped patch conv)
+    int workspace = -1;              // value id of the op's transient workspace (grouped conv slices)
     const float* scale = nullptr;  // per-channel scale (device)
     const float* w = nullptr;      // fp32 weights (device)
     const float* bias = nullptr;   // device
@@ -244,6 +251,7 @@ struct TBNModel::Session::Impl {
     std::unordered_map<std::string, PackedWeights> packed;      // key: name + "#" + variant
     std::unordered_map<std::string, Tensor> conv_packed;        // conv-layout copies of `packed` entries
     std::unordered_map<std::string, Tensor> scaled_addends;     // beta * C of quantized Gemms
+    std::unordered_map<std::string, Tensor> derived;            // depthwise +-1 weights, BatchNormalization folds
 
     // ---- the compiled plan ----
     bool planned = false;
@@ -370,6 +378,29 @@ struct TBNModel::Session::Impl {
 
     const float* const_f32(int id) const { return static_cast<const float*>(values[id].const_ptr); }
 
+    // Weights of a depthwise layer as fp32 on the device: the initializer
+    // itself, or its exact +-1 / -1,0,+1 values when the layer is quantized
+    // (`rule`: 0 BINARY bytes, 1 w > 0, 2 w >= 0, 3 TERNARY values).
+    const float* depthwise_weights(const std::string& wname, int rule) {
+        const std::string key = wname + "#dw" + std::to_string(rule);
+        auto it = derived.find(key);
+        if (it != derived.end()) return it->second.typed_data<float>();
+        const Tensor& w = initializer(wname);
+        const Tensor host = w.on_device() ? w.to_device(DeviceType::CPU) : w;
+        const int64_t n = host.num_elements();
+        std::vector<float> v(static_cast<size_t>(n));
+        for (int64_t i = 0; i < n; ++i) {
+            if (rule == 0) v[i] = host.typed_data<uint8_t>()[i] == 1 ? 1.0f : -1.0f;
+            else if (rule == 3) v[i] = static_cast<float>(host.typed_data<int8_t>()[i]);
+            else {
+                const float x = host.typed_data<float>()[i];
+                v[i] = (rule == 2 ? x >= 0.0f : x > 0.0f) ? 1.0f : -1.0f;
+            }
+        }
+        Tensor d(host.shape(), DataType::FLOAT32, v.data(), DeviceType::HIP);
+        return derived.emplace(key, d).first->second.typed_data<float>();
+    }
+
     void lower_conv(const ModelNode& node) {
         TBN_CHECK(node.inputs.size() >= 2, InvalidArgumentError, "Conv expects at least 2 inputs");
         TBN_CHECK(node.outputs.size() == 1, InvalidArgumentError, "Conv expects 1 output");
@@ -383,11 +414,16 @@ struct TBNModel::Session::Impl {
         TBN_CHECK(xs.rank() == 4, InvalidShapeError, "Conv input must be 4D (NCHW), got " + shape_to_string(xs));
         TBN_CHECK(ws.rank() == 4, InvalidShapeError, "Conv weights must be 4D, got " + shape_to_string(ws));
         const Conv2DParams p = conv_params(node, ws);
-        TBN_CHECK(p.groups == 1, NotImplementedError, "Conv '" + node.name + "': grouped convolution is not supported");
-        TBN_CHECK(xs.dims[1] == ws.dims[1], InvalidShapeError, "Conv '" + node.name + "': channel mismatch");
+        // conv2d_grouped (conv2d.cpp:372-384) throws for groups > 1; here a
+        // group of one input channel is the depthwise kernel and larger groups
+        // run the dense kernels group by group.
+        TBN_CHECK(p.groups >= 1 && ws.dims[0] % p.groups == 0, InvalidShapeError,
+                  "Conv '" + node.name + "': output channels must be divisible by group");
+        TBN_CHECK(xs.dims[1] == ws.dims[1] * p.groups, InvalidShapeError, "Conv '" + node.name + "': channel mismatch");
         Op op;
         op.node = node.name;
         op.in.push_back(xi);
+        op.groups = p.groups;
         op.desc = tbn_conv2d_desc{xs.dims[0], xs.dims[1], xs.dims[2], xs.dims[3], ws.dims[0], ws.dims[2],
                                   ws.dims[3], p.stride_h, p.stride_w, p.pad_h, p.pad_w, p.dilation_h, p.dilation_w};
         const int64_t OH = (xs.dims[2] + 2 * p.pad_h - p.dilation_h * (ws.dims[2] - 1) - 1) / p.stride_h + 1;
@@ -399,51 +435,134 @@ struct TBNModel::Session::Impl {
             TBN_CHECK(values[bi].shape.size() == ws.dims[0], InvalidShapeError,
                       "Conv '" + node.name + "': bias size must equal the output channels");
             op.bias = const_f32(bi);
+            op.bias_name = node.inputs[2];
         }
+        op.weight_name = wname;
+        const bool depthwise = p.groups > 1 && ws.dims[1] == 1;
         const DataType wt = values[wi].dtype;
+        int dw_rule = -1;  // depthwise weights: -1 fp32 as stored, else the depthwise_weights rule
         if (wt == DataType::BINARY) {
             op.kind = OpKind::ConvQuant;
-            op.pw = &packed_binary(wname, true, 0);
+            if (depthwise) dw_rule = 0;
+            else op.pw = &packed_binary(wname, true, 0);
         } else if (wt == DataType::TERNARY) {
             op.kind = OpKind::ConvQuant;
-            op.pw = &packed_ternary(wname, true);
+            if (depthwise) dw_rule = 3;
+            else op.pw = &packed_ternary(wname, true);
         } else if (wt == DataType::FLOAT32 && quant && quantize_allowed(node)) {
             op.kind = OpKind::ConvQuant;
             conv_scales(wname);
             if (conv_already_binary[wname]) {
                 // cached path: signs w >= 0, y = (acc + b) * s[m] (model.hpp:414-559)
-                op.pw = &packed_binary(wname, true, 2);
+                if (depthwise) dw_rule = 2;
+                else op.pw = &packed_binary(wname, true, 2);
                 op.scale = dev_scales[wname].typed_data<float>();
+                op.scale_name = wname;
                 op.flags |= TBN_EPI_BIAS_THEN_SCALE;
             } else {
                 // quantize_to_binary(W) (w > 0) then conv2d_binary, no scale (model.hpp:560-564)
-                op.pw = &packed_binary(wname, true, 1);
+                if (depthwise) dw_rule = 1;
+                else op.pw = &packed_binary(wname, true, 1);
             }
         } else {
             TBN_CHECK(wt == DataType::FLOAT32, InvalidArgumentError, "Conv '" + node.name + "': unsupported weight type");
             op.kind = OpKind::ConvF32;
             op.w = const_f32(wi);
         }
+        if (depthwise) {
+            op.kind = OpKind::ConvDepthwise;
+            op.w = dw_rule < 0 ? const_f32(wi) : depthwise_weights(wname, dw_rule);
+            op.out = new_value(node.outputs[0], Shape{xs.dims[0], ws.dims[0], OH, OW}, DataType::FLOAT32);
+            ops.push_back(op);
+            return;
+        }
+        // the descriptor one group's dense conv sees
+        tbn_conv2d_desc dg = op.desc;
+        dg.c /= p.groups;
+        dg.m /= p.groups;
         const int kind = op.pw && op.pw->kind == PackedWeights::Kind::Ternary ? TBN_WEIGHTS_TERNARY
                                                                               : TBN_WEIGHTS_BINARY;
         int64_t wbytes = 0;
-        if (op.kind == OpKind::ConvQuant && op.desc.c >= 16 &&
-            tbn_hip_conv_weights_bytes(kind, &op.desc, &wbytes) == TBN_SUCCESS) {
-            // patch conv: conv-layout weights once per Session, then no
-            // allocation and no re-ordering per run
-            const std::string key = wname + "#conv" + std::to_string(reinterpret_cast<uintptr_t>(op.pw));
-            auto it = conv_packed.find(key);
-            if (it == conv_packed.end()) {
-                Tensor cw = Tensor::empty({wbytes}, DataType::UINT8, DeviceType::HIP);
-                check_status(tbn_hip_pack_conv_weights(kind, op.pw->bits.typed_data<uint8_t>(), op.pw->K_pad,
-                                                       op.pw->N_pad, &op.desc, cw.typed_data<uint8_t>(), cur_stream()),
-                             ("Conv '" + node.name + "'").c_str());
-                it = conv_packed.emplace(key, cw).first;
+        if (op.kind == OpKind::ConvQuant && dg.c >= 16 &&
+            tbn_hip_conv_weights_bytes(kind, &dg, &wbytes) == TBN_SUCCESS) {
+            // patch conv: conv-layout weights once per Session (per group),
+            // then no allocation and no re-ordering per run
+            const int64_t col_bytes = kind == TBN_WEIGHTS_BINARY ? op.pw->K_pad / 8 : op.pw->K_pad / 4;
+            for (int64_t g = 0; g < p.groups; ++g) {
+                const std::string key = wname + "#conv" + std::to_string(reinterpret_cast<uintptr_t>(op.pw)) + "g" +
+                                        std::to_string(g) + "/" + std::to_string(p.groups);
+                auto it = conv_packed.find(key);
+                if (it == conv_packed.end()) {
+                    Tensor cw = Tensor::empty({wbytes}, DataType::UINT8, DeviceType::HIP);
+                    check_status(tbn_hip_pack_conv_weights(kind, op.pw->bits.typed_data<uint8_t>() + g * dg.m * col_bytes,
+                                                           op.pw->K_pad, op.pw->N_pad - g * dg.m, &dg,
+                                                           cw.typed_data<uint8_t>(), cur_stream()),
+                                 ("Conv '" + node.name + "'").c_str());
+                    it = conv_packed.emplace(key, cw).first;
+                }
+                op.group_conv_w.push_back(&it->second);
             }
-            op.conv_w = &it->second;
+            op.conv_w = op.group_conv_w[0];
+        }
+        if (p.groups > 1) {
+            const int64_t ws_floats = detail::grouped_conv_workspace(op.desc, p.groups);
+            if (ws_floats) op.workspace = new_value(node.name + "#groups", Shape{ws_floats}, DataType::FLOAT32);
         }
         op.out = new_value(node.outputs[0], Shape{xs.dims[0], ws.dims[0], OH, OW}, DataType::FLOAT32);
         ops.push_back(op);
+    }
+
+    // ONNX BatchNormalization in inference form (not in the reference):
+    // y = (x - mean) / sqrt(var + epsilon) * scale + B over dim 1, as
+    // y = x * k + t; folded into a preceding conv's epilogue by fold_batchnorm.
+    void lower_batchnorm(const ModelNode& node) {
+        TBN_CHECK(node.inputs.size() == 5 && !node.outputs.empty(), InvalidArgumentError,
+                  "BatchNormalization expects 5 inputs");
+        if (auto a = find_attr(node, "training_mode"); a && a->is_int())
+            TBN_CHECK(a->as_int() == 0, NotImplementedError, "BatchNormalization '" + node.name + "': training mode");
+        const int xi = lookup(node.inputs[0], node.name);
+        const Shape xs = values[xi].shape;
+        TBN_CHECK(xs.rank() >= 2, InvalidShapeError, "BatchNormalization input must be at least 2-D");
+        for (int i = 1; i < 5; ++i)
+            TBN_CHECK(graph->initializers.count(node.inputs[i]), NotImplementedError,
+                      "BatchNormalization '" + node.name + "': parameters must be initializers");
+        float eps = 1e-5f;
+        if (auto a = find_attr(node, "epsilon"); a && a->is_float()) eps = a->as_float();
+        std::vector<float> k, t;
+        detail::batch_norm_affine(initializer(node.inputs[1]), initializer(node.inputs[2]),
+                                  initializer(node.inputs[3]), initializer(node.inputs[4]), eps, xs.dims[1], k, t);
+        Op op;
+        op.kind = OpKind::ChannelAffine;
+        op.node = node.name;
+        op.in = {xi};
+        op.bn_k = k;
+        op.bn_t = t;
+        op.scale = derived_floats(node.name + "#bn_k", k);
+        op.bias = derived_floats(node.name + "#bn_t", t);
+        int64_t hw = 1;
+        for (size_t i = 2; i < xs.dims.size(); ++i) hw *= xs.dims[i];
+        op.outer = xs.dims[0];
+        op.inner = xs.dims[1];
+        op.rest = hw;
+        op.out = new_value(node.outputs[0], xs, DataType::FLOAT32);
+        ops.push_back(op);
+    }
+
+    // Device copy of `v`, kept for the Session's lifetime.  An entry already
+    // queued kernels may read is never replaced: other contents get a new key.
+    const float* derived_floats(std::string key, const std::vector<float>& v) {
+        for (;;) {
+            auto it = derived.find(key);
+            if (it == derived.end()) break;
+            const Tensor& t = it->second;
+            if (t.num_elements() == static_cast<int64_t>(v.size())) {
+                const std::vector<float> have = t.to_vector<float>();
+                if (std::memcmp(have.data(), v.data(), v.size() * sizeof(float)) == 0) return t.typed_data<float>();
+            }
+            key += "'";
+        }
+        Tensor d(Shape{static_cast<int64_t>(v.size())}, DataType::FLOAT32, v.data(), DeviceType::HIP);
+        return derived.emplace(key, d).first->second.typed_data<float>();
     }
 
     void lower_gemm(const ModelNode& node, bool matmul) {
@@ -590,6 +709,7 @@ struct TBNModel::Session::Impl {
     void lower(const ModelNode& node) {
         const std::string& t = node.op_type;
         if (t == "Conv") return lower_conv(node);
+        if (t == "BatchNormalization") return lower_batchnorm(node);
         if (t == "Gemm") return lower_gemm(node, false);
         if (t == "MatMul") return lower_gemm(node, true);
         if (t == "Add") return lower_add(node);
@@ -672,6 +792,48 @@ struct TBNModel::Session::Impl {
         (void)old_out;
     }
 
+    // A BatchNormalization reading a conv's output that nothing else reads
+    // becomes part of the conv's epilogue: with v = (acc + a) * s + b,
+    // v * k + t = acc * (s*k) + (a*s*k + b*k + t), products formed in double
+    // and rounded once.  The fp32 conv has no scale stage: its weights are
+    // scaled instead (w * k per output channel).
+    void fold_batchnorm() {
+        for (size_t i = 0; i < ops.size(); ++i) {
+            Op& bn = ops[i];
+            if (bn.dead || bn.kind != OpKind::ChannelAffine) continue;
+            const int p = producer(bn.in[0]);
+            if (p < 0) continue;
+            Op& c = ops[p];
+            const bool conv = c.kind == OpKind::ConvF32 || c.kind == OpKind::ConvQuant || c.kind == OpKind::ConvDepthwise;
+            if (!conv || c.residual >= 0 || (c.flags & (TBN_EPI_RELU | TBN_EPI_MAXPOOL2X2)) ||
+                sole_reader(c.out) != static_cast<int>(i) || static_cast<int64_t>(bn.bn_k.size()) != c.desc.m)
+                continue;
+            const int64_t M = c.desc.m;
+            const bool bts = (c.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
+            const std::vector<float> b = c.bias ? host_floats(c.bias_name) : std::vector<float>(M, 0.0f);
+            const std::vector<float> sc = c.scale ? channel_scales.at(c.scale_name) : std::vector<float>(M, 1.0f);
+            std::vector<float> s2(M), b2(M);
+            for (int64_t m = 0; m < M; ++m) {
+                const double k = bn.bn_k[m], t = bn.bn_t[m], sm = sc[m], bm = b[m];
+                s2[m] = static_cast<float>(sm * k);
+                b2[m] = static_cast<float>((bts ? bm * sm * k : bm * k) + t);
+            }
+            if (c.kind == OpKind::ConvF32) {
+                std::vector<float> w = host_floats(c.weight_name);
+                const int64_t per = static_cast<int64_t>(w.size()) / M;
+                for (int64_t m = 0; m < M; ++m)
+                    for (int64_t j = 0; j < per; ++j)
+                        w[m * per + j] = static_cast<float>(static_cast<double>(w[m * per + j]) * bn.bn_k[m]);
+                c.w = derived_floats(c.node + "#bn_w", w);
+            } else {
+                c.scale = derived_floats(c.node + "#bn_s", s2);
+                c.flags &= ~TBN_EPI_BIAS_THEN_SCALE;
+            }
+            c.bias = derived_floats(c.node + "#bn_b", b2);
+            absorb(p, static_cast<int>(i));
+        }
+    }
+
     // For Add(conv_out, other) where `other` is produced after the conv but
     // from values that exist before it (a ResNet projection shortcut in
     // export order), move other's producer in front of the conv so the add
@@ -698,14 +860,17 @@ struct TBNModel::Session::Impl {
     }
 
     void fuse() {
+        fold_batchnorm();
         hoist_residual_producers();
         for (size_t i = 0; i < ops.size(); ++i) {
             Op& op = ops[i];
             if (op.dead) continue;
-            const bool conv = op.kind == OpKind::ConvQuant || op.kind == OpKind::ConvF32;
+            const bool conv = op.kind == OpKind::ConvQuant || op.kind == OpKind::ConvF32 ||
+                              op.kind == OpKind::ConvDepthwise;
             const bool gemm = op.kind == OpKind::GemmQuant || op.kind == OpKind::GemmF32;
             // residual Add (+Relu) into a quantized conv whose addend is ready
-            if (op.kind == OpKind::ConvQuant && !(op.flags & (TBN_EPI_RELU | TBN_EPI_MAXPOOL2X2))) {
+            if (((op.kind == OpKind::ConvQuant && op.groups == 1) || op.kind == OpKind::ConvDepthwise) &&
+                !(op.flags & (TBN_EPI_RELU | TBN_EPI_MAXPOOL2X2))) {
                 int r = sole_reader(op.out);
                 if (r >= 0 && ops[r].kind == OpKind::Add) {
                     const int other = ops[r].in[0] == op.out ? ops[r].in[1] : ops[r].in[0];
@@ -720,7 +885,8 @@ struct TBNModel::Session::Impl {
                 }
             }
             // Relu into Conv / Gemm / Add
-            if ((conv || gemm || op.kind == OpKind::Add) && !(op.flags & TBN_EPI_MAXPOOL2X2)) {
+            if ((conv || gemm || op.kind == OpKind::Add || op.kind == OpKind::ChannelAffine) &&
+                !(op.flags & TBN_EPI_MAXPOOL2X2)) {
                 int r = sole_reader(op.out);
                 if (r >= 0 && ops[r].kind == OpKind::Relu) {
                     op.flags |= TBN_EPI_RELU;
@@ -728,7 +894,7 @@ struct TBNModel::Session::Impl {
                 }
             }
             // 2x2/2 floor MaxPool (with or without a Relu either side) into Conv
-            if (conv && op.residual < 0) {
+            if (conv && op.residual < 0 && op.groups == 1 && op.kind != OpKind::ConvDepthwise) {
                 int r = sole_reader(op.out);
                 if (r >= 0 && ops[r].kind == OpKind::MaxPool) {
                     const Pool2DParams& p = ops[r].pool;
@@ -844,7 +1010,8 @@ struct TBNModel::Session::Impl {
         plan_memory();
         launches = 0;
         for (const auto& op : ops)
-            if (!op.dead && op.kind != OpKind::View) ++launches;
+            if (!op.dead && op.kind != OpKind::View)
+                launches += op.groups > 1 && op.kind != OpKind::ConvDepthwise ? op.groups * (op.desc.n == 1 ? 1 : 3) : 1;
         planned = true;
         plan_quant = quant;
         plan_shapes.clear();
@@ -863,16 +1030,59 @@ struct TBNModel::Session::Impl {
 
     // ---- execution ---------------------------------------------------------------------
 
+    // A grouped conv with more than one input channel per group: one dense
+    // conv per group on channel slices of the input and output.
+    void launch_grouped(Op& op, tbn_stream_t s, const std::string& what) {
+        const int64_t G = op.groups, Mg = op.desc.m / G;
+        const int64_t w_per_group = Mg * (op.desc.c / G) * op.desc.kh * op.desc.kw;
+        const bool ternary = op.pw && op.pw->kind == PackedWeights::Kind::Ternary;
+        const int wkind = ternary ? TBN_WEIGHTS_TERNARY : TBN_WEIGHTS_BINARY;
+        detail::run_grouped_conv(
+            op.desc, G, fp(op.in[0]), fp(op.out), op.workspace >= 0 ? fp(op.workspace) : nullptr,
+            [&](int64_t g, const float* xg, const tbn_conv2d_desc& dg, float* yg) {
+                const float* sc = op.scale ? op.scale + g * Mg : nullptr;
+                const float* bi = op.bias ? op.bias + g * Mg : nullptr;
+                if (op.kind == OpKind::ConvF32) {
+                    check_status(tbn_hip_conv2d_f32(xg, &dg, op.w + g * w_per_group, bi, op.flags, yg, s), what.c_str());
+                } else if (!op.group_conv_w.empty()) {
+                    check_status(tbn_hip_conv2d_f32_prepacked(wkind, xg, &dg, op.group_conv_w[g]->typed_data<uint8_t>(),
+                                                              sc, 1.0f, bi, nullptr, op.flags, yg, s),
+                                 what.c_str());
+                } else {
+                    const int64_t col_bytes = ternary ? op.pw->K_pad / 4 : op.pw->K_pad / 8;
+                    check_status(tbn_hip_conv2d_f32_quantized(wkind, xg, &dg,
+                                                              op.pw->bits.typed_data<uint8_t>() + g * Mg * col_bytes,
+                                                              op.pw->K_pad, op.pw->N_pad - g * Mg, sc, 1.0f, bi,
+                                                              nullptr, op.flags, yg, s),
+                                 what.c_str());
+                }
+            },
+            s);
+    }
+
     void launch(Op& op, tbn_stream_t s) {
         const std::string what = "node '" + op.node + "'";
         switch (op.kind) {
             case OpKind::View:
                 return;
             case OpKind::ConvF32:
+                if (op.groups > 1) return launch_grouped(op, s, what);
                 check_status(tbn_hip_conv2d_f32(fp(op.in[0]), &op.desc, op.w, op.bias, op.flags, fp(op.out), s),
                              what.c_str());
                 return;
+            case OpKind::ConvDepthwise:
+                check_status(tbn_hip_conv2d_depthwise(fp(op.in[0]), &op.desc, op.w, op.scale, 1.0f, op.bias,
+                                                      op.residual >= 0 ? fp(op.residual) : nullptr, op.flags,
+                                                      fp(op.out), s),
+                             what.c_str());
+                return;
+            case OpKind::ChannelAffine:
+                check_status(tbn_hip_channel_affine(fp(op.in[0]), op.outer, op.inner, op.rest, op.scale, op.bias,
+                                                    op.flags, fp(op.out), s),
+                             what.c_str());
+                return;
             case OpKind::ConvQuant:
+                if (op.groups > 1) return launch_grouped(op, s, what);
                 if (op.conv_w) {
                     check_status(tbn_hip_conv2d_f32_prepacked(
                                      op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY

@@ -1,5 +1,6 @@
 // Operator entry points of the tbn runtime: argument checks in the
 // reference's terms, then HIP kernels of libtbn_hip.so on the current stream.
+#include <cmath>
 #include <string>
 #include <vector>
 
@@ -54,12 +55,14 @@ ConvShape conv_shape(const Tensor& input, const Tensor& weights, const Conv2DPar
     TBN_CHECK(weights.shape().rank() == 4, InvalidShapeError,
               "Conv2D weights must be 4D (MCHW), got " + shape_to_string(weights.shape()));
     require_float(input, "Conv2D input");
-    TBN_CHECK(p.groups == 1, NotImplementedError, "grouped convolution is not supported (groups must be 1)");
     const auto& x = input.shape().dims;
     const auto& w = weights.shape().dims;
-    TBN_CHECK(x[1] == w[1], InvalidShapeError,
+    TBN_CHECK(p.groups >= 1, InvalidArgumentError, "Groups must be positive");
+    TBN_CHECK(x[1] % p.groups == 0 && w[0] % p.groups == 0, InvalidShapeError,
+              "Input and output channels must be divisible by groups");
+    TBN_CHECK(x[1] == w[1] * p.groups, InvalidShapeError,
               "Input channels (" + std::to_string(x[1]) + ") must match weight channels (" +
-                  std::to_string(w[1]) + ")");
+                  std::to_string(w[1]) + ") times groups");
     ConvShape cs;
     cs.desc = tbn_conv2d_desc{x[0], x[1], x[2], x[3], w[0], w[2], w[3], p.stride_h, p.stride_w,
                               p.pad_h, p.pad_w, p.dilation_h, p.dilation_w};
@@ -259,6 +262,74 @@ Tensor qlinear_matmul_ternary(const Tensor& a, const Tensor& b, float b_scale, c
     return qlinear_matmul_packed(a, pack_ternary_weights(b, false), b_scale);
 }
 
+// conv2d.cpp:372-384 (which throws for groups > 1).
+Tensor conv2d_grouped(const Tensor& input, const Tensor& weights, const Tensor* bias, int64_t groups,
+                      const Conv2DParams& params) {
+    Conv2DParams p = params;
+    p.groups = groups;
+    ConvShape cs = conv_shape(input, weights, p);
+    require_float(weights, "Conv2D weights");
+    check_bias(bias, cs.desc.m);
+    if (groups == 1) return conv2d(input, weights, bias, p);
+    Tensor x = on_device(input), w = on_device(weights);
+    Tensor b = bias ? on_device(*bias) : Tensor();
+    Tensor y = Tensor::empty({cs.desc.n, cs.desc.m, cs.OH, cs.OW}, DataType::FLOAT32, DeviceType::HIP);
+    const float* wp = w.typed_data<float>();
+    const float* bp = bias ? b.typed_data<float>() : nullptr;
+    if (cs.desc.c == groups) {
+        check_status(tbn_hip_conv2d_depthwise(x.typed_data<float>(), &cs.desc, wp, nullptr, 1.0f, bp, nullptr, 0,
+                                              y.typed_data<float>(), stream()),
+                     "depthwise_conv2d");
+        return deliver(y, input);
+    }
+    const int64_t ws_floats = detail::grouped_conv_workspace(cs.desc, groups);
+    Tensor ws = ws_floats ? Tensor::empty({ws_floats}, DataType::FLOAT32, DeviceType::HIP) : Tensor();
+    const int64_t wpg = weights.num_elements() / groups;  // weights per group
+    detail::run_grouped_conv(
+        cs.desc, groups, x.typed_data<float>(), y.typed_data<float>(), ws_floats ? ws.typed_data<float>() : nullptr,
+        [&](int64_t g, const float* xg, const tbn_conv2d_desc& dg, float* yg) {
+            check_status(tbn_hip_conv2d_f32(xg, &dg, wp + g * wpg, bp ? bp + g * dg.m : nullptr, 0, yg, stream()),
+                         "conv2d_grouped");
+        },
+        stream());
+    return deliver(y, input);
+}
+
+// conv2d.cpp:386-393: groups = input channels.
+Tensor depthwise_conv2d(const Tensor& input, const Tensor& weights, const Tensor* bias, const Conv2DParams& params) {
+    TBN_CHECK(input.shape().rank() == 4, InvalidShapeError, "Conv2D input must be 4D (NCHW)");
+    return conv2d_grouped(input, weights, bias, input.shape().dims[1], params);
+}
+
+// conv2d.cpp:396-403: the same dilation on both axes.
+Tensor dilated_conv2d(const Tensor& input, const Tensor& weights, const Tensor* bias, int64_t dilation,
+                      const Conv2DParams& params) {
+    Conv2DParams p = params;
+    p.dilation_h = dilation;
+    p.dilation_w = dilation;
+    return conv2d(input, weights, bias, p);
+}
+
+Tensor batch_norm(const Tensor& input, const Tensor& scale, const Tensor& B, const Tensor& mean, const Tensor& var,
+                  float epsilon) {
+    require_float(input, "BatchNormalization input");
+    const auto& d = input.shape().dims;
+    TBN_CHECK(d.size() >= 2, InvalidShapeError, "BatchNormalization input must be at least 2-D");
+    const int64_t c = d[1];
+    std::vector<float> k, t;
+    detail::batch_norm_affine(scale, B, mean, var, epsilon, c, k, t);
+    int64_t hw = 1;
+    for (size_t i = 2; i < d.size(); ++i) hw *= d[i];
+    Tensor x = on_device(input);
+    Tensor kd = Tensor(Shape{c}, DataType::FLOAT32, k.data(), DeviceType::HIP);
+    Tensor td = Tensor(Shape{c}, DataType::FLOAT32, t.data(), DeviceType::HIP);
+    Tensor y = Tensor::empty(input.shape(), DataType::FLOAT32, DeviceType::HIP);
+    check_status(tbn_hip_channel_affine(x.typed_data<float>(), d[0], c, hw, kd.typed_data<float>(),
+                                        td.typed_data<float>(), 0, y.typed_data<float>(), stream()),
+                 "batch_norm");
+    return deliver(y, input);
+}
+
 Tensor gemm(const Tensor& A, const Tensor& B, const Tensor* C, float alpha, float beta, bool transA,
             bool transB) {
     TBN_CHECK(A.dtype() == DataType::FLOAT32, InvalidArgumentError, "gemm requires float32 input A");
@@ -290,6 +361,7 @@ Tensor gemm(const Tensor& A, const Tensor& B, const Tensor* C, float alpha, floa
 // ---- convolution -------------------------------------------------------------------------
 
 Tensor conv2d(const Tensor& input, const Tensor& weights, const Tensor* bias, const Conv2DParams& params) {
+    if (params.groups != 1) return conv2d_grouped(input, weights, bias, params.groups, params);
     ConvShape cs = conv_shape(input, weights, params);
     require_float(weights, "Conv2D weights");
     check_bias(bias, cs.desc.m);
@@ -303,6 +375,7 @@ Tensor conv2d(const Tensor& input, const Tensor& weights, const Tensor* bias, co
 }
 
 Tensor conv2d_binary(const Tensor& input, const Tensor& weights, const Tensor* bias, const Conv2DParams& params) {
+    TBN_CHECK(params.groups == 1, NotImplementedError, "grouped binary/ternary convolution: use a Session");
     ConvShape cs = conv_shape(input, weights, params);
     TBN_CHECK(weights.dtype() == DataType::BINARY, InvalidArgumentError, "conv2d_binary needs BINARY weights");
     check_bias(bias, cs.desc.m);
@@ -310,6 +383,7 @@ Tensor conv2d_binary(const Tensor& input, const Tensor& weights, const Tensor* b
 }
 
 Tensor conv2d_ternary(const Tensor& input, const Tensor& weights, const Tensor* bias, const Conv2DParams& params) {
+    TBN_CHECK(params.groups == 1, NotImplementedError, "grouped binary/ternary convolution: use a Session");
     ConvShape cs = conv_shape(input, weights, params);
     TBN_CHECK(weights.dtype() == DataType::TERNARY, InvalidArgumentError, "conv2d_ternary needs TERNARY weights");
     check_bias(bias, cs.desc.m);
@@ -318,6 +392,7 @@ Tensor conv2d_ternary(const Tensor& input, const Tensor& weights, const Tensor* 
 
 Tensor conv2d_binary_with_scales(const Tensor& input, const Tensor& weights, const Tensor* bias,
                                  const Conv2DParams& params, const std::vector<float>& channel_scales) {
+    TBN_CHECK(params.groups == 1, NotImplementedError, "grouped binary/ternary convolution: use a Session");
     ConvShape cs = conv_shape(input, weights, params);
     TBN_CHECK(weights.dtype() == DataType::BINARY, InvalidArgumentError,
               "conv2d_binary_with_scales needs BINARY weights");
@@ -369,6 +444,61 @@ Tensor relu(const Tensor& input) {
 }
 
 namespace detail {
+
+void conv_out_hw(const tbn_conv2d_desc& d, int64_t& OH, int64_t& OW) {
+    OH = (d.h + 2 * d.ph - d.dh * (d.kh - 1) - 1) / d.sh + 1;
+    OW = (d.w + 2 * d.pw - d.dw * (d.kw - 1) - 1) / d.sw + 1;
+}
+
+void batch_norm_affine(const Tensor& scale, const Tensor& B, const Tensor& mean, const Tensor& var, float epsilon,
+                       int64_t c, std::vector<float>& k, std::vector<float>& t) {
+    const Tensor* parts[4] = {&scale, &B, &mean, &var};
+    for (const Tensor* p : parts)
+        TBN_CHECK(p->dtype() == DataType::FLOAT32 && p->num_elements() == c, InvalidShapeError,
+                  "BatchNormalization parameters must be FLOAT32 with one value per channel");
+    const std::vector<float> s = scale.to_vector<float>(), b = B.to_vector<float>(), m = mean.to_vector<float>(),
+                             v = var.to_vector<float>();
+    k.resize(c);
+    t.resize(c);
+    for (int64_t i = 0; i < c; ++i) {
+        const double ki = static_cast<double>(s[i]) / std::sqrt(static_cast<double>(v[i]) + static_cast<double>(epsilon));
+        k[i] = static_cast<float>(ki);
+        t[i] = static_cast<float>(static_cast<double>(b[i]) - static_cast<double>(m[i]) * ki);
+    }
+}
+
+int64_t grouped_conv_workspace(const tbn_conv2d_desc& d, int64_t groups) {
+    if (d.n <= 1) return 0;
+    int64_t OH, OW;
+    conv_out_hw(d, OH, OW);
+    return d.n * (d.c / groups * d.h * d.w + d.m / groups * OH * OW);
+}
+
+void run_grouped_conv(const tbn_conv2d_desc& d, int64_t groups, const float* x, float* y, float* workspace,
+                      const std::function<void(int64_t, const float*, const tbn_conv2d_desc&, float*)>& conv,
+                      tbn_stream_t stream) {
+    int64_t OH, OW;
+    conv_out_hw(d, OH, OW);
+    tbn_conv2d_desc dg = d;
+    dg.c = d.c / groups;
+    dg.m = d.m / groups;
+    const int64_t hw = d.h * d.w, ohw = OH * OW;
+    const bool direct = d.n == 1;
+    TBN_CHECK(direct || workspace != nullptr, RuntimeError, "grouped conv: missing workspace");
+    float* xg = workspace;
+    float* yg = direct ? nullptr : workspace + d.n * dg.c * hw;
+    for (int64_t g = 0; g < groups; ++g) {
+        if (direct) {
+            conv(g, x + g * dg.c * hw, dg, y + g * dg.m * ohw);
+            continue;
+        }
+        check_status(tbn_hip_copy_channels(x, d.n, d.c, g * dg.c, dg.c, hw, xg, dg.c, 0, stream), "grouped conv gather");
+        conv(g, xg, dg, yg);
+        check_status(tbn_hip_copy_channels(yg, d.n, dg.m, 0, dg.m, ohw, y, d.m, g * dg.m, stream),
+                     "grouped conv scatter");
+    }
+}
+
 void add_view(const Shape& a, const Shape& b, int64_t& outer, int64_t& inner, int64_t& rest) {
     const auto& da = a.dims;
     const auto& db = b.dims;

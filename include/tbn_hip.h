@@ -260,6 +260,34 @@ int tbn_hip_conv2d_f32_prepacked(int weights, const float* x, const tbn_conv2d_d
  * flags: TBN_EPI_RELU, TBN_EPI_MAXPOOL2X2. */
 int tbn_hip_conv2d_f32(const float* x, const tbn_conv2d_desc* desc, const float* w,
                        const float* bias, int flags, float* y, tbn_stream_t stream);
+/* ---- grouped convolution and BatchNormalization ---------------------------
+ * The reference's conv2d_grouped / depthwise_conv2d throw for groups > 1
+ * (conv2d.cpp:372-393) and it has no BatchNormalization; these are new.  A
+ * grouped conv with more than one input channel per group runs each group
+ * through the dense entry points above on channel slices (tbn::conv2d_grouped
+ * and the Session do this), gathering and scattering the slices with
+ * tbn_hip_copy_channels when the batch is larger than one. */
+
+/* Depthwise Conv2D: one input channel per group (groups = desc->c), desc->m a
+ * multiple of desc->c, output channel m reading input channel m / (m/c);
+ * weights fp32 [M, 1, kh, kw] (for a quantized layer the exact +-1 or
+ * -1/0/+1 values).  Epilogue as tbn_hip_conv2d_f32_quantized: acc*alpha*s[m]
+ * + b[m], or (acc + b[m])*alpha*s[m] with TBN_EPI_BIAS_THEN_SCALE; scale and
+ * bias may be NULL; then + residual (may be NULL), then TBN_EPI_RELU.
+ * Replaces tbn::depthwise_conv2d (conv2d.cpp:386-393). */
+int tbn_hip_conv2d_depthwise(const float* x, const tbn_conv2d_desc* desc, const float* w,
+                             const float* scale, float alpha, const float* bias, const float* residual,
+                             int flags, float* y, tbn_stream_t stream);
+/* dst[i, dst_c0 + j, :] = src[i, src_c0 + j, :] for i < n, j < count, over
+ * rows of hw floats of src [n, src_c, hw] and dst [n, dst_c, hw]. */
+int tbn_hip_copy_channels(const float* src, int64_t n, int64_t src_c, int64_t src_c0, int64_t count,
+                          int64_t hw, float* dst, int64_t dst_c, int64_t dst_c0, tbn_stream_t stream);
+/* y[i, j, :] = x[i, j, :] * k[j] + t[j] (one fma), then TBN_EPI_RELU, over
+ * [n, c, hw]: an inference BatchNormalization with k = scale/sqrt(var + eps)
+ * and t = B - mean*k. */
+int tbn_hip_channel_affine(const float* x, int64_t n, int64_t c, int64_t hw, const float* k, const float* t,
+                           int flags, float* y, tbn_stream_t stream);
+
 /* fp32 GEMM (tbn::gemm, gemm.cpp:349-360): out = alpha*op(A)*op(B) + beta*C,
  * C NULL, [N] (c_is_1d) or [M, N]; flags: TBN_EPI_RELU. */
 int tbn_hip_gemm_f32(const float* A, const float* B, const float* Cin, int c_is_1d,

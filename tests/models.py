@@ -193,13 +193,38 @@ def _conv_attrs(attrs):
     return (s[0], s[1]), (p[0], p[1]), (d[0], d[1])
 
 
+class _Grouped:
+    """The oracle's conv2d_f64 / conv2d_f32 applied group by group: group g
+    convolves input channels [g*C/G, (g+1)*C/G) with output channels
+    [g*M/G, (g+1)*M/G) of the [M, C/G, kh, kw] weights (the definition of a
+    grouped convolution); every other oracle function passes through."""
+
+    def __init__(self, orc, groups):
+        self._orc, self._g = orc, groups
+
+    def __getattr__(self, name):
+        fn = getattr(self._orc, name)
+        if self._g == 1 or name not in ("conv2d_f64", "conv2d_f32"):
+            return fn
+
+        def grouped(x, w, bias=None, stride=(1, 1), pad=(0, 0), dil=(1, 1)):
+            cg, mg = x.shape[1] // self._g, w.shape[0] // self._g
+            outs = [fn(np.ascontiguousarray(x[:, g * cg:(g + 1) * cg]), np.ascontiguousarray(w[g * mg:(g + 1) * mg]),
+                       None if bias is None else np.ascontiguousarray(bias[g * mg:(g + 1) * mg]), stride, pad, dil)
+                    for g in range(self._g)]
+            return np.concatenate(outs, axis=1)
+        return grouped
+
+
 def run_oracle(spec, feeds, quant, orc, record=None):
     """Executes the graph on the CPU (float64 products, fp32 values between
     nodes) with the reference Session's branch structure.  Returns
     {output name: array}; `record`, if a dict, receives every value."""
     env = {k: np.asarray(v) for k, v in spec.inits.items()}
     env.update({k: np.asarray(v, np.float32) for k, v in feeds.items()})
+    orc_base = orc
     for n in spec.nodes:
+        orc = orc_base
         a = n.attrs
         quant_here = quant and a.get("tbn_quantize", 1) != 0
         if n.op == "Conv":
@@ -208,6 +233,8 @@ def run_oracle(spec, feeds, quant, orc, record=None):
             W = env[wname]
             b = env[n.inputs[2]].astype(np.float64) if len(n.inputs) > 2 else None
             stride, pad, dil = _conv_attrs(a)
+            groups = int(a.get("group", 1))
+            orc = _Grouped(orc_base, groups)
             dt = spec.init_dtypes.get(wname, "float32")
             if dt == "binary":
                 y = orc.conv2d_f64(x, np.where(W == 1, 1.0, -1.0).astype(np.float32), None, stride, pad, dil)
@@ -269,6 +296,13 @@ def run_oracle(spec, feeds, quant, orc, record=None):
             x = env[n.inputs[0]]
             ax = a.get("axis", 1)
             y = x.reshape(int(np.prod(x.shape[:ax])), -1)
+        elif n.op == "BatchNormalization":
+            # ONNX inference form: (x - mean) / sqrt(var + eps) * scale + B over dim 1
+            x = env[n.inputs[0]].astype(np.float64)
+            sc, bb, mu, var = (env[k].astype(np.float64) for k in n.inputs[1:5])
+            shp = (1, -1) + (1,) * (x.ndim - 2)
+            eps = np.float64(np.float32(a.get("epsilon", 1e-5)))
+            y = (x - mu.reshape(shp)) / np.sqrt(var.reshape(shp) + eps) * sc.reshape(shp) + bb.reshape(shp)
         elif n.op == "Reshape":
             # model.hpp:1039-1090: the shape input, one -1 inferred
             y = env[n.inputs[0]].reshape([int(d) for d in env[n.inputs[1]].reshape(-1)])
