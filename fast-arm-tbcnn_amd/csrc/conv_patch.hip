@@ -56,6 +56,9 @@ struct PatchGeom {
     // split-K over blocks: split s takes chunks [s * cps, min(chunks, (s + 1) * cps))
     // and writes raw sums; blocks_split = blocks of one split
     int splits, cps, blocks_split;
+    // 1: one LDS buffer (the next chunk waits in the staging registers and is
+    // stored after a barrier), for twice the blocks per CU; 0: two buffers
+    int single;
 };
 
 // Buffer resource (gfx9 word 3: raw dword addressing) over `bytes` from base;
@@ -354,7 +357,8 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
 
     load_chunk(cb);
     store_chunk(0);
-    float* epi_lds = reinterpret_cast<float*>(lds + 2 * buf_elems);  // [BM] multipliers, [BM] addends
+    // [BM] multipliers, [BM] addends after the buffer(s)
+    float* epi_lds = reinterpret_cast<float*>(lds + (g.single ? 1 : 2) * buf_elems);
     if (tid < Cfg::BM) {
         epi_lds[tid] = epi.alpha * raw_scale;
         epi_lds[Cfg::BM + tid] = raw_bias;
@@ -369,7 +373,7 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     const int tap_ds = g.dw * kPix;
     const int tap_dr = g.dh * g.PWi * kPix;
     for (int ch = cb; ch < ce; ++ch) {
-        const uint16_t* cur = lds + ((ch - cb) & 1) * buf_elems;
+        const uint16_t* cur = lds + (g.single ? 0 : ((ch - cb) & 1)) * buf_elems;
         auto read_b = [&](int toff, int kk, u32x4_t (&b)[3][Cfg::FC]) {
 #pragma unroll
             for (int p = 0; p < 3; ++p)
@@ -470,7 +474,8 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
             }
         }
         if (ch + 1 < ce) {
-            store_chunk((ch + 1 - cb) & 1);
+            if (g.single) __syncthreads();  // every wave is done reading the buffer
+            store_chunk(g.single ? 0 : (ch + 1 - cb) & 1);
             if (ch + 2 < ce) load_chunk(ch + 2);
         }
         __syncthreads();
@@ -681,15 +686,17 @@ struct TileChoice {
     int cfg;     // index into the PatchCfg menu
     int linear;  // 1: linear tiles, 0: 2-D tiles
     int TH, TW, BM, NT;
+    int single;  // 1: one LDS buffer
 };
 
 size_t lds_bytes(const PatchGeom& g, int BM, bool ternary) {
     const size_t buf = static_cast<size_t>(patch_buffer_elems(g.PHi * g.PWi, BM * g.taps, ternary ? 4 : 2)) * 2;
-    return 2 * buf + 2 * sizeof(float) * BM;  // two buffers + epilogue factors
+    return (g.single ? 1 : 2) * buf + 2 * sizeof(float) * BM;  // buffer(s) + epilogue factors
 }
 
 void fill_patch(PatchGeom& g, const TileChoice& c) {
     g.linear = c.linear;
+    g.single = c.single;
     int rows, cols;  // output rows / columns one tile's pixels span (at most)
     if (c.linear) {
         const int per = g.pool ? c.TH * c.TW / 4 : c.TH * c.TW;
@@ -739,14 +746,13 @@ using P7 = PatchCfg<64, 8, 8, 64, 32>;    // 64 channels per wave: each pixel fr
 using P8 = PatchCfg<64, 8, 16, 64, 32>;
 
 template <class Cfg>
-constexpr TileChoice choice(int cfg, int linear) {
-    return TileChoice{cfg, linear, Cfg::TH, Cfg::TW, Cfg::BM, Cfg::NT};
+constexpr TileChoice choice(int cfg, int linear, int single = 0) {
+    return TileChoice{cfg, linear, Cfg::TH, Cfg::TW, Cfg::BM, Cfg::NT, single};
 }
 
-// TBN_CONV_TILE=<id> forces a tile (tuning only): id = cfg for linear tiles,
-// 10 + cfg for 2-D tiles.
-// TBN_CONV_TILE=<id> forces one tile (id = menu index for linear tiles,
-// 10 + index for 2-D tiles): a tuning aid, read on every call.
+// TBN_CONV_TILE=<id> forces one tile, a tuning aid read on every call: id =
+// cfg for linear tiles, 10 + cfg for 2-D tiles, plus 20 for the one-buffer
+// variants.
 int tile_override() {
     const char* e = std::getenv("TBN_CONV_TILE");
     return e ? std::atoi(e) : -1;
@@ -759,7 +765,14 @@ int tile_override() {
 constexpr TileChoice kMenu[] = {choice<P0>(0, 1), choice<P1>(1, 1), choice<P2>(2, 1), choice<P3>(3, 1),
                                 choice<P4>(4, 1), choice<P7>(7, 1), choice<P8>(8, 1), choice<P0>(0, 0),
                                 choice<P1>(1, 0), choice<P2>(2, 0), choice<P3>(3, 0), choice<P4>(4, 0),
-                                choice<P5>(5, 0), choice<P6>(6, 0), choice<P7>(7, 0), choice<P8>(8, 0)};
+                                choice<P5>(5, 0), choice<P6>(6, 0), choice<P7>(7, 0), choice<P8>(8, 0),
+                                // one LDS buffer: twice the blocks per CU (or a
+                                // patch that fits only so); considered after the
+                                // two-buffer tiles, and by the measured choice
+                                choice<P0>(0, 1, 1), choice<P1>(1, 1, 1), choice<P2>(2, 1, 1), choice<P3>(3, 1, 1),
+                                choice<P7>(7, 1, 1), choice<P8>(8, 1, 1), choice<P0>(0, 0, 1), choice<P1>(1, 0, 1),
+                                choice<P2>(2, 0, 1), choice<P3>(3, 0, 1), choice<P6>(6, 0, 1), choice<P7>(7, 0, 1),
+                                choice<P8>(8, 0, 1)};
 
 // A tile can run this geometry: its patch fits the LDS and the staging
 // registers (8 items per thread for the patch and for the weight words).
@@ -775,7 +788,7 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
     int64_t best_blocks = -1;
     const int forced = tile_override();
     for (const auto& c : kMenu) {
-        const int id = c.linear ? c.cfg : 10 + c.cfg;
+        const int id = (c.linear ? c.cfg : 10 + c.cfg) + 20 * c.single;
         if (forced >= 0 && id != forced) continue;
         if (forced < 0) {
             if (g.M <= 32 && c.BM != 32) continue;
@@ -998,6 +1011,7 @@ int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
             splits *= 2;
     }
     if (const char* e = std::getenv("TBN_CONV_SPLITS")) splits = std::max(1, std::atoi(e));  // tuning aid
+    g.single = 0;
     g.cps = (g.chunks + splits - 1) / splits;
     g.splits = (g.chunks + g.cps - 1) / g.cps;
     g.blocks_split = 0;

@@ -287,3 +287,58 @@ def test_conv_patch_split_k_residual_and_ternary(dev, orc):
                  P(to_dev(bias)), 0, P(y2), None)
     ref2 = conv_ref(x, t.reshape(M, C, 3, 3).astype(np.float32), scale, 1.0, bias, (1, 1), (1, 1), (1, 1), 0)
     rm.assert_within_tolerance(host(y2), ref2, K, np.abs(x).max() * 1.5)
+
+
+@pytest.mark.parametrize("case", [(2, 64, 14, 14, 128, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_RELU),
+                                  (3, 96, 12, 10, 64, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_MAXPOOL2X2),
+                                  (2, 256, 7, 7, 96, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_BIAS_THEN_SCALE),
+                                  (2, 64, 15, 13, 64, 1, 1, (2, 2), (0, 0), (1, 1), 0)])
+def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
+    """Each tile of the menu (forced with TBN_CONV_TILE: linear and 2-D tiles,
+    with two LDS buffers or one) sums every output in the same order, so all
+    feasible tiles give bit-identical outputs; one of them is checked against
+    the float64 oracle."""
+    import os
+    N, C, H, W, M, kh, kw, stride, pad, dil, flags = case
+    rng = np.random.default_rng(C * 17 + M)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    wbytes = (rng.random((M, C, kh, kw)) < 0.5).astype(np.uint8)
+    scale = rng.uniform(0.5, 1.5, M).astype(np.float32)
+    bias = (rng.standard_normal(M) * 0.01).astype(np.float32)
+    K = C * kh * kw
+    packed, K_pad, N_pad = pack_conv_weights(wbytes, M, K)
+    d = tbn_hip.conv_desc(N, C, H, W, M, kh, kw, *stride, *pad, *dil)
+    OH, OW = tbn_hip.conv_out_hw(d)
+    oshape = (N, M, OH // 2, OW // 2) if flags & tbn_hip.EPI_MAXPOOL2X2 else (N, M, OH, OW)
+    import ctypes
+    wb = ctypes.c_int64()
+    tbn_hip.call("tbn_hip_conv_weights_bytes", tbn_hip.WEIGHTS_BINARY, d, ctypes.byref(wb))
+    cw = empty(wb.value, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_conv_weights", tbn_hip.WEIGHTS_BINARY, P(packed), K_pad, N_pad, d, P(cw), None)
+    dx, ds, db = to_dev(x), to_dev(scale), to_dev(bias)
+    outs = {}
+    old = os.environ.get("TBN_CONV_TILE")
+    try:
+        for tile in [t for base in (0, 10, 20, 30) for t in range(base, base + 9)]:
+            os.environ["TBN_CONV_TILE"] = str(tile)
+            y = empty(oshape, torch.float32)
+            y.fill_(np.nan)
+            # the pre-packed entry point runs only the patch kernel (no fallback)
+            rc = tbn_hip.lib().tbn_hip_conv2d_f32_prepacked(tbn_hip.WEIGHTS_BINARY, P(dx), d, P(cw), P(ds), 1.0,
+                                                            P(db), None, flags, P(y), None)
+            if rc == tbn_hip.INVALID_SHAPE:
+                continue  # this tile cannot hold the geometry
+            assert rc == 0, tbn_hip.last_error()
+            outs[tile] = host(y)
+    finally:
+        if old is None:
+            os.environ.pop("TBN_CONV_TILE", None)
+        else:
+            os.environ["TBN_CONV_TILE"] = old
+    assert any(t >= 20 for t in outs) and any(t < 20 for t in outs), sorted(outs)
+    first = next(iter(outs.values()))
+    for tile, y in outs.items():
+        assert np.array_equal(y, first), f"tile {tile} differs"
+    wsign = np.where(wbytes == 1, 1.0, -1.0).astype(np.float32)
+    ref = conv_ref(x, wsign, scale, 1.0, bias, stride, pad, dil, flags)
+    rm.assert_within_tolerance(first, ref, K, np.abs(x).max() * 1.5)
