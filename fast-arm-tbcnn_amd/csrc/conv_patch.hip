@@ -744,6 +744,7 @@ using P5 = PatchCfg<128, 4, 8, 64, 32>;   // small 2-D patches (strided / large 
 using P6 = PatchCfg<64, 4, 8, 32, 32>;
 using P7 = PatchCfg<64, 8, 8, 64, 32>;    // 64 channels per wave: each pixel fragment feeds 2 MFMAs
 using P8 = PatchCfg<64, 8, 16, 64, 32>;
+using P9 = PatchCfg<128, 8, 8, 32, 32>;   // 8 waves: two per SIMD share a tile
 
 template <class Cfg>
 constexpr TileChoice choice(int cfg, int linear, int single = 0) {
@@ -772,7 +773,8 @@ constexpr TileChoice kMenu[] = {choice<P0>(0, 1), choice<P1>(1, 1), choice<P2>(2
                                 choice<P0>(0, 1, 1), choice<P1>(1, 1, 1), choice<P2>(2, 1, 1), choice<P3>(3, 1, 1),
                                 choice<P7>(7, 1, 1), choice<P8>(8, 1, 1), choice<P0>(0, 0, 1), choice<P1>(1, 0, 1),
                                 choice<P2>(2, 0, 1), choice<P3>(3, 0, 1), choice<P6>(6, 0, 1), choice<P7>(7, 0, 1),
-                                choice<P8>(8, 0, 1)};
+                                choice<P8>(8, 0, 1), choice<P9>(9, 1), choice<P9>(9, 0), choice<P9>(9, 1, 1),
+                                choice<P9>(9, 0, 1)};
 
 // A tile can run this geometry: its patch fits the LDS and the staging
 // registers (8 items per thread for the patch and for the weight words).
@@ -864,7 +866,8 @@ int dispatch_patch(int id, const float* x, const PatchGeom& g, const uint8_t* w,
         case 5: return launch_patch<P5, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
         case 6: return launch_patch<P6, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
         case 7: return launch_patch<P7, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
-        default: return launch_patch<P8, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 8: return launch_patch<P8, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        default: return launch_patch<P9, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
     }
 }
 

@@ -319,7 +319,7 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
     outs = {}
     old = os.environ.get("TBN_CONV_TILE")
     try:
-        for tile in [t for base in (0, 10, 20, 30) for t in range(base, base + 9)]:
+        for tile in [t for base in (0, 10, 20, 30) for t in range(base, base + 10)]:
             os.environ["TBN_CONV_TILE"] = str(tile)
             y = empty(oshape, torch.float32)
             y.fill_(np.nan)
