@@ -146,6 +146,90 @@ __global__ void __launch_bounds__(256) depthwise3x3_kernel(const float* __restri
     }
 }
 
+// 3x3, stride 1, padding 1, dilation 1, W a multiple of 4 and at most 256:
+// a lane owns 4 output columns of 4 consecutive output rows.  Each input row
+// is one float4 load per lane, contiguous across the lanes of a row, and the
+// column each side comes from the neighbouring lane by shuffle (zero padding
+// at the image edge), so a wave reads whole rows once.  A wave holds
+// 64 / (W/4) row groups of the same or following planes.  Taps are summed in
+// (r, s) order, as depthwise_kernel does.
+constexpr int kRowsTR = 4;  // output rows per lane
+
+__global__ void __launch_bounds__(256) depthwise3x3_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                                const float* __restrict__ scale, float alpha,
+                                                                const float* __restrict__ bias,
+                                                                const float* __restrict__ residual, int flags,
+                                                                float* __restrict__ y, DwGeom g, int quads,
+                                                                int groups_per_wave, int tasks_plane,
+                                                                int64_t tasks) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rw = lane / quads, q = lane - rw * quads;
+    const bool lane_ok = rw < groups_per_wave;
+    const bool bts = (flags & TBN_EPI_BIAS_THEN_SCALE) != 0, relu = (flags & TBN_EPI_RELU) != 0;
+    const int64_t waves_total = static_cast<int64_t>(gridDim.x) * 4;
+    for (int64_t wv = static_cast<int64_t>(blockIdx.x) * 4 + wave; wv * groups_per_wave < tasks; wv += waves_total) {
+        const int64_t task = wv * groups_per_wave + rw;
+        const bool ok = lane_ok && task < tasks;
+        const int64_t plane = ok ? task / tasks_plane : 0;
+        const int oh0 = ok ? static_cast<int>(task - plane * tasks_plane) * kRowsTR : 0;
+        const int m = static_cast<int>(plane % g.M);
+        const int64_t n = plane / g.M;
+        const float* xp = x + (n * g.C + m / g.mult) * static_cast<int64_t>(g.H) * g.W + 4 * q;
+        float wv9[9];
+#pragma unroll
+        for (int t = 0; t < 9; ++t) wv9[t] = ok ? w[m * 9 + t] : 0.0f;
+        float acc[kRowsTR][4] = {};
+#pragma unroll
+        for (int i = 0; i < kRowsTR + 2; ++i) {
+            const int ih = oh0 - 1 + i;
+            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (ok && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H))
+                v = *reinterpret_cast<const float4*>(xp + static_cast<int64_t>(ih) * g.W);
+            // columns 4q - 1 and 4q + 4 from the neighbouring lanes of the same row
+            float left = __shfl_up(v.w, 1);
+            float right = __shfl_down(v.x, 1);
+            if (q == 0) left = 0.0f;
+            if (q == quads - 1) right = 0.0f;
+            const float in[6] = {left, v.x, v.y, v.z, v.w, right};
+#pragma unroll
+            for (int a = 0; a < kRowsTR; ++a) {
+                const int r = i - a;
+                if (r < 0 || r > 2) continue;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+#pragma unroll
+                    for (int s = 0; s < 3; ++s) acc[a][c] = fmaf(in[c + s], wv9[r * 3 + s], acc[a][c]);
+            }
+        }
+        if (!ok) continue;
+        const float mm = alpha * (scale ? scale[m] : 1.0f);
+        const float bb = bias ? bias[m] : 0.0f;
+        const float ea = bts ? bb : 0.0f, eb = bts ? 0.0f : bb;
+        const int64_t ybase = plane * g.OH * static_cast<int64_t>(g.OW) + 4 * q;
+#pragma unroll
+        for (int a = 0; a < kRowsTR; ++a) {
+            const int oh = oh0 + a;
+            if (oh >= g.OH) break;
+            const int64_t o = ybase + static_cast<int64_t>(oh) * g.OW;
+            float out[4];
+#pragma unroll
+            for (int c = 0; c < 4; ++c) out[c] = (acc[a][c] + ea) * mm + eb;
+            if (residual) {
+                const float4 rv = *reinterpret_cast<const float4*>(residual + o);
+                out[0] += rv.x;
+                out[1] += rv.y;
+                out[2] += rv.z;
+                out[3] += rv.w;
+            }
+            if (relu) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) out[c] = out[c] > 0.0f ? out[c] : 0.0f;
+            }
+            *reinterpret_cast<float4*>(y + o) = make_float4(out[0], out[1], out[2], out[3]);
+        }
+    }
+}
+
 // dst[n, dst_c0 + c, :] = src[n, src_c0 + c, :] for c < count; rows of `hw`
 // floats, `vec` = 4 when every row start is 16-byte aligned.
 template <int VEC>
@@ -235,6 +319,21 @@ int tbn_hip_conv2d_depthwise(const float* x, const tbn_conv2d_desc* desc, const 
     const int64_t tiles = g.tiles_w * tbn_hip::ceil_div(OH, kTileH);
     TBN_REQUIRE(tiles < lim, TBN_INVALID_SHAPE, "depthwise conv: output plane too large");
     g.tiles = static_cast<int>(tiles);
+    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
+                            reinterpret_cast<uintptr_t>(residual);
+    if (d.kh == 3 && d.kw == 3 && d.sh == 1 && d.sw == 1 && d.ph == 1 && d.pw == 1 && d.dh == 1 && d.dw == 1 &&
+        d.w % 4 == 0 && d.w <= 256 && align % 16 == 0) {
+        const int quads = static_cast<int>(d.w / 4);
+        const int per_wave = 64 / quads;
+        const int64_t tasks_plane = tbn_hip::ceil_div(OH, kRowsTR);
+        const int64_t tasks = g.planes * tasks_plane;
+        TBN_REQUIRE(tasks_plane < (1LL << 30), TBN_INVALID_SHAPE, "depthwise conv: output plane too large");
+        const int64_t waves = tbn_hip::ceil_div(tasks, per_wave);
+        const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(tbn_hip::ceil_div(waves, 4), 1 << 20));
+        hipLaunchKernelGGL(depthwise3x3_rows_kernel, dim3(blocks), dim3(256), 0, tbn_hip::stream_of(stream), x, w,
+                           scale, alpha, bias, residual, flags, y, g, quads, per_wave, int(tasks_plane), tasks);
+        return tbn_hip::check_launch("conv2d_depthwise");
+    }
     const int64_t pw4 = tbn_hip::ceil_div(OW, 4), pplane = pw4 * tbn_hip::ceil_div(OH, 4);
     const int64_t patches = g.planes * pplane;
     // stride 2 on wide planes: the generic kernel's 64-column rows coalesce
