@@ -8,6 +8,8 @@
 //
 // All three are HBM-bound elementwise-shaped kernels: coalesced 64-lane rows,
 // fp32 FMA on the VALU, no matrix cores.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace {
@@ -146,24 +148,40 @@ __global__ void __launch_bounds__(256) depthwise3x3_kernel(const float* __restri
     }
 }
 
-// 3x3, stride 1, padding 1, dilation 1, W a multiple of 4 and at most 256:
-// a lane owns 4 output columns of 4 consecutive output rows.  Each input row
-// is one float4 load per lane, contiguous across the lanes of a row, and the
-// column each side comes from the neighbouring lane by shuffle (zero padding
-// at the image edge), so a wave reads whole rows once.  A wave holds
-// 64 / (W/4) row groups of the same or following planes.  Taps are summed in
-// (r, s) order, as depthwise_kernel does.
+// 3x3, padding 1, dilation 1, stride S in {1, 2}: a lane owns VEC
+// consecutive output columns of kRowsTR consecutive output rows and reads the
+// VEC*S input columns under them as vector loads, contiguous across the
+// lanes of a row; the column to the left (and, at stride 1, to the right)
+// comes from the neighbouring lane by shuffle, zero at the image edge.  So a
+// wave reads whole rows once.  A wave holds 64 / (OW/VEC) row groups of the
+// same or following planes.  Taps are summed in (r, s) order, as
+// depthwise_kernel does.
 constexpr int kRowsTR = 4;  // output rows per lane
 
+template <int N>
+struct FloatVec;
+template <>
+struct FloatVec<1> { using T = float; };
+template <>
+struct FloatVec<2> { using T = float2; };
+template <>
+struct FloatVec<4> { using T = float4; };
+
+template <int VEC, int S>
 __global__ void __launch_bounds__(256) depthwise3x3_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                                 const float* __restrict__ scale, float alpha,
                                                                 const float* __restrict__ bias,
                                                                 const float* __restrict__ residual, int flags,
-                                                                float* __restrict__ y, DwGeom g, int quads,
+                                                                float* __restrict__ y, DwGeom g, int lanes_row,
                                                                 int groups_per_wave, int tasks_plane,
                                                                 int64_t tasks) {
+    constexpr int IN = VEC * S;                 // input columns a lane loads per row
+    constexpr int LV = IN < 4 ? IN : 4;         // floats per vector load
+    constexpr int ROWS = (kRowsTR - 1) * S + 3;  // input rows per row group
+    using V = typename FloatVec<LV>::T;
+    using VO = typename FloatVec<VEC>::T;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int rw = lane / quads, q = lane - rw * quads;
+    const int rw = lane / lanes_row, q = lane - rw * lanes_row;
     const bool lane_ok = rw < groups_per_wave;
     const bool bts = (flags & TBN_EPI_BIAS_THEN_SCALE) != 0, relu = (flags & TBN_EPI_RELU) != 0;
     const int64_t waves_total = static_cast<int64_t>(gridDim.x) * 4;
@@ -174,60 +192,88 @@ __global__ void __launch_bounds__(256) depthwise3x3_rows_kernel(const float* __r
         const int oh0 = ok ? static_cast<int>(task - plane * tasks_plane) * kRowsTR : 0;
         const int m = static_cast<int>(plane % g.M);
         const int64_t n = plane / g.M;
-        const float* xp = x + (n * g.C + m / g.mult) * static_cast<int64_t>(g.H) * g.W + 4 * q;
+        const float* xp = x + (n * g.C + m / g.mult) * static_cast<int64_t>(g.H) * g.W + IN * q;
         float wv9[9];
 #pragma unroll
         for (int t = 0; t < 9; ++t) wv9[t] = ok ? w[m * 9 + t] : 0.0f;
-        float acc[kRowsTR][4] = {};
+        float acc[kRowsTR][VEC] = {};
 #pragma unroll
-        for (int i = 0; i < kRowsTR + 2; ++i) {
-            const int ih = oh0 - 1 + i;
-            float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (ok && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H))
-                v = *reinterpret_cast<const float4*>(xp + static_cast<int64_t>(ih) * g.W);
-            // columns 4q - 1 and 4q + 4 from the neighbouring lanes of the same row
-            float left = __shfl_up(v.w, 1);
-            float right = __shfl_down(v.x, 1);
-            if (q == 0) left = 0.0f;
-            if (q == quads - 1) right = 0.0f;
-            const float in[6] = {left, v.x, v.y, v.z, v.w, right};
+        for (int i = 0; i < ROWS; ++i) {
+            const int ih = oh0 * S - 1 + i;
+            float v[IN];
+#pragma unroll
+            for (int e = 0; e < IN; ++e) v[e] = 0.0f;
+            if (ok && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H)) {
+                const V* src = reinterpret_cast<const V*>(xp + static_cast<int64_t>(ih) * g.W);
+#pragma unroll
+                for (int e = 0; e < IN / LV; ++e) {
+                    const V t = src[e];
+                    const float* f = reinterpret_cast<const float*>(&t);
+#pragma unroll
+                    for (int k = 0; k < LV; ++k) v[e * LV + k] = f[k];
+                }
+            }
+            // in[0] = column IN*q - 1, in[1 + e] = column IN*q + e, in[IN + 1] = column IN*q + IN
+            float in[IN + 2];
+            in[0] = __shfl_up(v[IN - 1], 1);
+            if (q == 0) in[0] = 0.0f;
+#pragma unroll
+            for (int e = 0; e < IN; ++e) in[1 + e] = v[e];
+            in[IN + 1] = 0.0f;
+            if (S == 1) {
+                in[IN + 1] = __shfl_down(v[0], 1);
+                if (q == lanes_row - 1) in[IN + 1] = 0.0f;
+            }
 #pragma unroll
             for (int a = 0; a < kRowsTR; ++a) {
-                const int r = i - a;
+                const int r = i - a * S;
                 if (r < 0 || r > 2) continue;
 #pragma unroll
-                for (int c = 0; c < 4; ++c)
+                for (int c = 0; c < VEC; ++c)
 #pragma unroll
-                    for (int s = 0; s < 3; ++s) acc[a][c] = fmaf(in[c + s], wv9[r * 3 + s], acc[a][c]);
+                    for (int s2 = 0; s2 < 3; ++s2) acc[a][c] = fmaf(in[c * S + s2], wv9[r * 3 + s2], acc[a][c]);
             }
         }
         if (!ok) continue;
         const float mm = alpha * (scale ? scale[m] : 1.0f);
         const float bb = bias ? bias[m] : 0.0f;
         const float ea = bts ? bb : 0.0f, eb = bts ? 0.0f : bb;
-        const int64_t ybase = plane * g.OH * static_cast<int64_t>(g.OW) + 4 * q;
+        const int64_t ybase = plane * g.OH * static_cast<int64_t>(g.OW) + VEC * q;
 #pragma unroll
         for (int a = 0; a < kRowsTR; ++a) {
             const int oh = oh0 + a;
             if (oh >= g.OH) break;
             const int64_t o = ybase + static_cast<int64_t>(oh) * g.OW;
-            float out[4];
+            float out[VEC];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) out[c] = (acc[a][c] + ea) * mm + eb;
+            for (int c = 0; c < VEC; ++c) out[c] = (acc[a][c] + ea) * mm + eb;
             if (residual) {
-                const float4 rv = *reinterpret_cast<const float4*>(residual + o);
-                out[0] += rv.x;
-                out[1] += rv.y;
-                out[2] += rv.z;
-                out[3] += rv.w;
+                const VO rv = *reinterpret_cast<const VO*>(residual + o);
+                const float* rf = reinterpret_cast<const float*>(&rv);
+#pragma unroll
+                for (int c = 0; c < VEC; ++c) out[c] += rf[c];
             }
             if (relu) {
 #pragma unroll
-                for (int c = 0; c < 4; ++c) out[c] = out[c] > 0.0f ? out[c] : 0.0f;
+                for (int c = 0; c < VEC; ++c) out[c] = out[c] > 0.0f ? out[c] : 0.0f;
             }
-            *reinterpret_cast<float4*>(y + o) = make_float4(out[0], out[1], out[2], out[3]);
+            VO ov;
+            float* of = reinterpret_cast<float*>(&ov);
+#pragma unroll
+            for (int c = 0; c < VEC; ++c) of[c] = out[c];
+            *reinterpret_cast<VO*>(y + o) = ov;
         }
     }
+}
+
+template <int VEC, int S>
+void launch_rows(const float* x, const float* w, const float* scale, float alpha, const float* bias,
+                 const float* residual, int flags, float* y, const DwGeom& g, int lanes_row, int per_wave,
+                 int tasks_plane, int64_t tasks, hipStream_t s) {
+    const int64_t waves = tbn_hip::ceil_div(tasks, per_wave);
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(tbn_hip::ceil_div(waves, 4), 1 << 20));
+    hipLaunchKernelGGL((depthwise3x3_rows_kernel<VEC, S>), dim3(blocks), dim3(256), 0, s, x, w, scale, alpha, bias,
+                       residual, flags, y, g, lanes_row, per_wave, tasks_plane, tasks);
 }
 
 // dst[n, dst_c0 + c, :] = src[n, src_c0 + c, :] for c < count; rows of `hw`
@@ -319,20 +365,40 @@ int tbn_hip_conv2d_depthwise(const float* x, const tbn_conv2d_desc* desc, const 
     const int64_t tiles = g.tiles_w * tbn_hip::ceil_div(OH, kTileH);
     TBN_REQUIRE(tiles < lim, TBN_INVALID_SHAPE, "depthwise conv: output plane too large");
     g.tiles = static_cast<int>(tiles);
-    const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
-                            reinterpret_cast<uintptr_t>(residual);
-    if (d.kh == 3 && d.kw == 3 && d.sh == 1 && d.sw == 1 && d.ph == 1 && d.pw == 1 && d.dh == 1 && d.dw == 1 &&
-        d.w % 4 == 0 && d.w <= 256 && align % 16 == 0) {
-        const int quads = static_cast<int>(d.w / 4);
-        const int per_wave = 64 / quads;
-        const int64_t tasks_plane = tbn_hip::ceil_div(OH, kRowsTR);
-        const int64_t tasks = g.planes * tasks_plane;
-        TBN_REQUIRE(tasks_plane < (1LL << 30), TBN_INVALID_SHAPE, "depthwise conv: output plane too large");
-        const int64_t waves = tbn_hip::ceil_div(tasks, per_wave);
-        const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(tbn_hip::ceil_div(waves, 4), 1 << 20));
-        hipLaunchKernelGGL(depthwise3x3_rows_kernel, dim3(blocks), dim3(256), 0, tbn_hip::stream_of(stream), x, w,
-                           scale, alpha, bias, residual, flags, y, g, quads, per_wave, int(tasks_plane), tasks);
-        return tbn_hip::check_launch("conv2d_depthwise");
+    // the row kernel: 3x3, padding 1, stride 1 (OW = W) or 2 with an even W
+    // (OW = W/2), VEC output columns per lane with OW / VEC lanes per row
+    if (d.kh == 3 && d.kw == 3 && d.ph == 1 && d.pw == 1 && d.dh == 1 && d.dw == 1 && d.sh == d.sw &&
+        (d.sh == 1 || (d.sh == 2 && d.w % 2 == 0))) {
+        const int S = static_cast<int>(d.sh);
+        const int vec = OW % 4 == 0 ? 4 : (OW % 2 == 0 ? 2 : 1);
+        const int lv = std::min(4, vec * S);
+        const uintptr_t align = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
+                                reinterpret_cast<uintptr_t>(residual);
+        if (OW / vec <= 64 && align % (4 * static_cast<uintptr_t>(std::max(lv, vec))) == 0) {
+            const int lanes_row = static_cast<int>(OW / vec);
+            const int per_wave = 64 / lanes_row;
+            const int64_t tasks_plane = tbn_hip::ceil_div(OH, kRowsTR);
+            const int64_t tasks = g.planes * tasks_plane;
+            hipStream_t st = tbn_hip::stream_of(stream);
+            auto go = [&](auto vec_c, auto s_c) {
+                launch_rows<decltype(vec_c)::value, decltype(s_c)::value>(x, w, scale, alpha, bias, residual, flags,
+                                                                          y, g, lanes_row, per_wave,
+                                                                          int(tasks_plane), tasks, st);
+            };
+            using I1 = std::integral_constant<int, 1>;
+            using I2 = std::integral_constant<int, 2>;
+            using I4 = std::integral_constant<int, 4>;
+            if (S == 1) {
+                if (vec == 4) go(I4{}, I1{});
+                else if (vec == 2) go(I2{}, I1{});
+                else go(I1{}, I1{});
+            } else {
+                if (vec == 4) go(I4{}, I2{});
+                else if (vec == 2) go(I2{}, I2{});
+                else go(I1{}, I2{});
+            }
+            return tbn_hip::check_launch("conv2d_depthwise");
+        }
     }
     const int64_t pw4 = tbn_hip::ceil_div(OW, 4), pplane = pw4 * tbn_hip::ceil_div(OH, 4);
     const int64_t patches = g.planes * pplane;

@@ -58,12 +58,13 @@ def test_depthwise_entry_point_epilogues(dev, orc, flags, with_scale, with_res):
                                                    (1, 56, 56, 1, tbn_hip.EPI_BIAS_THEN_SCALE),
                                                    (2, 29, 30, 1, tbn_hip.EPI_RELU), (1, 27, 28, 2, tbn_hip.EPI_RELU),
                                                    (1, 6, 256, 1, 0), (1, 9, 8, 1, tbn_hip.EPI_BIAS_THEN_SCALE),
-                                                   (1, 14, 14, 1, tbn_hip.EPI_RELU)])
+                                                   (1, 14, 14, 1, tbn_hip.EPI_RELU), (2, 15, 17, 1, tbn_hip.EPI_RELU),
+                                                   (1, 5, 300, 1, 0), (2, 56, 112, 1, tbn_hip.EPI_RELU)])
 def test_depthwise_3x3_register_blocked(dev, orc, stride, h, w, mult, flags):
-    """The 3x3 kernels: stride 1/2 with 4x4 outputs per thread (partial
-    patches at the right and bottom edges, padding on every side), and the
-    row kernel for stride 1 on widths that are multiples of 4 (several row
-    groups and planes per wave, partial row groups); residual throughout."""
+    """The 3x3 kernels: the row kernel (stride 1, or 2 on even widths; 4, 2
+    or 1 output columns per lane; several row groups and planes per wave,
+    partial row groups) and the 4x4-patch kernel (odd widths at stride 2,
+    rows wider than 256); residual throughout."""
     rng = np.random.default_rng(stride * 100 + h)
     n, c = 3, 20
     x = rng.standard_normal((n, c, h, w)).astype(np.float32)
