@@ -223,7 +223,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=20.0)
-    ap.add_argument("--only", choices=["gemm", "conv", "ternary", "tbn", "gemm1024", "lenet", "resnet"],
+    ap.add_argument("--only", choices=["gemm", "conv", "ternary", "tbn", "gemm1024", "lenet", "resnet", "groups"],
                     help="run one workload only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 device copies of 1 GiB (known bytes) for counter calibration")
@@ -303,6 +303,35 @@ def main():
         extra["gemm_cfg2_gflops_equiv"] = round(2.0 * 1024 ** 3 / (g_ms * 1e-3) / 1e9, 1)
         log(f"binary cfg2 1024^3: {g_ms * 1e3:.1f} us")
         del keep
+    if want("groups"):
+        # depthwise 3x3 (MobileNet-style, batch 32, 128 channels, 56x56) and an
+        # unfolded BatchNormalization over the same tensor: both HBM-bound
+        import ctypes
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev)
+        g.manual_seed(7)
+        n, c, h = 32, 128, 56
+        x = torch.randn((n, c, h, h), generator=g, device=dev)
+        w = torch.randn((c, 1, 3, 3), generator=g, device=dev)
+        kk = torch.rand(c, generator=g, device=dev) + 0.5
+        tt = torch.randn(c, generator=g, device=dev)
+        y = torch.empty_like(x)
+        d = tbn_hip.conv_desc(n, c, h, h, c, 3, 3, 1, 1, 1, 1)
+
+        def dw_step(sh):
+            tbn_hip.call("tbn_hip_conv2d_depthwise", x.data_ptr(), ctypes.byref(d), w.data_ptr(), None, 1.0, None,
+                         None, tbn_hip.EPI_RELU, y.data_ptr(), sh)
+
+        def bn_step(sh):
+            tbn_hip.call("tbn_hip_channel_affine", x.data_ptr(), n, c, h * h, kk.data_ptr(), tt.data_ptr(), 0,
+                         y.data_ptr(), sh)
+        nbytes = 2 * 4.0 * x.numel()
+        for name, fn in (("depthwise3x3", dw_step), ("batchnorm", bn_step)):
+            t_ms = timed(fn)
+            extra[name + "_32x128x56x56_us"] = round(t_ms * 1e3, 2)
+            extra[name + "_32x128x56x56_GBps"] = round(nbytes / (t_ms * 1e-3) / 1e9, 1)
+            log(f"{name} 32x128x56x56: {t_ms * 1e3:.1f} us, {nbytes / (t_ms * 1e-3) / 1e9:.0f} GB/s")
+        del x, y, w, kk, tt
     for which, key, replay in (("lenet", "lenet_session_us_per_forward", True),
                                ("resnet", "resnet18_session_ms_per_batch32", False)):
         if not want(which):
