@@ -207,13 +207,13 @@ struct TbnGemmArgs {
 template <int BR_, int BC_, int WR_, int WC_>
 struct I8Cfg {
     static constexpr int BR = BR_, BC = BC_, WR = WR_, WC = WC_;
-    static constexpr int KS = 64;         // k per step
+    static constexpr int KS = 128;        // k per step: one 16-byte weight word per column
     static constexpr int KROW = KS + 16;  // bytes per LDS row: conflict-free 16-byte fragment reads
     static constexpr int WAVES_R = BR / WR, WAVES_C = BC / WC;
     static constexpr int NT = 64 * WAVES_R * WAVES_C;
     static constexpr int FR = WR / 32, FC = WC / 32;
-    static constexpr int TPR = NT / BR;   // threads per A row (16 bytes each)
-    static_assert(TPR * 16 == KS, "a step's A tile is one 16-byte load per thread");
+    static constexpr int TPR = NT / BR;   // threads per A row (32 bytes each)
+    static_assert(TPR * 32 == KS, "a step's A tile is two 16-byte loads per thread");
 };
 
 using I8Wide = I8Cfg<128, 512, 128, 64>;
@@ -249,7 +249,7 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
     const int ar = tid / Cfg::TPR, ag = tid % Cfg::TPR;
     const __amdgpu_buffer_rsrc_t a_rs =
         make_rsrc(p.T + static_cast<int64_t>(r0) * p.ldt, static_cast<uint64_t>(p.M - r0) * p.ldt);
-    const int a_voff = ar * static_cast<int>(p.ldt) + ag * 16;
+    const int a_voff = ar * static_cast<int>(p.ldt) + ag * 32;
     const __amdgpu_buffer_rsrc_t b_rs =
         make_rsrc(p.bits + static_cast<int64_t>(c0) * p.col_bytes,
                   static_cast<uint64_t>(p.N_pad - c0) * static_cast<uint64_t>(p.col_bytes));
@@ -258,23 +258,32 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
     for (int j = 0; j < Cfg::FC; ++j)
         b_voff[j] = (wc * Cfg::WC + j * 32 + (lane & 31)) * static_cast<int>(p.col_bytes);
 
-    const int steps = p.K / KS;
-    const int pairs = (steps + 1) / 2;  // W words: 16 bytes = two steps
+    // K is a multiple of 64: a last step of 64 runs two of its four slices
+    // (the data loaded past K for the other two is never used)
+    const int steps = (p.K + KS - 1) / KS;
+    const int last_slices = (p.K % KS) ? (p.K % KS) / 32 : 4;
 
-    i32x4_t areg;
+    i32x4_t areg[2];
     uint32_t bw[Cfg::FC][4], bwn[Cfg::FC][4];
-    auto load_a = [&](int s) { areg = __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff, s * KS, 0); };
-    auto load_b = [&](int q, uint32_t (&w)[Cfg::FC][4]) {
+    auto load_a = [&](int s) {
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) areg[h2] = __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16 * h2, s * KS, 0);
+    };
+    auto load_b = [&](int s, uint32_t (&w)[Cfg::FC][4]) {
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             const u32x4_t x =
-                __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], q * 16, 0));
+                __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], s * 16, 0));
 #pragma unroll
             for (int d = 0; d < 4; ++d) w[j][d] = x[d];
         }
     };
-    const int a_store = ar * Cfg::KROW + ag * 16;
-    auto store_a = [&](int b) { *reinterpret_cast<i32x4_t*>(lds + b * Cfg::BR * Cfg::KROW + a_store) = areg; };
+    const int a_store = ar * Cfg::KROW + ag * 32;
+    auto store_a = [&](int b) {
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2)
+            *reinterpret_cast<i32x4_t*>(lds + b * Cfg::BR * Cfg::KROW + a_store + 16 * h2) = areg[h2];
+    };
 
     i32x16_t acc[Cfg::FR][Cfg::FC];
 #pragma unroll
@@ -286,17 +295,27 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
 
     const int a_frag = (wr * Cfg::WR + (lane & 31)) * Cfg::KROW + h * 16;
 
-    // one step s = 2q + u: two MFMA slices of 32 k on LDS buffer u; meanwhile
-    // step s+1's A goes to the other buffer and step s+2's A is fetched
-    auto step = [&](int q, auto uc) {
-        constexpr int u = decltype(uc)::value;
-        const int s = 2 * q + u;
+    // step s: four MFMA slices of 32 k on LDS buffer s & 1; meanwhile step
+    // s+1's A goes to the other buffer and step s+2's A and s+1's W words are
+    // fetched
+    load_a(0);
+    load_b(0, bw);
+    store_a(0);
+    if (steps > 1) {
+        load_a(1);
+        load_b(1, bwn);
+    }
+    __syncthreads();
+    for (int s = 0; s < steps; ++s) {
+        const int u = s & 1;
+        const int slices = s + 1 < steps ? 4 : last_slices;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < 4; ++kk) {
+            if (kk >= slices) break;
             i32x4_t bf[Cfg::FC];
 #pragma unroll
             for (int j = 0; j < Cfg::FC; ++j) {
-                const uint32_t word = bw[j][2 * u + kk];
+                const uint32_t word = bw[j][kk];
 #pragma unroll
                 for (int d = 0; d < 4; ++d)
                     bf[j][d] = static_cast<int>(spread4(__builtin_amdgcn_ubfe(word, 16 * h + 4 * d, 4)));
@@ -310,27 +329,18 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
                     acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[j], acc[i][j], 0, 0, 0);
             }
         }
-        if (s + 1 < steps) store_a(u ^ 1);
-        if (s + 2 < steps) load_a(s + 2);
-        if constexpr (u == 1) {
+        if (s + 1 < steps) {
+            store_a(u ^ 1);
 #pragma unroll
             for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
                 for (int d = 0; d < 4; ++d) bw[j][d] = bwn[j][d];
-            if (q + 2 < pairs) load_b(q + 2, bwn);
+        }
+        if (s + 2 < steps) {
+            load_a(s + 2);
+            load_b(s + 2, bwn);
         }
         __syncthreads();
-    };
-
-    load_a(0);
-    load_b(0, bw);
-    if (pairs > 1) load_b(1, bwn);
-    store_a(0);
-    if (steps > 1) load_a(1);
-    __syncthreads();
-    for (int q = 0; q < pairs; ++q) {
-        step(q, std::integral_constant<int, 0>{});
-        if (2 * q + 1 < steps) step(q, std::integral_constant<int, 1>{});
     }
 
     // epilogue: C = rowsum - 2 * acc; rows of register e: i*32 + 8*(e/4) + 4*h + e%4
