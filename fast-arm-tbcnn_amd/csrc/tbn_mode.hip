@@ -142,13 +142,22 @@ __global__ void ternarize_rows_kernel(const float* __restrict__ A, int64_t lda, 
         const float* src = A + static_cast<int64_t>(row) * lda;
         uint32_t* dst = reinterpret_cast<uint32_t*>(T + static_cast<int64_t>(row) * ldt);
         int sum = 0;
+        // rows of whole float4s (K and lda multiples of 4, A 16-byte aligned):
+        // one vector load per output word
+        const bool vec = (K % 4 == 0) && (lda % 4 == 0) && (reinterpret_cast<uintptr_t>(A) % 16 == 0);
         for (int64_t w = threadIdx.x; w < ldt / 4; w += blockDim.x) {
+            float v[4];
+            if (vec) {
+                const float4 f = 4 * w < K ? *reinterpret_cast<const float4*>(src + 4 * w) : make_float4(0, 0, 0, 0);
+                v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = 4 * w + e < K ? src[4 * w + e] : 0.0f;
+            }
             uint32_t word = 0;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int64_t c = 4 * w + e;
-                const float v = c < K ? src[c] : 0.0f;
-                const bool m = v < lo, p = !m && v > hi;
+                const bool m = v[e] < lo, p = !m && v[e] > hi;
                 sum += (p ? 1 : 0) - (m ? 1 : 0);
                 word |= tern_byte(p, m) << (8 * e);
             }
