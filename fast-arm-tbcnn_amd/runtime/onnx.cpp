@@ -134,6 +134,7 @@ void append_fixed(const Field& f, std::vector<T>& out, const char* what) {
     }
     expect(f, kLen, what);
     if (f.n % sizeof(T)) malformed(std::string(what) + ": packed length not a multiple of the element size");
+    if (f.n == 0) return;
     const size_t old = out.size();
     out.resize(old + f.n / sizeof(T));
     std::memcpy(out.data() + old, f.p, f.n);
@@ -240,7 +241,15 @@ bool safe_relative_path(const std::string& loc) {
     return true;
 }
 
-void read_external(const TensorFields& t, const std::string& base_dir, void* dst, size_t bytes) {
+// Where an external tensor's bytes are: the file (resolved against
+// `base_dir`, which `location` may not leave) and the offset, after checking
+// that the range holds exactly `bytes`.
+struct ExternalRange {
+    std::string path;
+    uint64_t offset = 0;
+};
+
+ExternalRange external_range(const TensorFields& t, const std::string& base_dir, size_t bytes) {
     std::string location;
     uint64_t offset = 0, length = 0;
     bool has_length = false;
@@ -271,12 +280,19 @@ void read_external(const TensorFields& t, const std::string& base_dir, void* dst
     TBN_CHECK(length == bytes, InvalidModelError,
               "tensor '" + t.name + "': external data holds " + std::to_string(length) + " bytes, its shape needs " +
                   std::to_string(bytes));
-    in.seekg(static_cast<std::streamoff>(offset));
-    in.read(static_cast<char*>(dst), static_cast<std::streamsize>(bytes));
-    TBN_CHECK(static_cast<bool>(in), InvalidModelError, "tensor '" + t.name + "': short read from " + path);
+    return {path, offset};
 }
 
-// onnx_parser.cpp:196-239, with external data and size checks.
+void read_external(const TensorFields& t, const ExternalRange& r, void* dst, size_t bytes) {
+    std::ifstream in(r.path, std::ios::binary);
+    in.seekg(static_cast<std::streamoff>(r.offset));
+    in.read(static_cast<char*>(dst), static_cast<std::streamsize>(bytes));
+    TBN_CHECK(static_cast<bool>(in), InvalidModelError, "tensor '" + t.name + "': short read from " + r.path);
+}
+
+// onnx_parser.cpp:196-239, with external data and size checks.  Every size is
+// checked against the data present before the tensor is allocated, so a
+// malformed shape cannot ask for more memory than the file backs.
 Tensor make_tensor(const TensorFields& t, const std::string& base_dir) {
     DataType dt;
     TBN_CHECK(map_dtype(t.data_type, dt), NotImplementedError,
@@ -295,14 +311,11 @@ Tensor make_tensor(const TensorFields& t, const std::string& base_dir) {
     const size_t bytes = static_cast<size_t>(numel) * esize;
     const bool external = t.data_location == 1 || !t.external.empty();
 
-    auto count_check = [&](size_t n, const char* field) {
-        TBN_CHECK(n == numel, InvalidModelError,
-                  "tensor '" + t.name + "': " + field + " holds " + std::to_string(n) + " values, its shape has " +
-                      std::to_string(numel));
-    };
     if (external) {
+        if (bytes == 0) return Tensor(shape, dt);
+        const ExternalRange range = external_range(t, base_dir, bytes);
         Tensor out(shape, dt);
-        if (bytes) read_external(t, base_dir, out.data(), bytes);
+        read_external(t, range, out.data(), bytes);
         return out;
     }
     if (t.has_raw) {
@@ -311,35 +324,36 @@ Tensor make_tensor(const TensorFields& t, const std::string& base_dir) {
                       std::to_string(bytes));
         return Tensor(shape, dt, t.raw);
     }
+    if (numel == 0) return Tensor(shape, dt);
+    // typed fields: float_data (FLOAT), int64_data (INT64), uint64_data
+    // (UINT32, UINT64), int32_data (INT32 and the 8/16-bit types, as their
+    // value or bits)
+    const char* field = dt == DataType::FLOAT32 ? "float_data"
+                        : dt == DataType::INT64 ? "int64_data"
+                        : (dt == DataType::UINT32 || dt == DataType::UINT64) ? "uint64_data"
+                                                                             : "int32_data";
+    const size_t count = dt == DataType::FLOAT32 ? t.float_data.size()
+                         : dt == DataType::INT64 ? t.int64_data.size()
+                         : (dt == DataType::UINT32 || dt == DataType::UINT64) ? t.uint64_data.size()
+                                                                              : t.int32_data.size();
+    TBN_CHECK(count == numel, InvalidModelError,
+              "tensor '" + t.name + "': " + field + " holds " + std::to_string(count) + " values, its shape has " +
+                  std::to_string(numel));
     Tensor out(shape, dt);
-    if (numel == 0) return out;
-    switch (dt) {
-        case DataType::FLOAT32:
-            count_check(t.float_data.size(), "float_data");
-            std::memcpy(out.data(), t.float_data.data(), bytes);
-            break;
-        case DataType::INT64:
-            count_check(t.int64_data.size(), "int64_data");
-            std::memcpy(out.data(), t.int64_data.data(), bytes);
-            break;
-        case DataType::UINT32:
-        case DataType::UINT64: {
-            count_check(t.uint64_data.size(), "uint64_data");
-            auto* dst = static_cast<uint8_t*>(out.data());
-            for (size_t i = 0; i < numel; ++i) {
-                const uint64_t v = t.uint64_data[i];
-                std::memcpy(dst + i * esize, &v, esize);  // little-endian: the low bytes
-            }
-            break;
+    auto* dst = static_cast<uint8_t*>(out.data());
+    if (dt == DataType::FLOAT32) {
+        std::memcpy(dst, t.float_data.data(), bytes);
+    } else if (dt == DataType::INT64) {
+        std::memcpy(dst, t.int64_data.data(), bytes);
+    } else if (dt == DataType::UINT32 || dt == DataType::UINT64) {
+        for (size_t i = 0; i < numel; ++i) {
+            const uint64_t v = t.uint64_data[i];
+            std::memcpy(dst + i * esize, &v, esize);  // little-endian: the low bytes
         }
-        default: {  // int32_data carries INT32 and the 8/16-bit types (as their value or bits)
-            count_check(t.int32_data.size(), "int32_data");
-            auto* dst = static_cast<uint8_t*>(out.data());
-            for (size_t i = 0; i < numel; ++i) {
-                const uint32_t v = static_cast<uint32_t>(t.int32_data[i]);
-                std::memcpy(dst + i * esize, &v, esize);
-            }
-            break;
+    } else {
+        for (size_t i = 0; i < numel; ++i) {
+            const uint32_t v = static_cast<uint32_t>(t.int32_data[i]);
+            std::memcpy(dst + i * esize, &v, esize);
         }
     }
     return out;
