@@ -157,9 +157,12 @@ int conv_quant(const float* x, const tbn_conv2d_desc* desc, const uint8_t* packe
         return tbn_hip::conv_patch_from_reference(TERNARY ? TBN_WEIGHTS_TERNARY : TBN_WEIGHTS_BINARY, x, desc, packed,
                                                  K_pad, N_pad, scale, alpha, bias, residual, flags, y,
                                                  tbn_hip::stream_of(stream));
-    ConvEpi epi{y, int(desc->m), g, scale, alpha, bias, residual, flags};
     const int64_t col_bytes = TERNARY ? K_pad / 4 : K_pad / 8;
     hipStream_t s = tbn_hip::stream_of(stream);
+    if (tbn_hip::conv_small_supported(desc))
+        return tbn_hip::conv_small_run(TERNARY ? 2 : 1, x, desc, packed, col_bytes, scale, alpha, bias, residual,
+                                       flags, y, s);
+    ConvEpi epi{y, int(desc->m), g, scale, alpha, bias, residual, flags};
     const int m = int(desc->m);
     if (m <= 32) {
         SignPacked<CfgM32::BR, CfgM32::NT, TERNARY> rowl{packed, col_bytes, int(N_pad)};
@@ -217,6 +220,9 @@ int tbn_hip_conv2d_f32(const float* x, const tbn_conv2d_desc* desc, const float*
     TBN_DEVICE_GUARD();
     if (tbn_hip::conv_stem_supported(desc, flags))
         return tbn_hip::conv_stem_run(x, desc, w, bias, flags, y, tbn_hip::stream_of(stream));
+    if (tbn_hip::conv_small_supported(desc))
+        return tbn_hip::conv_small_run(0, x, desc, w, 0, nullptr, 1.0f, bias, nullptr, flags, y,
+                                       tbn_hip::stream_of(stream));
     ConvEpi epi{y, int(desc->m), g, nullptr, 1.0f, bias, nullptr, flags};
     hipStream_t s = tbn_hip::stream_of(stream);
     const int m = int(desc->m);

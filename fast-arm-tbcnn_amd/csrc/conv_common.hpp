@@ -152,4 +152,11 @@ int conv_patch_from_reference(int weights, const float* x, const tbn_conv2d_desc
 bool conv_stem_supported(const tbn_conv2d_desc* desc, int flags);
 int conv_stem_run(const float* x, const tbn_conv2d_desc* desc, const float* w, const float* bias, int flags,
                   float* y, hipStream_t s);
+// Small layers (conv_small.hip): one image and a channel group per block,
+// staged in LDS, fp32 FMAs; chosen from one image's shape only.
+bool conv_small_supported(const tbn_conv2d_desc* desc);
+// wmode: 0 fp32 weights [M, K], 1 binary columns, 2 ternary columns (col_bytes each).
+int conv_small_run(int wmode, const float* x, const tbn_conv2d_desc* desc, const void* w, int64_t col_bytes,
+                   const float* scale, float alpha, const float* bias, const float* residual, int flags, float* y,
+                   hipStream_t s);
 }  // namespace tbn_hip

@@ -124,6 +124,145 @@ int f32_gemm_splits(int64_t N, int64_t K) {
     return static_cast<int>(std::min<int64_t>(8, K / 64));
 }
 
+// ---- small GEMMs (a classifier head: few columns, short K) ----------------
+// The weight columns are decoded to fp32 in LDS once per block; each block
+// then stages groups of rows of A in LDS and computes one output per thread
+// with a plain fp32 FMA chain over k in order.  Chosen from N and K only, so
+// a row's result does not depend on the batch.  Staging keeps four global
+// loads in flight per thread; rows sit ceil4(K) + 4 floats apart so the
+// 16-byte reads of different columns start on different banks.
+constexpr int kSmallGemmW = 8192;  // floats of decoded weights
+constexpr int kSmallGemmA = 8192;  // floats of staged rows
+
+struct SmallGemm {
+    const float* A;
+    int64_t a_row, a_k;   // element (m, k) at A[m*a_row + k*a_k]
+    const void* B;        // WMODE 0: fp32 element (k, n) at B[k*b_k + n*b_col]; else packed columns
+    int64_t b_k, b_col;   // WMODE 0 strides; WMODE 1/2: b_col = bytes per packed column
+    int M, N, K;
+    int Kp;               // LDS row stride
+    int rows;             // rows of A per group: min(256 / N, kSmallGemmA / Kp)
+};
+
+int small_gemm_stride(int64_t K) { return static_cast<int>((K + 3) / 4 * 4 + 4); }
+
+template <class Get, class Put>
+__device__ __forceinline__ void stage4_gemm(int count, Get get, Put put) {
+    for (int base = 0; base < count; base += 4 * 256) {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = base + j * 256 + static_cast<int>(threadIdx.x);
+            v[j] = i < count ? get(i) : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = base + j * 256 + static_cast<int>(threadIdx.x);
+            if (i < count) put(i, v[j]);
+        }
+    }
+}
+
+template <int WMODE>
+__global__ void __launch_bounds__(256) small_gemm_kernel(SmallGemm g, GemmEpi epi) {
+    __shared__ __align__(16) float ws[kSmallGemmW];
+    __shared__ __align__(16) float as[kSmallGemmA];
+    const int K = g.K, Kp = g.Kp;
+    if constexpr (WMODE == 0) {
+        const float* B = static_cast<const float*>(g.B);
+        stage4_gemm(g.N * K,
+                    [&](int i) {
+                        const int n = i / K, k = i - n * K;
+                        return B[static_cast<int64_t>(k) * g.b_k + static_cast<int64_t>(n) * g.b_col];
+                    },
+                    [&](int i, float v) {
+                        const int n = i / K;
+                        ws[n * Kp + (i - n * K)] = v;
+                    });
+    } else {
+        // one byte (8 binary or 4 ternary weights) per load
+        constexpr int per = WMODE == 1 ? 8 : 4;
+        const int bpc = (K + per - 1) / per;
+        const uint8_t* B = static_cast<const uint8_t*>(g.B);
+        stage4_gemm(g.N * bpc,
+                    [&](int i) {
+                        const int n = i / bpc;
+                        return static_cast<float>(B[static_cast<int64_t>(n) * g.b_col + (i - n * bpc)]);
+                    },
+                    [&](int i, float v) {
+                        const int n = i / bpc, j = i - n * bpc;
+                        const unsigned byte = static_cast<unsigned>(v);
+                        float* dst = ws + n * Kp + j * per;
+                        const int cnt = min(per, K - j * per);
+                        for (int q = 0; q < cnt; ++q) {
+                            if constexpr (WMODE == 1) {
+                                dst[q] = ((byte >> q) & 1u) ? -1.0f : 1.0f;
+                            } else {
+                                const unsigned code = (byte >> (2 * q)) & 3u;
+                                dst[q] = code == 0 ? -1.0f : (code == 2 ? 1.0f : 0.0f);
+                            }
+                        }
+                    });
+    }
+    const int groups = (g.M + g.rows - 1) / g.rows;
+    const int r = static_cast<int>(threadIdx.x) / g.N, n = static_cast<int>(threadIdx.x) - r * g.N;
+    const float* w = ws + n * Kp;
+    for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {
+        const int m0 = grp * g.rows;
+        const int rows = min(g.rows, g.M - m0);
+        __syncthreads();  // the previous group's rows are no longer read
+        stage4_gemm(rows * K,
+                    [&](int i) {
+                        const int rr = i / K, k = i - rr * K;
+                        return g.A[static_cast<int64_t>(m0 + rr) * g.a_row + static_cast<int64_t>(k) * g.a_k];
+                    },
+                    [&](int i, float v) {
+                        const int rr = i / K;
+                        as[rr * Kp + (i - rr * K)] = v;
+                    });
+        __syncthreads();
+        if (r >= rows) continue;
+        // the epilogue's operands, loaded before the FMA chain
+        const int m = m0 + r;
+        const float mult = epi.scale ? epi.alpha * epi.scale[n] : epi.alpha;
+        const float b = epi.bias ? epi.bias[n] : 0.0f;
+        const float cv = epi.cin ? epi.beta * (epi.cin_1d ? epi.cin[n] : epi.cin[static_cast<int64_t>(m) * g.N + n])
+                                 : 0.0f;
+        const float* a = as + r * Kp;
+        float acc = 0.0f;
+        int k = 0;
+#pragma unroll 2
+        for (; k + 4 <= K; k += 4) {
+            const float4 a4 = *reinterpret_cast<const float4*>(a + k);
+            const float4 w4 = *reinterpret_cast<const float4*>(w + k);
+            acc = fmaf(a4.x, w4.x, acc);
+            acc = fmaf(a4.y, w4.y, acc);
+            acc = fmaf(a4.z, w4.z, acc);
+            acc = fmaf(a4.w, w4.w, acc);
+        }
+        for (; k < K; ++k) acc = fmaf(a[k], w[k], acc);
+        // GemmEpi's arithmetic for one element
+        float v = (epi.flags & TBN_EPI_BIAS_THEN_SCALE) ? (acc + b) * mult : acc * mult + b;
+        if (epi.cin) v += cv;
+        if (epi.flags & TBN_EPI_RELU) v = v > 0.0f ? v : 0.0f;
+        epi.C[static_cast<int64_t>(m) * epi.ldc + n] = v;
+    }
+}
+
+bool small_gemm_fits(int64_t N, int64_t K) {
+    return N >= 1 && N <= 64 && K <= kSmallGemmA - 8 && N * small_gemm_stride(K) <= kSmallGemmW;
+}
+
+template <int WMODE>
+int launch_small_gemm(SmallGemm g, const GemmEpi& epi, hipStream_t s) {
+    g.Kp = small_gemm_stride(g.K);
+    g.rows = std::max(1, std::min(256 / g.N, kSmallGemmA / g.Kp));
+    const int64_t groups = tbn_hip::ceil_div(static_cast<int64_t>(g.M), g.rows);
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(groups, 2048));
+    hipLaunchKernelGGL(small_gemm_kernel<WMODE>, dim3(blocks), dim3(256), 0, s, g, epi);
+    return tbn_hip::check_launch("gemm (small)");
+}
+
 template <class Cfg, class ColL>
 int launch_gemm(const float* A, int64_t lda, int M, int N, int K, const ColL& coll,
                 const GemmEpi& epi, hipStream_t stream, const char* what) {
@@ -166,6 +305,10 @@ int gemm_quant(const float* A, int64_t lda, int64_t M, int64_t N, int64_t K, con
     GemmEpi epi{C, ldc, static_cast<int>(M), static_cast<int>(N), scale, alpha, bias,
                 (cin && beta != 0.0f) ? cin : nullptr, beta, cin_1d, flags};
     const int64_t col_bytes = TERNARY ? K_pad / 4 : K_pad / 8;
+    if (small_gemm_fits(N, K)) {
+        const SmallGemm sg{A, lda, 1, packed, 0, col_bytes, int(M), int(N), int(K), 0, 0};
+        return launch_small_gemm<TERNARY ? 2 : 1>(sg, epi, tbn_hip::stream_of(stream));
+    }
     {
         const tbn_hip::WideGemmArgs wa{A, lda, int(M), int(N), int(K), packed, col_bytes, int(N_pad), C, ldc,
                                        scale, alpha, bias, epi.cin, cin_1d, beta, flags};
@@ -247,6 +390,11 @@ int tbn_hip_gemm_f32(const float* A, const float* B, const float* Cin, int c_is_
     coll.row_fast = transB ? 0 : 1;
     GemmEpi epi{out, N, static_cast<int>(M), static_cast<int>(N), nullptr, alpha, nullptr,
                 (Cin && beta != 0.0f) ? Cin : nullptr, beta, c_is_1d, flags};
+    if (small_gemm_fits(N, K)) {
+        const SmallGemm sg{A, transA ? 1 : K, transA ? M : 1, B, transB ? 1 : N, transB ? K : 1,
+                           static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), 0, 0};
+        return launch_small_gemm<0>(sg, epi, tbn_hip::stream_of(stream));
+    }
     const int tiles_r = static_cast<int>(tbn_hip::ceil_div(M, Cfg::BR));
     const int tiles_c = static_cast<int>(tbn_hip::ceil_div(N, Cfg::BC));
     const int splits = f32_gemm_splits(N, K);

@@ -1193,16 +1193,22 @@ struct TBNModel::Session::Impl {
             return;
         }
         // HIP graph replay: the first run is eager (warms every cache), the
-        // second records the ops on a private stream, later runs replay.
-        if (!replay_stream) {
+        // second records the ops, later runs replay them.  The caller's
+        // stream is used directly; the null stream cannot be captured, so
+        // with it the ops run on a private stream ordered after it by events.
+        hipStream_t cs = static_cast<hipStream_t>(s);
+        const bool own = cs == nullptr;
+        if (own && !replay_stream) {
             if (hipStreamCreate(&replay_stream) != hipSuccess) throw RuntimeError("hipStreamCreate failed");
         }
-        hipStream_t rs = replay_stream;
-        hipEvent_t ev;
-        if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess) throw RuntimeError("hipEventCreate failed");
-        // the private stream starts after everything queued on the current stream
-        (void)hipEventRecord(ev, static_cast<hipStream_t>(s));
-        (void)hipStreamWaitEvent(rs, ev, 0);
+        hipStream_t rs = own ? replay_stream : cs;
+        hipEvent_t ev = nullptr;
+        if (own) {
+            if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess)
+                throw RuntimeError("hipEventCreate failed");
+            (void)hipEventRecord(ev, cs);
+            (void)hipStreamWaitEvent(rs, ev, 0);
+        }
         upload_inputs(rs);
         if (eager_runs < 1) {
             run_ops(rs);
@@ -1225,10 +1231,12 @@ struct TBNModel::Session::Impl {
             }
             if (hipGraphLaunch(hip_graph_exec, rs) != hipSuccess) throw RuntimeError("hipGraphLaunch failed");
         }
-        // the current stream continues after the replay
-        (void)hipEventRecord(ev, rs);
-        (void)hipStreamWaitEvent(static_cast<hipStream_t>(s), ev, 0);
-        (void)hipEventDestroy(ev);
+        if (own) {
+            // the null stream continues after the replay
+            (void)hipEventRecord(ev, rs);
+            (void)hipStreamWaitEvent(cs, ev, 0);
+            (void)hipEventDestroy(ev);
+        }
     }
 
     Tensor output_device(const std::string& name) {

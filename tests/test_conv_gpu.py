@@ -230,6 +230,84 @@ def test_conv_patch_writes_only_its_output(dev, orc, case):
     assert not np.isnan(out[:n_out]).any()
 
 
+@pytest.mark.parametrize("case", [
+    # N, C, H, W, M, kh, kw, stride, pad, dil, flags
+    (3, 5, 13, 11, 24, 3, 3, (2, 1), (2, 1), (1, 2), tbn_hip.EPI_RELU | tbn_hip.EPI_MAXPOOL2X2),
+    (2, 15, 8, 8, 40, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_BIAS_THEN_SCALE | tbn_hip.EPI_RELU),
+    (5, 1, 28, 28, 6, 5, 5, (1, 1), (2, 2), (1, 1), tbn_hip.EPI_RELU | tbn_hip.EPI_MAXPOOL2X2),
+    (2, 3, 7, 9, 130, 1, 1, (1, 1), (0, 0), (1, 1), 0),  # 1x1: many channels per block
+])
+@pytest.mark.parametrize("weights", ["binary", "ternary", "f32"])
+def test_conv_small_layers(dev, orc, case, weights):
+    """Small layers (C < 16, a padded image of <= 8192 floats, <= 16384
+    outputs per image) take the one-output-per-thread LDS kernel: padding,
+    stride, dilation, fused pool, the scale/bias orders, a residual where the
+    entry point takes one; each image's result is bit-identical to the same
+    image run alone (the path depends on one image's shape only)."""
+    N, C, H, W, M, kh, kw, stride, pad, dil, flags = case
+    rng = np.random.default_rng(N * 7 + C * 3 + M)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    K = C * kh * kw
+    scale = rng.uniform(0.5, 1.5, M).astype(np.float32)
+    bias = (rng.standard_normal(M) * 0.1).astype(np.float32)
+    d = tbn_hip.conv_desc(N, C, H, W, M, kh, kw, *stride, *pad, *dil)
+    OH, OW = tbn_hip.conv_out_hw(d)
+    pool = bool(flags & tbn_hip.EPI_MAXPOOL2X2)
+    oshape = (N, M, OH // 2, OW // 2) if pool else (N, M, OH, OW)
+    res = None if pool or weights == "f32" else rng.standard_normal((N, M, OH, OW)).astype(np.float32)
+    if weights == "f32":
+        wf = (rng.standard_normal((M, C, kh, kw)) * 0.3).astype(np.float32)
+        dw = to_dev(wf)
+        flags &= ~tbn_hip.EPI_BIAS_THEN_SCALE
+
+        def run(xs, n):
+            y = empty((n,) + oshape[1:], torch.float32)
+            dn = tbn_hip.conv_desc(n, C, H, W, M, kh, kw, *stride, *pad, *dil)
+            tbn_hip.call("tbn_hip_conv2d_f32", P(to_dev(xs)), dn, P(dw), P(to_dev(bias)), flags, P(y), None)
+            return host(y)
+        acc = rm.f64_conv(x, wf, None, stride, pad, dil)
+        ref = acc + bias.astype(np.float64)[None, :, None, None]
+        xmax = np.abs(x).max() * np.abs(wf).max()
+    else:
+        K_pad = (K + 31) // 32 * 32
+        if weights == "binary":
+            wbytes = (rng.random((M, C, kh, kw)) < 0.5).astype(np.uint8)
+            wv = np.where(wbytes == 1, 1.0, -1.0).astype(np.float32)
+            packed, K_pad, N_pad = pack_conv_weights(wbytes, M, K)
+            kind = tbn_hip.WEIGHTS_BINARY
+        else:
+            t = rng.choice(np.array([-1, 0, 1], np.int8), size=(M, C, kh, kw), p=[0.3, 0.4, 0.3])
+            wv = t.astype(np.float32)
+            N_pad = M
+            packed = empty(M * K_pad // 4, torch.uint8)
+            tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(t)), K, M, tbn_hip.LAYOUT_NK, K_pad, M, P(packed), None)
+            kind = tbn_hip.WEIGHTS_TERNARY
+        ds, db = to_dev(scale), to_dev(bias)
+
+        def run(xs, n, rs=None):
+            y = empty((n,) + oshape[1:], torch.float32)
+            dn = tbn_hip.conv_desc(n, C, H, W, M, kh, kw, *stride, *pad, *dil)
+            tbn_hip.call("tbn_hip_conv2d_f32_quantized", kind, P(to_dev(xs)), dn, P(packed), K_pad, N_pad, P(ds), 0.75,
+                         P(db), None if rs is None else P(to_dev(rs)), flags, P(y), None)
+            return host(y)
+        acc = rm.f64_conv(x, wv, None, stride, pad, dil)
+        mult = (np.float32(0.75) * scale).astype(np.float64)[None, :, None, None]
+        b = bias.astype(np.float64)[None, :, None, None]
+        ref = (acc + b) * mult if flags & tbn_hip.EPI_BIAS_THEN_SCALE else acc * mult + b
+        if res is not None:
+            ref = ref + res
+        xmax = np.abs(x).max() * 1.5
+    if flags & tbn_hip.EPI_RELU:
+        ref = np.maximum(ref, 0.0)
+    if pool:
+        ref = ref[:, :, :OH // 2 * 2, :OW // 2 * 2].reshape(N, M, OH // 2, 2, OW // 2, 2).max(axis=(3, 5))
+    out = run(x, N) if res is None else run(x, N, res)
+    assert out.shape == oshape
+    rm.assert_within_tolerance(out, ref, K, xmax)
+    one = run(x[1:2].copy(), 1) if res is None else run(x[1:2].copy(), 1, res[1:2].copy())
+    assert np.array_equal(one.view(np.uint32), out[1:2].view(np.uint32))
+
+
 def test_conv_f32_stem_inf_stays_local(dev, orc):
     """An infinite input pixel reaches only the outputs whose 7x7 window
     holds it: the stem kernel's padded tap columns (kw = 7 of 8) and padded

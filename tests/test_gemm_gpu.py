@@ -296,6 +296,37 @@ def test_gemm_ternary_cfg3(dev, orc):
     rm.assert_within_tolerance(out[rows], ref, K, np.abs(A).max() * 1.5)
 
 
+@pytest.mark.parametrize("M,K,N,lda", [(1, 256, 10, 256), (1000, 300, 7, 301), (33, 128, 64, 128), (5, 8000, 1, 8000)])
+def test_gemm_small_heads(dev, M, K, N, lda):
+    """Classifier heads (N <= 64, N*K <= 8192) take the LDS FMA kernel: one
+    output per thread, row groups looped over the grid, lda > K, the 2-D
+    addend and both scale/bias orders; a row's bits do not depend on the
+    number of rows."""
+    A, binw, scale, bias = make_binary_problem(M, K, N, seed=M + K + N, lda=lda)
+    packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+    xmax = np.abs(A).max() * 1.5
+    Ak = A[:, :K]
+    for flags, alpha in [(tbn_hip.EPI_RELU, 0.8), (tbn_hip.EPI_BIAS_THEN_SCALE, 1.2)]:
+        out = host(run_gemm("binary", A, lda, M, N, K, packed, K_pad, N_pad, scale, alpha, bias, flags))
+        ref = _f64_dev_gemm(Ak, binw, scale, alpha, bias, relu=bool(flags & tbn_hip.EPI_RELU),
+                            bias_then_scale=bool(flags & tbn_hip.EPI_BIAS_THEN_SCALE))
+        rm.assert_within_tolerance(out, ref, K, xmax * alpha)
+        last = host(run_gemm("binary", A[M - 1:].copy(), lda, 1, N, K, packed, K_pad, N_pad, scale, alpha, bias,
+                             flags))
+        assert np.array_equal(last.view(np.uint32), out[M - 1:].view(np.uint32))
+    cin = np.random.default_rng(3).standard_normal((M, N)).astype(np.float32)
+    C = empty((M, N), torch.float32)
+    tbn_hip.call("tbn_hip_gemm_f32_quantized", tbn_hip.WEIGHTS_BINARY, P(to_dev(A)), lda, M, N, K, P(packed), K_pad,
+                 N_pad, P(to_dev(scale)), 1.0, None, P(to_dev(cin)), 0, -0.5, 0, P(C), N, None)
+    rm.assert_within_tolerance(host(C), _f64_dev_gemm(Ak, binw, scale, 1.0, None, cin=cin, beta=-0.5), K, xmax)
+    t = np.random.default_rng(M).choice(np.array([-1, 0, 1], np.int8), size=(K, N))
+    K_pad4 = (K + 31) // 32 * 32
+    tp = empty(N * K_pad4 // 4, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(t)), K, N, tbn_hip.LAYOUT_KN, K_pad4, N, P(tp), None)
+    out = host(run_gemm("ternary", A, lda, M, N, K, tp, K_pad4, N, scale, 0.9, bias, tbn_hip.EPI_RELU))
+    rm.assert_within_tolerance(out, _f64_dev_ternary(Ak, t, scale, 0.9, bias, relu=True), K, xmax)
+
+
 def test_gemm_special_values(dev, orc):
     M, K, N = 4, 64, 8
     A = np.zeros((M, K), np.float32)
