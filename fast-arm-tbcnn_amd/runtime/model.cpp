@@ -228,6 +228,7 @@ struct Value {
     bool is_input = false;
     int view_of = -1;        // storage shared with another value
     const void* const_ptr = nullptr;
+    void* bound = nullptr;   // input read in place from the caller's device tensor
     int64_t offset = -1;     // arena offset (bytes)
     int def = -1, last = -1; // op index of definition and last use
 };
@@ -987,6 +988,7 @@ struct TBNModel::Session::Impl {
         if (val.is_const) return const_cast<void*>(val.const_ptr);
         const int r = root(v);
         if (values[r].is_const) return const_cast<void*>(values[r].const_ptr);
+        if (values[r].bound) return values[r].bound;
         return static_cast<uint8_t*>(arena.data()) + values[r].offset;
     }
     float* fp(int v) { return static_cast<float*>(ptr(v)); }
@@ -1155,10 +1157,40 @@ struct TBNModel::Session::Impl {
         }
     }
 
+    // A device input of the planned dtype, 256-byte aligned like the arena,
+    // that no graph output shares storage with is read in place by the ops
+    // (no copy); the others are copied into the arena.  No op writes to its
+    // inputs' storage (each op's output is placed apart from its live
+    // inputs), so the caller's tensor is only read.  Returns whether any
+    // binding changed since the last call.
+    bool bind_inputs() {
+        bool changed = false;
+        for (auto& kv : inputs) {
+            Value& v = values[root(value_id.at(kv.first))];
+            const Tensor& t = kv.second;
+            void* want = nullptr;
+            if (t.on_device() && t.dtype() == v.dtype && t.data_size() == v.shape.size() * element_size(v.dtype) &&
+                reinterpret_cast<uintptr_t>(t.data()) % 256 == 0) {
+                want = const_cast<void*>(t.data());
+                for (const auto& name : graph->outputs) {
+                    auto it = value_id.find(name);
+                    if (it != value_id.end() && &values[root(it->second)] == &v) want = nullptr;
+                }
+            }
+            if (v.bound != want) changed = true;
+            v.bound = want;
+        }
+        return changed;
+    }
+
     void upload_inputs(tbn_stream_t s) {
         for (auto& kv : inputs) {
             const int id = value_id.at(kv.first);
             const Tensor& t = kv.second;
+            if (values[root(id)].bound) continue;
+            const Value& v = values[root(id)];
+            TBN_CHECK(t.dtype() == v.dtype && t.data_size() == v.shape.size() * element_size(v.dtype),
+                      InvalidArgumentError, "Input '" + kv.first + "' has the wrong data type");
             if (t.on_device()) {
                 if (hipMemcpyAsync(ptr(id), t.data(), t.data_size(), hipMemcpyDeviceToDevice,
                                    static_cast<hipStream_t>(s)) != hipSuccess)
@@ -1187,6 +1219,8 @@ struct TBNModel::Session::Impl {
                       std::to_string(inputs.size()) + ")");
         if (!plan_valid()) compile();
         tbn_stream_t s = cur_stream();
+        // a replayed graph holds the input addresses it was recorded with
+        if (bind_inputs()) drop_graph();
         if (!graph_replay) {
             upload_inputs(s);
             run_ops(s);

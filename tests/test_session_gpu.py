@@ -131,6 +131,51 @@ def test_session_device_input(dev, tbn):
     assert np.array_equal(dev_out.numpy(), want)
 
 
+def test_session_device_input_read_in_place(dev, tbn):
+    """An aligned device input is read in place by the ops (no copy): replays
+    follow its contents, a different tensor is re-recorded, an unaligned one
+    is copied, and the caller's data is never written."""
+    import torch
+    spec = models.lenet(seed=8)
+    xs = [models.lenet_input(s) for s in (8, 9, 10)]
+    _, eager = _session(tbn, spec, quant=True)
+    wants = []
+    for x in xs:
+        eager.set_input("input", x)
+        eager.run()
+        wants.append(eager.get_output("output"))
+    stream = torch.cuda.Stream()
+    tbn.set_current_stream(stream.cuda_stream)
+    try:
+        with torch.cuda.stream(stream):
+            _, rs = _session(tbn, spec, quant=True, replay=True)
+            xd = torch.from_numpy(xs[0]).cuda()
+            rs.set_input("input", tbn.Tensor.wrap(xd.data_ptr(), list(xs[0].shape), "float32", "hip"))
+            for i in range(4):  # eager, capture, replays; the contents change in place
+                k = i % 2
+                xd.copy_(torch.from_numpy(xs[k]))
+                rs.run()
+                assert np.array_equal(rs.get_output("output"), wants[k]), f"run {i}"
+                assert np.array_equal(xd.cpu().numpy(), xs[k])
+            other = torch.from_numpy(xs[2]).cuda()
+            rs.set_input("input", tbn.Tensor.wrap(other.data_ptr(), list(xs[2].shape), "float32", "hip"))
+            for i in range(2):
+                rs.run()
+                assert np.array_equal(rs.get_output("output"), wants[2]), f"other tensor, run {i}"
+            flat = torch.zeros(xs[1].size + 64, device="cuda")
+            flat[1:1 + xs[1].size].copy_(torch.from_numpy(xs[1].reshape(-1)))
+            un = flat[1:1 + xs[1].size]
+            assert un.data_ptr() % 256 != 0
+            rs.set_input("input", tbn.Tensor.wrap(un.data_ptr(), list(xs[1].shape), "float32", "hip"))
+            for i in range(2):
+                rs.run()
+                assert np.array_equal(rs.get_output("output"), wants[1]), f"unaligned tensor, run {i}"
+            assert np.array_equal(un.cpu().numpy().reshape(xs[1].shape), xs[1])
+    finally:
+        stream.synchronize()
+        tbn.set_current_stream(0)
+
+
 def test_relu_ternary_replacement(dev, tbn, orc):
     """The reference turns Relu into a ternary activation when quantization is
     on and the input name contains conv2d_1 (model.hpp:1144-1165)."""
