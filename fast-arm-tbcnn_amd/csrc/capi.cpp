@@ -53,8 +53,14 @@ int alloc_async(void*& ptr, size_t bytes, hipStream_t s) {
 int stream_workspace(hipStream_t s, size_t bytes, void*& ptr, bool& temporary) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     const bool capturing = hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone;
+    // No allocation is recorded into a captured graph: a replay of a graph
+    // holding split-K temporaries as graph allocations ended in a memory
+    // fault once, with no cause found, so such calls are refused while the
+    // stream captures (the Session then runs that plan eagerly).
+    if (capturing)
+        return fail(TBN_NOT_IMPLEMENTED, "split-K workspace: no allocation while the stream is being captured");
     int dev = 0;
-    if (!capturing && hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
         std::lock_guard<std::mutex> lock(g_ws_mutex);
         Workspace& w = g_ws[dev];
         if (w.ptr && w.stream == s && w.bytes >= bytes) {

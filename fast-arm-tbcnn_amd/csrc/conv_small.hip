@@ -128,6 +128,23 @@ small_conv_kernel(const float* __restrict__ x, SmallGeom g, const void* __restri
     const int m_lo = i0 / g.plane;
     const int mb = (i_end - 1) / g.plane - m_lo + 1;
 
+    // this thread's output and its epilogue operands, loaded ahead of staging
+    const int i = i0 + static_cast<int>(threadIdx.x);
+    const bool live = i < i_end;
+    const int m = live ? i / g.plane : m_lo, pos = live ? i - m * g.plane : 0;
+    int oh, ow;
+    if (g.pool) {
+        const int win = pos >> 2, q = pos & 3;
+        oh = 2 * (win / g.PW) + (q >> 1);
+        ow = 2 * (win % g.PW) + (q & 1);
+    } else {
+        oh = pos / g.OW;
+        ow = pos - oh * g.OW;
+    }
+    const float mult = scale ? alpha * scale[m] : alpha;
+    const float b = bias ? bias[m] : 0.0f;
+    const float rv = residual ? residual[(static_cast<int64_t>(n) * g.M + m) * (g.OH * g.OW) + oh * g.OW + ow] : 0.0f;
+
     const int pp = g.Hp * g.Wp;
     const float* xn = x + static_cast<int64_t>(n) * g.C * g.H * g.W;
     stage4(g.C * pp,
@@ -149,27 +166,12 @@ small_conv_kernel(const float* __restrict__ x, SmallGeom g, const void* __restri
     }
     __syncthreads();
 
-    const int i = i0 + static_cast<int>(threadIdx.x);
-    if (i >= i_end) return;  // past the block's only barrier; pooled windows leave whole
-    const int m = i / g.plane, pos = i - m * g.plane;
-    int oh, ow;
-    if (g.pool) {
-        const int win = pos >> 2, q = pos & 3;
-        oh = 2 * (win / g.PW) + (q >> 1);
-        ow = 2 * (win % g.PW) + (q & 1);
-    } else {
-        oh = pos / g.OW;
-        ow = pos - oh * g.OW;
-    }
-    // the epilogue's operands, loaded before the FMA chain
-    const float mult = scale ? alpha * scale[m] : alpha;
-    const float b = bias ? bias[m] : 0.0f;
-    const float rv = residual ? residual[(static_cast<int64_t>(n) * g.M + m) * (g.OH * g.OW) + oh * g.OW + ow] : 0.0f;
+    if (!live) return;  // past the block's only barrier; pooled windows leave whole
     const float* x0 = xs + oh * g.sh * g.Wp + ow * g.sw;
     const float* wr = ws + (m - m_lo) * g.Kp;
     float acc = 0.0f;
     int k = 0;
-#pragma unroll 2
+#pragma unroll 4
     for (; k + 4 <= g.K; k += 4) {
         const int4 o = *reinterpret_cast<const int4*>(offs + k);
         const float4 w4 = *reinterpret_cast<const float4*>(wr + k);

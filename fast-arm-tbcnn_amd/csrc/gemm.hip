@@ -126,9 +126,10 @@ int f32_gemm_splits(int64_t N, int64_t K) {
 
 // ---- small GEMMs (a classifier head: few columns, short K) ----------------
 // The weight columns are decoded to fp32 in LDS once per block; each block
-// then stages groups of rows of A in LDS and computes one output per thread
-// with a plain fp32 FMA chain over k in order.  Chosen from N and K only, so
-// a row's result does not depend on the batch.  Staging keeps four global
+// then stages groups of rows of A in LDS; each output is computed by 1 to 8
+// lanes, each an fp32 FMA chain over its contiguous share of k, added in a
+// fixed pairwise tree.  Lanes and shares follow from N and K only, so a
+// row's result does not depend on the batch.  Staging keeps four global
 // loads in flight per thread; rows sit ceil4(K) + 4 floats apart so the
 // 16-byte reads of different columns start on different banks.
 constexpr int kSmallGemmW = 8192;  // floats of decoded weights
@@ -141,7 +142,9 @@ struct SmallGemm {
     int64_t b_k, b_col;   // WMODE 0 strides; WMODE 1/2: b_col = bytes per packed column
     int M, N, K;
     int Kp;               // LDS row stride
-    int rows;             // rows of A per group: min(256 / N, kSmallGemmA / Kp)
+    int lanes;            // lanes per output (a power of two, at most 8)
+    int kc;               // k per lane: ceil4(ceil(K / lanes))
+    int rows;             // rows of A per group: min(256 / (N * lanes), kSmallGemmA / Kp)
 };
 
 int small_gemm_stride(int64_t K) { return static_cast<int>((K + 3) / 4 * 4 + 4); }
@@ -204,8 +207,13 @@ __global__ void __launch_bounds__(256) small_gemm_kernel(SmallGemm g, GemmEpi ep
                         }
                     });
     }
+    // thread t: lane sl = t % S of output (row r, column n), (r, n) = divmod(t / S, N);
+    // lane sl sums k in [sl*kc, sl*kc + kc) and the S lanes add pairwise
     const int groups = (g.M + g.rows - 1) / g.rows;
-    const int r = static_cast<int>(threadIdx.x) / g.N, n = static_cast<int>(threadIdx.x) - r * g.N;
+    const int S = g.lanes, kc = g.kc;
+    const int t = static_cast<int>(threadIdx.x) / S, sl = static_cast<int>(threadIdx.x) % S;
+    const int r = t / g.N, n = t - r * g.N;
+    const int k_lo = min(sl * kc, K), k_hi = min(k_lo + kc, K);
     const float* w = ws + n * Kp;
     for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {
         const int m0 = grp * g.rows;
@@ -221,18 +229,20 @@ __global__ void __launch_bounds__(256) small_gemm_kernel(SmallGemm g, GemmEpi ep
                         as[rr * Kp + (i - rr * K)] = v;
                     });
         __syncthreads();
-        if (r >= rows) continue;
+        // every lane takes part in the shuffles; rows past the group's end
+        // compute on row 0 and store nothing
+        const bool live = r < rows;
         // the epilogue's operands, loaded before the FMA chain
-        const int m = m0 + r;
+        const int m = m0 + (live ? r : 0);
         const float mult = epi.scale ? epi.alpha * epi.scale[n] : epi.alpha;
         const float b = epi.bias ? epi.bias[n] : 0.0f;
         const float cv = epi.cin ? epi.beta * (epi.cin_1d ? epi.cin[n] : epi.cin[static_cast<int64_t>(m) * g.N + n])
                                  : 0.0f;
-        const float* a = as + r * Kp;
+        const float* a = as + (live ? r : 0) * Kp;
         float acc = 0.0f;
-        int k = 0;
-#pragma unroll 2
-        for (; k + 4 <= K; k += 4) {
+        int k = k_lo;
+#pragma unroll 4
+        for (; k + 4 <= k_hi; k += 4) {
             const float4 a4 = *reinterpret_cast<const float4*>(a + k);
             const float4 w4 = *reinterpret_cast<const float4*>(w + k);
             acc = fmaf(a4.x, w4.x, acc);
@@ -240,7 +250,9 @@ __global__ void __launch_bounds__(256) small_gemm_kernel(SmallGemm g, GemmEpi ep
             acc = fmaf(a4.z, w4.z, acc);
             acc = fmaf(a4.w, w4.w, acc);
         }
-        for (; k < K; ++k) acc = fmaf(a[k], w[k], acc);
+        for (; k < k_hi; ++k) acc = fmaf(a[k], w[k], acc);
+        for (int d = 1; d < S; d <<= 1) acc += __shfl_xor(acc, d);
+        if (!live || sl != 0) continue;
         // GemmEpi's arithmetic for one element
         float v = (epi.flags & TBN_EPI_BIAS_THEN_SCALE) ? (acc + b) * mult : acc * mult + b;
         if (epi.cin) v += cv;
@@ -256,7 +268,13 @@ bool small_gemm_fits(int64_t N, int64_t K) {
 template <int WMODE>
 int launch_small_gemm(SmallGemm g, const GemmEpi& epi, hipStream_t s) {
     g.Kp = small_gemm_stride(g.K);
-    g.rows = std::max(1, std::min(256 / g.N, kSmallGemmA / g.Kp));
+    // lanes per output from N and K only: as many as fit 256 threads with
+    // one row, up to 8, keeping at least 32 k per lane
+    g.lanes = 1;
+    while (g.lanes < 8 && g.N * g.lanes * 2 <= 256 && g.K >= 64 * g.lanes) g.lanes *= 2;
+    g.kc = (g.K + g.lanes - 1) / g.lanes;
+    g.kc = (g.kc + 3) / 4 * 4;
+    g.rows = std::max(1, std::min(256 / (g.N * g.lanes), kSmallGemmA / g.Kp));
     const int64_t groups = tbn_hip::ceil_div(static_cast<int64_t>(g.M), g.rows);
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(groups, 2048));
     hipLaunchKernelGGL(small_gemm_kernel<WMODE>, dim3(blocks), dim3(256), 0, s, g, epi);
@@ -306,7 +324,7 @@ int gemm_quant(const float* A, int64_t lda, int64_t M, int64_t N, int64_t K, con
                 (cin && beta != 0.0f) ? cin : nullptr, beta, cin_1d, flags};
     const int64_t col_bytes = TERNARY ? K_pad / 4 : K_pad / 8;
     if (small_gemm_fits(N, K)) {
-        const SmallGemm sg{A, lda, 1, packed, 0, col_bytes, int(M), int(N), int(K), 0, 0};
+        const SmallGemm sg{A, lda, 1, packed, 0, col_bytes, int(M), int(N), int(K), 0, 0, 0, 0};
         return launch_small_gemm<TERNARY ? 2 : 1>(sg, epi, tbn_hip::stream_of(stream));
     }
     {
@@ -392,7 +410,7 @@ int tbn_hip_gemm_f32(const float* A, const float* B, const float* Cin, int c_is_
                 (Cin && beta != 0.0f) ? Cin : nullptr, beta, c_is_1d, flags};
     if (small_gemm_fits(N, K)) {
         const SmallGemm sg{A, transA ? 1 : K, transA ? M : 1, B, transB ? 1 : N, transB ? K : 1,
-                           static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), 0, 0};
+                           static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), 0, 0, 0, 0};
         return launch_small_gemm<0>(sg, epi, tbn_hip::stream_of(stream));
     }
     const int tiles_r = static_cast<int>(tbn_hip::ceil_div(M, Cfg::BR));

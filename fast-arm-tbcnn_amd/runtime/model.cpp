@@ -267,6 +267,7 @@ struct TBNModel::Session::Impl {
     hipGraph_t hip_graph = nullptr;
     hipGraphExec_t hip_graph_exec = nullptr;
     int eager_runs = 0;
+    bool replay_off = false;  // the plan needs an allocation that capture refuses
 
     ~Impl() { drop_graph(); if (replay_stream) (void)hipStreamDestroy(replay_stream); }
 
@@ -996,6 +997,7 @@ struct TBNModel::Session::Impl {
     void compile() {
         drop_graph();
         eager_runs = 0;
+        replay_off = false;
         values.clear();
         value_id.clear();
         ops.clear();
@@ -1244,20 +1246,35 @@ struct TBNModel::Session::Impl {
             (void)hipStreamWaitEvent(rs, ev, 0);
         }
         upload_inputs(rs);
-        if (eager_runs < 1) {
+        if (eager_runs < 1 || replay_off) {
             run_ops(rs);
             ++eager_runs;
         } else {
             if (!hip_graph_exec) {
                 if (hipStreamBeginCapture(rs, hipStreamCaptureModeThreadLocal) != hipSuccess)
                     throw RuntimeError("hipStreamBeginCapture failed");
+                bool refused = false;
                 try {
                     run_ops(rs);
+                } catch (const NotImplementedError&) {
+                    // an op needs a split-K workspace, which is never
+                    // allocated under capture: this plan runs eagerly
+                    refused = true;
                 } catch (...) {
                     hipGraph_t g = nullptr;
                     (void)hipStreamEndCapture(rs, &g);
                     if (g) (void)hipGraphDestroy(g);
                     throw;
+                }
+                if (refused) {
+                    hipGraph_t g = nullptr;
+                    (void)hipStreamEndCapture(rs, &g);
+                    if (g) (void)hipGraphDestroy(g);
+                    (void)hipGetLastError();
+                    replay_off = true;
+                    run_ops(rs);
+                    ++eager_runs;
+                    goto done;
                 }
                 if (hipStreamEndCapture(rs, &hip_graph) != hipSuccess) throw RuntimeError("hipStreamEndCapture failed");
                 if (hipGraphInstantiate(&hip_graph_exec, hip_graph, nullptr, nullptr, 0) != hipSuccess)
@@ -1265,6 +1282,7 @@ struct TBNModel::Session::Impl {
             }
             if (hipGraphLaunch(hip_graph_exec, rs) != hipSuccess) throw RuntimeError("hipGraphLaunch failed");
         }
+    done:
         if (own) {
             // the null stream continues after the replay
             (void)hipEventRecord(ev, rs);
