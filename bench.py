@@ -28,8 +28,8 @@ sys.path.insert(0, str(ROOT / "fast-arm-tbcnn_amd" / "python"))
 sys.path.insert(0, str(ROOT / "fast-arm-tbcnn_amd" / "lib"))
 
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
-BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (the pipe the exact split runs on)
-FP32_PEAK_TFLOPS = 157.3    # MI355X dense fp32 (the arithmetic of the path: the relevant roofline)
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA: the pipe every exact fp32 x +-1 product runs on
+FP32_PEAK_TFLOPS = 157.3    # MI355X dense fp32 (vector or matrix), for comparison only
 TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
 
 
@@ -134,6 +134,9 @@ def conv_cfg4(torch, tbn_hip, seed):
     conv_w = torch.empty(wbytes.value, dtype=torch.uint8, device=dev)
     tbn_hip.call("tbn_hip_pack_conv_weights", tbn_hip.WEIGHTS_BINARY, packed.data_ptr(), K_pad, N_pad, desc,
                  conv_w.data_ptr(), None)
+    # the tile is timed once per geometry, as a Session does when it compiles
+    tbn_hip.call("tbn_hip_conv2d_tune_prepacked", tbn_hip.WEIGHTS_BINARY, x.data_ptr(), desc, conv_w.data_ptr(),
+                 scale.data_ptr(), 1.0, bias.data_ptr(), None, tbn_hip.EPI_RELU, y.data_ptr(), None)
     torch.cuda.synchronize()
 
     def step(sh):
@@ -170,6 +173,31 @@ def session_workload(torch, _tbn, which, stream, replay):
     def step(sh):
         sess.run()
     return step, (model, sess, xd)
+
+
+def mfma_roofline(flops, ms, kernel, algo_bytes, traffic_entry):
+    """Roofline object for a kernel on the bf16 matrix pipe: algorithmic
+    flop rate over the dense bf16 peak, the issued-MFMA rate (3 bf16 products
+    per fp32 x +-1 product), and HBM traffic from the calibrated counters."""
+    tflops = flops / (ms * 1e-3) / 1e12
+    out = {
+        "bound": "mfma",
+        "achieved": round(tflops, 2),
+        "peak": BF16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+        "traffic": None,
+        "kernel": kernel,
+        "mfma_issued": {"dtype": "bf16", "per_product": 3, "tflops": round(3.0 * tflops, 1),
+                        "peak": BF16_PEAK_TFLOPS, "frac": round(3.0 * tflops / BF16_PEAK_TFLOPS, 4)},
+        "fp32_peak_ratio": round(tflops / FP32_PEAK_TFLOPS, 3),
+        "algorithmic_bytes": int(algo_bytes),
+        "hbm_gbs_algorithmic": round(algo_bytes / (ms * 1e-3) / 1e9, 1),
+    }
+    if traffic_entry:
+        out["traffic"] = traffic_entry.get("bytes_per_launch")
+        out["traffic_kernel"] = traffic_entry.get("kernel")
+    return out
 
 
 def cpu_baseline(M, N, K, budget_s):
@@ -298,8 +326,8 @@ def main():
         del A, binw, packed, out
     if want("gemm1024"):
         step, keep, _, _ = packed_gemm(torch, tbn_hip, 1024, 1024, 1024, seed=4)
-        # split K with a workspace, which is never allocated under graph
-        # capture: stream-timed (the kernel outlasts the Python launch)
+        # stream-timed: a K-split launch takes the stream workspace, which
+        # graph capture refuses; each launch outlasts the Python call
         g_ms = timed(step)
         extra["gemm_cfg2_us"] = round(g_ms * 1e3, 2)
         extra["gemm_cfg2_gflops_equiv"] = round(2.0 * 1024 ** 3 / (g_ms * 1e-3) / 1e9, 1)
@@ -365,33 +393,19 @@ def main():
     flops = 2.0 * M * N * K
     gflops = flops / (ms * 1e-3) / 1e9
     algo_bytes = 4.0 * M * K + K_pad * N_pad / 8 + 4.0 * N + 4.0 * M * N
-    achieved_tflops = flops / (ms * 1e-3) / 1e12
-    # The path's arithmetic is fp32 (fp32 activations x +-1, fp32 accumulation):
-    # the roofline is MI355X's fp32 matrix peak.  The kernel reaches past it by
-    # running each fp32 x +-1 product as three exact bf16 MFMA products on the
-    # bf16 pipe; "mfma_issued" reports that pipe's own utilisation.
-    roofline = {
-        "bound": "mfma",
-        "achieved": round(achieved_tflops, 2),
-        "peak": FP32_PEAK_TFLOPS,
-        "unit": "TFLOP/s",
-        "frac": round(achieved_tflops / FP32_PEAK_TFLOPS, 4),
-        "traffic": None,
-        "kernel": "gemm_wide_kernel<WideCfg<128,512,128,64,64>,false,false>",
-        "mfma_issued": {
-            "dtype": "bf16",
-            "tflops": round(3.0 * achieved_tflops, 1),
-            "peak": BF16_PEAK_TFLOPS,
-            "frac": round(3.0 * achieved_tflops / BF16_PEAK_TFLOPS, 4),
-            "per_product": 3,
-        },
-        "algorithmic_bytes": int(algo_bytes),
-        "hbm_gbs_algorithmic": round(algo_bytes / (ms * 1e-3) / 1e9, 1),
-    }
-    if TRAFFIC_FILE.exists():
-        tr = json.loads(TRAFFIC_FILE.read_text()).get("gemm_f32_binary_4096")
-        if tr:
-            roofline["traffic"] = tr.get("bytes_per_launch")
+    traffic = json.loads(TRAFFIC_FILE.read_text()) if TRAFFIC_FILE.exists() else {}
+    # Every fp32 x +-1 product runs on the bf16 matrix pipe (three exact bf16
+    # products per fp32 one), so the roofline is the dense bf16 MFMA peak and
+    # `frac` is the algorithmic rate over it; `mfma_issued` counts the three
+    # products actually issued, and `fp32_peak_ratio` compares with the fp32
+    # peak a plain fp32 kernel would be bound by.
+    roofline = mfma_roofline(flops, ms, "gemm_wide_kernel<WideCfg<128,512,128,64,64>,false,false>",
+                             algo_bytes, traffic.get("gemm_f32_binary_4096"))
+    if "conv_us_per_batch" in extra:
+        conv_bytes = 4.0 * 64 * 64 * 196 + 128 * 640 / 8 + 8.0 * 128 + 4.0 * 64 * 128 * 196
+        extra["roofline_conv"] = mfma_roofline(2.0 * 64 * 196 * 576 * 128, extra["conv_us_per_batch"] * 1e-3,
+                                               extra.get("conv_kernel", "conv_patch_kernel"), conv_bytes,
+                                               traffic.get("conv_cfg4"))
 
     result = {
         "metric": "float×binary GEMM GFLOP/s-equiv @4096³; Conv2D 64→128 14×14 µs/batch",

@@ -1,4 +1,7 @@
 // Library-level C ABI: error strings, version, device check, synchronisation.
+#include <algorithm>
+#include <atomic>
+#include <cstdlib>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -87,6 +90,30 @@ void release_workspace(void* ptr, bool temporary, hipStream_t s) {
     if (temporary && ptr) (void)hipFreeAsync(ptr, s);
 }
 
+// Tuning controls: read from the environment once (TBN_CONV_TILE,
+// TBN_CONV_SPLITS, TBN_GEMM_SPLITS), then changed only through
+// tbn_hip_set_tuning.  Relaxed atomics: a value is a launch-shape choice, so a
+// call that races with a change simply sees the old or the new one.
+namespace {
+std::atomic<int> g_tuning[4];
+std::once_flag g_tuning_once;
+
+void tuning_init() {
+    auto env = [](const char* name, int dflt) {
+        const char* e = std::getenv(name);
+        return e && *e ? std::atoi(e) : dflt;
+    };
+    g_tuning[TBN_TUNE_CONV_TILE].store(env("TBN_CONV_TILE", -1), std::memory_order_relaxed);
+    g_tuning[TBN_TUNE_CONV_SPLITS].store(std::max(0, env("TBN_CONV_SPLITS", 0)), std::memory_order_relaxed);
+    g_tuning[TBN_TUNE_GEMM_SPLITS].store(std::max(0, env("TBN_GEMM_SPLITS", 0)), std::memory_order_relaxed);
+}
+}  // namespace
+
+int tuning(int option) {
+    std::call_once(g_tuning_once, tuning_init);
+    return g_tuning[option].load(std::memory_order_relaxed);
+}
+
 int ensure_device() {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
@@ -137,6 +164,24 @@ int tbn_hip_version(void) { return 100; /* 0.1.0 */ }
 int tbn_hip_device_check(void) {
     int rc = tbn_hip::ensure_device();
     return rc == TBN_SUCCESS ? tbn_hip::ok() : rc;
+}
+
+int tbn_hip_set_tuning(int option, int value) {
+    TBN_REQUIRE(option >= TBN_TUNE_CONV_TILE && option <= TBN_TUNE_GEMM_SPLITS, TBN_INVALID_ARGUMENT,
+                "unknown tuning option");
+    TBN_REQUIRE(option == TBN_TUNE_CONV_TILE ? value >= -1 : value >= 0, TBN_INVALID_ARGUMENT,
+                "tuning value out of range");
+    (void)tbn_hip::tuning(option);  // the environment is read before the first change
+    tbn_hip::g_tuning[option].store(value, std::memory_order_relaxed);
+    return tbn_hip::ok();
+}
+
+int tbn_hip_get_tuning(int option, int* value) {
+    TBN_REQUIRE(option >= TBN_TUNE_CONV_TILE && option <= TBN_TUNE_GEMM_SPLITS, TBN_INVALID_ARGUMENT,
+                "unknown tuning option");
+    TBN_REQUIRE(value != nullptr, TBN_INVALID_ARGUMENT, "null pointer");
+    *value = tbn_hip::tuning(option);
+    return tbn_hip::ok();
 }
 
 int tbn_hip_synchronize(tbn_stream_t stream) {

@@ -28,6 +28,9 @@ inline hipStream_t stream_of(tbn_stream_t s) { return reinterpret_cast<hipStream
 int stream_workspace(hipStream_t s, size_t bytes, void*& ptr, bool& temporary);
 void release_workspace(void* ptr, bool temporary, hipStream_t s);
 
+// Current value of a tuning control (TBN_TUNE_*), the environment read once.
+int tuning(int option);
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace tbn_hip

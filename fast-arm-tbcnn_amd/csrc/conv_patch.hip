@@ -751,13 +751,9 @@ constexpr TileChoice choice(int cfg, int linear, int single = 0) {
     return TileChoice{cfg, linear, Cfg::TH, Cfg::TW, Cfg::BM, Cfg::NT, single};
 }
 
-// TBN_CONV_TILE=<id> forces one tile, a tuning aid read on every call: id =
-// cfg for linear tiles, 10 + cfg for 2-D tiles, plus 20 for the one-buffer
-// variants.
-int tile_override() {
-    const char* e = std::getenv("TBN_CONV_TILE");
-    return e ? std::atoi(e) : -1;
-}
+// The TBN_TUNE_CONV_TILE control forces one tile: id = cfg for linear tiles,
+// 10 + cfg for 2-D tiles, plus 20 for the one-buffer variants.
+int tile_override() { return tbn_hip::tuning(TBN_TUNE_CONV_TILE); }
 
 // In preference order (linear tiles store whole 128-byte pixel runs; larger
 // tiles do more MFMA per decoded weight word), the first tile whose patch fits
@@ -873,12 +869,12 @@ int dispatch_patch(int id, const float* x, const PatchGeom& g, const uint8_t* w,
 
 // ---- tile selection by measurement ------------------------------------------
 // Which tile is fastest depends on image size, channel counts and stride in
-// ways a static rule gets wrong by up to 1.6x.  The first call for a shape
-// times every feasible tile (into a temporary output) and caches the winner
-// for the process; every tile accumulates each output in the same order
-// (chunk, tap, k-slice, hi/mid/lo), so the choice never changes results.
-// Calls under stream capture, TBN_CONV_TUNE=0 or a forced tile use the
-// static rule.
+// ways a static rule gets wrong by up to 1.6x.  tbn_hip_conv2d_tune_prepacked
+// (called once per layer, e.g. by the Session at compile time) times every
+// feasible tile and caches the winner for the process; the per-call path only
+// reads that cache, else uses the static rule, and never times, allocates or
+// waits.  Every tile accumulates each output in the same order (chunk, tap,
+// k-slice, hi/mid/lo), so the choice never changes results.
 
 struct PlanKey {
     int64_t v[16];
@@ -894,24 +890,20 @@ std::map<PlanKey, int>& plan_cache() {
     return m;
 }
 
-bool tuning_allowed(hipStream_t s) {
-    const char* e = std::getenv("TBN_CONV_TUNE");
-    if (e && e[0] == '0') return false;
-    if (tile_override() >= 0) return false;
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    return hipStreamIsCapturing(s, &st) == hipSuccess && st == hipStreamCaptureStatusNone;
+PlanKey plan_key(const tbn_conv2d_desc* d, bool ternary, const PatchEpi& epi) {
+    return PlanKey{{d->n, d->c, d->h, d->w, d->m, d->kh, d->kw, d->sh, d->sw, d->ph, d->pw, d->dh, d->dw,
+                    ternary ? 1 : 0, epi.flags, epi.residual ? 1 : 0}};
 }
 
 template <bool TERNARY>
 int dispatch_patch(int id, const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
                    const PatchEpi& epi, hipStream_t s);
 
+// The tile for this call: a forced tile, the tuned one, else the static rule.
 template <bool TERNARY>
-int select_tile(const tbn_conv2d_desc* d, PatchGeom& g, const float* x, const uint8_t* w, int64_t col_bytes,
-                int m_alloc, const PatchEpi& epi, hipStream_t s, TileChoice& out) {
-    const PlanKey key{{d->n, d->c, d->h, d->w, d->m, d->kh, d->kw, d->sh, d->sw, d->ph, d->pw, d->dh, d->dw,
-                       TERNARY ? 1 : 0, epi.flags, epi.residual ? 1 : 0}};
+int select_tile(const tbn_conv2d_desc* d, PatchGeom& g, const PatchEpi& epi, TileChoice& out) {
     if (tile_override() < 0) {
+        const PlanKey key = plan_key(d, TERNARY, epi);
         std::lock_guard<std::mutex> lock(plan_mutex());
         auto it = plan_cache().find(key);
         if (it != plan_cache().end()) {
@@ -921,58 +913,52 @@ int select_tile(const tbn_conv2d_desc* d, PatchGeom& g, const float* x, const ui
         }
     }
     if (!choose_tile(g, out)) return tbn_hip::fail(TBN_INVALID_SHAPE, "no conv tile fits this geometry");
-    if (!tuning_allowed(s)) return TBN_SUCCESS;
-    const int ceil_m = (g.M + 31) / 32 * 32;
-    int cands[sizeof(kMenu) / sizeof(kMenu[0])];
-    int ncand = 0;
-    for (int i = 0; i < static_cast<int>(sizeof(kMenu) / sizeof(kMenu[0])); ++i) {
-        PatchGeom t;
-        if (kMenu[i].BM > ceil_m || !tile_fits(g, kMenu[i], t)) continue;
-        cands[ncand++] = i;
-    }
-    if (ncand <= 1) return TBN_SUCCESS;
-    const int64_t plane = g.pool ? static_cast<int64_t>(g.PH) * g.PW : static_cast<int64_t>(g.OH) * g.OW;
-    const size_t ybytes = static_cast<size_t>(g.N) * g.M * plane * sizeof(float);
-    void* tmp = nullptr;
+    return TBN_SUCCESS;
+}
+
+// Times each feasible tile (one untimed launch, then two timed back to back,
+// all writing epi.y) and caches the fastest under the call's key.
+template <bool TERNARY>
+int tune_tile(const tbn_conv2d_desc* d, const PatchGeom& g0, const float* x, const uint8_t* w, int64_t col_bytes,
+              int m_alloc, const PatchEpi& epi, hipStream_t s) {
+    const int ceil_m = (g0.M + 31) / 32 * 32;
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    if (hipMallocAsync(&tmp, ybytes, s) != hipSuccess || hipEventCreate(&e0) != hipSuccess ||
-        hipEventCreate(&e1) != hipSuccess) {
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
         (void)hipGetLastError();
-        if (tmp) (void)hipFreeAsync(tmp, s);
         if (e0) (void)hipEventDestroy(e0);
-        return TBN_SUCCESS;  // keep the static choice
+        return tbn_hip::fail(TBN_RUNTIME_ERROR, "conv tuning: hipEventCreate failed");
     }
-    PatchEpi te = epi;
-    te.y = static_cast<float*>(tmp);
     int best = -1;
     float best_ms = 0.0f;
-    for (int k = 0; k < ncand; ++k) {
-        const TileChoice& c = kMenu[cands[k]];
+    int rc = TBN_SUCCESS;
+    for (int i = 0; i < static_cast<int>(sizeof(kMenu) / sizeof(kMenu[0])) && rc == TBN_SUCCESS; ++i) {
+        const TileChoice& c = kMenu[i];
         PatchGeom t;
-        tile_fits(g, c, t);
-        if (dispatch_patch<TERNARY>(c.cfg, x, t, w, col_bytes, m_alloc, te, s) != TBN_SUCCESS) continue;
+        if (c.BM > ceil_m || !tile_fits(g0, c, t)) continue;
+        if (dispatch_patch<TERNARY>(c.cfg, x, t, w, col_bytes, m_alloc, epi, s) != TBN_SUCCESS) continue;
         (void)hipEventRecord(e0, s);
         bool ok = true;
-        for (int r = 0; r < 2 && ok; ++r) ok = dispatch_patch<TERNARY>(c.cfg, x, t, w, col_bytes, m_alloc, te, s) == TBN_SUCCESS;
+        for (int r = 0; r < 2 && ok; ++r) ok = dispatch_patch<TERNARY>(c.cfg, x, t, w, col_bytes, m_alloc, epi, s) == TBN_SUCCESS;
         (void)hipEventRecord(e1, s);
         float ms = 0.0f;
-        if (!ok || hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) continue;
+        if (!ok) continue;
+        if (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms, e0, e1) != hipSuccess) {
+            rc = tbn_hip::fail(TBN_RUNTIME_ERROR, std::string("conv tuning: ") + hipGetErrorString(hipGetLastError()));
+            break;
+        }
         if (best < 0 || ms < best_ms) {
-            best = cands[k];
+            best = i;
             best_ms = ms;
         }
     }
-    (void)hipFreeAsync(tmp, s);
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
-    (void)hipGetLastError();
-    tbn_hip::ok();
-    if (best < 0) return TBN_SUCCESS;
-    out = kMenu[best];
-    fill_patch(g, out);
-    std::lock_guard<std::mutex> lock(plan_mutex());
-    plan_cache()[key] = best;
-    return TBN_SUCCESS;
+    if (rc != TBN_SUCCESS) return rc;
+    if (best >= 0) {
+        std::lock_guard<std::mutex> lock(plan_mutex());
+        plan_cache()[plan_key(d, TERNARY, epi)] = best;
+    }
+    return tbn_hip::ok();
 }
 
 int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
@@ -1013,7 +999,9 @@ int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
                g.chunks * g.taps / (splits * 2) >= 36)
             splits *= 2;
     }
-    if (const char* e = std::getenv("TBN_CONV_SPLITS")) splits = std::max(1, std::atoi(e));  // tuning aid
+    // a forced count (TBN_TUNE_CONV_SPLITS) applies to unpooled convs only:
+    // the split partials hold unpooled planes
+    if (!g.pool && tbn_hip::tuning(TBN_TUNE_CONV_SPLITS) > 0) splits = tbn_hip::tuning(TBN_TUNE_CONV_SPLITS);
     g.single = 0;
     g.cps = (g.chunks + splits - 1) / splits;
     g.splits = (g.chunks + g.cps - 1) / g.cps;
@@ -1023,11 +1011,21 @@ int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
 
 int conv_patch_dispatch(int weights, const float* x, const tbn_conv2d_desc* desc, PatchGeom& g,
                         const uint8_t* conv_weights, int64_t col_bytes, int m_alloc, const PatchEpi& epi,
-                        hipStream_t s);
+                        hipStream_t s, bool tune);
 
+// Bytes of split-K partial sums a call with this geometry needs (0 when K is
+// not split).
+int64_t conv_patch_partial_bytes(const PatchGeom& g) {
+    return g.splits > 1 ? static_cast<int64_t>(g.N) * g.M * g.OH * g.OW * g.splits * 4 : 0;
+}
+
+// One patch conv.  The split-K partial sums go to `scratch` when given (at
+// least conv_patch_partial_bytes, else TBN_INVALID_ARGUMENT), else to the
+// stream workspace.  With `tune`, the feasible tiles are timed instead and
+// the fastest is cached for later calls (y is written by every tile).
 int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, const uint8_t* conv_weights,
                    const float* scale, float alpha, const float* bias, const float* residual, int flags, float* y,
-                   hipStream_t s) {
+                   hipStream_t s, bool tune = false, void* scratch = nullptr, int64_t scratch_bytes = 0) {
     TBN_REQUIRE(weights == TBN_WEIGHTS_BINARY || weights == TBN_WEIGHTS_TERNARY, TBN_INVALID_ARGUMENT,
                 "unknown weights kind");
     TBN_REQUIRE((flags & ~(TBN_EPI_RELU | TBN_EPI_BIAS_THEN_SCALE | TBN_EPI_MAXPOOL2X2)) == 0,
@@ -1037,6 +1035,8 @@ int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, con
     if (rc) return rc;
     TBN_REQUIRE(!(residual && g.pool), TBN_INVALID_ARGUMENT,
                 "a residual input cannot be combined with the fused max pool");
+    // the split-K reduce writes unpooled planes: never split a pooled conv
+    TBN_REQUIRE(!(g.splits > 1 && g.pool), TBN_INVALID_ARGUMENT, "a pooled conv cannot split K");
     TileChoice tc;
     {
         PatchGeom t = g;
@@ -1053,15 +1053,22 @@ int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, con
     PatchEpi epi{y, scale, alpha, bias, residual, flags, nullptr};
     void* part = nullptr;
     bool temporary = false;
-    if (g.splits > 1) {
-        const int64_t total = static_cast<int64_t>(g.N) * g.M * g.OH * g.OW;
-        rc = tbn_hip::stream_workspace(s, static_cast<size_t>(total) * g.splits * sizeof(float), part, temporary);
-        if (rc) return rc;
+    const int64_t part_bytes = conv_patch_partial_bytes(g);
+    if (part_bytes) {
+        if (scratch) {
+            TBN_REQUIRE(scratch_bytes >= part_bytes, TBN_INVALID_ARGUMENT,
+                        "conv scratch holds " + std::to_string(scratch_bytes) + " bytes; this geometry needs " +
+                            std::to_string(part_bytes));
+            part = scratch;
+        } else {
+            rc = tbn_hip::stream_workspace(s, static_cast<size_t>(part_bytes), part, temporary);
+            if (rc) return rc;
+        }
         epi.partial = static_cast<float*>(part);
     }
-    rc = conv_patch_dispatch(weights, x, desc, g, conv_weights, col_bytes, m_alloc, epi, s);
+    rc = conv_patch_dispatch(weights, x, desc, g, conv_weights, col_bytes, m_alloc, epi, s, tune);
     if (part) {
-        if (rc == TBN_SUCCESS) {
+        if (rc == TBN_SUCCESS && !tune) {
             const int64_t total = static_cast<int64_t>(g.N) * g.M * g.OH * g.OW;
             const int blocks = static_cast<int>(std::min<int64_t>(tbn_hip::ceil_div(total, 256), 4096));
             PatchEpi fin = epi;
@@ -1070,22 +1077,24 @@ int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, con
                                static_cast<const float*>(part), g.splits, total, g.M, g.OH * g.OW, fin);
             rc = tbn_hip::check_launch("conv2d (split-K reduce)");
         }
-        tbn_hip::release_workspace(part, temporary, s);
+        if (!scratch) tbn_hip::release_workspace(part, temporary, s);
     }
     return rc;
 }
 
 int conv_patch_dispatch(int weights, const float* x, const tbn_conv2d_desc* desc, PatchGeom& g,
                         const uint8_t* conv_weights, int64_t col_bytes, int m_alloc, const PatchEpi& epi,
-                        hipStream_t s) {
+                        hipStream_t s, bool tune) {
     int rc;
     TileChoice tc;
     if (weights == TBN_WEIGHTS_TERNARY) {
-        rc = select_tile<true>(desc, g, x, conv_weights, col_bytes, m_alloc, epi, s, tc);
+        if (tune) return tune_tile<true>(desc, g, x, conv_weights, col_bytes, m_alloc, epi, s);
+        rc = select_tile<true>(desc, g, epi, tc);
         if (rc) return rc;
         return dispatch_patch<true>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, epi, s);
     }
-    rc = select_tile<false>(desc, g, x, conv_weights, col_bytes, m_alloc, epi, s, tc);
+    if (tune) return tune_tile<false>(desc, g, x, conv_weights, col_bytes, m_alloc, epi, s);
+    rc = select_tile<false>(desc, g, epi, tc);
     if (rc) return rc;
     return dispatch_patch<false>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, epi, s);
 }
@@ -1169,6 +1178,17 @@ int tbn_hip_conv2d_f32_prepacked(int weights, const float* x, const tbn_conv2d_d
                                  const float* residual, int flags, float* y, tbn_stream_t stream) {
     return conv_patch_run(weights, x, desc, conv_weights, scale, alpha, bias, residual, flags, y,
                           tbn_hip::stream_of(stream));
+}
+
+int tbn_hip_conv2d_tune_prepacked(int weights, const float* x, const tbn_conv2d_desc* desc,
+                                  const uint8_t* conv_weights, const float* scale, float alpha, const float* bias,
+                                  const float* residual, int flags, float* y, tbn_stream_t stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    const hipStream_t s = tbn_hip::stream_of(stream);
+    TBN_REQUIRE(hipStreamIsCapturing(s, &st) == hipSuccess && st == hipStreamCaptureStatusNone,
+                TBN_INVALID_ARGUMENT, "conv tuning waits for the stream and cannot run under stream capture");
+    if (tbn_hip::tuning(TBN_TUNE_CONV_TILE) >= 0) return tbn_hip::ok();  // a forced tile: nothing to choose
+    return conv_patch_run(weights, x, desc, conv_weights, scale, alpha, bias, residual, flags, y, s, true);
 }
 
 }  // extern "C"

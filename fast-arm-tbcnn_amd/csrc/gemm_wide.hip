@@ -422,10 +422,8 @@ __global__ void splitk_reduce_kernel(tbn_hip::WideGemmArgs p, const float* __res
 // ~1024 waves, at least 4 K steps each and at most 8 (each split adds M*N*8
 // bytes of partial traffic).
 int split_count(int64_t tiles, int steps) {
-    if (const char* e = std::getenv("TBN_GEMM_SPLITS")) {  // tuning aid
-        const int forced = std::atoi(e);
-        if (forced >= 1) return std::min(forced, std::max(steps, 1));
-    }
+    const int forced = tbn_hip::tuning(TBN_TUNE_GEMM_SPLITS);
+    if (forced >= 1) return std::min(forced, std::max(steps, 1));
     if (tiles >= 128) return 1;
     int sp = static_cast<int>((128 + tiles - 1) / tiles);
     sp = std::min(sp, 8);

@@ -269,6 +269,11 @@ PYBIND11_MODULE(_tbn, m) {
               return qlinear_matmul_binary(as_tensor(a), as_tensor(b), s);
           },
           py::arg("a"), py::arg("b_binary"), py::arg("b_scale") = 1.0f);
+    m.def("qlinear_matmul_binary_float",
+          [](const py::object& a, const py::object& b, float s) {
+              return qlinear_matmul_binary_float(as_tensor(a), as_tensor(b), s);
+          },
+          py::arg("a"), py::arg("b_binary_float"), py::arg("b_scale") = 1.0f);
     m.def("qlinear_matmul_binary_tbn",
           [](const py::object& a, const py::object& b, float s, float lo, float hi) {
               return qlinear_matmul_binary_tbn(as_tensor(a), as_tensor(b), s, TilingParams{}, lo, hi);

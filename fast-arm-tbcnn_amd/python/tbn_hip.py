@@ -34,6 +34,9 @@ EPI_BIAS_THEN_SCALE = 2
 EPI_MAXPOOL2X2 = 4
 WEIGHTS_BINARY = 0
 WEIGHTS_TERNARY = 1
+TUNE_CONV_TILE = 1
+TUNE_CONV_SPLITS = 2
+TUNE_GEMM_SPLITS = 3
 OP_SUB = 0
 OP_GREATER = 1
 OP_LESS = 2
@@ -61,6 +64,8 @@ _SIGNATURES = {
     "tbn_hip_version": ([], _I32),
     "tbn_hip_device_check": ([], _I32),
     "tbn_hip_synchronize": ([_P], _I32),
+    "tbn_hip_set_tuning": ([_I32, _I32], _I32),
+    "tbn_hip_get_tuning": ([_I32, ctypes.POINTER(ctypes.c_int)], _I32),
     "tbn_hip_quantize_to_binary_f32": ([_P, _I64, _F32, _P, _P], _I32),
     "tbn_hip_quantize_to_binary_i8": ([_P, _I64, _P, _P], _I32),
     "tbn_hip_quantize_to_ternary_f32": ([_P, _I64, _F32, _F32, _P, _P], _I32),
@@ -94,6 +99,8 @@ _SIGNATURES = {
     "tbn_hip_conv_weights_bytes": ([_I32, ctypes.POINTER(ConvDesc), ctypes.POINTER(ctypes.c_int64)], _I32),
     "tbn_hip_pack_conv_weights": ([_I32, _P, _I64, _I64, ctypes.POINTER(ConvDesc), _P, _P], _I32),
     "tbn_hip_conv2d_f32_prepacked": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P, _P], _I32),
+    "tbn_hip_conv2d_tune_prepacked": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P, _P],
+                                      _I32),
     "tbn_hip_elementwise": ([_I32, _P, _I64, _P, _I64, _F32, _P, _P], _I32),
     "tbn_hip_ternary_activation": ([_P, _I64, _F32, _P, _P], _I32),
     "tbn_hip_ternary_pack_f32": ([_P, _I64, _I64, _I64, _I64, _I64, _F32, _F32, _P, _P, _P], _I32),
@@ -161,3 +168,21 @@ def padded_dims(K, N):
     """K_pad = ceil128(K), N_pad = ceil8(N) as the reference runtime pads
     (tbn-runtime/src/operators/quantized_gemm_neon.cpp:53-55)."""
     return (K + 127) // 128 * 128, (N + 7) // 8 * 8
+
+
+class tuning:
+    """Context manager that sets a tuning control (TUNE_*) and restores it."""
+
+    def __init__(self, option, value):
+        self.option, self.value = option, value
+
+    def __enter__(self):
+        old = ctypes.c_int()
+        call("tbn_hip_get_tuning", self.option, ctypes.byref(old))
+        self.old = old.value
+        call("tbn_hip_set_tuning", self.option, self.value)
+        return self
+
+    def __exit__(self, *exc):
+        call("tbn_hip_set_tuning", self.option, self.old)
+        return False

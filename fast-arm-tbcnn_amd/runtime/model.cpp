@@ -1012,6 +1012,7 @@ struct TBNModel::Session::Impl {
         for (const auto& node : graph->nodes) lower(node);
         fuse();
         plan_memory();
+        tune_convs();
         launches = 0;
         for (const auto& op : ops)
             if (!op.dead && op.kind != OpKind::View)
@@ -1020,6 +1021,26 @@ struct TBNModel::Session::Impl {
         plan_quant = quant;
         plan_shapes.clear();
         for (auto& kv : inputs) plan_shapes[kv.first] = kv.second.shape();
+    }
+
+    // Times the conv tiles of every patch conv once per geometry (the library
+    // keeps the winner for the process), so no run times, allocates or waits
+    // for tile selection.  Skipped while the caller's stream captures: those
+    // convs then use the library's static tile rule.
+    void tune_convs() {
+        const tbn_stream_t s = cur_stream();
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(static_cast<hipStream_t>(s), &st) != hipSuccess ||
+            st != hipStreamCaptureStatusNone)
+            return;
+        for (auto& op : ops) {
+            if (op.dead || op.kind != OpKind::ConvQuant || op.groups > 1 || !op.conv_w) continue;
+            check_status(tbn_hip_conv2d_tune_prepacked(
+                             op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY : TBN_WEIGHTS_TERNARY,
+                             fp(op.in[0]), &op.desc, op.conv_w->typed_data<uint8_t>(), op.scale, 1.0f, op.bias,
+                             op.residual >= 0 ? fp(op.residual) : nullptr, op.flags, fp(op.out), s),
+                         ("tuning node '" + op.node + "'").c_str());
+        }
     }
 
     bool plan_valid() const {

@@ -108,6 +108,21 @@ int tbn_hip_device_check(void);
 /* Waits for `stream` and reports any asynchronous device error. */
 int tbn_hip_synchronize(tbn_stream_t stream);
 
+/* ---- tuning controls (no counterpart in the reference) ---------------------
+ * Process-wide launch-shape choices.  Each starts from an environment variable
+ * read once, at the first call that needs it (TBN_CONV_TILE, TBN_CONV_SPLITS,
+ * TBN_GEMM_SPLITS), and changes only through tbn_hip_set_tuning.  They pick
+ * kernel variants: a forced conv tile never changes a result (every tile sums
+ * in the same order); a forced split count changes the summation order. */
+enum tbn_tuning {
+    TBN_TUNE_CONV_TILE = 1,   /* patch-conv tile id, -1 = automatic (default)   */
+    TBN_TUNE_CONV_SPLITS = 2, /* patch-conv K splits, 0 = automatic; pooled
+                                 convs never split                               */
+    TBN_TUNE_GEMM_SPLITS = 3  /* wide GEMM K splits, 0 = automatic              */
+};
+int tbn_hip_set_tuning(int option, int value);
+int tbn_hip_get_tuning(int option, int* value);
+
 /* ---- quantization (north_star subsystem 1) --------------------------------- */
 
 /* quantize_to_binary(W, threshold), FLOAT32 input: out[i] = w[i] > threshold.
@@ -248,11 +263,23 @@ int tbn_hip_conv_weights_bytes(int weights, const tbn_conv2d_desc* desc, int64_t
 int tbn_hip_pack_conv_weights(int weights, const uint8_t* packed, int64_t K_pad, int64_t N_pad,
                               const tbn_conv2d_desc* desc, uint8_t* conv_weights, tbn_stream_t stream);
 /* tbn_hip_conv2d_f32_quantized on conv-layout weights: same arithmetic and
- * epilogue, no allocation.  Returns TBN_INVALID_SHAPE for geometries whose
- * patch does not fit (very large kernels or dilations). */
+ * epilogue, no weight re-order.  Returns TBN_INVALID_SHAPE for geometries
+ * whose patch does not fit (very large kernels or dilations).  Geometries
+ * that split K (small maps with many input channels) keep their partial sums
+ * in the library's per-device stream workspace, allocated on first use. */
 int tbn_hip_conv2d_f32_prepacked(int weights, const float* x, const tbn_conv2d_desc* desc,
                                  const uint8_t* conv_weights, const float* scale, float alpha, const float* bias,
                                  const float* residual, int flags, float* y, tbn_stream_t stream);
+/* Same arguments as tbn_hip_conv2d_f32_prepacked (no counterpart in the
+ * reference): times every conv tile that fits this geometry, a few launches
+ * each, all writing y, and keeps the fastest for later calls with the same
+ * geometry, epilogue flags and residual use (a process-wide cache).  Without
+ * it a call uses a static rule.  Waits for `stream`; refused under stream
+ * capture.  Every tile sums in the same order, so it never changes results.
+ * The Session calls it once per conv layer when it compiles its plan. */
+int tbn_hip_conv2d_tune_prepacked(int weights, const float* x, const tbn_conv2d_desc* desc,
+                                  const uint8_t* conv_weights, const float* scale, float alpha, const float* bias,
+                                  const float* residual, int flags, float* y, tbn_stream_t stream);
 
 /* ---- fp32 layers and epilogue operators (Session support) ------------------ */
 

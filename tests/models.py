@@ -216,6 +216,17 @@ class _Grouped:
         return grouped
 
 
+def gemm_already_binary(B):
+    """The quantized Gemm's "already binary" test (model.hpp:765-786): the
+    flattened B is sampled at i = 0, step, 2*step, ... with step =
+    max(1, size // 1000), and every sample must be exactly -1, 1, 0, 0.999
+    or -0.999 (fp32 equality, so -0.0 passes as 0)."""
+    flat = np.asarray(B, np.float32).reshape(-1)
+    step = max(1, flat.size // 1000)
+    ok = set(np.float32([-1.0, 1.0, 0.0, 0.999, -0.999]).tolist())
+    return all(float(v) in ok for v in flat[::step])
+
+
 def run_oracle(spec, feeds, quant, orc, record=None):
     """Executes the graph on the CPU (float64 products, fp32 values between
     nodes) with the reference Session's branch structure.  Returns
@@ -267,10 +278,7 @@ def run_oracle(spec, feeds, quant, orc, record=None):
             tA, tB = bool(a.get("transA", 0)), bool(a.get("transB", 0))
             C = env[n.inputs[2]] if (n.op == "Gemm" and len(n.inputs) > 2) else None
             if quant_here and n.op == "Gemm" and B.dtype == np.float32 and not tA and not tB:
-                flat = B.reshape(-1)
-                step = max(1, flat.size // 1000)
-                ok = set(np.float32([-1.0, 1.0, 0.0, 0.999, -0.999]).tolist())
-                already = all(float(v) in ok for v in flat[::step])
+                already = gemm_already_binary(B)
                 sign = np.where(B >= 0 if already else B > 0, 1.0, -1.0)
                 y = A @ sign
             else:

@@ -372,11 +372,10 @@ def test_conv_patch_split_k_residual_and_ternary(dev, orc):
                                   (2, 256, 7, 7, 96, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_BIAS_THEN_SCALE),
                                   (2, 64, 15, 13, 64, 1, 1, (2, 2), (0, 0), (1, 1), 0)])
 def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
-    """Each tile of the menu (forced with TBN_CONV_TILE: linear and 2-D tiles,
+    """Each tile of the menu (forced with the conv-tile control: linear and 2-D tiles,
     with two LDS buffers or one) sums every output in the same order, so all
     feasible tiles give bit-identical outputs; one of them is checked against
     the float64 oracle."""
-    import os
     N, C, H, W, M, kh, kw, stride, pad, dil, flags = case
     rng = np.random.default_rng(C * 17 + M)
     x = rng.standard_normal((N, C, H, W)).astype(np.float32)
@@ -395,10 +394,8 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
     tbn_hip.call("tbn_hip_pack_conv_weights", tbn_hip.WEIGHTS_BINARY, P(packed), K_pad, N_pad, d, P(cw), None)
     dx, ds, db = to_dev(x), to_dev(scale), to_dev(bias)
     outs = {}
-    old = os.environ.get("TBN_CONV_TILE")
-    try:
-        for tile in [t for base in (0, 10, 20, 30) for t in range(base, base + 10)]:
-            os.environ["TBN_CONV_TILE"] = str(tile)
+    for tile in [t for base in (0, 10, 20, 30) for t in range(base, base + 10)]:
+        with tbn_hip.tuning(tbn_hip.TUNE_CONV_TILE, tile):
             y = empty(oshape, torch.float32)
             y.fill_(np.nan)
             # the pre-packed entry point runs only the patch kernel (no fallback)
@@ -408,11 +405,6 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
                 continue  # this tile cannot hold the geometry
             assert rc == 0, tbn_hip.last_error()
             outs[tile] = host(y)
-    finally:
-        if old is None:
-            os.environ.pop("TBN_CONV_TILE", None)
-        else:
-            os.environ["TBN_CONV_TILE"] = old
     assert any(t >= 20 for t in outs) and any(t < 20 for t in outs), sorted(outs)
     first = next(iter(outs.values()))
     for tile, y in outs.items():
@@ -420,3 +412,62 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
     wsign = np.where(wbytes == 1, 1.0, -1.0).astype(np.float32)
     ref = conv_ref(x, wsign, scale, 1.0, bias, stride, pad, dil, flags)
     rm.assert_within_tolerance(first, ref, K, np.abs(x).max() * 1.5)
+
+
+def _prepacked_setup(case, seed):
+    import ctypes
+    N, C, H, W, M, kh, kw, stride, pad, dil, flags = case
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    wbytes = (rng.random((M, C, kh, kw)) < 0.5).astype(np.uint8)
+    scale = rng.uniform(0.5, 1.5, M).astype(np.float32)
+    bias = (rng.standard_normal(M) * 0.01).astype(np.float32)
+    packed, K_pad, N_pad = pack_conv_weights(wbytes, M, C * kh * kw)
+    d = tbn_hip.conv_desc(N, C, H, W, M, kh, kw, *stride, *pad, *dil)
+    wb = ctypes.c_int64()
+    tbn_hip.call("tbn_hip_conv_weights_bytes", tbn_hip.WEIGHTS_BINARY, d, ctypes.byref(wb))
+    cw = empty(wb.value, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_conv_weights", tbn_hip.WEIGHTS_BINARY, P(packed), K_pad, N_pad, d, P(cw), None)
+    OH, OW = tbn_hip.conv_out_hw(d)
+    oshape = (N, M, OH // 2, OW // 2) if flags & tbn_hip.EPI_MAXPOOL2X2 else (N, M, OH, OW)
+    ref = conv_ref(x, np.where(wbytes == 1, 1.0, -1.0).astype(np.float32), scale, 1.0, bias, stride, pad, dil, flags)
+    return dict(x=to_dev(x), d=d, cw=cw, s=to_dev(scale), b=to_dev(bias), flags=flags, oshape=oshape, ref=ref,
+                K=C * kh * kw, xmax=float(np.abs(x).max()))
+
+
+def _run_prepacked(st, entry="tbn_hip_conv2d_f32_prepacked"):
+    y = empty(st["oshape"], torch.float32)
+    y.fill_(np.nan)
+    tbn_hip.call(entry, tbn_hip.WEIGHTS_BINARY, P(st["x"]), st["d"], P(st["cw"]), P(st["s"]), 1.0, P(st["b"]),
+                 None, st["flags"], P(y), None)
+    return host(y)
+
+
+@pytest.mark.parametrize("case", [CASES[0], (4, 64, 56, 56, 128, 3, 3, (1, 1), (1, 1), (1, 1), 0),
+                                  (3, 256, 7, 7, 96, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_RELU)],
+                         ids=["cfg4", "56x56", "splitK"])
+def test_conv_tune_keeps_the_bits(dev, case):
+    """tbn_hip_conv2d_tune_prepacked times the tiles and caches one; calls
+    before (static rule) and after (tuned tile) give the same bits."""
+    st = _prepacked_setup(case, 21)
+    before = _run_prepacked(st)
+    _run_prepacked(st, "tbn_hip_conv2d_tune_prepacked")
+    after = _run_prepacked(st)
+    assert np.array_equal(before, after)
+    rm.assert_within_tolerance(after, st["ref"], st["K"], st["xmax"] * 1.5)
+
+
+def test_conv_forced_splits_skip_pooled_convs(dev):
+    """A forced K-split count applies to unpooled convs only: a conv with the
+    fused 2x2 pool keeps one split (same bits as unforced), an unpooled one
+    splits and stays within tolerance."""
+    pooled = _prepacked_setup((3, 96, 12, 10, 64, 3, 3, (1, 1), (1, 1), (1, 1),
+                               tbn_hip.EPI_MAXPOOL2X2 | tbn_hip.EPI_RELU), 22)
+    plain = _prepacked_setup((2, 128, 14, 14, 64, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_RELU), 23)
+    want_pooled = _run_prepacked(pooled)
+    with tbn_hip.tuning(tbn_hip.TUNE_CONV_SPLITS, 2):
+        got_pooled = _run_prepacked(pooled)
+        got_plain = _run_prepacked(plain)
+    assert np.array_equal(got_pooled, want_pooled)
+    rm.assert_within_tolerance(got_pooled, pooled["ref"], pooled["K"], pooled["xmax"] * 1.5)
+    rm.assert_within_tolerance(got_plain, plain["ref"], plain["K"], plain["xmax"] * 1.5)
