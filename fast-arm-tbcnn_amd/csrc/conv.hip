@@ -16,11 +16,20 @@
 // weight transpose, qlinear_matmul_binary, reshape, bias),
 // conv2d_binary_with_scales (conv2d.cpp:319-369), conv2d (conv2d.cpp:78-192)
 // and the Session's cached binary conv (model.hpp:414-559).
+#include <mutex>
 #include <string>
 
 #include "common.hpp"
 #include "conv_common.hpp"
 #include "mfma_core.hpp"
+
+// Scratch of the no-allocation conv entry point: the re-ordered weights and
+// the split-K partial sums of a patch conv.  One copy per device, held until
+// the process ends; calls on one device share it (overlapping calls race).
+// Its device address comes from hipGetSymbolAddress, once per device, on the
+// first such call with that device current: in host code the array's name
+// is only a stand-in, never a device address.
+static __device__ __align__(256) uint8_t scratch[TBN_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -130,6 +139,28 @@ int launch_conv_impl(const RowL& rowl, const float* x, const ConvGeom& g, const 
     return tbn_hip::check_launch(what);
 }
 
+std::mutex g_scratch_mutex;
+void* g_scratch_addr[64] = {};
+
+int noalloc_scratch(void*& out) {
+    int dev = -1;
+    const hipError_t ge = hipGetDevice(&dev);
+    TBN_REQUIRE(ge == hipSuccess && dev >= 0 && dev < 64, TBN_DEVICE_NOT_SUPPORTED, "no current HIP device");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            (void)hipGetLastError();
+            return tbn_hip::fail(TBN_RUNTIME_ERROR,
+                                 std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+        }
+        g_scratch_addr[dev] = p;
+    }
+    out = g_scratch_addr[dev];
+    return TBN_SUCCESS;
+}
+
 // Inputs with at least this many channels take the patch path (conv_patch.hip);
 // narrower ones (LeNet) gather straight from NCHW here, where padding C to a
 // chunk of 32 would waste most of the K loop.
@@ -138,7 +169,7 @@ constexpr int64_t kPatchMinChannels = 16;
 template <bool TERNARY>
 int conv_quant(const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed, int64_t K_pad,
                int64_t N_pad, const float* scale, float alpha, const float* bias,
-               const float* residual, int flags, float* y, tbn_stream_t stream) {
+               const float* residual, int flags, float* y, tbn_stream_t stream, bool noalloc = false) {
     const char* what = TERNARY ? "conv2d_f32_ternary" : "conv2d_f32_binary";
     ConvGeom g;
     int rc = make_geom(desc, flags, g);
@@ -152,11 +183,26 @@ int conv_quant(const float* x, const tbn_conv2d_desc* desc, const uint8_t* packe
                 "a residual input cannot be combined with the fused max pool");
     if (g.Q == 0) return tbn_hip::ok();
     TBN_REQUIRE(x && packed && y, TBN_INVALID_ARGUMENT, "null pointer");
+    const int wkind = TERNARY ? TBN_WEIGHTS_TERNARY : TBN_WEIGHTS_BINARY;
+    const bool patch = desc->c >= kPatchMinChannels && tbn_hip::conv_patch_supported(desc);
+    int64_t need = 0;
+    if (noalloc && patch) {
+        need = tbn_hip::conv_patch_scratch_bytes(wkind, desc, flags);
+        TBN_REQUIRE(need >= 0, TBN_INVALID_SHAPE, "conv geometry not supported");
+        TBN_REQUIRE(need <= static_cast<int64_t>(TBN_NOALLOC_SCRATCH_BYTES), TBN_INVALID_SHAPE,
+                    "this conv needs " + std::to_string(need) + " bytes of scratch (re-ordered weights and split-K "
+                    "sums); the no-allocation entry point holds " + std::to_string(TBN_NOALLOC_SCRATCH_BYTES));
+    }
     TBN_DEVICE_GUARD();
-    if (desc->c >= kPatchMinChannels && tbn_hip::conv_patch_supported(desc))
-        return tbn_hip::conv_patch_from_reference(TERNARY ? TBN_WEIGHTS_TERNARY : TBN_WEIGHTS_BINARY, x, desc, packed,
-                                                 K_pad, N_pad, scale, alpha, bias, residual, flags, y,
-                                                 tbn_hip::stream_of(stream));
+    if (patch) {
+        void* scratch_ptr = nullptr;
+        if (noalloc) {
+            const int rc = noalloc_scratch(scratch_ptr);
+            if (rc) return rc;
+        }
+        return tbn_hip::conv_patch_from_reference(wkind, x, desc, packed, K_pad, N_pad, scale, alpha, bias, residual,
+                                                 flags, y, tbn_hip::stream_of(stream), scratch_ptr, need);
+    }
     const int64_t col_bytes = TERNARY ? K_pad / 4 : K_pad / 8;
     hipStream_t s = tbn_hip::stream_of(stream);
     if (tbn_hip::conv_small_supported(desc))
@@ -205,6 +251,19 @@ int tbn_hip_conv2d_f32_quantized(int weights, const float* x, const tbn_conv2d_d
     if (weights == TBN_WEIGHTS_TERNARY)
         return conv_quant<true>(x, desc, packed, K_pad, N_pad, scale, alpha, bias, residual, flags,
                                 y, stream);
+    return tbn_hip::fail(TBN_INVALID_ARGUMENT, "unknown weights kind");
+}
+
+int tbn_hip_conv2d_f32_quantized_noalloc(int weights, const float* x, const tbn_conv2d_desc* desc,
+                                         const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                                         const float* scale, float alpha, const float* bias,
+                                         const float* residual, int flags, float* y, tbn_stream_t stream) {
+    if (weights == TBN_WEIGHTS_BINARY)
+        return conv_quant<false>(x, desc, packed, K_pad, N_pad, scale, alpha, bias, residual, flags, y, stream,
+                                 true);
+    if (weights == TBN_WEIGHTS_TERNARY)
+        return conv_quant<true>(x, desc, packed, K_pad, N_pad, scale, alpha, bias, residual, flags, y, stream,
+                                true);
     return tbn_hip::fail(TBN_INVALID_ARGUMENT, "unknown weights kind");
 }
 

@@ -141,12 +141,18 @@ inline int make_geom(const tbn_conv2d_desc* d, int flags, ConvGeom& g) {
 
 namespace tbn_hip {
 // The patch conv path (conv_patch.hip): whether it handles `desc`, and a run
-// fed with reference-layout packed weights (re-ordered into a stream-ordered
-// temporary for the call).
+// fed with reference-layout packed weights, re-ordered into a stream-ordered
+// temporary for the call, or, when `scratch` is given, into its first bytes
+// with the split-K partial sums after them (no allocation at all).
 bool conv_patch_supported(const tbn_conv2d_desc* desc);
 int conv_patch_from_reference(int weights, const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed,
                               int64_t K_pad, int64_t N_pad, const float* scale, float alpha, const float* bias,
-                              const float* residual, int flags, float* y, hipStream_t s);
+                              const float* residual, int flags, float* y, hipStream_t s, void* scratch = nullptr,
+                              int64_t scratch_bytes = 0);
+// Scratch bytes conv_patch_from_reference needs with `scratch` given: the
+// conv-layout weights (rounded up to 256 bytes) plus the split-K partial sums;
+// -1 when make_patch_geom rejects the geometry.
+int64_t conv_patch_scratch_bytes(int weights, const tbn_conv2d_desc* desc, int flags);
 // The fp32 stem path (conv_stem.hip): few input channels, 7-wide kernels,
 // stride 2 along W, <= 64 output channels, bias + optional ReLU.
 bool conv_stem_supported(const tbn_conv2d_desc* desc, int flags);

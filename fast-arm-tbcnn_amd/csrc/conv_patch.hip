@@ -1110,10 +1110,27 @@ bool conv_patch_supported(const tbn_conv2d_desc* desc) {
     return choose_tile(g, tc);
 }
 
+int64_t conv_patch_scratch_bytes(int weights, const tbn_conv2d_desc* desc, int flags) {
+    PatchGeom g;
+    if (make_patch_geom(desc, flags, g) != TBN_SUCCESS) return -1;
+    return (conv_weight_bytes(weights, desc) + 255) / 256 * 256 + conv_patch_partial_bytes(g);
+}
+
 int conv_patch_from_reference(int weights, const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed,
                               int64_t K_pad, int64_t N_pad, const float* scale, float alpha, const float* bias,
-                              const float* residual, int flags, float* y, hipStream_t s) {
+                              const float* residual, int flags, float* y, hipStream_t s, void* scratch,
+                              int64_t scratch_bytes) {
     const int64_t wbytes = conv_weight_bytes(weights, desc);
+    if (scratch) {
+        const int64_t wspan = (wbytes + 255) / 256 * 256;
+        TBN_REQUIRE(scratch_bytes >= wspan, TBN_INVALID_ARGUMENT, "conv scratch too small for the weights");
+        uint8_t* cw = static_cast<uint8_t*>(scratch);
+        int rc = tbn_hip_pack_conv_weights(weights, packed, K_pad, N_pad, desc, cw, s);
+        if (rc == TBN_SUCCESS)
+            rc = conv_patch_run(weights, x, desc, cw, scale, alpha, bias, residual, flags, y, s, false,
+                                cw + wspan, scratch_bytes - wspan);
+        return rc;
+    }
     void* buf = nullptr;
     hipError_t e = hipMallocAsync(&buf, static_cast<size_t>(wbytes), s);
     if (e != hipSuccess) {

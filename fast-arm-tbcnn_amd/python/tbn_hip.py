@@ -32,6 +32,7 @@ EPI_NONE = 0
 EPI_RELU = 1
 EPI_BIAS_THEN_SCALE = 2
 EPI_MAXPOOL2X2 = 4
+NOALLOC_SCRATCH_BYTES = 16 << 20
 WEIGHTS_BINARY = 0
 WEIGHTS_TERNARY = 1
 TUNE_CONV_TILE = 1
@@ -96,6 +97,8 @@ _SIGNATURES = {
                                     _F32, _I32, _P, _I64, _P], _I32),
     "tbn_hip_conv2d_f32_quantized": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _I64, _I64, _P, _F32, _P, _P,
                                       _I32, _P, _P], _I32),
+    "tbn_hip_conv2d_f32_quantized_noalloc": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _I64, _I64, _P, _F32, _P,
+                                              _P, _I32, _P, _P], _I32),
     "tbn_hip_conv_weights_bytes": ([_I32, ctypes.POINTER(ConvDesc), ctypes.POINTER(ctypes.c_int64)], _I32),
     "tbn_hip_pack_conv_weights": ([_I32, _P, _I64, _I64, ctypes.POINTER(ConvDesc), _P, _P], _I32),
     "tbn_hip_conv2d_f32_prepacked": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P, _P], _I32),

@@ -254,6 +254,23 @@ int tbn_hip_conv2d_f32_quantized(int weights, const float* x, const tbn_conv2d_d
  * that runs a layer many times (the Session) packs once and calls
  * tbn_hip_conv2d_f32_prepacked, which allocates nothing. */
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): tbn_hip_conv2d_f32_quantized with the same arguments and
+ * results, except that where that entry point takes a stream-ordered
+ * temporary (the weight re-order and the split-K partial sums of convs with
+ * >= 16 input channels) this one uses a static device buffer of the library,
+ * TBN_NOALLOC_SCRATCH_BYTES per device, held until the process ends.  It
+ * calls no allocator.  A conv that needs more scratch than that returns
+ * TBN_INVALID_SHAPE before any work.  Every call on one device shares that
+ * device's buffer, so calls that overlap on one device (other streams or
+ * threads) race; calls ordered on one stream are safe. */
+#define TBN_NOALLOC_SCRATCH_BYTES (16u << 20)
+int tbn_hip_conv2d_f32_quantized_noalloc(int weights, const float* x, const tbn_conv2d_desc* desc,
+                                         const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                                         const float* scale, float alpha, const float* bias,
+                                         const float* residual, int flags, float* y, tbn_stream_t stream);
+
 /* Bytes of the conv-layout weights for `desc` (weights: TBN_WEIGHTS_BINARY or
  * TBN_WEIGHTS_TERNARY): ceil8(M) * Kc / 8 (binary) or / 4 (ternary). */
 int tbn_hip_conv_weights_bytes(int weights, const tbn_conv2d_desc* desc, int64_t* bytes);
