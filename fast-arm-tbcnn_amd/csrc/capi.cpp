@@ -30,22 +30,31 @@ int ok() {
 // allocation on a stream makes the GPU wait on the allocator between kernels
 // (about 6 us per call), so each device keeps one buffer for the stream that
 // last used it, grown as needed; consecutive users on that stream are
-// ordered by the stream.  Calls on another stream, or under stream capture
-// (where an allocation belongs to the graph), get a stream-ordered temporary.
+// ordered by the stream.  Calls on another stream get a stream-ordered
+// temporary.  Every allocation starts with kWorkspaceCounters int32 counters,
+// zeroed when it is made; kernels that use them leave them zero again.  No
+// allocation is recorded into a captured graph: such calls are refused.
 namespace {
 struct Workspace {
     hipStream_t stream = nullptr;
     void* ptr = nullptr;
-    size_t bytes = 0;
+    size_t bytes = 0;  // data bytes after the counters
 };
 std::mutex g_ws_mutex;
 Workspace g_ws[64];
 
-int alloc_async(void*& ptr, size_t bytes, hipStream_t s) {
-    const hipError_t e = hipMallocAsync(&ptr, bytes, s);
+constexpr size_t kCounterBytes = kWorkspaceCounters * sizeof(int);
+
+// Allocates counters + `bytes` on stream s and zeroes the counters.
+int alloc_async(void*& base, size_t bytes, hipStream_t s) {
+    hipError_t e = hipMallocAsync(&base, kCounterBytes + bytes, s);
+    if (e == hipSuccess) {
+        e = hipMemsetAsync(base, 0, kCounterBytes, s);
+        if (e != hipSuccess) (void)hipFreeAsync(base, s);
+    }
     if (e != hipSuccess) {
         (void)hipGetLastError();
-        ptr = nullptr;
+        base = nullptr;
         return fail(e == hipErrorOutOfMemory ? TBN_OUT_OF_MEMORY : TBN_RUNTIME_ERROR,
                     std::string("workspace allocation failed: ") + hipGetErrorString(e));
     }
@@ -53,41 +62,45 @@ int alloc_async(void*& ptr, size_t bytes, hipStream_t s) {
 }
 }  // namespace
 
-int stream_workspace(hipStream_t s, size_t bytes, void*& ptr, bool& temporary) {
+int stream_workspace(hipStream_t s, size_t bytes, void*& ptr, bool& temporary, int** counters) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     const bool capturing = hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone;
-    // No allocation is recorded into a captured graph: a replay of a graph
-    // holding split-K temporaries as graph allocations ended in a memory
-    // fault once, with no cause found, so such calls are refused while the
+    // A replay of a graph holding split-K temporaries as graph allocations
+    // ended in a memory fault once (DESIGN notes what was examined), so no
+    // allocation is recorded into a graph: such calls are refused while the
     // stream captures (the Session then runs that plan eagerly).
     if (capturing)
         return fail(TBN_NOT_IMPLEMENTED, "split-K workspace: no allocation while the stream is being captured");
+    void* base = nullptr;
+    temporary = true;
     int dev = 0;
     if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
         std::lock_guard<std::mutex> lock(g_ws_mutex);
         Workspace& w = g_ws[dev];
         if (w.ptr && w.stream == s && w.bytes >= bytes) {
-            ptr = w.ptr;
+            base = w.ptr;
             temporary = false;
-            return TBN_SUCCESS;
-        }
-        if (!w.ptr || w.stream == s) {
+        } else if (!w.ptr || w.stream == s) {
             if (w.ptr) (void)hipFreeAsync(w.ptr, w.stream);
             w = Workspace{};
             const size_t grown = bytes + bytes / 4;
-            const int rc = alloc_async(ptr, grown, s);
+            const int rc = alloc_async(base, grown, s);
             if (rc) return rc;
-            w = Workspace{s, ptr, grown};
+            w = Workspace{s, base, grown};
             temporary = false;
-            return TBN_SUCCESS;
         }
     }
-    temporary = true;
-    return alloc_async(ptr, bytes, s);
+    if (temporary) {
+        const int rc = alloc_async(base, bytes, s);
+        if (rc) return rc;
+    }
+    ptr = static_cast<uint8_t*>(base) + kCounterBytes;
+    if (counters) *counters = static_cast<int*>(base);
+    return TBN_SUCCESS;
 }
 
 void release_workspace(void* ptr, bool temporary, hipStream_t s) {
-    if (temporary && ptr) (void)hipFreeAsync(ptr, s);
+    if (temporary && ptr) (void)hipFreeAsync(static_cast<uint8_t*>(ptr) - kCounterBytes, s);
 }
 
 // Tuning controls: read from the environment once (TBN_CONV_TILE,
@@ -95,7 +108,7 @@ void release_workspace(void* ptr, bool temporary, hipStream_t s) {
 // tbn_hip_set_tuning.  Relaxed atomics: a value is a launch-shape choice, so a
 // call that races with a change simply sees the old or the new one.
 namespace {
-std::atomic<int> g_tuning[4];
+std::atomic<int> g_tuning[5];
 std::once_flag g_tuning_once;
 
 void tuning_init() {
@@ -106,6 +119,7 @@ void tuning_init() {
     g_tuning[TBN_TUNE_CONV_TILE].store(env("TBN_CONV_TILE", -1), std::memory_order_relaxed);
     g_tuning[TBN_TUNE_CONV_SPLITS].store(std::max(0, env("TBN_CONV_SPLITS", 0)), std::memory_order_relaxed);
     g_tuning[TBN_TUNE_GEMM_SPLITS].store(std::max(0, env("TBN_GEMM_SPLITS", 0)), std::memory_order_relaxed);
+    g_tuning[TBN_TUNE_GEMM_TILE].store(env("TBN_GEMM_TILE", -1), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -167,17 +181,18 @@ int tbn_hip_device_check(void) {
 }
 
 int tbn_hip_set_tuning(int option, int value) {
-    TBN_REQUIRE(option >= TBN_TUNE_CONV_TILE && option <= TBN_TUNE_GEMM_SPLITS, TBN_INVALID_ARGUMENT,
+    TBN_REQUIRE(option >= TBN_TUNE_CONV_TILE && option <= TBN_TUNE_GEMM_TILE, TBN_INVALID_ARGUMENT,
                 "unknown tuning option");
-    TBN_REQUIRE(option == TBN_TUNE_CONV_TILE ? value >= -1 : value >= 0, TBN_INVALID_ARGUMENT,
-                "tuning value out of range");
+    TBN_REQUIRE(option == TBN_TUNE_CONV_TILE ? value >= -1
+                                             : (option == TBN_TUNE_GEMM_TILE ? value >= -1 && value <= 1 : value >= 0),
+                TBN_INVALID_ARGUMENT, "tuning value out of range");
     (void)tbn_hip::tuning(option);  // the environment is read before the first change
     tbn_hip::g_tuning[option].store(value, std::memory_order_relaxed);
     return tbn_hip::ok();
 }
 
 int tbn_hip_get_tuning(int option, int* value) {
-    TBN_REQUIRE(option >= TBN_TUNE_CONV_TILE && option <= TBN_TUNE_GEMM_SPLITS, TBN_INVALID_ARGUMENT,
+    TBN_REQUIRE(option >= TBN_TUNE_CONV_TILE && option <= TBN_TUNE_GEMM_TILE, TBN_INVALID_ARGUMENT,
                 "unknown tuning option");
     TBN_REQUIRE(value != nullptr, TBN_INVALID_ARGUMENT, "null pointer");
     *value = tbn_hip::tuning(option);

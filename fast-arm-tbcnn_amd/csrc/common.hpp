@@ -23,9 +23,13 @@ int check_launch(const char* what);
 inline hipStream_t stream_of(tbn_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 // Device scratch for split-K partial sums on stream s: a per-device buffer
-// reused by consecutive calls on one stream, else (another stream, stream
-// capture) a stream-ordered temporary; release_workspace frees only the latter.
-int stream_workspace(hipStream_t s, size_t bytes, void*& ptr, bool& temporary);
+// reused by consecutive calls on one stream, else (another stream) a
+// stream-ordered temporary; release_workspace frees only the latter.  Refused
+// (TBN_NOT_IMPLEMENTED) while s captures.  `counters`, if given, receives
+// kWorkspaceCounters int32 counters that are zero when the call starts and
+// that the call's kernels must leave zero.
+constexpr int kWorkspaceCounters = 16384;
+int stream_workspace(hipStream_t s, size_t bytes, void*& ptr, bool& temporary, int** counters = nullptr);
 void release_workspace(void* ptr, bool temporary, hipStream_t s);
 
 // Current value of a tuning control (TBN_TUNE_*), the environment read once.

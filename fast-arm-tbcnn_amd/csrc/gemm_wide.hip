@@ -49,7 +49,11 @@ struct WideCfg {
     static_assert(KK % 2 == 0 && KS == 64, "two k-slice fragment buffers; 8 / 16 weight bytes per step");
 };
 
+// Tile menu: 128 x 512 blocks of 8 waves for shapes whose tiles fill the chip;
+// 64 x 128 blocks (4 waves of 32 x 64, two blocks per CU) for mid-size shapes,
+// which split K across blocks to reach two waves per SIMD.
 using Wide = WideCfg<128, 512, 128, 64, 64>;
+using WideSmall = WideCfg<64, 128, 32, 64, 64>;
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x2_t __attribute__((ext_vector_type(2)));
@@ -102,10 +106,14 @@ template <int I>
 using int_c = std::integral_constant<int, I>;
 
 // One block: a BR x BC tile of C over the K steps [s0, s0 + ns).  SPLIT
-// blocks (split-K) write their raw sums to `partial` for splitk_reduce_kernel.
+// blocks (split-K) write their raw sums to `partial`; the last block of a
+// tile to finish (counted in counters[tile], which it leaves zero) adds the
+// splits' sums in split order and runs the epilogue, so the result is the
+// same on every run whichever block finishes last.
 template <class Cfg, bool TERNARY, bool SPLIT>
 __global__ void __launch_bounds__(Cfg::NT)
-gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per_split, float* partial) {
+gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per_split, float* partial,
+                 int* counters) {
     __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 3 * Cfg::BR * Cfg::KROW];
     constexpr int kPlane = Cfg::BR * Cfg::KROW;  // bf16 per plane
     constexpr int KS = Cfg::KS;
@@ -305,22 +313,70 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
     }
 
     if constexpr (SPLIT) {
-        // raw sums of this split: partial[split][m][n]
-        float* part = partial + static_cast<int64_t>(split) * p.M * p.N;
+        // Raw sums of this split go to partial[split][m][n]; the last block of
+        // the tile to count itself in adds all splits in split order.  The
+        // sums are written and read at device scope (sc1: through to the
+        // memory side, never a stale line of another XCD's L2), so no L2-wide
+        // write-back or invalidate is needed; the barrier's wait for the
+        // stores orders them before the count.  Buffer accesses over one
+        // split's M x N sums (host-checked below 2^31 bytes): rows past M
+        // are dropped / read zero, columns past N touch sums no stored output
+        // uses (and are never stored: n < N is checked).
+        constexpr int kDeviceScope = 16;  // cache policy SC1
+        const int64_t MN = static_cast<int64_t>(p.M) * p.N;
+        const int nsplit = static_cast<int>(gridDim.x) / total;
+        int voff[Cfg::FR][Cfg::FC];
 #pragma unroll
-        for (int i = 0; i < Cfg::FR; ++i) {
-            const int mrow = r0 + wr * Cfg::WR + i * 32 + 4 * h;
+        for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
             for (int j = 0; j < Cfg::FC; ++j) {
                 const int n = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
+                voff[i][j] = n < p.N ? ((r0 + wr * Cfg::WR + i * 32 + 4 * h) * p.N + n) * 4 : 0x7FFFFFF0;
+            }
+        {
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(partial + split * MN, static_cast<uint64_t>(MN) * 4);
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int m = mrow + 8 * (e >> 2) + (e & 3);
-                    if (m < p.M && n < p.N) part[static_cast<int64_t>(m) * p.N + n] = acc[i][j][e];
-                }
+            for (int e = 0; e < 16; ++e) {
+                const int soff = (8 * (e >> 2) + (e & 3)) * p.N * 4;
+#pragma unroll
+                for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+                    for (int j = 0; j < Cfg::FC; ++j)
+                        // __float_as_uint, not __builtin_bit_cast: hipcc (ROCm 7.2) folds a bit
+                        // cast of a vector element with a loop index to element 0
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][e]), rs, voff[i][j], soff,
+                                                              kDeviceScope);
             }
         }
-        return;
+        __syncthreads();  // every wave's stores complete
+        __shared__ int is_last;
+        if (tid == 0)
+            is_last = __hip_atomic_fetch_add(counters + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      nsplit - 1;
+        __syncthreads();
+        if (!is_last) return;
+        // 0 + split 0 + split 1 + ... per output, in split order
+#pragma unroll
+        for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        for (int sp = 0; sp < nsplit; ++sp) {
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(partial + sp * MN, static_cast<uint64_t>(MN) * 4);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int soff = (8 * (e >> 2) + (e & 3)) * p.N * 4;
+#pragma unroll
+                for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+                    for (int j = 0; j < Cfg::FC; ++j)
+                        acc[i][j][e] += __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff[i][j], soff, kDeviceScope));
+            }
+        }
+        // ready for the next launch on this workspace
+        if (tid == 0) __hip_atomic_store(counters + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // ---- epilogue: C[m, n] = relu?(acc * alpha * scale[n] + bias[n] (+ beta * cin)) ----
@@ -375,68 +431,67 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
     }
 }
 
-// C = epilogue(sum over splits of partial[s]) with the sums taken in split
-// order, so the result is the same on every run.  Rows are grid-strided over
-// blockIdx.y; each thread takes 4 consecutive columns (float4 when N % 4 == 0).
-__global__ void splitk_reduce_kernel(tbn_hip::WideGemmArgs p, const float* __restrict__ partial, int splits) {
-    const int64_t MN = static_cast<int64_t>(p.M) * p.N;
-    const bool bias_then_scale = (p.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
-    const bool relu = (p.flags & TBN_EPI_RELU) != 0;
-    const bool vec = (p.N % 4) == 0;
-    const int n0 = 4 * (blockIdx.x * blockDim.x + threadIdx.x);
-    if (n0 >= p.N) return;
-    const int cnt = min(4, p.N - n0);
-    float mult[4], badd[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int n = min(n0 + e, p.N - 1);
-        mult[e] = p.scale ? p.alpha * p.scale[n] : p.alpha;
-        badd[e] = p.bias ? p.bias[n] : 0.0f;
-    }
-    for (int m = blockIdx.y; m < p.M; m += gridDim.y) {
-        const int64_t row = static_cast<int64_t>(m) * p.N + n0;
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int sp = 0; sp < splits; ++sp) {
-            const float* src = partial + sp * MN + row;
-            if (vec) {
-                const float4 v = *reinterpret_cast<const float4*>(src);
-                acc[0] += v.x, acc[1] += v.y, acc[2] += v.z, acc[3] += v.w;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (e < cnt) acc[e] += src[e];
-            }
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            if (e >= cnt) break;
-            float v = bias_then_scale ? (acc[e] + badd[e]) * mult[e] : acc[e] * mult[e] + badd[e];
-            if (p.cin) v += p.beta * (p.cin_1d ? p.cin[n0 + e] : p.cin[row + e]);
-            if (relu) v = v > 0.0f ? v : 0.0f;
-            p.C[static_cast<int64_t>(m) * p.ldc + n0 + e] = v;
-        }
-    }
-}
+// Tile and K-split choice.  Shapes whose 128 x 512 tiles fill the chip (>= 128
+// blocks of 8 waves) take them whole.  Others take the 64 x 128 tile with K
+// split over up to 8 blocks per tile, aiming at 512 blocks (two per CU), each
+// split keeping at least 4 K steps (measured on config 2, 1024^3: 2 or 4
+// splits 15.6 us, 1 split 18.6, 8 splits 20.8; config 3, 256 x 4096^2
+// ternary: 4 splits 36.6 us, 2 splits 42.7, 8 splits 40.4; the 128 x 512 and
+// 128 x 256 tiles with any split were slower).  The choice reads only M, N
+// and K, so a GEMM's result does not depend on anything else.
+// TBN_TUNE_GEMM_TILE / TBN_TUNE_GEMM_SPLITS force either.
+struct WidePlan {
+    int cfg = 0;      // 0 Wide, 1 WideSmall
+    int tiles_r = 0, tiles_c = 0, steps = 0, splits = 1, per = 0;
+    int64_t blocks() const { return static_cast<int64_t>(tiles_r) * tiles_c * splits; }
+};
 
-// K-split count: 1 when the tiles fill the chip; otherwise enough splits for
-// ~1024 waves, at least 4 K steps each and at most 8 (each split adds M*N*8
-// bytes of partial traffic).
-int split_count(int64_t tiles, int steps) {
+template <class Cfg>
+WidePlan plan_for(int cfg, int M, int N, int K) {
+    WidePlan w;
+    w.cfg = cfg;
+    w.tiles_r = static_cast<int>(tbn_hip::ceil_div(M, Cfg::BR));
+    w.tiles_c = static_cast<int>(tbn_hip::ceil_div(N, Cfg::BC));
+    w.steps = static_cast<int>(tbn_hip::ceil_div(K, Cfg::KS));
+    const int64_t tiles = static_cast<int64_t>(w.tiles_r) * w.tiles_c;
+    int sp = 1;
     const int forced = tbn_hip::tuning(TBN_TUNE_GEMM_SPLITS);
-    if (forced >= 1) return std::min(forced, std::max(steps, 1));
-    if (tiles >= 128) return 1;
-    int sp = static_cast<int>((128 + tiles - 1) / tiles);
-    sp = std::min(sp, 8);
-    sp = std::min(sp, steps / 4);
-    return std::max(sp, 1);
+    if (forced >= 1) {
+        sp = std::min(forced, std::max(w.steps, 1));
+    } else if (cfg != 0 && tiles < 512) {
+        sp = static_cast<int>(std::min<int64_t>((512 + tiles - 1) / tiles, 8));
+        sp = std::max(1, std::min(sp, w.steps / 4));
+    }
+    w.per = (w.steps + sp - 1) / sp;
+    w.splits = (w.steps + w.per - 1) / w.per;  // splits that own at least one step
+    return w;
 }
 
-template <bool TERNARY, bool SPLIT>
-void launch_wide(const tbn_hip::WideGemmArgs& a, int tiles_r, int tiles_c, int splits, int per, float* part,
+WidePlan choose_plan(int M, int N, int K) {
+    const int forced = tbn_hip::tuning(TBN_TUNE_GEMM_TILE);
+    if (forced == 0) return plan_for<Wide>(0, M, N, K);
+    if (forced == 1) return plan_for<WideSmall>(1, M, N, K);
+    const WidePlan big = plan_for<Wide>(0, M, N, K);
+    if (big.blocks() >= 128) return big;
+    return plan_for<WideSmall>(1, M, N, K);
+}
+
+template <class Cfg, bool TERNARY>
+void launch_wide(const tbn_hip::WideGemmArgs& a, const WidePlan& w, float* part, int* counters,
                  hipStream_t stream) {
-    using Cfg = Wide;
-    hipLaunchKernelGGL((gemm_wide_kernel<Cfg, TERNARY, SPLIT>), dim3(tiles_r * tiles_c * splits), dim3(Cfg::NT), 0,
-                       stream, a, tiles_r, tiles_c, per, part);
+    const dim3 grid(static_cast<unsigned>(w.blocks()));
+    if (w.splits > 1)
+        hipLaunchKernelGGL((gemm_wide_kernel<Cfg, TERNARY, true>), grid, dim3(Cfg::NT), 0, stream, a, w.tiles_r,
+                           w.tiles_c, w.per, part, counters);
+    else
+        hipLaunchKernelGGL((gemm_wide_kernel<Cfg, TERNARY, false>), grid, dim3(Cfg::NT), 0, stream, a, w.tiles_r,
+                           w.tiles_c, w.per, nullptr, nullptr);
+}
+
+template <bool TERNARY>
+void launch_plan(const tbn_hip::WideGemmArgs& a, const WidePlan& w, float* part, int* counters, hipStream_t s) {
+    if (w.cfg == 0) launch_wide<Wide, TERNARY>(a, w, part, counters, s);
+    else launch_wide<WideSmall, TERNARY>(a, w, part, counters, s);
 }
 
 }  // namespace
@@ -444,47 +499,33 @@ void launch_wide(const tbn_hip::WideGemmArgs& a, int tiles_r, int tiles_c, int s
 namespace tbn_hip {
 
 bool gemm_wide_fits(const WideGemmArgs& a, bool ternary) {
-    using Cfg = Wide;
-    const int64_t tiles = ceil_div(a.M, Cfg::BR) * ceil_div(a.N, Cfg::BC);
-    const int steps = static_cast<int>(ceil_div(a.K, Cfg::KS));
-    const int64_t blocks = tiles * split_count(tiles, steps);
-    // shapes whose tiles (with K splits) fill at least half the chip
-    return a.K >= Cfg::KS && blocks >= 128 && a.M >= 128 && a.N >= 512 && a.lda % 4 == 0 &&
+    const WidePlan w = choose_plan(a.M, a.N, a.K);
+    const int waves = w.cfg == 0 ? 8 : 4;
+    const int bc = w.cfg == 0 ? 512 : 128;
+    // shapes that give at least half the chip one wave per SIMD
+    return a.K >= 64 && w.blocks() * waves >= 512 && a.M >= 64 && a.N >= 128 && a.lda % 4 == 0 &&
            reinterpret_cast<uintptr_t>(a.A) % 16 == 0 && a.col_bytes % 16 == 0 &&
            reinterpret_cast<uintptr_t>(a.packed) % 16 == 0 && a.lda <= (1 << 22) &&
-           static_cast<int64_t>(Cfg::BC) * a.col_bytes < (1LL << 31) && (ternary || a.col_bytes % 16 == 0);
+           static_cast<int64_t>(bc) * a.col_bytes < (1LL << 31) && (ternary || a.col_bytes % 16 == 0) &&
+           static_cast<int64_t>(w.tiles_r) * w.tiles_c <= kWorkspaceCounters &&
+           (w.splits == 1 || static_cast<int64_t>(a.M + 128) * a.N * 4 < (1LL << 31));
 }
 
 int gemm_wide(const WideGemmArgs& a, bool ternary, hipStream_t stream) {
-    using Cfg = Wide;
-    const int tiles_r = static_cast<int>(ceil_div(a.M, Cfg::BR));
-    const int tiles_c = static_cast<int>(ceil_div(a.N, Cfg::BC));
-    const int steps = static_cast<int>(ceil_div(a.K, Cfg::KS));
-    const int splits = split_count(static_cast<int64_t>(tiles_r) * tiles_c, steps);
+    const WidePlan w = choose_plan(a.M, a.N, a.K);
     const char* what = ternary ? "gemm_f32_ternary (wide)" : "gemm_f32_binary (wide)";
-    if (splits == 1) {
-        if (ternary) launch_wide<true, false>(a, tiles_r, tiles_c, 1, steps, nullptr, stream);
-        else launch_wide<false, false>(a, tiles_r, tiles_c, 1, steps, nullptr, stream);
-        return check_launch(what);
-    }
-    const int per = (steps + splits - 1) / splits;
-    const int used = (steps + per - 1) / per;  // splits that own at least one step
     void* part = nullptr;
-    const size_t bytes = static_cast<size_t>(used) * a.M * a.N * sizeof(float);
+    int* counters = nullptr;
     bool temporary = false;
-    const int wrc = stream_workspace(stream, bytes, part, temporary);
-    if (wrc) return wrc;
-    if (ternary) launch_wide<true, true>(a, tiles_r, tiles_c, used, per, static_cast<float*>(part), stream);
-    else launch_wide<false, true>(a, tiles_r, tiles_c, used, per, static_cast<float*>(part), stream);
-    int rc = check_launch(what);
-    if (rc == TBN_SUCCESS) {
-        const int gx = static_cast<int>(ceil_div(ceil_div(a.N, 4), 256));
-        const int gy = static_cast<int>(std::min<int64_t>(a.M, 65535));
-        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(gx, gy), dim3(256), 0, stream, a,
-                           static_cast<const float*>(part), used);
-        rc = check_launch("gemm split-K reduce");
+    if (w.splits > 1) {
+        const size_t bytes = static_cast<size_t>(w.splits) * a.M * a.N * sizeof(float);
+        const int wrc = stream_workspace(stream, bytes, part, temporary, &counters);
+        if (wrc) return wrc;
     }
-    release_workspace(part, temporary, stream);
+    if (ternary) launch_plan<true>(a, w, static_cast<float*>(part), counters, stream);
+    else launch_plan<false>(a, w, static_cast<float*>(part), counters, stream);
+    const int rc = check_launch(what);
+    if (part) release_workspace(part, temporary, stream);
     return rc;
 }
 

@@ -38,6 +38,7 @@ WEIGHTS_TERNARY = 1
 TUNE_CONV_TILE = 1
 TUNE_CONV_SPLITS = 2
 TUNE_GEMM_SPLITS = 3
+TUNE_GEMM_TILE = 4
 OP_SUB = 0
 OP_GREATER = 1
 OP_LESS = 2

@@ -111,14 +111,17 @@ int tbn_hip_synchronize(tbn_stream_t stream);
 /* ---- tuning controls (no counterpart in the reference) ---------------------
  * Process-wide launch-shape choices.  Each starts from an environment variable
  * read once, at the first call that needs it (TBN_CONV_TILE, TBN_CONV_SPLITS,
- * TBN_GEMM_SPLITS), and changes only through tbn_hip_set_tuning.  They pick
- * kernel variants: a forced conv tile never changes a result (every tile sums
- * in the same order); a forced split count changes the summation order. */
+ * TBN_GEMM_SPLITS, TBN_GEMM_TILE), and changes only through tbn_hip_set_tuning.
+ * They pick kernel variants: a forced conv tile never changes a result (every
+ * tile sums in the same order); a forced split count or GEMM tile changes the
+ * summation order. */
 enum tbn_tuning {
     TBN_TUNE_CONV_TILE = 1,   /* patch-conv tile id, -1 = automatic (default)   */
     TBN_TUNE_CONV_SPLITS = 2, /* patch-conv K splits, 0 = automatic; pooled
                                  convs never split                               */
-    TBN_TUNE_GEMM_SPLITS = 3  /* wide GEMM K splits, 0 = automatic              */
+    TBN_TUNE_GEMM_SPLITS = 3, /* wide GEMM K splits, 0 = automatic              */
+    TBN_TUNE_GEMM_TILE = 4    /* wide GEMM tile: 0 = 128x512, 1 = 64x128,
+                                 -1 = automatic (default)                        */
 };
 int tbn_hip_set_tuning(int option, int value);
 int tbn_hip_get_tuning(int option, int* value);

@@ -397,3 +397,63 @@ def test_gemm_error_codes(dev):
     assert e.value.code == tbn_hip.INVALID_ARGUMENT
     # empty problems are no-ops
     tbn_hip.call("tbn_hip_gemm_f32_binary", None, 0, 0, 8, 64, None, 64, 8, None, 1.0, None, 0, None, 8, None)
+
+
+@pytest.mark.parametrize("tile,splits", [(0, 1), (0, 3), (1, 1), (1, 2), (1, 5), (1, 8)])
+@pytest.mark.parametrize("ternary", [False, True], ids=["binary", "ternary"])
+def test_gemm_wide_every_tile_and_split(dev, orc, tile, splits, ternary):
+    """Each wide tile (128x512, 64x128), whole or with K split over
+    blocks whose last finisher adds the splits in split order: within the
+    tolerance of the float64 oracle, and bit-identical on a second run (the
+    order does not depend on which block finishes last)."""
+    M, K, N = 300, 1100, 700
+    rng = np.random.default_rng(tile * 10 + splits + 100 * ternary)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    scale = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
+    K_pad, N_pad = tbn_hip.padded_dims(K, N)
+    if ternary:
+        t = rng.choice(np.int8([-1, 0, 1]), size=(K, N), p=[0.3, 0.4, 0.3])
+        packed = empty(N_pad * K_pad // 4, torch.uint8)
+        tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(t)), K, N, tbn_hip.LAYOUT_KN, K_pad, N_pad, P(packed), None)
+        ref = _f64_dev_ternary(A, t, scale, bias=bias, relu=True)
+    else:
+        binw = (rng.random((K, N)) < 0.5).astype(np.uint8)
+        packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+        ref = _f64_dev_gemm(A, binw, scale, bias=bias, relu=True)
+    kind = "ternary" if ternary else "binary"
+    with tbn_hip.tuning(tbn_hip.TUNE_GEMM_TILE, tile), tbn_hip.tuning(tbn_hip.TUNE_GEMM_SPLITS, splits):
+        c1 = host(run_gemm(kind, A, K, M, N, K, packed, K_pad, N_pad, scale, 1.0, bias, tbn_hip.EPI_RELU))
+        c2 = host(run_gemm(kind, A, K, M, N, K, packed, K_pad, N_pad, scale, 1.0, bias, tbn_hip.EPI_RELU))
+    assert np.array_equal(c1.view(np.uint32), c2.view(np.uint32))
+    rm.assert_within_tolerance(c1, ref, K, np.abs(A).max() * 1.5)
+
+
+def test_gemm_split_counters_survive_other_workspace_users(dev, orc):
+    """The split-K GEMM's tile counters live at the head of the stream
+    workspace that conv split-K and TBN mode also use: alternating those
+    calls with split GEMMs of other shapes keeps every GEMM correct."""
+    rng = np.random.default_rng(77)
+    shapes = [(1024, 1024, 1024), (256, 4096, 2048), (130, 700, 900)]
+    probs = []
+    for M, K, N in shapes:
+        A = rng.standard_normal((M, K)).astype(np.float32)
+        binw = (rng.random((K, N)) < 0.5).astype(np.uint8)
+        packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+        probs.append((A, binw, packed, K_pad, N_pad, _f64_dev_gemm(A, binw, np.ones(N, np.float32))))
+    x = rng.standard_normal((3, 256, 7, 7)).astype(np.float32)
+    wb = (rng.random((96, 256 * 9)) < 0.5).astype(np.uint8)
+    Kc_pad, Nc_pad = tbn_hip.padded_dims(256 * 9, 96)
+    cpk = empty(Nc_pad * Kc_pad // 8, torch.uint8)
+    tbn_hip.call("tbn_hip_pack_binary", P(to_dev(wb)), 256 * 9, 96, tbn_hip.LAYOUT_NK, Kc_pad, Nc_pad, P(cpk), None)
+    d = tbn_hip.conv_desc(3, 256, 7, 7, 96, 3, 3, 1, 1, 1, 1)
+    dx = to_dev(x)
+    for rnd in range(2):
+        for A, binw, packed, K_pad, N_pad, ref in probs:
+            M, K = A.shape
+            N = binw.shape[1]
+            C = host(run_gemm("binary", A, K, M, N, K, packed, K_pad, N_pad))
+            rm.assert_within_tolerance(C, ref, K, np.abs(A).max())
+            y = empty((3, 96, 7, 7), torch.float32)  # a split-K conv in between
+            tbn_hip.call("tbn_hip_conv2d_f32_binary", P(dx), d, P(cpk), Kc_pad, Nc_pad, None, 1.0, None, 0, P(y),
+                         None)
