@@ -745,6 +745,7 @@ using P6 = PatchCfg<64, 4, 8, 32, 32>;
 using P7 = PatchCfg<64, 8, 8, 64, 32>;    // 64 channels per wave: each pixel fragment feeds 2 MFMAs
 using P8 = PatchCfg<64, 8, 16, 64, 32>;
 using P9 = PatchCfg<128, 8, 8, 32, 32>;   // 8 waves: two per SIMD share a tile
+using P10 = PatchCfg<32, 14, 16, 32, 32>; // linear: 224 pixels, a whole 14 x 14 (or smaller) image, 7 waves
 
 template <class Cfg>
 constexpr TileChoice choice(int cfg, int linear, int single = 0) {
@@ -752,7 +753,7 @@ constexpr TileChoice choice(int cfg, int linear, int single = 0) {
 }
 
 // The TBN_TUNE_CONV_TILE control forces one tile: id = cfg for linear tiles,
-// 10 + cfg for 2-D tiles, plus 20 for the one-buffer variants.
+// 16 + cfg for 2-D tiles, plus 32 for the one-buffer variants.
 int tile_override() { return tbn_hip::tuning(TBN_TUNE_CONV_TILE); }
 
 // In preference order (linear tiles store whole 128-byte pixel runs; larger
@@ -770,7 +771,7 @@ constexpr TileChoice kMenu[] = {choice<P0>(0, 1), choice<P1>(1, 1), choice<P2>(2
                                 choice<P7>(7, 1, 1), choice<P8>(8, 1, 1), choice<P0>(0, 0, 1), choice<P1>(1, 0, 1),
                                 choice<P2>(2, 0, 1), choice<P3>(3, 0, 1), choice<P6>(6, 0, 1), choice<P7>(7, 0, 1),
                                 choice<P8>(8, 0, 1), choice<P9>(9, 1), choice<P9>(9, 0), choice<P9>(9, 1, 1),
-                                choice<P9>(9, 0, 1)};
+                                choice<P9>(9, 0, 1), choice<P10>(10, 1), choice<P10>(10, 1, 1)};
 
 // A tile can run this geometry: its patch fits the LDS and the staging
 // registers (8 items per thread for the patch and for the weight words).
@@ -786,7 +787,7 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
     int64_t best_blocks = -1;
     const int forced = tile_override();
     for (const auto& c : kMenu) {
-        const int id = (c.linear ? c.cfg : 10 + c.cfg) + 20 * c.single;
+        const int id = (c.linear ? c.cfg : 16 + c.cfg) + 32 * c.single;
         if (forced >= 0 && id != forced) continue;
         if (forced < 0) {
             if (g.M <= 32 && c.BM != 32) continue;
@@ -863,7 +864,8 @@ int dispatch_patch(int id, const float* x, const PatchGeom& g, const uint8_t* w,
         case 6: return launch_patch<P6, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
         case 7: return launch_patch<P7, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
         case 8: return launch_patch<P8, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
-        default: return launch_patch<P9, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 9: return launch_patch<P9, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        default: return launch_patch<P10, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
     }
 }
 

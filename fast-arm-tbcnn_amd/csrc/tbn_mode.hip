@@ -304,9 +304,37 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
 
     const int a_frag = (wr * Cfg::WR + (lane & 31)) * Cfg::KROW + h * 16;
 
-    // step s: four MFMA slices of 32 k on LDS buffer s & 1; meanwhile step
+    // Step s: four MFMA slices of 32 k on LDS buffer s & 1; meanwhile step
     // s+1's A goes to the other buffer and step s+2's A and s+1's W words are
-    // fetched
+    // fetched.  Software pipeline across slices: slice kk+1's weight bits are
+    // expanded and its A fragments read from LDS while slice kk's MFMAs run
+    // (the next step's slice 0 comes from the next step's words and, after
+    // the barrier, from the other LDS buffer).
+    i32x4_t bfr[2][Cfg::FC];
+    i32x4_t afr[2][Cfg::FR];
+    auto expand_b = [&](const uint32_t (&w)[Cfg::FC][4], int kk, i32x4_t (&bf)[Cfg::FC]) {
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j) {
+            const uint32_t word = w[j][kk];
+#pragma unroll
+            for (int d = 0; d < 4; ++d)
+                bf[j][d] = static_cast<int>(spread4(__builtin_amdgcn_ubfe(word, 16 * h + 4 * d, 4)));
+        }
+    };
+    auto read_a = [&](int u, int kk, i32x4_t (&af)[Cfg::FR]) {
+#pragma unroll
+        for (int i = 0; i < Cfg::FR; ++i)
+            af[i] = *reinterpret_cast<const i32x4_t*>(lds + u * Cfg::BR * Cfg::KROW + i * 32 * Cfg::KROW + a_frag +
+                                                      kk * 32);
+    };
+    auto mfmas = [&](const i32x4_t (&af)[Cfg::FR], const i32x4_t (&bf)[Cfg::FC]) {
+#pragma unroll
+        for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+    };
+
     load_a(0);
     load_b(0, bw);
     store_a(0);
@@ -314,42 +342,56 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
         load_a(1);
         load_b(1, bwn);
     }
+    expand_b(bw, 0, bfr[0]);
     __syncthreads();
-    for (int s = 0; s < steps; ++s) {
+    int s = 0;
+    // full steps that have a successor: four slices, the last one prepares the
+    // next step's slice 0 weights (its A fragments follow the barrier)
+    for (; s + 1 < steps; ++s) {
         const int u = s & 1;
-        const int slices = s + 1 < steps ? 4 : last_slices;
+        read_a(u, 0, afr[0]);
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-            if (kk >= slices) break;
-            i32x4_t bf[Cfg::FC];
-#pragma unroll
-            for (int j = 0; j < Cfg::FC; ++j) {
-                const uint32_t word = bw[j][kk];
-#pragma unroll
-                for (int d = 0; d < 4; ++d)
-                    bf[j][d] = static_cast<int>(spread4(__builtin_amdgcn_ubfe(word, 16 * h + 4 * d, 4)));
+            if (kk + 1 < 4) {
+                read_a(u, kk + 1, afr[(kk + 1) & 1]);
+                expand_b(bw, kk + 1, bfr[(kk + 1) & 1]);
+            } else {
+                expand_b(bwn, 0, bfr[0]);
             }
+            mfmas(afr[kk & 1], bfr[kk & 1]);
+            // per slice: the next slice's 4 fragment reads up front, then 8
+            // MFMAs, each followed by 3 of the 24 expansion VALU
+            if (kk + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, Cfg::FR, 0);
 #pragma unroll
-            for (int i = 0; i < Cfg::FR; ++i) {
-                const i32x4_t af = *reinterpret_cast<const i32x4_t*>(lds + u * Cfg::BR * Cfg::KROW + i * 32 * Cfg::KROW +
-                                                                    a_frag + kk * 32);
-#pragma unroll
-                for (int j = 0; j < Cfg::FC; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[j], acc[i][j], 0, 0, 0);
+            for (int q = 0; q < Cfg::FR * Cfg::FC; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
             }
         }
-        if (s + 1 < steps) {
-            store_a(u ^ 1);
+        store_a(u ^ 1);
 #pragma unroll
-            for (int j = 0; j < Cfg::FC; ++j)
+        for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
-                for (int d = 0; d < 4; ++d) bw[j][d] = bwn[j][d];
-        }
+            for (int d = 0; d < 4; ++d) bw[j][d] = bwn[j][d];
         if (s + 2 < steps) {
             load_a(s + 2);
             load_b(s + 2, bwn);
         }
         __syncthreads();
+    }
+    // the last step: 2 or 4 slices (K is a multiple of 64)
+    {
+        const int u = s & 1;
+        read_a(u, 0, afr[0]);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            if (kk >= last_slices) break;
+            if (kk + 1 < last_slices) {
+                read_a(u, kk + 1, afr[(kk + 1) & 1]);
+                expand_b(bw, kk + 1, bfr[(kk + 1) & 1]);
+            }
+            mfmas(afr[kk & 1], bfr[kk & 1]);
+        }
     }
 
     // epilogue: C = rowsum - 2 * acc; rows of register e: i*32 + 8*(e/4) + 4*h + e%4

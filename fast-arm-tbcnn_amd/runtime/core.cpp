@@ -79,10 +79,19 @@ size_t size_class(size_t bytes) {
     return (bytes + (2u << 20) - 1) & ~((size_t(2) << 20) - 1);
 }
 
+// A freed block is reused on the stream that released it right away (stream
+// order covers the kernels that used it), and on any other stream only once
+// the event recorded on the releasing stream at release time has completed.
+struct FreeBlock {
+    void* ptr;
+    Stream stream;      // current stream of the releasing thread
+    hipEvent_t ready;   // recorded there at release; null: nothing pending
+};
+
 struct Pool {
     std::mutex mu;
-    std::map<std::pair<int, size_t>, std::vector<void*>> free_blocks;  // (device, class) -> blocks
-    std::unordered_map<void*, std::pair<int, size_t>> live;              // block -> (device, class)
+    std::map<std::pair<int, size_t>, std::vector<FreeBlock>> free_blocks;  // (device, class) -> blocks
+    std::unordered_map<void*, std::pair<int, size_t>> live;                  // block -> (device, class)
     size_t cached = 0, allocated = 0;
 };
 
@@ -100,8 +109,12 @@ int current_device() {
 void free_cached_locked(Pool& p, int dev) {
     for (auto it = p.free_blocks.begin(); it != p.free_blocks.end();) {
         if (dev >= 0 && it->first.first != dev) { ++it; continue; }
-        for (void* b : it->second) {
-            (void)hipFree(b);
+        for (FreeBlock& b : it->second) {
+            if (b.ready) {
+                (void)hipEventSynchronize(b.ready);
+                (void)hipEventDestroy(b.ready);
+            }
+            (void)hipFree(b.ptr);
             p.cached -= it->first.second;
         }
         it = p.free_blocks.erase(it);
@@ -124,13 +137,21 @@ void* allocate(size_t bytes) {
     Pool& p = pool();
     std::lock_guard<std::mutex> lock(p.mu);
     auto it = p.free_blocks.find({dev, cls});
-    if (it != p.free_blocks.end() && !it->second.empty()) {
-        void* b = it->second.back();
-        it->second.pop_back();
-        p.cached -= cls;
-        p.live[b] = {dev, cls};
-        p.allocated += cls;
-        return b;
+    if (it != p.free_blocks.end()) {
+        std::vector<FreeBlock>& v = it->second;
+        for (size_t i = v.size(); i-- > 0;) {
+            FreeBlock& fb = v[i];
+            const bool usable = fb.stream == t_stream || !fb.ready || hipEventQuery(fb.ready) == hipSuccess;
+            if (!usable) continue;
+            void* b = fb.ptr;
+            if (fb.ready) (void)hipEventDestroy(fb.ready);
+            v.erase(v.begin() + static_cast<std::ptrdiff_t>(i));
+            p.cached -= cls;
+            p.live[b] = {dev, cls};
+            p.allocated += cls;
+            (void)hipGetLastError();  // a pending hipEventQuery status is not an error
+            return b;
+        }
     }
     void* b = nullptr;
     hipError_t e = hipMalloc(&b, cls);
@@ -151,7 +172,19 @@ void release(void* b) noexcept {
     std::lock_guard<std::mutex> lock(p.mu);
     auto it = p.live.find(b);
     if (it == p.live.end()) return;
-    p.free_blocks[it->second].push_back(b);
+    hipEvent_t ev = nullptr;
+    bool recorded = false;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) == hipSuccess) {
+        recorded = hipEventRecord(ev, static_cast<hipStream_t>(t_stream)) == hipSuccess;
+        if (!recorded) (void)hipEventDestroy(ev);
+    }
+    if (!recorded) {
+        // no event: wait for the device, so the block is free for any stream
+        ev = nullptr;
+        (void)hipDeviceSynchronize();
+    }
+    (void)hipGetLastError();
+    p.free_blocks[it->second].push_back(FreeBlock{b, t_stream, ev});
     p.cached += it->second.second;
     p.allocated -= it->second.second;
     p.live.erase(it);

@@ -394,7 +394,7 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
     tbn_hip.call("tbn_hip_pack_conv_weights", tbn_hip.WEIGHTS_BINARY, P(packed), K_pad, N_pad, d, P(cw), None)
     dx, ds, db = to_dev(x), to_dev(scale), to_dev(bias)
     outs = {}
-    for tile in [t for base in (0, 10, 20, 30) for t in range(base, base + 10)]:
+    for tile in [t for base in (0, 16, 32, 48) for t in range(base, base + 11)]:
         with tbn_hip.tuning(tbn_hip.TUNE_CONV_TILE, tile):
             y = empty(oshape, torch.float32)
             y.fill_(np.nan)
@@ -405,7 +405,7 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
                 continue  # this tile cannot hold the geometry
             assert rc == 0, tbn_hip.last_error()
             outs[tile] = host(y)
-    assert any(t >= 20 for t in outs) and any(t < 20 for t in outs), sorted(outs)
+    assert any(t >= 32 for t in outs) and any(t < 32 for t in outs), sorted(outs)
     first = next(iter(outs.values()))
     for tile, y in outs.items():
         assert np.array_equal(y, first), f"tile {tile} differs"
