@@ -115,12 +115,17 @@ __device__ __forceinline__ bool tile_pixel(const PatchGeom& g, int q0, int row0,
     return valid;
 }
 
-template <int BM_, int TH_, int TW_, int WM_, int WQ_>
+// KG > 1: KG groups of waves, group g taking chunks g, g + KG, ... of the
+// block's K range into its own accumulators; the groups' sums are added in
+// group order at the end (used for two-chunk layers, both chunks staged at
+// once, so a block's compute runs in half the time on twice the waves).
+template <int BM_, int TH_, int TW_, int WM_, int WQ_, int KG_ = 1>
 struct PatchCfg {
-    static constexpr int BM = BM_, TH = TH_, TW = TW_, WM = WM_, WQ = WQ_;
+    static constexpr int BM = BM_, TH = TH_, TW = TW_, WM = WM_, WQ = WQ_, KG = KG_;
     static constexpr int QT = TH * TW;
     static constexpr int WAVES_M = BM / WM, WAVES_Q = QT / WQ;
-    static constexpr int NT = 64 * WAVES_M * WAVES_Q;
+    static constexpr int WAVES = WAVES_M * WAVES_Q;  // per K group
+    static constexpr int NT = 64 * WAVES * KG;
     static constexpr int FR = WM / 32, FC = WQ / 32;
     static_assert(QT % WQ == 0 && BM % WM == 0 && WM % 32 == 0 && WQ % 32 == 0, "bad tile");
     static_assert(TH % 2 == 0 && TW % 2 == 0, "tiles must hold whole 2x2 pool windows");
@@ -196,11 +201,15 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave / Cfg::WAVES_Q;
-    const int wq = wave % Cfg::WAVES_Q;
+    const int kgrp = wave / Cfg::WAVES;  // K group
+    const int wg = wave - kgrp * Cfg::WAVES;
+    const int wm = wg / Cfg::WAVES_Q;
+    const int wq = wg % Cfg::WAVES_Q;
 
     // block -> (channel tile, image, spatial tile); channel tiles of one pixel
-    // tile are neighbours so the patch is shared through L2
+    // tile are neighbours in the logical order, and blocks are dealt
+    // round-robin over the 8 XCDs, so the logical order runs consecutively on
+    // one XCD: the tile's patch is fetched into that XCD's L2 once
     const int tiles_m = (g.M + Cfg::BM - 1) / Cfg::BM;
     int bid = static_cast<int>(blockIdx.x);
     int sp = 0;  // K split of this block
@@ -208,6 +217,7 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
         sp = bid / g.blocks_split;
         bid -= sp * g.blocks_split;
     }
+    if (g.blocks_split % 8 == 0) bid = (bid % 8) * (g.blocks_split / 8) + bid / 8;
     const int cb = sp * g.cps;                        // the block's chunks [cb, ce)
     const int ce = min(g.chunks, cb + g.cps);
     const int mt = bid % tiles_m;
@@ -364,6 +374,7 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
         epi_lds[Cfg::BM + tid] = raw_bias;
     }
     if (cb + 1 < ce) load_chunk(cb + 1);
+    if constexpr (Cfg::KG > 1) store_chunk(1);  // both chunks (host-checked: exactly KG = 2)
     __syncthreads();
 
     const int kg = lane >> 5;
@@ -372,7 +383,7 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     // patch offset of tap (r, s): (r*dh*PWi + s*dw) * kPix
     const int tap_ds = g.dw * kPix;
     const int tap_dr = g.dh * g.PWi * kPix;
-    for (int ch = cb; ch < ce; ++ch) {
+    for (int ch = cb + kgrp; ch < ce; ch += Cfg::KG) {
         const uint16_t* cur = lds + (g.single ? 0 : ((ch - cb) & 1)) * buf_elems;
         auto read_b = [&](int toff, int kk, u32x4_t (&b)[3][Cfg::FC]) {
 #pragma unroll
@@ -473,12 +484,35 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                 s = next_s;
             }
         }
-        if (ch + 1 < ce) {
+        if (Cfg::KG == 1 && ch + 1 < ce) {
             if (g.single) __syncthreads();  // every wave is done reading the buffer
             store_chunk(g.single ? 0 : (ch + 1 - cb) & 1);
             if (ch + 2 < ce) load_chunk(ch + 2);
         }
         __syncthreads();
+    }
+    if constexpr (Cfg::KG > 1) {
+        // group 1 hands its sums to group 0 through the (now free) patch
+        // buffers, [wave][f][j][e][lane]; group 0 adds them after its own
+        float* red = reinterpret_cast<float*>(lds);
+        constexpr int kVals = Cfg::FR * Cfg::FC * 16;
+        float* mine = red + wg * kVals * 64 + lane;
+        if (kgrp == 1) {
+#pragma unroll
+            for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+                for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) mine[((f * Cfg::FC + j) * 16 + e) * 64] = acc[f][j][e];
+        }
+        __syncthreads();
+        if (kgrp != 0) return;
+#pragma unroll
+        for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[f][j][e] += mine[((f * Cfg::FC + j) * 16 + e) * 64];
     }
 
     // ---- epilogue: scale, bias, residual, ReLU, optional 2x2 max pool ----
@@ -687,6 +721,7 @@ struct TileChoice {
     int linear;  // 1: linear tiles, 0: 2-D tiles
     int TH, TW, BM, NT;
     int single;  // 1: one LDS buffer
+    int kg;      // K groups of waves (PatchCfg::KG)
 };
 
 size_t lds_bytes(const PatchGeom& g, int BM, bool ternary) {
@@ -746,10 +781,16 @@ using P7 = PatchCfg<64, 8, 8, 64, 32>;    // 64 channels per wave: each pixel fr
 using P8 = PatchCfg<64, 8, 16, 64, 32>;
 using P9 = PatchCfg<128, 8, 8, 32, 32>;   // 8 waves: two per SIMD share a tile
 using P10 = PatchCfg<32, 14, 16, 32, 32>; // linear: 224 pixels, a whole 14 x 14 (or smaller) image, 7 waves
+// two K groups (layers of exactly two chunks, 33..64 input channels)
+using P11 = PatchCfg<128, 8, 8, 64, 32, 2>;
+using P12 = PatchCfg<64, 8, 8, 32, 32, 2>;
+using P13 = PatchCfg<64, 8, 16, 64, 32, 2>;
+using P14 = PatchCfg<32, 14, 16, 32, 32, 2>;
+using P15 = PatchCfg<64, 8, 8, 64, 32, 2>;
 
 template <class Cfg>
 constexpr TileChoice choice(int cfg, int linear, int single = 0) {
-    return TileChoice{cfg, linear, Cfg::TH, Cfg::TW, Cfg::BM, Cfg::NT, single};
+    return TileChoice{cfg, linear, Cfg::TH, Cfg::TW, Cfg::BM, Cfg::NT, single, Cfg::KG};
 }
 
 // The TBN_TUNE_CONV_TILE control forces one tile: id = cfg for linear tiles,
@@ -771,15 +812,26 @@ constexpr TileChoice kMenu[] = {choice<P0>(0, 1), choice<P1>(1, 1), choice<P2>(2
                                 choice<P7>(7, 1, 1), choice<P8>(8, 1, 1), choice<P0>(0, 0, 1), choice<P1>(1, 0, 1),
                                 choice<P2>(2, 0, 1), choice<P3>(3, 0, 1), choice<P6>(6, 0, 1), choice<P7>(7, 0, 1),
                                 choice<P8>(8, 0, 1), choice<P9>(9, 1), choice<P9>(9, 0), choice<P9>(9, 1, 1),
-                                choice<P9>(9, 0, 1), choice<P10>(10, 1), choice<P10>(10, 1, 1)};
+                                choice<P9>(9, 0, 1), choice<P10>(10, 1), choice<P10>(10, 1, 1),
+                                choice<P11>(11, 1), choice<P12>(12, 1), choice<P13>(13, 1), choice<P14>(14, 1),
+                                choice<P15>(15, 1), choice<P11>(11, 0), choice<P12>(12, 0), choice<P13>(13, 0),
+                                choice<P15>(15, 0)};
 
 // A tile can run this geometry: its patch fits the LDS and the staging
 // registers (8 items per thread for the patch and for the weight words).
+// Layers of exactly two chunks (33..64 input channels), 3x3, one K split:
+// two K groups of waves.  Decided by the shape alone, and every tile of a
+// class sums in the same order, so the tile choice never changes a result.
+bool two_group_shape(const PatchGeom& g) { return g.chunks == 2 && g.taps == 9 && g.splits == 1; }
+
 bool tile_fits(const PatchGeom& g, const TileChoice& c, PatchGeom& t) {
+    if ((c.kg == 2) != two_group_shape(g)) return false;
     t = g;
     fill_patch(t, c);
+    const size_t bufs = lds_bytes(t, c.BM, true) - 2 * sizeof(float) * c.BM;
+    const bool red_fits = c.kg == 1 || static_cast<size_t>(c.BM) * c.TH * c.TW * 4 <= bufs;
     return lds_bytes(t, c.BM, true) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= 8 * c.NT &&
-           c.BM * t.taps <= 8 * c.NT;
+           c.BM * t.taps <= 8 * c.NT && red_fits && (c.kg == 1 || !c.single);
 }
 
 bool choose_tile(PatchGeom& g, TileChoice& out) {
@@ -865,7 +917,12 @@ int dispatch_patch(int id, const float* x, const PatchGeom& g, const uint8_t* w,
         case 7: return launch_patch<P7, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
         case 8: return launch_patch<P8, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
         case 9: return launch_patch<P9, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
-        default: return launch_patch<P10, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 10: return launch_patch<P10, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 11: return launch_patch<P11, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 12: return launch_patch<P12, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 13: return launch_patch<P13, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        case 14: return launch_patch<P14, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
+        default: return launch_patch<P15, TERNARY>(x, g, w, col_bytes, m_alloc, epi, s);
     }
 }
 

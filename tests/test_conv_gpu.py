@@ -394,7 +394,7 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
     tbn_hip.call("tbn_hip_pack_conv_weights", tbn_hip.WEIGHTS_BINARY, P(packed), K_pad, N_pad, d, P(cw), None)
     dx, ds, db = to_dev(x), to_dev(scale), to_dev(bias)
     outs = {}
-    for tile in [t for base in (0, 16, 32, 48) for t in range(base, base + 11)]:
+    for tile in range(64):
         with tbn_hip.tuning(tbn_hip.TUNE_CONV_TILE, tile):
             y = empty(oshape, torch.float32)
             y.fill_(np.nan)
@@ -405,7 +405,10 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
                 continue  # this tile cannot hold the geometry
             assert rc == 0, tbn_hip.last_error()
             outs[tile] = host(y)
-    assert any(t >= 32 for t in outs) and any(t < 32 for t in outs), sorted(outs)
+    two_groups = (C + 31) // 32 == 2 and kh * kw == 9  # two K groups of waves: no one-buffer tiles
+    assert len(outs) >= 2, sorted(outs)
+    if not two_groups:
+        assert any(t >= 32 for t in outs) and any(t < 32 for t in outs), sorted(outs)
     first = next(iter(outs.values()))
     for tile, y in outs.items():
         assert np.array_equal(y, first), f"tile {tile} differs"
