@@ -830,7 +830,8 @@ bool tile_fits(const PatchGeom& g, const TileChoice& c, PatchGeom& t) {
     fill_patch(t, c);
     const size_t bufs = lds_bytes(t, c.BM, true) - 2 * sizeof(float) * c.BM;
     const bool red_fits = c.kg == 1 || static_cast<size_t>(c.BM) * c.TH * c.TW * 4 <= bufs;
-    return lds_bytes(t, c.BM, true) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= 8 * c.NT &&
+    const int stage_items = c.kg == 1 ? 8 : 4;  // staging registers per thread (MAXI)
+    return lds_bytes(t, c.BM, true) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= stage_items * c.NT &&
            c.BM * t.taps <= 8 * c.NT && red_fits && (c.kg == 1 || !c.single);
 }
 
@@ -890,17 +891,19 @@ int launch_patch_items(const float* x, const PatchGeom& g, const uint8_t* w, int
                        const PatchEpi& epi, hipStream_t s) {
     const int per_thread = (4 * g.PHi * g.PWi + Cfg::NT - 1) / Cfg::NT;
     const int wper_thread = (Cfg::BM * g.taps + Cfg::NT - 1) / Cfg::NT;
-    if (per_thread > 8 || wper_thread > 8)
+    if (per_thread > 8 || wper_thread > 8 || (Cfg::KG > 1 && per_thread > 4))
         return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for the staging registers");
     if (per_thread <= 4) return launch_patch_taps<Cfg, TERNARY, TAPS, 4>(x, g, w, col_bytes, m_alloc, epi, s);
-    return launch_patch_taps<Cfg, TERNARY, TAPS, 8>(x, g, w, col_bytes, m_alloc, epi, s);
+    if constexpr (Cfg::KG > 1) return TBN_INVALID_SHAPE;  // not reached (checked above)
+    else return launch_patch_taps<Cfg, TERNARY, TAPS, 8>(x, g, w, col_bytes, m_alloc, epi, s);
 }
 
 template <class Cfg, bool TERNARY>
 int launch_patch(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
                  const PatchEpi& epi, hipStream_t s) {
     if (g.kh == 3 && g.kw == 3) return launch_patch_items<Cfg, TERNARY, 9>(x, g, w, col_bytes, m_alloc, epi, s);
-    return launch_patch_items<Cfg, TERNARY, 0>(x, g, w, col_bytes, m_alloc, epi, s);
+    if constexpr (Cfg::KG > 1) return TBN_INVALID_SHAPE;  // K groups serve 3x3 kernels only (tile_fits)
+    else return launch_patch_items<Cfg, TERNARY, 0>(x, g, w, col_bytes, m_alloc, epi, s);
 }
 
 template <bool TERNARY>
