@@ -45,8 +45,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 
 // Two bit planes [rows, cols / 8] of A [M, K] (zero padded): bit c of row r is
 // set in neg when a < lo, in pos when a > hi.  One thread per 32-bit word.
-// GeMM/05-final/GeMM.cpp:71-112; tbn-runtime/src/operators/quantized_gemm_neon.cpp:118-141
-__global__ void ternary_planes_kernel(const float* __restrict__ A, int64_t lda, int64_t M, int64_t K,
+// Float input: GeMM/05-final/GeMM.cpp:71-112 and
+// tbn-runtime/src/operators/quantized_gemm_neon.cpp:118-141; int8 input (lo =
+// -0.5, hi = 0.5, so the sign picks the plane): GeMM/05-final/GeMM.cpp:29-69.
+template <typename T>
+__global__ void ternary_planes_kernel(const T* __restrict__ A, int64_t lda, int64_t M, int64_t K,
                                       int64_t rows, int64_t wpr, float lo, float hi, uint32_t* __restrict__ pos,
                                       uint32_t* __restrict__ neg) {
     const int64_t total = rows * wpr;
@@ -56,10 +59,10 @@ __global__ void ternary_planes_kernel(const float* __restrict__ A, int64_t lda, 
         const int64_t c0 = (t - row * wpr) * 32;
         uint32_t p = 0, m = 0;
         if (row < M) {
-            const float* src = A + row * lda;
+            const T* src = A + row * lda;
 #pragma unroll 8
             for (int e = 0; e < 32; ++e) {
-                const float v = (c0 + e < K) ? src[c0 + e] : 0.0f;
+                const float v = (c0 + e < K) ? static_cast<float>(src[c0 + e]) : 0.0f;
                 m |= (v < lo ? 1u : 0u) << e;
                 p |= (!(v < lo) && v > hi ? 1u : 0u) << e;
             }
@@ -213,19 +216,22 @@ struct TbnGemmArgs {
     float scale;          // float output: out = float(C) * scale
 };
 
-template <int BR_, int BC_, int WR_, int WC_>
+template <int BR_, int BC_, int WR_, int WC_, int KS_>
 struct I8Cfg {
     static constexpr int BR = BR_, BC = BC_, WR = WR_, WC = WC_;
-    static constexpr int KS = 128;        // k per step: one 16-byte weight word per column
+    static constexpr int KS = KS_;        // k per step (one barrier): KS / 128 16-byte weight words per column
+    static constexpr int SL = KS / 32;    // MFMA slices per step
+    static constexpr int WPS = KS / 32;   // 32-bit weight words per column per step
     static constexpr int KROW = KS + 16;  // bytes per LDS row: conflict-free 16-byte fragment reads
     static constexpr int WAVES_R = BR / WR, WAVES_C = BC / WC;
     static constexpr int NT = 64 * WAVES_R * WAVES_C;
     static constexpr int FR = WR / 32, FC = WC / 32;
-    static constexpr int TPR = NT / BR;   // threads per A row (32 bytes each)
-    static_assert(TPR * 32 == KS, "a step's A tile is two 16-byte loads per thread");
+    static constexpr int TPR = NT / BR;   // threads per A row
+    static constexpr int ALD = KS / TPR / 16;  // 16-byte A loads per thread per step
+    static_assert(TPR * ALD * 16 == KS && KS % 128 == 0, "a step's A tile is whole 16-byte loads per thread");
 };
 
-using I8Wide = I8Cfg<128, 512, 128, 64>;
+using I8Wide = I8Cfg<128, 512, 128, 64, 128>;
 
 // 4 weight bits (bit i = weight k0 + i, 1 means -1) -> 4 bytes b_i in {0, 1}:
 // the multiply copies bit i to bit 8i without carries.
@@ -258,7 +264,7 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
     const int ar = tid / Cfg::TPR, ag = tid % Cfg::TPR;
     const __amdgpu_buffer_rsrc_t a_rs =
         make_rsrc(p.T + static_cast<int64_t>(r0) * p.ldt, static_cast<uint64_t>(p.M - r0) * p.ldt);
-    const int a_voff = ar * static_cast<int>(p.ldt) + ag * 32;
+    const int a_voff = ar * static_cast<int>(p.ldt) + ag * 16 * Cfg::ALD;
     const __amdgpu_buffer_rsrc_t b_rs =
         make_rsrc(p.bits + static_cast<int64_t>(c0) * p.col_bytes,
                   static_cast<uint64_t>(p.N_pad - c0) * static_cast<uint64_t>(p.col_bytes));
@@ -269,28 +275,34 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
 
     // K is a multiple of 64: a last step of 64 runs two of its four slices
     // (the data loaded past K for the other two is never used)
+    // K is a multiple of 64: the last step runs K % KS / 32 of its slices
+    // (the data loaded past K for the others is never used)
+    constexpr int SL = Cfg::SL, WPS = Cfg::WPS;
     const int steps = (p.K + KS - 1) / KS;
-    const int last_slices = (p.K % KS) ? (p.K % KS) / 32 : 4;
+    const int last_slices = (p.K % KS) ? (p.K % KS) / 32 : SL;
 
-    i32x4_t areg[2];
-    uint32_t bw[Cfg::FC][4], bwn[Cfg::FC][4];
+    i32x4_t areg[Cfg::ALD];
+    uint32_t bw[Cfg::FC][WPS], bwn[Cfg::FC][WPS];
     auto load_a = [&](int s) {
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) areg[h2] = __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16 * h2, s * KS, 0);
+        for (int h2 = 0; h2 < Cfg::ALD; ++h2)
+            areg[h2] = __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16 * h2, s * KS, 0);
     };
-    auto load_b = [&](int s, uint32_t (&w)[Cfg::FC][4]) {
+    auto load_b = [&](int s, uint32_t (&w)[Cfg::FC][WPS]) {
 #pragma unroll
-        for (int j = 0; j < Cfg::FC; ++j) {
-            const u32x4_t x =
-                __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], s * 16, 0));
+        for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
-            for (int d = 0; d < 4; ++d) w[j][d] = x[d];
-        }
+            for (int q = 0; q < WPS / 4; ++q) {
+                const u32x4_t x = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], s * (KS / 8) + 16 * q, 0));
+#pragma unroll
+                for (int d = 0; d < 4; ++d) w[j][4 * q + d] = x[d];
+            }
     };
-    const int a_store = ar * Cfg::KROW + ag * 32;
+    const int a_store = ar * Cfg::KROW + ag * 16 * Cfg::ALD;
     auto store_a = [&](int b) {
 #pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2)
+        for (int h2 = 0; h2 < Cfg::ALD; ++h2)
             *reinterpret_cast<i32x4_t*>(lds + b * Cfg::BR * Cfg::KROW + a_store + 16 * h2) = areg[h2];
     };
 
@@ -312,7 +324,7 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
     // the barrier, from the other LDS buffer).
     i32x4_t bfr[2][Cfg::FC];
     i32x4_t afr[2][Cfg::FR];
-    auto expand_b = [&](const uint32_t (&w)[Cfg::FC][4], int kk, i32x4_t (&bf)[Cfg::FC]) {
+    auto expand_b = [&](const uint32_t (&w)[Cfg::FC][WPS], int kk, i32x4_t (&bf)[Cfg::FC]) {
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             const uint32_t word = w[j][kk];
@@ -351,8 +363,8 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
         const int u = s & 1;
         read_a(u, 0, afr[0]);
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            if (kk + 1 < 4) {
+        for (int kk = 0; kk < SL; ++kk) {
+            if (kk + 1 < SL) {
                 read_a(u, kk + 1, afr[(kk + 1) & 1]);
                 expand_b(bw, kk + 1, bfr[(kk + 1) & 1]);
             } else {
@@ -361,7 +373,7 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
             mfmas(afr[kk & 1], bfr[kk & 1]);
             // per slice: the next slice's 4 fragment reads up front, then 8
             // MFMAs, each followed by 3 of the 24 expansion VALU
-            if (kk + 1 < 4) __builtin_amdgcn_sched_group_barrier(0x100, Cfg::FR, 0);
+            if (kk + 1 < SL) __builtin_amdgcn_sched_group_barrier(0x100, Cfg::FR, 0);
 #pragma unroll
             for (int q = 0; q < Cfg::FR * Cfg::FC; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -372,19 +384,19 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
-            for (int d = 0; d < 4; ++d) bw[j][d] = bwn[j][d];
+            for (int d = 0; d < WPS; ++d) bw[j][d] = bwn[j][d];
         if (s + 2 < steps) {
             load_a(s + 2);
             load_b(s + 2, bwn);
         }
         __syncthreads();
     }
-    // the last step: 2 or 4 slices (K is a multiple of 64)
+    // the last step: an even number of slices (K is a multiple of 64)
     {
         const int u = s & 1;
         read_a(u, 0, afr[0]);
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
+        for (int kk = 0; kk < SL; ++kk) {
             if (kk >= last_slices) break;
             if (kk + 1 < last_slices) {
                 read_a(u, kk + 1, afr[(kk + 1) & 1]);
@@ -452,8 +464,13 @@ struct Scratch {
 
 extern "C" {
 
-int tbn_hip_ternary_pack_f32(const float* A, int64_t lda, int64_t M, int64_t K, int64_t rows, int64_t cols, float lo,
-                             float hi, uint8_t* pos, uint8_t* neg, tbn_stream_t stream) {
+}  // extern "C"
+
+namespace {
+
+template <typename T>
+int ternary_pack(const T* A, int64_t lda, int64_t M, int64_t K, int64_t rows, int64_t cols, float lo, float hi,
+                 uint8_t* pos, uint8_t* neg, tbn_stream_t stream, const char* what) {
     TBN_REQUIRE(M >= 0 && K >= 0 && rows >= M && cols >= K, TBN_INVALID_ARGUMENT,
                 "padded dimensions must cover the matrix");
     TBN_REQUIRE(rows % 8 == 0 && cols % 64 == 0, TBN_INVALID_ARGUMENT,
@@ -463,10 +480,44 @@ int tbn_hip_ternary_pack_f32(const float* A, int64_t lda, int64_t M, int64_t K, 
     TBN_REQUIRE(pos && neg && (M == 0 || K == 0 || A), TBN_INVALID_ARGUMENT, "null pointer");
     TBN_DEVICE_GUARD();
     const int64_t wpr = cols / 32;
-    hipLaunchKernelGGL(ternary_planes_kernel, dim3(grid_for(rows * wpr, 256)), dim3(256), 0,
+    hipLaunchKernelGGL(ternary_planes_kernel<T>, dim3(grid_for(rows * wpr, 256)), dim3(256), 0,
                        tbn_hip::stream_of(stream), A, lda, M, K, rows, wpr, lo, hi,
                        reinterpret_cast<uint32_t*>(pos), reinterpret_cast<uint32_t*>(neg));
-    return tbn_hip::check_launch("ternary_pack_f32");
+    return tbn_hip::check_launch(what);
+}
+
+// Ternary rows (pos / neg planes, m rows of n / 8 bytes) times BinaryMatrix
+// columns: int32 C, or float(C) * scale when `float_out`, into out [m, ldo]
+// for the first `cols` columns.
+int planes_gemm(const uint8_t* pos, const uint8_t* neg, const uint8_t* bits, int64_t m, int64_t n, int64_t cols,
+                int64_t bit_cols, bool float_out, float scale, void* out, int64_t ldo, hipStream_t s) {
+    Scratch scr;
+    scr.stream = s;
+    const size_t tbytes = static_cast<size_t>(m) * n;
+    if (int rc = scr.get(tbytes + static_cast<size_t>(m) * 4 + 16)) return rc;
+    int8_t* T = static_cast<int8_t*>(scr.ptr);
+    int* rowsum = reinterpret_cast<int*>(static_cast<uint8_t*>(scr.ptr) + ((tbytes + 15) / 16) * 16);
+    hipLaunchKernelGGL(planes_to_rows_kernel, dim3(static_cast<int>(std::min<int64_t>(m, 65536))), dim3(256), 0, s,
+                       pos, neg, static_cast<int>(m), n, T, rowsum);
+    int rc = tbn_hip::check_launch("tbn_gemm (planes)");
+    if (rc != TBN_SUCCESS) return rc;
+    TbnGemmArgs a{T, n, rowsum, static_cast<int>(m), static_cast<int>(cols), static_cast<int>(n), bits, n / 8,
+                  static_cast<int>(bit_cols), out, ldo, scale};
+    return launch_i8_gemm(a, float_out, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int tbn_hip_ternary_pack_f32(const float* A, int64_t lda, int64_t M, int64_t K, int64_t rows, int64_t cols, float lo,
+                             float hi, uint8_t* pos, uint8_t* neg, tbn_stream_t stream) {
+    return ternary_pack(A, lda, M, K, rows, cols, lo, hi, pos, neg, stream, "ternary_pack_f32");
+}
+
+int tbn_hip_ternary_pack_i8(const int8_t* A, int64_t lda, int64_t M, int64_t K, int64_t rows, int64_t cols,
+                            uint8_t* pos, uint8_t* neg, tbn_stream_t stream) {
+    return ternary_pack(A, lda, M, K, rows, cols, -0.5f, 0.5f, pos, neg, stream, "ternary_pack_i8");
 }
 
 int tbn_hip_im2col_ternary_packed(const float* x, const tbn_conv2d_desc* desc, int64_t m_pad, int64_t k_pad,
@@ -503,19 +554,26 @@ int tbn_hip_tbn_gemm(const uint8_t* pos, const uint8_t* neg, const uint8_t* bits
             return tbn_hip::fail(TBN_RUNTIME_ERROR, "hipMemsetAsync failed");
         return tbn_hip::ok();
     }
-    Scratch scr;
-    scr.stream = s;
-    const size_t tbytes = static_cast<size_t>(m) * n;
-    if (int rc = scr.get(tbytes + static_cast<size_t>(m) * 4 + 16)) return rc;
-    int8_t* T = static_cast<int8_t*>(scr.ptr);
-    int* rowsum = reinterpret_cast<int*>(static_cast<uint8_t*>(scr.ptr) + ((tbytes + 15) / 16) * 16);
-    hipLaunchKernelGGL(planes_to_rows_kernel, dim3(static_cast<int>(std::min<int64_t>(m, 65536))), dim3(256), 0, s,
-                       pos, neg, static_cast<int>(m), n, T, rowsum);
-    int rc = tbn_hip::check_launch("tbn_gemm (planes)");
-    if (rc != TBN_SUCCESS) return rc;
-    TbnGemmArgs a{T, n, rowsum, static_cast<int>(m), static_cast<int>(k), static_cast<int>(n), bits, n / 8,
-                  static_cast<int>(k), C, k, 1.0f};
-    return launch_i8_gemm(a, false, s);
+    return planes_gemm(pos, neg, bits, m, n, k, k, false, 1.0f, C, k, s);
+}
+
+int tbn_hip_tbn_gemm_scaled(const uint8_t* pos, const uint8_t* neg, const uint8_t* bits, int64_t m, int64_t n,
+                            int64_t k, int64_t cols, float scale, float* out, int64_t ldo, tbn_stream_t stream) {
+    TBN_REQUIRE(m >= 0 && n >= 0 && k >= 0 && m < (1LL << 31) && k < (1LL << 31) && n < (1LL << 24),
+                TBN_INVALID_SHAPE, "m, n, k out of range");
+    TBN_REQUIRE(n % 64 == 0, TBN_INVALID_ARGUMENT, "the shared dimension n must be a multiple of 64");
+    TBN_REQUIRE(cols >= 0 && cols <= k, TBN_INVALID_SHAPE, "cols must be in [0, k]");
+    TBN_REQUIRE(ldo >= cols, TBN_INVALID_ARGUMENT, "ldo must be >= cols");
+    if (m == 0 || cols == 0) return tbn_hip::ok();
+    TBN_REQUIRE(out && (n == 0 || (pos && neg && bits)), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    hipStream_t s = tbn_hip::stream_of(stream);
+    if (n == 0) {
+        if (hipMemset2DAsync(out, ldo * sizeof(float), 0, cols * sizeof(float), m, s) != hipSuccess)
+            return tbn_hip::fail(TBN_RUNTIME_ERROR, "hipMemset2DAsync failed");
+        return tbn_hip::ok();
+    }
+    return planes_gemm(pos, neg, bits, m, n, cols, k, true, scale, out, ldo, s);
 }
 
 int tbn_hip_qlinear_matmul_binary_tbn(const float* A, int64_t lda, int64_t M, int64_t K, const uint8_t* packed,

@@ -17,17 +17,9 @@
 #include <vector>
 
 #include "tensor.hpp"
+#include "tiling.hpp"
 
 namespace tbn {
-
-// Tiling of the reference's CPU GeMM (GeMM/05-final/GeMM.hpp:16-43).  Accepted
-// for source compatibility and ignored: the GPU kernels pick their own tiles,
-// and no shape is rejected for tiling reasons (the reference throws when
-// m % mmk or k % nmk is non-zero).
-struct TilingParams {
-    uint32_t mblk = 64, nblk = 64, kblk = 128, mmk = 32, nmk = 32;
-    static constexpr TilingParams default_128x128() noexcept { return TilingParams{}; }
-};
 
 // tbn::Conv2DParams (tbn-runtime/include/tbn/operators/conv2d.hpp:12-37).  The
 // kernel size is taken from the weight tensor.

@@ -14,6 +14,7 @@
 #include <string>
 #include <vector>
 
+#include "tbn/gemm_engine.hpp"
 #include "tbn/tbn.hpp"
 
 namespace py = pybind11;
@@ -307,6 +308,95 @@ PYBIND11_MODULE(_tbn, m) {
           },
           py::arg("A"), py::arg("B"), py::arg("C") = py::none(), py::arg("alpha") = 1.0f, py::arg("beta") = 0.0f,
           py::arg("transA") = false, py::arg("transB") = false);
+
+    // ---- the GeMM engine API (GeMM/05-final/GeMM.hpp:16-239) ----
+    py::class_<TilingParams>(m, "TilingParams")
+        .def(py::init([](uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk, uint32_t nmk) {
+                 return TilingParams{mblk, nblk, kblk, mmk, nmk};
+             }),
+             py::arg("mblk") = 64, py::arg("nblk") = 64, py::arg("kblk") = 128, py::arg("mmk") = 32,
+             py::arg("nmk") = 32)
+        .def_readwrite("mblk", &TilingParams::mblk)
+        .def_readwrite("nblk", &TilingParams::nblk)
+        .def_readwrite("kblk", &TilingParams::kblk)
+        .def_readwrite("mmk", &TilingParams::mmk)
+        .def_readwrite("nmk", &TilingParams::nmk)
+        .def("validate", &TilingParams::validate, py::arg("m"), py::arg("n"), py::arg("k"))
+        .def_static("default_128x128", &TilingParams::default_128x128);
+    auto bytes_of = [](std::span<const std::uint8_t> s) {
+        py::array_t<uint8_t> out(static_cast<py::ssize_t>(s.size()));
+        if (!s.empty()) std::memcpy(out.mutable_data(), s.data(), s.size());
+        return out;
+    };
+    auto int8_span = [](const py::array_t<int8_t, py::array::c_style | py::array::forcecast>& a) {
+        return std::span<const std::int8_t>(a.data(), static_cast<size_t>(a.size()));
+    };
+    py::class_<TernaryMatrix>(m, "TernaryMatrix")
+        .def(py::init<>())
+        .def_static("pack",
+                    [int8_span](const py::array_t<int8_t, py::array::c_style | py::array::forcecast>& a,
+                                uint32_t rows, uint32_t cols) { return TernaryMatrix::pack(int8_span(a), rows, cols); },
+                    py::arg("data"), py::arg("rows"), py::arg("cols"))
+        .def_static("pack_from_float",
+                    [](const py::array_t<float, py::array::c_style | py::array::forcecast>& a, uint32_t rows,
+                       uint32_t cols, float lo, float hi) {
+                        if (static_cast<size_t>(a.size()) != static_cast<size_t>(rows) * cols)
+                            throw std::invalid_argument("TernaryMatrix: data size doesn't match dimensions");
+                        return TernaryMatrix::pack_from_float(a.data(), rows, cols, lo, hi);
+                    },
+                    py::arg("data"), py::arg("rows"), py::arg("cols"), py::arg("threshold_low") = -0.1f,
+                    py::arg("threshold_high") = 0.1f)
+        .def_property_readonly("rows", &TernaryMatrix::rows)
+        .def_property_readonly("cols", &TernaryMatrix::cols)
+        .def("empty", &TernaryMatrix::empty)
+        .def_property_readonly("positive", [bytes_of](const TernaryMatrix& t) { return bytes_of(t.view().positive); })
+        .def_property_readonly("negative", [bytes_of](const TernaryMatrix& t) { return bytes_of(t.view().negative); });
+    py::class_<BinaryMatrix>(m, "BinaryMatrix")
+        .def(py::init<>())
+        .def_static("pack",
+                    [int8_span](const py::array_t<int8_t, py::array::c_style | py::array::forcecast>& a,
+                                uint32_t rows, uint32_t cols) { return BinaryMatrix::pack(int8_span(a), rows, cols); },
+                    py::arg("data"), py::arg("rows"), py::arg("cols"))
+        .def_property_readonly("rows", &BinaryMatrix::rows)
+        .def_property_readonly("cols", &BinaryMatrix::cols)
+        .def("empty", &BinaryMatrix::empty)
+        .def_property_readonly("bits", [bytes_of](const BinaryMatrix& b) { return bytes_of(b.view().bits); });
+    py::class_<GemmEngine>(m, "GemmEngine")
+        .def(py::init<>())
+        .def("compute",
+             [](GemmEngine& e, const TernaryMatrix& A, const BinaryMatrix& B, const py::object& params) {
+                 const TilingParams p =
+                     params.is_none() ? TilingParams::default_128x128() : params.cast<TilingParams>();
+                 const Int32Matrix C = e.compute(A.view(), B.view(), p);
+                 py::array_t<int32_t> out({static_cast<py::ssize_t>(C.rows()), static_cast<py::ssize_t>(C.cols())});
+                 if (C.size()) std::memcpy(out.mutable_data(), C.data().data(), C.size() * sizeof(int32_t));
+                 return out;
+             },
+             py::arg("A"), py::arg("B"), py::arg("params") = py::none())
+        .def("last_flops", &GemmEngine::last_flops);
+    py::class_<PackedBinaryWeights>(m, "PackedBinaryWeights")
+        .def_static("from_int8",
+                    [int8_span](const py::array_t<int8_t, py::array::c_style | py::array::forcecast>& w,
+                                uint32_t rows, uint32_t cols, const TilingParams& t) {
+                        return PackedBinaryWeights::from_int8(int8_span(w), rows, cols, t);
+                    },
+                    py::arg("weights"), py::arg("rows"), py::arg("cols"),
+                    py::arg("tiling") = TilingParams::default_128x128())
+        .def("valid", &PackedBinaryWeights::valid)
+        .def_readonly("b_packed", &PackedBinaryWeights::b_packed)
+        .def_readonly("tiling", &PackedBinaryWeights::tiling)
+        .def_readonly("original_m", &PackedBinaryWeights::original_m)
+        .def_readonly("original_n", &PackedBinaryWeights::original_n)
+        .def_readonly("original_k", &PackedBinaryWeights::original_k);
+    m.def("qlinear_matmul_binary_blocked_packed",
+          [](const py::object& a, const BinaryMatrix& b, uint32_t n_orig, float scale, const TilingParams& p,
+             float lo, float hi) { return qlinear_matmul_binary_blocked_packed(as_tensor(a), b, n_orig, scale, p, lo, hi); },
+          py::arg("a"), py::arg("b_packed"), py::arg("n_orig"), py::arg("scale") = 1.0f,
+          py::arg("params") = TilingParams::default_128x128(), py::arg("threshold_low") = -0.1f,
+          py::arg("threshold_high") = 0.1f);
+    m.def("qlinear_matmul_binary_blocked_prepacked", &qlinear_matmul_binary_blocked_prepacked, py::arg("a_packed"),
+          py::arg("b_packed"), py::arg("m_orig"), py::arg("n_orig"), py::arg("scale") = 1.0f,
+          py::arg("params") = TilingParams::default_128x128());
 
     auto conv_def = [&m](const char* name, Tensor (*fn)(const Tensor&, const Tensor&, const Tensor*,
                                                           const Conv2DParams&)) {

@@ -110,6 +110,8 @@ _SIGNATURES = {
     "tbn_hip_ternary_pack_f32": ([_P, _I64, _I64, _I64, _I64, _I64, _F32, _F32, _P, _P, _P], _I32),
     "tbn_hip_im2col_ternary_packed": ([_P, ctypes.POINTER(ConvDesc), _I64, _I64, _F32, _F32, _P, _P, _P], _I32),
     "tbn_hip_tbn_gemm": ([_P, _P, _P, _I64, _I64, _I64, _P, _P], _I32),
+    "tbn_hip_tbn_gemm_scaled": ([_P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P, _I64, _P], _I32),
+    "tbn_hip_ternary_pack_i8": ([_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P], _I32),
     "tbn_hip_qlinear_matmul_binary_tbn": ([_P, _I64, _I64, _I64, _P, _I64, _I64, _I64, _F32, _F32, _F32, _P, _I64,
                                            _P], _I32),
 }

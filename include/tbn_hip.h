@@ -383,6 +383,13 @@ int tbn_hip_ternary_activation(const float* x, int64_t n, float threshold, float
 int tbn_hip_ternary_pack_f32(const float* A, int64_t lda, int64_t M, int64_t K, int64_t rows,
                              int64_t cols, float lo, float hi, uint8_t* pos, uint8_t* neg,
                              tbn_stream_t stream);
+/* TernaryMatrix::pack (GeMM/05-final/GeMM.cpp:29-69) on the device: int8
+ * values of A [M, K] (row stride lda) into the same two bit planes of rows x
+ * cols/8 bytes, zero padded; a negative value sets its neg bit, a positive
+ * one its pos bit (the reference accepts only -1, 0 and +1: check them first,
+ * as tbn::TernaryMatrix::pack does).  rows % 8 == 0, cols % 64 == 0. */
+int tbn_hip_ternary_pack_i8(const int8_t* A, int64_t lda, int64_t M, int64_t K, int64_t rows,
+                            int64_t cols, uint8_t* pos, uint8_t* neg, tbn_stream_t stream);
 /* impl::im2col_ternary_packed (conv2d.cpp:511-601): the im2col matrix
  * [n*OH*OW, c*kh*kw] of x, column (c*kh + r)*kw + s, ternarized into bit
  * planes of m_pad rows x k_pad/8 bytes; taps outside the image and padding
@@ -398,6 +405,13 @@ int tbn_hip_im2col_ternary_packed(const float* x, const tbn_conv2d_desc* desc, i
  * here).  Uses a stream-ordered temporary of m*(n+4) bytes. */
 int tbn_hip_tbn_gemm(const uint8_t* pos, const uint8_t* neg, const uint8_t* bits, int64_t m,
                      int64_t n, int64_t k, int32_t* C, tbn_stream_t stream);
+/* The extraction and scaling of qlinear_matmul_binary_blocked_prepacked
+ * (quantized_gemm_neon.cpp:314-350) fused into tbn_hip_tbn_gemm: out[i, j] =
+ * float(C[i, j]) * scale for the first m rows and `cols` (<= k) columns of C,
+ * out row stride ldo. */
+int tbn_hip_tbn_gemm_scaled(const uint8_t* pos, const uint8_t* neg, const uint8_t* bits, int64_t m,
+                            int64_t n, int64_t k, int64_t cols, float scale, float* out, int64_t ldo,
+                            tbn_stream_t stream);
 /* qlinear_matmul_binary as the reference computes it (quantized_gemm_neon.cpp:
  * 160-243,380-430): out[M, N] = float(sum_k t(A[m,k]) * w[k,n]) * scale with
  * t the ternarization at (lo, hi) and w the packed BinaryMatrix (K_pad % 64

@@ -118,3 +118,28 @@ def test_resnet18_graph_shapes():
     assert spec.value_info["pool_out"] == (2, 64, 56, 56)
     assert spec.value_info["l4b1_r2_out"] == (2, 512, 7, 7)
     assert spec.outputs == {"logits": (2, 1000)}
+
+
+def test_gemm_engine_host_checks(tbn):
+    """The GeMM engine API's argument checks (GeMM/05-final/GeMM.hpp:24-37,
+    GeMM.cpp:29-150, test_final.cpp:76-133) throw before any device work."""
+    t = tbn.TilingParams.default_128x128()
+    assert (t.mblk, t.nblk, t.kblk, t.mmk, t.nmk) == (64, 64, 128, 32, 32)
+    t.validate(128, 128, 128)
+    for args, msg in [((128, 64, 128), "n must be multiple of 128"), ((48, 128, 128), "m must be multiple of mmk"),
+                      ((128, 128, 40), "k must be multiple of nmk")]:
+        with pytest.raises(ValueError, match=msg):
+            t.validate(*args)
+    with pytest.raises(ValueError, match="kblk must be multiple of 128"):
+        tbn.TilingParams(64, 64, 64, 32, 32).validate(128, 128, 128)
+    bad = np.zeros(8 * 64, np.int8); bad[0] = 2
+    with pytest.raises(ValueError, match="values must be -1, 0, or \\+1"):
+        tbn.TernaryMatrix.pack(bad, 8, 64)
+    with pytest.raises(ValueError, match="values must be -1 or \\+1"):
+        tbn.BinaryMatrix.pack(np.zeros(64 * 8, np.int8), 64, 8)
+    with pytest.raises(ValueError, match="rows must be multiple of 8"):
+        tbn.TernaryMatrix.pack(np.zeros(100, np.int8), 10, 10)
+    with pytest.raises(ValueError, match="cols must be multiple of 64"):
+        tbn.TernaryMatrix.pack_from_float(np.zeros(8 * 32, np.float32), 8, 32)
+    assert tbn.TernaryMatrix().empty() and tbn.BinaryMatrix().empty()
+    assert tbn.TernaryMatrix().rows == 0 and tbn.BinaryMatrix().cols == 0
