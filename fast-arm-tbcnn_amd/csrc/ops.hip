@@ -94,10 +94,45 @@ __global__ void __launch_bounds__(256) maxpool3x3s2_kernel(const float* __restri
     }
 }
 
-// tbn::global_avgpool2d (pooling.cpp:184-216): one thread per plane, summing
-// in memory order so the result matches the sequential reference bit for bit.
-__global__ void __launch_bounds__(256) global_avgpool_kernel(const float* __restrict__ x, int64_t planes,
-                                                              int64_t hw, float* __restrict__ y) {
+// tbn::avgpool2d (pooling.cpp:83-148): the window's taps inside the image
+// summed in row-major window order; the count adds taps outside the image
+// only with count_include_pad; an empty count gives 0.
+__global__ void avgpool2d_kernel(const float* __restrict__ x, int64_t planes, int H, int W, int OH, int OW, int kh,
+                                 int kw, int sh, int sw, int ph, int pw, int dh, int dw, int include_pad,
+                                 float* __restrict__ y) {
+    const int per_plane = OH * OW;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= per_plane) return;
+    const int oh = i / OW;
+    const int ow = i - oh * OW;
+    const int ih0 = oh * sh - ph, iw0 = ow * sw - pw;
+    for (int64_t plane = blockIdx.y; plane < planes; plane += gridDim.y) {
+        const float* src = x + plane * H * W;
+        float sum = 0.0f;
+        int count = 0;
+        for (int r = 0; r < kh; ++r) {
+            const int ih = ih0 + r * dh;
+            for (int s = 0; s < kw; ++s) {
+                const int iw = iw0 + s * dw;
+                if (ih >= 0 && ih < H && iw >= 0 && iw < W) {
+                    sum += src[ih * W + iw];
+                    ++count;
+                } else if (include_pad) {
+                    ++count;
+                }
+            }
+        }
+        y[plane * per_plane + i] = count > 0 ? sum / static_cast<float>(count) : 0.0f;
+    }
+}
+
+// tbn::global_avgpool2d (pooling.cpp:184-216) and tbn::global_maxpool2d
+// (pooling.cpp:151-181): one thread per plane, walking it in memory order so
+// the result matches the sequential reference bit for bit (the sum's
+// rounding; for the maximum, which of -0 / +0 is kept, NaN ignored).
+template <bool MAX>
+__global__ void __launch_bounds__(256) global_pool_kernel(const float* __restrict__ x, int64_t planes,
+                                                          int64_t hw, float* __restrict__ y) {
     // a block owns 64 consecutive planes (contiguous in memory); each chunk
     // of 64 positions of all 64 planes is staged through LDS with coalesced
     // loads, then thread p adds its plane's values in memory order
@@ -105,7 +140,7 @@ __global__ void __launch_bounds__(256) global_avgpool_kernel(const float* __rest
     const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 64;
     const int np = static_cast<int>(planes - p0 < 64 ? planes - p0 : 64);
     const int tid = threadIdx.x;
-    float sum = 0.0f;
+    float acc = MAX ? -INFINITY : 0.0f;
     for (int64_t c0 = 0; c0 < hw; c0 += 64) {
         const int cl = static_cast<int>(hw - c0 < 64 ? hw - c0 : 64);
         for (int idx = tid; idx < np * 64; idx += 256) {
@@ -114,10 +149,13 @@ __global__ void __launch_bounds__(256) global_avgpool_kernel(const float* __rest
         }
         __syncthreads();
         if (tid < np)
-            for (int i = 0; i < cl; ++i) sum += tile[tid][i];
+            for (int i = 0; i < cl; ++i) {
+                if (MAX) acc = first_max(acc, tile[tid][i]);
+                else acc += tile[tid][i];
+            }
         __syncthreads();
     }
-    if (tid < np) y[p0 + tid] = sum / static_cast<float>(hw);
+    if (tid < np) y[p0 + tid] = MAX ? acc : acc / static_cast<float>(hw);
 }
 
 __global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, int64_t outer,
@@ -249,9 +287,51 @@ int tbn_hip_global_avgpool2d(const float* x, int64_t n, int64_t c, int64_t h, in
     if (n * c == 0) return tbn_hip::ok();
     TBN_REQUIRE(x && y, TBN_INVALID_ARGUMENT, "null pointer");
     TBN_DEVICE_GUARD();
-    hipLaunchKernelGGL(global_avgpool_kernel, dim3(tbn_hip::ceil_div(n * c, 64)), dim3(256), 0,
+    hipLaunchKernelGGL(global_pool_kernel<false>, dim3(tbn_hip::ceil_div(n * c, 64)), dim3(256), 0,
                        tbn_hip::stream_of(stream), x, n * c, h * w, y);
     return tbn_hip::check_launch("global_avgpool2d");
+}
+
+int tbn_hip_global_maxpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, float* y,
+                             tbn_stream_t stream) {
+    TBN_REQUIRE(n >= 0 && c >= 0 && h > 0 && w > 0, TBN_INVALID_SHAPE, "invalid input shape");
+    if (n * c == 0) return tbn_hip::ok();
+    TBN_REQUIRE(x && y, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    hipLaunchKernelGGL(global_pool_kernel<true>, dim3(tbn_hip::ceil_div(n * c, 64)), dim3(256), 0,
+                       tbn_hip::stream_of(stream), x, n * c, h * w, y);
+    return tbn_hip::check_launch("global_maxpool2d");
+}
+
+int tbn_hip_avgpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, int64_t kh, int64_t kw, int64_t sh,
+                      int64_t sw, int64_t ph, int64_t pw, int64_t dh, int64_t dw, int ceil_mode,
+                      int count_include_pad, float* y, int64_t* out_hw, tbn_stream_t stream) {
+    TBN_REQUIRE(n >= 0 && c >= 0 && h > 0 && w > 0, TBN_INVALID_SHAPE, "invalid input shape");
+    TBN_REQUIRE(kh > 0 && kw > 0 && sh > 0 && sw > 0 && dh > 0 && dw > 0 && ph >= 0 && pw >= 0,
+                TBN_INVALID_ARGUMENT, "invalid pooling parameters");
+    // pooling.cpp:97-104: the output size does not involve the dilation
+    int64_t OH, OW;
+    if (ceil_mode) {
+        OH = (h + 2 * ph - kh + sh - 1) / sh + 1;
+        OW = (w + 2 * pw - kw + sw - 1) / sw + 1;
+    } else {
+        OH = (h + 2 * ph - kh) / sh + 1;
+        OW = (w + 2 * pw - kw) / sw + 1;
+    }
+    TBN_REQUIRE(OH > 0 && OW > 0, TBN_INVALID_SHAPE, "invalid pooled output size");
+    if (out_hw) { out_hw[0] = OH; out_hw[1] = OW; }
+    if (!y || n * c == 0) return tbn_hip::ok();
+    TBN_REQUIRE(x != nullptr, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_DEVICE_GUARD();
+    TBN_REQUIRE(h * w < (1LL << 31) && OH * OW < (1LL << 31) && kh * kw < (1LL << 31), TBN_INVALID_SHAPE,
+                "pooling plane too large");
+    hipLaunchKernelGGL(avgpool2d_kernel,
+                       dim3(static_cast<unsigned>(tbn_hip::ceil_div(OH * OW, kThreads)),
+                            static_cast<unsigned>(std::min<int64_t>(n * c, 65535))),
+                       dim3(kThreads), 0, tbn_hip::stream_of(stream), x, n * c, int(h), int(w), int(OH), int(OW),
+                       int(kh), int(kw), int(sh), int(sw), int(ph), int(pw), int(dh), int(dw),
+                       count_include_pad ? 1 : 0, y);
+    return tbn_hip::check_launch("avgpool2d");
 }
 
 int tbn_hip_add(const float* a, const float* b, int64_t outer, int64_t inner, int64_t rest,

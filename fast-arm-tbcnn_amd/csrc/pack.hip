@@ -9,6 +9,8 @@
 // one column) so each thread issues one aligned store.  Weight packing runs
 // once per Session, so these kernels favour simple coalesced reads over
 // tiling.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace {
@@ -81,12 +83,36 @@ struct FloatGE0 {
     __device__ bool neg(int64_t idx) const { return !(p[idx] >= 0.0f); }
 };
 
+// The Session's rule for a Gemm weight tensor it did not pack in advance
+// (model.hpp:765-845): w >= 0 when every sampled value is one of -1, 0, +1,
+// +-0.999, else w > 0.  `ge` is decided per block before packing.
+struct FloatSampled {
+    const float* p;
+    bool ge;
+    __device__ bool neg(int64_t idx) const { return ge ? !(p[idx] >= 0.0f) : !(p[idx] > 0.0f); }
+};
+
+// The reference's sampled check (model.hpp:773-781): elements 0, step,
+// 2*step, ... of the tensor in memory order, step = max(1, elems / 1000).
+__device__ bool sampled_binary_block(const float* w, int64_t elems) {
+    const int64_t step = elems / 1000 > 1 ? elems / 1000 : 1;
+    bool bad = false;
+    for (int64_t i = threadIdx.x * step; i < elems; i += static_cast<int64_t>(blockDim.x) * step) {
+        const float v = w[i];
+        bad |= !(v == -1.0f || v == 1.0f || v == 0.0f || v == 0.999f || v == -0.999f);
+    }
+    return !__syncthreads_or(bad);
+}
+
 // Word (n, wi) holds k = 32*wi .. 32*wi+31 of column n.  For layout KN the
 // thread index runs fastest over n so reads of W[k, :] coalesce; for NK it
 // runs fastest over wi so each thread reads 32 contiguous weights of row n.
+// FloatSampled sources decide their rule first (all threads of the block take
+// part in that barrier).
 template <class Src>
 __global__ void pack_binary_kernel(Src src, int64_t K, int64_t N, int layout, int64_t K_pad,
                                    int64_t N_pad, uint32_t* __restrict__ packed) {
+    if constexpr (std::is_same_v<Src, FloatSampled>) src.ge = sampled_binary_block(src.p, K * N);
     const int64_t words_per_col = K_pad / 32;
     const int64_t total = N_pad * words_per_col;
     for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total;
@@ -287,7 +313,8 @@ int tbn_hip_quantize_pack_binary_f32(const float* w, int64_t K, int64_t N, int l
     int rc = check_pack_dims(K, N, layout, K_pad, N_pad, 64);
     if (rc) return rc;
     TBN_REQUIRE(N_pad % 8 == 0, TBN_INVALID_SHAPE, "N_pad must be a multiple of 8");
-    TBN_REQUIRE(sign_rule == TBN_SIGN_GT_THRESHOLD || sign_rule == TBN_SIGN_GE_ZERO,
+    TBN_REQUIRE(sign_rule == TBN_SIGN_GT_THRESHOLD || sign_rule == TBN_SIGN_GE_ZERO ||
+                    sign_rule == TBN_SIGN_GEMM_SAMPLED,
                 TBN_INVALID_ARGUMENT, "unknown sign rule");
     TBN_REQUIRE(packed && (K * N == 0 || w), TBN_INVALID_ARGUMENT, "null pointer");
     TBN_DEVICE_GUARD();
@@ -298,9 +325,12 @@ int tbn_hip_quantize_pack_binary_f32(const float* w, int64_t K, int64_t N, int l
         hipLaunchKernelGGL(pack_binary_kernel<FloatGT>, dim3(grid_for(words)), dim3(kThreads), 0,
                            stream_of(stream), FloatGT{w, threshold}, K, N, layout, K_pad, N_pad,
                            out);
-    else
+    else if (sign_rule == TBN_SIGN_GE_ZERO)
         hipLaunchKernelGGL(pack_binary_kernel<FloatGE0>, dim3(grid_for(words)), dim3(kThreads), 0,
                            stream_of(stream), FloatGE0{w}, K, N, layout, K_pad, N_pad, out);
+    else
+        hipLaunchKernelGGL(pack_binary_kernel<FloatSampled>, dim3(grid_for(words)), dim3(kThreads), 0,
+                           stream_of(stream), FloatSampled{w, false}, K, N, layout, K_pad, N_pad, out);
     return check_launch("quantize_pack_binary_f32");
 }
 

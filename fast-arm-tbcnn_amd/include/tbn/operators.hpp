@@ -158,6 +158,11 @@ Tensor gemm(const Tensor& A, const Tensor& B, const Tensor* C = nullptr, float a
             float beta = 0.0f, bool transA = false, bool transB = false);
 // pooling.cpp:10-80 (floor or ceil output size, padding skipped).
 Tensor maxpool2d(const Tensor& input, const Pool2DParams& params = Pool2DParams());
+// pooling.cpp:83-148 (taps outside the image skipped, or counted as zeros
+// with count_include_pad).
+Tensor avgpool2d(const Tensor& input, const Pool2DParams& params = Pool2DParams());
+// [N, C, H, W] -> [N, C, 1, 1] (pooling.cpp:151-181).
+Tensor global_maxpool2d(const Tensor& input);
 // [N, C, H, W] -> [N, C, 1, 1] (pooling.cpp:184-216).
 Tensor global_avgpool2d(const Tensor& input);
 // max(x, 0) (model.hpp:1166-1171).

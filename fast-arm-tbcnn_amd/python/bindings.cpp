@@ -456,6 +456,20 @@ PYBIND11_MODULE(_tbn, m) {
           py::arg("input"), py::arg("kernel") = std::vector<int64_t>{2, 2},
           py::arg("stride") = std::vector<int64_t>{2, 2}, py::arg("pad") = std::vector<int64_t>{0, 0},
           py::arg("ceil_mode") = false);
+    m.def("avgpool2d",
+          [](const py::object& x, std::vector<int64_t> kernel, std::vector<int64_t> stride, std::vector<int64_t> pad,
+             bool ceil_mode, bool count_include_pad) {
+              TBN_CHECK(kernel.size() == 2 && stride.size() == 2 && pad.size() == 2, InvalidArgumentError,
+                        "kernel, stride and pad take two values");
+              Pool2DParams p(kernel[0], kernel[1], stride[0], stride[1], pad[0], pad[1]);
+              p.ceil_mode = ceil_mode;
+              p.count_include_pad = count_include_pad;
+              return avgpool2d(as_tensor(x), p);
+          },
+          py::arg("input"), py::arg("kernel") = std::vector<int64_t>{2, 2},
+          py::arg("stride") = std::vector<int64_t>{2, 2}, py::arg("pad") = std::vector<int64_t>{0, 0},
+          py::arg("ceil_mode") = false, py::arg("count_include_pad") = false);
+    m.def("global_maxpool2d", [](const py::object& x) { return global_maxpool2d(as_tensor(x)); });
     m.def("global_avgpool2d", [](const py::object& x) { return global_avgpool2d(as_tensor(x)); });
     m.def("relu", [](const py::object& x) { return relu(as_tensor(x)); });
     m.def("add", [](const py::object& a, const py::object& b) { return add(as_tensor(a), as_tensor(b)); });

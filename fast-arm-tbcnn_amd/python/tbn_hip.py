@@ -28,6 +28,7 @@ LAYOUT_KN = 0
 LAYOUT_NK = 1
 SIGN_GT_THRESHOLD = 0
 SIGN_GE_ZERO = 1
+SIGN_GEMM_SAMPLED = 2
 EPI_NONE = 0
 EPI_RELU = 1
 EPI_BIAS_THEN_SCALE = 2
@@ -89,6 +90,9 @@ _SIGNATURES = {
     "tbn_hip_maxpool2d": ([_P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P,
                            ctypes.POINTER(ctypes.c_int64), _P], _I32),
     "tbn_hip_global_avgpool2d": ([_P, _I64, _I64, _I64, _I64, _P, _P], _I32),
+    "tbn_hip_global_maxpool2d": ([_P, _I64, _I64, _I64, _I64, _P, _P], _I32),
+    "tbn_hip_avgpool2d": ([_P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
+                           _P, ctypes.POINTER(ctypes.c_int64), _P], _I32),
     "tbn_hip_add": ([_P, _P, _I64, _I64, _I64, _I64, _I32, _P, _P], _I32),
     "tbn_hip_relu": ([_P, _I64, _P, _P], _I32),
     "tbn_hip_conv2d_depthwise": ([_P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P, _P], _I32),

@@ -142,7 +142,10 @@ Conv2DParams conv_params(const ModelNode& node, const Shape& w) {
 
 // Pool2DParams as execute_maxpool reads them (model.hpp:577-628): strides
 // default to the kernel size.
-Pool2DParams pool_params(const ModelNode& node) {
+// MaxPool (model.hpp:578-629) and AveragePool (model.hpp:632-682) attributes:
+// strides default to the kernel, pads read as [top, left, ...]; MaxPool reads
+// ceil_mode, AveragePool count_include_pad (and never ceil_mode).
+Pool2DParams pool_params(const ModelNode& node, bool average = false) {
     Pool2DParams p;
     if (auto a = find_attr(node, "kernel_shape"); a && a->is_ints() && a->as_ints().size() >= 2) {
         p.kernel_h = a->as_ints()[0];
@@ -161,7 +164,11 @@ Pool2DParams pool_params(const ModelNode& node) {
         p.pad_h = a->as_ints()[0];
         p.pad_w = a->as_ints()[1];
     }
-    if (auto a = find_attr(node, "ceil_mode"); a && a->is_int()) p.ceil_mode = a->as_int() != 0;
+    if (average) {
+        if (auto a = find_attr(node, "count_include_pad"); a && a->is_int()) p.count_include_pad = a->as_int() != 0;
+    } else if (auto a = find_attr(node, "ceil_mode"); a && a->is_int()) {
+        p.ceil_mode = a->as_int() != 0;
+    }
     return p;
 }
 
@@ -178,7 +185,9 @@ enum class OpKind {
     Relu,
     TernaryAct,
     MaxPool,
+    AvgPool,
     GlobalAvgPool,
+    GlobalMaxPool,
     Elementwise,
     View,
 };
@@ -203,6 +212,7 @@ struct Op {
     const float* scale = nullptr;  // per-channel scale (device)
     const float* w = nullptr;      // fp32 weights (device)
     const float* bias = nullptr;   // device
+    int bias_value = -1;           // or a bias computed / supplied at run time
     // gemm
     int64_t M = 0, K = 0, N = 0;
     float alpha = 1.0f, beta = 0.0f;
@@ -210,6 +220,7 @@ struct Op {
     const float* cin = nullptr;    // constant addend (device) or null
     int cin_value = -1;            // or an activation addend
     int cin_1d = 0;
+    int dyn_b = -1;                // quantized Gemm whose B is packed on every run
     // pooling / elementwise
     Pool2DParams pool;
     int64_t outer = 0, inner = 0, rest = 0;
@@ -334,6 +345,19 @@ struct TBNModel::Session::Impl {
         return packed.emplace(key, pack_binary_weights(device_init(wname), nk, rule == 2)).first->second;
     }
 
+    // The packed-bits buffer of a quantized Gemm whose B is not an initializer
+    // (filled by the op itself on every run).
+    const PackedWeights& dynamic_binary(const std::string& node_name, int64_t K, int64_t N) {
+        PackedWeights pw;
+        pw.kind = PackedWeights::Kind::Binary;
+        pw.K = K;
+        pw.N = N;
+        pw.K_pad = detail::ceil_to(K, 128);
+        pw.N_pad = detail::ceil_to(N, 8);
+        pw.bits = Tensor::empty({pw.N_pad * pw.K_pad / 8}, DataType::UINT8, DeviceType::HIP);
+        return packed.insert_or_assign(node_name + "#dyn", std::move(pw)).first->second;
+    }
+
     const PackedWeights& packed_ternary(const std::string& wname, bool nk) {
         const std::string key = wname + "#t" + std::to_string(nk);
         auto it = packed.find(key);
@@ -432,12 +456,19 @@ struct TBNModel::Session::Impl {
         const int64_t OW = (xs.dims[3] + 2 * p.pad_w - p.dilation_w * (ws.dims[3] - 1) - 1) / p.stride_w + 1;
         TBN_CHECK(OH > 0 && OW > 0, InvalidShapeError, "Conv '" + node.name + "': invalid output dimensions");
         if (node.inputs.size() >= 3 && !node.inputs[2].empty()) {
+            // any value of the graph, as the reference reads it (model.hpp:207-214)
             const int bi = lookup(node.inputs[2], node.name);
-            TBN_CHECK(values[bi].is_const, NotImplementedError, "Conv '" + node.name + "': bias must be an initializer");
             TBN_CHECK(values[bi].shape.size() == ws.dims[0], InvalidShapeError,
                       "Conv '" + node.name + "': bias size must equal the output channels");
-            op.bias = const_f32(bi);
-            op.bias_name = node.inputs[2];
+            if (values[bi].is_const) {
+                op.bias = const_f32(bi);
+                op.bias_name = node.inputs[2];
+            } else {
+                TBN_CHECK(values[bi].dtype == DataType::FLOAT32, InvalidArgumentError,
+                          "Conv '" + node.name + "': bias must be FLOAT32");
+                op.bias_value = bi;
+                op.in.push_back(bi);
+            }
         }
         op.weight_name = wname;
         const bool depthwise = p.groups > 1 && ws.dims[1] == 1;
@@ -604,12 +635,19 @@ struct TBNModel::Session::Impl {
         const bool quantized = quant && quantize_allowed(node) && !matmul && values[bi].dtype == DataType::FLOAT32 &&
                                !op.transA && !op.transB;
         if (quantized) {
-            TBN_CHECK(values[bi].is_const, NotImplementedError, "Gemm '" + node.name + "': B must be an initializer");
             op.kind = OpKind::GemmQuant;
             const std::string& bname = node.inputs[1];
-            // already binary: signs w >= 0 (model.hpp:790-841); otherwise
-            // quantize_to_binary (w > 0) (model.hpp:842-845); scale 1 either way.
-            op.pw = &packed_binary(bname, false, gemm_already_binary(bname) ? 2 : 1);
+            if (values[bi].is_const) {
+                // already binary: signs w >= 0 (model.hpp:790-841); otherwise
+                // quantize_to_binary (w > 0) (model.hpp:842-845); scale 1 either way.
+                op.pw = &packed_binary(bname, false, gemm_already_binary(bname) ? 2 : 1);
+            } else {
+                // B computed or supplied at run time: the same test and packing
+                // on the device on every run (TBN_SIGN_GEMM_SAMPLED).
+                op.pw = &dynamic_binary(node.name, op.K, op.N);
+                op.dyn_b = bi;
+                op.in.push_back(bi);
+            }
             // then result * alpha + beta * C (model.hpp:847-870)
         } else {
             op.kind = OpKind::GemmF32;
@@ -634,19 +672,27 @@ struct TBNModel::Session::Impl {
         op.node = node.name;
         op.in = {xi};
         Shape out = values[xi].shape;
-        if (kind == OpKind::MaxPool || kind == OpKind::GlobalAvgPool) {
+        if (kind == OpKind::MaxPool || kind == OpKind::AvgPool || kind == OpKind::GlobalAvgPool ||
+            kind == OpKind::GlobalMaxPool) {
             TBN_CHECK(out.rank() == 4, InvalidShapeError, node.op_type + " input must be 4D (NCHW)");
         }
-        if (kind == OpKind::MaxPool) {
-            op.pool = pool_params(node);
+        if (kind == OpKind::MaxPool || kind == OpKind::AvgPool) {
+            op.pool = pool_params(node, kind == OpKind::AvgPool);
             const auto& d = out.dims;
+            const Pool2DParams& p = op.pool;
             int64_t hw[2];
-            check_status(tbn_hip_maxpool2d(nullptr, d[0], d[1], d[2], d[3], op.pool.kernel_h, op.pool.kernel_w,
-                                           op.pool.stride_h, op.pool.stride_w, op.pool.pad_h, op.pool.pad_w, 1, 1,
-                                           op.pool.ceil_mode, nullptr, hw, nullptr),
-                         ("MaxPool '" + node.name + "'").c_str());
+            const std::string what = node.op_type + " '" + node.name + "'";
+            if (kind == OpKind::MaxPool)
+                check_status(tbn_hip_maxpool2d(nullptr, d[0], d[1], d[2], d[3], p.kernel_h, p.kernel_w, p.stride_h,
+                                               p.stride_w, p.pad_h, p.pad_w, 1, 1, p.ceil_mode, nullptr, hw, nullptr),
+                             what.c_str());
+            else
+                check_status(tbn_hip_avgpool2d(nullptr, d[0], d[1], d[2], d[3], p.kernel_h, p.kernel_w, p.stride_h,
+                                               p.stride_w, p.pad_h, p.pad_w, 1, 1, 0, p.count_include_pad, nullptr,
+                                               hw, nullptr),
+                             what.c_str());
             out = Shape{d[0], d[1], hw[0], hw[1]};
-        } else if (kind == OpKind::GlobalAvgPool) {
+        } else if (kind == OpKind::GlobalAvgPool || kind == OpKind::GlobalMaxPool) {
             out = Shape{out.dims[0], out.dims[1], 1, 1};
         } else if (kind == OpKind::TernaryAct) {
             op.scalar = 0.5f;
@@ -723,7 +769,9 @@ struct TBNModel::Session::Impl {
             return lower_unary(node, ternary ? OpKind::TernaryAct : OpKind::Relu);
         }
         if (t == "MaxPool") return lower_unary(node, OpKind::MaxPool);
+        if (t == "AveragePool" || t == "AvgPool") return lower_unary(node, OpKind::AvgPool);
         if (t == "GlobalAveragePool" || t == "GlobalAvgPool") return lower_unary(node, OpKind::GlobalAvgPool);
+        if (t == "GlobalMaxPool") return lower_unary(node, OpKind::GlobalMaxPool);
         if (t == "Flatten") {
             const int xi = lookup(node.inputs[0], node.name);
             int64_t axis = 1;
@@ -807,7 +855,7 @@ struct TBNModel::Session::Impl {
             if (p < 0) continue;
             Op& c = ops[p];
             const bool conv = c.kind == OpKind::ConvF32 || c.kind == OpKind::ConvQuant || c.kind == OpKind::ConvDepthwise;
-            if (!conv || c.residual >= 0 || (c.flags & (TBN_EPI_RELU | TBN_EPI_MAXPOOL2X2)) ||
+            if (!conv || c.residual >= 0 || c.bias_value >= 0 || (c.flags & (TBN_EPI_RELU | TBN_EPI_MAXPOOL2X2)) ||
                 sole_reader(c.out) != static_cast<int>(i) || static_cast<int64_t>(bn.bn_k.size()) != c.desc.m)
                 continue;
             const int64_t M = c.desc.m;
@@ -1037,7 +1085,7 @@ struct TBNModel::Session::Impl {
             if (op.dead || op.kind != OpKind::ConvQuant || op.groups > 1 || !op.conv_w) continue;
             check_status(tbn_hip_conv2d_tune_prepacked(
                              op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY : TBN_WEIGHTS_TERNARY,
-                             fp(op.in[0]), &op.desc, op.conv_w->typed_data<uint8_t>(), op.scale, 1.0f, op.bias,
+                             fp(op.in[0]), &op.desc, op.conv_w->typed_data<uint8_t>(), op.scale, 1.0f, bias_of(op),
                              op.residual >= 0 ? fp(op.residual) : nullptr, op.flags, fp(op.out), s),
                          ("tuning node '" + op.node + "'").c_str());
         }
@@ -1055,6 +1103,8 @@ struct TBNModel::Session::Impl {
 
     // ---- execution ---------------------------------------------------------------------
 
+    const float* bias_of(const Op& op) { return op.bias ? op.bias : (op.bias_value >= 0 ? fp(op.bias_value) : nullptr); }
+
     // A grouped conv with more than one input channel per group: one dense
     // conv per group on channel slices of the input and output.
     void launch_grouped(Op& op, tbn_stream_t s, const std::string& what) {
@@ -1066,7 +1116,7 @@ struct TBNModel::Session::Impl {
             op.desc, G, fp(op.in[0]), fp(op.out), op.workspace >= 0 ? fp(op.workspace) : nullptr,
             [&](int64_t g, const float* xg, const tbn_conv2d_desc& dg, float* yg) {
                 const float* sc = op.scale ? op.scale + g * Mg : nullptr;
-                const float* bi = op.bias ? op.bias + g * Mg : nullptr;
+                const float* bi = bias_of(op) ? bias_of(op) + g * Mg : nullptr;
                 if (op.kind == OpKind::ConvF32) {
                     check_status(tbn_hip_conv2d_f32(xg, &dg, op.w + g * w_per_group, bi, op.flags, yg, s), what.c_str());
                 } else if (!op.group_conv_w.empty()) {
@@ -1092,11 +1142,11 @@ struct TBNModel::Session::Impl {
                 return;
             case OpKind::ConvF32:
                 if (op.groups > 1) return launch_grouped(op, s, what);
-                check_status(tbn_hip_conv2d_f32(fp(op.in[0]), &op.desc, op.w, op.bias, op.flags, fp(op.out), s),
+                check_status(tbn_hip_conv2d_f32(fp(op.in[0]), &op.desc, op.w, bias_of(op), op.flags, fp(op.out), s),
                              what.c_str());
                 return;
             case OpKind::ConvDepthwise:
-                check_status(tbn_hip_conv2d_depthwise(fp(op.in[0]), &op.desc, op.w, op.scale, 1.0f, op.bias,
+                check_status(tbn_hip_conv2d_depthwise(fp(op.in[0]), &op.desc, op.w, op.scale, 1.0f, bias_of(op),
                                                       op.residual >= 0 ? fp(op.residual) : nullptr, op.flags,
                                                       fp(op.out), s),
                              what.c_str());
@@ -1113,7 +1163,7 @@ struct TBNModel::Session::Impl {
                                      op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY
                                                                                 : TBN_WEIGHTS_TERNARY,
                                      fp(op.in[0]), &op.desc, op.conv_w->typed_data<uint8_t>(), op.scale, 1.0f,
-                                     op.bias, op.residual >= 0 ? fp(op.residual) : nullptr, op.flags, fp(op.out),
+                                     bias_of(op), op.residual >= 0 ? fp(op.residual) : nullptr, op.flags, fp(op.out),
                                      s),
                                  what.c_str());
                     return;
@@ -1121,11 +1171,18 @@ struct TBNModel::Session::Impl {
                 check_status(tbn_hip_conv2d_f32_quantized(
                                  op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY : TBN_WEIGHTS_TERNARY,
                                  fp(op.in[0]), &op.desc, op.pw->bits.typed_data<uint8_t>(), op.pw->K_pad,
-                                 op.pw->N_pad, op.scale, 1.0f, op.bias, op.residual >= 0 ? fp(op.residual) : nullptr,
+                                 op.pw->N_pad, op.scale, 1.0f, bias_of(op), op.residual >= 0 ? fp(op.residual) : nullptr,
                                  op.flags, fp(op.out), s),
                              what.c_str());
                 return;
             case OpKind::GemmQuant: {
+                if (op.dyn_b >= 0)
+                    check_status(tbn_hip_quantize_pack_binary_f32(fp(op.dyn_b), op.K, op.N, TBN_LAYOUT_KN,
+                                                                  TBN_SIGN_GEMM_SAMPLED, 0.0f, op.pw->K_pad,
+                                                                  op.pw->N_pad,
+                                                                  const_cast<uint8_t*>(op.pw->bits.typed_data<uint8_t>()),
+                                                                  s),
+                                 what.c_str());
                 const float* cin = op.cin ? op.cin : (op.cin_value >= 0 ? fp(op.cin_value) : nullptr);
                 check_status(tbn_hip_gemm_f32_quantized(
                                  op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY : TBN_WEIGHTS_TERNARY,
@@ -1164,9 +1221,24 @@ struct TBNModel::Session::Impl {
                              what.c_str());
                 return;
             }
+            case OpKind::AvgPool: {
+                const auto& d = values[op.in[0]].shape.dims;
+                const Pool2DParams& p = op.pool;
+                check_status(tbn_hip_avgpool2d(fp(op.in[0]), d[0], d[1], d[2], d[3], p.kernel_h, p.kernel_w,
+                                               p.stride_h, p.stride_w, p.pad_h, p.pad_w, 1, 1, 0,
+                                               p.count_include_pad, fp(op.out), nullptr, s),
+                             what.c_str());
+                return;
+            }
             case OpKind::GlobalAvgPool: {
                 const auto& d = values[op.in[0]].shape.dims;
                 check_status(tbn_hip_global_avgpool2d(fp(op.in[0]), d[0], d[1], d[2], d[3], fp(op.out), s),
+                             what.c_str());
+                return;
+            }
+            case OpKind::GlobalMaxPool: {
+                const auto& d = values[op.in[0]].shape.dims;
+                check_status(tbn_hip_global_maxpool2d(fp(op.in[0]), d[0], d[1], d[2], d[3], fp(op.out), s),
                              what.c_str());
                 return;
             }

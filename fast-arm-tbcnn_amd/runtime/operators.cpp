@@ -412,14 +412,46 @@ Tensor maxpool2d(const Tensor& input, const Pool2DParams& p) {
     const auto& d = input.shape().dims;
     int64_t hw[2] = {0, 0};
     check_status(tbn_hip_maxpool2d(nullptr, d[0], d[1], d[2], d[3], p.kernel_h, p.kernel_w, p.stride_h,
-                                   p.stride_w, p.pad_h, p.pad_w, 1, 1, p.ceil_mode, nullptr, hw, stream()),
+                                   p.stride_w, p.pad_h, p.pad_w, p.dilation_h, p.dilation_w, p.ceil_mode, nullptr,
+                                   hw, stream()),
                  "maxpool2d");
     Tensor x = on_device(input);
     Tensor y = Tensor::empty({d[0], d[1], hw[0], hw[1]}, DataType::FLOAT32, DeviceType::HIP);
     check_status(tbn_hip_maxpool2d(x.typed_data<float>(), d[0], d[1], d[2], d[3], p.kernel_h, p.kernel_w,
-                                   p.stride_h, p.stride_w, p.pad_h, p.pad_w, 1, 1, p.ceil_mode,
-                                   y.typed_data<float>(), nullptr, stream()),
+                                   p.stride_h, p.stride_w, p.pad_h, p.pad_w, p.dilation_h, p.dilation_w,
+                                   p.ceil_mode, y.typed_data<float>(), nullptr, stream()),
                  "maxpool2d");
+    return deliver(y, input);
+}
+
+Tensor avgpool2d(const Tensor& input, const Pool2DParams& p) {
+    TBN_CHECK(input.shape().rank() == 4, InvalidShapeError,
+              "AvgPool2D input must be 4D (NCHW), got " + shape_to_string(input.shape()));
+    TBN_CHECK(input.dtype() == DataType::FLOAT32, InvalidArgumentError, "AvgPool2D requires float32 input");
+    const auto& d = input.shape().dims;
+    int64_t hw[2] = {0, 0};
+    check_status(tbn_hip_avgpool2d(nullptr, d[0], d[1], d[2], d[3], p.kernel_h, p.kernel_w, p.stride_h, p.stride_w,
+                                   p.pad_h, p.pad_w, p.dilation_h, p.dilation_w, p.ceil_mode, p.count_include_pad,
+                                   nullptr, hw, stream()),
+                 "avgpool2d");
+    Tensor x = on_device(input);
+    Tensor y = Tensor::empty({d[0], d[1], hw[0], hw[1]}, DataType::FLOAT32, DeviceType::HIP);
+    check_status(tbn_hip_avgpool2d(x.typed_data<float>(), d[0], d[1], d[2], d[3], p.kernel_h, p.kernel_w, p.stride_h,
+                                   p.stride_w, p.pad_h, p.pad_w, p.dilation_h, p.dilation_w, p.ceil_mode,
+                                   p.count_include_pad, y.typed_data<float>(), nullptr, stream()),
+                 "avgpool2d");
+    return deliver(y, input);
+}
+
+Tensor global_maxpool2d(const Tensor& input) {
+    TBN_CHECK(input.shape().rank() == 4, InvalidShapeError, "GlobalMaxPool2D input must be 4D (NCHW)");
+    require_float(input, "GlobalMaxPool2D input");
+    const auto& d = input.shape().dims;
+    Tensor x = on_device(input);
+    Tensor y = Tensor::empty({d[0], d[1], 1, 1}, DataType::FLOAT32, DeviceType::HIP);
+    check_status(tbn_hip_global_maxpool2d(x.typed_data<float>(), d[0], d[1], d[2], d[3], y.typed_data<float>(),
+                                          stream()),
+                 "global_maxpool2d");
     return deliver(y, input);
 }
 

@@ -72,8 +72,13 @@ enum tbn_layout { TBN_LAYOUT_KN = 0, TBN_LAYOUT_NK = 1 };
  *   TBN_SIGN_GT_THRESHOLD  +1 iff w > threshold; 0, -0.0, NaN -> -1
  *                          (quantize_to_binary, quantized_gemm_neon.cpp:553)
  *   TBN_SIGN_GE_ZERO       +1 iff w >= 0; 0, -0.0 -> +1, NaN -> -1
- *                          (Session sign extraction, model.hpp:433,803) */
-enum tbn_sign_rule { TBN_SIGN_GT_THRESHOLD = 0, TBN_SIGN_GE_ZERO = 1 };
+ *                          (Session sign extraction, model.hpp:433,803)
+ *   TBN_SIGN_GEMM_SAMPLED  the Session's Gemm rule decided on the device:
+ *                          GE_ZERO when the sampled elements 0, s, 2s, ... of
+ *                          W in memory order (s = max(1, K*N/1000)) are all
+ *                          -1, 0, +1 or +-0.999, else GT_THRESHOLD at 0
+ *                          (model.hpp:765-845); threshold is ignored */
+enum tbn_sign_rule { TBN_SIGN_GT_THRESHOLD = 0, TBN_SIGN_GE_ZERO = 1, TBN_SIGN_GEMM_SAMPLED = 2 };
 
 /* Epilogue flags for the GEMM / conv entry points. */
 enum tbn_epilogue {
@@ -346,6 +351,18 @@ int tbn_hip_maxpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w
                       int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
                       int64_t dh, int64_t dw, int ceil_mode, float* y, int64_t* out_hw,
                       tbn_stream_t stream);
+/* AvgPool2D (tbn::avgpool2d, pooling.cpp:83-148): sum of the window's taps
+ * inside the image in window order, divided by their count (taps outside the
+ * image also counted with count_include_pad; 0 for an empty count).  Output
+ * size as tbn_hip_maxpool2d; out_hw and a NULL y work the same way. */
+int tbn_hip_avgpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, int64_t kh,
+                      int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, int64_t dh,
+                      int64_t dw, int ceil_mode, int count_include_pad, float* y, int64_t* out_hw,
+                      tbn_stream_t stream);
+/* GlobalMaxPool2D (tbn::global_maxpool2d, pooling.cpp:151-181), y [n, c]:
+ * -inf start, running max in memory order (NaN ignored). */
+int tbn_hip_global_maxpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, float* y,
+                             tbn_stream_t stream);
 /* GlobalAvgPool2D (tbn::global_avgpool2d, pooling.cpp:184-216), y [n, c]. */
 int tbn_hip_global_avgpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w,
                              float* y, tbn_stream_t stream);

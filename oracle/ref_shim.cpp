@@ -1,5 +1,6 @@
 // C entry points over the reference's own fp32 operators (tbn::conv2d,
-// tbn::gemm, tbn::maxpool2d, tbn::global_avgpool2d), compiled from the
+// tbn::gemm, tbn::maxpool2d, tbn::avgpool2d, tbn::global_maxpool2d,
+// tbn::global_avgpool2d), compiled from the
 // reference sources by `make ref` into oracle/_ref/.  TEST INFRASTRUCTURE
 // ONLY: tests/ use it to check the CPU oracle's restatements of these
 // operators bit for bit.  Only the fp32 operator sources are built: the
@@ -62,6 +63,32 @@ int ref_maxpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, in
         out_hw[0] = r.shape().dims[2];
         out_hw[1] = r.shape().dims[3];
         if (y) copy_out(r, y);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_avgpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, int64_t kh, int64_t kw,
+                  int64_t sh, int64_t sw, int64_t ph, int64_t pw, int ceil_mode, int count_include_pad, float* y,
+                  int64_t* out_hw) {
+    try {
+        tbn::Pool2DParams p(kh, kw, sh, sw, ph, pw);
+        p.ceil_mode = ceil_mode != 0;
+        p.count_include_pad = count_include_pad != 0;
+        tbn::Tensor r = tbn::avgpool2d(host_tensor(x, {n, c, h, w}), p);
+        out_hw[0] = r.shape().dims[2];
+        out_hw[1] = r.shape().dims[3];
+        if (y) copy_out(r, y);
+        return 0;
+    } catch (const std::exception&) {
+        return -1;
+    }
+}
+
+int ref_global_maxpool2d(const float* x, int64_t n, int64_t c, int64_t h, int64_t w, float* y) {
+    try {
+        copy_out(tbn::global_maxpool2d(host_tensor(x, {n, c, h, w})), y);
         return 0;
     } catch (const std::exception&) {
         return -1;

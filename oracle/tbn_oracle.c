@@ -419,6 +419,60 @@ int tbo_maxpool2d(const float* x, int64_t N, int64_t C, int64_t H, int64_t W,
     return TBO_OK;
 }
 
+/* AvgPool2D: output size as MaxPool2D (no dilation term); per window the
+ * taps inside the image summed in window order and counted, taps outside
+ * counted too with count_include_pad; sum / count, or 0 for count 0.
+ * tbn-runtime/src/operators/pooling.cpp:83-148 */
+int tbo_avgpool2d(const float* x, int64_t N, int64_t C, int64_t H, int64_t W,
+                  int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                  int64_t dh, int64_t dw, int ceil_mode, int count_include_pad, float* y,
+                  int64_t* out_hw)
+{
+    int64_t OH, OW;
+    if (ceil_mode) {
+        OH = (H + 2 * ph - kh + sh - 1) / sh + 1;
+        OW = (W + 2 * pw - kw + sw - 1) / sw + 1;
+    } else {
+        OH = (H + 2 * ph - kh) / sh + 1;
+        OW = (W + 2 * pw - kw) / sw + 1;
+    }
+    if (out_hw) { out_hw[0] = OH; out_hw[1] = OW; }
+    if (!y) return TBO_OK;
+    for (int64_t nc = 0; nc < N * C; ++nc)
+        for (int64_t oh = 0; oh < OH; ++oh)
+            for (int64_t ow = 0; ow < OW; ++ow) {
+                float sum = 0.0f;
+                int count = 0;
+                for (int64_t r = 0; r < kh; ++r)
+                    for (int64_t s = 0; s < kw; ++s) {
+                        const int64_t ih = oh * sh - ph + r * dh;
+                        const int64_t iw = ow * sw - pw + s * dw;
+                        if (ih >= 0 && ih < H && iw >= 0 && iw < W) {
+                            sum += x[(nc * H + ih) * W + iw];
+                            ++count;
+                        } else if (count_include_pad) {
+                            ++count;
+                        }
+                    }
+                y[(nc * OH + oh) * OW + ow] = count > 0 ? sum / (float)count : 0.0f;
+            }
+    return TBO_OK;
+}
+
+/* GlobalMaxPool2D: -inf start, running max(acc, v) over the plane in memory
+ * order (NaN ignored; of equal -0 / +0 the first is kept).
+ * tbn-runtime/src/operators/pooling.cpp:151-181 */
+void tbo_global_maxpool2d(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, float* y)
+{
+    const int64_t hw = H * W;
+    for (int64_t nc = 0; nc < N * C; ++nc) {
+        float mx = -INFINITY;
+        for (int64_t i = 0; i < hw; ++i)
+            if (mx < x[nc * hw + i]) mx = x[nc * hw + i];
+        y[nc] = mx;
+    }
+}
+
 /* GlobalAvgPool2D: sequential fp32 sum over the plane divided by H*W.
  * tbn-runtime/src/operators/pooling.cpp:184-216 */
 void tbo_global_avgpool2d(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, float* y)

@@ -91,6 +91,11 @@ int  tbo_maxpool2d(const float* x, int64_t N, int64_t C, int64_t H, int64_t W,
                    int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
                    int64_t dh, int64_t dw, int ceil_mode, float* y, int64_t* out_hw);
 void tbo_global_avgpool2d(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, float* y);
+int  tbo_avgpool2d(const float* x, int64_t N, int64_t C, int64_t H, int64_t W,
+                   int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw,
+                   int64_t dh, int64_t dw, int ceil_mode, int count_include_pad, float* y,
+                   int64_t* out_hw);
+void tbo_global_maxpool2d(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, float* y);
 void tbo_gemm_f32_blocked(const float* A, const float* B, const float* Cin, int c_is_1d,
                           int64_t M, int64_t K, int64_t N, float alpha, float beta,
                           int transA, int transB, float* out);

@@ -297,9 +297,19 @@ def run_oracle(spec, feeds, quant, orc, record=None):
             s = a.get("strides", k)
             p = a.get("pads", [0, 0, 0, 0])
             y = orc.maxpool2d(env[n.inputs[0]], tuple(k), tuple(s), (p[0], p[1]), ceil_mode=bool(a.get("ceil_mode", 0)))
+        elif n.op in ("AveragePool", "AvgPool"):
+            # model.hpp:632-682: no ceil_mode, count_include_pad read
+            k = a.get("kernel_shape", [2, 2])
+            s = a.get("strides", k)
+            p = a.get("pads", [0, 0, 0, 0])
+            y = orc.avgpool2d(env[n.inputs[0]], tuple(k), tuple(s), (p[0], p[1]),
+                              count_include_pad=bool(a.get("count_include_pad", 0)))
         elif n.op in ("GlobalAveragePool", "GlobalAvgPool"):
             x = env[n.inputs[0]]
             y = orc.global_avgpool2d(x).reshape(x.shape[0], x.shape[1], 1, 1)
+        elif n.op == "GlobalMaxPool":
+            x = env[n.inputs[0]]
+            y = orc.global_maxpool2d(x).reshape(x.shape[0], x.shape[1], 1, 1)
         elif n.op == "Flatten":
             x = env[n.inputs[0]]
             ax = a.get("axis", 1)

@@ -175,6 +175,24 @@ def maxpool2d(x, k, s, p=(0, 0), d=(1, 1), ceil_mode=False):
     return y
 
 
+def avgpool2d(x, k, s, p=(0, 0), d=(1, 1), ceil_mode=False, count_include_pad=False):
+    x = _c(x, np.float32); N, C, H, W = x.shape
+    hw = np.zeros(2, np.int64)
+    args = [I64(N), I64(C), I64(H), I64(W), I64(k[0]), I64(k[1]), I64(s[0]), I64(s[1]),
+            I64(p[0]), I64(p[1]), I64(d[0]), I64(d[1]), ctypes.c_int(int(ceil_mode)),
+            ctypes.c_int(int(count_include_pad))]
+    lib().tbo_avgpool2d(_p(x), *args, None, _p(hw))
+    y = np.empty((N, C, int(hw[0]), int(hw[1])), np.float32)
+    lib().tbo_avgpool2d(_p(x), *args, _p(y), _p(hw))
+    return y
+
+
+def global_maxpool2d(x):
+    x = _c(x, np.float32); N, C, H, W = x.shape
+    y = np.empty((N, C), np.float32)
+    lib().tbo_global_maxpool2d(_p(x), I64(N), I64(C), I64(H), I64(W), _p(y)); return y
+
+
 def global_avgpool2d(x):
     x = _c(x, np.float32); N, C, H, W = x.shape
     y = np.empty((N, C), np.float32)

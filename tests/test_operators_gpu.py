@@ -206,3 +206,15 @@ def test_gemm_fp32(dev, tbn, on_device, tA, tB):
     args = [_dev(tbn, v) for v in (A, B, C)] if on_device else [A, B, C]
     got = _out(tbn.gemm(*args, alpha=0.5, beta=2.0, transA=tA, transB=tB), on_device)
     rm.assert_within_tolerance(got, ref, K, np.abs(A).max() * np.abs(B).max())
+
+
+@pytest.mark.parametrize("on_device", [False, True])
+def test_avgpool2d_and_global_maxpool2d(dev, tbn, orc, on_device):
+    """tbn::avgpool2d / tbn::global_maxpool2d (pooling.cpp:83-181), bitwise."""
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((2, 8, 15, 13)).astype(np.float32)
+    a = _dev(tbn, x) if on_device else x
+    y = _out(tbn.avgpool2d(a, [3, 3], [2, 2], [1, 1], False, True), on_device)
+    assert np.array_equal(y, orc.avgpool2d(x, (3, 3), (2, 2), (1, 1), count_include_pad=True))
+    g = _out(tbn.global_maxpool2d(a), on_device)
+    assert np.array_equal(g.reshape(2, 8), orc.global_maxpool2d(x))

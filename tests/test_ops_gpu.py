@@ -1,5 +1,6 @@
-"""Pooling / elementwise operators on the GPU vs the oracle.  Max, ReLU and
-the sequential-sum GlobalAvgPool are exact, so these compare bit for bit."""
+"""Pooling / elementwise operators on the GPU vs the oracle.  Max, ReLU, the
+window-order AvgPool and the sequential-sum GlobalAvgPool round exactly as
+the reference does, so these compare bit for bit."""
 import numpy as np
 import pytest
 import torch
@@ -66,6 +67,55 @@ def test_global_avgpool_bit_exact(dev, orc, shape):
     y = empty(shape[:2], torch.float32)
     tbn_hip.call("tbn_hip_global_avgpool2d", P(to_dev(x)), *shape, P(y), None)
     assert np.array_equal(host(y), orc.global_avgpool2d(x))
+
+
+def gpu_avgpool(x, k, s, p=(0, 0), ceil_mode=False, include_pad=False):
+    N, C, H, W = x.shape
+    import ctypes
+    hw = (ctypes.c_int64 * 2)()
+    args = [N, C, H, W, k[0], k[1], s[0], s[1], p[0], p[1], 1, 1, int(ceil_mode), int(include_pad)]
+    tbn_hip.call("tbn_hip_avgpool2d", None, *args, None, hw, None)
+    y = empty((N, C, hw[0], hw[1]), torch.float32)
+    tbn_hip.call("tbn_hip_avgpool2d", P(to_dev(x)), *args, P(y), hw, None)
+    return host(y)
+
+
+@pytest.mark.parametrize("k,s,p,ceil_mode,inc", [((2, 2), (2, 2), (0, 0), False, False),
+                                                 ((3, 3), (2, 2), (1, 1), False, False),
+                                                 ((3, 3), (2, 2), (1, 1), False, True),
+                                                 ((3, 3), (2, 2), (0, 0), True, False),
+                                                 ((3, 3), (2, 2), (0, 0), True, True),
+                                                 ((2, 3), (1, 2), (1, 1), False, True),
+                                                 ((7, 7), (1, 1), (0, 0), False, False)])
+def test_avgpool_bit_exact(dev, orc, k, s, p, ceil_mode, inc):
+    """tbn::avgpool2d (pooling.cpp:83-148): same window order, same count, so
+    the sums and divisions round identically."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((2, 3, 9, 8)).astype(np.float32)
+    x[1, 2, 4, 4] = np.inf
+    got = gpu_avgpool(x, k, s, p, ceil_mode, inc)
+    ref = orc.avgpool2d(x, k, s, p, ceil_mode=ceil_mode, count_include_pad=inc)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    xk = (np.arange(32) % 10).astype(np.float32).reshape(1, 2, 4, 4)
+    assert gpu_avgpool(xk, (2, 2), (2, 2))[0, 0].reshape(-1).tolist() == [2.5, 4.5, 5.5, 2.5]
+
+
+@pytest.mark.parametrize("shape", [(1, 2, 4, 4), (32, 512, 7, 7), (3, 5, 1, 1), (2, 70, 13, 11)])
+def test_global_maxpool_bit_exact(dev, orc, shape):
+    """tbn::global_maxpool2d (pooling.cpp:151-181): NaN ignored, -inf for an
+    all-NaN plane, the first of equal -0 / +0 kept."""
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(shape).astype(np.float32)
+    x[0, 0].flat[0] = np.nan
+    if shape[1] > 1:
+        x[0, 1] = 0.0
+        x[0, 1].flat[0] = -0.0
+    if shape[0] > 1:
+        x[-1, -1] = np.nan
+    y = empty(shape[:2], torch.float32)
+    tbn_hip.call("tbn_hip_global_maxpool2d", P(to_dev(x)), *shape, P(y), None)
+    ref = orc.global_maxpool2d(x)
+    assert np.array_equal(host(y).view(np.uint32), ref.view(np.uint32))
 
 
 def test_add_broadcasts_and_relu(dev):

@@ -286,6 +286,68 @@ def test_global_avgpool(orc):
     np.testing.assert_allclose(orc.global_avgpool2d(x2).reshape(-1), [x2[0, 0].mean(), x2[0, 1].mean()], rtol=1e-7)
 
 
+def test_avgpool_known_answer(orc):
+    # the reference's pooling test input (tbn-runtime/tests/test_pooling.cpp:
+    # 7-17,46-60), i % 10 over [1,2,4,4], 2x2/2: window means by hand
+    x = (np.arange(32) % 10).astype(np.float32).reshape(1, 2, 4, 4)
+    y = orc.avgpool2d(x, (2, 2), (2, 2))
+    assert y.shape == (1, 2, 2, 2)
+    assert y[0, 0].reshape(-1).tolist() == [2.5, 4.5, 5.5, 2.5]
+    assert orc.global_maxpool2d(x).reshape(-1).tolist() == [9.0, 9.0]
+
+
+def _np_avgpool(x, k, s, p, ceil_mode, include_pad):
+    """Window sums over a NaN-padded copy: NaN marks taps outside the image.
+    Integer-valued inputs keep every sum exact, so one rounding (the
+    division) is left and the comparison is exact."""
+    N, C, H, W = x.shape
+    if ceil_mode:
+        OH = (H + 2 * p[0] - k[0] + s[0] - 1) // s[0] + 1
+        OW = (W + 2 * p[1] - k[1] + s[1] - 1) // s[1] + 1
+    else:
+        OH = (H + 2 * p[0] - k[0]) // s[0] + 1
+        OW = (W + 2 * p[1] - k[1]) // s[1] + 1
+    big = np.full((N, C, OH * s[0] + k[0] + p[0], OW * s[1] + k[1] + p[1]), np.nan)
+    big[:, :, p[0]:p[0] + H, p[1]:p[1] + W] = x
+    y = np.empty((N, C, OH, OW), np.float32)
+    for oh in range(OH):
+        for ow in range(OW):
+            win = big[:, :, oh * s[0]:oh * s[0] + k[0], ow * s[1]:ow * s[1] + k[1]].reshape(N, C, -1)
+            inside = ~np.isnan(win)
+            total = np.where(inside, win, 0.0).sum(-1)
+            count = np.full((N, C), k[0] * k[1]) if include_pad else inside.sum(-1)
+            y[:, :, oh, ow] = np.where(count > 0, total.astype(np.float32) / np.maximum(count, 1).astype(np.float32), 0)
+    return y
+
+
+@pytest.mark.parametrize("k,s,p,ceil_mode,include_pad", [
+    ((2, 2), (2, 2), (0, 0), False, False), ((3, 3), (2, 2), (1, 1), False, False),
+    ((3, 3), (2, 2), (1, 1), False, True), ((3, 3), (2, 2), (0, 0), True, False),
+    ((3, 3), (2, 2), (0, 0), True, True), ((2, 3), (1, 2), (1, 1), False, True)])
+def test_avgpool_vs_numpy(orc, k, s, p, ceil_mode, include_pad):
+    rng = np.random.default_rng(16)
+    x = rng.integers(-50, 50, size=(2, 3, 9, 8)).astype(np.float32)
+    got = orc.avgpool2d(x, k, s, p, ceil_mode=ceil_mode, count_include_pad=include_pad)
+    assert np.array_equal(got, _np_avgpool(x, k, s, p, ceil_mode, include_pad))
+
+
+def test_global_maxpool_special_values(orc):
+    rng = np.random.default_rng(17)
+    x = rng.standard_normal((2, 3, 5, 6)).astype(np.float32)
+    x[0, 0, 1, 2] = np.nan
+    x[1, 2] = np.nan  # an all-NaN plane keeps the -inf start
+    y = orc.global_maxpool2d(x)
+    want = np.nanmax(np.where(np.isnan(x), -np.inf, x).reshape(2, 3, -1), axis=-1).astype(np.float32)
+    assert np.array_equal(y, want)
+    assert y[1, 2] == -np.inf
+    # equal -0 / +0: the first in memory order is kept
+    z = np.zeros((1, 2, 1, 2), np.float32)
+    z[0, 0, 0, 0] = -0.0
+    z[0, 1, 0, 1] = -0.0
+    zy = orc.global_maxpool2d(z)
+    assert np.signbit(zy[0, 0]) and not np.signbit(zy[0, 1])
+
+
 @pytest.mark.parametrize("transA,transB", [(False, False), (False, True), (True, False)])
 def test_gemm_f32_blocked(orc, transA, transB):
     rng = np.random.default_rng(15)

@@ -99,3 +99,33 @@ def test_global_avgpool_matches_reference_bitwise(orc, ref):
     assert ref.ref_global_avgpool2d(_p(x), I64(3), I64(5), I64(7), I64(7), _p(want)) == 0
     got = orc.global_avgpool2d(x)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("k,s,p,ceil,inc", [((2, 2), (2, 2), (0, 0), False, False), ((3, 3), (2, 2), (1, 1), False, True),
+                                            ((3, 3), (2, 2), (1, 1), True, False), ((3, 3), (2, 2), (0, 0), True, True),
+                                            ((2, 3), (1, 2), (1, 0), False, True)])
+def test_avgpool2d_matches_reference_bitwise(orc, ref, k, s, p, ceil, inc):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((2, 3, 13, 11)).astype(np.float32)
+    x[0, 1, 3, 4] = np.nan
+    hw = np.zeros(2, np.int64)
+    args = [I64(2), I64(3), I64(13), I64(11), I64(k[0]), I64(k[1]), I64(s[0]), I64(s[1]), I64(p[0]), I64(p[1]),
+            ctypes.c_int(int(ceil)), ctypes.c_int(int(inc))]
+    assert ref.ref_avgpool2d(_p(x), *args, None, _p(hw)) == 0
+    want = np.empty((2, 3, int(hw[0]), int(hw[1])), np.float32)
+    assert ref.ref_avgpool2d(_p(x), *args, _p(want), _p(hw)) == 0
+    got = orc.avgpool2d(x, k, s, p, ceil_mode=ceil, count_include_pad=inc)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_global_maxpool_matches_reference_bitwise(orc, ref):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((3, 5, 7, 7)).astype(np.float32)
+    x[0, 0, 2, 2] = np.nan
+    x[1, 1] = 0.0
+    x[1, 1, 0, 0] = -0.0
+    x[2, 3] = np.nan
+    want = np.empty((3, 5), np.float32)
+    assert ref.ref_global_maxpool2d(_p(x), I64(3), I64(5), I64(7), I64(7), _p(want)) == 0
+    got = orc.global_maxpool2d(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -79,6 +79,32 @@ def test_quantize_pack_binary_fused(dev, orc, rule, thr, layout):
     assert np.array_equal(host(out), orc.pack_binary(binw, K, N, layout, K_pad, N_pad))
 
 
+@pytest.mark.parametrize("K,N", [(300, 37), (64, 8), (1024, 1000)])
+@pytest.mark.parametrize("passes", [True, False])
+def test_quantize_pack_binary_gemm_sampled(dev, orc, K, N, passes):
+    """TBN_SIGN_GEMM_SAMPLED: the Session's Gemm test (model.hpp:773-781)
+    decided on the device.  Sampled elements hold -1, 0, -0, +1, +-0.999 (the
+    values the test accepts); an unsampled 0.5 does not matter; one sampled
+    0.998 rejects the tensor, which then packs as w > 0."""
+    rng = np.random.default_rng(K + N)
+    w = np.where(rng.random(K * N) < 0.5, 1.0, -1.0).astype(np.float32)
+    step = max(1, w.size // 1000)
+    sampled = np.arange(0, w.size, step)
+    w[sampled[:6]] = [0.0, -0.0, 0.999, -0.999, 1.0, -1.0]
+    if step > 1:
+        w[sampled[7] + 1] = 0.5   # between samples
+    if not passes:
+        w[sampled[-1]] = 0.998
+    from models import gemm_already_binary
+    assert gemm_already_binary(w.reshape(K, N)) == passes
+    K_pad, N_pad = tbn_hip.padded_dims(K, N)
+    out = empty(N_pad * K_pad // 8, torch.uint8)
+    tbn_hip.call("tbn_hip_quantize_pack_binary_f32", P(to_dev(w)), K, N, tbn_hip.LAYOUT_KN,
+                 tbn_hip.SIGN_GEMM_SAMPLED, 0.0, K_pad, N_pad, P(out), None)
+    binw = orc.sign_ge0_f32(w) if passes else orc.quantize_to_binary_f32(w, 0.0)
+    assert np.array_equal(host(out), orc.pack_binary(binw, K, N, tbn_hip.LAYOUT_KN, K_pad, N_pad))
+
+
 @pytest.mark.parametrize("n", [1, 4, 5, 1001, 4096 * 4096])
 def test_pack_ternary2_bit_exact(dev, orc, n):
     rng = np.random.default_rng(n)

@@ -303,3 +303,67 @@ def test_session_errors(dev, tbn):
     with pytest.raises(tbn.TBNError) as e:
         s2.run()
     assert e.value.code == -3
+
+
+def _pool_graph(seed, include_pad):
+    """Conv (bias from a graph input) -> AveragePool 3x3/2 p1 -> Relu ->
+    GlobalMaxPool -> Flatten -> quantized Gemm whose B is a graph input."""
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal((8, 3, 3, 3)) * 0.3).astype(np.float32)
+    nodes = [
+        models.Node("conv", "Conv", ["x", "w", "bias"], ["c"], {"pads": [1, 1, 1, 1]}),
+        models.Node("ap", "AveragePool", ["c"], ["a"],
+                    {"kernel_shape": [3, 3], "strides": [2, 2], "pads": [1, 1, 1, 1],
+                     "count_include_pad": int(include_pad)}),
+        models.Node("r", "Relu", ["a"], ["ar"]),
+        models.Node("gmp", "GlobalMaxPool", ["ar"], ["g"]),
+        models.Node("flat", "Flatten", ["g"], ["f"], {"axis": 1}),
+        models.Node("fc", "Gemm", ["f", "B"], ["y"], {}),
+    ]
+    vi = {"c": (2, 8, 11, 9), "a": (2, 8, 6, 5), "ar": (2, 8, 6, 5), "g": (2, 8, 1, 1), "f": (2, 8), "y": (2, 10)}
+    return models.Spec(nodes, {"w": w}, {"w": "float32"}, {"x": (2, 3, 11, 9), "bias": (8,), "B": (8, 10)},
+                       {"y": (2, 10)}, vi)
+
+
+@pytest.mark.parametrize("include_pad", [False, True])
+def test_session_pools_and_runtime_operands(dev, tbn, orc, include_pad):
+    """AveragePool / GlobalMaxPool nodes (model.hpp:256-263,632-694), a Conv
+    bias and a quantized Gemm B supplied at run time (model.hpp:207-214,
+    765-845: B is tested and packed on every run), against the oracle
+    executor; quantization on and off, two different B on the same Session."""
+    spec = _pool_graph(21, include_pad)
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((2, 3, 11, 9)).astype(np.float32)
+    bias = rng.standard_normal(8).astype(np.float32)
+    B_binary = np.where(rng.random((8, 10)) < 0.5, 1.0, -1.0).astype(np.float32)
+    B_binary[0, :3] = [0.0, -0.0, 0.999]   # accepted by the sampled test: w >= 0 signs
+    B_float = rng.standard_normal((8, 10)).astype(np.float32)
+    B_float[1, :2] = [0.0, -0.0]            # rejected: w > 0 signs, so 0 reads as -1
+    for quant in (True, False):
+        _, s = _session(tbn, spec, quant=quant)
+        for B in (B_binary, B_float, B_binary):
+            feeds = {"x": x, "bias": bias, "B": B}
+            for k, v in feeds.items():
+                s.set_input(k, v)
+            s.run()
+            out = s.get_output("y")
+            rec = {}
+            ref = models.run_oracle(spec, feeds, quant, orc, record=rec)["y"]
+            _check(out, ref, 8, np.abs(rec["f"]).max())
+
+
+def test_avgpool_global_maxpool_session_nodes_bitwise(dev, tbn, orc):
+    """The two pooling nodes alone: bit-exact against the oracle."""
+    nodes = [models.Node("ap", "AveragePool", ["x"], ["a"], {"kernel_shape": [3, 2], "strides": [2, 1],
+                                                           "pads": [1, 0, 1, 0], "count_include_pad": 1}),
+             models.Node("gmp", "GlobalMaxPool", ["a"], ["g"])]
+    spec = models.Spec(nodes, {}, {}, {"x": (3, 4, 9, 7)}, {"a": (3, 4, 5, 6), "g": (3, 4, 1, 1)},
+                       {"a": (3, 4, 5, 6), "g": (3, 4, 1, 1)})
+    x = np.random.default_rng(23).standard_normal((3, 4, 9, 7)).astype(np.float32)
+    x[0, 0, 0, 0] = np.nan
+    _, s = _session(tbn, spec, quant=False)
+    s.set_input("x", x)
+    s.run()
+    ref = models.run_oracle(spec, {"x": x}, False, orc)
+    assert np.array_equal(s.get_output("a").view(np.uint32), ref["a"].view(np.uint32))
+    assert np.array_equal(s.get_output("g").view(np.uint32), ref["g"].view(np.uint32))
