@@ -184,7 +184,7 @@ int tbn_hip_set_tuning(int option, int value) {
     TBN_REQUIRE(option >= TBN_TUNE_CONV_TILE && option <= TBN_TUNE_GEMM_TILE, TBN_INVALID_ARGUMENT,
                 "unknown tuning option");
     TBN_REQUIRE(option == TBN_TUNE_CONV_TILE ? value >= -1
-                                             : (option == TBN_TUNE_GEMM_TILE ? value >= -1 && value <= 1 : value >= 0),
+                                             : (option == TBN_TUNE_GEMM_TILE ? value >= -1 && value <= 2 : value >= 0),
                 TBN_INVALID_ARGUMENT, "tuning value out of range");
     (void)tbn_hip::tuning(option);  // the environment is read before the first change
     tbn_hip::g_tuning[option].store(value, std::memory_order_relaxed);

@@ -1,25 +1,26 @@
 // Wide-tile float x binary GEMM: C = epilogue(A * W), A fp32 [M, K] row-major,
 // W the reference's BinaryMatrix (column n = K_pad bits, bit 1 = -1).
 //
-// A block owns BR = 128 rows of A x BC = 512 columns of W; its 8 waves each
-// own all 128 rows x 64 columns (4 x 2 MFMA fragments of 32 x 32), so every
-// packed weight column belongs to exactly one wave and is decoded once per
-// block, in registers, straight from global memory.  The A tile of a K step
-// (128 x 32 fp32) is split by the block into three bf16 planes in LDS (hi +
-// mid + lo = a exactly) and shared by all 8 waves; LDS holds two steps so one
-// barrier per step suffices.  Per step and wave: 48 v_mfma_f32_32x32x16_bf16
-// against ~100 VALU (split 8 elements, decode 4 weight bytes).
+// The large tile: a block owns BR = 128 rows of A x BC = 512 columns of W;
+// its 8 waves each own all 128 rows x 64 columns (4 x 2 MFMA fragments of
+// 32 x 32), so every packed weight column belongs to exactly one wave and is
+// decoded once per block, in registers, straight from global memory.  The A
+// tile of a K step (128 x 64 fp32) is split by the block into three bf16
+// planes in LDS (hi + mid + lo = a exactly) and shared by all 8 waves; LDS
+// holds two steps so one barrier per step suffices.  Per step and wave: 96
+// v_mfma_f32_32x32x16_bf16 against ~330 VALU (split 16 elements, decode 8
+// weight bytes per column fragment and k slice).  The mid-size tiles (64 x
+// 128, and 32 x 128 in two K groups) have the same structure with fewer
+// fragments per wave and load two steps ahead.
 //
 // Memory: A and W are read with buffer loads whose resource covers the
 // block's rows / columns to the end of the matrix: rows >= M and columns >=
 // N_pad read as zero, and the voffsets are fixed per lane (the K position is
 // the scalar offset), so the steady-state loop issues no address arithmetic.
-// A K step past K (K % 32 != 0) is zeroed before the split.  Global loads run
-// two steps ahead of their split; W words are fetched 16 bytes (128 k) at a
-// time, one quad of steps ahead.
+// A K step past K (K % 64 != 0) is zeroed before the split.
 //
 // Blocks are dealt round-robin over the 8 XCDs; the tile order puts the
-// BC-column tiles of one 128-row band of A on the same XCD, so the band is
+// BC-column tiles of one BR-row band of A on the same XCD, so the band is
 // fetched from HBM once into that XCD's L2 and read there by its tiles.
 #include <algorithm>
 #include <cstdlib>
@@ -33,27 +34,41 @@ namespace {
 
 using namespace tbnk;
 
-template <int BR_, int BC_, int WR_, int WC_, int KS_>
+template <int BR_, int BC_, int WR_, int WC_, int KS_, bool DEEP_ = false, int KG_ = 1>
 struct WideCfg {
     static constexpr int BR = BR_, BC = BC_, WR = WR_, WC = WC_;
     static constexpr int KS = KS_;                 // K per step (one LDS buffer, one barrier)
+    // DEEP: global loads issued two steps before their data is needed (A in
+    // two register slots, W words a pair of steps at a time, three pairs
+    // live), for tiles with few MFMAs per step; else one step before.
+    static constexpr bool DEEP = DEEP_;
+    // KG: groups of waves that each run one contiguous part of the K steps on
+    // the whole tile (own LDS buffers, same barriers), their sums added in
+    // group order through LDS at the end.
+    static constexpr int KG = KG_;
     static constexpr int KROW = KS + 8;            // bf16 per LDS row: conflict-free 16-byte fragment reads
     static constexpr int WAVES_R = BR / WR, WAVES_C = BC / WC;
-    static constexpr int NT = 64 * WAVES_R * WAVES_C;
+    static constexpr int NTG = 64 * WAVES_R * WAVES_C;  // threads per K group
+    static constexpr int NT = NTG * KG;
     static constexpr int FR = WR / 32, FC = WC / 32;
     static constexpr int KK = KS / 16;             // MFMA k-slices per step
-    static constexpr int EPT = BR * KS / NT;       // A elements a thread stages per step
+    static constexpr int EPT = BR * KS / NTG;      // A elements a thread stages per step
     static constexpr int TPR = KS / EPT;           // threads per A row
     static_assert(EPT % 8 == 0 && KS % EPT == 0, "a thread stages whole 8-element groups of one row");
     static_assert(WR % 32 == 0 && WC % 32 == 0 && BR % WR == 0 && BC % WC == 0, "bad tile");
     static_assert(KK % 2 == 0 && KS == 64, "two k-slice fragment buffers; 8 / 16 weight bytes per step");
+    static_assert(KG == 1 || KG == 2, "one or two K groups");
+    static_assert(KG == 1 || 2 * 3 * BR * KROW * 2 >= NTG * FR * FC * 16 * 4, "group sums fit the A buffers");
 };
 
 // Tile menu: 128 x 512 blocks of 8 waves for shapes whose tiles fill the chip;
 // 64 x 128 blocks (4 waves of 32 x 64, two blocks per CU) for mid-size shapes,
-// which split K across blocks to reach two waves per SIMD.
+// which split K across blocks to reach two waves per SIMD; 32 x 128 blocks of
+// two K groups of 4 waves (32 x 32 each) that reach two waves per SIMD
+// without a split across blocks.
 using Wide = WideCfg<128, 512, 128, 64, 64>;
-using WideSmall = WideCfg<64, 128, 32, 64, 64>;
+using WideSmall = WideCfg<64, 128, 32, 64, 64, true>;
+using WideMid = WideCfg<32, 128, 32, 32, 64, true, 2>;
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x2_t __attribute__((ext_vector_type(2)));
@@ -114,16 +129,18 @@ template <class Cfg, bool TERNARY, bool SPLIT>
 __global__ void __launch_bounds__(Cfg::NT)
 gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per_split, float* partial,
                  int* counters) {
-    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 3 * Cfg::BR * Cfg::KROW];
+    __shared__ __attribute__((aligned(16))) uint16_t lds_all[Cfg::KG * 2 * 3 * Cfg::BR * Cfg::KROW];
     constexpr int kPlane = Cfg::BR * Cfg::KROW;  // bf16 per plane
     constexpr int KS = Cfg::KS;
     constexpr int WPS = TERNARY ? 4 : 2;        // 32-bit weight words per column per step
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
+    const int lane = threadIdx.x & 63;
+    const int kgrp = Cfg::KG == 1 ? 0 : static_cast<int>(threadIdx.x) / Cfg::NTG;
+    const int tid = static_cast<int>(threadIdx.x) - kgrp * Cfg::NTG;  // thread within its K group
     const int wave = tid >> 6;
     const int wr = wave / Cfg::WAVES_C;
     const int wc = wave % Cfg::WAVES_C;
+    uint16_t* const lds = lds_all + kgrp * (2 * 3 * kPlane);
     const int h = lane >> 5;
     // +1.0 bf16 pair kept in a VGPR so each decoded dword is one v_and_or_b32
     uint32_t ones;
@@ -140,8 +157,28 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
     const int r0 = tr * Cfg::BR;
     const int c0 = tc * Cfg::BC;
     const int all_steps = (p.K + KS - 1) / KS;
-    const int s0 = SPLIT ? split * steps_per_split : 0;
-    const int ns = SPLIT ? min(steps_per_split, all_steps - s0) : all_steps;
+    // a K group's steps: the host gives each group the same count
+    const int per_group = (SPLIT ? steps_per_split : all_steps) / Cfg::KG;
+    const int s0 = (SPLIT ? split * steps_per_split : 0) + kgrp * per_group;
+    const int ns = SPLIT ? min(per_group, all_steps - s0) : per_group;
+
+    // epilogue operands: the mid-size tiles (DEEP), whose run is short, fetch
+    // them now so their latency overlaps the main loop; the large tile, short
+    // of registers, after it
+    float mult[Cfg::FC], badd[Cfg::FC];
+    int ncol[Cfg::FC];
+    auto fetch_epilogue = [&]() {
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j) {
+            ncol[j] = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
+            const int nc = min(ncol[j], p.N - 1);
+            mult[j] = p.alpha;
+            badd[j] = 0.0f;
+            if (p.scale) mult[j] = p.alpha * p.scale[nc];
+            if (p.bias) badd[j] = p.bias[nc];
+        }
+    };
+    if constexpr (Cfg::DEEP) fetch_epilogue();
 
     // A staging: thread -> row ar, EPT consecutive k from ag * EPT
     const int ar = tid / Cfg::TPR, ag = tid % Cfg::TPR;
@@ -157,21 +194,49 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
     for (int j = 0; j < Cfg::FC; ++j)
         b_voff[j] = (wc * Cfg::WC + j * 32 + (lane & 31)) * static_cast<int>(p.col_bytes);
 
-    float areg[Cfg::EPT];                              // A of the next step, in flight
+    constexpr int ASLOTS = Cfg::DEEP ? 2 : 1;
+    constexpr int PW = 2 * WPS;                        // W words per column per pair of steps
+    float areg[ASLOTS][Cfg::EPT];                      // A of the next step(s), in flight
     uint32_t bw[Cfg::FC][WPS], bwn[Cfg::FC][WPS];      // W words of the current / next step
+    uint32_t wp[3][Cfg::FC][PW];                       // DEEP: W words of pairs q, q + 1, q + 2
     u32x4_t bfr[2][Cfg::FC];                           // decoded W fragments, alternating k-slices
+    if constexpr (Cfg::DEEP) {
+#pragma unroll
+        for (int x = 0; x < 3; ++x)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int d = 0; d < PW; ++d) wp[x][j][d] = 0;
+    }
 
     // loads past the end of A / W return zeros or data of later rows / columns
     // that no result uses, so they need no guard; s is an absolute step
-    auto load_a = [&](int s) {
+    auto load_a = [&](int s, auto slot) {
+        constexpr int sl = decltype(slot)::value;
         const int soff = s * KS * 4;
 #pragma unroll
         for (int v = 0; v < Cfg::EPT / 4; ++v) {
             const f32x4_t x =
                 __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16 * v, soff, 0));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) areg[4 * v + e] = x[e];
+            for (int e = 0; e < 4; ++e) areg[sl][4 * v + e] = x[e];
         }
+    };
+    // DEEP: the W words of steps 2q', 2q' + 1 (one pair) into wp[x]
+    auto load_pair = [&](int s, int x) {
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int c = 0; c < PW / 4; ++c) {
+                const u32x4_t v = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], s * 4 * WPS + 16 * c, 0));
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    if (x == 0) wp[0][j][4 * c + d] = v[d];
+                    else if (x == 1) wp[1][j][4 * c + d] = v[d];
+                    else wp[2][j][4 * c + d] = v[d];
+                }
+            }
     };
     auto load_b = [&](int s, uint32_t (&w)[Cfg::FC][WPS]) {
 #pragma unroll
@@ -190,29 +255,32 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
         }
     };
     // k-slice kk (16 k) of a step's words: binary 8 bits, ternary 16 bits per lane half
-    auto decode_b = [&](const uint32_t (&w)[Cfg::FC][WPS], int kk, u32x4_t (&bf)[Cfg::FC]) {
+    // (`w` may be a pair's words: `base` selects the step's first word)
+    auto decode_b = [&](const auto& w, int kk, u32x4_t (&bf)[Cfg::FC], int base = 0) {
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             if constexpr (TERNARY)
-                bf[j] = decode_ternary8_y(__builtin_amdgcn_ubfe(w[j][kk], 16 * h, 16), ones);
+                bf[j] = decode_ternary8_y(__builtin_amdgcn_ubfe(w[j][base + kk], 16 * h, 16), ones);
             else
-                bf[j] = decode_binary8_y(__builtin_amdgcn_ubfe(w[j][kk / 2], 16 * (kk & 1) + 8 * h, 16), ones);
+                bf[j] = decode_binary8_y(__builtin_amdgcn_ubfe(w[j][base + kk / 2], 16 * (kk & 1) + 8 * h, 16),
+                                         ones);
         }
     };
     // split the staged step into the three planes of LDS buffer b; with
     // MASK, values at k >= K (last step) are zeroed first
     const int a_store = ar * Cfg::KROW + ag * Cfg::EPT;
-    auto store_a = [&](int b, int s, auto mask) {
+    auto store_a = [&](int b, int s, auto mask, auto slot) {
+        constexpr int sl = decltype(slot)::value;
         if constexpr (decltype(mask)::value) {
             const int kbase = s * KS + ag * Cfg::EPT;
 #pragma unroll
             for (int e = 0; e < Cfg::EPT; ++e)
-                if (kbase + e >= p.K) areg[e] = 0.0f;
+                if (kbase + e >= p.K) areg[sl][e] = 0.0f;
         }
 #pragma unroll
         for (int v = 0; v < Cfg::EPT / 8; ++v) {
             uint4 hi, mid, lo;
-            split8(areg + 8 * v, hi, mid, lo);
+            split8(areg[sl] + 8 * v, hi, mid, lo);
             uint16_t* d = lds + b * 3 * kPlane + a_store + 8 * v;
             *reinterpret_cast<uint4*>(d) = hi;
             *reinterpret_cast<uint4*>(d + kPlane) = mid;
@@ -235,16 +303,31 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
     // MFMAs with the W fragments decoded one slice ahead; meanwhile split step
     // l+1's A (in registers) into the other buffer and fetch step l+2's A and
     // W words.  FULL steps (l + 2 < ns) need no guards.
+    //
+    // DEEP: A of steps l + 1 and l + 2 sit in register slots (l + 1) & 1 and
+    // l & 1; after step l's MFMAs, step l + 1 is split from its slot, which
+    // then receives step l + 3.  The W words of pair q live in wp[0], of q + 1
+    // in wp[1]; pair q + 2's are fetched into wp[2] as pair q starts and
+    // rotated in as it ends.
     auto step = [&](int q, auto uc, auto full) {
         constexpr int u = decltype(uc)::value;
         constexpr bool FULL = decltype(full)::value;
         const int l = 2 * q + u;
         const int s = s0 + l;
+        if constexpr (Cfg::DEEP && u == 0) {
+            if (FULL || 2 * q + 4 < ns) load_pair(s + 4, 2);
+        }
 #pragma unroll
         for (int kk = 0; kk < Cfg::KK; ++kk) {
             // next slice's W fragments (the next step's first slice after the last)
-            if (kk + 1 < Cfg::KK) decode_b(bw, kk + 1, bfr[(kk + 1) & 1]);
-            else decode_b(bwn, 0, bfr[0]);
+            if constexpr (Cfg::DEEP) {
+                if (kk + 1 < Cfg::KK) decode_b(wp[0], kk + 1, bfr[(kk + 1) & 1], u * WPS);
+                else if (u == 0) decode_b(wp[0], 0, bfr[0], WPS);
+                else decode_b(wp[1], 0, bfr[0], 0);
+            } else {
+                if (kk + 1 < Cfg::KK) decode_b(bw, kk + 1, bfr[(kk + 1) & 1]);
+                else decode_b(bwn, 0, bfr[0]);
+            }
 #pragma unroll
             for (int pl = 0; pl < 3; ++pl) {
                 u32x4_t af[Cfg::FR];
@@ -258,18 +341,37 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
                     for (int j = 0; j < Cfg::FC; ++j) acc[i][j] = mfma32(af[i], bfr[kk & 1][j], acc[i][j]);
             }
         }
-        if constexpr (FULL) {
-            store_a(u ^ 1, s + 1, bool_c<false>{});
-            load_a(s + 2);
+        if constexpr (Cfg::DEEP) {
+            if constexpr (FULL) {
+                store_a(u ^ 1, s + 1, bool_c<false>{}, int_c<u ^ 1>{});
+                load_a(s + 3, int_c<u ^ 1>{});
+            } else {
+                if (l + 1 < ns) store_a(u ^ 1, s + 1, bool_c<true>{}, int_c<u ^ 1>{});
+                if (l + 3 < ns) load_a(s + 3, int_c<u ^ 1>{});
+            }
+            if constexpr (u == 1) {
+#pragma unroll
+                for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                    for (int d = 0; d < PW; ++d) {
+                        wp[0][j][d] = wp[1][j][d];
+                        wp[1][j][d] = wp[2][j][d];
+                    }
+            }
         } else {
-            if (l + 1 < ns) store_a(u ^ 1, s + 1, bool_c<true>{});
-            if (l + 2 < ns) load_a(s + 2);
+            if constexpr (FULL) {
+                store_a(u ^ 1, s + 1, bool_c<false>{}, int_c<0>{});
+                load_a(s + 2, int_c<0>{});
+            } else {
+                if (l + 1 < ns) store_a(u ^ 1, s + 1, bool_c<true>{}, int_c<0>{});
+                if (l + 2 < ns) load_a(s + 2, int_c<0>{});
+            }
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int d = 0; d < WPS; ++d) bw[j][d] = bwn[j][d];
+            load_b(s + 2, bwn);
         }
-#pragma unroll
-        for (int j = 0; j < Cfg::FC; ++j)
-#pragma unroll
-            for (int d = 0; d < WPS; ++d) bw[j][d] = bwn[j][d];
-        load_b(s + 2, bwn);
         if constexpr (FULL) {
             // 4 fragment reads ahead, then per fragment: 2 MFMAs, the next read, VALU
             constexpr int kReads = Cfg::KK * 3 * Cfg::FR;
@@ -291,25 +393,60 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
         __syncthreads();
     };
 
-    // prologue: step s0 split into buffer 0, step s0+1 in flight, W words of
-    // steps s0 and s0+1, W fragments of step s0's first slice decoded
-    load_a(s0);
-    load_b(s0, bw);
-    load_b(s0 + 1, bwn);
-    store_a(0, s0, bool_c<true>{});
-    load_a(s0 + 1);
-    decode_b(bw, 0, bfr[0]);
+    // prologue: step s0 split into buffer 0, step s0+1 (DEEP: and s0+2) in
+    // flight, W words of steps s0 and s0+1 (DEEP: of pairs 0 and 1), W
+    // fragments of step s0's first slice decoded
+    if constexpr (Cfg::DEEP) {
+        load_a(s0, int_c<0>{});
+        load_pair(s0, 0);
+        load_a(s0 + 1, int_c<1>{});
+        load_pair(s0 + 2, 1);
+        store_a(0, s0, bool_c<true>{}, int_c<0>{});
+        load_a(s0 + 2, int_c<0>{});
+        decode_b(wp[0], 0, bfr[0], 0);
+    } else {
+        load_a(s0, int_c<0>{});
+        load_b(s0, bw);
+        load_b(s0 + 1, bwn);
+        store_a(0, s0, bool_c<true>{}, int_c<0>{});
+        load_a(s0 + 1, int_c<0>{});
+        decode_b(bw, 0, bfr[0]);
+    }
     __syncthreads();
 
     const int pairs = (ns + 1) / 2;
     int q = 0;
-    for (; 2 * q + 3 < ns; ++q) {
+    constexpr int kAhead = Cfg::DEEP ? 4 : 3;  // a pair is FULL when its loads stay below step ns
+    for (; 2 * q + kAhead < ns; ++q) {
         step(q, int_c<0>{}, bool_c<true>{});
         step(q, int_c<1>{}, bool_c<true>{});
     }
     for (; q < pairs; ++q) {
         step(q, int_c<0>{}, bool_c<false>{});
         if (2 * q + 1 < ns) step(q, int_c<1>{}, bool_c<false>{});
+    }
+
+    if constexpr (Cfg::KG == 2) {
+        // group 1's sums through LDS (the A buffers are free after the last
+        // barrier) into group 0, which adds them after its own and goes on
+        float* red = reinterpret_cast<float*>(lds_all);
+        if (kgrp == 1) {
+#pragma unroll
+            for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+                for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        red[((i * Cfg::FC + j) * 16 + e) * Cfg::NTG + tid] = acc[i][j][e];
+        }
+        __syncthreads();
+        if (kgrp == 1) return;
+#pragma unroll
+        for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] += red[((i * Cfg::FC + j) * 16 + e) * Cfg::NTG + tid];
     }
 
     if constexpr (SPLIT) {
@@ -380,17 +517,7 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
     }
 
     // ---- epilogue: C[m, n] = relu?(acc * alpha * scale[n] + bias[n] (+ beta * cin)) ----
-    float mult[Cfg::FC], badd[Cfg::FC];
-    int ncol[Cfg::FC];
-#pragma unroll
-    for (int j = 0; j < Cfg::FC; ++j) {
-        ncol[j] = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
-        const int nc = min(ncol[j], p.N - 1);
-        mult[j] = p.alpha;
-        badd[j] = 0.0f;
-        if (p.scale) mult[j] = p.alpha * p.scale[nc];
-        if (p.bias) badd[j] = p.bias[nc];
-    }
+    if constexpr (!Cfg::DEEP) fetch_epilogue();
     const bool bias_then_scale = (p.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
     const bool relu = (p.flags & TBN_EPI_RELU) != 0;
 #pragma unroll
@@ -432,16 +559,18 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
 }
 
 // Tile and K-split choice.  Shapes whose 128 x 512 tiles fill the chip (>= 128
-// blocks of 8 waves) take them whole.  Others take the 64 x 128 tile with K
-// split over up to 8 blocks per tile, aiming at 512 blocks (two per CU), each
-// split keeping at least 4 K steps (measured on config 2, 1024^3: 2 or 4
-// splits 15.6 us, 1 split 18.6, 8 splits 20.8; config 3, 256 x 4096^2
-// ternary: 4 splits 36.6 us, 2 splits 42.7, 8 splits 40.4; the 128 x 512 and
-// 128 x 256 tiles with any split were slower).  The choice reads only M, N
-// and K, so a GEMM's result does not depend on anything else.
-// TBN_TUNE_GEMM_TILE / TBN_TUNE_GEMM_SPLITS force either.
+// blocks of 8 waves) take them whole.  Others with an even number of K steps
+// whose 32 x 128 tiles number at least 256 take those, in two K groups (one
+// block of 8 waves per CU, no partial sums through memory; config 2, 1024^3:
+// 10.2 us kernel time against 15.2 for the 64 x 128 tile split 4 ways).  The
+// rest take the 64 x 128 tile with K split over up to 8 blocks per tile,
+// aiming at 512 blocks (two per CU), each split keeping at least 4 K steps
+// (config 3, 256 x 4096^2 ternary: 4 splits 36.6 us, 2 splits 42.7, 8 splits
+// 40.4; the 128 x 512 and 128 x 256 tiles with any split were slower).  The
+// choice reads only M, N and K, so a GEMM's result does not depend on
+// anything else.  TBN_TUNE_GEMM_TILE / TBN_TUNE_GEMM_SPLITS force either.
 struct WidePlan {
-    int cfg = 0;      // 0 Wide, 1 WideSmall
+    int cfg = 0;      // 0 Wide, 1 WideSmall, 2 WideMid
     int tiles_r = 0, tiles_c = 0, steps = 0, splits = 1, per = 0;
     int64_t blocks() const { return static_cast<int64_t>(tiles_r) * tiles_c * splits; }
 };
@@ -456,7 +585,9 @@ WidePlan plan_for(int cfg, int M, int N, int K) {
     const int64_t tiles = static_cast<int64_t>(w.tiles_r) * w.tiles_c;
     int sp = 1;
     const int forced = tbn_hip::tuning(TBN_TUNE_GEMM_SPLITS);
-    if (forced >= 1) {
+    if (Cfg::KG > 1) {
+        sp = 1;  // the K groups split K inside the block
+    } else if (forced >= 1) {
         sp = std::min(forced, std::max(w.steps, 1));
     } else if (cfg != 0 && tiles < 512) {
         sp = static_cast<int>(std::min<int64_t>((512 + tiles - 1) / tiles, 8));
@@ -467,12 +598,20 @@ WidePlan plan_for(int cfg, int M, int N, int K) {
     return w;
 }
 
+// WideMid needs an even step count (its two K groups take equal halves).
+bool mid_ok(int K) { return tbn_hip::ceil_div(K, WideMid::KS) % 2 == 0; }
+
 WidePlan choose_plan(int M, int N, int K) {
     const int forced = tbn_hip::tuning(TBN_TUNE_GEMM_TILE);
     if (forced == 0) return plan_for<Wide>(0, M, N, K);
     if (forced == 1) return plan_for<WideSmall>(1, M, N, K);
+    if (forced == 2 && mid_ok(K)) return plan_for<WideMid>(2, M, N, K);
     const WidePlan big = plan_for<Wide>(0, M, N, K);
     if (big.blocks() >= 128) return big;
+    if (forced != 1 && mid_ok(K)) {
+        const WidePlan mid = plan_for<WideMid>(2, M, N, K);
+        if (mid.blocks() >= 256 && mid.steps >= 4) return mid;
+    }
     return plan_for<WideSmall>(1, M, N, K);
 }
 
@@ -480,10 +619,13 @@ template <class Cfg, bool TERNARY>
 void launch_wide(const tbn_hip::WideGemmArgs& a, const WidePlan& w, float* part, int* counters,
                  hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(w.blocks()));
-    if (w.splits > 1)
-        hipLaunchKernelGGL((gemm_wide_kernel<Cfg, TERNARY, true>), grid, dim3(Cfg::NT), 0, stream, a, w.tiles_r,
-                           w.tiles_c, w.per, part, counters);
-    else
+    if constexpr (Cfg::KG == 1) {
+        if (w.splits > 1) {
+            hipLaunchKernelGGL((gemm_wide_kernel<Cfg, TERNARY, true>), grid, dim3(Cfg::NT), 0, stream, a,
+                               w.tiles_r, w.tiles_c, w.per, part, counters);
+            return;
+        }
+    }
         hipLaunchKernelGGL((gemm_wide_kernel<Cfg, TERNARY, false>), grid, dim3(Cfg::NT), 0, stream, a, w.tiles_r,
                            w.tiles_c, w.per, nullptr, nullptr);
 }
@@ -491,7 +633,8 @@ void launch_wide(const tbn_hip::WideGemmArgs& a, const WidePlan& w, float* part,
 template <bool TERNARY>
 void launch_plan(const tbn_hip::WideGemmArgs& a, const WidePlan& w, float* part, int* counters, hipStream_t s) {
     if (w.cfg == 0) launch_wide<Wide, TERNARY>(a, w, part, counters, s);
-    else launch_wide<WideSmall, TERNARY>(a, w, part, counters, s);
+    else if (w.cfg == 1) launch_wide<WideSmall, TERNARY>(a, w, part, counters, s);
+    else launch_wide<WideMid, TERNARY>(a, w, part, counters, s);
 }
 
 }  // namespace
@@ -500,7 +643,7 @@ namespace tbn_hip {
 
 bool gemm_wide_fits(const WideGemmArgs& a, bool ternary) {
     const WidePlan w = choose_plan(a.M, a.N, a.K);
-    const int waves = w.cfg == 0 ? 8 : 4;
+    const int waves = w.cfg == 1 ? 4 : 8;
     const int bc = w.cfg == 0 ? 512 : 128;
     // shapes that give at least half the chip one wave per SIMD
     return a.K >= 64 && w.blocks() * waves >= 512 && a.M >= 64 && a.N >= 128 && a.lda % 4 == 0 &&

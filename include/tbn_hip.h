@@ -126,6 +126,7 @@ enum tbn_tuning {
                                  convs never split                               */
     TBN_TUNE_GEMM_SPLITS = 3, /* wide GEMM K splits, 0 = automatic              */
     TBN_TUNE_GEMM_TILE = 4    /* wide GEMM tile: 0 = 128x512, 1 = 64x128,
+                                 2 = 32x128 in two K groups (even K/64 only),
                                  -1 = automatic (default)                        */
 };
 int tbn_hip_set_tuning(int option, int value);

@@ -399,13 +399,15 @@ def test_gemm_error_codes(dev):
     tbn_hip.call("tbn_hip_gemm_f32_binary", None, 0, 0, 8, 64, None, 64, 8, None, 1.0, None, 0, None, 8, None)
 
 
-@pytest.mark.parametrize("tile,splits", [(0, 1), (0, 3), (1, 1), (1, 2), (1, 5), (1, 8)])
+@pytest.mark.parametrize("tile,splits", [(0, 1), (0, 3), (1, 1), (1, 2), (1, 5), (1, 8), (2, 1), (2, 4)])
 @pytest.mark.parametrize("ternary", [False, True], ids=["binary", "ternary"])
 def test_gemm_wide_every_tile_and_split(dev, orc, tile, splits, ternary):
-    """Each wide tile (128x512, 64x128), whole or with K split over
-    blocks whose last finisher adds the splits in split order: within the
-    tolerance of the float64 oracle, and bit-identical on a second run (the
-    order does not depend on which block finishes last)."""
+    """Each wide tile (128x512, 64x128, and 32x128 whose two K groups each
+    take half of the 18 K steps, the last one partial), whole or with K split
+    over blocks whose last finisher adds the splits in split order (the
+    K-group tile ignores a forced split): within the tolerance of the float64
+    oracle, and bit-identical on a second run (the order does not depend on
+    which block finishes last)."""
     M, K, N = 300, 1100, 700
     rng = np.random.default_rng(tile * 10 + splits + 100 * ternary)
     A = rng.standard_normal((M, K)).astype(np.float32)
