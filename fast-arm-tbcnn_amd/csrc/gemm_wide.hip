@@ -129,6 +129,332 @@ template <class Cfg, bool TERNARY, bool SPLIT>
 __global__ void __launch_bounds__(Cfg::NT)
 gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per_split, float* partial,
                  int* counters) {
+    __shared__ __attribute__((aligned(16))) uint16_t lds[2 * 3 * Cfg::BR * Cfg::KROW];
+    constexpr int kPlane = Cfg::BR * Cfg::KROW;  // bf16 per plane
+    constexpr int KS = Cfg::KS;
+    constexpr int WPS = TERNARY ? 4 : 2;        // 32-bit weight words per column per step
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wr = wave / Cfg::WAVES_C;
+    const int wc = wave % Cfg::WAVES_C;
+    const int h = lane >> 5;
+    // +1.0 bf16 pair kept in a VGPR so each decoded dword is one v_and_or_b32
+    uint32_t ones;
+    asm volatile("v_mov_b32 %0, 0x3f803f80" : "=v"(ones));
+
+    // tile order: the tiles of one XCD (blockIdx % 8) are consecutive in t,
+    // and consecutive t share a row band of A; split-K blocks are split-major
+    const int total = tiles_r * tiles_c;
+    const int split = SPLIT ? static_cast<int>(blockIdx.x) / total : 0;
+    int t = static_cast<int>(blockIdx.x) - split * total;
+    if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
+    const int tr = t / tiles_c;
+    const int tc = t - tr * tiles_c;
+    const int r0 = tr * Cfg::BR;
+    const int c0 = tc * Cfg::BC;
+    const int all_steps = (p.K + KS - 1) / KS;
+    const int s0 = SPLIT ? split * steps_per_split : 0;
+    const int ns = SPLIT ? min(steps_per_split, all_steps - s0) : all_steps;
+
+    // A staging: thread -> row ar, EPT consecutive k from ag * EPT
+    const int ar = tid / Cfg::TPR, ag = tid % Cfg::TPR;
+    const __amdgpu_buffer_rsrc_t a_rs =
+        make_rsrc(p.A + static_cast<int64_t>(r0) * p.lda, static_cast<uint64_t>(p.M - r0) * p.lda * 4);
+    const int a_voff = (ar * static_cast<int>(p.lda) + ag * Cfg::EPT) * 4;
+    // W: lane's columns c0 + wc*WC + j*32 + lane%32
+    const __amdgpu_buffer_rsrc_t b_rs =
+        make_rsrc(p.packed + static_cast<int64_t>(c0) * p.col_bytes,
+                  static_cast<uint64_t>(p.N_pad - c0) * static_cast<uint64_t>(p.col_bytes));
+    int b_voff[Cfg::FC];
+#pragma unroll
+    for (int j = 0; j < Cfg::FC; ++j)
+        b_voff[j] = (wc * Cfg::WC + j * 32 + (lane & 31)) * static_cast<int>(p.col_bytes);
+
+    float areg[Cfg::EPT];                              // A of the next step, in flight
+    uint32_t bw[Cfg::FC][WPS], bwn[Cfg::FC][WPS];      // W words of the current / next step
+    u32x4_t bfr[2][Cfg::FC];                           // decoded W fragments, alternating k-slices
+
+    // loads past the end of A / W return zeros or data of later rows / columns
+    // that no result uses, so they need no guard; s is an absolute step
+    auto load_a = [&](int s) {
+        const int soff = s * KS * 4;
+#pragma unroll
+        for (int v = 0; v < Cfg::EPT / 4; ++v) {
+            const f32x4_t x =
+                __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16 * v, soff, 0));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) areg[4 * v + e] = x[e];
+        }
+    };
+    auto load_b = [&](int s, uint32_t (&w)[Cfg::FC][WPS]) {
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j) {
+            if constexpr (TERNARY) {
+                const u32x4_t x = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], s * 4 * WPS, 0));
+#pragma unroll
+                for (int d = 0; d < WPS; ++d) w[j][d] = x[d];
+            } else {
+                const uint64_t x = __builtin_bit_cast(
+                    uint64_t, __builtin_amdgcn_raw_buffer_load_b64(b_rs, b_voff[j], s * 4 * WPS, 0));
+                w[j][0] = static_cast<uint32_t>(x);
+                w[j][1] = static_cast<uint32_t>(x >> 32);
+            }
+        }
+    };
+    // k-slice kk (16 k) of a step's words: binary 8 bits, ternary 16 bits per lane half
+    auto decode_b = [&](const uint32_t (&w)[Cfg::FC][WPS], int kk, u32x4_t (&bf)[Cfg::FC]) {
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j) {
+            if constexpr (TERNARY)
+                bf[j] = decode_ternary8_y(__builtin_amdgcn_ubfe(w[j][kk], 16 * h, 16), ones);
+            else
+                bf[j] = decode_binary8_y(__builtin_amdgcn_ubfe(w[j][kk / 2], 16 * (kk & 1) + 8 * h, 16), ones);
+        }
+    };
+    // split the staged step into the three planes of LDS buffer b; with
+    // MASK, values at k >= K (last step) are zeroed first
+    const int a_store = ar * Cfg::KROW + ag * Cfg::EPT;
+    auto store_a = [&](int b, int s, auto mask) {
+        if constexpr (decltype(mask)::value) {
+            const int kbase = s * KS + ag * Cfg::EPT;
+#pragma unroll
+            for (int e = 0; e < Cfg::EPT; ++e)
+                if (kbase + e >= p.K) areg[e] = 0.0f;
+        }
+#pragma unroll
+        for (int v = 0; v < Cfg::EPT / 8; ++v) {
+            uint4 hi, mid, lo;
+            split8(areg + 8 * v, hi, mid, lo);
+            uint16_t* d = lds + b * 3 * kPlane + a_store + 8 * v;
+            *reinterpret_cast<uint4*>(d) = hi;
+            *reinterpret_cast<uint4*>(d + kPlane) = mid;
+            *reinterpret_cast<uint4*>(d + 2 * kPlane) = lo;
+        }
+    };
+
+    f32x16_t acc[Cfg::FR][Cfg::FC];
+#pragma unroll
+    for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+    // fragment read base: row wr*WR + lane%32, k offset 8*(lane/32)
+    const int a_frag = (wr * Cfg::WR + (lane & 31)) * Cfg::KROW + h * 8;
+
+    // Local step l = 2q + u on LDS buffer u: per k-slice kk, 3 planes x FR x FC
+    // MFMAs with the W fragments decoded one slice ahead; meanwhile split step
+    // l+1's A (in registers) into the other buffer and fetch step l+2's A and
+    // W words.  FULL steps (l + 2 < ns) need no guards.
+    auto step = [&](int q, auto uc, auto full) {
+        constexpr int u = decltype(uc)::value;
+        constexpr bool FULL = decltype(full)::value;
+        const int l = 2 * q + u;
+        const int s = s0 + l;
+#pragma unroll
+        for (int kk = 0; kk < Cfg::KK; ++kk) {
+            // next slice's W fragments (the next step's first slice after the last)
+            if (kk + 1 < Cfg::KK) decode_b(bw, kk + 1, bfr[(kk + 1) & 1]);
+            else decode_b(bwn, 0, bfr[0]);
+#pragma unroll
+            for (int pl = 0; pl < 3; ++pl) {
+                u32x4_t af[Cfg::FR];
+#pragma unroll
+                for (int i = 0; i < Cfg::FR; ++i)
+                    af[i] = *reinterpret_cast<const u32x4_t*>(lds + (u * 3 + pl) * kPlane + i * 32 * Cfg::KROW +
+                                                             a_frag + kk * 16);
+#pragma unroll
+                for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+                    for (int j = 0; j < Cfg::FC; ++j) acc[i][j] = mfma32(af[i], bfr[kk & 1][j], acc[i][j]);
+            }
+        }
+        if constexpr (FULL) {
+            store_a(u ^ 1, s + 1, bool_c<false>{});
+            load_a(s + 2);
+        } else {
+            if (l + 1 < ns) store_a(u ^ 1, s + 1, bool_c<true>{});
+            if (l + 2 < ns) load_a(s + 2);
+        }
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int d = 0; d < WPS; ++d) bw[j][d] = bwn[j][d];
+        load_b(s + 2, bwn);
+        if constexpr (FULL) {
+            // 4 fragment reads ahead, then per fragment: 2 MFMAs, the next read, VALU
+            constexpr int kReads = Cfg::KK * 3 * Cfg::FR;
+            constexpr int kPairs = Cfg::KK * 3 * Cfg::FR * Cfg::FC / 2;
+            constexpr int kValu = TERNARY ? 7 : 5;
+            __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+            for (int r = 0; r < kReads - 4; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
+            }
+#pragma unroll
+            for (int r = kReads - 4; r < kPairs; ++r) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+                __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
+            }
+        }
+        __syncthreads();
+    };
+
+    // prologue: step s0 split into buffer 0, step s0+1 in flight, W words of
+    // steps s0 and s0+1, W fragments of step s0's first slice decoded
+    load_a(s0);
+    load_b(s0, bw);
+    load_b(s0 + 1, bwn);
+    store_a(0, s0, bool_c<true>{});
+    load_a(s0 + 1);
+    decode_b(bw, 0, bfr[0]);
+    __syncthreads();
+
+    const int pairs = (ns + 1) / 2;
+    int q = 0;
+    for (; 2 * q + 3 < ns; ++q) {
+        step(q, int_c<0>{}, bool_c<true>{});
+        step(q, int_c<1>{}, bool_c<true>{});
+    }
+    for (; q < pairs; ++q) {
+        step(q, int_c<0>{}, bool_c<false>{});
+        if (2 * q + 1 < ns) step(q, int_c<1>{}, bool_c<false>{});
+    }
+
+    if constexpr (SPLIT) {
+        // Raw sums of this split go to partial[split][m][n]; the last block of
+        // the tile to count itself in adds all splits in split order.  The
+        // sums are written and read at device scope (sc1: through to the
+        // memory side, never a stale line of another XCD's L2), so no L2-wide
+        // write-back or invalidate is needed; the barrier's wait for the
+        // stores orders them before the count.  Buffer accesses over one
+        // split's M x N sums (host-checked below 2^31 bytes): rows past M
+        // are dropped / read zero, columns past N touch sums no stored output
+        // uses (and are never stored: n < N is checked).
+        constexpr int kDeviceScope = 16;  // cache policy SC1
+        const int64_t MN = static_cast<int64_t>(p.M) * p.N;
+        const int nsplit = static_cast<int>(gridDim.x) / total;
+        int voff[Cfg::FR][Cfg::FC];
+#pragma unroll
+        for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j) {
+                const int n = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
+                voff[i][j] = n < p.N ? ((r0 + wr * Cfg::WR + i * 32 + 4 * h) * p.N + n) * 4 : 0x7FFFFFF0;
+            }
+        {
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(partial + split * MN, static_cast<uint64_t>(MN) * 4);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int soff = (8 * (e >> 2) + (e & 3)) * p.N * 4;
+#pragma unroll
+                for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+                    for (int j = 0; j < Cfg::FC; ++j)
+                        // __float_as_uint, not __builtin_bit_cast: hipcc (ROCm 7.2) folds a bit
+                        // cast of a vector element with a loop index to element 0
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][e]), rs, voff[i][j], soff,
+                                                              kDeviceScope);
+            }
+        }
+        __syncthreads();  // every wave's stores complete
+        __shared__ int is_last;
+        if (tid == 0)
+            is_last = __hip_atomic_fetch_add(counters + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                      nsplit - 1;
+        __syncthreads();
+        if (!is_last) return;
+        // 0 + split 0 + split 1 + ... per output, in split order
+#pragma unroll
+        for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+        for (int sp = 0; sp < nsplit; ++sp) {
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(partial + sp * MN, static_cast<uint64_t>(MN) * 4);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int soff = (8 * (e >> 2) + (e & 3)) * p.N * 4;
+#pragma unroll
+                for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+                    for (int j = 0; j < Cfg::FC; ++j)
+                        acc[i][j][e] += __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff[i][j], soff, kDeviceScope));
+            }
+        }
+        // ready for the next launch on this workspace
+        if (tid == 0) __hip_atomic_store(counters + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    // ---- epilogue: C[m, n] = relu?(acc * alpha * scale[n] + bias[n] (+ beta * cin)) ----
+    float mult[Cfg::FC], badd[Cfg::FC];
+    int ncol[Cfg::FC];
+#pragma unroll
+    for (int j = 0; j < Cfg::FC; ++j) {
+        ncol[j] = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
+        const int nc = min(ncol[j], p.N - 1);
+        mult[j] = p.alpha;
+        badd[j] = 0.0f;
+        if (p.scale) mult[j] = p.alpha * p.scale[nc];
+        if (p.bias) badd[j] = p.bias[nc];
+    }
+    const bool bias_then_scale = (p.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
+    const bool relu = (p.flags & TBN_EPI_RELU) != 0;
+#pragma unroll
+    for (int i = 0; i < Cfg::FR; ++i) {
+        const int mrow = r0 + wr * Cfg::WR + i * 32 + 4 * h;
+        float v[Cfg::FC][16];
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float a = acc[i][j][e];
+                v[j][e] = bias_then_scale ? (a + badd[j]) * mult[j] : a * mult[j] + badd[j];
+            }
+        if (p.cin) {
+            float cv[Cfg::FC][16];
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int m = min(mrow + 8 * (e >> 2) + (e & 3), p.M - 1);
+                    const int nc = min(ncol[j], p.N - 1);
+                    cv[j][e] = p.cin_1d ? p.cin[nc] : p.cin[static_cast<int64_t>(m) * p.N + nc];
+                }
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) v[j][e] += p.beta * cv[j][e];
+        }
+#pragma unroll
+        for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int m = mrow + 8 * (e >> 2) + (e & 3);
+                float x = v[j][e];
+                if (relu) x = x > 0.0f ? x : 0.0f;
+                if (m < p.M && ncol[j] < p.N) p.C[static_cast<int64_t>(m) * p.ldc + ncol[j]] = x;
+            }
+    }
+}
+
+// The mid-size kernel: the same block structure (and the same split-K
+// finish) for the DEEP configurations, with two-step-ahead loads and K
+// groups.  The large tile keeps its own kernel above, whose register
+// allocation the extra machinery disturbs (measured 3 % slower at 4096^3 when
+// both shared one kernel).
+template <class Cfg, bool TERNARY, bool SPLIT>
+__global__ void __launch_bounds__(Cfg::NT)
+gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per_split, float* partial,
+                int* counters) {
     __shared__ __attribute__((aligned(16))) uint16_t lds_all[Cfg::KG * 2 * 3 * Cfg::BR * Cfg::KROW];
     constexpr int kPlane = Cfg::BR * Cfg::KROW;  // bf16 per plane
     constexpr int KS = Cfg::KS;
@@ -165,9 +491,7 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
     // epilogue operands: the mid-size tiles (DEEP), whose run is short, fetch
     // them now so their latency overlaps the main loop; the large tile, short
     // of registers, after it
-    float mult[Cfg::FC], badd[Cfg::FC];
-    int ncol[Cfg::FC];
-    auto fetch_epilogue = [&]() {
+    auto fetch_epilogue = [&](float (&mult)[Cfg::FC], float (&badd)[Cfg::FC], int (&ncol)[Cfg::FC]) {
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             ncol[j] = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
@@ -178,7 +502,9 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
             if (p.bias) badd[j] = p.bias[nc];
         }
     };
-    if constexpr (Cfg::DEEP) fetch_epilogue();
+    float mult_e[Cfg::DEEP ? Cfg::FC : 1], badd_e[Cfg::DEEP ? Cfg::FC : 1];
+    int ncol_e[Cfg::DEEP ? Cfg::FC : 1];
+    if constexpr (Cfg::DEEP) fetch_epilogue(mult_e, badd_e, ncol_e);
 
     // A staging: thread -> row ar, EPT consecutive k from ag * EPT
     const int ar = tid / Cfg::TPR, ag = tid % Cfg::TPR;
@@ -198,7 +524,7 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
     constexpr int PW = 2 * WPS;                        // W words per column per pair of steps
     float areg[ASLOTS][Cfg::EPT];                      // A of the next step(s), in flight
     uint32_t bw[Cfg::FC][WPS], bwn[Cfg::FC][WPS];      // W words of the current / next step
-    uint32_t wp[3][Cfg::FC][PW];                       // DEEP: W words of pairs q, q + 1, q + 2
+    uint32_t wp[3][Cfg::DEEP ? Cfg::FC : 1][Cfg::DEEP ? PW : 1];  // DEEP: W words of pairs q, q + 1, q + 2
     u32x4_t bfr[2][Cfg::FC];                           // decoded W fragments, alternating k-slices
     if constexpr (Cfg::DEEP) {
 #pragma unroll
@@ -517,7 +843,21 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
     }
 
     // ---- epilogue: C[m, n] = relu?(acc * alpha * scale[n] + bias[n] (+ beta * cin)) ----
-    if constexpr (!Cfg::DEEP) fetch_epilogue();
+    float mult[Cfg::FC], badd[Cfg::FC];
+    int ncol[Cfg::FC];
+#pragma unroll
+    for (int j = 0; j < Cfg::FC; ++j) {
+        if constexpr (Cfg::DEEP) {
+            mult[j] = mult_e[j], badd[j] = badd_e[j], ncol[j] = ncol_e[j];
+        } else {
+            ncol[j] = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
+            const int nc = min(ncol[j], p.N - 1);
+            mult[j] = p.alpha;
+            badd[j] = 0.0f;
+            if (p.scale) mult[j] = p.alpha * p.scale[nc];
+            if (p.bias) badd[j] = p.bias[nc];
+        }
+    }
     const bool bias_then_scale = (p.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
     const bool relu = (p.flags & TBN_EPI_RELU) != 0;
 #pragma unroll
@@ -615,19 +955,30 @@ WidePlan choose_plan(int M, int N, int K) {
     return plan_for<WideSmall>(1, M, N, K);
 }
 
+// Kernel variants: the large tile on gemm_wide_kernel, the mid-size (DEEP)
+// tiles on gemm_mid_kernel.
 template <class Cfg, bool TERNARY>
 void launch_wide(const tbn_hip::WideGemmArgs& a, const WidePlan& w, float* part, int* counters,
                  hipStream_t stream) {
     const dim3 grid(static_cast<unsigned>(w.blocks()));
-    if constexpr (Cfg::KG == 1) {
-        if (w.splits > 1) {
-            hipLaunchKernelGGL((gemm_wide_kernel<Cfg, TERNARY, true>), grid, dim3(Cfg::NT), 0, stream, a,
-                               w.tiles_r, w.tiles_c, w.per, part, counters);
-            return;
+    if constexpr (!Cfg::DEEP) {
+        if (w.splits > 1)
+            hipLaunchKernelGGL((gemm_wide_kernel<Cfg, TERNARY, true>), grid, dim3(Cfg::NT), 0, stream, a, w.tiles_r,
+                               w.tiles_c, w.per, part, counters);
+        else
+            hipLaunchKernelGGL((gemm_wide_kernel<Cfg, TERNARY, false>), grid, dim3(Cfg::NT), 0, stream, a, w.tiles_r,
+                               w.tiles_c, w.per, nullptr, nullptr);
+    } else {
+        if constexpr (Cfg::KG == 1) {
+            if (w.splits > 1) {
+                hipLaunchKernelGGL((gemm_mid_kernel<Cfg, TERNARY, true>), grid, dim3(Cfg::NT), 0, stream, a,
+                                   w.tiles_r, w.tiles_c, w.per, part, counters);
+                return;
+            }
         }
-    }
-        hipLaunchKernelGGL((gemm_wide_kernel<Cfg, TERNARY, false>), grid, dim3(Cfg::NT), 0, stream, a, w.tiles_r,
+        hipLaunchKernelGGL((gemm_mid_kernel<Cfg, TERNARY, false>), grid, dim3(Cfg::NT), 0, stream, a, w.tiles_r,
                            w.tiles_c, w.per, nullptr, nullptr);
+    }
 }
 
 template <bool TERNARY>

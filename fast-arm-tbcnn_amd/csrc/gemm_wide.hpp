@@ -28,8 +28,9 @@ struct WideGemmArgs {
 // fill the chip, 16-byte aligned fp32 rows and 16-byte multiple packed columns.
 // `packed` holds BinaryMatrix columns, or 2-bit ternary columns when ternary.
 bool gemm_wide_fits(const WideGemmArgs& a, bool ternary);
-// Runs it; shapes with few tiles split K and sum the splits in a second,
-// deterministic pass (stream-ordered temporary of splits * M * N floats).
+// Runs it; shapes with few tiles split K over blocks, the last block of each
+// tile adding the splits in split order (stream workspace of splits * M * N
+// floats).
 int gemm_wide(const WideGemmArgs& a, bool ternary, hipStream_t stream);
 
 }  // namespace tbn_hip
