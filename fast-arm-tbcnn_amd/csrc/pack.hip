@@ -53,16 +53,72 @@ __global__ void sign_ge0_kernel(const float* __restrict__ w, int64_t n, uint8_t*
         out[i] = (w[i] >= 0.0f) ? 1 : 0;
 }
 
-// One thread per channel, summing in the same sequential order as the
-// Session (model.hpp:388-394) so the scale is bit-identical.
-__global__ void channel_mean_abs_kernel(const float* __restrict__ w, int64_t channels,
-                                        int64_t per_channel, float* __restrict__ scale) {
-    const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (c >= channels) return;
-    const float* row = w + c * per_channel;
+// mean |w| per channel, summed in the same sequential order as the Session
+// (model.hpp:388-394) so the scale is bit-identical: a block owns 64
+// channels (contiguous rows).  Chunks of 128 positions of all 64 rows go
+// through LDS (two buffers) with coalesced loads, the next chunk's loads in
+// flight while thread c adds its row's values of the current one in order,
+// 16 LDS reads ahead of the adds.
+constexpr int kMeanChunk = 128;
+__global__ void __launch_bounds__(256) channel_mean_abs_kernel(const float* __restrict__ w, int64_t channels,
+                                                               int64_t per_channel, float* __restrict__ scale) {
+    constexpr int kPitch = kMeanChunk + 4;  // 16-byte aligned rows
+    constexpr int kPer = 64 * kMeanChunk / 256;
+    __shared__ __attribute__((aligned(16))) float tile[2][64][kPitch];
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 64;
+    const int nc = static_cast<int>(channels - c0 < 64 ? channels - c0 : 64);
+    const int tid = threadIdx.x;
+    float pre[kPer];
+    // Every lane loads (an out-of-range slot reads element 0 and is zeroed
+    // when stored), so the loads issue back to back with no branch around
+    // them and the wait for them falls at the store, after the chunk's sums.
+    auto in_range = [&](int j, int64_t k0) {
+        const int idx = tid + 256 * j;
+        return (idx / kMeanChunk < nc) & (k0 + idx % kMeanChunk < per_channel);
+    };
+    auto load = [&](int64_t k0) {
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int idx = tid + 256 * j;
+            pre[j] = w[in_range(j, k0) ? (c0 + idx / kMeanChunk) * per_channel + k0 + idx % kMeanChunk : 0];
+        }
+    };
+    auto store = [&](int b, int64_t k0) {
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int idx = tid + 256 * j;
+            tile[b][idx / kMeanChunk][idx % kMeanChunk] = in_range(j, k0) ? fabsf(pre[j]) : 0.0f;
+        }
+    };
     float acc = 0.0f;
-    for (int64_t i = 0; i < per_channel; ++i) acc += fabsf(row[i]);
-    scale[c] = acc / (float)per_channel;
+    const int64_t chunks = (per_channel + kMeanChunk - 1) / kMeanChunk;
+    load(0);
+    store(0, 0);
+    __syncthreads();
+    for (int64_t ch = 0; ch < chunks; ++ch) {
+        const int b = static_cast<int>(ch & 1);
+        if (ch + 1 < chunks) load((ch + 1) * kMeanChunk);
+        const int kl = static_cast<int>(per_channel - ch * kMeanChunk < kMeanChunk ? per_channel - ch * kMeanChunk
+                                                                                     : kMeanChunk);
+        if (tid < nc) {
+            const float* row = tile[b][tid];
+            int i = 0;
+            for (; i + 16 <= kl; i += 16) {
+                float v[16];
+#pragma unroll
+                for (int e = 0; e < 16; e += 4) {
+                    const float4 q = *reinterpret_cast<const float4*>(row + i + e);
+                    v[e] = q.x, v[e + 1] = q.y, v[e + 2] = q.z, v[e + 3] = q.w;
+                }
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc += v[e];
+            }
+            for (; i < kl; ++i) acc += row[i];
+        }
+        if (ch + 1 < chunks) store(b ^ 1, (ch + 1) * kMeanChunk);
+        __syncthreads();
+    }
+    if (tid < nc) scale[c0 + tid] = acc / static_cast<float>(per_channel);
 }
 
 // ---- BinaryMatrix packing ---------------------------------------------------
@@ -287,7 +343,7 @@ int tbn_hip_channel_mean_abs(const float* w, int64_t channels, int64_t per_chann
     TBN_REQUIRE(channels == 0 || (w && scale), TBN_INVALID_ARGUMENT, "null pointer");
     TBN_DEVICE_GUARD();
     if (channels == 0) return tbn_hip::ok();
-    hipLaunchKernelGGL(channel_mean_abs_kernel, dim3(tbn_hip::ceil_div(channels, 64)), dim3(64),
+    hipLaunchKernelGGL(channel_mean_abs_kernel, dim3(tbn_hip::ceil_div(channels, 64)), dim3(256),
                        0, stream_of(stream), w, channels, per_channel, scale);
     return check_launch("channel_mean_abs");
 }

@@ -459,3 +459,36 @@ def test_gemm_split_counters_survive_other_workspace_users(dev, orc):
             y = empty((3, 96, 7, 7), torch.float32)  # a split-K conv in between
             tbn_hip.call("tbn_hip_conv2d_f32_binary", P(dx), d, P(cpk), Kc_pad, Nc_pad, None, 1.0, None, 0, P(y),
                          None)
+
+
+def test_gemm_mid_tile_graph_replay(dev):
+    """The config-2 GEMM (32 x 128 tile, two K groups, no workspace) records
+    into a HIP graph; each of several replays, with eager work and
+    synchronizations between them, matches the eager result bit for bit."""
+    M = N = K = 1024
+    rng = np.random.default_rng(31)
+    A = to_dev(rng.standard_normal((M, K)).astype(np.float32))
+    binw = (rng.random((K, N)) < 0.5).astype(np.uint8)
+    packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+    scale = to_dev(rng.uniform(0.5, 1.5, N).astype(np.float32))
+    eager = empty((M, N), torch.float32)
+    out = empty((M, N), torch.float32)
+
+    def launch(C, stream):
+        tbn_hip.call("tbn_hip_gemm_f32_binary", P(A), K, M, N, K, P(packed), K_pad, N_pad, P(scale), 1.0, None,
+                     tbn_hip.EPI_RELU, P(C), N, stream)
+
+    launch(eager, None)
+    torch.cuda.synchronize()
+    cap = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        launch(out, torch.cuda.current_stream().cuda_stream)
+    for r in range(3):
+        out.fill_(np.nan)
+        noise = torch.randn((M, N), device=dev)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r}"
+        del noise

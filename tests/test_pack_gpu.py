@@ -34,7 +34,7 @@ def test_elementwise_quantizers_bit_exact(dev, orc):
     assert np.array_equal(host(out_i), orc.quantize_to_binary_i8(wi))
 
 
-@pytest.mark.parametrize("shape", [(6, 1, 5, 5), (16, 6, 5, 5), (512, 256, 3, 3)])
+@pytest.mark.parametrize("shape", [(6, 1, 5, 5), (16, 6, 5, 5), (512, 256, 3, 3), (130, 7, 3, 3), (100, 1, 1, 65)])
 def test_channel_mean_abs_bit_exact(dev, orc, shape):
     rng = np.random.default_rng(1)
     w = rng.standard_normal(shape).astype(np.float32) * 0.1
