@@ -97,21 +97,19 @@ __device__ __forceinline__ u32x4_t decode_binary8_y(uint32_t x, uint32_t ones) {
 }
 
 // 8 two-bit ternary codes (code i in bits 2i, 2i+1: 00 -> -1, 10 -> +1, 01 and
-// 11 -> 0) -> 8 bf16.  With u = ~x, bit 2i+1 of u is the sign and bit 2i says
-// "nonzero"; v holds u at i and i + 14, so one shift places code 2d's bits at
-// 15 and code 2d+1's at 31.  The +-1 pair is built like the binary decode and
-// the zero codes are masked with a packed 16-bit arithmetic shift.
-__device__ __forceinline__ u32x4_t decode_ternary8_y(uint32_t x, uint32_t ones) {
-    const uint32_t u = x ^ 0xFFFFu;
-    const uint32_t v = u | (u << 14);
+// 11 -> 0) -> 8 bf16 of TWICE the weight.  With u = ~x, bit 2i+1 of u is the
+// sign and bit 2i says "nonzero"; placed at bits 15 and 14 of a half they are
+// the bf16 bits of -2 (0xC000), +2 (0x4000), -0 (0x8000) or +0.  y holds code
+// i at bits 2i and 2i + 14 (bits 16 and up of x must be zero), so one shift
+// puts code 2d at bits 15:14 and code 2d+1 at 31:30 and one v_bfi_b32
+// (~sg & mask) finishes a dword.  The kernels halve the sums before the
+// epilogue: every product and partial sum is scaled by 2, which fp32 rounding
+// commutes with, so the result equals the sum over +-1 / 0 weights.
+__device__ __forceinline__ u32x4_t decode_ternary8_x2(uint32_t x) {
+    const uint32_t y = x | (x << 14);
     u32x4_t r;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-        const uint32_t sg = v << (14 - 4 * d);  // bit 15 <- u[4d+1], bit 31 <- u[4d+3]
-        const uint32_t val = (sg & 0x80008000u) | ones;
-        const i16x2_t nz = __builtin_bit_cast(i16x2_t, sg << 1) >> 15;  // halves: -1 where nonzero
-        r[d] = val & __builtin_bit_cast(uint32_t, nz);
-    }
+    for (int d = 0; d < 4; ++d) r[d] = ~(y << (14 - 4 * d)) & 0xC000C000u;
     return r;
 }
 
@@ -209,7 +207,7 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             if constexpr (TERNARY)
-                bf[j] = decode_ternary8_y(__builtin_amdgcn_ubfe(w[j][kk], 16 * h, 16), ones);
+                bf[j] = decode_ternary8_x2(__builtin_amdgcn_ubfe(w[j][kk], 16 * h, 16));
             else
                 bf[j] = decode_binary8_y(__builtin_amdgcn_ubfe(w[j][kk / 2], 16 * (kk & 1) + 8 * h, 16), ones);
         }
@@ -289,7 +287,7 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
             // 4 fragment reads ahead, then per fragment: 2 MFMAs, the next read, VALU
             constexpr int kReads = Cfg::KK * 3 * Cfg::FR;
             constexpr int kPairs = Cfg::KK * 3 * Cfg::FR * Cfg::FC / 2;
-            constexpr int kValu = TERNARY ? 7 : 5;
+            constexpr int kValu = 5;
             __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
             for (int r = 0; r < kReads - 4; ++r) {
@@ -416,7 +414,7 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
         for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float a = acc[i][j][e];
+                const float a = TERNARY ? acc[i][j][e] * 0.5f : acc[i][j][e];  // ternary sums are doubled
                 v[j][e] = bias_then_scale ? (a + badd[j]) * mult[j] : a * mult[j] + badd[j];
             }
         if (p.cin) {
@@ -586,7 +584,7 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             if constexpr (TERNARY)
-                bf[j] = decode_ternary8_y(__builtin_amdgcn_ubfe(w[j][base + kk], 16 * h, 16), ones);
+                bf[j] = decode_ternary8_x2(__builtin_amdgcn_ubfe(w[j][base + kk], 16 * h, 16));
             else
                 bf[j] = decode_binary8_y(__builtin_amdgcn_ubfe(w[j][base + kk / 2], 16 * (kk & 1) + 8 * h, 16),
                                          ones);
@@ -702,7 +700,7 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
             // 4 fragment reads ahead, then per fragment: 2 MFMAs, the next read, VALU
             constexpr int kReads = Cfg::KK * 3 * Cfg::FR;
             constexpr int kPairs = Cfg::KK * 3 * Cfg::FR * Cfg::FC / 2;
-            constexpr int kValu = TERNARY ? 7 : 5;
+            constexpr int kValu = 5;
             __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
             for (int r = 0; r < kReads - 4; ++r) {
@@ -868,7 +866,7 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
         for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const float a = acc[i][j][e];
+                const float a = TERNARY ? acc[i][j][e] * 0.5f : acc[i][j][e];  // ternary sums are doubled
                 v[j][e] = bias_then_scale ? (a + badd[j]) * mult[j] : a * mult[j] + badd[j];
             }
         if (p.cin) {
