@@ -151,7 +151,7 @@ template <bool TERNARY>
 __device__ __forceinline__ u32x4_t weight_frag(uint2 w, int kk, int kg, uint32_t ones) {
     if (TERNARY) {
         const uint32_t word = kk ? w.y : w.x;
-        return decode_ternary8((word >> (16 * kg)) & 0xFFFFu);
+        return decode_ternary8_x2((word >> (16 * kg)) & 0xFFFFu);  // twice the weights
     }
     return decode_binary8_fast(__builtin_amdgcn_ubfe(w.x, 8 * (2 * kk + kg), 16), ones);
 }
@@ -513,6 +513,16 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
             for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[f][j][e] += mine[((f * Cfg::FC + j) * 16 + e) * 64];
+    }
+
+    if constexpr (TERNARY) {
+        // the ternary weights went in as twice their value (exact to undo)
+#pragma unroll
+        for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[f][j][e] *= 0.5f;
     }
 
     // ---- epilogue: scale, bias, residual, ReLU, optional 2x2 max pool ----

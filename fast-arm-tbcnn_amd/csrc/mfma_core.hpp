@@ -145,6 +145,24 @@ __device__ __forceinline__ u32x4_t decode_ternary8(uint32_t y) {
     return r;
 }
 
+// 8 two-bit ternary codes (code i in bits 2i, 2i+1: 00 -> -1, 10 -> +1, 01 and
+// 11 -> 0) -> 8 bf16 of TWICE the weight.  With u = ~x, bit 2i+1 of u is the
+// sign and bit 2i says "nonzero"; placed at bits 15 and 14 of a half they are
+// the bf16 bits of -2 (0xC000), +2 (0x4000), -0 (0x8000) or +0.  y holds code
+// i at bits 2i and 2i + 14 (bits 16 and up of x must be zero), so one shift
+// puts code 2d at bits 15:14 and code 2d+1 at 31:30, and an AND of the
+// inverted word finishes a dword (the inversion is done once, on y).  Kernels
+// using it halve their sums before the epilogue: every product and partial
+// sum is scaled by 2, which fp32 rounding commutes with (away from overflow
+// and subnormals), so the result equals the sum over +-1 / 0 weights.
+__device__ __forceinline__ u32x4_t decode_ternary8_x2(uint32_t x) {
+    const uint32_t y = x | (x << 14);
+    u32x4_t r;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) r[d] = ~(y << (14 - 4 * d)) & 0xC000C000u;
+    return r;
+}
+
 __device__ __forceinline__ f32x16_t mfma32(u32x4_t a, u32x4_t b, f32x16_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                    __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
