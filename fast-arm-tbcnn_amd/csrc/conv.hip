@@ -267,13 +267,24 @@ int tbn_hip_conv2d_f32_quantized_noalloc(int weights, const float* x, const tbn_
     return tbn_hip::fail(TBN_INVALID_ARGUMENT, "unknown weights kind");
 }
 
+int tbn_hip_conv2d_f32_supported(const tbn_conv2d_desc* desc, int flags) {
+    ConvGeom g;
+    const int rc = make_geom(desc, flags, g);
+    if (rc) return rc;
+    TBN_REQUIRE((flags & ~(TBN_EPI_RELU | TBN_EPI_MAXPOOL2X2 | TBN_EPI_MAXPOOL3X3S2)) == 0, TBN_INVALID_ARGUMENT,
+                "unsupported epilogue flags for conv2d_f32");
+    TBN_REQUIRE(!(flags & TBN_EPI_MAXPOOL3X3S2) || tbn_hip::conv_stem_supported(desc, flags), TBN_NOT_IMPLEMENTED,
+                "the fused 3x3/2 max pool takes the stem shape (3 channels, 7x7, stride 2, M <= 64) with ReLU only");
+    return tbn_hip::ok();
+}
+
 int tbn_hip_conv2d_f32(const float* x, const tbn_conv2d_desc* desc, const float* w,
                        const float* bias, int flags, float* y, tbn_stream_t stream) {
     ConvGeom g;
     int rc = make_geom(desc, flags, g);
     if (rc) return rc;
-    TBN_REQUIRE((flags & ~(TBN_EPI_RELU | TBN_EPI_MAXPOOL2X2)) == 0, TBN_INVALID_ARGUMENT,
-                "unsupported epilogue flags for conv2d_f32");
+    rc = tbn_hip_conv2d_f32_supported(desc, flags);
+    if (rc) return rc;
     if (g.Q == 0) return tbn_hip::ok();
     TBN_REQUIRE(x && w && y, TBN_INVALID_ARGUMENT, "null pointer");
     TBN_DEVICE_GUARD();

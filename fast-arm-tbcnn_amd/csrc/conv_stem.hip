@@ -22,6 +22,15 @@
 // one.  Tiles are dealt wave-major across blocks (wave w of every block
 // before wave w + 1 of any), so the tiles beyond a whole round land on
 // different SIMDs.
+//
+// With the 3x3 stride-2 pad-1 max pool fused (after ReLU), a wave's tile is
+// 3 x 4 pooled outputs: the 7 x 9 conv pixels their windows cover (63 of the
+// 64 fragment columns), so the window rows and columns shared with the
+// neighbouring tiles are computed by both.  The pool reads the tile back
+// from the wave's patch buffer.  After ReLU every value is +0 or more and
+// none is NaN, so the maximum does not depend on the order it is taken in
+// and equals the separate pool's bit for bit; conv pixels outside the image
+// count as 0, which cannot exceed a window's largest in-image value.
 #include <algorithm>
 #include <mutex>
 #include <string>
@@ -33,15 +42,20 @@ namespace {
 using namespace tbnk;
 
 constexpr int kRows = 64;    // output channels per tile (M <= 64)
-constexpr int kTileH = 4;    // output tile: 4 rows x 16 columns (one wave)
-constexpr int kTileW = 16;
 constexpr int kWaves = 8;    // waves per block
 constexpr uint32_t kOutside = 0x80000000u;
+// fused pool: a wave's tile is kPoolTH x kPoolTW pooled outputs; its 64 x 32
+// (pixel, channel) staging table has a pitch of 33 floats (pixels two rows
+// apart, read by the two lane halves together, start 18 banks apart)
+constexpr int kPoolTH = 3, kPoolTW = 4;
+constexpr int kTPitch = 33;
+constexpr int kTWords = 64 * kTPitch;
 
 struct StemGeom {
     int N, H, W, M;
     int ph, pw;
     int OH, OW;
+    int PH, PW;  // pooled output (fused pool only)
     int tiles_w, tiles_img, tiles;
     int relu;
 };
@@ -71,25 +85,34 @@ __device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_
 }
 
 // Compile-time geometry: C channels, KH x KW taps, stride SH x SW, no
-// dilation (pads, image size, batch and M <= 64 are runtime).
-template <int C_, int KH_, int KW_, int SH_, int SW_>
+// dilation (pads, image size, batch and M <= 64 are runtime); a wave's conv
+// tile is TR x TC pixels (at most 64), pixel i of the two 32-column
+// fragments being tile row i / TC, column i % TC.
+template <int C_, int KH_, int KW_, int SH_, int SW_, int TR_, int TC_>
 struct StemShape {
-    static constexpr int C = C_, KH = KH_, KW = KW_, SH = SH_, SW = SW_;
+    static constexpr int C = C_, KH = KH_, KW = KW_, SH = SH_, SW = SW_, TR = TR_, TC = TC_;
+    static constexpr int PIX = TR * TC;
     static constexpr int SLICES = (KH * C + 1) / 2;                    // k8 groups: KH * C, two per slice
     static constexpr int K_PAD = 16 * SLICES;
     static constexpr int KROW = K_PAD + 8;                             // LDS weight row: conflict-free reads
-    static constexpr int PROWS = (kTileH - 1) * SH + KH;               // a wave's patch rows
-    static constexpr int PITCH = ((kTileW - 1) * SW + 8 + 3) / 4 * 4;  // row pitch (elements)
+    static constexpr int PROWS = (TR - 1) * SH + KH;                   // a wave's patch rows
+    static constexpr int PITCH = ((TC - 1) * SW + 8 + 3) / 4 * 4;      // row pitch (elements)
     static constexpr int PATCH = C * PROWS * PITCH;
     static constexpr int PAIRS = PATCH / 2;                            // dwords per plane
     static constexpr int PER = (PAIRS + 63) / 64;                      // pairs staged per lane
+    // a wave's LDS buffer (dwords): the patch's three planes, or the fused
+    // pool's staging table after the MFMAs
+    static constexpr int WBUF = 3 * PAIRS > kTWords ? 3 * PAIRS : kTWords;
     static constexpr size_t LDS = static_cast<size_t>(3) * kRows * KROW * 2 + kRows * 4 +
-                                  static_cast<size_t>(kWaves) * 3 * PAIRS * 4;
+                                  static_cast<size_t>(kWaves) * WBUF * 4;
     static_assert(KW <= 8 && SW % 2 == 0 && PITCH % 4 == 0, "a lane's run: 8 columns from an even one");
+    static_assert(PIX <= 64, "two 32-pixel fragments");
     static_assert(LDS <= 160 * 1024, "LDS");
 };
 
-template <class S>
+// POOL: the tile is a pooled tile (kPoolTH x kPoolTW, S::TR = 2 kPoolTH + 1,
+// S::TC = 2 kPoolTW + 1) and y is the pooled output.
+template <class S, bool POOL>
 __global__ void __launch_bounds__(64 * kWaves) stem_conv_kernel(const float* __restrict__ x, StemGeom g,
                                                                 const float* __restrict__ w,
                                                                 const float* __restrict__ bias,
@@ -104,7 +127,7 @@ __global__ void __launch_bounds__(64 * kWaves) stem_conv_kernel(const float* __r
     // resources, are too: a resource in VGPRs would loop every load and store
     const int wave = __builtin_amdgcn_readfirstlane(tid_all >> 6);
     constexpr int pplane = S::PAIRS;
-    uint32_t* pl = reinterpret_cast<uint32_t*>(bl + kRows) + wave * 3 * pplane;  // [3 planes][C][PROWS][PITCH]
+    uint32_t* pl = reinterpret_cast<uint32_t*>(bl + kRows) + wave * S::WBUF;  // [3 planes][C][PROWS][PITCH]
 
     // ---- weights, once per block: item = (row m, k8 = r * C + c), the run
     //      w[m, c, r, 0..kw) split into the three planes (zero past M, KH, KW) ----
@@ -145,12 +168,21 @@ __global__ void __launch_bounds__(64 * kWaves) stem_conv_kernel(const float* __r
     //      [C][PROWS][PITCH] (the pitch is even: both in one row) ----
     const uint32_t HW = static_cast<uint32_t>(g.H) * g.W;
     float stage[S::PER][2];
+    // conv pixel (oh0, ow0) is the tile's first (for a pooled tile starting at
+    // pooled (pr0, pc0): conv (2 pr0 - 1, 2 pc0 - 1), the windows' first row
+    // and column, possibly -1)
     auto tile_origin = [&](int t, int& n, int& oh0, int& ow0) {
         n = t / g.tiles_img;
         const int r = t - n * g.tiles_img;
         const int th = r / g.tiles_w;
-        oh0 = th * kTileH;
-        ow0 = (r - th * g.tiles_w) * kTileW;
+        const int tw = r - th * g.tiles_w;
+        if (POOL) {
+            oh0 = 2 * th * kPoolTH - 1;
+            ow0 = 2 * tw * kPoolTW - 1;
+        } else {
+            oh0 = th * S::TR;
+            ow0 = tw * S::TC;
+        }
     };
     auto load_patch = [&](int t) {
         int n, oh0, ow0;
@@ -192,12 +224,14 @@ __global__ void __launch_bounds__(64 * kWaves) stem_conv_kernel(const float* __r
 
     // ---- this lane's fragment pixels (in dwords of a plane) ----
     const int kg = lane >> 5;
-    int pix[2];  // fragment j: tile rows 2j (lanes 0-15) and 2j + 1 (lanes 16-31)
+    int pix[2];  // fragment j: tile pixel i = 32 j + lane % 32 (past the tile: pixel 0)
+    int prow[2], pcol[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int tr = 2 * j + ((lane & 31) >> 4);
-        const int tc = lane & 15;
-        pix[j] = (tr * S::SH * S::PITCH + tc * S::SW) / 2;
+        const int i = 32 * j + (lane & 31);
+        prow[j] = i < S::PIX ? i / S::TC : 0;
+        pcol[j] = i < S::PIX ? i - (i / S::TC) * S::TC : 0;
+        pix[j] = (prow[j] * S::SH * S::PITCH + pcol[j] * S::SW) / 2;
     }
     // k8 = 2 sl + kg: tap row r, channel c at dword offset koff(sl, kg) of the patch
     auto koff = [&](int sl, int k) {
@@ -276,29 +310,105 @@ __global__ void __launch_bounds__(64 * kWaves) stem_conv_kernel(const float* __r
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-        // ---- epilogue: + bias, ReLU; buffer stores into image n's output
-        //      (rows past M and pixels past the image carry kOutside) ----
         int n, oh0, ow0;
         tile_origin(t, n, oh0, ow0);
-        const uint32_t plane = static_cast<uint32_t>(g.OH) * g.OW;
-        const __amdgpu_buffer_rsrc_t ys =
-            make_rsrc(y + static_cast<int64_t>(n) * g.M * plane, static_cast<uint32_t>(g.M) * plane * 4);
+        if constexpr (!POOL) {
+            // ---- epilogue: + bias, ReLU; buffer stores into image n's output
+            //      (rows past M and pixels past the image carry kOutside) ----
+            const uint32_t plane = static_cast<uint32_t>(g.OH) * g.OW;
+            const __amdgpu_buffer_rsrc_t ys =
+                make_rsrc(y + static_cast<int64_t>(n) * g.M * plane, static_cast<uint32_t>(g.M) * plane * 4);
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int oh = oh0 + 2 * j + ((lane & 31) >> 4);
-            const int ow = ow0 + (lane & 15);
-            const uint32_t base =
-                (oh < g.OH && ow < g.OW) ? (static_cast<uint32_t>(4 * kg) * plane + oh * g.OW + ow) * 4 : kOutside;
+            for (int j = 0; j < 2; ++j) {
+                const int oh = oh0 + prow[j];
+                const int ow = ow0 + pcol[j];
+                const bool ok = 32 * j + (lane & 31) < S::PIX && oh < g.OH && ow < g.OW;
+                const uint32_t base = ok ? (static_cast<uint32_t>(4 * kg) * plane + oh * g.OW + ow) * 4 : kOutside;
 #pragma unroll
-            for (int f = 0; f < 2; ++f)
+                for (int f = 0; f < 2; ++f)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int row = f * 32 + 8 * (e >> 2) + (e & 3);  // + 4 * kg in `base`
-                    float v = acc[f][j][e] * 1.0f + bl[row + 4 * kg];
-                    if (g.relu) v = v > 0.0f ? v : 0.0f;
-                    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ys,
-                                                          base + static_cast<uint32_t>(row) * plane * 4, 0, 0);
+                    for (int e = 0; e < 16; ++e) {
+                        const int row = f * 32 + 8 * (e >> 2) + (e & 3);  // + 4 * kg in `base`
+                        float v = acc[f][j][e] * 1.0f + bl[row + 4 * kg];
+                        if (g.relu) v = v > 0.0f ? v : 0.0f;
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), ys,
+                                                              base + static_cast<uint32_t>(row) * plane * 4, 0, 0);
+                    }
+            }
+        } else {
+            // ---- fused pool, one 32-channel half (fragment row f) at a time:
+            //      + bias, ReLU (pixels outside the conv output: 0) into
+            //      T[pixel][channel] (pitch kTPitch) in the wave's LDS buffer,
+            //      then per (channel, pooled row) the column maxima of the
+            //      window rows and the four pooled values.  Every T address is
+            //      a per-lane base plus a constant offset ----
+            float* tl = reinterpret_cast<float*>(pl);
+            bool pv[2];
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int oh = oh0 + prow[j], ow = ow0 + pcol[j];
+                pv[j] = 32 * j + (lane & 31) < S::PIX && static_cast<unsigned>(oh) < static_cast<unsigned>(g.OH) &&
+                        static_cast<unsigned>(ow) < static_cast<unsigned>(g.OW);
+            }
+            const int pr0 = (oh0 + 1) / 2, pc0 = (ow0 + 1) / 2;
+            const uint32_t pplane_out = static_cast<uint32_t>(g.PH) * g.PW;
+            const __amdgpu_buffer_rsrc_t ys =
+                make_rsrc(y + static_cast<int64_t>(n) * g.M * pplane_out, static_cast<uint32_t>(g.M) * pplane_out * 4);
+            const bool vec = (g.PW & 3) == 0;  // four pooled columns are one aligned 16-byte store
+#pragma unroll
+            for (int f = 0; f < 2; ++f) {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    float* trow = tl + (32 * j + (lane & 31)) * kTPitch + 4 * kg;
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int ch = 8 * (e >> 2) + (e & 3);  // + 4 kg in trow
+                        float v = acc[f][j][e] * 1.0f + bl[f * 32 + ch + 4 * kg];
+                        v = (pv[j] && v > 0.0f) ? v : 0.0f;
+                        trow[ch] = v;
+                    }
                 }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                // tasks (channel, pooled row): lane, and lane + 64 for lanes 0-31
+#pragma unroll
+                for (int round = 0; round < 2; ++round) {
+                    const int task = lane + 64 * round;
+                    if (task < 32 * kPoolTH) {
+                        const int ch = task & 31, pp = task >> 5;
+                        const float* tcol = tl + 2 * pp * S::TC * kTPitch + ch;
+                        float m[S::TC];
+#pragma unroll
+                        for (int b = 0; b < S::TC; ++b) {
+                            const float v0 = tcol[b * kTPitch];
+                            const float v1 = tcol[(S::TC + b) * kTPitch];
+                            const float v2 = tcol[(2 * S::TC + b) * kTPitch];
+                            m[b] = fmaxf(fmaxf(v0, v1), v2);
+                        }
+                        float q[kPoolTW];
+#pragma unroll
+                        for (int c = 0; c < kPoolTW; ++c) q[c] = fmaxf(fmaxf(m[2 * c], m[2 * c + 1]), m[2 * c + 2]);
+                        const int pr = pr0 + pp, cg = f * 32 + ch;
+                        const bool row_ok = pr < g.PH && cg < g.M;
+                        const uint32_t base = (static_cast<uint32_t>(cg) * pplane_out + pr * g.PW + pc0) * 4;
+                        if (vec) {
+                            u32x4_t qv;
+#pragma unroll
+                            for (int c = 0; c < kPoolTW; ++c) qv[c] = __float_as_uint(q[c]);
+                            __builtin_amdgcn_raw_buffer_store_b128(qv, ys, row_ok ? base : kOutside, 0, 0);
+                        } else {
+#pragma unroll
+                            for (int c = 0; c < kPoolTW; ++c)
+                                __builtin_amdgcn_raw_buffer_store_b32(
+                                    __float_as_uint(q[c]), ys, row_ok && pc0 + c < g.PW ? base + 4 * c : kOutside, 0,
+                                    0);
+                        }
+                    }
+                }
+                // the next half's (or tile's) writes come after these reads
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
         }
     }
 }
@@ -318,11 +428,17 @@ int stem_cu_count() {
     return cached[dev];
 }
 
-using Stem7x7 = StemShape<3, 7, 7, 2, 2>;  // the ResNet stem
+using Stem7x7 = StemShape<3, 7, 7, 2, 2, 4, 16>;  // the ResNet stem: 4 x 16 conv pixels per wave
+using Stem7x7Pool = StemShape<3, 7, 7, 2, 2, 2 * kPoolTH + 1, 2 * kPoolTW + 1>;  // with the 3x3/2 pool
+static_assert(Stem7x7Pool::WBUF >= kTWords, "the pool's staging table fits the wave's buffer");
 
+// Shapes the stem kernel takes: flags RELU, or RELU | MAXPOOL3X3S2 (the
+// pool: 3x3, stride 2, pad 1, floor).
 bool stem_geom(const tbn_conv2d_desc* d, int flags, StemGeom& g) {
     using S = Stem7x7;
-    if (!d || flags & ~TBN_EPI_RELU) return false;
+    if (!d || flags & ~(TBN_EPI_RELU | TBN_EPI_MAXPOOL3X3S2)) return false;
+    const bool pool = (flags & TBN_EPI_MAXPOOL3X3S2) != 0;
+    if (pool && !(flags & TBN_EPI_RELU)) return false;
     if (d->c != S::C || d->kh != S::KH || d->kw != S::KW || d->sh != S::SH || d->sw != S::SW || d->dh != 1 ||
         d->dw != 1 || d->m > kRows || d->m <= 0)
         return false;
@@ -332,8 +448,15 @@ bool stem_geom(const tbn_conv2d_desc* d, int flags, StemGeom& g) {
     g.N = int(d->n); g.H = int(d->h); g.W = int(d->w); g.M = int(d->m);
     g.ph = int(d->ph); g.pw = int(d->pw);
     g.OH = int(OH); g.OW = int(OW);
-    g.tiles_w = (g.OW + kTileW - 1) / kTileW;
-    g.tiles_img = ((g.OH + kTileH - 1) / kTileH) * g.tiles_w;
+    g.PH = pool ? (g.OH - 1) / 2 + 1 : 0;
+    g.PW = pool ? (g.OW - 1) / 2 + 1 : 0;
+    if (pool) {
+        g.tiles_w = (g.PW + kPoolTW - 1) / kPoolTW;
+        g.tiles_img = ((g.PH + kPoolTH - 1) / kPoolTH) * g.tiles_w;
+    } else {
+        g.tiles_w = (g.OW + S::TC - 1) / S::TC;
+        g.tiles_img = ((g.OH + S::TR - 1) / S::TR) * g.tiles_w;
+    }
     const int64_t tiles = static_cast<int64_t>(d->n) * g.tiles_img;
     // 32-bit offsets below 2^31: one input image, one output image (all 64
     // rows of a tile, also past M)
@@ -353,22 +476,27 @@ bool conv_stem_supported(const tbn_conv2d_desc* desc, int flags) {
     return stem_geom(desc, flags, g);
 }
 
-int conv_stem_run(const float* x, const tbn_conv2d_desc* desc, const float* w, const float* bias, int flags,
-                  float* y, hipStream_t s) {
-    StemGeom g;
-    TBN_REQUIRE(stem_geom(desc, flags, g), TBN_INVALID_SHAPE, "shape not handled by the stem conv kernel");
-    if (g.tiles == 0) return ok();
-    using S = Stem7x7;
+template <class S, bool POOL>
+int launch_stem(const float* x, const StemGeom& g, const float* w, const float* bias, float* y, hipStream_t s) {
     static bool attr_set = false;
     if (!attr_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&stem_conv_kernel<S>),
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&stem_conv_kernel<S, POOL>),
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
         if (e != hipSuccess) return fail(TBN_RUNTIME_ERROR, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
         attr_set = true;
     }
     const int blocks = static_cast<int>(std::min<int64_t>(ceil_div(g.tiles, kWaves), stem_cu_count()));
-    hipLaunchKernelGGL((stem_conv_kernel<S>), dim3(blocks), dim3(64 * kWaves), S::LDS, s, x, g, w, bias, y);
-    return check_launch("conv2d_f32 (stem)");
+    hipLaunchKernelGGL((stem_conv_kernel<S, POOL>), dim3(blocks), dim3(64 * kWaves), S::LDS, s, x, g, w, bias, y);
+    return check_launch(POOL ? "conv2d_f32 (stem + 3x3/2 max pool)" : "conv2d_f32 (stem)");
+}
+
+int conv_stem_run(const float* x, const tbn_conv2d_desc* desc, const float* w, const float* bias, int flags,
+                  float* y, hipStream_t s) {
+    StemGeom g;
+    TBN_REQUIRE(stem_geom(desc, flags, g), TBN_INVALID_SHAPE, "shape not handled by the stem conv kernel");
+    if (g.tiles == 0) return ok();
+    if (flags & TBN_EPI_MAXPOOL3X3S2) return launch_stem<Stem7x7Pool, true>(x, g, w, bias, y, s);
+    return launch_stem<Stem7x7, false>(x, g, w, bias, y, s);
 }
 
 }  // namespace tbn_hip

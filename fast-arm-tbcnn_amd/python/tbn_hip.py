@@ -33,6 +33,7 @@ EPI_NONE = 0
 EPI_RELU = 1
 EPI_BIAS_THEN_SCALE = 2
 EPI_MAXPOOL2X2 = 4
+EPI_MAXPOOL3X3S2 = 8
 NOALLOC_SCRATCH_BYTES = 16 << 20
 WEIGHTS_BINARY = 0
 WEIGHTS_TERNARY = 1
@@ -86,6 +87,7 @@ _SIGNATURES = {
     "tbn_hip_conv2d_f32_binary": ([_P, ctypes.POINTER(ConvDesc), _P, _I64, _I64, _P, _F32, _P, _I32, _P, _P], _I32),
     "tbn_hip_conv2d_f32_ternary": ([_P, ctypes.POINTER(ConvDesc), _P, _I64, _I64, _P, _F32, _P, _I32, _P, _P], _I32),
     "tbn_hip_conv2d_f32": ([_P, ctypes.POINTER(ConvDesc), _P, _P, _I32, _P, _P], _I32),
+    "tbn_hip_conv2d_f32_supported": ([ctypes.POINTER(ConvDesc), _I32], _I32),
     "tbn_hip_gemm_f32": ([_P, _P, _P, _I32, _I64, _I64, _I64, _F32, _F32, _I32, _I32, _I32, _P, _P], _I32),
     "tbn_hip_maxpool2d": ([_P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P,
                            ctypes.POINTER(ctypes.c_int64), _P], _I32),

@@ -943,6 +943,21 @@ struct TBNModel::Session::Impl {
                     absorb(static_cast<int>(i), r);
                 }
             }
+            // 3x3/2 pad-1 floor MaxPool after the fp32 stem conv with its Relu
+            // fused (the ResNet stem), when the library takes the shape
+            if (op.kind == OpKind::ConvF32 && op.groups == 1 && op.residual < 0 && (op.flags & TBN_EPI_RELU) &&
+                !(op.flags & TBN_EPI_MAXPOOL2X2)) {
+                int r = sole_reader(op.out);
+                if (r >= 0 && ops[r].kind == OpKind::MaxPool) {
+                    const Pool2DParams& p = ops[r].pool;
+                    if (p.kernel_h == 3 && p.kernel_w == 3 && p.stride_h == 2 && p.stride_w == 2 && p.pad_h == 1 &&
+                        p.pad_w == 1 && p.dilation_h == 1 && p.dilation_w == 1 && !p.ceil_mode &&
+                        tbn_hip_conv2d_f32_supported(&op.desc, op.flags | TBN_EPI_MAXPOOL3X3S2) == TBN_SUCCESS) {
+                        op.flags |= TBN_EPI_MAXPOOL3X3S2;
+                        absorb(static_cast<int>(i), r);
+                    }
+                }
+            }
             // 2x2/2 floor MaxPool (with or without a Relu either side) into Conv
             if (conv && op.residual < 0 && op.groups == 1 && op.kind != OpKind::ConvDepthwise) {
                 int r = sole_reader(op.out);

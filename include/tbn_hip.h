@@ -87,7 +87,11 @@ enum tbn_epilogue {
     TBN_EPI_BIAS_THEN_SCALE = 2, /* y = (acc + b) * s  (Session cached conv,  */
                                  /*  model.hpp:523-557); default y = acc*s + b */
                                  /*  (conv2d_binary_with_scales, conv2d.cpp:319-369) */
-    TBN_EPI_MAXPOOL2X2 = 4       /* conv only: fused 2x2 stride-2 max pool      */
+    TBN_EPI_MAXPOOL2X2 = 4,      /* conv only: fused 2x2 stride-2 max pool      */
+    TBN_EPI_MAXPOOL3X3S2 = 8     /* tbn_hip_conv2d_f32 with TBN_EPI_RELU, stem
+                                    shape only (3 input channels, 7x7, stride 2,
+                                    M <= 64): fused 3x3 stride-2 pad-1 floor max
+                                    pool (the ResNet stem's, model.hpp:577-629) */
 };
 
 /* Convolution geometry (NCHW input, [M, C, kh, kw] weights, groups = 1),
@@ -310,9 +314,16 @@ int tbn_hip_conv2d_tune_prepacked(int weights, const float* x, const tbn_conv2d_
 /* ---- fp32 layers and epilogue operators (Session support) ------------------ */
 
 /* fp32 Conv2D (tbn::conv2d, conv2d.cpp:78-192), weights fp32 [M, C, kh, kw];
- * flags: TBN_EPI_RELU, TBN_EPI_MAXPOOL2X2. */
+ * flags: TBN_EPI_RELU, TBN_EPI_MAXPOOL2X2, or TBN_EPI_RELU |
+ * TBN_EPI_MAXPOOL3X3S2 (y then [N, M, (OH-1)/2+1, (OW-1)/2+1]; other shapes
+ * return TBN_NOT_IMPLEMENTED). */
 int tbn_hip_conv2d_f32(const float* x, const tbn_conv2d_desc* desc, const float* w,
                        const float* bias, int flags, float* y, tbn_stream_t stream);
+/* TBN_SUCCESS when tbn_hip_conv2d_f32 takes this geometry and these flags
+ * (TBN_NOT_IMPLEMENTED for a fused 3x3/2 pool off the stem shape).  No
+ * counterpart in the reference (it has no fused pool); for a caller such as
+ * the Session deciding whether to fuse a MaxPool into the conv before it. */
+int tbn_hip_conv2d_f32_supported(const tbn_conv2d_desc* desc, int flags);
 /* ---- grouped convolution and BatchNormalization ---------------------------
  * The reference's conv2d_grouped / depthwise_conv2d throw for groups > 1
  * (conv2d.cpp:372-393) and it has no BatchNormalization; these are new.  A

@@ -55,3 +55,21 @@ def test_conv_weight_sizes_are_host_only():
     assert lib.tbn_hip_conv_weights_bytes(5, ctypes.byref(d), ctypes.byref(wb)) == tbn_hip.INVALID_ARGUMENT
     big = tbn_hip.conv_desc(1, 64, 200, 200, 8, 15, 15, 1, 1, 28, 28, 4, 4)  # patch cannot fit the LDS
     assert lib.tbn_hip_conv_weights_bytes(0, ctypes.byref(big), ctypes.byref(wb)) == tbn_hip.INVALID_SHAPE
+
+
+def test_fused_stem_pool_shape_rule():
+    """TBN_EPI_MAXPOOL3X3S2 is taken on the stem shape (3 channels, 7x7,
+    stride 2, M <= 64) with ReLU and refused (NOT_IMPLEMENTED) otherwise; the
+    query runs on the host."""
+    lib = tbn_hip.lib()
+    pool = tbn_hip.EPI_RELU | tbn_hip.EPI_MAXPOOL3X3S2
+    stem = tbn_hip.conv_desc(32, 3, 224, 224, 64, 7, 7, 2, 2, 3, 3)
+    assert lib.tbn_hip_conv2d_f32_supported(ctypes.byref(stem), pool) == tbn_hip.SUCCESS
+    assert lib.tbn_hip_conv2d_f32_supported(ctypes.byref(stem), tbn_hip.EPI_RELU) == tbn_hip.SUCCESS
+    # no ReLU, too many channels, another kernel size or stride
+    assert lib.tbn_hip_conv2d_f32_supported(ctypes.byref(stem), tbn_hip.EPI_MAXPOOL3X3S2) == tbn_hip.NOT_IMPLEMENTED
+    for d in [tbn_hip.conv_desc(1, 3, 64, 64, 65, 7, 7, 2, 2, 3, 3), tbn_hip.conv_desc(1, 4, 64, 64, 64, 7, 7, 2, 2, 3, 3),
+              tbn_hip.conv_desc(1, 3, 64, 64, 64, 5, 5, 2, 2, 2, 2), tbn_hip.conv_desc(1, 3, 64, 64, 64, 7, 7, 1, 1, 3, 3)]:
+        assert lib.tbn_hip_conv2d_f32_supported(ctypes.byref(d), pool) == tbn_hip.NOT_IMPLEMENTED
+        assert "stem shape" in tbn_hip.last_error()
+    assert lib.tbn_hip_conv2d_f32_supported(ctypes.byref(stem), 16) == tbn_hip.INVALID_ARGUMENT

@@ -308,6 +308,39 @@ def test_conv_small_layers(dev, orc, case, weights):
     assert np.array_equal(one.view(np.uint32), out[1:2].view(np.uint32))
 
 
+@pytest.mark.parametrize("case", [(2, 224, 224, 64), (1, 65, 47, 40), (3, 30, 34, 64), (1, 9, 9, 8),
+                                  (1, 40, 46, 64)])
+def test_conv_f32_stem_maxpool3x3s2_fused(dev, orc, case):
+    """The stem conv with ReLU and the 3x3/2 pad-1 max pool fused
+    (TBN_EPI_MAXPOOL3X3S2; the pool of model.hpp:577-629) equals the stem
+    conv with ReLU followed by the oracle's maxpool2d bit for bit: after the
+    ReLU every value is +0 or more and none is NaN, so the order the maximum
+    is taken in does not matter.  The input holds NaN, +-inf and -0.0; pooled
+    widths divisible by 4 take the 16-byte store path, the others 4-byte
+    stores; partial tiles at the bottom and right, M < 64."""
+    N, H, W, M = case
+    rng = np.random.default_rng(H * W + M)
+    x = rng.standard_normal((N, 3, H, W)).astype(np.float32)
+    flat = x.reshape(-1)
+    flat[rng.choice(flat.size, 6, replace=False)] = [np.nan, np.inf, -np.inf, -0.0, np.nan, 0.0]
+    w = (rng.standard_normal((M, 3, 7, 7)) * 0.1).astype(np.float32)
+    b = (rng.standard_normal(M) * 0.05).astype(np.float32)
+    d = tbn_hip.conv_desc(N, 3, H, W, M, 7, 7, 2, 2, 3, 3)
+    OH, OW = tbn_hip.conv_out_hw(d)
+    PH, PW = (OH - 1) // 2 + 1, (OW - 1) // 2 + 1
+    dx, dw, db = to_dev(x), to_dev(w), to_dev(b)
+    conv = empty((N, M, OH, OW), torch.float32)
+    tbn_hip.call("tbn_hip_conv2d_f32", P(dx), d, P(dw), P(db), tbn_hip.EPI_RELU, P(conv), None)
+    y = empty((N, M, PH, PW), torch.float32)
+    y.fill_(np.nan)  # every output is written
+    tbn_hip.call("tbn_hip_conv2d_f32", P(dx), d, P(dw), P(db), tbn_hip.EPI_RELU | tbn_hip.EPI_MAXPOOL3X3S2, P(y),
+                 None)
+    ref = orc.maxpool2d(host(conv), (3, 3), (2, 2), (1, 1))
+    assert ref.shape == (N, M, PH, PW)
+    got = host(y)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def test_conv_f32_stem_inf_stays_local(dev, orc):
     """An infinite input pixel reaches only the outputs whose 7x7 window
     holds it: the stem kernel's padded tap columns (kw = 7 of 8) and padded
