@@ -357,13 +357,18 @@ __global__ void __launch_bounds__(64 * kWaves) stem_conv_kernel(const float* __r
             const bool vec = (g.PW & 3) == 0;  // four pooled columns are one aligned 16-byte store
 #pragma unroll
             for (int f = 0; f < 2; ++f) {
+                // the half's biases first: read after the table writes, each
+                // would wait for the write before it (both are LDS)
+                float bv[16];
+#pragma unroll
+                for (int e = 0; e < 16; ++e) bv[e] = bl[f * 32 + 8 * (e >> 2) + (e & 3) + 4 * kg];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     float* trow = tl + (32 * j + (lane & 31)) * kTPitch + 4 * kg;
 #pragma unroll
                     for (int e = 0; e < 16; ++e) {
                         const int ch = 8 * (e >> 2) + (e & 3);  // + 4 kg in trow
-                        float v = acc[f][j][e] * 1.0f + bl[f * 32 + ch + 4 * kg];
+                        float v = acc[f][j][e] * 1.0f + bv[e];
                         v = (pv[j] && v > 0.0f) ? v : 0.0f;
                         trow[ch] = v;
                     }
