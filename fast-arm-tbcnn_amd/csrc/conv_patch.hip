@@ -59,6 +59,11 @@ struct PatchGeom {
     // 1: one LDS buffer (the next chunk waits in the staging registers and is
     // stored after a barrier), for twice the blocks per CU; 0: two buffers
     int single;
+    // 1: 2-D tiles of 8-pixel rows whose 32-pixel fragments take rows
+    // {0, 4, 1, 5} and {2, 6, 3, 7}: with a patch pitch of 2 mod 4 pixels
+    // (80-byte records) the two rows one 16-lane group reads then sit in
+    // disjoint LDS banks
+    int rowperm;
 };
 
 // Buffer resource (gfx9 word 3: raw dword addressing) over `bytes` from base;
@@ -106,6 +111,7 @@ __device__ __forceinline__ bool tile_pixel(const PatchGeom& g, int q0, int row0,
         } else {
             i = ql / Cfg::TW;
             j = ql - i * Cfg::TW;
+            if (Cfg::TW == 8 && g.rowperm) i = (i & ~3) / 2 + ((i >> 1) & 1) + 4 * (i & 1);
         }
         oh = row0 + i;
         ow = col0 + j;
@@ -742,6 +748,7 @@ size_t lds_bytes(const PatchGeom& g, int BM, bool ternary) {
 void fill_patch(PatchGeom& g, const TileChoice& c) {
     g.linear = c.linear;
     g.single = c.single;
+    g.rowperm = 0;
     int rows, cols;  // output rows / columns one tile's pixels span (at most)
     if (c.linear) {
         const int per = g.pool ? c.TH * c.TW / 4 : c.TH * c.TW;
@@ -776,6 +783,7 @@ void fill_patch(PatchGeom& g, const TileChoice& c) {
     };
     g.mul_patch = magic(static_cast<int64_t>(g.PHi) * g.PWi);
     g.mul_pwi = magic(g.PWi);
+    g.rowperm = (!c.linear && !g.pool && c.TH == 8 && c.TW == 8 && g.PWi % 4 == 2) ? 1 : 0;
 }
 
 // Tile menu: (BM, TH, TW, wave tile); TH x TW is also the pixel count of a
