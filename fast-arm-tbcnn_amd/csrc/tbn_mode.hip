@@ -6,17 +6,17 @@
 //   * tbn_hip_ternary_pack_f32 / tbn_hip_im2col_ternary_packed produce the
 //     reference's two row-major bit planes (TernaryMatrix::pack_from_float,
 //     im2col_ternary_packed), bit for bit.
-//   * The GEMM runs on v_mfma_i32_32x32x32_i8.  The ternary activations are
-//     expanded once per call into int8 rows T (-1 / 0 / +1, zero padded) with
-//     their row sums; the weights stay packed and each wave expands its own
-//     columns' bits to 0/1 bytes b in registers (3 VALU per 4 weights).  With
-//     w = 1 - 2b the exact result is C = rowsum(T) - 2 * (T . b), accumulated
-//     in int32 -- the value the reference forms as popcount(pos) -
-//     popcount(neg) per 64-bit word (GeMM/05-final/GeMM.cpp:160-252).
-//   * Block tile 128 rows x 512 columns, 8 waves of 128 x 64 (4 x 2 fragments),
-//     64 k per LDS buffer (two int8 MFMA slices), one barrier per step; rows
-//     of T and packed columns are read with buffer loads (out-of-range rows /
-//     columns read as zero).
+//   * The GEMM runs on the fp4 matrix cores
+//     (v_mfma_scale_f32_32x32x64_f8f6f4, unit scales): -1, 0 and +1 are exact
+//     E2M1 values, so every product is exact and every partial sum an integer
+//     below 2^24, exact in the fp32 accumulators -- the value the reference
+//     forms as popcount(pos) - popcount(neg) per 64-bit word
+//     (GeMM/05-final/GeMM.cpp:160-252).  One pass per call turns the
+//     activations (fp32 rows or bit planes) and the packed weight columns
+//     into k-contiguous fp4 rows (two values a byte).
+//   * Block tile 256 x 256, 8 waves of 128 x 64 (4 x 2 fragments), 256 k per
+//     LDS buffer; both operands go global -> LDS by buffer_load ... lds (rows
+//     past the matrix read as zero), one barrier per step.
 #include <type_traits>
 
 #include "common.hpp"
@@ -118,139 +118,193 @@ __global__ void im2col_ternary_kernel(const float* __restrict__ x, Im2colDims d,
 }
 
 // ---------------------------------------------------------------------------
-// Expansion to int8 rows + row sums (the GEMM's activation operand)
+// The fp4 operands of the GEMM
 // ---------------------------------------------------------------------------
 
-// Block-wide int32 sum (blockDim.x a multiple of 64, at most 1024).
-__device__ __forceinline__ int block_sum(int v, int* red) {
+// fp4 (E2M1) codes: +1 = 0x2, -1 = 0xA, 0 = 0x0
+constexpr uint32_t kF4Plus = 0x2u, kF4Minus = 0xAu;
+
+// Activation rows of the operand pass, one fp4 dword (8 values) per call.
+// fp32 rows ternarized at (lo, hi): v < lo -> -1, v > hi -> +1, else 0 (NaN
+// gives 0), zero beyond K (GeMM/05-final/GeMM.cpp:71-112 and
+// tbn-runtime/src/operators/quantized_gemm_neon.cpp:118-141 form the same
+// values as bit planes).
+struct RowsF32 {
+    const float* A;
+    int64_t lda;
+    int K;
+    float lo, hi;
+    bool vec;  // K, lda multiples of 4 and A 16-byte aligned
+    __device__ __forceinline__ uint32_t word(int64_t row, int k0) const {
+        const float* src = A + row * lda;
+        float v[8];
+        if (vec) {
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    int s = 0;
-    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) s += red[w];
-    return s;
+            for (int q = 0; q < 2; ++q) {
+                const float4 f = k0 + 4 * q < K ? *reinterpret_cast<const float4*>(src + k0 + 4 * q)
+                                                : make_float4(0, 0, 0, 0);
+                v[4 * q] = f.x, v[4 * q + 1] = f.y, v[4 * q + 2] = f.z, v[4 * q + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = k0 + e < K ? src[k0 + e] : 0.0f;
+        }
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const bool m = v[e] < lo, p = !m && v[e] > hi;
+            w |= (m ? kF4Minus : (p ? kF4Plus : 0u)) << (4 * e);
+        }
+        return w;
+    }
+};
+
+// The reference's two bit planes (row-major, n / 8 bytes a row): a value
+// with both bits set is 0, as in its popcount(pos) - popcount(neg)
+// (GeMM/05-final/GeMM.cpp:160-252).
+struct RowsPlanes {
+    const uint8_t* pos;
+    const uint8_t* neg;
+    int64_t row_bytes;
+    __device__ __forceinline__ uint32_t word(int64_t row, int k0) const {
+        const int64_t i = row * row_bytes + k0 / 8;
+        const uint32_t pb = pos[i], mb = neg[i];
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const bool p = (pb >> e) & 1u, m = (mb >> e) & 1u;
+            w |= (p && !m ? kF4Plus : (m && !p ? kF4Minus : 0u)) << (4 * e);
+        }
+        return w;
+    }
+};
+
+// 8 BinaryMatrix bits (bit 1 = -1) -> 8 fp4 codes: bit e moved to bit 4 e + 3
+// over the +1 code (0x2 | 0x8 = 0xA is -1).
+__device__ __forceinline__ uint32_t bits_word(uint32_t b) {
+    uint32_t x = b & 0xFFu;
+    x = (x | (x << 12)) & 0x000F000Fu;
+    x = (x | (x << 6)) & 0x03030303u;
+    x = (x | (x << 3)) & 0x11111111u;
+    return 0x22222222u | (x << 3);
 }
 
-// int8 byte of one ternary value from its plane bits.
-__device__ __forceinline__ uint32_t tern_byte(bool p, bool m) { return m ? 0xFFu : (p ? 0x01u : 0x00u); }
-
-// fp32 rows -> int8 T[row, 0..ldt) and rowsum[row]; one block per row.
-__global__ void ternarize_rows_kernel(const float* __restrict__ A, int64_t lda, int M, int K, int64_t ldt, float lo,
-                                      float hi, int8_t* __restrict__ T, int* __restrict__ rowsum) {
-    __shared__ int red[16];
-    for (int row = blockIdx.x; row < M; row += gridDim.x) {
-        const float* src = A + static_cast<int64_t>(row) * lda;
-        uint32_t* dst = reinterpret_cast<uint32_t*>(T + static_cast<int64_t>(row) * ldt);
-        int sum = 0;
-        // rows of whole float4s (K and lda multiples of 4, A 16-byte aligned):
-        // one vector load per output word
-        const bool vec = (K % 4 == 0) && (lda % 4 == 0) && (reinterpret_cast<uintptr_t>(A) % 16 == 0);
-        for (int64_t w = threadIdx.x; w < ldt / 4; w += blockDim.x) {
-            float v[4];
-            if (vec) {
-                const float4 f = 4 * w < K ? *reinterpret_cast<const float4*>(src + 4 * w) : make_float4(0, 0, 0, 0);
-                v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) v[e] = 4 * w + e < K ? src[4 * w + e] : 0.0f;
-            }
-            uint32_t word = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const bool m = v[e] < lo, p = !m && v[e] > hi;
-                sum += (p ? 1 : 0) - (m ? 1 : 0);
-                word |= tern_byte(p, m) << (8 * e);
-            }
-            dst[w] = word;
+// Both GEMM operands in one pass: items [0, a_items) are the activation
+// dwords T4[row, 0..wpr) (8 values each), the rest the weight columns, 32
+// bits of a column each (one 4-byte load, one 16-byte store into W4[col,
+// 0..k / 2)).  Indices fit 32 bits (checked on the host).
+template <class Act>
+__global__ void f4_operands_kernel(Act act, uint32_t a_items, uint32_t wpr, uint32_t* __restrict__ T4,
+                                   const uint8_t* __restrict__ bits, int64_t col_bytes, uint32_t wpc,
+                                   uint32_t w_items, uint32_t* __restrict__ W4) {
+    const uint32_t total = a_items + w_items;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+        if (i < a_items) {
+            const uint32_t row = i / wpr;
+            T4[i] = act.word(row, static_cast<int>(8 * (i - row * wpr)));
+        } else {
+            const uint32_t j = i - a_items;
+            const uint32_t c = j / wpc;
+            const uint32_t b = *reinterpret_cast<const uint32_t*>(bits + c * col_bytes + 4 * (j - c * wpc));
+            const u32x4_t out = {bits_word(b), bits_word(b >> 8), bits_word(b >> 16), bits_word(b >> 24)};
+            *reinterpret_cast<u32x4_t*>(W4 + 4 * static_cast<int64_t>(j)) = out;
         }
-        sum = block_sum(sum, red);
-        if (threadIdx.x == 0) rowsum[row] = sum;
     }
 }
 
-// Bit planes [M, n / 8] -> int8 T[row, 0..n) and rowsum[row]; one block per row.
-__global__ void planes_to_rows_kernel(const uint8_t* __restrict__ pos, const uint8_t* __restrict__ neg, int M,
-                                      int64_t n, int8_t* __restrict__ T, int* __restrict__ rowsum) {
-    __shared__ int red[16];
-    for (int row = blockIdx.x; row < M; row += gridDim.x) {
-        const uint8_t* rp = pos + static_cast<int64_t>(row) * (n / 8);
-        const uint8_t* rm = neg + static_cast<int64_t>(row) * (n / 8);
-        uint32_t* dst = reinterpret_cast<uint32_t*>(T + static_cast<int64_t>(row) * n);
-        int sum = 0;
-        for (int64_t w = threadIdx.x; w < n / 4; w += blockDim.x) {
-            const uint32_t pb = (rp[w >> 1] >> (4 * (w & 1))) & 0xFu;
-            const uint32_t mb = (rm[w >> 1] >> (4 * (w & 1))) & 0xFu;
-            uint32_t word = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const bool p = (pb >> e) & 1u, m = (mb >> e) & 1u;
-                // both bits set contributes 0 in the reference's formula
-                const bool pp = p && !m, mm = m && !p;
-                sum += (pp ? 1 : 0) - (mm ? 1 : 0);
-                word |= tern_byte(pp, mm) << (8 * e);
-            }
-            dst[w] = word;
-        }
-        sum = block_sum(sum, red);
-        if (threadIdx.x == 0) rowsum[row] = sum;
-    }
-}
-
 // ---------------------------------------------------------------------------
-// The int8 GEMM
+// The fp4 GEMM (the TBN product on the fp4 matrix cores)
 // ---------------------------------------------------------------------------
+//
+// -1, 0 and +1 are exact fp4 (E2M1) values: codes 0xA, 0x0 and 0x2.  With the
+// ternary activations and the +-1 weights both in fp4, every product is
+// exact and every partial sum is an integer of magnitude at most K <= 2^24,
+// so v_mfma_scale_f32_32x32x64_f8f6f4 (unit scales) accumulates C exactly in
+// fp32 (at twice the int8 MFMA rate).  Operands are
+// k-contiguous rows of nibbles, low nibble first: a lane's MFMA operand is
+// the 32 values k = 32 (lane / 32) .. +31 of its row or column, 16 bytes.
 
-struct TbnGemmArgs {
-    const int8_t* T;      // [M, ldt] ternary activations, zero beyond K
-    int64_t ldt;          // bytes per row (>= K, multiple of 16)
-    const int* rowsum;    // [M]
+struct F4GemmArgs {
+    const uint8_t* A;     // [M, lda] fp4 activations, two per byte, zero beyond K
+    int64_t lda;          // bytes per row (a multiple of 16)
+    const uint8_t* B;     // [n_alloc, ldb] fp4 weights (+-1), one row per output column
+    int64_t ldb;
+    int n_alloc;          // rows present in B
     int M, N, K;          // K = shared dimension, a multiple of 64
-    const uint8_t* bits;  // BinaryMatrix columns (col_bytes each, bit 1 = -1)
-    int64_t col_bytes;
-    int N_pad;            // columns present in bits
     void* out;            // int32 or float [M, ldo]
     int64_t ldo;
     float scale;          // float output: out = float(C) * scale
 };
 
-template <int BR_, int BC_, int WR_, int WC_, int KS_>
-struct I8Cfg {
+template <int BR_, int BC_, int WR_, int WC_, int KS_, int NBUF_, bool EARLY_>
+struct F4Cfg {
     static constexpr int BR = BR_, BC = BC_, WR = WR_, WC = WC_;
-    static constexpr int KS = KS_;        // k per step (one barrier): KS / 128 16-byte weight words per column
-    static constexpr int SL = KS / 32;    // MFMA slices per step
-    static constexpr int WPS = KS / 32;   // 32-bit weight words per column per step
-    static constexpr int KROW = KS + 16;  // bytes per LDS row: conflict-free 16-byte fragment reads
+    static constexpr int KS = KS_;                  // k per step (one barrier): KS / 64 MFMA slices
+    static constexpr int NBUF = NBUF_;              // LDS buffers: loads run NBUF - 1 steps ahead
+    static constexpr bool EARLY = EARLY_;           // a slice's fragment reads all issued before its MFMAs
+    static constexpr int SL = KS / 64;
+    static_assert(SL % 2 == 0, "fragment registers alternate by slice");
+    static constexpr int RB = KS / 2;               // bytes of a row per step
+    static constexpr int PARTS = RB / 16;           // 16-byte parts of a row per step
+    static_assert(PARTS == 4 || PARTS == 8 || PARTS == 16, "swizzle");
     static constexpr int WAVES_R = BR / WR, WAVES_C = BC / WC;
-    static constexpr int NT = 64 * WAVES_R * WAVES_C;
+    static constexpr int WAVES = WAVES_R * WAVES_C;
+    static constexpr int NT = 64 * WAVES;
     static constexpr int FR = WR / 32, FC = WC / 32;
-    static constexpr int TPR = NT / BR;   // threads per A row
-    static constexpr int ALD = KS / TPR / 16;  // 16-byte A loads per thread per step
-    static_assert(TPR * ALD * 16 == KS && KS % 128 == 0, "a step's A tile is whole 16-byte loads per thread");
+    static constexpr int BUF = (BR + BC) * RB;      // bytes of one LDS buffer (A rows, then B rows)
+    static constexpr int LOADS = BUF / 1024 / WAVES;  // 1 KB direct-to-LDS loads per wave per step
+    static_assert(LOADS * WAVES * 1024 == BUF && (BR * RB) % 1024 == 0, "tile");
+    static_assert(NBUF >= 2 && NBUF <= 4 && NBUF * BUF <= 160 * 1024 && LOADS * (NBUF - 2) <= 63, "LDS / vmcnt");
 };
 
-using I8Wide = I8Cfg<128, 512, 128, 64, 128>;
+// 256 x 256 blocks of 8 waves (2 x 4), each 128 rows x 64 columns (4 x 2
+// fragments); both operands staged through LDS, so a weight row serves the
+// block's two row waves and an activation row its four column waves.  256 k
+// per step (four MFMA slices, 64 KB), two buffers: one LDS tile per CU.
+// (Four buffers of 128 k measured 3 % slower at 4096^3.)
+using F4Wide = F4Cfg<256, 256, 128, 64, 256, 2, false>;
 
-// 4 weight bits (bit i = weight k0 + i, 1 means -1) -> 4 bytes b_i in {0, 1}:
-// the multiply copies bit i to bit 8i without carries.
-__device__ __forceinline__ uint32_t spread4(uint32_t nib) { return __umul24(nib, 0x204081u) & 0x01010101u; }
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
 
+__device__ __forceinline__ f32x16_t mfma_f4(i32x4_t a, i32x4_t b, f32x16_t c) {
+    const i32x8_t a8 = {a[0], a[1], a[2], a[3], 0, 0, 0, 0};
+    const i32x8_t b8 = {b[0], b[1], b[2], b[3], 0, 0, 0, 0};
+    // formats 4 / 4: fp4 (E2M1) A and B; scales 2^(127 - 127) = 1
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, 4, 4, 0, 127, 0, 127);
+}
+
+// buffer_load_dwordx4 ... lds: lane l's 16 bytes at voffset + soffset go to
+// LDS at dst + 16 l.
+__device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rs, uint8_t* dst, int voffset, int soffset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16, voffset, soffset,
+                                             0, 0);
+}
+
+// LDS slot (16 bytes) of part q of tile row r: rows of P parts, the part
+// index XOR-swizzled so the 16-byte fragment reads of 16 consecutive rows
+// (one part each) hit distinct banks.  A 256-byte bank line holds 16 / P
+// rows; the rows sharing a line position differ in r / (16 / P).
+template <int P>
+__device__ __forceinline__ int f4_swz(int r) { return (r / (16 / P)) & (P - 1); }
+template <int P>
+__device__ __forceinline__ int f4_slot(int r, int q) { return r * P + (q ^ f4_swz<P>(r)); }
+
+// Operands go global -> LDS with buffer_load_dwordx4 ... lds (no registers,
+// no LDS store instructions): a wave's load writes 64 consecutive 16-byte
+// slots, so each lane loads the global part that belongs in its slot.
 template <class Cfg, bool FLOAT_OUT>
-__global__ void __launch_bounds__(Cfg::NT)
-tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * Cfg::BR * Cfg::KROW];
-    __shared__ __attribute__((aligned(16))) int rs_lds[Cfg::BR];
-    constexpr int KS = Cfg::KS;
+__global__ void __launch_bounds__(Cfg::NT) tbn_f4_gemm_kernel(F4GemmArgs p, int tiles_r, int tiles_c) {
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::NBUF * Cfg::BUF];
+    constexpr int RB = Cfg::RB;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wr = wave / Cfg::WAVES_C;
     const int wc = wave % Cfg::WAVES_C;
     const int h = lane >> 5;
 
+    // the tiles of one XCD (blockIdx % 8) are consecutive in t
     const int total = tiles_r * tiles_c;
     int t = blockIdx.x;
     if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
@@ -259,198 +313,167 @@ tbn_i8_gemm_kernel(TbnGemmArgs p, int tiles_r, int tiles_c) {
     const int r0 = tr * Cfg::BR;
     const int c0 = tc * Cfg::BC;
 
-    if (tid < Cfg::BR) rs_lds[tid] = (r0 + tid < p.M) ? p.rowsum[r0 + tid] : 0;
-
-    const int ar = tid / Cfg::TPR, ag = tid % Cfg::TPR;
+    // rows past M / columns past n_alloc read as zero (buffer range)
     const __amdgpu_buffer_rsrc_t a_rs =
-        make_rsrc(p.T + static_cast<int64_t>(r0) * p.ldt, static_cast<uint64_t>(p.M - r0) * p.ldt);
-    const int a_voff = ar * static_cast<int>(p.ldt) + ag * 16 * Cfg::ALD;
+        make_rsrc(p.A + static_cast<int64_t>(r0) * p.lda, static_cast<uint64_t>(p.M - r0) * p.lda);
     const __amdgpu_buffer_rsrc_t b_rs =
-        make_rsrc(p.bits + static_cast<int64_t>(c0) * p.col_bytes,
-                  static_cast<uint64_t>(p.N_pad - c0) * static_cast<uint64_t>(p.col_bytes));
-    int b_voff[Cfg::FC];
+        make_rsrc(p.B + static_cast<int64_t>(c0) * p.ldb,
+                  c0 < p.n_alloc ? static_cast<uint64_t>(p.n_alloc - c0) * p.ldb : 0);
+    // load i of this wave fills slots [64 (wave * LOADS + i), + 64) of a buffer:
+    // A rows first, then B rows; lane -> (row, stored part) -> global part
+    int voff[Cfg::LOADS];
+    bool is_a[Cfg::LOADS];
 #pragma unroll
-    for (int j = 0; j < Cfg::FC; ++j)
-        b_voff[j] = (wc * Cfg::WC + j * 32 + (lane & 31)) * static_cast<int>(p.col_bytes);
-
-    // K is a multiple of 64: a last step of 64 runs two of its four slices
-    // (the data loaded past K for the other two is never used)
-    // K is a multiple of 64: the last step runs K % KS / 32 of its slices
-    // (the data loaded past K for the others is never used)
-    constexpr int SL = Cfg::SL, WPS = Cfg::WPS;
-    const int steps = (p.K + KS - 1) / KS;
-    const int last_slices = (p.K % KS) ? (p.K % KS) / 32 : SL;
-
-    i32x4_t areg[Cfg::ALD];
-    uint32_t bw[Cfg::FC][WPS], bwn[Cfg::FC][WPS];
-    auto load_a = [&](int s) {
+    for (int i = 0; i < Cfg::LOADS; ++i) {
+        const int slot = 64 * (wave * Cfg::LOADS + i) + lane;
+        const int row_all = slot / Cfg::PARTS;  // row of the A + B tile
+        const bool a = (wave * Cfg::LOADS + i) * (64 / Cfg::PARTS) < Cfg::BR;  // a load's rows lie on one side
+        const int r = a ? row_all : row_all - Cfg::BR;
+        const int q = (slot % Cfg::PARTS) ^ f4_swz<Cfg::PARTS>(row_all);
+        is_a[i] = a;
+        voff[i] = r * static_cast<int>(a ? p.lda : p.ldb) + q * 16;
+    }
+    auto load = [&](int s, int u) {
 #pragma unroll
-        for (int h2 = 0; h2 < Cfg::ALD; ++h2)
-            areg[h2] = __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16 * h2, s * KS, 0);
-    };
-    auto load_b = [&](int s, uint32_t (&w)[Cfg::FC][WPS]) {
-#pragma unroll
-        for (int j = 0; j < Cfg::FC; ++j)
-#pragma unroll
-            for (int q = 0; q < WPS / 4; ++q) {
-                const u32x4_t x = __builtin_bit_cast(
-                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], s * (KS / 8) + 16 * q, 0));
-#pragma unroll
-                for (int d = 0; d < 4; ++d) w[j][4 * q + d] = x[d];
-            }
-    };
-    const int a_store = ar * Cfg::KROW + ag * 16 * Cfg::ALD;
-    auto store_a = [&](int b) {
-#pragma unroll
-        for (int h2 = 0; h2 < Cfg::ALD; ++h2)
-            *reinterpret_cast<i32x4_t*>(lds + b * Cfg::BR * Cfg::KROW + a_store + 16 * h2) = areg[h2];
+        for (int i = 0; i < Cfg::LOADS; ++i)
+            load_lds16(is_a[i] ? a_rs : b_rs, lds + u * Cfg::BUF + 1024 * (wave * Cfg::LOADS + i), voff[i], s * RB);
     };
 
-    i32x16_t acc[Cfg::FR][Cfg::FC];
+    f32x16_t acc[Cfg::FR][Cfg::FC];
 #pragma unroll
     for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0;
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    const int a_frag = (wr * Cfg::WR + (lane & 31)) * Cfg::KROW + h * 16;
-
-    // Step s: four MFMA slices of 32 k on LDS buffer s & 1; meanwhile step
-    // s+1's A goes to the other buffer and step s+2's A and s+1's W words are
-    // fetched.  Software pipeline across slices: slice kk+1's weight bits are
-    // expanded and its A fragments read from LDS while slice kk's MFMAs run
-    // (the next step's slice 0 comes from the next step's words and, after
-    // the barrier, from the other LDS buffer).
-    i32x4_t bfr[2][Cfg::FC];
-    i32x4_t afr[2][Cfg::FR];
-    auto expand_b = [&](const uint32_t (&w)[Cfg::FC][WPS], int kk, i32x4_t (&bf)[Cfg::FC]) {
-#pragma unroll
-        for (int j = 0; j < Cfg::FC; ++j) {
-            const uint32_t word = w[j][kk];
-#pragma unroll
-            for (int d = 0; d < 4; ++d)
-                bf[j][d] = static_cast<int>(spread4(__builtin_amdgcn_ubfe(word, 16 * h + 4 * d, 4)));
-        }
-    };
-    auto read_a = [&](int u, int kk, i32x4_t (&af)[Cfg::FR]) {
+    const int arow = wr * Cfg::WR + (lane & 31);              // + 32 i
+    const int brow = Cfg::BR + wc * Cfg::WC + (lane & 31);    // + 32 j
+    auto read_frags = [&](int u, int sl, i32x4_t (&af)[Cfg::FR], i32x4_t (&bf)[Cfg::FC]) {
+        const int q = 2 * sl + h;
 #pragma unroll
         for (int i = 0; i < Cfg::FR; ++i)
-            af[i] = *reinterpret_cast<const i32x4_t*>(lds + u * Cfg::BR * Cfg::KROW + i * 32 * Cfg::KROW + a_frag +
-                                                      kk * 32);
-    };
-    auto mfmas = [&](const i32x4_t (&af)[Cfg::FR], const i32x4_t (&bf)[Cfg::FC]) {
-#pragma unroll
-        for (int i = 0; i < Cfg::FR; ++i)
-#pragma unroll
-            for (int j = 0; j < Cfg::FC; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
-    };
-
-    load_a(0);
-    load_b(0, bw);
-    store_a(0);
-    if (steps > 1) {
-        load_a(1);
-        load_b(1, bwn);
-    }
-    expand_b(bw, 0, bfr[0]);
-    __syncthreads();
-    int s = 0;
-    // full steps that have a successor: four slices, the last one prepares the
-    // next step's slice 0 weights (its A fragments follow the barrier)
-    for (; s + 1 < steps; ++s) {
-        const int u = s & 1;
-        read_a(u, 0, afr[0]);
-#pragma unroll
-        for (int kk = 0; kk < SL; ++kk) {
-            if (kk + 1 < SL) {
-                read_a(u, kk + 1, afr[(kk + 1) & 1]);
-                expand_b(bw, kk + 1, bfr[(kk + 1) & 1]);
-            } else {
-                expand_b(bwn, 0, bfr[0]);
-            }
-            mfmas(afr[kk & 1], bfr[kk & 1]);
-            // per slice: the next slice's 4 fragment reads up front, then 8
-            // MFMAs, each followed by 3 of the 24 expansion VALU
-            if (kk + 1 < SL) __builtin_amdgcn_sched_group_barrier(0x100, Cfg::FR, 0);
-#pragma unroll
-            for (int q = 0; q < Cfg::FR * Cfg::FC; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);
-            }
-        }
-        store_a(u ^ 1);
+            af[i] = *reinterpret_cast<const i32x4_t*>(lds + u * Cfg::BUF + 16 * f4_slot<Cfg::PARTS>(arow + 32 * i, q));
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j)
+            bf[j] = *reinterpret_cast<const i32x4_t*>(lds + u * Cfg::BUF + 16 * f4_slot<Cfg::PARTS>(brow + 32 * j, q));
+    };
+    // MFMAs of one slice from fragment registers af / bf, with the LDS reads
+    // issued just before (the next slice's fragments) spread between them
+    auto mfmas = [&](const i32x4_t (&af)[Cfg::FR], const i32x4_t (&bf)[Cfg::FC], bool reads) {
 #pragma unroll
-            for (int d = 0; d < WPS; ++d) bw[j][d] = bwn[j][d];
-        if (s + 2 < steps) {
-            load_a(s + 2);
-            load_b(s + 2, bwn);
-        }
-        __syncthreads();
-    }
-    // the last step: an even number of slices (K is a multiple of 64)
-    {
-        const int u = s & 1;
-        read_a(u, 0, afr[0]);
+        for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
-        for (int kk = 0; kk < SL; ++kk) {
-            if (kk >= last_slices) break;
-            if (kk + 1 < last_slices) {
-                read_a(u, kk + 1, afr[(kk + 1) & 1]);
-                expand_b(bw, kk + 1, bfr[(kk + 1) & 1]);
+            for (int j = 0; j < Cfg::FC; ++j) acc[i][j] = mfma_f4(af[i], bf[j], acc[i][j]);
+        if (reads) {
+            if (Cfg::EARLY) {
+                __builtin_amdgcn_sched_group_barrier(0x100, Cfg::FR + Cfg::FC, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, Cfg::FR * Cfg::FC, 0);
+            } else {
+#pragma unroll
+                for (int q = 0; q < Cfg::FR + Cfg::FC; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, Cfg::FR * Cfg::FC - Cfg::FR - Cfg::FC, 0);
             }
-            mfmas(afr[kk & 1], bfr[kk & 1]);
         }
+    };
+
+    // Step s computes from LDS buffer s % NBUF while the loads of steps up to
+    // s + NBUF - 1 fly straight into the others.  The fragments of slice
+    // sl + 1 are read during slice sl; the step's barrier sits before its last
+    // slice's MFMAs, so the next step's first fragments are read while they
+    // run.  Before the barrier a wave has waited for its loads of step s + 1
+    // and for its own LDS reads of buffer s % NBUF, which the loads issued
+    // after the barrier (for step s + NBUF) overwrite.
+    const int steps = (p.K + Cfg::KS - 1) / Cfg::KS;
+    const int last_slices = (p.K % Cfg::KS) ? (p.K % Cfg::KS) / 64 : Cfg::SL;
+#pragma unroll
+    for (int t = 0; t < Cfg::NBUF - 1; ++t)
+        if (t < steps) load(t, t);
+    // this wave's loads still allowed in flight once step t's have landed:
+    // those of the newer steps t + 1 .. min(steps - 1, t + NBUF - 2)
+    auto wait_step = [&](int t) {
+        const int newer = min(steps - 1, t + Cfg::NBUF - 2) - t;
+        if (newer >= 2) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * Cfg::LOADS) : "memory");
+        else if (newer == 1) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(Cfg::LOADS) : "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    };
+    // The barriers are bare s_barrier: a workgroup fence would wait for every
+    // load in flight, the later steps' too.
+    wait_step(0);
+    __builtin_amdgcn_s_barrier();
+    i32x4_t af[2][Cfg::FR], bf[2][Cfg::FC];
+    read_frags(0, 0, af[0], bf[0]);
+    // a full step s < steps - 1; STEADY: steps s + 1 .. s + NBUF - 2 all exist
+    auto full_step = [&](int s, auto steady_c) {
+        constexpr bool STEADY = decltype(steady_c)::value;
+        const int u = s % Cfg::NBUF;
+        if (STEADY) load(s + Cfg::NBUF - 1, (s + Cfg::NBUF - 1) % Cfg::NBUF);
+#pragma unroll
+        for (int sl = 0; sl + 1 < Cfg::SL; ++sl) {
+            read_frags(u, sl + 1, af[(sl + 1) & 1], bf[(sl + 1) & 1]);
+            mfmas(af[sl & 1], bf[sl & 1], true);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (STEADY) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((Cfg::NBUF - 2) * Cfg::LOADS) : "memory");
+        else wait_step(s + 1);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        read_frags((s + 1) % Cfg::NBUF, 0, af[0], bf[0]);
+        mfmas(af[1], bf[1], true);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    int s = 0;
+    for (; s + Cfg::NBUF - 1 < steps; ++s) full_step(s, std::true_type{});
+    for (; s + 1 < steps; ++s) full_step(s, std::false_type{});
+    // the last step: its first fragments are in af[0] / bf[0]
+    const int u = s % Cfg::NBUF;
+#pragma unroll
+    for (int sl = 0; sl < Cfg::SL; ++sl) {
+        if (sl >= last_slices) break;
+        if (sl + 1 < last_slices) read_frags(u, sl + 1, af[(sl + 1) & 1], bf[(sl + 1) & 1]);
+        mfmas(af[sl & 1], bf[sl & 1], false);
     }
 
-    // epilogue: C = rowsum - 2 * acc; rows of register e: i*32 + 8*(e/4) + 4*h + e%4
+    // epilogue: C (an exact integer in fp32); rows of register e: i*32 + 8*(e/4) + 4*h + e%4
 #pragma unroll
-    for (int i = 0; i < Cfg::FR; ++i) {
-        int rsum[16];
-#pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {
-            const i32x4_t r = *reinterpret_cast<const i32x4_t*>(rs_lds + wr * Cfg::WR + i * 32 + 8 * e4 + 4 * h);
-            rsum[4 * e4] = r[0], rsum[4 * e4 + 1] = r[1], rsum[4 * e4 + 2] = r[2], rsum[4 * e4 + 3] = r[3];
-        }
+    for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             const int n = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int m = r0 + wr * Cfg::WR + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-                const int c = rsum[e] - 2 * acc[i][j][e];
                 if (m < p.M && n < p.N) {
                     if (FLOAT_OUT)
-                        static_cast<float*>(p.out)[static_cast<int64_t>(m) * p.ldo + n] = static_cast<float>(c) * p.scale;
+                        static_cast<float*>(p.out)[static_cast<int64_t>(m) * p.ldo + n] = acc[i][j][e] * p.scale;
                     else
-                        static_cast<int*>(p.out)[static_cast<int64_t>(m) * p.ldo + n] = c;
+                        static_cast<int*>(p.out)[static_cast<int64_t>(m) * p.ldo + n] = static_cast<int>(acc[i][j][e]);
                 }
             }
         }
-    }
 }
 
-int launch_i8_gemm(const TbnGemmArgs& a, bool float_out, hipStream_t stream) {
-    using Cfg = I8Wide;
+int launch_f4_gemm(const F4GemmArgs& a, bool float_out, hipStream_t stream) {
+    using Cfg = F4Wide;
+    TBN_REQUIRE(a.K <= (1 << 24), TBN_INVALID_SHAPE, "TBN GEMM: shared dimension above 2^24 (fp32 sums inexact)");
     const int tiles_r = static_cast<int>(tbn_hip::ceil_div(a.M, Cfg::BR));
     const int tiles_c = static_cast<int>(tbn_hip::ceil_div(a.N, Cfg::BC));
     if (float_out)
-        hipLaunchKernelGGL((tbn_i8_gemm_kernel<Cfg, true>), dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, stream, a,
+        hipLaunchKernelGGL((tbn_f4_gemm_kernel<Cfg, true>), dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, stream, a,
                            tiles_r, tiles_c);
     else
-        hipLaunchKernelGGL((tbn_i8_gemm_kernel<Cfg, false>), dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, stream, a,
+        hipLaunchKernelGGL((tbn_f4_gemm_kernel<Cfg, false>), dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, stream, a,
                            tiles_r, tiles_c);
-    return tbn_hip::check_launch("tbn_gemm");
+    return tbn_hip::check_launch("tbn_gemm (fp4)");
 }
 
 int grid_for(int64_t items, int threads) {
     return static_cast<int>(std::min<int64_t>(tbn_hip::ceil_div(std::max<int64_t>(items, 1), threads), 65536));
 }
 
-// Stream-ordered scratch for the int8 rows and row sums.
 // Device scratch of one call (the stream workspace, see common.hpp).
 struct Scratch {
     void* ptr = nullptr;
@@ -460,13 +483,6 @@ struct Scratch {
     ~Scratch() { tbn_hip::release_workspace(ptr, temporary, stream); }
 };
 
-}  // namespace
-
-extern "C" {
-
-}  // extern "C"
-
-namespace {
 
 template <typename T>
 int ternary_pack(const T* A, int64_t lda, int64_t M, int64_t K, int64_t rows, int64_t cols, float lo, float hi,
@@ -486,6 +502,20 @@ int ternary_pack(const T* A, int64_t lda, int64_t M, int64_t K, int64_t rows, in
     return tbn_hip::check_launch(what);
 }
 
+// One launch of f4_operands_kernel: `rows` activation rows and `cols` weight
+// columns (col_bytes apart), both over the first k (a multiple of 64) values.
+template <class Act>
+int launch_f4_operands(const Act& act, int64_t rows, int64_t k, uint32_t* T4, const uint8_t* bits, int64_t col_bytes,
+                       int64_t cols, uint32_t* W4, hipStream_t s, const char* what) {
+    const int64_t a_items = rows * (k / 8), w_items = cols * (k / 32);
+    TBN_REQUIRE(a_items + w_items < (int64_t{1} << 31), TBN_INVALID_SHAPE,
+                "operands beyond 2^31 fp4 dwords (8 GiB) in one call");
+    hipLaunchKernelGGL(f4_operands_kernel<Act>, dim3(grid_for(a_items + w_items, 256)), dim3(256), 0, s, act,
+                       static_cast<uint32_t>(a_items), static_cast<uint32_t>(k / 8), T4, bits, col_bytes,
+                       static_cast<uint32_t>(k / 32), static_cast<uint32_t>(w_items), W4);
+    return tbn_hip::check_launch(what);
+}
+
 // Ternary rows (pos / neg planes, m rows of n / 8 bytes) times BinaryMatrix
 // columns: int32 C, or float(C) * scale when `float_out`, into out [m, ldo]
 // for the first `cols` columns.
@@ -493,17 +523,18 @@ int planes_gemm(const uint8_t* pos, const uint8_t* neg, const uint8_t* bits, int
                 int64_t bit_cols, bool float_out, float scale, void* out, int64_t ldo, hipStream_t s) {
     Scratch scr;
     scr.stream = s;
-    const size_t tbytes = static_cast<size_t>(m) * n;
-    if (int rc = scr.get(tbytes + static_cast<size_t>(m) * 4 + 16)) return rc;
-    int8_t* T = static_cast<int8_t*>(scr.ptr);
-    int* rowsum = reinterpret_cast<int*>(static_cast<uint8_t*>(scr.ptr) + ((tbytes + 15) / 16) * 16);
-    hipLaunchKernelGGL(planes_to_rows_kernel, dim3(static_cast<int>(std::min<int64_t>(m, 65536))), dim3(256), 0, s,
-                       pos, neg, static_cast<int>(m), n, T, rowsum);
-    int rc = tbn_hip::check_launch("tbn_gemm (planes)");
+    const size_t tbytes = (static_cast<size_t>(m) * (n / 2) + 255) / 256 * 256;
+    const size_t wbytes = static_cast<size_t>(bit_cols) * (n / 2);
+    if (int rc = scr.get(tbytes + wbytes)) return rc;
+    uint32_t* T4 = static_cast<uint32_t*>(scr.ptr);
+    uint32_t* W4 = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(scr.ptr) + tbytes);
+    int rc = launch_f4_operands(RowsPlanes{pos, neg, n / 8}, m, n, T4, bits, n / 8, bit_cols, W4, s,
+                                "tbn_gemm (fp4 operands)");
     if (rc != TBN_SUCCESS) return rc;
-    TbnGemmArgs a{T, n, rowsum, static_cast<int>(m), static_cast<int>(cols), static_cast<int>(n), bits, n / 8,
-                  static_cast<int>(bit_cols), out, ldo, scale};
-    return launch_i8_gemm(a, float_out, s);
+    F4GemmArgs a{reinterpret_cast<const uint8_t*>(T4), n / 2, reinterpret_cast<const uint8_t*>(W4), n / 2,
+                 static_cast<int>(bit_cols), static_cast<int>(m), static_cast<int>(cols), static_cast<int>(n), out,
+                 ldo, scale};
+    return launch_f4_gemm(a, float_out, s);
 }
 
 }  // namespace
@@ -596,17 +627,19 @@ int tbn_hip_qlinear_matmul_binary_tbn(const float* A, int64_t lda, int64_t M, in
     }
     Scratch scr;
     scr.stream = s;
-    const size_t tbytes = static_cast<size_t>(M) * K_pad;
-    if (int rc = scr.get(tbytes + static_cast<size_t>(M) * 4 + 16)) return rc;
-    int8_t* T = static_cast<int8_t*>(scr.ptr);
-    int* rowsum = reinterpret_cast<int*>(static_cast<uint8_t*>(scr.ptr) + ((tbytes + 15) / 16) * 16);
-    hipLaunchKernelGGL(ternarize_rows_kernel, dim3(static_cast<int>(std::min<int64_t>(M, 65536))), dim3(256), 0, s,
-                       A, lda, static_cast<int>(M), static_cast<int>(K), K_pad, lo, hi, T, rowsum);
-    int rc = tbn_hip::check_launch("qlinear_matmul_binary_tbn (ternarize)");
+    const size_t tbytes = (static_cast<size_t>(M) * (K_pad / 2) + 255) / 256 * 256;
+    const size_t wbytes = static_cast<size_t>(N_pad) * (K_pad / 2);
+    if (int rc = scr.get(tbytes + wbytes)) return rc;
+    uint32_t* T4 = static_cast<uint32_t*>(scr.ptr);
+    uint32_t* W4 = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(scr.ptr) + tbytes);
+    const bool vec = K % 4 == 0 && lda % 4 == 0 && reinterpret_cast<uintptr_t>(A) % 16 == 0;
+    int rc = launch_f4_operands(RowsF32{A, lda, static_cast<int>(K), lo, hi, vec}, M, K_pad, T4, packed, K_pad / 8,
+                                N_pad, W4, s, "qlinear_matmul_binary_tbn (fp4 operands)");
     if (rc != TBN_SUCCESS) return rc;
-    TbnGemmArgs a{T, K_pad, rowsum, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K_pad), packed,
-                  K_pad / 8, static_cast<int>(N_pad), out, ldo, scale};
-    return launch_i8_gemm(a, true, s);
+    F4GemmArgs a{reinterpret_cast<const uint8_t*>(T4), K_pad / 2, reinterpret_cast<const uint8_t*>(W4), K_pad / 2,
+                 static_cast<int>(N_pad), static_cast<int>(M), static_cast<int>(N), static_cast<int>(K_pad), out,
+                 ldo, scale};
+    return launch_f4_gemm(a, true, s);
 }
 
 }  // extern "C"
