@@ -431,7 +431,8 @@ int tbn_hip_im2col_ternary_packed(const float* x, const tbn_conv2d_desc* desc, i
  * ternary rows (pos / neg planes, m x n/8 bytes) times the BinaryMatrix
  * columns `bits` (k columns of n/8 bytes).  n % 64 == 0 (the reference needs
  * n % 128 == 0 and m, k multiples of its micro tiles; no tiling constraint
- * here).  Uses a stream-ordered temporary of m*(n+4) bytes. */
+ * here), n < 2^24.  Uses the stream workspace for the fp4 operand rows:
+ * m*n/2 (rounded up to 256) + k*n/2 bytes. */
 int tbn_hip_tbn_gemm(const uint8_t* pos, const uint8_t* neg, const uint8_t* bits, int64_t m,
                      int64_t n, int64_t k, int32_t* C, tbn_stream_t stream);
 /* The extraction and scaling of qlinear_matmul_binary_blocked_prepacked
@@ -444,7 +445,8 @@ int tbn_hip_tbn_gemm_scaled(const uint8_t* pos, const uint8_t* neg, const uint8_
 /* qlinear_matmul_binary as the reference computes it (quantized_gemm_neon.cpp:
  * 160-243,380-430): out[M, N] = float(sum_k t(A[m,k]) * w[k,n]) * scale with
  * t the ternarization at (lo, hi) and w the packed BinaryMatrix (K_pad % 64
- * == 0, N_pad >= N).  Uses a stream-ordered temporary of M*(K_pad+4) bytes. */
+ * == 0, K_pad < 2^24, N_pad >= N).  Uses the stream workspace for the fp4
+ * operand rows: M*K_pad/2 (rounded up to 256) + N_pad*K_pad/2 bytes. */
 int tbn_hip_qlinear_matmul_binary_tbn(const float* A, int64_t lda, int64_t M, int64_t K,
                                       const uint8_t* packed, int64_t K_pad, int64_t N,
                                       int64_t N_pad, float scale, float lo, float hi, float* out,
