@@ -21,7 +21,9 @@
 //
 // Blocks are dealt round-robin over the 8 XCDs; the tile order puts the
 // BC-column tiles of one BR-row band of A on the same XCD, so the band is
-// fetched from HBM once into that XCD's L2 and read there by its tiles.
+// fetched from HBM once into that XCD's L2 and read there by its tiles.  The
+// mid-size tiles give each XCD the rectangle of tiles with the fewest A and W
+// bytes to fetch (whole row bands, or e.g. 2 bands x half the columns).
 #include <algorithm>
 #include <cstdlib>
 #include <string>
@@ -435,7 +437,7 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
 template <class Cfg, bool TERNARY, bool SPLIT>
 __global__ void __launch_bounds__(Cfg::NT)
 gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per_split, float* partial,
-                int* counters) {
+                int* counters, int xcd_cols) {
     __shared__ __attribute__((aligned(16))) uint16_t lds_all[Cfg::KG * 2 * 3 * Cfg::BR * Cfg::KROW];
     constexpr int kPlane = Cfg::BR * Cfg::KROW;  // bf16 per plane
     constexpr int KS = Cfg::KS;
@@ -453,14 +455,26 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
     uint32_t ones;
     asm volatile("v_mov_b32 %0, 0x3f803f80" : "=v"(ones));
 
-    // tile order: the tiles of one XCD (blockIdx % 8) are consecutive in t,
-    // and consecutive t share a row band of A; split-K blocks are split-major
+    // tile order (split-K blocks are split-major): XCD x = blockIdx % 8 owns a
+    // rectangle of tiles -- with xcd_cols = R, the XCDs form an (8 / R) x R
+    // grid over the tile grid (host-checked to divide it) -- so a row band of
+    // A and a column tile of W are fetched into few XCDs' L2; with R = 1 an
+    // XCD's tiles are whole row bands
     const int total = tiles_r * tiles_c;
     const int split = SPLIT ? static_cast<int>(blockIdx.x) / total : 0;
     int t = static_cast<int>(blockIdx.x) - split * total;
-    if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
-    const int tr = t / tiles_c;
-    const int tc = t - tr * tiles_c;
+    int tr, tc;
+    if (xcd_cols > 1) {
+        const int x = t % 8, j = t / 8;
+        const int rb = tiles_r * xcd_cols / 8, cb = tiles_c / xcd_cols;  // rectangle: rb row bands x cb tiles
+        tr = (x / xcd_cols) * rb + j / cb;
+        tc = (x % xcd_cols) * cb + j % cb;
+        t = tr * tiles_c + tc;
+    } else {
+        if (total % 8 == 0) t = (t % 8) * (total / 8) + t / 8;
+        tr = t / tiles_c;
+        tc = t - tr * tiles_c;
+    }
     const int r0 = tr * Cfg::BR;
     const int c0 = tc * Cfg::BC;
     const int all_steps = (p.K + KS - 1) / KS;
@@ -893,11 +907,12 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
 struct WidePlan {
     int cfg = 0;      // 0 Wide, 1 WideSmall, 2 WideMid
     int tiles_r = 0, tiles_c = 0, steps = 0, splits = 1, per = 0;
+    int xcd_cols = 1;  // mid-size tiles: XCD grid columns (gemm_mid_kernel's tile order)
     int64_t blocks() const { return static_cast<int64_t>(tiles_r) * tiles_c * splits; }
 };
 
 template <class Cfg>
-WidePlan plan_for(int cfg, int M, int N, int K) {
+WidePlan plan_for(int cfg, int M, int N, int K, bool ternary) {
     WidePlan w;
     w.cfg = cfg;
     w.tiles_r = static_cast<int>(tbn_hip::ceil_div(M, Cfg::BR));
@@ -916,24 +931,38 @@ WidePlan plan_for(int cfg, int M, int N, int K) {
     }
     w.per = (w.steps + sp - 1) / sp;
     w.splits = (w.steps + w.per - 1) / w.per;  // splits that own at least one step
+    if (Cfg::DEEP && tiles % 8 == 0) {
+        // the XCD rectangle with the fewest A and W bytes to fetch per XCD (ties
+        // to the narrower): config 3 (8 x 32 tiles) takes 2 x 16 per XCD, 3 MB
+        // against 4.5 MB for whole row bands (31.0 -> 30.2 us); config 2
+        // (32 x 8 tiles) keeps whole row bands
+        const double a_band = static_cast<double>(Cfg::BR) * K * 4;
+        const double w_tile = static_cast<double>(Cfg::BC) * K / (ternary ? 4 : 8);
+        double best = 0.0;
+        for (int r = 1; r <= 8; r *= 2) {
+            if ((w.tiles_r * r) % 8 || w.tiles_c % r) continue;
+            const double bytes = (w.tiles_r * r / 8) * a_band + (w.tiles_c / r) * w_tile;
+            if (r == 1 || bytes < best) best = bytes, w.xcd_cols = r;
+        }
+    }
     return w;
 }
 
 // WideMid needs an even step count (its two K groups take equal halves).
 bool mid_ok(int K) { return tbn_hip::ceil_div(K, WideMid::KS) % 2 == 0; }
 
-WidePlan choose_plan(int M, int N, int K) {
+WidePlan choose_plan(int M, int N, int K, bool ternary) {
     const int forced = tbn_hip::tuning(TBN_TUNE_GEMM_TILE);
-    if (forced == 0) return plan_for<Wide>(0, M, N, K);
-    if (forced == 1) return plan_for<WideSmall>(1, M, N, K);
-    if (forced == 2 && mid_ok(K)) return plan_for<WideMid>(2, M, N, K);
-    const WidePlan big = plan_for<Wide>(0, M, N, K);
+    if (forced == 0) return plan_for<Wide>(0, M, N, K, ternary);
+    if (forced == 1) return plan_for<WideSmall>(1, M, N, K, ternary);
+    if (forced == 2 && mid_ok(K)) return plan_for<WideMid>(2, M, N, K, ternary);
+    const WidePlan big = plan_for<Wide>(0, M, N, K, ternary);
     if (big.blocks() >= 128) return big;
     if (forced != 1 && mid_ok(K)) {
-        const WidePlan mid = plan_for<WideMid>(2, M, N, K);
+        const WidePlan mid = plan_for<WideMid>(2, M, N, K, ternary);
         if (mid.blocks() >= 256 && mid.steps >= 4) return mid;
     }
-    return plan_for<WideSmall>(1, M, N, K);
+    return plan_for<WideSmall>(1, M, N, K, ternary);
 }
 
 // Kernel variants: the large tile on gemm_wide_kernel, the mid-size (DEEP)
@@ -953,12 +982,12 @@ void launch_wide(const tbn_hip::WideGemmArgs& a, const WidePlan& w, float* part,
         if constexpr (Cfg::KG == 1) {
             if (w.splits > 1) {
                 hipLaunchKernelGGL((gemm_mid_kernel<Cfg, TERNARY, true>), grid, dim3(Cfg::NT), 0, stream, a,
-                                   w.tiles_r, w.tiles_c, w.per, part, counters);
+                                   w.tiles_r, w.tiles_c, w.per, part, counters, w.xcd_cols);
                 return;
             }
         }
         hipLaunchKernelGGL((gemm_mid_kernel<Cfg, TERNARY, false>), grid, dim3(Cfg::NT), 0, stream, a, w.tiles_r,
-                           w.tiles_c, w.per, nullptr, nullptr);
+                           w.tiles_c, w.per, nullptr, nullptr, w.xcd_cols);
     }
 }
 
@@ -974,7 +1003,7 @@ void launch_plan(const tbn_hip::WideGemmArgs& a, const WidePlan& w, float* part,
 namespace tbn_hip {
 
 bool gemm_wide_fits(const WideGemmArgs& a, bool ternary) {
-    const WidePlan w = choose_plan(a.M, a.N, a.K);
+    const WidePlan w = choose_plan(a.M, a.N, a.K, ternary);
     const int waves = w.cfg == 1 ? 4 : 8;
     const int bc = w.cfg == 0 ? 512 : 128;
     // shapes that give at least half the chip one wave per SIMD
@@ -987,7 +1016,7 @@ bool gemm_wide_fits(const WideGemmArgs& a, bool ternary) {
 }
 
 int gemm_wide(const WideGemmArgs& a, bool ternary, hipStream_t stream) {
-    const WidePlan w = choose_plan(a.M, a.N, a.K);
+    const WidePlan w = choose_plan(a.M, a.N, a.K, ternary);
     const char* what = ternary ? "gemm_f32_ternary (wide)" : "gemm_f32_binary (wide)";
     void* part = nullptr;
     int* counters = nullptr;
