@@ -112,7 +112,7 @@ def test_tbn_gemm_golden_64_padded(dev, orc):
 
 
 @pytest.mark.parametrize("m,n,k", [(16, 128, 8), (48, 256, 40), (160, 512, 136), (528, 1024, 600), (64, 192, 72),
-                                   (128, 320, 104)])
+                                   (128, 320, 104), (296, 2112, 520)])
 def test_tbn_gemm_matches_oracle(dev, orc, m, n, k):
     rng = np.random.default_rng(m + n + k)
     A = (rng.standard_normal((m, n)) * 0.2).astype(np.float32)
