@@ -287,6 +287,10 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
             }
         }
         __syncthreads();
+        // no instruction crosses a step boundary: the scheduler would otherwise
+        // hoist the next step's split of A above this step's barrier, next to
+        // the loads of its data, and wait there for them (vmcnt(0) each step)
+        __builtin_amdgcn_sched_barrier(0);
     };
 
     // prologue: step s0 split into buffer 0, step s0+1 in flight, W words of
