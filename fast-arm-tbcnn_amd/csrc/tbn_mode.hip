@@ -437,21 +437,27 @@ __global__ void __launch_bounds__(Cfg::NT) tbn_f4_gemm_kernel(F4GemmArgs p, int 
         mfmas(af[sl & 1], bf[sl & 1], false);
     }
 
-    // epilogue: C (an exact integer in fp32); rows of register e: i*32 + 8*(e/4) + 4*h + e%4
+    // epilogue: C (an exact integer in fp32); rows of register e: i*32 +
+    // 8*(e/4) + 4*h + e%4.  Buffer stores over this block's rows [r0, M):
+    // rows past M fall outside the resource and columns past N get an offset
+    // outside it, so no store is behind a branch (ldo < 2^21, host-checked).
+    const __amdgpu_buffer_rsrc_t o_rs =
+        make_rsrc(static_cast<uint8_t*>(p.out) + static_cast<int64_t>(r0) * p.ldo * 4,
+                  static_cast<uint64_t>(p.M - r0) * p.ldo * 4);
+    const int ldo4 = static_cast<int>(p.ldo) * 4;
 #pragma unroll
     for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             const int n = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
+            const int row = wr * Cfg::WR + i * 32 + 4 * h;
+            const uint32_t voff = n < p.N ? static_cast<uint32_t>(row * ldo4 + n * 4) : 0x80000000u;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int m = r0 + wr * Cfg::WR + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (m < p.M && n < p.N) {
-                    if (FLOAT_OUT)
-                        static_cast<float*>(p.out)[static_cast<int64_t>(m) * p.ldo + n] = acc[i][j][e] * p.scale;
-                    else
-                        static_cast<int*>(p.out)[static_cast<int64_t>(m) * p.ldo + n] = static_cast<int>(acc[i][j][e]);
-                }
+                const int soff = (8 * (e >> 2) + (e & 3)) * ldo4;
+                const uint32_t bits = FLOAT_OUT ? __float_as_uint(acc[i][j][e] * p.scale)
+                                                : static_cast<uint32_t>(static_cast<int>(acc[i][j][e]));
+                __builtin_amdgcn_raw_buffer_store_b32(bits, o_rs, voff, soff, 0);
             }
         }
 }
@@ -459,6 +465,7 @@ __global__ void __launch_bounds__(Cfg::NT) tbn_f4_gemm_kernel(F4GemmArgs p, int 
 int launch_f4_gemm(const F4GemmArgs& a, bool float_out, hipStream_t stream) {
     using Cfg = F4Wide;
     TBN_REQUIRE(a.K <= (1 << 24), TBN_INVALID_SHAPE, "TBN GEMM: shared dimension above 2^24 (fp32 sums inexact)");
+    TBN_REQUIRE(a.ldo < (1 << 21), TBN_INVALID_SHAPE, "TBN GEMM: output row stride of 2^21 elements or more");
     const int tiles_r = static_cast<int>(tbn_hip::ceil_div(a.M, Cfg::BR));
     const int tiles_c = static_cast<int>(tbn_hip::ceil_div(a.N, Cfg::BC));
     if (float_out)
