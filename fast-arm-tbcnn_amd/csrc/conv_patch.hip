@@ -176,6 +176,9 @@ struct PatchEpi {
     const float* residual;
     int flags;
     float* partial;  // split-K: raw sums [split][N][M][OH * OW] instead of y (null: no split)
+    // split-K with tile counters (zero on entry, left zero): the last block of
+    // each tile adds the splits and runs the epilogue; null: a reduce kernel does
+    int* counters;
 };
 
 // bf16 elements of one LDS buffer: three planes of patch + 1 pixel records
@@ -555,9 +558,15 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     }
     if (epi.partial) {
         // split-K (never with the pool, host-checked): raw sums of this
-        // block's chunks into split sp's plane set
-        const __amdgpu_buffer_rsrc_t p_rs =
-            make_rsrc(epi.partial + static_cast<int64_t>(sp) * g.N * g.M * plane + obase, obytes);
+        // block's chunks into split sp's plane set.  With tile counters the
+        // sums go through at device scope (cache policy SC1: to the memory
+        // side, never a stale line of another XCD's L2), the barrier's wait
+        // for the stores orders them before the count, and the last block of
+        // the tile to count itself in adds the splits in split order (as the
+        // reduce kernel does) and runs the epilogue below.
+        constexpr int kDeviceScope = 16;
+        const int64_t split_elems = static_cast<int64_t>(g.N) * g.M * plane;
+        const __amdgpu_buffer_rsrc_t p_rs = make_rsrc(epi.partial + sp * split_elems + obase, obytes);
 #pragma unroll
         for (int f = 0; f < Cfg::FR; ++f)
 #pragma unroll
@@ -569,9 +578,32 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                     uint32_t v;
                     asm volatile("v_mov_b32 %0, %1" : "=v"(v) : "v"(acc[f][j][e]));
                     __builtin_amdgcn_raw_buffer_store_b32(v, p_rs, voff[j] + (f * 32 + 8 * (e >> 2) + (e & 3)) * plane4,
-                                                          0, 0);
+                                                          0, kDeviceScope);
                 }
-        return;
+        if (!epi.counters) return;
+        __syncthreads();  // every wave's stores complete (and the patch buffers are free)
+        int* is_last = reinterpret_cast<int*>(lds);  // no static LDS: the dynamic size may be the maximum
+        if (tid == 0)
+            *is_last = __hip_atomic_fetch_add(epi.counters + bid, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       g.splits - 1;
+        __syncthreads();
+        if (!*is_last) return;
+        for (int s2 = 0; s2 < g.splits; ++s2) {
+            const __amdgpu_buffer_rsrc_t rs = make_rsrc(epi.partial + s2 * split_elems + obase, obytes);
+#pragma unroll
+            for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+                for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const float v = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(
+                                       rs, voff[j] + (f * 32 + 8 * (e >> 2) + (e & 3)) * plane4, 0, kDeviceScope));
+                        acc[f][j][e] = s2 == 0 ? v : acc[f][j][e] + v;
+                    }
+        }
+        // ready for the next launch on this workspace
+        if (tid == 0) __hip_atomic_store(epi.counters + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // v' = (v + a) * s + b with (a, b) = (bias, 0) for bias-then-scale, else (0, bias)
     const bool bts = (epi.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
@@ -1091,7 +1123,7 @@ int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
 
 int conv_patch_dispatch(int weights, const float* x, const tbn_conv2d_desc* desc, PatchGeom& g,
                         const uint8_t* conv_weights, int64_t col_bytes, int m_alloc, const PatchEpi& epi,
-                        hipStream_t s, bool tune);
+                        hipStream_t s, bool tune, bool* finished);
 
 // Bytes of split-K partial sums a call with this geometry needs (0 when K is
 // not split).
@@ -1130,7 +1162,7 @@ int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, con
     const int64_t Kc = static_cast<int64_t>(g.chunks) * g.taps * kChunk;
     const int64_t col_bytes = Kc / (weights == TBN_WEIGHTS_BINARY ? 8 : 4);
     const int m_alloc = int((desc->m + 7) / 8 * 8);
-    PatchEpi epi{y, scale, alpha, bias, residual, flags, nullptr};
+    PatchEpi epi{y, scale, alpha, bias, residual, flags, nullptr, nullptr};
     void* part = nullptr;
     bool temporary = false;
     const int64_t part_bytes = conv_patch_partial_bytes(g);
@@ -1141,14 +1173,17 @@ int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, con
                             std::to_string(part_bytes));
             part = scratch;
         } else {
-            rc = tbn_hip::stream_workspace(s, static_cast<size_t>(part_bytes), part, temporary);
+            // the stream workspace also brings the tile counters of the
+            // in-kernel split-K finish
+            rc = tbn_hip::stream_workspace(s, static_cast<size_t>(part_bytes), part, temporary, &epi.counters);
             if (rc) return rc;
         }
         epi.partial = static_cast<float*>(part);
     }
-    rc = conv_patch_dispatch(weights, x, desc, g, conv_weights, col_bytes, m_alloc, epi, s, tune);
+    bool finished = false;
+    rc = conv_patch_dispatch(weights, x, desc, g, conv_weights, col_bytes, m_alloc, epi, s, tune, &finished);
     if (part) {
-        if (rc == TBN_SUCCESS && !tune) {
+        if (rc == TBN_SUCCESS && !tune && !finished) {
             const int64_t total = static_cast<int64_t>(g.N) * g.M * g.OH * g.OW;
             const int blocks = static_cast<int>(std::min<int64_t>(tbn_hip::ceil_div(total, 256), 4096));
             PatchEpi fin = epi;
@@ -1164,19 +1199,28 @@ int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, con
 
 int conv_patch_dispatch(int weights, const float* x, const tbn_conv2d_desc* desc, PatchGeom& g,
                         const uint8_t* conv_weights, int64_t col_bytes, int m_alloc, const PatchEpi& epi,
-                        hipStream_t s, bool tune) {
+                        hipStream_t s, bool tune, bool* finished) {
+    // tile timing launches without the in-kernel split-K finish
+    PatchEpi e = epi;
+    if (tune) e.counters = nullptr;
+    if (finished) *finished = false;
     int rc;
     TileChoice tc;
     if (weights == TBN_WEIGHTS_TERNARY) {
-        if (tune) return tune_tile<true>(desc, g, x, conv_weights, col_bytes, m_alloc, epi, s);
-        rc = select_tile<true>(desc, g, epi, tc);
-        if (rc) return rc;
-        return dispatch_patch<true>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, epi, s);
+        if (tune) return tune_tile<true>(desc, g, x, conv_weights, col_bytes, m_alloc, e, s);
+        rc = select_tile<true>(desc, g, e, tc);
+    } else {
+        if (tune) return tune_tile<false>(desc, g, x, conv_weights, col_bytes, m_alloc, e, s);
+        rc = select_tile<false>(desc, g, e, tc);
     }
-    if (tune) return tune_tile<false>(desc, g, x, conv_weights, col_bytes, m_alloc, epi, s);
-    rc = select_tile<false>(desc, g, epi, tc);
     if (rc) return rc;
-    return dispatch_patch<false>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, epi, s);
+    // one counter per tile of a split
+    const int64_t tiles = static_cast<int64_t>(g.N) * g.tiles_img * ((g.M + tc.BM - 1) / tc.BM);
+    if (tiles > tbn_hip::kWorkspaceCounters) e.counters = nullptr;
+    rc = weights == TBN_WEIGHTS_TERNARY ? dispatch_patch<true>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, e, s)
+                                        : dispatch_patch<false>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, e, s);
+    if (finished) *finished = e.partial && e.counters;
+    return rc;
 }
 
 }  // namespace
