@@ -141,9 +141,10 @@ inline int make_geom(const tbn_conv2d_desc* d, int flags, ConvGeom& g) {
 
 namespace tbn_hip {
 // The patch conv path (conv_patch.hip): whether it handles `desc`, and a run
-// fed with reference-layout packed weights, re-ordered into a stream-ordered
-// temporary for the call, or, when `scratch` is given, into its first bytes
-// with the split-K partial sums after them (no allocation at all).
+// fed with reference-layout packed weights, re-ordered into the stream
+// workspace for the call (a stream-ordered temporary while the stream
+// captures), or, when `scratch` is given, into its first bytes with the
+// split-K partial sums after them (no allocation at all).
 bool conv_patch_supported(const tbn_conv2d_desc* desc);
 int conv_patch_from_reference(int weights, const float* x, const tbn_conv2d_desc* desc, const uint8_t* packed,
                               int64_t K_pad, int64_t N_pad, const float* scale, float alpha, const float* bias,

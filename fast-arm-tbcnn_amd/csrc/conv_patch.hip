@@ -1137,7 +1137,8 @@ int64_t conv_patch_partial_bytes(const PatchGeom& g) {
 // the fastest is cached for later calls (y is written by every tile).
 int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, const uint8_t* conv_weights,
                    const float* scale, float alpha, const float* bias, const float* residual, int flags, float* y,
-                   hipStream_t s, bool tune = false, void* scratch = nullptr, int64_t scratch_bytes = 0) {
+                   hipStream_t s, bool tune = false, void* scratch = nullptr, int64_t scratch_bytes = 0,
+                   int* counters = nullptr) {
     TBN_REQUIRE(weights == TBN_WEIGHTS_BINARY || weights == TBN_WEIGHTS_TERNARY, TBN_INVALID_ARGUMENT,
                 "unknown weights kind");
     TBN_REQUIRE((flags & ~(TBN_EPI_RELU | TBN_EPI_BIAS_THEN_SCALE | TBN_EPI_MAXPOOL2X2)) == 0,
@@ -1172,6 +1173,7 @@ int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, con
                         "conv scratch holds " + std::to_string(scratch_bytes) + " bytes; this geometry needs " +
                             std::to_string(part_bytes));
             part = scratch;
+            epi.counters = counters;  // the scratch's owner may bring tile counters
         } else {
             // the stream workspace also brings the tile counters of the
             // in-kernel split-K finish
@@ -1255,6 +1257,30 @@ int conv_patch_from_reference(int weights, const float* x, const tbn_conv2d_desc
                                 cw + wspan, scratch_bytes - wspan);
         return rc;
     }
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    const bool capturing = hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone;
+    if (!capturing) {
+        // the stream workspace: the re-ordered weights, the split-K sums after
+        // them, and the tile counters of the in-kernel split-K finish
+        PatchGeom g;
+        int rc = make_patch_geom(desc, flags, g);
+        if (rc) return rc;
+        const int64_t wspan = (wbytes + 255) / 256 * 256;
+        const int64_t bytes = wspan + conv_patch_partial_bytes(g);
+        void* ws = nullptr;
+        int* counters = nullptr;
+        bool temporary = false;
+        rc = stream_workspace(s, static_cast<size_t>(bytes), ws, temporary, &counters);
+        if (rc) return rc;
+        uint8_t* cw = static_cast<uint8_t*>(ws);
+        rc = tbn_hip_pack_conv_weights(weights, packed, K_pad, N_pad, desc, cw, s);
+        if (rc == TBN_SUCCESS)
+            rc = conv_patch_run(weights, x, desc, cw, scale, alpha, bias, residual, flags, y, s, false, cw + wspan,
+                                bytes - wspan, counters);
+        release_workspace(ws, temporary, s);
+        return rc;
+    }
+    // under capture: a stream-ordered allocation recorded with the call
     void* buf = nullptr;
     hipError_t e = hipMallocAsync(&buf, static_cast<size_t>(wbytes), s);
     if (e != hipSuccess) {
