@@ -10,10 +10,12 @@
 // once per block instead of once per tap, and the chunk's global loads are in
 // flight during the previous chunk's kh*kw K steps of MFMAs.
 //
-// Weights use the conv layout k' = ((c / 32) * taps + tap) * 32 + c % 32 (taps =
-// kh*kw), made once from the reference's packed columns by
-// tbn_hip_pack_conv_weights; the block stages the chunk's 32-bit (binary) or
-// 64-bit (ternary) words [tap][channel] into LDS next to the patch, and each
+// Weights use the conv layout: one 32-bit (binary) or 64-bit (ternary) word
+// per (chunk, tap, output channel) holds the 32 channels c % 32 of that
+// chunk and tap, words ordered [chunk * taps + tap][channel] (taps = kh*kw),
+// so the lanes of a staging load read consecutive words.  It is made once from
+// the reference's packed columns by tbn_hip_pack_conv_weights; the block
+// stages the chunk's words [tap][channel] into LDS next to the patch, and each
 // lane decodes its channel's word to bf16 +-1 / 0 in registers.  The inner
 // loop touches only LDS.  Output channels are the MFMA rows, tile pixels the columns; with
 // the fused 2x2 max pool the pixels are enumerated window by window so a window
@@ -299,8 +301,9 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
         const int item = tid + it * Cfg::NT;
         const int ml = item % Cfg::BM;
         const int tap = item / Cfg::BM;
-        const bool ok = item < witems;
-        woff[it] = ok ? static_cast<uint32_t>(m0 + ml) * static_cast<uint32_t>(col_bytes) + tap * kWordBytes
+        const bool ok = item < witems && m0 + ml < m_alloc;
+        woff[it] = ok ? (static_cast<uint32_t>(tap) * static_cast<uint32_t>(m_alloc) + static_cast<uint32_t>(m0 + ml)) *
+                            kWordBytes
                       : kOutside;
         wslot[it] = (ok ? item : witems) * kWordHalves;
     }
@@ -309,7 +312,7 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
 
     auto load_chunk = [&](int ch) {
         const uint32_t cofs = static_cast<uint32_t>(ch * kChunk) * HW4;
-        const uint32_t wofs_ch = static_cast<uint32_t>(ch * g.taps) * kWordBytes;
+        const uint32_t wofs_ch = static_cast<uint32_t>(ch * g.taps) * static_cast<uint32_t>(m_alloc) * kWordBytes;
 #pragma unroll
         for (int it = 0; it < kMaxItems; ++it) {
             if (it < per_thread) {
@@ -711,14 +714,25 @@ __device__ __forceinline__ bool conv_k_to_ref(const ConvWeightDims& d, int64_t k
 
 // One thread per output byte; padding channels and columns get +1 (bit 0),
 // which meets zero activations.
+// Output byte t of the conv layout, words of `wb` bytes ordered
+// [step][channel] (step = chunk * taps + tap): its channel m and its byte kb
+// within that channel's k' order (32 k' per step).
+__device__ __forceinline__ void conv_layout_byte(const ConvWeightDims& d, int64_t t, int wb, int& m, int64_t& kb) {
+    const int64_t word = t / wb;
+    const int64_t step = word / d.M_alloc;
+    m = static_cast<int>(word - step * d.M_alloc);
+    kb = step * wb + (t - word * wb);
+}
+
 __global__ void reorder_conv_binary_kernel(const uint8_t* __restrict__ ref, ConvWeightDims d,
                                            uint8_t* __restrict__ out) {
     const int64_t bpc = d.Kc / 8;
     const int64_t total = static_cast<int64_t>(d.M_alloc) * bpc;
     for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
          t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int m = static_cast<int>(t / bpc);
-        const int64_t kb = t - m * bpc;
+        int m;
+        int64_t kb;
+        conv_layout_byte(d, t, 4, m, kb);
         uint32_t byte = 0;
         if (m < d.M) {
             const uint8_t* col = ref + m * (d.K_pad / 8);
@@ -738,8 +752,9 @@ __global__ void reorder_conv_ternary_kernel(const uint8_t* __restrict__ ref, Con
     const int64_t total = static_cast<int64_t>(d.M_alloc) * bpc;
     for (int64_t t = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; t < total;
          t += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        const int m = static_cast<int>(t / bpc);
-        const int64_t kb = t - m * bpc;
+        int m;
+        int64_t kb;
+        conv_layout_byte(d, t, 8, m, kb);
         uint32_t byte = 0x55u;
         if (m < d.M) {
             const uint8_t* col = ref + m * (d.K_pad / 4);

@@ -259,10 +259,13 @@ int tbn_hip_conv2d_f32_quantized(int weights, const float* x, const tbn_conv2d_d
  * For inputs of 16 or more channels the conv kernels behind the entry points
  * above stage each block's input patch (32 channels at a time, split into the
  * three bf16 parts) in LDS and run every tap from it.  Their weights use the
- * "conv layout": column m holds Kc = ceil(C/32) * kh*kw * 32 values in the
- * order k' = ((c / 32) * kh*kw + r*kw + s) * 32 + c % 32, in the reference's
- * encoding (bit 1 = -1, or the 2-bit code); channels >= C are +1 / 0 and meet
- * zero activations.  The entry points above re-order the reference layout
+ * "conv layout": for each step = (c / 32) * kh*kw + r*kw + s, one word per
+ * output channel m (ceil8(M) of them) holds the 32 channels c % 32 of that
+ * step, bit (or 2-bit code) c % 32 of the word, in the reference's encoding
+ * (bit 1 = -1, or the 2-bit code); words are 4 bytes (binary) or 8 bytes
+ * (ternary) and ordered [step][m], so that neighbouring channels' words sit
+ * next to each other.  Channels >= C, and channels m >= M, are +1 / 0 and
+ * meet zero activations.  The entry points above re-order the reference layout
  * into a stream-ordered temporary (hipMallocAsync) on every call; a caller
  * that runs a layer many times (the Session) packs once and calls
  * tbn_hip_conv2d_f32_prepacked, which allocates nothing. */

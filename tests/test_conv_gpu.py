@@ -124,8 +124,9 @@ def test_conv_f32(dev, orc, case):
 
 
 def _np_conv_layout_bits(wbytes, M_alloc):
-    """Closed form of the conv weight layout: column m, bit
-    k' = ((c // 32) * kh*kw + r*kw + s) * 32 + c % 32 set iff -1."""
+    """Closed form of the conv weight layout: one 4-byte word per
+    (step = (c // 32) * kh*kw + r*kw + s, output channel m), words ordered
+    [step][m], bit c % 32 of the word set iff the weight is -1."""
     M, C, kh, kw = wbytes.shape
     chunks = (C + 31) // 32
     full = np.zeros((M_alloc, chunks, 32, kh * kw), np.uint8)  # [m, chunk, c%32, tap]
@@ -134,7 +135,8 @@ def _np_conv_layout_bits(wbytes, M_alloc):
     padded[:, :C] = t
     full[:M] = padded.reshape(M, chunks, 32, kh * kw)
     neg = full.transpose(0, 1, 3, 2).reshape(M_alloc, -1)  # [m, chunk, tap, c%32]
-    return np.packbits(neg, axis=1, bitorder="little").reshape(-1)
+    words = np.packbits(neg, axis=1, bitorder="little").reshape(M_alloc, -1, 4)  # [m, step, 4 bytes]
+    return words.transpose(1, 0, 2).reshape(-1)
 
 
 @pytest.mark.parametrize("case", [(2, 16, 9, 9, 40, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_RELU),
