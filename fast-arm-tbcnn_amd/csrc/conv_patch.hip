@@ -187,7 +187,7 @@ struct PatchEpi {
 // (the spare record takes the stores of items past the patch), the weight
 // words plus a spare one; rounded to 16 bytes so both buffers stay aligned.
 __host__ __device__ inline int patch_buffer_elems(int patch, int words, int word_halves) {
-    return (3 * (patch + 1) * kPix + word_halves * (words + 1) + 7) / 8 * 8;
+    return (3 * (patch + 1) * kPix + word_halves * words + 8 + 7) / 8 * 8;  // + a 16-byte spare slot
 }
 
 // TAPS = 9: 3x3 kernels, taps unrolled and the chunk's weight words held in
@@ -263,9 +263,13 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     const int items = 4 * patch;
     const int per_thread = (items + Cfg::NT - 1) / Cfg::NT;  // <= kMaxItems (host-checked)
     constexpr int kMaxItems = MAXI;
-    const int witems = Cfg::BM * g.taps;
+    // a weight item is 16 bytes: the words of kWPI neighbouring channels of one
+    // tap (one load, one LDS write)
+    constexpr int kWPI = TERNARY ? 2 : 4;
+    constexpr int kGroupsM = Cfg::BM / kWPI;
+    const int witems = kGroupsM * g.taps;
     const int wper_thread = (witems + Cfg::NT - 1) / Cfg::NT;  // <= kMaxWItems (host-checked)
-    constexpr int kMaxWItems = TAPS > 0 ? std::min(8, (Cfg::BM * TAPS + Cfg::NT - 1) / Cfg::NT) : 8;
+    constexpr int kMaxWItems = TAPS > 0 ? std::min(4, (kGroupsM * TAPS + Cfg::NT - 1) / Cfg::NT) : 4;
     const int64_t img = static_cast<int64_t>(n) * g.C * g.H * g.W;
     const uint32_t HW4 = static_cast<uint32_t>(g.H) * g.W * 4;
     constexpr uint32_t kWordBytes = TERNARY ? 8 : 4;
@@ -299,16 +303,16 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
 #pragma unroll
     for (int it = 0; it < kMaxWItems; ++it) {
         const int item = tid + it * Cfg::NT;
-        const int ml = item % Cfg::BM;
-        const int tap = item / Cfg::BM;
-        const bool ok = item < witems && m0 + ml < m_alloc;
+        const int ml = (item % kGroupsM) * kWPI;
+        const int tap = item / kGroupsM;
+        const bool ok = item < witems && m0 + ml < m_alloc;  // m_alloc: a multiple of 8
         woff[it] = ok ? (static_cast<uint32_t>(tap) * static_cast<uint32_t>(m_alloc) + static_cast<uint32_t>(m0 + ml)) *
                             kWordBytes
                       : kOutside;
-        wslot[it] = (ok ? item : witems) * kWordHalves;
+        wslot[it] = (item < witems ? tap * Cfg::BM + ml : Cfg::BM * g.taps) * kWordHalves;
     }
     float stage[kMaxItems][8];
-    uint2 wstage[kMaxWItems];
+    u32x4_t wstage[kMaxWItems];
 
     auto load_chunk = [&](int ch) {
         const uint32_t cofs = static_cast<uint32_t>(ch * kChunk) * HW4;
@@ -325,13 +329,8 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
 #pragma unroll
         for (int it = 0; it < kMaxWItems; ++it) {
             if (it < wper_thread) {
-                const uint32_t o = woff[it] + wofs_ch;
-                if (TERNARY) {
-                    const auto v = __builtin_amdgcn_raw_buffer_load_b64(w_rs, o, 0, 0);
-                    wstage[it] = make_uint2(v[0], v[1]);
-                } else {
-                    wstage[it] = make_uint2(__builtin_amdgcn_raw_buffer_load_b32(w_rs, o, 0, 0), 0u);
-                }
+                wstage[it] = __builtin_bit_cast(
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rs, woff[it] + wofs_ch, 0, 0));
             }
         }
     };
@@ -351,9 +350,7 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
 #pragma unroll
         for (int it = 0; it < kMaxWItems; ++it) {
             if (it < wper_thread) {
-                uint16_t* d = dst + wofs + wslot[it];
-                if (TERNARY) *reinterpret_cast<uint2*>(d) = wstage[it];
-                else *reinterpret_cast<uint32_t*>(d) = wstage[it].x;
+                *reinterpret_cast<u32x4_t*>(dst + wofs + wslot[it]) = wstage[it];
             }
         }
     };
@@ -955,8 +952,8 @@ template <class Cfg, bool TERNARY, int TAPS>
 int launch_patch_items(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
                        const PatchEpi& epi, hipStream_t s) {
     const int per_thread = (4 * g.PHi * g.PWi + Cfg::NT - 1) / Cfg::NT;
-    const int wper_thread = (Cfg::BM * g.taps + Cfg::NT - 1) / Cfg::NT;
-    if (per_thread > 8 || wper_thread > 8 || (Cfg::KG > 1 && per_thread > 4))
+    const int wper_thread = (Cfg::BM / (TERNARY ? 2 : 4) * g.taps + Cfg::NT - 1) / Cfg::NT;
+    if (per_thread > 8 || wper_thread > 4 || (Cfg::KG > 1 && per_thread > 4))
         return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for the staging registers");
     if (per_thread <= 4) return launch_patch_taps<Cfg, TERNARY, TAPS, 4>(x, g, w, col_bytes, m_alloc, epi, s);
     if constexpr (Cfg::KG > 1) return TBN_INVALID_SHAPE;  // not reached (checked above)
