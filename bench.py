@@ -14,6 +14,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
                        [--only gemm|conv|ternary|tbn|gemm1024|lenet|resnet]
 """
 import argparse
+import ctypes
 import json
 import os
 import pathlib
@@ -145,7 +146,6 @@ def conv_cfg4(torch, tbn_hip, seed):
     y = torch.empty((64, 128, 14, 14), device=dev)
     desc = tbn_hip.conv_desc(64, 64, 14, 14, 128, 3, 3, 1, 1, 1, 1)
     # weights re-ordered once into the conv layout, as a Session does at init
-    import ctypes
     wbytes = ctypes.c_int64()
     tbn_hip.call("tbn_hip_conv_weights_bytes", tbn_hip.WEIGHTS_BINARY, desc, ctypes.byref(wbytes))
     conv_w = torch.empty(wbytes.value, dtype=torch.uint8, device=dev)
@@ -319,6 +319,12 @@ def main():
         conv_flops = 2.0 * 64 * 196 * 576 * 128
         extra["conv_us_per_batch"] = round(conv_ms * 1e3, 2)
         extra["conv_gflops_equiv"] = round(conv_flops / (conv_ms * 1e-3) / 1e9, 1)
+        # the tile this process's tuner chose (it can differ between runs
+        # within a few percent; all tiles sum in the same order)
+        kname = ctypes.create_string_buffer(160)
+        tbn_hip.call("tbn_hip_conv2d_kernel_name", tbn_hip.WEIGHTS_BINARY, keep[-1], tbn_hip.EPI_RELU, 0, kname,
+                     len(kname))
+        extra["conv_kernel"] = kname.value.decode()
         ref_ms = timed(step_ref)
         extra["conv_reference_layout_us_per_batch"] = round(ref_ms * 1e3, 2)
         log(f"conv cfg4 batch 64: {conv_ms * 1e3:.1f} us/batch pre-packed, {ref_ms * 1e3:.1f} us with the "
@@ -364,7 +370,6 @@ def main():
     if want("groups"):
         # depthwise 3x3 (MobileNet-style, batch 32, 128 channels, 56x56) and an
         # unfolded BatchNormalization over the same tensor: both HBM-bound
-        import ctypes
         dev = torch.device("cuda:0")
         g = torch.Generator(device=dev)
         g.manual_seed(7)
@@ -431,9 +436,13 @@ def main():
                              algo_bytes, traffic.get("gemm_f32_binary_4096"))
     if "conv_us_per_batch" in extra:
         conv_bytes = 4.0 * 64 * 64 * 196 + 128 * 640 / 8 + 8.0 * 128 + 4.0 * 64 * 128 * 196
+        # counter traffic measured on the kernel this run timed (one entry per
+        # tile the tuner takes on this shape), else none
+        conv_traffic = next((e for k, e in traffic.items() if k.startswith("conv_cfg4") and isinstance(e, dict)
+                             and e.get("kernel") == extra.get("conv_kernel")), None)
         extra["roofline_conv"] = mfma_roofline(2.0 * 64 * 196 * 576 * 128, extra["conv_us_per_batch"] * 1e-3,
                                                extra.get("conv_kernel", "conv_patch_kernel"), conv_bytes,
-                                               traffic.get("conv_cfg4"))
+                                               conv_traffic)
 
     result = {
         "metric": "float×binary GEMM GFLOP/s-equiv @4096³; Conv2D 64→128 14×14 µs/batch",

@@ -21,6 +21,7 @@
 // the fused 2x2 max pool the pixels are enumerated window by window so a window
 // sits in four neighbouring lanes.
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <map>
 #include <mutex>
@@ -782,6 +783,7 @@ struct TileChoice {
     int TH, TW, BM, NT;
     int single;  // 1: one LDS buffer
     int kg;      // K groups of waves (PatchCfg::KG)
+    int WM, WQ;  // wave tile (PatchCfg::WM, WQ)
 };
 
 size_t lds_bytes(const PatchGeom& g, int BM, bool ternary) {
@@ -852,7 +854,7 @@ using P15 = PatchCfg<64, 8, 8, 64, 32, 2>;
 
 template <class Cfg>
 constexpr TileChoice choice(int cfg, int linear, int single = 0) {
-    return TileChoice{cfg, linear, Cfg::TH, Cfg::TW, Cfg::BM, Cfg::NT, single, Cfg::KG};
+    return TileChoice{cfg, linear, Cfg::TH, Cfg::TW, Cfg::BM, Cfg::NT, single, Cfg::KG, Cfg::WM, Cfg::WQ};
 }
 
 // The TBN_TUNE_CONV_TILE control forces one tile: id = cfg for linear tiles,
@@ -1357,6 +1359,28 @@ int tbn_hip_conv2d_f32_prepacked(int weights, const float* x, const tbn_conv2d_d
                                  const float* residual, int flags, float* y, tbn_stream_t stream) {
     return conv_patch_run(weights, x, desc, conv_weights, scale, alpha, bias, residual, flags, y,
                           tbn_hip::stream_of(stream));
+}
+
+int tbn_hip_conv2d_kernel_name(int weights, const tbn_conv2d_desc* desc, int flags, int has_residual, char* name,
+                               size_t len) {
+    TBN_REQUIRE(weights == TBN_WEIGHTS_BINARY || weights == TBN_WEIGHTS_TERNARY, TBN_INVALID_ARGUMENT,
+                "unknown weights kind");
+    TBN_REQUIRE(desc && name && len > 0, TBN_INVALID_ARGUMENT, "null pointer");
+    PatchGeom g;
+    int rc = make_patch_geom(desc, flags, g);
+    if (rc) return rc;
+    PatchEpi epi{};
+    epi.flags = flags;
+    epi.residual = has_residual ? reinterpret_cast<const float*>(desc) : nullptr;  // only tested for null
+    TileChoice tc;
+    rc = weights == TBN_WEIGHTS_TERNARY ? select_tile<true>(desc, g, epi, tc) : select_tile<false>(desc, g, epi, tc);
+    if (rc) return rc;
+    // the launch's template arguments, as launch_patch / launch_patch_items pick them
+    const int taps = (g.kh == 3 && g.kw == 3) ? 9 : 0;
+    const int maxi = (4 * g.PHi * g.PWi + tc.NT - 1) / tc.NT <= 4 ? 4 : 8;
+    std::snprintf(name, len, "conv_patch_kernel<PatchCfg<%d, %d, %d, %d, %d, %d>, %s, %d, %d>", tc.BM, tc.TH, tc.TW,
+                  tc.WM, tc.WQ, tc.kg, weights == TBN_WEIGHTS_TERNARY ? "true" : "false", taps, maxi);
+    return tbn_hip::ok();
 }
 
 int tbn_hip_conv2d_tune_prepacked(int weights, const float* x, const tbn_conv2d_desc* desc,

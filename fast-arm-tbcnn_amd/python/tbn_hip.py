@@ -111,6 +111,8 @@ _SIGNATURES = {
     "tbn_hip_conv2d_f32_prepacked": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P, _P], _I32),
     "tbn_hip_conv2d_tune_prepacked": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P, _P],
                                       _I32),
+    "tbn_hip_conv2d_kernel_name": ([_I32, ctypes.POINTER(ConvDesc), _I32, _I32, ctypes.c_char_p, ctypes.c_size_t],
+                                   _I32),
     "tbn_hip_elementwise": ([_I32, _P, _I64, _P, _I64, _F32, _P, _P], _I32),
     "tbn_hip_ternary_activation": ([_P, _I64, _F32, _P, _P], _I32),
     "tbn_hip_ternary_pack_f32": ([_P, _I64, _I64, _I64, _I64, _I64, _F32, _F32, _P, _P, _P], _I32),

@@ -313,6 +313,13 @@ int tbn_hip_conv2d_f32_prepacked(int weights, const float* x, const tbn_conv2d_d
 int tbn_hip_conv2d_tune_prepacked(int weights, const float* x, const tbn_conv2d_desc* desc,
                                   const uint8_t* conv_weights, const float* scale, float alpha, const float* bias,
                                   const float* residual, int flags, float* y, tbn_stream_t stream);
+/* No counterpart in the reference (a diagnostic for profiling).  Writes into
+ * name (len bytes, NUL-terminated, truncated if short) the kernel, as a
+ * profiler names it, that tbn_hip_conv2d_f32_prepacked runs for this
+ * geometry, flags and residual presence in this process now: the tile the
+ * tuner cached, a forced tile, else the static rule.  No GPU work. */
+int tbn_hip_conv2d_kernel_name(int weights, const tbn_conv2d_desc* desc, int flags, int has_residual, char* name,
+                               size_t len);
 
 /* ---- fp32 layers and epilogue operators (Session support) ------------------ */
 

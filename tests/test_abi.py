@@ -57,6 +57,26 @@ def test_conv_weight_sizes_are_host_only():
     assert lib.tbn_hip_conv_weights_bytes(0, ctypes.byref(big), ctypes.byref(wb)) == tbn_hip.INVALID_SHAPE
 
 
+def test_conv_kernel_name_is_host_only():
+    """The diagnostic names the patch kernel a pre-packed conv launches (the
+    static rule here: nothing was tuned in this process), with the template
+    arguments the launch picks, and rejects bad arguments."""
+    lib = tbn_hip.lib()
+    buf = ctypes.create_string_buffer(160)
+    d = tbn_hip.conv_desc(64, 64, 14, 14, 128, 3, 3, 1, 1, 1, 1)  # config 4
+    assert lib.tbn_hip_conv2d_kernel_name(0, ctypes.byref(d), tbn_hip.EPI_RELU, 0, buf, len(buf)) == 0
+    name = buf.value.decode()
+    assert name.startswith("conv_patch_kernel<PatchCfg<") and name.endswith(">, false, 9, 4>"), name
+    assert name.count(",") == 8 and ", 2>" in name, name  # two chunks of 32 channels: two K groups
+    assert lib.tbn_hip_conv2d_kernel_name(1, ctypes.byref(d), 0, 1, buf, len(buf)) == 0
+    assert ">, true, 9, 4>" in buf.value.decode()
+    d5 = tbn_hip.conv_desc(2, 96, 19, 23, 72, 5, 5, 1, 2, 2, 2)  # a 5x5 kernel: the any-size variant
+    assert lib.tbn_hip_conv2d_kernel_name(0, ctypes.byref(d5), 0, 0, buf, len(buf)) == 0
+    assert ">, false, 0, " in buf.value.decode()
+    assert lib.tbn_hip_conv2d_kernel_name(7, ctypes.byref(d), 0, 0, buf, len(buf)) == tbn_hip.INVALID_ARGUMENT
+    assert lib.tbn_hip_conv2d_kernel_name(0, ctypes.byref(d), 0, 0, None, 0) == tbn_hip.INVALID_ARGUMENT
+
+
 def test_fused_stem_pool_shape_rule():
     """TBN_EPI_MAXPOOL3X3S2 is taken on the stem shape (3 channels, 7x7,
     stride 2, M <= 64) with ReLU and refused (NOT_IMPLEMENTED) otherwise; the
