@@ -428,7 +428,9 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
                 const int m = mrow + 8 * (e >> 2) + (e & 3);
                 float x = v[j][e];
                 if (relu) x = x > 0.0f ? x : 0.0f;
-                if (m < p.M && ncol[j] < p.N) p.C[static_cast<int64_t>(m) * p.ldc + ncol[j]] = x;
+                // non-temporal: C is not read again here (0.7 % at 4096^3, 1-2 % at the mid-size shapes)
+                if (m < p.M && ncol[j] < p.N)
+                    __builtin_nontemporal_store(x, &p.C[static_cast<int64_t>(m) * p.ldc + ncol[j]]);
             }
     }
 }
@@ -892,7 +894,9 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
                 const int m = mrow + 8 * (e >> 2) + (e & 3);
                 float x = v[j][e];
                 if (relu) x = x > 0.0f ? x : 0.0f;
-                if (m < p.M && ncol[j] < p.N) p.C[static_cast<int64_t>(m) * p.ldc + ncol[j]] = x;
+                // non-temporal: C is not read again here (0.7 % at 4096^3, 1-2 % at the mid-size shapes)
+                if (m < p.M && ncol[j] < p.N)
+                    __builtin_nontemporal_store(x, &p.C[static_cast<int64_t>(m) * p.ldc + ncol[j]]);
             }
     }
 }
