@@ -432,8 +432,12 @@ def main():
     # `frac` is the algorithmic rate over it; `mfma_issued` counts the three
     # products actually issued, and `fp32_peak_ratio` compares with the fp32
     # peak a plain fp32 kernel would be bound by.
-    roofline = mfma_roofline(flops, ms, "gemm_wide_kernel<WideCfg<128,512,128,64,64>,false,false>",
-                             algo_bytes, traffic.get("gemm_f32_binary_4096"))
+    kname = ctypes.create_string_buffer(256)
+    tbn_hip.call("tbn_hip_gemm_kernel_name", tbn_hip.WEIGHTS_BINARY, M, N, K, K, K_pad, N_pad, kname, 256)
+    gemm_traffic = traffic.get("gemm_f32_binary_4096")
+    if gemm_traffic and gemm_traffic.get("kernel") != kname.value.decode():
+        gemm_traffic = None  # counters of another kernel do not describe this one
+    roofline = mfma_roofline(flops, ms, kname.value.decode(), algo_bytes, gemm_traffic)
     if "conv_us_per_batch" in extra:
         conv_bytes = 4.0 * 64 * 64 * 196 + 128 * 640 / 8 + 8.0 * 128 + 4.0 * 64 * 128 * 196
         # counter traffic measured on the kernel this run timed (one entry per

@@ -559,12 +559,11 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     }
     if (epi.partial) {
         // split-K (never with the pool, host-checked): raw sums of this
-        // block's chunks into split sp's plane set.  With tile counters the
-        // sums go through at device scope (cache policy SC1: to the memory
-        // side, never a stale line of another XCD's L2), the barrier's wait
-        // for the stores orders them before the count, and the last block of
-        // the tile to count itself in adds the splits in split order (as the
-        // reduce kernel does) and runs the epilogue below.
+        // block's chunks into split sp's plane set, stored with the
+        // device-scope policy (sc1).  With tile counters, splitk_arrive
+        // orders every wave's stores before the count and the count before
+        // the last block's loads; that block adds the splits in split order
+        // (as the reduce kernel does) and runs the epilogue below.
         constexpr int kDeviceScope = 16;
         const int64_t split_elems = static_cast<int64_t>(g.N) * g.M * plane;
         const __amdgpu_buffer_rsrc_t p_rs = make_rsrc(epi.partial + sp * split_elems + obase, obytes);
@@ -582,13 +581,10 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                                                           0, kDeviceScope);
                 }
         if (!epi.counters) return;
-        __syncthreads();  // every wave's stores complete (and the patch buffers are free)
-        int* is_last = reinterpret_cast<int*>(lds);  // no static LDS: the dynamic size may be the maximum
-        if (tid == 0)
-            *is_last = __hip_atomic_fetch_add(epi.counters + bid, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                       g.splits - 1;
-        __syncthreads();
-        if (!*is_last) return;
+        // the flag lives in the patch buffers, free once every wave is past
+        // its last MFMA (the first barrier inside splitk_arrive); no static
+        // LDS: the dynamic size may be the maximum
+        if (!splitk_arrive(epi.counters + bid, g.splits, reinterpret_cast<int*>(lds))) return;
         for (int s2 = 0; s2 < g.splits; ++s2) {
             const __amdgpu_buffer_rsrc_t rs = make_rsrc(epi.partial + s2 * split_elems + obase, obytes);
 #pragma unroll
@@ -1292,42 +1288,27 @@ int conv_patch_from_reference(int weights, const float* x, const tbn_conv2d_desc
                                 cw + wspan, scratch_bytes - wspan);
         return rc;
     }
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    const bool capturing = hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone;
-    if (!capturing) {
-        // the stream workspace: the re-ordered weights, the split-K sums after
-        // them, and the tile counters of the in-kernel split-K finish
-        PatchGeom g;
-        int rc = make_patch_geom(desc, flags, g);
-        if (rc) return rc;
-        const int64_t wspan = (wbytes + 255) / 256 * 256;
-        const int64_t bytes = wspan + conv_patch_partial_bytes(g);
-        void* ws = nullptr;
-        int* counters = nullptr;
-        bool temporary = false;
-        rc = stream_workspace(s, static_cast<size_t>(bytes), ws, temporary, &counters);
-        if (rc) return rc;
-        uint8_t* cw = static_cast<uint8_t*>(ws);
-        rc = tbn_hip_pack_conv_weights(weights, packed, K_pad, N_pad, desc, cw, s);
-        if (rc == TBN_SUCCESS)
-            rc = conv_patch_run(weights, x, desc, cw, scale, alpha, bias, residual, flags, y, s, false, cw + wspan,
-                                bytes - wspan, counters);
-        release_workspace(ws, temporary, s);
-        return rc;
-    }
-    // under capture: a stream-ordered allocation recorded with the call
-    void* buf = nullptr;
-    hipError_t e = hipMallocAsync(&buf, static_cast<size_t>(wbytes), s);
-    if (e != hipSuccess) {
-        (void)hipGetLastError();
-        return fail(e == hipErrorOutOfMemory ? TBN_OUT_OF_MEMORY : TBN_RUNTIME_ERROR,
-                    std::string("conv weight buffer allocation failed: ") + hipGetErrorString(e));
-    }
-    int rc = tbn_hip_pack_conv_weights(weights, packed, K_pad, N_pad, desc, static_cast<uint8_t*>(buf), s);
+    // the stream workspace: the re-ordered weights, the split-K sums after
+    // them, and the tile counters of the in-kernel split-K finish.  While s
+    // captures, stream_workspace refuses (TBN_NOT_IMPLEMENTED): nothing is
+    // allocated into a graph; callers that capture use the prepacked or the
+    // no-allocation entry points.
+    PatchGeom g;
+    int rc = make_patch_geom(desc, flags, g);
+    if (rc) return rc;
+    const int64_t wspan = (wbytes + 255) / 256 * 256;
+    const int64_t bytes = wspan + conv_patch_partial_bytes(g);
+    void* ws = nullptr;
+    int* counters = nullptr;
+    bool temporary = false;
+    rc = stream_workspace(s, static_cast<size_t>(bytes), ws, temporary, &counters);
+    if (rc) return rc;
+    uint8_t* cw = static_cast<uint8_t*>(ws);
+    rc = tbn_hip_pack_conv_weights(weights, packed, K_pad, N_pad, desc, cw, s);
     if (rc == TBN_SUCCESS)
-        rc = conv_patch_run(weights, x, desc, static_cast<const uint8_t*>(buf), scale, alpha, bias, residual, flags,
-                            y, s);
-    (void)hipFreeAsync(buf, s);
+        rc = conv_patch_run(weights, x, desc, cw, scale, alpha, bias, residual, flags, y, s, false, cw + wspan,
+                            bytes - wspan, counters);
+    release_workspace(ws, temporary, s);
     return rc;
 }
 

@@ -5,6 +5,7 @@
 // columns (packed weights, or the fp32 B matrix for tbn::gemm), so each
 // result register row is 32 consecutive columns of C: 128-byte stores.
 #include <algorithm>
+#include <cstdio>
 #include <string>
 
 #include "common.hpp"
@@ -346,6 +347,36 @@ int gemm_quant(const float* A, int64_t lda, int64_t M, int64_t N, int64_t K, con
 }  // namespace
 
 extern "C" {
+
+int tbn_hip_gemm_kernel_name(int weights, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t K_pad,
+                             int64_t N_pad, char* name, size_t len) {
+    TBN_REQUIRE(weights == TBN_WEIGHTS_BINARY || weights == TBN_WEIGHTS_TERNARY, TBN_INVALID_ARGUMENT,
+                "unknown weights kind");
+    TBN_REQUIRE(name && len > 0, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_REQUIRE(M > 0 && N > 0 && K > 0 && M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31) && lda >= K &&
+                    K_pad >= K && K_pad % 32 == 0 && N_pad >= N,
+                TBN_INVALID_SHAPE, "no kernel runs for this shape");
+    const bool ternary = weights == TBN_WEIGHTS_TERNARY;
+    std::string k;
+    if (small_gemm_fits(N, K)) {
+        k = ternary ? "small_gemm_kernel<2>" : "small_gemm_kernel<1>";
+    } else {
+        // 16-byte aligned operands, as the Session and the bench allocate them
+        alignas(16) static const float kAligned[4] = {};
+        const tbn_hip::WideGemmArgs wa{kAligned, lda, int(M), int(N), int(K),
+                                       reinterpret_cast<const uint8_t*>(kAligned), ternary ? K_pad / 4 : K_pad / 8,
+                                       int(N_pad), nullptr, N, nullptr, 1.0f, nullptr, nullptr, 0, 0.0f, 0};
+        if (tbn_hip::gemm_wide_fits(wa, ternary)) {
+            k = tbn_hip::gemm_wide_kernel_name(wa, ternary);
+        } else {
+            const bool big = tbn_hip::ceil_div(M, CfgBig::BR) * tbn_hip::ceil_div(N, CfgBig::BC) >= 256;
+            k = std::string("mfma_tile_kernel<TileCfg<") + (big ? "128, 256, 64, 128, 2" : "64, 64, 32, 32, 1") +
+                ">, ...>";
+        }
+    }
+    std::snprintf(name, len, "%s", k.c_str());
+    return tbn_hip::ok();
+}
 
 int tbn_hip_gemm_f32_binary(const float* A, int64_t lda, int64_t M, int64_t N, int64_t K,
                             const uint8_t* packed, int64_t K_pad, int64_t N_pad,

@@ -15,8 +15,9 @@
 //
 // Memory: A and W are read with buffer loads whose resource covers the
 // block's rows / columns to the end of the matrix: rows >= M and columns >=
-// N_pad read as zero, and the voffsets are fixed per lane (the K position is
-// the scalar offset), so the steady-state loop issues no address arithmetic.
+// N_pad read as zero, and the voffsets are fixed per lane (the K position
+// moves the resource base, scalar work), so the steady-state loop issues no
+// vector address arithmetic.
 // A K step past K (K % 64 != 0) is zeroed before the split.
 //
 // Blocks are dealt round-robin over the 8 XCDs; the tile order puts the
@@ -74,15 +75,6 @@ using WideMid = WideCfg<32, 128, 32, 32, 64, true, 2>;
 
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef short i16x2_t __attribute__((ext_vector_type(2)));
-
-// Buffer resource word 3 for gfx9: 32-bit dword data format, raw addressing.
-constexpr int kRsrcWord3 = 0x00020000;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint64_t bytes) {
-    const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : static_cast<uint32_t>(bytes);
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(n),
-                                             kRsrcWord3);
-}
 
 // 8 BinaryMatrix bits (bit e = weight k0 + e, 1 means -1) -> 8 bf16 +-1.0.
 // Bits 16 and up of x must be zero; bits 8..15 are ignored.  y holds bit e at
@@ -143,13 +135,12 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
 
     // A staging: thread -> row ar, EPT consecutive k from ag * EPT
     const int ar = tid / Cfg::TPR, ag = tid % Cfg::TPR;
-    const __amdgpu_buffer_rsrc_t a_rs =
-        make_rsrc(p.A + static_cast<int64_t>(r0) * p.lda, static_cast<uint64_t>(p.M - r0) * p.lda * 4);
+    const float* a_base = p.A + static_cast<int64_t>(r0) * p.lda;
+    const uint64_t a_bytes = static_cast<uint64_t>(p.M - r0) * p.lda * 4;
     const int a_voff = (ar * static_cast<int>(p.lda) + ag * Cfg::EPT) * 4;
     // W: lane's columns c0 + wc*WC + j*32 + lane%32
-    const __amdgpu_buffer_rsrc_t b_rs =
-        make_rsrc(p.packed + static_cast<int64_t>(c0) * p.col_bytes,
-                  static_cast<uint64_t>(p.N_pad - c0) * static_cast<uint64_t>(p.col_bytes));
+    const uint8_t* b_base = p.packed + static_cast<int64_t>(c0) * p.col_bytes;
+    const uint64_t b_bytes = static_cast<uint64_t>(p.N_pad - c0) * static_cast<uint64_t>(p.col_bytes);
     int b_voff[Cfg::FC];
 #pragma unroll
     for (int j = 0; j < Cfg::FC; ++j)
@@ -160,28 +151,31 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
     u32x4_t bfr[2][Cfg::FC];                           // decoded W fragments, alternating k-slices
 
     // loads past the end of A / W return zeros or data of later rows / columns
-    // that no result uses, so they need no guard; s is an absolute step
+    // that no result uses, so they need no guard; s is an absolute step, its
+    // byte offset folded into the resource base (scalar work) so that every
+    // byte past the end of A or W is range-checked
     auto load_a = [&](int s) {
-        const int soff = s * KS * 4;
+        const __amdgpu_buffer_rsrc_t a_rs = buffer_range(a_base, a_bytes, static_cast<uint64_t>(s) * KS * 4);
 #pragma unroll
         for (int v = 0; v < Cfg::EPT / 4; ++v) {
             const f32x4_t x =
-                __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16 * v, soff, 0));
+                __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16 * v, 0, 0));
 #pragma unroll
             for (int e = 0; e < 4; ++e) areg[4 * v + e] = x[e];
         }
     };
     auto load_b = [&](int s, uint32_t (&w)[Cfg::FC][WPS]) {
+        const __amdgpu_buffer_rsrc_t b_rs = buffer_range(b_base, b_bytes, static_cast<uint64_t>(s) * 4 * WPS);
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             if constexpr (TERNARY) {
                 const u32x4_t x = __builtin_bit_cast(
-                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], s * 4 * WPS, 0));
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], 0, 0));
 #pragma unroll
                 for (int d = 0; d < WPS; ++d) w[j][d] = x[d];
             } else {
                 const uint64_t x = __builtin_bit_cast(
-                    uint64_t, __builtin_amdgcn_raw_buffer_load_b64(b_rs, b_voff[j], s * 4 * WPS, 0));
+                    uint64_t, __builtin_amdgcn_raw_buffer_load_b64(b_rs, b_voff[j], 0, 0));
                 w[j][0] = static_cast<uint32_t>(x);
                 w[j][1] = static_cast<uint32_t>(x >> 32);
             }
@@ -317,13 +311,13 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
     if constexpr (SPLIT) {
         // Raw sums of this split go to partial[split][m][n]; the last block of
         // the tile to count itself in adds all splits in split order.  The
-        // sums are written and read at device scope (sc1: through to the
-        // memory side, never a stale line of another XCD's L2), so no L2-wide
-        // write-back or invalidate is needed; the barrier's wait for the
-        // stores orders them before the count.  Buffer accesses over one
-        // split's M x N sums (host-checked below 2^31 bytes): rows past M
-        // are dropped / read zero, columns past N touch sums no stored output
-        // uses (and are never stored: n < N is checked).
+        // sums are written and read with the device-scope policy (sc1), and
+        // splitk_arrive orders every wave's stores before the count and the
+        // count before the last block's loads.  Buffer accesses over one
+        // split's M x N sums (host-checked below 2^31 bytes): the row step of
+        // register e is folded into the resource base, so rows past M are
+        // dropped / read zero by the range check; lanes of columns past N
+        // carry an offset beyond every range.
         constexpr int kDeviceScope = 16;  // cache policy SC1
         const int64_t MN = static_cast<int64_t>(p.M) * p.N;
         const int nsplit = static_cast<int>(gridDim.x) / total;
@@ -335,28 +329,22 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
                 const int n = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
                 voff[i][j] = n < p.N ? ((r0 + wr * Cfg::WR + i * 32 + 4 * h) * p.N + n) * 4 : 0x7FFFFFF0;
             }
-        {
-            const __amdgpu_buffer_rsrc_t rs = make_rsrc(partial + split * MN, static_cast<uint64_t>(MN) * 4);
+        const uint64_t split_bytes = static_cast<uint64_t>(MN) * 4;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int soff = (8 * (e >> 2) + (e & 3)) * p.N * 4;
+        for (int e = 0; e < 16; ++e) {
+            const __amdgpu_buffer_rsrc_t rs = buffer_range(
+                partial + split * MN, split_bytes, static_cast<uint64_t>(8 * (e >> 2) + (e & 3)) * p.N * 4);
 #pragma unroll
-                for (int i = 0; i < Cfg::FR; ++i)
+            for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
-                    for (int j = 0; j < Cfg::FC; ++j)
-                        // __float_as_uint, not __builtin_bit_cast: hipcc (ROCm 7.2) folds a bit
-                        // cast of a vector element with a loop index to element 0
-                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][e]), rs, voff[i][j], soff,
-                                                              kDeviceScope);
-            }
+                for (int j = 0; j < Cfg::FC; ++j)
+                    // __float_as_uint, not __builtin_bit_cast: hipcc (ROCm 7.2) folds a bit
+                    // cast of a vector element with a loop index to element 0
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][e]), rs, voff[i][j], 0,
+                                                          kDeviceScope);
         }
-        __syncthreads();  // every wave's stores complete
         __shared__ int is_last;
-        if (tid == 0)
-            is_last = __hip_atomic_fetch_add(counters + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                      nsplit - 1;
-        __syncthreads();
-        if (!is_last) return;
+        if (!splitk_arrive(counters + t, nsplit, &is_last)) return;
         // 0 + split 0 + split 1 + ... per output, in split order
 #pragma unroll
         for (int i = 0; i < Cfg::FR; ++i)
@@ -365,16 +353,16 @@ gemm_wide_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_pe
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
         for (int sp = 0; sp < nsplit; ++sp) {
-            const __amdgpu_buffer_rsrc_t rs = make_rsrc(partial + sp * MN, static_cast<uint64_t>(MN) * 4);
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int soff = (8 * (e >> 2) + (e & 3)) * p.N * 4;
+                const __amdgpu_buffer_rsrc_t rs = buffer_range(
+                    partial + sp * MN, split_bytes, static_cast<uint64_t>(8 * (e >> 2) + (e & 3)) * p.N * 4);
 #pragma unroll
                 for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
                     for (int j = 0; j < Cfg::FC; ++j)
                         acc[i][j][e] += __builtin_bit_cast(
-                            float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff[i][j], soff, kDeviceScope));
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff[i][j], 0, kDeviceScope));
             }
         }
         // ready for the next launch on this workspace
@@ -509,13 +497,12 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
 
     // A staging: thread -> row ar, EPT consecutive k from ag * EPT
     const int ar = tid / Cfg::TPR, ag = tid % Cfg::TPR;
-    const __amdgpu_buffer_rsrc_t a_rs =
-        make_rsrc(p.A + static_cast<int64_t>(r0) * p.lda, static_cast<uint64_t>(p.M - r0) * p.lda * 4);
+    const float* a_base = p.A + static_cast<int64_t>(r0) * p.lda;
+    const uint64_t a_bytes = static_cast<uint64_t>(p.M - r0) * p.lda * 4;
     const int a_voff = (ar * static_cast<int>(p.lda) + ag * Cfg::EPT) * 4;
     // W: lane's columns c0 + wc*WC + j*32 + lane%32
-    const __amdgpu_buffer_rsrc_t b_rs =
-        make_rsrc(p.packed + static_cast<int64_t>(c0) * p.col_bytes,
-                  static_cast<uint64_t>(p.N_pad - c0) * static_cast<uint64_t>(p.col_bytes));
+    const uint8_t* b_base = p.packed + static_cast<int64_t>(c0) * p.col_bytes;
+    const uint64_t b_bytes = static_cast<uint64_t>(p.N_pad - c0) * static_cast<uint64_t>(p.col_bytes);
     int b_voff[Cfg::FC];
 #pragma unroll
     for (int j = 0; j < Cfg::FC; ++j)
@@ -537,14 +524,16 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
     }
 
     // loads past the end of A / W return zeros or data of later rows / columns
-    // that no result uses, so they need no guard; s is an absolute step
+    // that no result uses, so they need no guard; s is an absolute step, its
+    // byte offset folded into the resource base (scalar work) so that every
+    // byte past the end of A or W is range-checked
     auto load_a = [&](int s, auto slot) {
         constexpr int sl = decltype(slot)::value;
-        const int soff = s * KS * 4;
+        const __amdgpu_buffer_rsrc_t a_rs = buffer_range(a_base, a_bytes, static_cast<uint64_t>(s) * KS * 4);
 #pragma unroll
         for (int v = 0; v < Cfg::EPT / 4; ++v) {
             const f32x4_t x =
-                __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16 * v, soff, 0));
+                __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_voff + 16 * v, 0, 0));
 #pragma unroll
             for (int e = 0; e < 4; ++e) areg[sl][4 * v + e] = x[e];
         }
@@ -555,8 +544,10 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
         for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
             for (int c = 0; c < PW / 4; ++c) {
+                const __amdgpu_buffer_rsrc_t b_rs =
+                    buffer_range(b_base, b_bytes, static_cast<uint64_t>(s) * 4 * WPS + 16 * c);
                 const u32x4_t v = __builtin_bit_cast(
-                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], s * 4 * WPS + 16 * c, 0));
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], 0, 0));
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
                     if (x == 0) wp[0][j][4 * c + d] = v[d];
@@ -566,16 +557,17 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
             }
     };
     auto load_b = [&](int s, uint32_t (&w)[Cfg::FC][WPS]) {
+        const __amdgpu_buffer_rsrc_t b_rs = buffer_range(b_base, b_bytes, static_cast<uint64_t>(s) * 4 * WPS);
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             if constexpr (TERNARY) {
                 const u32x4_t x = __builtin_bit_cast(
-                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], s * 4 * WPS, 0));
+                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(b_rs, b_voff[j], 0, 0));
 #pragma unroll
                 for (int d = 0; d < WPS; ++d) w[j][d] = x[d];
             } else {
                 const uint64_t x = __builtin_bit_cast(
-                    uint64_t, __builtin_amdgcn_raw_buffer_load_b64(b_rs, b_voff[j], s * 4 * WPS, 0));
+                    uint64_t, __builtin_amdgcn_raw_buffer_load_b64(b_rs, b_voff[j], 0, 0));
                 w[j][0] = static_cast<uint32_t>(x);
                 w[j][1] = static_cast<uint32_t>(x >> 32);
             }
@@ -779,13 +771,13 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
     if constexpr (SPLIT) {
         // Raw sums of this split go to partial[split][m][n]; the last block of
         // the tile to count itself in adds all splits in split order.  The
-        // sums are written and read at device scope (sc1: through to the
-        // memory side, never a stale line of another XCD's L2), so no L2-wide
-        // write-back or invalidate is needed; the barrier's wait for the
-        // stores orders them before the count.  Buffer accesses over one
-        // split's M x N sums (host-checked below 2^31 bytes): rows past M
-        // are dropped / read zero, columns past N touch sums no stored output
-        // uses (and are never stored: n < N is checked).
+        // sums are written and read with the device-scope policy (sc1), and
+        // splitk_arrive orders every wave's stores before the count and the
+        // count before the last block's loads.  Buffer accesses over one
+        // split's M x N sums (host-checked below 2^31 bytes): the row step of
+        // register e is folded into the resource base, so rows past M are
+        // dropped / read zero by the range check; lanes of columns past N
+        // carry an offset beyond every range.
         constexpr int kDeviceScope = 16;  // cache policy SC1
         const int64_t MN = static_cast<int64_t>(p.M) * p.N;
         const int nsplit = static_cast<int>(gridDim.x) / total;
@@ -797,28 +789,22 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
                 const int n = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
                 voff[i][j] = n < p.N ? ((r0 + wr * Cfg::WR + i * 32 + 4 * h) * p.N + n) * 4 : 0x7FFFFFF0;
             }
-        {
-            const __amdgpu_buffer_rsrc_t rs = make_rsrc(partial + split * MN, static_cast<uint64_t>(MN) * 4);
+        const uint64_t split_bytes = static_cast<uint64_t>(MN) * 4;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int soff = (8 * (e >> 2) + (e & 3)) * p.N * 4;
+        for (int e = 0; e < 16; ++e) {
+            const __amdgpu_buffer_rsrc_t rs = buffer_range(
+                partial + split * MN, split_bytes, static_cast<uint64_t>(8 * (e >> 2) + (e & 3)) * p.N * 4);
 #pragma unroll
-                for (int i = 0; i < Cfg::FR; ++i)
+            for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
-                    for (int j = 0; j < Cfg::FC; ++j)
-                        // __float_as_uint, not __builtin_bit_cast: hipcc (ROCm 7.2) folds a bit
-                        // cast of a vector element with a loop index to element 0
-                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][e]), rs, voff[i][j], soff,
-                                                              kDeviceScope);
-            }
+                for (int j = 0; j < Cfg::FC; ++j)
+                    // __float_as_uint, not __builtin_bit_cast: hipcc (ROCm 7.2) folds a bit
+                    // cast of a vector element with a loop index to element 0
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][e]), rs, voff[i][j], 0,
+                                                          kDeviceScope);
         }
-        __syncthreads();  // every wave's stores complete
         __shared__ int is_last;
-        if (tid == 0)
-            is_last = __hip_atomic_fetch_add(counters + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                      nsplit - 1;
-        __syncthreads();
-        if (!is_last) return;
+        if (!splitk_arrive(counters + t, nsplit, &is_last)) return;
         // 0 + split 0 + split 1 + ... per output, in split order
 #pragma unroll
         for (int i = 0; i < Cfg::FR; ++i)
@@ -827,16 +813,16 @@ gemm_mid_kernel(tbn_hip::WideGemmArgs p, int tiles_r, int tiles_c, int steps_per
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
         for (int sp = 0; sp < nsplit; ++sp) {
-            const __amdgpu_buffer_rsrc_t rs = make_rsrc(partial + sp * MN, static_cast<uint64_t>(MN) * 4);
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int soff = (8 * (e >> 2) + (e & 3)) * p.N * 4;
+                const __amdgpu_buffer_rsrc_t rs = buffer_range(
+                    partial + sp * MN, split_bytes, static_cast<uint64_t>(8 * (e >> 2) + (e & 3)) * p.N * 4);
 #pragma unroll
                 for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
                     for (int j = 0; j < Cfg::FC; ++j)
                         acc[i][j][e] += __builtin_bit_cast(
-                            float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff[i][j], soff, kDeviceScope));
+                            float, __builtin_amdgcn_raw_buffer_load_b32(rs, voff[i][j], 0, kDeviceScope));
             }
         }
         // ready for the next launch on this workspace
@@ -1021,6 +1007,16 @@ bool gemm_wide_fits(const WideGemmArgs& a, bool ternary) {
            static_cast<int64_t>(bc) * a.col_bytes < (1LL << 31) && (ternary || a.col_bytes % 16 == 0) &&
            static_cast<int64_t>(w.tiles_r) * w.tiles_c <= kWorkspaceCounters &&
            (w.splits == 1 || static_cast<int64_t>(a.M + 128) * a.N * 4 < (1LL << 31));
+}
+
+std::string gemm_wide_kernel_name(const WideGemmArgs& a, bool ternary) {
+    const WidePlan w = choose_plan(a.M, a.N, a.K, ternary);
+    const char* cfg = w.cfg == 0   ? "WideCfg<128, 512, 128, 64, 64, false, 1>"
+                      : w.cfg == 1 ? "WideCfg<64, 128, 32, 64, 64, true, 1>"
+                                   : "WideCfg<32, 128, 32, 32, 64, true, 2>";
+    const bool split = w.splits > 1 && w.cfg != 2;
+    return std::string(w.cfg == 0 ? "gemm_wide_kernel<" : "gemm_mid_kernel<") + cfg + ", " +
+           (ternary ? "true" : "false") + ", " + (split ? "true" : "false") + ">";
 }
 
 int gemm_wide(const WideGemmArgs& a, bool ternary, hipStream_t stream) {

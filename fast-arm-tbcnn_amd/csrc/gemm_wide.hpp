@@ -2,6 +2,8 @@
 // quantized GEMM entry points when the shape fills the chip with its tiles.
 #pragma once
 
+#include <string>
+
 #include "common.hpp"
 
 namespace tbn_hip {
@@ -32,5 +34,8 @@ bool gemm_wide_fits(const WideGemmArgs& a, bool ternary);
 // tile adding the splits in split order (stream workspace of splits * M * N
 // floats).
 int gemm_wide(const WideGemmArgs& a, bool ternary, hipStream_t stream);
+// The kernel gemm_wide launches for this shape now (tuning controls
+// included), as a profiler names it.
+std::string gemm_wide_kernel_name(const WideGemmArgs& a, bool ternary);
 
 }  // namespace tbn_hip

@@ -184,6 +184,46 @@ inline FastDiv make_fastdiv(uint32_t d) {
 }
 
 // ---------------------------------------------------------------------------
+// Buffer resources and the split-K finish
+// ---------------------------------------------------------------------------
+
+// Raw dword buffer resource over [base + skip, base + bytes): the range check
+// then drops every access whose voffset reaches past `bytes - skip`, so an
+// offset that would otherwise go in the (unchecked) SGPR offset field is
+// folded into the base instead and stays bounds-checked.  skip >= bytes gives
+// an empty range (every access dropped).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_range(const void* base, uint64_t bytes, uint64_t skip) {
+    const uint64_t left = bytes > skip ? bytes - skip : 0;
+    const uint32_t n = left > 0xFFFFFFFFull ? 0xFFFFFFFFu : static_cast<uint32_t>(left);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(static_cast<const char*>(base)) + skip,
+                                             static_cast<short>(0), static_cast<int>(n), 0x00020000);
+}
+
+// Split-K arrival of one block at its tile's counter, after every thread has
+// issued its partial-sum stores (device-scope policy).  Returns true in every
+// thread of the block that arrives last; that block may then read all splits'
+// partial sums.  The ordering:
+//   1. each wave waits until its own stores are acknowledged (vmcnt(0)): the
+//      workgroup barrier alone emits no such wait on gfx950;
+//   2. the barrier then orders every wave's completed stores before thread 0;
+//   3. thread 0's increment is acquire-release at agent scope: its release
+//      half writes back this XCD's L2 (which covers the other waves' lines)
+//      and waits before the increment, its acquire half invalidates the
+//      non-coherent cache lines after it;
+//   4. the last block's waves each run an agent-scope acquire fence before
+//      reading the other blocks' sums.
+__device__ __forceinline__ bool splitk_arrive(int* counter, int arrivals, int* flag_lds) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+        *flag_lds = __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == arrivals - 1;
+    __syncthreads();
+    const bool last = *flag_lds != 0;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    return last;
+}
+
+// ---------------------------------------------------------------------------
 // Operand loaders.  Each has a register stage (`Regs`), `load` (global ->
 // registers for the K step starting at k0) and `store` (registers -> LDS in
 // the [piece][row][k] bf16 layout).

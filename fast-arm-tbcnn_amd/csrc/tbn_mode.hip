@@ -313,12 +313,13 @@ __global__ void __launch_bounds__(Cfg::NT) tbn_f4_gemm_kernel(F4GemmArgs p, int 
     const int r0 = tr * Cfg::BR;
     const int c0 = tc * Cfg::BC;
 
-    // rows past M / columns past n_alloc read as zero (buffer range)
-    const __amdgpu_buffer_rsrc_t a_rs =
-        make_rsrc(p.A + static_cast<int64_t>(r0) * p.lda, static_cast<uint64_t>(p.M - r0) * p.lda);
-    const __amdgpu_buffer_rsrc_t b_rs =
-        make_rsrc(p.B + static_cast<int64_t>(c0) * p.ldb,
-                  c0 < p.n_alloc ? static_cast<uint64_t>(p.n_alloc - c0) * p.ldb : 0);
+    // rows past M / columns past n_alloc read as zero (buffer range); the
+    // K step's byte offset is folded into each step's resource base, so the
+    // last row's bytes past the end are range-checked too
+    const uint8_t* a_base = p.A + static_cast<int64_t>(r0) * p.lda;
+    const uint64_t a_bytes = static_cast<uint64_t>(p.M - r0) * p.lda;
+    const uint8_t* b_base = p.B + static_cast<int64_t>(c0) * p.ldb;
+    const uint64_t b_bytes = c0 < p.n_alloc ? static_cast<uint64_t>(p.n_alloc - c0) * p.ldb : 0;
     // load i of this wave fills slots [64 (wave * LOADS + i), + 64) of a buffer:
     // A rows first, then B rows; lane -> (row, stored part) -> global part
     int voff[Cfg::LOADS];
@@ -334,9 +335,11 @@ __global__ void __launch_bounds__(Cfg::NT) tbn_f4_gemm_kernel(F4GemmArgs p, int 
         voff[i] = r * static_cast<int>(a ? p.lda : p.ldb) + q * 16;
     }
     auto load = [&](int s, int u) {
+        const __amdgpu_buffer_rsrc_t a_rs = buffer_range(a_base, a_bytes, static_cast<uint64_t>(s) * RB);
+        const __amdgpu_buffer_rsrc_t b_rs = buffer_range(b_base, b_bytes, static_cast<uint64_t>(s) * RB);
 #pragma unroll
         for (int i = 0; i < Cfg::LOADS; ++i)
-            load_lds16(is_a[i] ? a_rs : b_rs, lds + u * Cfg::BUF + 1024 * (wave * Cfg::LOADS + i), voff[i], s * RB);
+            load_lds16(is_a[i] ? a_rs : b_rs, lds + u * Cfg::BUF + 1024 * (wave * Cfg::LOADS + i), voff[i], 0);
     };
 
     f32x16_t acc[Cfg::FR][Cfg::FC];
@@ -438,28 +441,36 @@ __global__ void __launch_bounds__(Cfg::NT) tbn_f4_gemm_kernel(F4GemmArgs p, int 
     }
 
     // epilogue: C (an exact integer in fp32); rows of register e: i*32 +
-    // 8*(e/4) + 4*h + e%4.  Buffer stores over this block's rows [r0, M):
-    // rows past M fall outside the resource and columns past N get an offset
-    // outside it, so no store is behind a branch (ldo < 2^21, host-checked).
-    const __amdgpu_buffer_rsrc_t o_rs =
-        make_rsrc(static_cast<uint8_t*>(p.out) + static_cast<int64_t>(r0) * p.ldo * 4,
-                  static_cast<uint64_t>(p.M - r0) * p.ldo * 4);
+    // 8*(e/4) + 4*h + e%4.  Buffer stores over this block's rows [r0, M),
+    // the row step of register e folded into the resource base: rows past M
+    // fall outside the range and columns past N get an offset outside every
+    // range, so no store is behind a branch (ldo < 2^21, host-checked, keeps
+    // row * ldo * 4 below 2^31 for the 256 rows of a tile).
+    const uint64_t out_bytes = static_cast<uint64_t>(p.M - r0) * p.ldo * 4;
+    const uint8_t* out0 = static_cast<uint8_t*>(p.out) + static_cast<int64_t>(r0) * p.ldo * 4;
     const int ldo4 = static_cast<int>(p.ldo) * 4;
+    uint32_t ooff[Cfg::FR][Cfg::FC];
 #pragma unroll
     for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
         for (int j = 0; j < Cfg::FC; ++j) {
             const int n = c0 + wc * Cfg::WC + j * 32 + (lane & 31);
             const int row = wr * Cfg::WR + i * 32 + 4 * h;
-            const uint32_t voff = n < p.N ? static_cast<uint32_t>(row * ldo4 + n * 4) : 0x80000000u;
+            ooff[i][j] = n < p.N ? static_cast<uint32_t>(row * ldo4 + n * 4) : 0x80000000u;
+        }
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int soff = (8 * (e >> 2) + (e & 3)) * ldo4;
+    for (int e = 0; e < 16; ++e) {
+        const __amdgpu_buffer_rsrc_t o_rs =
+            buffer_range(out0, out_bytes, static_cast<uint64_t>(8 * (e >> 2) + (e & 3)) * ldo4);
+#pragma unroll
+        for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j) {
                 const uint32_t bits = FLOAT_OUT ? __float_as_uint(acc[i][j][e] * p.scale)
                                                 : static_cast<uint32_t>(static_cast<int>(acc[i][j][e]));
-                __builtin_amdgcn_raw_buffer_store_b32(bits, o_rs, voff, soff, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(bits, o_rs, ooff[i][j], 0, 0);
             }
-        }
+    }
 }
 
 int launch_f4_gemm(const F4GemmArgs& a, bool float_out, hipStream_t stream) {

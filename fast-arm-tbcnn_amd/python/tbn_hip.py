@@ -106,6 +106,7 @@ _SIGNATURES = {
                                       _I32, _P, _P], _I32),
     "tbn_hip_conv2d_f32_quantized_noalloc": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _I64, _I64, _P, _F32, _P,
                                               _P, _I32, _P, _P], _I32),
+    "tbn_hip_gemm_kernel_name": ([_I32, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_char_p, ctypes.c_size_t], _I32),
     "tbn_hip_conv_weights_bytes": ([_I32, ctypes.POINTER(ConvDesc), ctypes.POINTER(ctypes.c_int64)], _I32),
     "tbn_hip_pack_conv_weights": ([_I32, _P, _I64, _I64, ctypes.POINTER(ConvDesc), _P, _P], _I32),
     "tbn_hip_conv2d_f32_prepacked": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P, _P], _I32),

@@ -195,6 +195,9 @@ int tbn_hip_quantize_pack_ternary_f32(const float* w, int64_t K, int64_t N, int 
  * scale: per-column fp32 [N] or NULL (then s = 1); alpha: scalar multiplier
  * (the reference's scalar `scale` argument); bias: [N] or NULL.
  * C: fp32 [M, N], ldc >= N.  Requires K_pad % 32 == 0, K_pad >= K, N_pad >= N.
+ * Shapes whose tiles would not fill the chip split K over blocks and keep the
+ * partial sums in the library's per-device stream workspace; those calls
+ * return TBN_NOT_IMPLEMENTED while the stream captures.
  * Replaces tbn::qlinear_matmul_binary / _blocked_packed / _naive
  * (quantized_gemm_neon.cpp:63-90,249-309,380-430), computing the fp32-activation
  * product of qlinear_matmul_binary_naive. */
@@ -212,6 +215,15 @@ int tbn_hip_gemm_f32_ternary(const float* A, int64_t lda, int64_t M, int64_t N, 
 
 /* Weight kinds of the general entry points below. */
 enum tbn_weights_kind { TBN_WEIGHTS_BINARY = 0, TBN_WEIGHTS_TERNARY = 1 };
+
+/* No counterpart in the reference (a diagnostic for profiling).  Writes into
+ * name (len bytes, NUL-terminated, truncated if short) the kernel, as a
+ * profiler names it, that tbn_hip_gemm_f32_binary (weights
+ * TBN_WEIGHTS_BINARY) or _ternary runs for this shape in this process now
+ * (tuning controls included), for 16-byte aligned A and packed weights.  No
+ * GPU work. */
+int tbn_hip_gemm_kernel_name(int weights, int64_t M, int64_t N, int64_t K, int64_t lda, int64_t K_pad,
+                             int64_t N_pad, char* name, size_t len);
 
 /* General quantized GEMM used by the Session's quantized Gemm node
  * (model.hpp:763-870): weights binary or ternary as above, and
@@ -266,9 +278,11 @@ int tbn_hip_conv2d_f32_quantized(int weights, const float* x, const tbn_conv2d_d
  * (ternary) and ordered [step][m], so that neighbouring channels' words sit
  * next to each other.  Channels >= C, and channels m >= M, are +1 / 0 and
  * meet zero activations.  The entry points above re-order the reference layout
- * into a stream-ordered temporary (hipMallocAsync) on every call; a caller
- * that runs a layer many times (the Session) packs once and calls
- * tbn_hip_conv2d_f32_prepacked, which allocates nothing. */
+ * into the library's per-device stream workspace on every call, and return
+ * TBN_NOT_IMPLEMENTED while their stream captures (nothing is allocated into
+ * a graph); a caller that runs a layer many times (the Session) packs once
+ * and calls tbn_hip_conv2d_f32_prepacked, and a caller that must capture a
+ * reference-layout conv uses tbn_hip_conv2d_f32_quantized_noalloc. */
 
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
@@ -299,7 +313,8 @@ int tbn_hip_pack_conv_weights(int weights, const uint8_t* packed, int64_t K_pad,
  * epilogue, no weight re-order.  Returns TBN_INVALID_SHAPE for geometries
  * whose patch does not fit (very large kernels or dilations).  Geometries
  * that split K (small maps with many input channels) keep their partial sums
- * in the library's per-device stream workspace, allocated on first use. */
+ * in the library's per-device stream workspace, allocated on first use;
+ * such geometries return TBN_NOT_IMPLEMENTED while the stream captures. */
 int tbn_hip_conv2d_f32_prepacked(int weights, const float* x, const tbn_conv2d_desc* desc,
                                  const uint8_t* conv_weights, const float* scale, float alpha, const float* bias,
                                  const float* residual, int flags, float* y, tbn_stream_t stream);

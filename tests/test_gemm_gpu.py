@@ -4,6 +4,8 @@ subsystem 2).  Tolerance (north_star): rel-L2 <= 1e-5 and max-abs <=
 against the float64 oracle; the fp32 sequential oracle is checked the same way.
 Full-size shapes (4096^3) are checked through size-independent properties:
 exact row spot checks, column checksums and linearity."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -399,17 +401,25 @@ def test_gemm_error_codes(dev):
     tbn_hip.call("tbn_hip_gemm_f32_binary", None, 0, 0, 8, 64, None, 64, 8, None, 1.0, None, 0, None, 8, None)
 
 
-@pytest.mark.parametrize("tile,splits", [(0, 1), (0, 3), (1, 1), (1, 2), (1, 5), (1, 8), (2, 1), (2, 4)])
-@pytest.mark.parametrize("ternary", [False, True], ids=["binary", "ternary"])
-def test_gemm_wide_every_tile_and_split(dev, orc, tile, splits, ternary):
-    """Each wide tile (128x512, 64x128, and 32x128 whose two K groups each
-    take half of the 18 K steps, the last one partial), whole or with K split
-    over blocks whose last finisher adds the splits in split order (the
-    K-group tile ignores a forced split): within the tolerance of the float64
-    oracle, and bit-identical on a second run (the order does not depend on
-    which block finishes last)."""
-    M, K, N = 300, 1100, 700
-    rng = np.random.default_rng(tile * 10 + splits + 100 * ternary)
+# (tile, forced splits) -> (M, K, N): each shape gives the forced tile enough
+# blocks to run on the wide kernels (gemm_wide_fits), with ragged M and N and
+# a partial last K step (K = 1100); the K-group tile ignores a forced split.
+WIDE_CASES = {(0, 1): (1100, 1100, 4000), (0, 3): (300, 1100, 3600), (0, 8): (300, 1100, 1600),
+              (1, 1): (300, 1100, 3300), (1, 2): (300, 1100, 1700), (1, 5): (300, 1100, 700),
+              (1, 8): (300, 1100, 700), (2, 1): (300, 1100, 1000), (2, 4): (300, 1100, 1000)}
+WIDE_FAMILY = {0: "gemm_wide_kernel<WideCfg<128, 512,", 1: "gemm_mid_kernel<WideCfg<64, 128,",
+               2: "gemm_mid_kernel<WideCfg<32, 128,"}
+
+
+def gemm_kernel_name(ternary, M, N, K, K_pad, N_pad):
+    name = ctypes.create_string_buffer(256)
+    tbn_hip.call("tbn_hip_gemm_kernel_name", int(ternary), M, N, K, K, K_pad, N_pad, name, 256)
+    return name.value.decode()
+
+
+def make_wide_operands(rng, M, K, N, ternary):
+    """A, scale, bias and the packed weights of one wide-tile case, with the
+    float64 product of its sign matrix for the checker."""
     A = rng.standard_normal((M, K)).astype(np.float32)
     scale = rng.uniform(0.5, 1.5, N).astype(np.float32)
     bias = (rng.standard_normal(N) * 0.01).astype(np.float32)
@@ -418,17 +428,62 @@ def test_gemm_wide_every_tile_and_split(dev, orc, tile, splits, ternary):
         t = rng.choice(np.int8([-1, 0, 1]), size=(K, N), p=[0.3, 0.4, 0.3])
         packed = empty(N_pad * K_pad // 4, torch.uint8)
         tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(t)), K, N, tbn_hip.LAYOUT_KN, K_pad, N_pad, P(packed), None)
-        ref = _f64_dev_ternary(A, t, scale, bias=bias, relu=True)
+        ref = lambda: _f64_dev_ternary(A, t, scale, bias=bias, relu=True)  # noqa: E731
     else:
         binw = (rng.random((K, N)) < 0.5).astype(np.uint8)
         packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
-        ref = _f64_dev_gemm(A, binw, scale, bias=bias, relu=True)
+        ref = lambda: _f64_dev_gemm(A, binw, scale, bias=bias, relu=True)  # noqa: E731
+    return A, scale, bias, packed, K_pad, N_pad, ref
+
+
+@pytest.mark.parametrize("tile,splits", sorted(WIDE_CASES))
+@pytest.mark.parametrize("ternary", [False, True], ids=["binary", "ternary"])
+def test_gemm_wide_every_tile_and_split(dev, orc, tile, splits, ternary):
+    """Each wide tile (128x512, 64x128, and 32x128 whose two K groups each
+    take half of the 18 K steps, the last one partial), whole or with K split
+    over blocks whose last finisher adds the splits in split order: the kernel
+    the library names is the forced tile's (split-K where forced), the result
+    is within the tolerance of the float64 product, and bit-identical on a
+    second run (the order does not depend on which block finishes last)."""
+    M, K, N = WIDE_CASES[(tile, splits)]
+    rng = np.random.default_rng(tile * 10 + splits + 100 * ternary)
+    A, scale, bias, packed, K_pad, N_pad, ref = make_wide_operands(rng, M, K, N, ternary)
     kind = "ternary" if ternary else "binary"
     with tbn_hip.tuning(tbn_hip.TUNE_GEMM_TILE, tile), tbn_hip.tuning(tbn_hip.TUNE_GEMM_SPLITS, splits):
+        name = gemm_kernel_name(ternary, M, N, K, K_pad, N_pad)
         c1 = host(run_gemm(kind, A, K, M, N, K, packed, K_pad, N_pad, scale, 1.0, bias, tbn_hip.EPI_RELU))
         c2 = host(run_gemm(kind, A, K, M, N, K, packed, K_pad, N_pad, scale, 1.0, bias, tbn_hip.EPI_RELU))
+    assert name.startswith(WIDE_FAMILY[tile]), name
+    assert name.endswith(", true>" if splits > 1 and tile != 2 else ", false>"), name
     assert np.array_equal(c1.view(np.uint32), c2.view(np.uint32))
-    rm.assert_within_tolerance(c1, ref, K, np.abs(A).max() * 1.5)
+    rm.assert_within_tolerance(c1, ref(), K, np.abs(A).max() * 1.5)
+
+
+@pytest.mark.parametrize("tile,splits", [(0, 1), (0, 8), (1, 5), (2, 1)])
+@pytest.mark.parametrize("ternary", [False, True], ids=["binary", "ternary"])
+def test_gemm_wide_leaves_memory_past_the_output_alone(dev, orc, tile, splits, ternary):
+    """Ragged M through each wide tile, whole and split over K (the partial
+    sums' row step lives in the buffer resource's base, so rows past M stay
+    range-checked): 32 guard rows of NaN after C, and the columns between N
+    and ldc, keep their bits; rows < M equal a plain run's."""
+    M, K, N = WIDE_CASES[(tile, splits)]
+    ldc = N + 8
+    rng = np.random.default_rng(17 + tile + splits + 100 * ternary)
+    A, scale, _, packed, K_pad, N_pad, _ = make_wide_operands(rng, M, K, N, ternary)
+    kind = "ternary" if ternary else "binary"
+    big = empty((M + 32, ldc), torch.float32)
+    big.fill_(np.nan)
+    guard = host(big).view(np.uint32).copy()
+    dA, ds = to_dev(A), to_dev(scale)
+    with tbn_hip.tuning(tbn_hip.TUNE_GEMM_TILE, tile), tbn_hip.tuning(tbn_hip.TUNE_GEMM_SPLITS, splits):
+        assert gemm_kernel_name(ternary, M, N, K, K_pad, N_pad).startswith(WIDE_FAMILY[tile])
+        tbn_hip.call(f"tbn_hip_gemm_f32_{kind}", P(dA), K, M, N, K, P(packed), K_pad, N_pad, P(ds), 1.0, None, 0,
+                     P(big), ldc, None)
+        plain = host(run_gemm(kind, A, K, M, N, K, packed, K_pad, N_pad, scale, 1.0, None, 0))
+    out = host(big)
+    assert np.array_equal(out[:M, :N].view(np.uint32), plain.view(np.uint32))
+    assert np.array_equal(out[M:].view(np.uint32), guard[M:]), "rows past M were written"
+    assert np.array_equal(out[:, N:].view(np.uint32), guard[:, N:]), "columns past N were written"
 
 
 def test_gemm_split_counters_survive_other_workspace_users(dev, orc):

@@ -182,6 +182,30 @@ def test_qlinear_tbn_matches_oracle(dev, orc, M, K, N):
     assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
 
 
+@pytest.mark.parametrize("M,N,ldo", [(2, 40, 40), (16, 300, 301), (300, 700, 700), (1040, 260, 264)])
+def test_qlinear_tbn_leaves_memory_past_the_output_alone(dev, orc, M, N, ldo):
+    """Ragged M (not a multiple of the 32-row fragments): the epilogue's
+    stores for rows past M are dropped by the buffer range check, so 32 guard
+    rows of NaN after the output (and the columns between N and ldo) keep
+    their bits."""
+    K = 330
+    rng = np.random.default_rng(M + N)
+    A = special_matrix(M, K, seed=M)
+    binw = (rng.random((K, N)) < 0.5).astype(np.uint8)
+    packed, K_pad, N_pad = gpu_pack_binary(binw, K, N)
+    big = empty((M + 32, ldo), torch.float32)
+    big.fill_(np.nan)
+    guard = host(big).view(np.uint32).copy()
+    tbn_hip.call("tbn_hip_qlinear_matmul_binary_tbn", P(to_dev(A)), K, M, K, P(packed), K_pad, N, N_pad, 0.5, LO,
+                 HI, P(big), ldo, None)
+    out = host(big)
+    rc, ref = orc.qlinear_matmul_binary_tbn(A, binw, 0.5, TILING)
+    assert rc == 0
+    assert np.array_equal(out[:M, :N].view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(out[M:].view(np.uint32), guard[M:]), "rows past M were written"
+    assert np.array_equal(out[:, N:].view(np.uint32), guard[:, N:]), "columns past N were written"
+
+
 def test_qlinear_tbn_headline_shape_exact(dev):
     """4096^3: every element equals float(exact integer product) * scale
     (the integer product formed in float64 on the GPU, exact below 2^53)."""
