@@ -22,12 +22,12 @@
 #include "common.hpp"
 #include "conv_common.hpp"
 #include "mfma_core.hpp"
+#include "tbn_f4.hpp"
 
 namespace {
 
 using namespace tbnk;
 
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
 typedef int i32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
@@ -121,9 +121,6 @@ __global__ void im2col_ternary_kernel(const float* __restrict__ x, Im2colDims d,
 // The fp4 operands of the GEMM
 // ---------------------------------------------------------------------------
 
-// fp4 (E2M1) codes: +1 = 0x2, -1 = 0xA, 0 = 0x0
-constexpr uint32_t kF4Plus = 0x2u, kF4Minus = 0xAu;
-
 // Activation rows of the operand pass, one fp4 dword (8 values) per call.
 // fp32 rows ternarized at (lo, hi): v < lo -> -1, v > hi -> +1, else 0 (NaN
 // gives 0), zero beyond K (GeMM/05-final/GeMM.cpp:71-112 and
@@ -179,16 +176,6 @@ struct RowsPlanes {
     }
 };
 
-// 8 BinaryMatrix bits (bit 1 = -1) -> 8 fp4 codes: bit e moved to bit 4 e + 3
-// over the +1 code (0x2 | 0x8 = 0xA is -1).
-__device__ __forceinline__ uint32_t bits_word(uint32_t b) {
-    uint32_t x = b & 0xFFu;
-    x = (x | (x << 12)) & 0x000F000Fu;
-    x = (x | (x << 6)) & 0x03030303u;
-    x = (x | (x << 3)) & 0x11111111u;
-    return 0x22222222u | (x << 3);
-}
-
 // Both GEMM operands in one pass: items [0, a_items) are the activation
 // dwords T4[row, 0..wpr) (8 values each), the rest the weight columns, 32
 // bits of a column each (one 4-byte load, one 16-byte store into W4[col,
@@ -234,6 +221,10 @@ struct F4GemmArgs {
     void* out;            // int32 or float [M, ldo]
     int64_t ldo;
     float scale;          // float output: out = float(C) * scale
+    const float* cin;     // float output with an addend: out = fma(beta, cin, float(C) * scale)
+    int cin_1d;           // cin [N] (else [M, N], row stride N)
+    float beta;
+    int relu;             // float output: then max(out, 0) (+0 for -0 and NaN)
 };
 
 template <int BR_, int BC_, int WR_, int WC_, int KS_, int NBUF_, bool EARLY_>
@@ -264,15 +255,6 @@ struct F4Cfg {
 // (Four buffers of 128 k measured 3 % slower at 4096^3.)
 using F4Wide = F4Cfg<256, 256, 128, 64, 256, 2, false>;
 
-typedef int i32x8_t __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ f32x16_t mfma_f4(i32x4_t a, i32x4_t b, f32x16_t c) {
-    const i32x8_t a8 = {a[0], a[1], a[2], a[3], 0, 0, 0, 0};
-    const i32x8_t b8 = {b[0], b[1], b[2], b[3], 0, 0, 0, 0};
-    // formats 4 / 4: fp4 (E2M1) A and B; scales 2^(127 - 127) = 1
-    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, c, 4, 4, 0, 127, 0, 127);
-}
-
 // buffer_load_dwordx4 ... lds: lane l's 16 bytes at voffset + soffset go to
 // LDS at dst + 16 l.
 __device__ __forceinline__ void load_lds16(__amdgpu_buffer_rsrc_t rs, uint8_t* dst, int voffset, int soffset) {
@@ -292,7 +274,7 @@ __device__ __forceinline__ int f4_slot(int r, int q) { return r * P + (q ^ f4_sw
 // Operands go global -> LDS with buffer_load_dwordx4 ... lds (no registers,
 // no LDS store instructions): a wave's load writes 64 consecutive 16-byte
 // slots, so each lane loads the global part that belongs in its slot.
-template <class Cfg, bool FLOAT_OUT>
+template <class Cfg, bool FLOAT_OUT, bool SESSION = false>
 __global__ void __launch_bounds__(Cfg::NT) tbn_f4_gemm_kernel(F4GemmArgs p, int tiles_r, int tiles_c) {
     __shared__ __attribute__((aligned(1024))) uint8_t lds[Cfg::NBUF * Cfg::BUF];
     constexpr int RB = Cfg::RB;
@@ -466,8 +448,24 @@ __global__ void __launch_bounds__(Cfg::NT) tbn_f4_gemm_kernel(F4GemmArgs p, int 
         for (int i = 0; i < Cfg::FR; ++i)
 #pragma unroll
             for (int j = 0; j < Cfg::FC; ++j) {
-                const uint32_t bits = FLOAT_OUT ? __float_as_uint(acc[i][j][e] * p.scale)
-                                                : static_cast<uint32_t>(static_cast<int>(acc[i][j][e]));
+                uint32_t bits;
+                if constexpr (SESSION) {
+                    // the Session's quantized Gemm (model.hpp:847-870): result * alpha,
+                    // then += beta * C, one fused multiply-add as AArch64 compilers
+                    // contract it; then a fused Relu node
+                    float v = acc[i][j][e] * p.scale;
+                    if (p.cin) {
+                        const int m = min(r0 + wr * Cfg::WR + i * 32 + 4 * h + 8 * (e >> 2) + (e & 3), p.M - 1);
+                        const int n = min(c0 + wc * Cfg::WC + j * 32 + (lane & 31), p.N - 1);
+                        const float c = p.cin_1d ? p.cin[n] : p.cin[static_cast<int64_t>(m) * p.N + n];
+                        v = __builtin_fmaf(p.beta, c, v);
+                    }
+                    if (p.relu) v = v > 0.0f ? v : 0.0f;
+                    bits = __float_as_uint(v);
+                } else {
+                    bits = FLOAT_OUT ? __float_as_uint(acc[i][j][e] * p.scale)
+                                     : static_cast<uint32_t>(static_cast<int>(acc[i][j][e]));
+                }
                 __builtin_amdgcn_raw_buffer_store_b32(bits, o_rs, ooff[i][j], 0, 0);
             }
     }
@@ -479,7 +477,10 @@ int launch_f4_gemm(const F4GemmArgs& a, bool float_out, hipStream_t stream) {
     TBN_REQUIRE(a.ldo < (1 << 21), TBN_INVALID_SHAPE, "TBN GEMM: output row stride of 2^21 elements or more");
     const int tiles_r = static_cast<int>(tbn_hip::ceil_div(a.M, Cfg::BR));
     const int tiles_c = static_cast<int>(tbn_hip::ceil_div(a.N, Cfg::BC));
-    if (float_out)
+    if (float_out && (a.cin || a.relu))
+        hipLaunchKernelGGL((tbn_f4_gemm_kernel<Cfg, true, true>), dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, stream,
+                           a, tiles_r, tiles_c);
+    else if (float_out)
         hipLaunchKernelGGL((tbn_f4_gemm_kernel<Cfg, true>), dim3(tiles_r * tiles_c), dim3(Cfg::NT), 0, stream, a,
                            tiles_r, tiles_c);
     else
@@ -551,7 +552,7 @@ int planes_gemm(const uint8_t* pos, const uint8_t* neg, const uint8_t* bits, int
     if (rc != TBN_SUCCESS) return rc;
     F4GemmArgs a{reinterpret_cast<const uint8_t*>(T4), n / 2, reinterpret_cast<const uint8_t*>(W4), n / 2,
                  static_cast<int>(bit_cols), static_cast<int>(m), static_cast<int>(cols), static_cast<int>(n), out,
-                 ldo, scale};
+                 ldo, scale, nullptr, 0, 0.0f, 0};
     return launch_f4_gemm(a, float_out, s);
 }
 
@@ -625,6 +626,53 @@ int tbn_hip_tbn_gemm_scaled(const uint8_t* pos, const uint8_t* neg, const uint8_
     return planes_gemm(pos, neg, bits, m, n, cols, k, true, scale, out, ldo, s);
 }
 
+int tbn_hip_pack_f4_weights(const uint8_t* packed, int64_t K_pad, int64_t N_pad, uint8_t* w4, tbn_stream_t stream) {
+    TBN_REQUIRE(K_pad >= 0 && N_pad >= 0 && K_pad % 64 == 0 && K_pad < (1LL << 24) && N_pad < (1LL << 31),
+                TBN_INVALID_SHAPE, "K_pad must be a multiple of 64 below 2^24");
+    if (K_pad == 0 || N_pad == 0) return tbn_hip::ok();
+    TBN_REQUIRE(packed && w4, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_REQUIRE(reinterpret_cast<uintptr_t>(packed) % 4 == 0 && reinterpret_cast<uintptr_t>(w4) % 16 == 0,
+                TBN_INVALID_ARGUMENT, "packed must be 4-byte and w4 16-byte aligned");
+    TBN_DEVICE_GUARD();
+    return launch_f4_operands(RowsF32{nullptr, 0, 0, 0.0f, 0.0f, false}, 0, K_pad, nullptr, packed, K_pad / 8, N_pad,
+                              reinterpret_cast<uint32_t*>(w4), tbn_hip::stream_of(stream), "pack_f4_weights");
+}
+
+int tbn_hip_gemm_tbn_prepacked(const float* A, int64_t lda, int64_t M, int64_t K, const uint8_t* w4, int64_t K_pad,
+                               int64_t N, int64_t N_pad, float alpha, const float* cin, int cin_1d, float beta,
+                               float lo, float hi, int flags, uint8_t* t4, float* out, int64_t ldo,
+                               tbn_stream_t stream) {
+    TBN_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M < (1LL << 31) && N < (1LL << 31) && K_pad < (1LL << 24),
+                TBN_INVALID_SHAPE, "M, N, K out of range");
+    TBN_REQUIRE(K_pad >= K && K_pad % 64 == 0, TBN_INVALID_SHAPE, "K_pad must be >= K and a multiple of 64");
+    TBN_REQUIRE(N_pad >= N, TBN_INVALID_SHAPE, "N_pad must be >= N");
+    TBN_REQUIRE(M == 0 || lda >= K, TBN_INVALID_ARGUMENT, "lda must be >= K");
+    TBN_REQUIRE(ldo >= N, TBN_INVALID_ARGUMENT, "ldo must be >= N");
+    TBN_REQUIRE((flags & ~TBN_EPI_RELU) == 0, TBN_INVALID_ARGUMENT, "unsupported epilogue flags for a TBN Gemm");
+    if (M == 0 || N == 0) return tbn_hip::ok();
+    TBN_REQUIRE(out && t4 && (K == 0 || A) && (K_pad == 0 || w4), TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_REQUIRE(reinterpret_cast<uintptr_t>(t4) % 16 == 0 && reinterpret_cast<uintptr_t>(w4) % 16 == 0,
+                TBN_INVALID_ARGUMENT, "t4 and w4 must be 16-byte aligned");
+    TBN_DEVICE_GUARD();
+    hipStream_t s = tbn_hip::stream_of(stream);
+    const bool add = cin && beta != 0.0f;
+    if (K_pad == 0) {
+        TBN_REQUIRE(!add && !flags, TBN_NOT_IMPLEMENTED, "TBN Gemm with an empty shared dimension and an epilogue");
+        if (hipMemset2DAsync(out, ldo * sizeof(float), 0, N * sizeof(float), M, s) != hipSuccess)
+            return tbn_hip::fail(TBN_RUNTIME_ERROR, "hipMemset2DAsync failed");
+        return tbn_hip::ok();
+    }
+    const bool vec = K % 4 == 0 && lda % 4 == 0 && reinterpret_cast<uintptr_t>(A) % 16 == 0;
+    int rc = launch_f4_operands(RowsF32{A, lda, static_cast<int>(K), lo, hi, vec}, M, K_pad,
+                                reinterpret_cast<uint32_t*>(t4), nullptr, 0, 0, nullptr, s,
+                                "gemm_tbn_prepacked (fp4 activations)");
+    if (rc != TBN_SUCCESS) return rc;
+    F4GemmArgs a{t4, K_pad / 2, w4, K_pad / 2, static_cast<int>(N_pad), static_cast<int>(M), static_cast<int>(N),
+                 static_cast<int>(K_pad), out, ldo, alpha, add ? cin : nullptr, cin_1d, beta,
+                 (flags & TBN_EPI_RELU) ? 1 : 0};
+    return launch_f4_gemm(a, true, s);
+}
+
 int tbn_hip_qlinear_matmul_binary_tbn(const float* A, int64_t lda, int64_t M, int64_t K, const uint8_t* packed,
                                       int64_t K_pad, int64_t N, int64_t N_pad, float scale, float lo, float hi,
                                       float* out, int64_t ldo, tbn_stream_t stream) {
@@ -656,7 +704,7 @@ int tbn_hip_qlinear_matmul_binary_tbn(const float* A, int64_t lda, int64_t M, in
     if (rc != TBN_SUCCESS) return rc;
     F4GemmArgs a{reinterpret_cast<const uint8_t*>(T4), K_pad / 2, reinterpret_cast<const uint8_t*>(W4), K_pad / 2,
                  static_cast<int>(N_pad), static_cast<int>(M), static_cast<int>(N), static_cast<int>(K_pad), out,
-                 ldo, scale};
+                 ldo, scale, nullptr, 0, 0.0f, 0};
     return launch_f4_gemm(a, true, s);
 }
 

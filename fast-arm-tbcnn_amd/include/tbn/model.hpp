@@ -79,10 +79,18 @@ struct ModelGraph {
     std::vector<std::string> outputs;
 };
 
-// Arithmetic of quantized layers in a Session with quantization enabled.
+// Arithmetic of the quantized layers of a Session (the reference's
+// conv2d_binary / conv2d_ternary convs, and with quantization enabled its
+// auto-quantized convs and Gemms).
 //   F32: fp32 activations times exact +-1 (times the per-channel scale where
-//        the reference applies one), fp32 accumulation.
-enum class QuantArithmetic { F32 };
+//        the reference applies one), fp32 accumulation -- the float x binary
+//        product (the default).
+//   TBN: the reference's own arithmetic, bit for bit: activations ternarized
+//        at +-0.1, integer products with the +-1 weights, float(C) then the
+//        reference's bias / scale / alpha / beta steps (model.hpp:414-564,
+//        763-870; conv2d.cpp:195-316).  Grouped and depthwise convs, which
+//        the reference cannot run, keep F32.
+enum class QuantArithmetic { F32, TBN };
 
 class TBNModel {
 public:
@@ -121,6 +129,9 @@ public:
 
         void set_quantization(bool enable);
         bool is_quantization_enabled() const;
+        // The arithmetic of the quantized layers (F32 by default).
+        void set_quant_arithmetic(QuantArithmetic a);
+        QuantArithmetic quant_arithmetic() const;
         void set_tiling(const TilingParams& p);
         const TilingParams& get_tiling() const;
 

@@ -154,14 +154,26 @@ Conv2DParams conv_params(const Tensor& w, std::vector<int64_t> stride, std::vect
     return p;
 }
 
+QuantArithmetic parse_arithmetic(const std::string& a) {
+    if (a == "f32") return QuantArithmetic::F32;
+    if (a == "tbn") return QuantArithmetic::TBN;
+    throw InvalidArgumentError("arithmetic must be 'f32' or 'tbn', got '" + a + "'");
+}
+
+const char* arithmetic_name(QuantArithmetic a) { return a == QuantArithmetic::TBN ? "tbn" : "f32"; }
+
 // The reference's PyModel (bindings.cpp:53-110): an ONNX file (or a graph)
-// with one Session reused by every run().
+// with one Session reused by every run().  `arithmetic` picks the quantized
+// layers' arithmetic: "f32" (float x binary) or "tbn" (the reference's own
+// ternarized integer product, bit for bit).
 class PyModel {
 public:
-    PyModel(TBNModel model, uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk, uint32_t nmk)
+    PyModel(TBNModel model, uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk, uint32_t nmk,
+            const std::string& arithmetic = "f32")
         : model_(std::move(model)) {
         TilingParams t{mblk, nblk, kblk, mmk, nmk};
         session_ = std::make_unique<TBNModel::Session>(model_.create_session(t));
+        session_->set_quant_arithmetic(parse_arithmetic(arithmetic));
     }
     py::array run(const py::object& input, bool use_quantization) {
         const auto& ins = model_.graph().inputs;
@@ -543,6 +555,10 @@ PYBIND11_MODULE(_tbn, m) {
     py::class_<TBNModel::Session>(m, "Session")
         .def("set_quantization", &TBNModel::Session::set_quantization)
         .def("is_quantization_enabled", &TBNModel::Session::is_quantization_enabled)
+        .def("set_quant_arithmetic",
+             [](TBNModel::Session& s, const std::string& a) { s.set_quant_arithmetic(parse_arithmetic(a)); },
+             py::arg("arithmetic"))
+        .def("quant_arithmetic", [](const TBNModel::Session& s) { return arithmetic_name(s.quant_arithmetic()); })
         .def("set_input", [](TBNModel::Session& s, const std::string& n, const py::object& t) { s.set_input(n, as_tensor(t)); })
         .def("run", &TBNModel::Session::run)
         .def("get_output", [](const TBNModel::Session& s, const std::string& n) { return to_numpy(s.get_output(n)); })
@@ -585,14 +601,18 @@ PYBIND11_MODULE(_tbn, m) {
 
     py::class_<PyModel>(m, "Model")
         .def(py::init([](const std::string& path, uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk,
-                         uint32_t nmk) { return new PyModel(load_onnx_model(path), mblk, nblk, kblk, mmk, nmk); }),
+                         uint32_t nmk, const std::string& arithmetic) {
+                 return new PyModel(load_onnx_model(path), mblk, nblk, kblk, mmk, nmk, arithmetic);
+             }),
              py::arg("path"), py::arg("mblk") = 64, py::arg("nblk") = 64, py::arg("kblk") = 128,
-             py::arg("mmk") = 32, py::arg("nmk") = 32,
+             py::arg("mmk") = 32, py::arg("nmk") = 32, py::arg("arithmetic") = "f32",
              "Load an ONNX model; the tiling arguments are accepted for compatibility.")
         .def(py::init([](std::shared_ptr<ModelGraph> g, uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk,
-                         uint32_t nmk) { return new PyModel(TBNModel(std::move(g)), mblk, nblk, kblk, mmk, nmk); }),
+                         uint32_t nmk, const std::string& arithmetic) {
+                 return new PyModel(TBNModel(std::move(g)), mblk, nblk, kblk, mmk, nmk, arithmetic);
+             }),
              py::arg("graph"), py::arg("mblk") = 64, py::arg("nblk") = 64, py::arg("kblk") = 128,
-             py::arg("mmk") = 32, py::arg("nmk") = 32)
+             py::arg("mmk") = 32, py::arg("nmk") = 32, py::arg("arithmetic") = "f32")
         .def("run", &PyModel::run, py::arg("input"), py::arg("use_quantization") = false)
         .def("run_quantized", [](PyModel& p, const py::object& x) { return p.run(x, true); }, py::arg("input"))
         .def("input_names", &PyModel::input_names)
@@ -603,11 +623,12 @@ PYBIND11_MODULE(_tbn, m) {
 
     // bindings.cpp:154-167 of the reference: load_model returns a Model.
     m.def("load_model",
-          [](const std::string& path, uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk, uint32_t nmk) {
-              return new PyModel(load_onnx_model(path), mblk, nblk, kblk, mmk, nmk);
+          [](const std::string& path, uint32_t mblk, uint32_t nblk, uint32_t kblk, uint32_t mmk, uint32_t nmk,
+             const std::string& arithmetic) {
+              return new PyModel(load_onnx_model(path), mblk, nblk, kblk, mmk, nmk, arithmetic);
           },
           py::arg("path"), py::arg("mblk") = 64, py::arg("nblk") = 64, py::arg("kblk") = 128, py::arg("mmk") = 32,
-          py::arg("nmk") = 32, py::return_value_policy::take_ownership);
+          py::arg("nmk") = 32, py::arg("arithmetic") = "f32", py::return_value_policy::take_ownership);
 
     // The C++ reader itself, for inspecting a model without a Session.
     py::class_<OnnxParser>(m, "OnnxParser")

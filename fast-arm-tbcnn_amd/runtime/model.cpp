@@ -208,7 +208,10 @@ struct Op {
     std::string weight_name, scale_name, bias_name;  // initializers behind w / scale / bias
     std::vector<float> bn_k, bn_t;   // ChannelAffine: y = x * k + t per channel (host copy)
     std::vector<const Tensor*> group_conv_w;  // per-group conv-layout weights (grouped patch conv)
-    int workspace = -1;              // value id of the op's transient workspace (grouped conv slices)
+    int workspace = -1;              // value id of the op's transient workspace (grouped conv slices,
+                                     // a TBN Gemm's fp4 activation rows)
+    bool tbn = false;                // TBN arithmetic (ternarized activations, integer products)
+    const Tensor* tbn_w = nullptr;   // its fp4 weights: TBN conv layout, or [N_pad, K_pad / 2] rows
     const float* scale = nullptr;  // per-channel scale (device)
     const float* w = nullptr;      // fp32 weights (device)
     const float* bias = nullptr;   // device
@@ -252,6 +255,7 @@ struct TBNModel::Session::Impl {
     std::shared_ptr<ModelGraph> graph;
     TilingParams tiling;
     bool quant = false;
+    QuantArithmetic arith = QuantArithmetic::F32;
     bool graph_replay = false;
     std::unordered_map<std::string, Tensor> inputs;
 
@@ -264,10 +268,12 @@ struct TBNModel::Session::Impl {
     std::unordered_map<std::string, Tensor> conv_packed;        // conv-layout copies of `packed` entries
     std::unordered_map<std::string, Tensor> scaled_addends;     // beta * C of quantized Gemms
     std::unordered_map<std::string, Tensor> derived;            // depthwise +-1 weights, BatchNormalization folds
+    std::unordered_map<std::string, Tensor> tbn_packed;         // fp4 weights of TBN-mode layers
 
     // ---- the compiled plan ----
     bool planned = false;
     bool plan_quant = false;
+    QuantArithmetic plan_arith = QuantArithmetic::F32;
     std::map<std::string, Shape> plan_shapes;
     std::deque<Value> values;  // deque: references stay valid as values are added
     std::unordered_map<std::string, int> value_id;
@@ -338,11 +344,48 @@ struct TBNModel::Session::Impl {
     }
 
     const PackedWeights& packed_binary(const std::string& wname, bool nk, int rule) {
-        // rule: 0 = BINARY bytes, 1 = float w > 0, 2 = float w >= 0
+        // rule: 0 = BINARY bytes, 1 = float w > 0, 2 = float w >= 0, 3 = TERNARY
+        // values collapsed to signs as conv2d_ternary does (t < 0 -> -1, 0 and
+        // +1 -> +1; conv2d.cpp:195-217)
         const std::string key = wname + "#b" + std::to_string(nk) + std::to_string(rule);
         auto it = packed.find(key);
         if (it != packed.end()) return it->second;
+        if (rule == 3) {
+            const Tensor& w = initializer(wname);
+            const Tensor host = w.on_device() ? w.to_device(DeviceType::CPU) : w;
+            Tensor bin(host.shape(), DataType::BINARY);
+            for (int64_t i = 0; i < host.num_elements(); ++i)
+                bin.typed_data<uint8_t>()[i] = host.typed_data<int8_t>()[i] < 0 ? 0 : 1;
+            return packed.emplace(key, pack_binary_weights(bin.to_device(DeviceType::HIP), nk, false)).first->second;
+        }
         return packed.emplace(key, pack_binary_weights(device_init(wname), nk, rule == 2)).first->second;
+    }
+
+    // fp4 weights of a TBN-mode conv (the TBN conv layout) or Gemm ([N_pad,
+    // K_pad / 2] rows), made once per Session from the packed bits.
+    const Tensor& tbn_conv_weights(const std::string& node, const PackedWeights& pw, const tbn_conv2d_desc& d) {
+        const std::string key = node + "#tbnconv" + std::to_string(reinterpret_cast<uintptr_t>(&pw));
+        auto it = tbn_packed.find(key);
+        if (it != tbn_packed.end()) return it->second;
+        int64_t bytes = 0;
+        check_status(tbn_hip_tbn_conv_weights_bytes(&d, &bytes), ("Conv '" + node + "'").c_str());
+        Tensor w4 = Tensor::empty({bytes}, DataType::UINT8, DeviceType::HIP);
+        check_status(tbn_hip_pack_tbn_conv_weights(pw.bits.typed_data<uint8_t>(), pw.K_pad, pw.N_pad, &d,
+                                                   w4.typed_data<uint8_t>(), cur_stream()),
+                     ("Conv '" + node + "'").c_str());
+        return tbn_packed.emplace(key, w4).first->second;
+    }
+
+    const Tensor& tbn_gemm_weights(const std::string& node, const PackedWeights& pw, bool fill) {
+        const std::string key = node + "#tbngemm" + std::to_string(reinterpret_cast<uintptr_t>(&pw));
+        auto it = tbn_packed.find(key);
+        if (it != tbn_packed.end()) return it->second;
+        Tensor w4 = Tensor::empty({pw.N_pad * pw.K_pad / 2}, DataType::UINT8, DeviceType::HIP);
+        if (fill)
+            check_status(tbn_hip_pack_f4_weights(pw.bits.typed_data<uint8_t>(), pw.K_pad, pw.N_pad,
+                                                 w4.typed_data<uint8_t>(), cur_stream()),
+                         ("Gemm '" + node + "'").c_str());
+        return tbn_packed.emplace(key, w4).first->second;
     }
 
     // The packed-bits buffer of a quantized Gemm whose B is not an initializer
@@ -473,6 +516,8 @@ struct TBNModel::Session::Impl {
         op.weight_name = wname;
         const bool depthwise = p.groups > 1 && ws.dims[1] == 1;
         const DataType wt = values[wi].dtype;
+        // TBN arithmetic for the convs the reference itself can run
+        const bool tbn = arith == QuantArithmetic::TBN && p.groups == 1;
         int dw_rule = -1;  // depthwise weights: -1 fp32 as stored, else the depthwise_weights rule
         if (wt == DataType::BINARY) {
             op.kind = OpKind::ConvQuant;
@@ -481,7 +526,7 @@ struct TBNModel::Session::Impl {
         } else if (wt == DataType::TERNARY) {
             op.kind = OpKind::ConvQuant;
             if (depthwise) dw_rule = 3;
-            else op.pw = &packed_ternary(wname, true);
+            else op.pw = tbn ? &packed_binary(wname, true, 3) : &packed_ternary(wname, true);
         } else if (wt == DataType::FLOAT32 && quant && quantize_allowed(node)) {
             op.kind = OpKind::ConvQuant;
             conv_scales(wname);
@@ -505,6 +550,15 @@ struct TBNModel::Session::Impl {
         if (depthwise) {
             op.kind = OpKind::ConvDepthwise;
             op.w = dw_rule < 0 ? const_f32(wi) : depthwise_weights(wname, dw_rule);
+            op.out = new_value(node.outputs[0], Shape{xs.dims[0], ws.dims[0], OH, OW}, DataType::FLOAT32);
+            ops.push_back(op);
+            return;
+        }
+        if (tbn && op.kind == OpKind::ConvQuant) {
+            // ternarized taps times the +-1 weights, then the reference's
+            // bias / scale steps (model.hpp:482-557, conv2d.cpp:220-316)
+            op.tbn = true;
+            op.tbn_w = &tbn_conv_weights(node.name, *op.pw, op.desc);
             op.out = new_value(node.outputs[0], Shape{xs.dims[0], ws.dims[0], OH, OW}, DataType::FLOAT32);
             ops.push_back(op);
             return;
@@ -649,6 +703,14 @@ struct TBNModel::Session::Impl {
                 op.in.push_back(bi);
             }
             // then result * alpha + beta * C (model.hpp:847-870)
+            if (arith == QuantArithmetic::TBN) {
+                // qlinear_matmul_binary_blocked_packed's ternarized product
+                // (quantized_gemm_neon.cpp:249-309); the fp4 activation rows
+                // go to a workspace slot of the arena
+                op.tbn = true;
+                op.tbn_w = &tbn_gemm_weights(node.name, *op.pw, op.dyn_b < 0);
+                op.workspace = new_value(node.name + "#t4", Shape{op.M * (op.pw->K_pad / 2)}, DataType::UINT8);
+            }
         } else {
             op.kind = OpKind::GemmF32;
             op.in.push_back(bi);
@@ -958,14 +1020,19 @@ struct TBNModel::Session::Impl {
                     }
                 }
             }
-            // 2x2/2 floor MaxPool (with or without a Relu either side) into Conv
+            // 2x2/2 floor MaxPool (with or without a Relu either side) into Conv;
+            // a TBN conv fuses the pool only together with a Relu
             if (conv && op.residual < 0 && op.groups == 1 && op.kind != OpKind::ConvDepthwise) {
                 int r = sole_reader(op.out);
                 if (r >= 0 && ops[r].kind == OpKind::MaxPool) {
                     const Pool2DParams& p = ops[r].pool;
                     const Shape& s = values[op.out].shape;
+                    int after = sole_reader(ops[r].out);
+                    const bool relu_ok = !op.tbn || (op.flags & TBN_EPI_RELU) ||
+                                         (after >= 0 && ops[after].kind == OpKind::Relu);
                     if (p.kernel_h == 2 && p.kernel_w == 2 && p.stride_h == 2 && p.stride_w == 2 && p.pad_h == 0 &&
-                        p.pad_w == 0 && s.dims[2] >= 2 && s.dims[3] >= 2) {
+                        p.pad_w == 0 && p.dilation_h == 1 && p.dilation_w == 1 && !p.ceil_mode && s.dims[2] >= 2 &&
+                        s.dims[3] >= 2 && relu_ok) {
                         op.flags |= TBN_EPI_MAXPOOL2X2;
                         absorb(static_cast<int>(i), r);
                         int r2 = sole_reader(op.out);
@@ -1082,6 +1149,7 @@ struct TBNModel::Session::Impl {
                 launches += op.groups > 1 && op.kind != OpKind::ConvDepthwise ? op.groups * (op.desc.n == 1 ? 1 : 3) : 1;
         planned = true;
         plan_quant = quant;
+        plan_arith = arith;
         plan_shapes.clear();
         for (auto& kv : inputs) plan_shapes[kv.first] = kv.second.shape();
     }
@@ -1107,7 +1175,7 @@ struct TBNModel::Session::Impl {
     }
 
     bool plan_valid() const {
-        if (!planned || plan_quant != quant) return false;
+        if (!planned || plan_quant != quant || plan_arith != arith) return false;
         if (plan_shapes.size() != inputs.size()) return false;
         for (auto& kv : inputs) {
             auto it = plan_shapes.find(kv.first);
@@ -1173,6 +1241,14 @@ struct TBNModel::Session::Impl {
                 return;
             case OpKind::ConvQuant:
                 if (op.groups > 1) return launch_grouped(op, s, what);
+                if (op.tbn) {
+                    check_status(tbn_hip_conv2d_tbn_prepacked(fp(op.in[0]), &op.desc, op.tbn_w->typed_data<uint8_t>(),
+                                                              op.scale, 1.0f, bias_of(op),
+                                                              op.residual >= 0 ? fp(op.residual) : nullptr, op.flags,
+                                                              -0.1f, 0.1f, fp(op.out), s),
+                                 what.c_str());
+                    return;
+                }
                 if (op.conv_w) {
                     check_status(tbn_hip_conv2d_f32_prepacked(
                                      op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY
@@ -1199,6 +1275,19 @@ struct TBNModel::Session::Impl {
                                                                   s),
                                  what.c_str());
                 const float* cin = op.cin ? op.cin : (op.cin_value >= 0 ? fp(op.cin_value) : nullptr);
+                if (op.tbn) {
+                    uint8_t* w4 = const_cast<uint8_t*>(op.tbn_w->typed_data<uint8_t>());
+                    if (op.dyn_b >= 0)
+                        check_status(tbn_hip_pack_f4_weights(op.pw->bits.typed_data<uint8_t>(), op.pw->K_pad,
+                                                             op.pw->N_pad, w4, s),
+                                     what.c_str());
+                    check_status(tbn_hip_gemm_tbn_prepacked(fp(op.in[0]), op.K, op.M, op.K, w4, op.pw->K_pad, op.N,
+                                                            op.pw->N_pad, op.alpha, cin, op.cin_1d, op.beta, -0.1f,
+                                                            0.1f, op.flags, static_cast<uint8_t*>(ptr(op.workspace)),
+                                                            fp(op.out), op.N, s),
+                                 what.c_str());
+                    return;
+                }
                 check_status(tbn_hip_gemm_f32_quantized(
                                  op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY : TBN_WEIGHTS_TERNARY,
                                  fp(op.in[0]), op.K, op.M, op.N, op.K, op.pw->bits.typed_data<uint8_t>(),
@@ -1415,6 +1504,7 @@ struct TBNModel::Session::Impl {
         for (auto& kv : dev_init) b += kv.second.data_size();
         for (auto& kv : packed) b += kv.second.bits.data_size();
         for (auto& kv : conv_packed) b += kv.second.data_size();
+        for (auto& kv : tbn_packed) b += kv.second.data_size();
         for (auto& kv : dev_scales) b += kv.second.data_size();
         return b;
     }
@@ -1436,6 +1526,8 @@ TBNModel::Session& TBNModel::Session::operator=(Session&&) noexcept = default;
 
 void TBNModel::Session::set_quantization(bool enable) { impl_->quant = enable; }
 bool TBNModel::Session::is_quantization_enabled() const { return impl_->quant; }
+void TBNModel::Session::set_quant_arithmetic(QuantArithmetic a) { impl_->arith = a; }
+QuantArithmetic TBNModel::Session::quant_arithmetic() const { return impl_->arith; }
 void TBNModel::Session::set_tiling(const TilingParams& p) { impl_->tiling = p; }
 const TilingParams& TBNModel::Session::get_tiling() const { return impl_->tiling; }
 

@@ -477,6 +477,59 @@ int tbn_hip_qlinear_matmul_binary_tbn(const float* A, int64_t lda, int64_t M, in
                                       int64_t N_pad, float scale, float lo, float hi, float* out,
                                       int64_t ldo, tbn_stream_t stream);
 
+/* BinaryMatrix columns (K_pad / 8 bytes each, bit 1 = -1) -> fp4 weight rows
+ * w4 [N_pad, K_pad / 2] (two E2M1 codes a byte, low nibble first: +1 = 0x2,
+ * -1 = 0xA), the operand layout of tbn_hip_gemm_tbn_prepacked.  K_pad % 64 ==
+ * 0, packed 4-byte and w4 16-byte aligned.  The B-side half of
+ * qlinear_matmul_binary_blocked_packed's per-Session cache
+ * (model.hpp:809-833), done once. */
+int tbn_hip_pack_f4_weights(const uint8_t* packed, int64_t K_pad, int64_t N_pad, uint8_t* w4,
+                            tbn_stream_t stream);
+/* The Session's quantized Gemm as the reference computes it
+ * (qlinear_matmul_binary_blocked_packed, quantized_gemm_neon.cpp:249-309, then
+ * model.hpp:847-870): out[m, n] = float(sum_k t(A[m, k]) * w[k, n]) * alpha,
+ * then, when cin is given and beta != 0, out = fma(beta, cin, out) with cin
+ * [N] (cin_1d) or [M, N] (row stride N) -- the reference's `r += beta * c`
+ * as AArch64 compilers contract it; then TBN_EPI_RELU (the only flag).  t is
+ * the ternarization at (lo, hi) (v < lo -> -1, v > hi -> +1, else 0); w4 from
+ * tbn_hip_pack_f4_weights.  t4: caller scratch of M * K_pad / 2 bytes
+ * (16-byte aligned) for the fp4 activation rows, so the call allocates
+ * nothing. */
+int tbn_hip_gemm_tbn_prepacked(const float* A, int64_t lda, int64_t M, int64_t K, const uint8_t* w4,
+                               int64_t K_pad, int64_t N, int64_t N_pad, float alpha, const float* cin,
+                               int cin_1d, float beta, float lo, float hi, int flags, uint8_t* t4,
+                               float* out, int64_t ldo, tbn_stream_t stream);
+
+/* ---- TBN-mode Conv2D (implicit GEMM, ternarized while staging) ------------ */
+
+/* Bytes of the TBN conv weights for desc: ceil(M / 32) fragments x kh*kw*
+ * ceil(C / 64) k-steps x 1024. */
+int tbn_hip_tbn_conv_weights_bytes(const tbn_conv2d_desc* desc, int64_t* bytes);
+/* Re-orders the reference-layout BinaryMatrix of the [M, C*kh*kw] weights
+ * (layout NK, as tbn_hip_conv2d_f32_binary takes them) into the TBN conv
+ * layout: for each 32-channel fragment and k-step (chunk of 64 input
+ * channels x tap), 64 lanes x 16 bytes of fp4 codes, lane l holding channel
+ * l % 32 and input channels 32 (l / 32) .. +31 of the chunk.  w4 16-byte
+ * aligned.  The weight-side cache of the Session's conv (model.hpp:456-480). */
+int tbn_hip_pack_tbn_conv_weights(const uint8_t* packed, int64_t K_pad, int64_t N_pad,
+                                  const tbn_conv2d_desc* desc, uint8_t* w4, tbn_stream_t stream);
+/* The reference Session's quantized convolution (model.hpp:482-557 with
+ * im2col_ternary_packed, conv2d.cpp:511-601; conv2d_binary, conv2d.cpp:
+ * 220-316): every input tap ternarized at (lo, hi), taps outside the image 0,
+ * times the +-1 weights in exact integer arithmetic (C = the reference's
+ * int32), then y = float(C) * alpha*s[m] + b[m] (two roundings) or with
+ * TBN_EPI_BIAS_THEN_SCALE (float(C) + b[m]) * alpha*s[m]; scale and bias may
+ * be NULL.  Then `residual` (same layout as y) is added, TBN_EPI_RELU, and
+ * TBN_EPI_MAXPOOL2X2 (floor mode; needs TBN_EPI_RELU and no residual).
+ * C*kh*kw <= 2^24.  No workspace, no allocation: capturable. */
+int tbn_hip_conv2d_tbn_prepacked(const float* x, const tbn_conv2d_desc* desc, const uint8_t* w4,
+                                 const float* scale, float alpha, const float* bias, const float* residual,
+                                 int flags, float lo, float hi, float* y, tbn_stream_t stream);
+/* No counterpart in the reference (a diagnostic for profiling): the kernel
+ * and tile tbn_hip_conv2d_tbn_prepacked runs for desc and flags.  No GPU
+ * work. */
+int tbn_hip_conv2d_tbn_kernel_name(const tbn_conv2d_desc* desc, int flags, char* name, size_t len);
+
 #ifdef __cplusplus
 }
 #endif

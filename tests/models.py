@@ -227,10 +227,21 @@ def gemm_already_binary(B):
     return all(float(v) in ok for v in flat[::step])
 
 
-def run_oracle(spec, feeds, quant, orc, record=None):
+def run_oracle(spec, feeds, quant, orc, record=None, arithmetic="f32", overrides=None):
     """Executes the graph on the CPU (float64 products, fp32 values between
     nodes) with the reference Session's branch structure.  Returns
-    {output name: array}; `record`, if a dict, receives every value."""
+    {output name: array}; `record`, if a dict, receives every value.
+
+    arithmetic="tbn": the quantized layers in the reference's own arithmetic
+    (model.hpp:414-564,763-870; conv2d.cpp:195-316), bit for bit: ternarized
+    activations, exact integer products, float(C) and the bias / scale /
+    alpha / beta steps in float32 (tests/tbn_ref.py), and residual Adds in
+    float32.  `overrides` maps value names to arrays used instead of
+    computing the nodes that produce them (to continue from a device value)."""
+    import tbn_ref
+
+    tbn = arithmetic == "tbn"
+    overrides = overrides or {}
     env = {k: np.asarray(v) for k, v in spec.inits.items()}
     env.update({k: np.asarray(v, np.float32) for k, v in feeds.items()})
     orc_base = orc
@@ -238,6 +249,48 @@ def run_oracle(spec, feeds, quant, orc, record=None):
         orc = orc_base
         a = n.attrs
         quant_here = quant and a.get("tbn_quantize", 1) != 0
+        if n.outputs[0] in overrides:
+            env[n.outputs[0]] = np.asarray(overrides[n.outputs[0]], np.float32)
+            continue
+        if tbn and n.op == "Conv" and int(a.get("group", 1)) == 1:
+            dt = spec.init_dtypes.get(n.inputs[1], "float32")
+            if dt in ("binary", "ternary") or quant_here:
+                x, W = env[n.inputs[0]], env[n.inputs[1]]
+                b = env[n.inputs[2]].astype(np.float32) if len(n.inputs) > 2 else None
+                stride, pad, dil = _conv_attrs(a)
+                scale = None
+                if dt == "binary":
+                    sign = np.where(W == 1, 1, -1)
+                elif dt == "ternary":
+                    sign = np.where(W < 0, -1, 1)  # conv2d_ternary (conv2d.cpp:195-217)
+                else:
+                    s = orc.channel_mean_abs(W)
+                    already = orc.already_binary(W, s)
+                    sign = np.where(W >= 0 if already else W > 0, 1, -1)
+                    scale = s if already else None
+                C = tbn_ref.tbn_conv_int(orc, x, sign, stride, pad, dil)
+                y = C.astype(np.float32)
+                if b is not None:
+                    y = y + b[None, :, None, None]
+                if scale is not None:
+                    y = y * np.asarray(scale, np.float32)[None, :, None, None]
+                env[n.outputs[0]] = y.astype(np.float32)
+                continue
+        if tbn and n.op == "Gemm" and quant_here:
+            A, B = env[n.inputs[0]], env[n.inputs[1]]
+            if B.dtype == np.float32 and not a.get("transA", 0) and not a.get("transB", 0):
+                already = gemm_already_binary(B)
+                sign = np.where(B >= 0 if already else B > 0, 1, -1)
+                C = env[n.inputs[2]] if len(n.inputs) > 2 else None
+                env[n.outputs[0]] = tbn_ref.tbn_gemm_session(orc, A, sign, a.get("alpha", 1.0), C,
+                                                             a.get("beta", 1.0))
+                continue
+        if tbn and n.op == "Add":
+            xa, xb = env[n.inputs[0]].astype(np.float32), env[n.inputs[1]].astype(np.float32)
+            if xa.ndim == 4 and xb.ndim in (1, 3):
+                xb = xb.reshape(1, -1, 1, 1)
+            env[n.outputs[0]] = (xa + xb).astype(np.float32)
+            continue
         if n.op == "Conv":
             x = env[n.inputs[0]]
             wname = n.inputs[1]
