@@ -166,11 +166,32 @@ def conv_cfg4(torch, tbn_hip, seed):
     return step, step_reference_layout, (x, packed, conv_w, scale, bias, y, desc)
 
 
-def session_workload(torch, _tbn, which, stream, replay):
+def conv_cfg4_tbn(torch, tbn_hip, keep):
+    """Config 4's layer in TBN arithmetic (the reference's own quantized
+    conv: taps ternarized at +-0.1, integer products, float(C) * s + b, ReLU)
+    on the same inputs and weights, the weights in the TBN conv layout."""
+    x, packed, _, scale, bias, y, desc = keep
+    K_pad, N_pad = tbn_hip.padded_dims(576, 128)
+    nbytes = ctypes.c_int64()
+    tbn_hip.call("tbn_hip_tbn_conv_weights_bytes", desc, ctypes.byref(nbytes))
+    w4 = torch.empty(nbytes.value, dtype=torch.uint8, device=x.device)
+    tbn_hip.call("tbn_hip_pack_tbn_conv_weights", packed.data_ptr(), K_pad, N_pad, desc, w4.data_ptr(), None)
+    tbn_hip.call("tbn_hip_tbn_conv_scratch_bytes", desc, ctypes.byref(nbytes))
+    scratch = torch.empty(nbytes.value, dtype=torch.uint8, device=x.device)
+    torch.cuda.synchronize()
+
+    def step(sh):
+        tbn_hip.call("tbn_hip_conv2d_tbn_prepacked", x.data_ptr(), desc, w4.data_ptr(), scale.data_ptr(), 1.0,
+                     bias.data_ptr(), None, tbn_hip.EPI_RELU, -0.1, 0.1, scratch.data_ptr(), y.data_ptr(), sh)
+    return step, (w4, scratch)
+
+
+def session_workload(torch, _tbn, which, stream, replay, arithmetic="f32"):
     """Config 1 (LeNet, batch 1) or config 5 (ResNet-18, batch 32) through
     TBNModel::Session with quantization on, eager or replaying the Session's
     HIP graph of the forward (the same kernels, launched without the host);
-    the input is already in HBM, the output stays there."""
+    the input is already in HBM, the output stays there.  arithmetic "tbn":
+    the reference's own quantized arithmetic (QuantArithmetic::TBN)."""
     sys.path.insert(0, str(ROOT / "tests"))
     import models
     if which == "lenet":
@@ -180,6 +201,7 @@ def session_workload(torch, _tbn, which, stream, replay):
     model = _tbn.TBNModel(models.build_graph(spec, _tbn))
     sess = model.create_session()
     sess.set_quantization(True)
+    sess.set_quant_arithmetic(arithmetic)
     xd = torch.from_numpy(x).cuda()
     torch.cuda.synchronize()
     _tbn.set_current_stream(stream.cuda_stream)
@@ -271,7 +293,8 @@ def main():
     ap.add_argument("--prewarm", type=float, default=0.3,
                     help="seconds of untimed headline launches before its warmup steps (GPU clock ramp); "
                          "the other lines prewarm for a third of it")
-    ap.add_argument("--only", choices=["gemm", "conv", "ternary", "tbn", "gemm1024", "lenet", "resnet", "groups"],
+    ap.add_argument("--only", choices=["gemm", "conv", "conv_tbn", "ternary", "tbn", "gemm1024", "lenet", "resnet",
+                                       "lenet_tbn", "resnet_tbn", "groups"],
                     help="run one workload only (for profiling)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 device copies of 1 GiB (known bytes) for counter calibration")
@@ -311,8 +334,26 @@ def main():
         ms = timed(step, warm=False)
         log(f"gemm 4096^3 float x binary: {ms * 1e3:.1f} us/launch, {2.0 * M * N * K / ms / 1e9:.1f} TFLOP/s-eq")
         del keep
-    if want("conv"):
+    if want("conv") or want("conv_tbn"):
         step, step_ref, keep = conv_cfg4(torch, tbn_hip, seed=2)
+    if want("conv_tbn"):
+        tstep, w4 = conv_cfg4_tbn(torch, tbn_hip, keep)
+        with torch.cuda.stream(stream):
+            prewarm(lambda: tstep(sh), args.prewarm / 3, torch)
+        tc_ms = time_graph(tstep, args.steps, args.warmup, torch)
+        kname = ctypes.create_string_buffer(160)
+        tbn_hip.call("tbn_hip_conv2d_tbn_kernel_name", keep[-1], tbn_hip.EPI_RELU, kname, len(kname))
+        # HBM-bound: the fp32 input read once, the fp4 weights, the fp32 output
+        tc_bytes = 4.0 * 64 * 64 * 196 + w4[0].numel() + 8.0 * 128 + 4.0 * 64 * 128 * 196
+        extra["conv_tbn_us_per_batch"] = round(tc_ms * 1e3, 2)
+        extra["roofline_conv_tbn"] = {
+            "bound": "hbm", "achieved": round(tc_bytes / (tc_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(tc_bytes / (tc_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": kname.value.decode(), "algorithmic_bytes": int(tc_bytes),
+            "gops_equiv": round(2.0 * 64 * 196 * 576 * 128 / (tc_ms * 1e-3) / 1e9, 1)}
+        log(f"conv cfg4 batch 64, TBN arithmetic: {tc_ms * 1e3:.2f} us/batch ({kname.value.decode()})")
+        del w4
+    if want("conv"):
         with torch.cuda.stream(stream):
             prewarm(lambda: step(sh), args.prewarm / 3, torch)
         conv_ms = time_graph(step, args.steps, args.warmup, torch)
@@ -329,6 +370,7 @@ def main():
         extra["conv_reference_layout_us_per_batch"] = round(ref_ms * 1e3, 2)
         log(f"conv cfg4 batch 64: {conv_ms * 1e3:.1f} us/batch pre-packed, {ref_ms * 1e3:.1f} us with the "
             f"per-call weight re-order of the reference-layout entry point")
+    if want("conv") or want("conv_tbn"):
         del keep
     if want("ternary"):
         step, keep, _, _ = packed_gemm(torch, tbn_hip, 256, 4096, 4096, seed=3, ternary=True)
@@ -395,17 +437,19 @@ def main():
             extra[name + "_32x128x56x56_GBps"] = round(nbytes / (t_ms * 1e-3) / 1e9, 1)
             log(f"{name} 32x128x56x56: {t_ms * 1e3:.1f} us, {nbytes / (t_ms * 1e-3) / 1e9:.0f} GB/s")
         del x, y, w, kk, tt
-    for which, key, replay in (("lenet", "lenet_session_us_per_forward", False),
-                               ("lenet", "lenet_session_replay_us_per_forward", True),
-                               ("resnet", "resnet18_session_ms_per_batch32", False)):
-        if not want(which):
+    for which, key, replay, arith in (("lenet", "lenet_session_us_per_forward", False, "f32"),
+                                      ("lenet", "lenet_session_replay_us_per_forward", True, "f32"),
+                                      ("resnet", "resnet18_session_ms_per_batch32", False, "f32"),
+                                      ("lenet", "lenet_tbn_session_replay_us_per_forward", True, "tbn"),
+                                      ("resnet", "resnet18_tbn_session_ms_per_batch32", False, "tbn")):
+        if not want(which if arith == "f32" else which + "_tbn"):
             continue
-        step, keep = session_workload(torch, _tbn, which, stream, replay)
+        step, keep = session_workload(torch, _tbn, which, stream, replay, arith)
         s_ms = timed(step)
         extra[key] = round(s_ms * (1e3 if which == "lenet" else 1.0), 3)
-        extra[which + "_session_launches"] = keep[1].planned_launches()
-        log(f"{which} session ({'graph replay' if replay else 'eager'}): {s_ms * 1e3:.1f} us per forward "
-            f"({keep[1].planned_launches()} launches)")
+        extra[which + ("_tbn" if arith == "tbn" else "") + "_session_launches"] = keep[1].planned_launches()
+        log(f"{which} session ({arith}, {'graph replay' if replay else 'eager'}): {s_ms * 1e3:.1f} us per "
+            f"forward ({keep[1].planned_launches()} launches)")
         _tbn.set_current_stream(0)
         del keep
 

@@ -104,11 +104,11 @@ void release_workspace(void* ptr, bool temporary, hipStream_t s) {
 }
 
 // Tuning controls: read from the environment once (TBN_CONV_TILE,
-// TBN_CONV_SPLITS, TBN_GEMM_SPLITS), then changed only through
+// TBN_CONV_SPLITS, TBN_GEMM_SPLITS, TBN_GEMM_TILE, TBN_TBN_CONV), then changed only through
 // tbn_hip_set_tuning.  Relaxed atomics: a value is a launch-shape choice, so a
 // call that races with a change simply sees the old or the new one.
 namespace {
-std::atomic<int> g_tuning[5];
+std::atomic<int> g_tuning[6];
 std::once_flag g_tuning_once;
 
 void tuning_init() {
@@ -120,6 +120,7 @@ void tuning_init() {
     g_tuning[TBN_TUNE_CONV_SPLITS].store(std::max(0, env("TBN_CONV_SPLITS", 0)), std::memory_order_relaxed);
     g_tuning[TBN_TUNE_GEMM_SPLITS].store(std::max(0, env("TBN_GEMM_SPLITS", 0)), std::memory_order_relaxed);
     g_tuning[TBN_TUNE_GEMM_TILE].store(env("TBN_GEMM_TILE", -1), std::memory_order_relaxed);
+    g_tuning[TBN_TUNE_TBN_CONV].store(std::max(0, std::min(2, env("TBN_TBN_CONV", 0))), std::memory_order_relaxed);
 }
 }  // namespace
 
@@ -181,10 +182,13 @@ int tbn_hip_device_check(void) {
 }
 
 int tbn_hip_set_tuning(int option, int value) {
-    TBN_REQUIRE(option >= TBN_TUNE_CONV_TILE && option <= TBN_TUNE_GEMM_TILE, TBN_INVALID_ARGUMENT,
+    TBN_REQUIRE(option >= TBN_TUNE_CONV_TILE && option <= TBN_TUNE_TBN_CONV, TBN_INVALID_ARGUMENT,
                 "unknown tuning option");
-    TBN_REQUIRE(option == TBN_TUNE_CONV_TILE ? value >= -1
-                                             : (option == TBN_TUNE_GEMM_TILE ? value >= -1 && value <= 2 : value >= 0),
+    TBN_REQUIRE(option == TBN_TUNE_CONV_TILE
+                    ? value >= -1
+                    : (option == TBN_TUNE_GEMM_TILE ? value >= -1 && value <= 2
+                                                    : (option == TBN_TUNE_TBN_CONV ? value >= 0 && value <= 2
+                                                                                   : value >= 0)),
                 TBN_INVALID_ARGUMENT, "tuning value out of range");
     (void)tbn_hip::tuning(option);  // the environment is read before the first change
     tbn_hip::g_tuning[option].store(value, std::memory_order_relaxed);
@@ -192,7 +196,7 @@ int tbn_hip_set_tuning(int option, int value) {
 }
 
 int tbn_hip_get_tuning(int option, int* value) {
-    TBN_REQUIRE(option >= TBN_TUNE_CONV_TILE && option <= TBN_TUNE_GEMM_TILE, TBN_INVALID_ARGUMENT,
+    TBN_REQUIRE(option >= TBN_TUNE_CONV_TILE && option <= TBN_TUNE_TBN_CONV, TBN_INVALID_ARGUMENT,
                 "unknown tuning option");
     TBN_REQUIRE(value != nullptr, TBN_INVALID_ARGUMENT, "null pointer");
     *value = tbn_hip::tuning(option);

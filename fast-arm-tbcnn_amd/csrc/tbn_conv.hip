@@ -8,17 +8,25 @@
 // + b[m] or (float(C) + b[m]) * alpha*s[m], then residual, ReLU, 2x2 max
 // pool as the following nodes compute them.
 //
-// Implicit GEMM on the fp4 matrix cores: no im2col matrix and no bit planes
-// are materialised.  A block owns one tile of TR x TC output pixels of one
-// image and WV fragments of 32 output channels (one wave each).  K runs over
-// chunks of 64 input channels; for each chunk the block stages the input
-// patch the tile needs straight from NCHW fp32 into LDS, ternarized on the
-// way into fp4 pixel records (64 codes, 32 bytes each), and every tap of the
-// kernel is then one MFMA k-step (32 x 32 x 64) read from the same records.
-// The weights are pre-packed once per layer in MFMA fragment order (1 KB per
-// fragment and k-step, one 16-byte load per lane) and read from L2.
-// MFMA rows are output channels and columns pixels, so a fragment's 32
-// lanes store 32 consecutive pixels of a channel plane.
+// No im2col matrix and no bit planes.  The fused kernel (tbn_conv_fused_
+// kernel) stages each block's input patch from NCHW fp32 into LDS as fp4
+// records, ternarized on the way, and runs every tap from them; it takes
+// every geometry whose patch fits a tile of at most 8 staged items per
+// thread.  The others (and TBN_TUNE_TBN_CONV = 2) run two passes:
+//   1. tbn_records_kernel streams the fp32 NCHW input once from HBM and
+//      writes it ternarized as fp4 pixel records: for each image, chunk of
+//      64 input channels and pixel, 32 bytes (two E2M1 codes a byte), laid
+//      out [n][chunk][ih][iw] -- an eighth of the input's bytes.
+//   2. tbn_conv_kernel is an implicit GEMM on the fp4 matrix cores
+//      (v_mfma_scale_f32_32x32x64_f8f6f4): MFMA rows are output channels,
+//      columns output pixels (32 consecutive ones per fragment, so a
+//      fragment's lanes store contiguous runs of a channel plane), and each
+//      k-step is one tap of one chunk.  Every wave works alone (no LDS, no
+//      barrier): it loads its weight fragments (pre-packed once per layer in
+//      fragment order, 1 KB per k-step) and its pixels' records for a group
+//      of k-steps with all loads in flight, straight from L2, then runs the
+//      group's MFMAs; taps outside the image read zero through the buffer
+//      range check.
 #include <algorithm>
 #include <cstdio>
 #include <string>
@@ -31,9 +39,8 @@ namespace {
 using namespace tbnk;
 
 constexpr int kChunk = 64;             // input channels per k-step
-constexpr int kRec = 32;               // LDS bytes per pixel record: 64 fp4 codes
+constexpr int kRec = 32;               // bytes of a pixel's chunk record: 64 fp4 codes
 constexpr uint32_t kOutside = 0x80000000u;
-constexpr int kMaxLds = 64 * 1024;     // patch bytes a block may stage
 
 struct TbnGeom {
     int N, C, H, W, M, kh, kw, sh, sw, ph, pw, dh, dw;
@@ -41,14 +48,21 @@ struct TbnGeom {
     int pool;              // fused 2x2 / 2 max pool (floor mode)
     int YH, YW;            // stored output plane
     int chunks, taps, ksteps, mfrags;
-    int TR, TC;            // conv output rows / columns per tile (both even when pooled)
-    int tiles_r, tiles_c;  // tiles per image
-    int PR, PC;            // patch rows / columns (input pixels)
-    int FC;                // pixel fragments (32 pixels) per tile
-    int WV;                // waves per block, one 32-channel fragment each
-    int mblocks;           // channel blocks
-    int64_t blocks() const { return static_cast<int64_t>(N) * tiles_r * tiles_c * mblocks; }
-    int lds() const { return PR * PC * kRec; }
+    int64_t pixels;        // computed output pixels: N*OH*OW, or N*YH*YW*4 by window when pooled
+    int64_t pfrags;        // pixel fragments of 32
+    int FCW;               // pixel fragments per wave
+    int G;                 // k-steps per load group
+    // the fused kernel: one tile of TR x TC output pixels of one image per
+    // block, WV 32-channel fragments (one wave each), FC pixel fragments
+    int fused;
+    int TR, TC, tiles_r, tiles_c, PR, PC, FC, WV, mblocks, IPT, GF;
+    FastDiv div_npix, div_pc;  // staging items -> (channel group, patch pixel) -> (row, column)
+    __host__ __device__ int64_t fused_blocks() const {
+        return static_cast<int64_t>(N) * tiles_r * tiles_c * mblocks;
+    }
+    __host__ __device__ int64_t groups() const { return (pfrags + FCW - 1) / FCW; }
+    __host__ __device__ int64_t waves() const { return static_cast<int64_t>(mfrags) * groups(); }
+    __host__ __device__ int64_t record_bytes() const { return static_cast<int64_t>(N) * chunks * H * W * kRec; }
 };
 
 struct TbnConvArgs {
@@ -63,6 +77,11 @@ struct TbnConvArgs {
     float lo, hi;
 };
 
+// Stand-ins for an absent scale (1) or bias (0), so the epilogue's loads
+// are unconditional and all in flight together.
+__device__ const float kUnitScale[1] = {1.0f};
+__device__ const float kNoBias[1] = {0.0f};
+
 // v from lane (lane & ~3) | perm[lane & 3] of the same quad (DPP quad_perm).
 template <int CTRL>
 __device__ __forceinline__ float quad_perm(float v) {
@@ -73,16 +92,208 @@ __device__ __forceinline__ float quad_perm(float v) {
 // multiply-add), in the reference's order: float(C) * s + b (conv2d_binary
 // and its scaled variants) or (float(C) + b) * s (the Session's cached conv),
 // then + the residual (the following Add node).
-__device__ __forceinline__ float epilogue_value(float acc, float mult, float bb, bool bts, const float* res) {
+__device__ __forceinline__ float epilogue_value(float acc, float mult, float bb, bool bts, bool add, float res) {
 #pragma clang fp contract(off)
     float v = bts ? (acc + bb) * mult : acc * mult + bb;
-    if (res) v = v + *res;
+    if (add) v = v + res;
     return v;
 }
 
-// Tile pixel p (0 .. 32 FC) -> conv output offsets (r, c) inside the tile:
-// row-major, or by 2 x 2 window when pooled (p / 4 a window, p % 4 its
-// position: bit 0 the column, bit 1 the row).
+// Output pixel p -> (n, oh, ow): row-major over [N, OH, OW], or by 2 x 2
+// window when pooled (p / 4 a window of the pooled plane, p % 4 its
+// position: bit 0 the column, bit 1 the row).  p < 2^31 (host-checked).
+__device__ __forceinline__ void pixel_coords(const TbnGeom& g, int p, int& n, int& oh, int& ow) {
+    if (g.pool) {
+        const int q = p >> 2;
+        const int plane = g.YH * g.YW;
+        n = q / plane;
+        const int rem = q - n * plane;
+        const int py = rem / g.YW;
+        oh = 2 * py + ((p >> 1) & 1);
+        ow = 2 * (rem - py * g.YW) + (p & 1);
+    } else {
+        const int plane = g.OH * g.OW;
+        n = p / plane;
+        const int rem = p - n * plane;
+        oh = rem / g.OW;
+        ow = rem - oh * g.OW;
+    }
+}
+
+// Pass 1: item i = (image n, chunk, input pixel, group of 8 channels), the
+// group fastest, so 8 consecutive lanes write one pixel's 32-byte record and
+// a wave 8 whole records; each load reads, across the wave, runs of 8 pixels
+// (32 bytes) of 8 channel planes.
+__global__ void __launch_bounds__(256) tbn_records_kernel(const float* __restrict__ x, TbnGeom g, float lo, float hi,
+                                                          uint32_t* __restrict__ xt) {
+    const int HW = g.H * g.W;
+    const int64_t total = static_cast<int64_t>(g.N) * g.chunks * HW * 8;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        const int cg = static_cast<int>(i & 7);
+        const int64_t rec = i >> 3;
+        const int64_t nc = rec / HW;
+        const int pix = static_cast<int>(rec - nc * HW);
+        const int chunk = static_cast<int>(nc % g.chunks);
+        const int64_t n = nc / g.chunks;
+        const int c0 = chunk * kChunk + 8 * cg;
+        const float* src = x + (n * g.C + c0) * HW + pix;
+        float v[8];
+        if (c0 + 8 <= g.C) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = __builtin_nontemporal_load(src + e * HW);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = c0 + e < g.C ? src[e * HW] : 0.0f;
+        }
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) w |= ternary_f4(v[e], lo, hi) << (4 * e);
+        xt[i] = w;
+    }
+}
+
+// Pass 2.  Wave wv owns channel fragment wv % mfrags and pixel fragments
+// [FCW * (wv / mfrags), +FCW): the waves of one block share their pixels'
+// records through the CU's caches.
+template <int FCW, int G>
+__global__ void __launch_bounds__(256) tbn_conv_kernel(TbnGeom g, TbnConvArgs a, const uint8_t* __restrict__ xt) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wv = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+    if (wv >= g.waves()) return;  // whole waves; the kernel has no barrier
+    const int mf = static_cast<int>(wv % g.mfrags);
+    const int pg = static_cast<int>(wv / g.mfrags);
+    const int h = lane >> 5;
+
+    // per lane and fragment: the pixel, the patch origin (ih0, iw0) and the
+    // byte offset of the record of (n, chunk 0, ih0, iw0); a tap adds a
+    // wave-uniform offset, and its validity is two unsigned compares
+    int n_[FCW], oh_[FCW], ow_[FCW], ih0[FCW], iw0[FCW], base[FCW];
+    bool ok[FCW];
+#pragma unroll
+    for (int j = 0; j < FCW; ++j) {
+        const int p = (pg * FCW + j) * 32 + (lane & 31);
+        ok[j] = p < g.pixels;
+        pixel_coords(g, ok[j] ? p : 0, n_[j], oh_[j], ow_[j]);
+        iw0[j] = ow_[j] * g.sw - g.pw;
+        ih0[j] = oh_[j] * g.sh - g.ph;
+        base[j] = ((n_[j] * g.chunks * g.H + ih0[j]) * g.W + iw0[j]) * kRec + 16 * h;
+        if (!ok[j]) ih0[j] = -(1 << 30);  // a pixel past the end reads no tap
+    }
+    // records: host-checked below 2^31 bytes, so a 32-bit offset reaches
+    // every one and kOutside none
+    const __amdgpu_buffer_rsrc_t xt_rs = buffer_range(xt, static_cast<uint64_t>(g.record_bytes()), 0);
+
+    f32x16_t acc[FCW];
+#pragma unroll
+    for (int j = 0; j < FCW; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
+
+    // the epilogue's per-channel scale and bias, loaded with the first group
+    const int h4 = mf * 32 + 4 * h;
+    const float* sp = a.scale ? a.scale : kUnitScale;
+    const float* bp = a.bias ? a.bias : kNoBias;
+    const int smask = a.scale ? -1 : 0, bmask = a.bias ? -1 : 0;
+    float mults[16], biases[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int mc = min(h4 + 8 * (e >> 2) + (e & 3), g.M - 1);
+        mults[e] = sp[mc & smask];  // times alpha below: alpha * 1 = alpha exactly
+        biases[e] = bp[mc & bmask];
+    }
+
+    const i32x4_t* wp = reinterpret_cast<const i32x4_t*>(a.w4) + static_cast<int64_t>(mf) * g.ksteps * 64 + lane;
+    const int chunk_bytes = g.H * g.W * kRec;
+    // (chunk, r, s) of k-step ks0 + u, advanced by counters (no division)
+    int c_ = 0, r_ = 0, s_ = 0;
+    for (int ks0 = 0; ks0 < g.ksteps; ks0 += G) {
+        i32x4_t wr[G];
+        i32x4_t ar[G][FCW];
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            // k-steps past the end repeat the last one with zero activations
+            const int ks = min(ks0 + u, g.ksteps - 1);
+            const bool live = ks0 + u < g.ksteps;
+            wr[u] = wp[ks * 64];
+            const int dy = r_ * g.dh, dx = s_ * g.dw;
+            const int toff = c_ * chunk_bytes + (dy * g.W + dx) * kRec;
+            if (live) {
+                if (++s_ == g.kw) {
+                    s_ = 0;
+                    if (++r_ == g.kh) r_ = 0, ++c_;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < FCW; ++j) {
+                const bool in = live && static_cast<unsigned>(ih0[j] + dy) < static_cast<unsigned>(g.H) &&
+                                static_cast<unsigned>(iw0[j] + dx) < static_cast<unsigned>(g.W);
+                const uint32_t off = in ? static_cast<uint32_t>(base[j] + toff) : kOutside;
+                ar[u][j] = __builtin_bit_cast(i32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xt_rs, off, 0, 0));
+            }
+        }
+        // every load of the group in flight before the first MFMA waits
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < G; ++u)
+#pragma unroll
+            for (int j = 0; j < FCW; ++j) acc[j] = mfma_f4(wr[u], ar[u][j], acc[j]);
+    }
+
+    // epilogue: acc is the exact integer C; rows of register e: 8 (e / 4) +
+    // 4 h + e % 4 of the fragment
+    const bool bts = (a.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
+    const bool relu = (a.flags & TBN_EPI_RELU) != 0;
+    const int64_t plane = static_cast<int64_t>(g.YH) * g.YW;
+    // element (channel mf*32 + 4 h, this lane's pixel) of y (and residual);
+    // register e adds (8 (e / 4) + e % 4) planes
+    int64_t obase[FCW];
+#pragma unroll
+    for (int j = 0; j < FCW; ++j) {
+        const int oy = g.pool ? oh_[j] >> 1 : oh_[j], ox = g.pool ? ow_[j] >> 1 : ow_[j];
+        obase[j] = (static_cast<int64_t>(n_[j]) * g.M + mf * 32 + 4 * h) * plane + static_cast<int64_t>(oy) * g.YW + ox;
+    }
+    // the residual addends, all loads in flight together (lanes that store
+    // nothing read element 0)
+    const bool add = a.residual != nullptr;
+    float res[FCW][16];
+    if (add) {
+#pragma unroll
+        for (int j = 0; j < FCW; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = 8 * (e >> 2) + (e & 3);
+                const bool st = ok[j] && mf * 32 + 4 * h + row < g.M;
+                res[j][e] = a.residual[st ? obase[j] + row * plane : 0];
+            }
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int row = 8 * (e >> 2) + (e & 3);
+        const int m = mf * 32 + 4 * h + row;
+        const float mult = a.alpha * mults[e], bb = biases[e];
+#pragma unroll
+        for (int j = 0; j < FCW; ++j) {
+            const int64_t idx = obase[j] + row * plane;
+            if (g.pool) {
+                float v = epilogue_value(acc[j][e], mult, bb, bts, false, 0.0f);
+                if (relu) v = v > 0.0f ? v : 0.0f;
+                // the window's four values sit in lanes 4q .. 4q + 3 (after ReLU
+                // every value is +0 or more and none is NaN: order-free maximum)
+                v = fmaxf(v, quad_perm<0xB1>(v));
+                v = fmaxf(v, quad_perm<0x4E>(v));
+                if (m < g.M && ok[j] && (lane & 3) == 0) a.y[idx] = v;
+            } else if (m < g.M && ok[j]) {
+                float v = epilogue_value(acc[j][e], mult, bb, bts, add, add ? res[j][e] : 0.0f);
+                if (relu) v = v > 0.0f ? v : 0.0f;
+                a.y[idx] = v;
+            }
+        }
+    }
+}
+
+// Tile pixel p -> conv output offsets (r, c) inside a TR x TC tile:
+// row-major, or by 2 x 2 window when pooled.
 __device__ __forceinline__ void tile_pixel(const TbnGeom& g, int p, int& r, int& c) {
     if (g.pool) {
         const int q = p >> 2, qc = g.TC >> 1;
@@ -95,18 +306,25 @@ __device__ __forceinline__ void tile_pixel(const TbnGeom& g, int p, int& r, int&
     }
 }
 
-template <int FC>
-__global__ void __launch_bounds__(256) tbn_conv_kernel(TbnGeom g, TbnConvArgs a) {
+// The fused kernel: no record pass.  A block stages, per chunk of 64 input
+// channels, the input patch of its tile (PR x PC pixels) from NCHW fp32
+// straight into LDS as fp4 records, ternarized on the way: each thread issues
+// its IPT items' loads (8 channels of one patch pixel each) before any
+// arrives, together with its wave's weight fragments for the chunk's first
+// GF taps and (once) the epilogue's scale and bias.  Every tap is then one
+// MFMA k-step read from the same records.
+template <int FC, int IPT, int GF>
+__global__ void __launch_bounds__(256) tbn_conv_fused_kernel(TbnGeom g, TbnConvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x;
-    const int nt = blockDim.x;
+    const int nt = 64 * g.WV;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int h = lane >> 5;
 
-    // block -> (image, tile, channel block); the channel blocks of one tile
-    // are consecutive in b, and consecutive b run on one XCD (blocks are
-    // dealt round-robin over the 8 XCDs), so a patch is fetched into one L2
+    // block -> (image, tile, channel block); the channel blocks of a tile are
+    // consecutive in b, and consecutive b share an XCD (blocks are dealt
+    // round-robin over the 8 XCDs), so a patch is fetched into one L2
     int b = blockIdx.x;
     const int total = gridDim.x;
     if (total % 8 == 0) b = (b % 8) * (total / 8) + b / 8;
@@ -120,12 +338,25 @@ __global__ void __launch_bounds__(256) tbn_conv_kernel(TbnGeom g, TbnConvArgs a)
     const int ih0 = oh0 * g.sh - g.ph, iw0 = ow0 * g.sw - g.pw;
     const int mf = mb * g.WV + wave;
     const bool active = mf < g.mfrags;
+    const int mfc = active ? mf : 0;
 
-    // this lane's pixel in each fragment: its record in the patch (tap 0)
+    // the epilogue's per-channel scale and bias, in flight from the start
+    const int h4 = mfc * 32 + 4 * h;
+    const float* sp = a.scale ? a.scale : kUnitScale;
+    const float* bp = a.bias ? a.bias : kNoBias;
+    const int smask = a.scale ? -1 : 0, bmask = a.bias ? -1 : 0;
+    float mults[16], biases[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int mc = min(h4 + 8 * (e >> 2) + (e & 3), g.M - 1);
+        mults[e] = sp[mc & smask];
+        biases[e] = bp[mc & bmask];
+    }
+
+    // this lane's pixel in each fragment and its record in the patch (tap 0)
     const int oh_lim = g.pool ? 2 * g.YH : g.OH, ow_lim = g.pool ? 2 * g.YW : g.OW;
-    int rec[FC];
+    int rec[FC], pr_[FC], pc_[FC];
     bool ok[FC];
-    int pr_[FC], pc_[FC];
 #pragma unroll
     for (int j = 0; j < FC; ++j) {
         int r, c;
@@ -136,44 +367,12 @@ __global__ void __launch_bounds__(256) tbn_conv_kernel(TbnGeom g, TbnConvArgs a)
         rec[j] = ok[j] ? (r * g.sh * g.PC + c * g.sw) * kRec + 16 * h : 16 * h;
     }
 
-    // staging: item i = (channel group cg of 8, patch pixel), pixels fastest
-    // so a load instruction reads consecutive pixels of one channel row
     const int npix = g.PR * g.PC;
     const int items = npix * 8;
     const uint32_t HW4 = static_cast<uint32_t>(g.H * g.W) * 4;
     const __amdgpu_buffer_rsrc_t x_rs =
         buffer_range(a.x + static_cast<int64_t>(n) * g.C * g.H * g.W, static_cast<uint64_t>(g.C) * HW4, 0);
-    auto stage = [&](int chunk) {
-        for (int i0 = tid; i0 < items; i0 += 4 * nt) {
-            float v[4][8];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int i = i0 + u * nt;
-                const int cg = i / npix, pix = i - (i / npix) * npix;
-                const int pr = pix / g.PC, pc = pix - (pix / g.PC) * g.PC;
-                const int ih = ih0 + pr, iw = iw0 + pc;
-                const bool in = i < items && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
-                                static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
-                // channels past C fall beyond the resource and read zero
-                const uint32_t o =
-                    in ? (static_cast<uint32_t>(chunk * kChunk + cg * 8) * g.H * g.W + ih * g.W + iw) * 4 : kOutside;
-#pragma unroll
-                for (int e = 0; e < 8; ++e)
-                    v[u][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x_rs, o + e * HW4, 0, 0));
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int i = i0 + u * nt;
-                if (i < items) {
-                    const int cg = i / npix, pix = i - (i / npix) * npix;
-                    uint32_t w = 0;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) w |= ternary_f4(v[u][e], a.lo, a.hi) << (4 * e);
-                    *reinterpret_cast<uint32_t*>(lds + pix * kRec + cg * 4) = w;
-                }
-            }
-        }
-    };
+    const i32x4_t* wp = reinterpret_cast<const i32x4_t*>(a.w4) + static_cast<int64_t>(mfc) * g.ksteps * 64 + lane;
 
     f32x16_t acc[FC];
 #pragma unroll
@@ -181,61 +380,115 @@ __global__ void __launch_bounds__(256) tbn_conv_kernel(TbnGeom g, TbnConvArgs a)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
 
-    // this wave's weight fragments: [mf][k-step][lane] x 16 bytes
-    const i32x4_t* wp = reinterpret_cast<const i32x4_t*>(a.w4) +
-                        (static_cast<int64_t>(active ? mf : 0) * g.ksteps) * 64 + lane;
-    i32x4_t wcur = active ? wp[0] : i32x4_t{0, 0, 0, 0};
     for (int chunk = 0; chunk < g.chunks; ++chunk) {
-        if (chunk) __syncthreads();  // every wave is done with the previous chunk's records
-        stage(chunk);
+        // the weights of the chunk's first GF taps (taps past the end: zero)
+        i32x4_t wr[GF];
+#pragma unroll
+        for (int u = 0; u < GF; ++u) {
+            const bool live = active && u < g.taps;
+            wr[u] = live ? wp[(chunk * g.taps + u) * 64] : i32x4_t{0, 0, 0, 0};
+        }
+        // the patch: item i = (channel group cg, patch pixel), pixels fastest
+        // so one load reads consecutive pixels of a channel row; channels
+        // past C fall beyond the resource and read zero
+        float v[IPT][8];
+#pragma unroll
+        for (int k = 0; k < IPT; ++k) {
+            const int i = tid + k * nt;
+            const int cg = static_cast<int>(g.div_npix.div(i)), pix = i - cg * npix;
+            const int pr = static_cast<int>(g.div_pc.div(pix)), pc = pix - pr * g.PC;
+            const int ih = ih0 + pr, iw = iw0 + pc;
+            const bool in = i < items && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
+                            static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
+            const uint32_t o =
+                in ? (static_cast<uint32_t>(chunk * kChunk + cg * 8) * g.H * g.W + ih * g.W + iw) * 4 : kOutside;
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+                v[k][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x_rs, o + e * HW4, 0, 0));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (chunk) __syncthreads();  // every wave is done reading the previous chunk's records
+#pragma unroll
+        for (int k = 0; k < IPT; ++k) {
+            const int i = tid + k * nt;
+            if (i < items) {
+                const int cg = static_cast<int>(g.div_npix.div(i)), pix = i - cg * npix;
+                uint32_t w = 0;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) w |= ternary_f4(v[k][e], a.lo, a.hi) << (4 * e);
+                *reinterpret_cast<uint32_t*>(lds + pix * kRec + cg * 4) = w;
+            }
+        }
         __syncthreads();
         if (active) {
-            for (int tap = 0; tap < g.taps; ++tap) {
-                const int ks = chunk * g.taps + tap;
-                const i32x4_t wnext = ks + 1 < g.ksteps ? wp[(ks + 1) * 64] : wcur;
-                const int r = tap / g.kw, s = tap - (tap / g.kw) * g.kw;
-                const int toff = (r * g.dh * g.PC + s * g.dw) * kRec;
-                i32x4_t bf[FC];
+            int r_ = 0, s_ = 0;  // (r, s) of tap t0 + u, advanced by counters
+            for (int t0 = 0; t0 < g.taps; t0 += GF) {
+                if (t0) {
 #pragma unroll
-                for (int j = 0; j < FC; ++j) bf[j] = *reinterpret_cast<const i32x4_t*>(lds + rec[j] + toff);
+                    for (int u = 0; u < GF; ++u) {
+                        const bool live = t0 + u < g.taps;
+                        wr[u] = live ? wp[(chunk * g.taps + t0 + u) * 64] : i32x4_t{0, 0, 0, 0};
+                    }
+                }
 #pragma unroll
-                for (int j = 0; j < FC; ++j) acc[j] = mfma_f4(wcur, bf[j], acc[j]);
-                wcur = wnext;
+                for (int u = 0; u < GF; ++u) {
+                    const bool live = t0 + u < g.taps;
+                    const int toff = live ? (r_ * g.dh * g.PC + s_ * g.dw) * kRec : 0;
+                    if (live && ++s_ == g.kw) s_ = 0, ++r_;
+                    i32x4_t bf[FC];
+#pragma unroll
+                    for (int j = 0; j < FC; ++j) bf[j] = *reinterpret_cast<const i32x4_t*>(lds + rec[j] + toff);
+#pragma unroll
+                    for (int j = 0; j < FC; ++j) acc[j] = mfma_f4(wr[u], bf[j], acc[j]);
+                }
             }
         }
     }
     if (!active) return;
 
-    // epilogue: acc is the exact integer C; rows of register e: 8 (e / 4) +
-    // 4 h + e % 4 of the fragment
+    // epilogue: buffer stores into image n's output planes (32-bit offsets,
+    // host-checked): rows past M fall beyond the resource, lanes with no
+    // pixel to store carry kOutside, so no store is behind a branch
     const bool bts = (a.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
     const bool relu = (a.flags & TBN_EPI_RELU) != 0;
-    const int64_t plane = static_cast<int64_t>(g.YH) * g.YW;
+    const uint32_t plane4 = static_cast<uint32_t>(g.YH * g.YW) * 4;
+    const int64_t img = static_cast<int64_t>(n) * g.M * g.YH * g.YW;
+    const __amdgpu_buffer_rsrc_t y_rs = buffer_range(a.y + img, static_cast<uint64_t>(g.M) * plane4, 0);
+    uint32_t voff[FC];
+#pragma unroll
+    for (int j = 0; j < FC; ++j) {
+        const int oh = oh0 + pr_[j], ow = ow0 + pc_[j];
+        const int oy = g.pool ? oh >> 1 : oh, ox = g.pool ? ow >> 1 : ow;
+        const bool st = ok[j] && (!g.pool || (lane & 3) == 0);
+        voff[j] = st ? static_cast<uint32_t>(mf * 32 + 4 * h) * plane4 + static_cast<uint32_t>(oy * g.YW + ox) * 4
+                     : kOutside;
+    }
+    const bool add = a.residual != nullptr;
+    float res[FC][16];
+    if (add) {
+        const __amdgpu_buffer_rsrc_t r_rs = buffer_range(a.residual + img, static_cast<uint64_t>(g.M) * plane4, 0);
+#pragma unroll
+        for (int j = 0; j < FC; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                res[j][e] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(r_rs, voff[j] + (8 * (e >> 2) + (e & 3)) * plane4, 0, 0));
+    }
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-        const int m = mf * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-        const int mc = min(m, g.M - 1);
-        const float mult = a.scale ? a.alpha * a.scale[mc] : a.alpha;
-        const float bb = a.bias ? a.bias[mc] : 0.0f;
-        const int64_t cbase = (static_cast<int64_t>(n) * g.M + mc) * plane;
+        const uint32_t roff = (8 * (e >> 2) + (e & 3)) * plane4;
+        const float mult = a.alpha * mults[e], bb = biases[e];
 #pragma unroll
         for (int j = 0; j < FC; ++j) {
-            const int oh = oh0 + pr_[j], ow = ow0 + pc_[j];
+            float v = epilogue_value(acc[j][e], mult, bb, bts, add, add ? res[j][e] : 0.0f);
+            if (relu) v = v > 0.0f ? v : 0.0f;
             if (g.pool) {
-                float v = epilogue_value(acc[j][e], mult, bb, bts, nullptr);
-                if (relu) v = v > 0.0f ? v : 0.0f;
                 // the window's four values sit in lanes 4q .. 4q + 3 (after ReLU
                 // every value is +0 or more and none is NaN: order-free maximum)
                 v = fmaxf(v, quad_perm<0xB1>(v));
                 v = fmaxf(v, quad_perm<0x4E>(v));
-                if (m < g.M && ok[j] && (lane & 3) == 0)
-                    a.y[cbase + static_cast<int64_t>(oh >> 1) * g.YW + (ow >> 1)] = v;
-            } else if (m < g.M && ok[j]) {
-                const int64_t idx = cbase + static_cast<int64_t>(oh) * g.YW + ow;
-                float v = epilogue_value(acc[j][e], mult, bb, bts, a.residual ? a.residual + idx : nullptr);
-                if (relu) v = v > 0.0f ? v : 0.0f;
-                a.y[idx] = v;
             }
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rs, voff[j] + roff, 0, 0);
         }
     }
 }
@@ -282,15 +535,14 @@ int make_tbn_geom(const tbn_conv2d_desc* d, int flags, TbnGeom& g) {
     const int64_t OH = (d->h + 2 * d->ph - d->dh * (d->kh - 1) - 1) / d->sh + 1;
     const int64_t OW = (d->w + 2 * d->pw - d->dw * (d->kw - 1) - 1) / d->sw + 1;
     TBN_REQUIRE(OH > 0 && OW > 0, TBN_INVALID_SHAPE, "invalid output dimensions");
-    const int64_t K = d->c * d->kh * d->kw;
-    TBN_REQUIRE(K <= (1 << 24), TBN_INVALID_SHAPE, "TBN conv: C*kh*kw above 2^24 (fp32 sums inexact)");
-    // 32-bit buffer offsets: channel planes up to the last chunk's end and 8
-    // planes past the outside marker stay below 2^32
-    const int64_t cpad = (d->c + kChunk - 1) / kChunk * kChunk;
-    TBN_REQUIRE(d->c * d->h * d->w * 4 < (1LL << 31) && (cpad + 8) * d->h * d->w * 4 < (1LL << 32) &&
-                    d->h * d->w * 32 < (1LL << 31) && d->m < (1 << 24) &&
-                    d->n < (1LL << 31) && d->n * d->m * OH * OW < (1LL << 62),
-                TBN_INVALID_SHAPE, "TBN conv: image above 2^31 bytes");
+    TBN_REQUIRE(d->c * d->kh * d->kw <= (1 << 24), TBN_INVALID_SHAPE,
+                "TBN conv: C*kh*kw above 2^24 (fp32 sums inexact)");
+    const int64_t chunks = (d->c + kChunk - 1) / kChunk;
+    // the records of the whole input are addressed with 32-bit offsets
+    TBN_REQUIRE(d->n * chunks * d->h * d->w * kRec < (1LL << 31) && d->n * OH * OW * 4 < (1LL << 31) &&
+                    d->m < (1 << 24) &&
+                    d->n * d->m * OH * OW < (1LL << 62) && d->h < (1 << 24) && d->w < (1 << 24),
+                TBN_INVALID_SHAPE, "TBN conv: input records of 2^31 bytes or more");
     g.N = static_cast<int>(d->n);
     g.C = static_cast<int>(d->c), g.H = static_cast<int>(d->h), g.W = static_cast<int>(d->w);
     g.M = static_cast<int>(d->m);
@@ -305,15 +557,33 @@ int make_tbn_geom(const tbn_conv2d_desc* d, int flags, TbnGeom& g) {
     TBN_REQUIRE(g.YH > 0 && g.YW > 0, TBN_INVALID_SHAPE, "pooled output is empty");
     TBN_REQUIRE(!g.pool || (flags & TBN_EPI_RELU), TBN_NOT_IMPLEMENTED,
                 "TBN conv: the fused 2x2 max pool needs the fused ReLU");
-    g.chunks = static_cast<int>((d->c + kChunk - 1) / kChunk);
+    g.chunks = static_cast<int>(chunks);
     g.taps = g.kh * g.kw;
     g.ksteps = g.chunks * g.taps;
     g.mfrags = (g.M + 31) / 32;
+    g.pixels = g.pool ? static_cast<int64_t>(g.N) * g.YH * g.YW * 4 : static_cast<int64_t>(g.N) * g.OH * g.OW;
+    g.pfrags = (g.pixels + 31) / 32;
+    // two pixel fragments per wave (each weight fragment serves two MFMAs)
+    // while that still leaves about eight waves per CU, else one
+    g.FCW = g.mfrags * ((g.pfrags + 1) / 2) >= 2048 ? 2 : 1;
+    // k-steps per load group: each group costs one memory round trip, a
+    // wasted (padding) step an MFMA and two cached loads
+    static const int kGroups[] = {9, 8, 4, 3, 2, 1};
+    double best = 0.0;
+    for (int G : kGroups) {
+        const int trips = (g.ksteps + G - 1) / G;
+        const double cost = trips + 0.05 * (trips * G - g.ksteps);
+        if (G == 9 || cost < best) best = cost, g.G = G;
+    }
+    TBN_REQUIRE((g.waves() + 3) / 4 < (1LL << 31), TBN_INVALID_SHAPE, "TBN conv: grid too large");
 
-    // tile: the largest share of useful MFMA columns, weighed by how well the
-    // grid fills the chip (512 blocks: two per CU); ties to larger tiles
+    // fused tile: staged pixels per thread bounded (IPT <= 8 items of 8
+    // channels), at most 4 pixel fragments; the score is the share of useful
+    // MFMA columns weighed by how well the grid fills the chip (512 blocks)
+    // and by the patch pixels staged per output pixel (the halo)
     const int rows = g.pool ? 2 * g.YH : g.OH, cols = g.pool ? 2 * g.YW : g.OW;
-    double best = -1.0;
+    double best_score = -1.0;
+    g.fused = 0;
     for (int wv = std::min(4, g.mfrags); wv >= 1; wv = wv == 4 ? 2 : wv - 1) {
         const int mblocks = (g.mfrags + wv - 1) / wv;
         for (int tc = cols; tc >= 1; tc = tc > 8 ? (tc + 1) / 2 : 0) {
@@ -323,14 +593,16 @@ int make_tbn_geom(const tbn_conv2d_desc* d, int flags, TbnGeom& g) {
                 if (px > 128) break;
                 const int PR = (tr - 1) * g.sh + (g.kh - 1) * g.dh + 1;
                 const int PC = (TC - 1) * g.sw + (g.kw - 1) * g.dw + 1;
-                if (static_cast<int64_t>(PR) * PC * kRec > kMaxLds) break;
+                if (static_cast<int64_t>(PR) * PC * 8 > 8LL * 64 * wv) break;
                 const int fc = (px + 31) / 32;
                 const int tr_n = (rows + tr - 1) / tr, tc_n = (cols + TC - 1) / TC;
                 const double useful = static_cast<double>(rows) * cols / (static_cast<double>(tr_n) * tc_n * fc * 32);
                 const double blocks = static_cast<double>(g.N) * tr_n * tc_n * mblocks;
-                const double score = useful * std::min(1.0, blocks / 512.0) + 1e-6 * px + 1e-9 * wv;
-                if (score > best) {
-                    best = score;
+                const double halo = static_cast<double>(PR) * PC / std::min(px, rows * cols);
+                const double score = useful * std::min(1.0, blocks / 512.0) / (1.0 + 0.1 * halo) + 1e-9 * wv;
+                if (score > best_score) {
+                    best_score = score;
+                    g.fused = 1;
                     g.TR = tr, g.TC = TC, g.FC = fc, g.WV = wv, g.mblocks = mblocks;
                     g.tiles_r = tr_n, g.tiles_c = tc_n, g.PR = PR, g.PC = PC;
                 }
@@ -338,15 +610,70 @@ int make_tbn_geom(const tbn_conv2d_desc* d, int flags, TbnGeom& g) {
         }
         if (wv == 1) break;
     }
-    TBN_REQUIRE(best >= 0.0, TBN_INVALID_SHAPE, "TBN conv: no tile's input patch fits the LDS");
-    TBN_REQUIRE(g.blocks() < (1LL << 31), TBN_INVALID_SHAPE, "TBN conv: grid too large");
+    if (g.fused) {
+        g.div_npix = make_fastdiv(static_cast<uint32_t>(g.PR * g.PC));
+        g.div_pc = make_fastdiv(static_cast<uint32_t>(g.PC));
+        const int ipt = (g.PR * g.PC * 8 + 64 * g.WV - 1) / (64 * g.WV);
+        g.IPT = ipt <= 2 ? 2 : (ipt <= 4 ? 4 : 8);
+        g.GF = g.taps == 1 ? 1 : 9;
+        g.FC = g.FC == 3 ? 4 : g.FC;
+        const int variant = tbn_hip::tuning(TBN_TUNE_TBN_CONV);
+        if (variant == 2 || g.fused_blocks() >= (1LL << 31) || d->c * d->h * d->w * 4 >= (1LL << 31) ||
+            (d->c + 64 + 8) * d->h * d->w * 4 >= (1LL << 32) ||
+            (d->m + 32) * static_cast<int64_t>(g.YH) * g.YW * 4 >= (1LL << 31))
+            g.fused = 0;  // the two-pass kernels (the forced choice, or 32-bit offsets would not reach)
+    }
     return TBN_SUCCESS;
 }
 
+template <int FCW, int G>
+void launch_conv(const TbnGeom& g, const TbnConvArgs& a, const uint8_t* xt, hipStream_t s) {
+    hipLaunchKernelGGL((tbn_conv_kernel<FCW, G>), dim3(static_cast<unsigned>((g.waves() + 3) / 4)), dim3(256), 0, s,
+                       g, a, xt);
+}
+
+template <int FCW>
+void launch_conv_g(const TbnGeom& g, const TbnConvArgs& a, const uint8_t* xt, hipStream_t s) {
+    switch (g.G) {
+        case 9: return launch_conv<FCW, 9>(g, a, xt, s);
+        case 8: return launch_conv<FCW, 8>(g, a, xt, s);
+        case 4: return launch_conv<FCW, 4>(g, a, xt, s);
+        case 3: return launch_conv<FCW, 3>(g, a, xt, s);
+        case 2: return launch_conv<FCW, 2>(g, a, xt, s);
+        default: return launch_conv<FCW, 1>(g, a, xt, s);
+    }
+}
+
+template <int FC, int IPT>
+void launch_fused_g(const TbnGeom& g, const TbnConvArgs& a, hipStream_t s) {
+    const dim3 grid(static_cast<unsigned>(g.fused_blocks())), block(64 * g.WV);
+    const size_t lds = static_cast<size_t>(g.PR) * g.PC * kRec;
+    if (g.GF == 1) hipLaunchKernelGGL((tbn_conv_fused_kernel<FC, IPT, 1>), grid, block, lds, s, g, a);
+    else hipLaunchKernelGGL((tbn_conv_fused_kernel<FC, IPT, 9>), grid, block, lds, s, g, a);
+}
+
 template <int FC>
-void launch_fc(const TbnGeom& g, const TbnConvArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL(tbn_conv_kernel<FC>, dim3(static_cast<unsigned>(g.blocks())), dim3(64 * g.WV),
-                       static_cast<size_t>(g.lds()), s, g, a);
+void launch_fused_i(const TbnGeom& g, const TbnConvArgs& a, hipStream_t s) {
+    if (g.IPT == 2) launch_fused_g<FC, 2>(g, a, s);
+    else if (g.IPT == 4) launch_fused_g<FC, 4>(g, a, s);
+    else launch_fused_g<FC, 8>(g, a, s);
+}
+
+int run_tbn_fused(const TbnGeom& g, const TbnConvArgs& a, hipStream_t s) {
+    if (g.FC == 1) launch_fused_i<1>(g, a, s);
+    else if (g.FC == 2) launch_fused_i<2>(g, a, s);
+    else launch_fused_i<4>(g, a, s);
+    return tbn_hip::check_launch("conv2d_tbn (fused)");
+}
+
+int run_tbn_conv(const TbnGeom& g, const TbnConvArgs& a, uint8_t* xt, hipStream_t s) {
+    const int64_t items = static_cast<int64_t>(g.N) * g.chunks * 8 * g.H * g.W;
+    const int blocks = static_cast<int>(std::min<int64_t>((items + 255) / 256, 1 << 20));
+    hipLaunchKernelGGL(tbn_records_kernel, dim3(blocks), dim3(256), 0, s, a.x, g, a.lo, a.hi,
+                       reinterpret_cast<uint32_t*>(xt));
+    if (g.FCW == 2) launch_conv_g<2>(g, a, xt, s);
+    else launch_conv_g<1>(g, a, xt, s);
+    return tbn_hip::check_launch("conv2d_tbn");
 }
 
 }  // namespace
@@ -359,6 +686,15 @@ int tbn_hip_tbn_conv_weights_bytes(const tbn_conv2d_desc* desc, int64_t* bytes) 
     const int rc = make_tbn_geom(desc, 0, g);
     if (rc) return rc;
     *bytes = static_cast<int64_t>(g.mfrags) * g.ksteps * 1024;
+    return tbn_hip::ok();
+}
+
+int tbn_hip_tbn_conv_scratch_bytes(const tbn_conv2d_desc* desc, int64_t* bytes) {
+    TBN_REQUIRE(bytes, TBN_INVALID_ARGUMENT, "null pointer");
+    TbnGeom g;
+    const int rc = make_tbn_geom(desc, 0, g);
+    if (rc) return rc;
+    *bytes = g.fused ? 0 : g.record_bytes();
     return tbn_hip::ok();
 }
 
@@ -381,24 +717,28 @@ int tbn_hip_pack_tbn_conv_weights(const uint8_t* packed, int64_t K_pad, int64_t 
 
 int tbn_hip_conv2d_tbn_prepacked(const float* x, const tbn_conv2d_desc* desc, const uint8_t* w4, const float* scale,
                                  float alpha, const float* bias, const float* residual, int flags, float lo, float hi,
-                                 float* y, tbn_stream_t stream) {
+                                 uint8_t* scratch, float* y, tbn_stream_t stream) {
     TbnGeom g;
     int rc = make_tbn_geom(desc, flags, g);
     if (rc) return rc;
     TBN_REQUIRE(!(residual && g.pool), TBN_INVALID_ARGUMENT, "a residual excludes the fused max pool");
     if (g.N == 0) return tbn_hip::ok();
     TBN_REQUIRE(x && w4 && y, TBN_INVALID_ARGUMENT, "null pointer");
-    TBN_REQUIRE(reinterpret_cast<uintptr_t>(w4) % 16 == 0, TBN_INVALID_ARGUMENT, "w4 must be 16-byte aligned");
+    TBN_REQUIRE(reinterpret_cast<uintptr_t>(w4) % 16 == 0 && reinterpret_cast<uintptr_t>(scratch) % 16 == 0,
+                TBN_INVALID_ARGUMENT, "w4 and scratch must be 16-byte aligned");
     TBN_DEVICE_GUARD();
     const TbnConvArgs a{x, w4, y, scale, alpha, bias, residual, flags, lo, hi};
     const hipStream_t s = tbn_hip::stream_of(stream);
-    switch (g.FC) {
-        case 1: launch_fc<1>(g, a, s); break;
-        case 2: launch_fc<2>(g, a, s); break;
-        case 3: launch_fc<3>(g, a, s); break;
-        default: launch_fc<4>(g, a, s); break;
-    }
-    return tbn_hip::check_launch("conv2d_tbn");
+    if (g.fused) return run_tbn_fused(g, a, s);
+    if (scratch) return run_tbn_conv(g, a, scratch, s);
+    // the stream workspace (refused while s captures)
+    void* ws = nullptr;
+    bool temporary = false;
+    rc = tbn_hip::stream_workspace(s, static_cast<size_t>(g.record_bytes()), ws, temporary);
+    if (rc) return rc;
+    rc = run_tbn_conv(g, a, static_cast<uint8_t*>(ws), s);
+    tbn_hip::release_workspace(ws, temporary, s);
+    return rc;
 }
 
 int tbn_hip_conv2d_tbn_kernel_name(const tbn_conv2d_desc* desc, int flags, char* name, size_t len) {
@@ -406,8 +746,10 @@ int tbn_hip_conv2d_tbn_kernel_name(const tbn_conv2d_desc* desc, int flags, char*
     TbnGeom g;
     const int rc = make_tbn_geom(desc, flags, g);
     if (rc) return rc;
-    std::snprintf(name, len, "tbn_conv_kernel<%d> (tile %dx%d, %d waves, %lld blocks)", g.FC, g.TR, g.TC, g.WV,
-                  static_cast<long long>(g.blocks()));
+    if (g.fused)
+        std::snprintf(name, len, "tbn_conv_fused_kernel<%d, %d, %d>", g.FC, g.IPT, g.GF);
+    else
+        std::snprintf(name, len, "tbn_conv_kernel<%d, %d>", g.FCW, g.G);
     return tbn_hip::ok();
 }
 

@@ -211,6 +211,7 @@ struct Op {
     int workspace = -1;              // value id of the op's transient workspace (grouped conv slices,
                                      // a TBN Gemm's fp4 activation rows)
     bool tbn = false;                // TBN arithmetic (ternarized activations, integer products)
+    int64_t tbn_scratch = 0;         // bytes of a TBN conv's record scratch (0: the fused kernel needs none)
     const Tensor* tbn_w = nullptr;   // its fp4 weights: TBN conv layout, or [N_pad, K_pad / 2] rows
     const float* scale = nullptr;  // per-channel scale (device)
     const float* w = nullptr;      // fp32 weights (device)
@@ -559,6 +560,10 @@ struct TBNModel::Session::Impl {
             // bias / scale steps (model.hpp:482-557, conv2d.cpp:220-316)
             op.tbn = true;
             op.tbn_w = &tbn_conv_weights(node.name, *op.pw, op.desc);
+            // the two-pass kernels' ternarized input: a workspace slot of the arena
+            check_status(tbn_hip_tbn_conv_scratch_bytes(&op.desc, &op.tbn_scratch),
+                         ("Conv '" + node.name + "'").c_str());
+            if (op.tbn_scratch) op.workspace = new_value(node.name + "#t4", Shape{op.tbn_scratch}, DataType::UINT8);
             op.out = new_value(node.outputs[0], Shape{xs.dims[0], ws.dims[0], OH, OW}, DataType::FLOAT32);
             ops.push_back(op);
             return;
@@ -1245,7 +1250,11 @@ struct TBNModel::Session::Impl {
                     check_status(tbn_hip_conv2d_tbn_prepacked(fp(op.in[0]), &op.desc, op.tbn_w->typed_data<uint8_t>(),
                                                               op.scale, 1.0f, bias_of(op),
                                                               op.residual >= 0 ? fp(op.residual) : nullptr, op.flags,
-                                                              -0.1f, 0.1f, fp(op.out), s),
+                                                              -0.1f, 0.1f,
+                                                              op.workspace >= 0
+                                                                  ? static_cast<uint8_t*>(ptr(op.workspace))
+                                                                  : nullptr,
+                                                              fp(op.out), s),
                                  what.c_str());
                     return;
                 }

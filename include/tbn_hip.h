@@ -120,7 +120,8 @@ int tbn_hip_synchronize(tbn_stream_t stream);
 /* ---- tuning controls (no counterpart in the reference) ---------------------
  * Process-wide launch-shape choices.  Each starts from an environment variable
  * read once, at the first call that needs it (TBN_CONV_TILE, TBN_CONV_SPLITS,
- * TBN_GEMM_SPLITS, TBN_GEMM_TILE), and changes only through tbn_hip_set_tuning.
+ * TBN_GEMM_SPLITS, TBN_GEMM_TILE, TBN_TBN_CONV), and changes only through
+ * tbn_hip_set_tuning.
  * They pick kernel variants: a forced conv tile never changes a result (every
  * tile sums in the same order); a forced split count or GEMM tile changes the
  * summation order. */
@@ -129,9 +130,14 @@ enum tbn_tuning {
     TBN_TUNE_CONV_SPLITS = 2, /* patch-conv K splits, 0 = automatic; pooled
                                  convs never split                               */
     TBN_TUNE_GEMM_SPLITS = 3, /* wide GEMM K splits, 0 = automatic              */
-    TBN_TUNE_GEMM_TILE = 4    /* wide GEMM tile: 0 = 128x512, 1 = 64x128,
+    TBN_TUNE_GEMM_TILE = 4,   /* wide GEMM tile: 0 = 128x512, 1 = 64x128,
                                  2 = 32x128 in two K groups (even K/64 only),
                                  -1 = automatic (default)                        */
+    TBN_TUNE_TBN_CONV = 5     /* TBN conv kernels: 0 = automatic (default),
+                                 1 = the fused kernel where a tile fits,
+                                 2 = the two-pass kernels (ternarized records in
+                                 the caller's scratch, then the product); both
+                                 give the same bits                               */
 };
 int tbn_hip_set_tuning(int option, int value);
 int tbn_hip_get_tuning(int option, int* value);
@@ -513,6 +519,11 @@ int tbn_hip_tbn_conv_weights_bytes(const tbn_conv2d_desc* desc, int64_t* bytes);
  * aligned.  The weight-side cache of the Session's conv (model.hpp:456-480). */
 int tbn_hip_pack_tbn_conv_weights(const uint8_t* packed, int64_t K_pad, int64_t N_pad,
                                   const tbn_conv2d_desc* desc, uint8_t* w4, tbn_stream_t stream);
+/* Bytes of the scratch tbn_hip_conv2d_tbn_prepacked needs for desc under the
+ * current tuning: 0 where the fused kernel runs (it stages the ternarized
+ * input in LDS), else the input ternarized into fp4 pixel records,
+ * n * ceil(C / 64) * h * w * 32. */
+int tbn_hip_tbn_conv_scratch_bytes(const tbn_conv2d_desc* desc, int64_t* bytes);
 /* The reference Session's quantized convolution (model.hpp:482-557 with
  * im2col_ternary_packed, conv2d.cpp:511-601; conv2d_binary, conv2d.cpp:
  * 220-316): every input tap ternarized at (lo, hi), taps outside the image 0,
@@ -521,13 +532,17 @@ int tbn_hip_pack_tbn_conv_weights(const uint8_t* packed, int64_t K_pad, int64_t 
  * TBN_EPI_BIAS_THEN_SCALE (float(C) + b[m]) * alpha*s[m]; scale and bias may
  * be NULL.  Then `residual` (same layout as y) is added, TBN_EPI_RELU, and
  * TBN_EPI_MAXPOOL2X2 (floor mode; needs TBN_EPI_RELU and no residual).
- * C*kh*kw <= 2^24.  No workspace, no allocation: capturable. */
+ * C*kh*kw <= 2^24.  `scratch` (16-byte aligned, tbn_hip_tbn_conv_scratch_bytes)
+ * receives the ternarized input; with scratch the call allocates nothing and
+ * may be captured; NULL takes the library's stream workspace, refused
+ * (TBN_NOT_IMPLEMENTED) while the stream captures. */
 int tbn_hip_conv2d_tbn_prepacked(const float* x, const tbn_conv2d_desc* desc, const uint8_t* w4,
                                  const float* scale, float alpha, const float* bias, const float* residual,
-                                 int flags, float lo, float hi, float* y, tbn_stream_t stream);
-/* No counterpart in the reference (a diagnostic for profiling): the kernel
- * and tile tbn_hip_conv2d_tbn_prepacked runs for desc and flags.  No GPU
- * work. */
+                                 int flags, float lo, float hi, uint8_t* scratch, float* y,
+                                 tbn_stream_t stream);
+/* No counterpart in the reference (a diagnostic for profiling): the conv
+ * kernel tbn_hip_conv2d_tbn_prepacked runs for desc and flags, as a profiler
+ * names it.  No GPU work. */
 int tbn_hip_conv2d_tbn_kernel_name(const tbn_conv2d_desc* desc, int flags, char* name, size_t len);
 
 #ifdef __cplusplus

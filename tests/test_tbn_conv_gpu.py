@@ -69,13 +69,31 @@ def pack_tbn_conv(binw, d):
 def run_tbn_conv(x, d, w4, scale, bias, residual, flags, out_shape):
     y = empty(out_shape, torch.float32)
     y.fill_(np.nan)
+    nbytes = ctypes.c_int64()
+    tbn_hip.call("tbn_hip_tbn_conv_scratch_bytes", ctypes.byref(d), ctypes.byref(nbytes))
+    scratch = empty(max(nbytes.value, 16), torch.uint8)
     tbn_hip.call("tbn_hip_conv2d_tbn_prepacked", P(x), ctypes.byref(d), P(w4), P(scale), 1.0, P(bias), P(residual),
-                 flags, tbn_ref.LO, tbn_ref.HI, P(y), None)
-    return host(y)
+                 flags, tbn_ref.LO, tbn_ref.HI, P(scratch), P(y), None)
+    out = host(y)
+    # the same call on the library's stream workspace gives the same bits
+    y.fill_(np.nan)
+    tbn_hip.call("tbn_hip_conv2d_tbn_prepacked", P(x), ctypes.byref(d), P(w4), P(scale), 1.0, P(bias), P(residual),
+                 flags, tbn_ref.LO, tbn_ref.HI, None, P(y), None)
+    assert np.array_equal(host(y).view(np.uint32), out.view(np.uint32))
+    return out
 
 
+@pytest.mark.parametrize("variant", [1, 2], ids=["fused", "two_pass"])
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[:7])))
-def test_tbn_conv_matches_oracle(dev, orc, case):
+def test_tbn_conv_matches_oracle(dev, orc, case, variant):
+    """Both kernel variants (the fused kernel staging ternarized patches in
+    LDS, where a tile fits; the records pass then the barrier-free product)
+    bit-exact against the oracle, with and without caller scratch."""
+    with tbn_hip.tuning(tbn_hip.TUNE_TBN_CONV, variant):
+        _check_case(orc, case)
+
+
+def _check_case(orc, case):
     N, C, H, W, M, kh, kw, stride, pad, dil, flags, with_scale, with_res = case
     rng = np.random.default_rng(N * 131 + C * 7 + M + kh)
     x = threshold_input(rng, (N, C, H, W))
@@ -132,9 +150,9 @@ def test_tbn_conv_error_codes(dev):
     for flags, code in cases:
         with pytest.raises(tbn_hip.TbnError) as e:
             tbn_hip.call("tbn_hip_conv2d_tbn_prepacked", P(x), ctypes.byref(d), P(buf), None, 1.0, None, None, flags,
-                         -0.1, 0.1, P(y), None)
+                         -0.1, 0.1, P(buf), P(y), None)
         assert e.value.code == code
     with pytest.raises(tbn_hip.TbnError) as e:  # residual with the fused pool
         tbn_hip.call("tbn_hip_conv2d_tbn_prepacked", P(x), ctypes.byref(d), P(buf), None, 1.0, None, P(y),
-                     RELU | POOL, -0.1, 0.1, P(y), None)
+                     RELU | POOL, -0.1, 0.1, P(buf), P(y), None)
     assert e.value.code == tbn_hip.INVALID_ARGUMENT
