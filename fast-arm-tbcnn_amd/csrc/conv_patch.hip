@@ -47,10 +47,23 @@ struct PatchGeom {
     int tiles_h, tiles_w;  // 2-D tiles per image (linear == 0)
     int pool, PH, PW;      // fused 2x2 pool and its output size
     int VH, VW;            // extent of computed pixels (2*PH x 2*PW when pooling)
-    int linear;            // 1: a tile is QT consecutive pixels (QT/4 pool windows) of one image
-    int tiles_img;         // tiles per image
-    uint32_t mul_patch;    // ceil(2^32 / (PHi*PWi)): staging item -> channel group by multiply-high
-    uint32_t mul_pwi;      // ceil(2^32 / PWi), or 0 when PWi == 1
+    // 1: a tile is QT consecutive pixels (QT/4 pool windows) of one image;
+    // 2 (stacked): QT consecutive pixels of the flattened N x OH x OW output,
+    // for stride 1: the images are stacked into one tall image in which input
+    // row ih of image n is virtual row n * vpitch + ih (vpitch = H + ph), so
+    // the ph zero rows below one image are the ph above the next, and output
+    // (n, oh) reads virtual rows n * vpitch + oh - ph + r * dh.  A tile's
+    // patch is virtual rows [row0, row0 + PHi) at full padded width, and its
+    // output runs are whole 4*QT-byte spans of each channel plane.
+    int linear;
+    int vpitch;            // stacked: virtual rows per image
+    int tiles_img;         // tiles per image (stacked: tiles of the whole batch)
+    // the kernel's runtime divisors, as branch-free multiply-high dividers:
+    // staging item -> channel group and patch pixel -> row (PHi*PWi, PWi);
+    // block -> split, channel tile, image, tile row (blocks_split, channel
+    // tiles, tiles_img, tiles_w); pixel -> row, window -> row, flattened pixel
+    // -> image (OW, PW, OH*OW); virtual row -> image (vpitch)
+    UDiv div_patch, div_pwi, div_split, div_mt, div_img, div_tw, div_ow, div_pw, div_plane, div_vpitch;
     // patch sampling: patch pixel (pr, pc) is input (ih0 + pr*psh, iw0 + pc*psw);
     // output (oh, ow) reads patch pixel ((oh-row0)*poh, (ow-col0)*pow).  1x1
     // kernels stage only the pixels they use (psh = sh, poh = 1); others stage
@@ -77,12 +90,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
                                              0x00020000);
 }
 
-// n / d for the staging coordinates (n * d < 2^32): multiply-high by the
-// host's ceil(2^32 / d); mul == 0 stands for d == 1.
-__device__ __forceinline__ int div_by(int n, uint32_t mul) {
-    return mul ? static_cast<int>(__umulhi(static_cast<uint32_t>(n), mul)) : n;
-}
-
 // Output pixel of the tile-local index ql and its patch index.  Linear tiles
 // run along the flattened image (pool windows when pooling), so a fragment's
 // 32 lanes hold 32 consecutive pixels (or 8 windows) of one channel;
@@ -90,18 +97,31 @@ __device__ __forceinline__ int div_by(int n, uint32_t mul) {
 // and mapped to patch index 0 (their results are never stored).
 template <class Cfg>
 __device__ __forceinline__ bool tile_pixel(const PatchGeom& g, int q0, int row0, int col0, int ql, int& oh,
-                                           int& ow, int& patch_index) {
+                                           int& ow, int& patch_index, int& img) {
     bool valid;
+    img = 0;
+    if (g.linear == 2) {
+        // stacked: image, row and column of flattened pixel q0 + ql
+        const int plane = g.OH * g.OW;
+        const int q = q0 + ql;
+        valid = q < g.N * plane;
+        img = valid ? udiv(q, g.div_plane) : 0;
+        const int p = q - img * plane;
+        oh = udiv(p, g.div_ow);
+        ow = p - oh * g.OW;
+        patch_index = valid ? (img * g.vpitch + oh - g.ph - row0) * g.PWi + ow : 0;
+        return valid;
+    }
     if (g.linear) {
         if (g.pool) {
             const int w = q0 + (ql >> 2);
-            const int pr = w / g.PW;
+            const int pr = udiv(w, g.div_pw);
             oh = 2 * pr + ((ql >> 1) & 1);
             ow = 2 * (w - pr * g.PW) + (ql & 1);
             valid = w < g.PH * g.PW;
         } else {
             const int q = q0 + ql;
-            oh = q / g.OW;
+            oh = udiv(q, g.div_ow);
             ow = q - oh * g.OW;
             valid = q < g.OH * g.OW;
         }
@@ -224,39 +244,55 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     // one XCD: the tile's patch is fetched into that XCD's L2 once
     const int tiles_m = (g.M + Cfg::BM - 1) / Cfg::BM;
     int bid = static_cast<int>(blockIdx.x);
-    int sp = 0;  // K split of this block
-    if (g.splits > 1) {
-        sp = bid / g.blocks_split;
-        bid -= sp * g.blocks_split;
-    }
-    if (g.blocks_split % 8 == 0) bid = (bid % 8) * (g.blocks_split / 8) + bid / 8;
+    const int sp = udiv(bid, g.div_split);  // K split of this block
+    bid -= sp * g.blocks_split;
+    if ((g.blocks_split & 7) == 0) bid = (bid & 7) * (g.blocks_split >> 3) + (bid >> 3);
     const int cb = sp * g.cps;                        // the block's chunks [cb, ce)
     const int ce = min(g.chunks, cb + g.cps);
-    const int mt = bid % tiles_m;
-    int st = bid / tiles_m;
-    const int n = st / g.tiles_img;
+    int st = udiv(bid, g.div_mt);
+    const int mt = bid - st * tiles_m;
+    const int n = udiv(st, g.div_img);
     st -= n * g.tiles_img;
     const int m0 = mt * Cfg::BM;
-    int q0 = 0, oh0, ow0;  // first pixel / window of a linear tile; first row / col of the patch
-    if (g.linear) {
-        q0 = st * (g.pool ? Cfg::QT / 4 : Cfg::QT);
-        oh0 = g.pool ? 2 * (q0 / g.PW) : q0 / g.OW;
+    // first pixel / window of a linear tile; first output row / col of the
+    // tile (stacked: the patch's first virtual row); the patch's first input
+    // row (stacked: virtual row) and column
+    int q0 = 0, oh0, ow0, ih0, iw0;
+    if (g.linear == 2) {
+        q0 = st * Cfg::QT;
+        const int plane = g.OH * g.OW;
+        const int n0 = udiv(q0, g.div_plane);
+        oh0 = n0 * g.vpitch + udiv(q0 - n0 * plane, g.div_ow) - g.ph;
         ow0 = 0;
+        ih0 = oh0;
+        iw0 = -g.pw;
     } else {
-        const int th = st / g.tiles_w;
-        oh0 = th * Cfg::TH;
-        ow0 = (st - th * g.tiles_w) * Cfg::TW;
+        if (g.linear) {
+            q0 = st * (g.pool ? Cfg::QT / 4 : Cfg::QT);
+            oh0 = g.pool ? 2 * udiv(q0, g.div_pw) : udiv(q0, g.div_ow);
+            ow0 = 0;
+        } else {
+            const int th = udiv(st, g.div_tw);
+            oh0 = th * Cfg::TH;
+            ow0 = (st - th * g.tiles_w) * Cfg::TW;
+        }
+        ih0 = oh0 * g.sh - g.ph;
+        iw0 = ow0 * g.sw - g.pw;
     }
-    const int ih0 = oh0 * g.sh - g.ph, iw0 = ow0 * g.sw - g.pw;
 
     // per-channel epilogue factors of the block's BM channels: loaded now (the
     // load latency hides behind the first chunk), written to LDS after the
     // patch buffers with the first chunk, read back as float4 by the epilogue
-    float raw_scale = 1.0f, raw_bias = 0.0f;
-    if (tid < Cfg::BM) {
-        const int m = min(m0 + tid, g.M - 1);
-        if (epi.scale) raw_scale = epi.scale[m];
-        if (epi.bias) raw_bias = epi.bias[m];
+    // (buffer loads from ranges that are empty for a null pointer, read 0,
+    // then select: no branch or wait lies between these loads and the
+    // chunk's)
+    float raw_scale, raw_bias;
+    {
+        const uint32_t mofs = static_cast<uint32_t>(min(m0 + tid, g.M - 1)) * 4;
+        const __amdgpu_buffer_rsrc_t s_rs = make_rsrc(epi.scale, epi.scale ? static_cast<uint64_t>(g.M) * 4 : 0);
+        const __amdgpu_buffer_rsrc_t b_rs = make_rsrc(epi.bias, epi.bias ? static_cast<uint64_t>(g.M) * 4 : 0);
+        raw_scale = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s_rs, mofs, 0, 0));
+        raw_bias = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b_rs, mofs, 0, 0));
     }
 
     // ---- staging of one chunk: patch items = (8-channel group, pixel) and
@@ -280,7 +316,9 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     // gets an offset of at least kOutside, and a channel past C lands past the
     // image's C planes: the range check returns 0 for both, so no load waits
     // on a branch or a select.
-    const __amdgpu_buffer_rsrc_t x_rs = make_rsrc(x + img, static_cast<uint64_t>(g.C) * HW4);
+    const uint32_t img_bytes = static_cast<uint32_t>(g.C) * HW4;  // stacked: image pitch of the offsets
+    const __amdgpu_buffer_rsrc_t x_rs =
+        make_rsrc(x + img, static_cast<uint64_t>(img_bytes) * (g.linear == 2 ? g.N : 1));
     const __amdgpu_buffer_rsrc_t w_rs = make_rsrc(wbits, static_cast<uint64_t>(m_alloc) * col_bytes);
     constexpr uint32_t kOutside = 0x80000000u;
     // per item, computed once: chunk-0 byte offset and LDS slot (an item past
@@ -290,15 +328,24 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
 #pragma unroll
     for (int it = 0; it < kMaxItems; ++it) {
         const int item = tid + it * Cfg::NT;
-        const int grp = div_by(item, g.mul_patch);
+        const int grp = udiv(item, g.div_patch);
         const int pp = item - grp * patch;
-        const int pr = div_by(pp, g.mul_pwi);
-        const int ih = ih0 + pr * g.psh;
+        const int pr = udiv(pp, g.div_pwi);
+        int ih = ih0 + pr * g.psh;
         const int iw = iw0 + (pp - pr * g.PWi) * g.psw;
         const bool in_patch = item < items;
+        uint32_t img_ofs = 0;
+        if (g.linear == 2) {
+            // virtual row -> image and row (the rows past H are the zero band;
+            // ih stays negative before image 0 and the image test drops the last's)
+            const int nv = ih >= 0 ? udiv(ih, g.div_vpitch) : 0;
+            ih = ih >= 0 && nv < g.N && ih - nv * g.vpitch < g.H ? ih - nv * g.vpitch : -1;
+            img_ofs = static_cast<uint32_t>(nv) * img_bytes;
+        }
         const bool ok = in_patch && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
                         static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
-        xoff[it] = ok ? static_cast<uint32_t>(grp * 8) * HW4 + static_cast<uint32_t>(ih * g.W + iw) * 4 : kOutside;
+        xoff[it] = ok ? img_ofs + static_cast<uint32_t>(grp * 8) * HW4 + static_cast<uint32_t>(ih * g.W + iw) * 4
+                      : kOutside;
         xslot[it] = in_patch ? pp * kPix + grp * 8 : patch * kPix;
     }
 #pragma unroll
@@ -312,36 +359,44 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                       : kOutside;
         wslot[it] = (item < witems ? tap * Cfg::BM + ml : Cfg::BM * g.taps) * kWordHalves;
     }
-    float stage[kMaxItems][8];
-    u32x4_t wstage[kMaxWItems];
+    // With 3x3 taps every thread stages exactly kMaxItems patch items and
+    // kMaxWItems weight items (the launch picks MAXI, the smallest of 1, 2, 4,
+    // 8 that covers the patch; items past it load from kOutside into the
+    // spare slots), so the loads carry no branch, and no wait, between them;
+    // other kernels stage per_thread / wper_thread items.
+    constexpr bool kAll = TAPS > 0;
+    using Stage = float[kMaxItems][8];
+    using WStage = u32x4_t[kMaxWItems];
+    Stage stage;
+    WStage wstage;
 
-    auto load_chunk = [&](int ch) {
+    auto load_chunk = [&](int ch, Stage& st_, WStage& wst_) {
         const uint32_t cofs = static_cast<uint32_t>(ch * kChunk) * HW4;
         const uint32_t wofs_ch = static_cast<uint32_t>(ch * g.taps) * static_cast<uint32_t>(m_alloc) * kWordBytes;
 #pragma unroll
         for (int it = 0; it < kMaxItems; ++it) {
-            if (it < per_thread) {
+            if (kAll || it < per_thread) {
                 const uint32_t o = xoff[it] + cofs;
 #pragma unroll
                 for (int e = 0; e < 8; ++e)
-                    stage[it][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x_rs, o + e * HW4, 0, 0));
+                    st_[it][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x_rs, o + e * HW4, 0, 0));
             }
         }
 #pragma unroll
         for (int it = 0; it < kMaxWItems; ++it) {
-            if (it < wper_thread) {
-                wstage[it] = __builtin_bit_cast(
-                    u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(w_rs, woff[it] + wofs_ch, 0, 0));
+            if (kAll || it < wper_thread) {
+                wst_[it] = __builtin_bit_cast(u32x4_t,
+                                              __builtin_amdgcn_raw_buffer_load_b128(w_rs, woff[it] + wofs_ch, 0, 0));
             }
         }
     };
-    auto store_chunk = [&](int b) {
+    auto store_chunk = [&](int b, Stage& st_, WStage& wst_) {
         uint16_t* dst = lds + b * buf_elems;
 #pragma unroll
         for (int it = 0; it < kMaxItems; ++it) {
-            if (it < per_thread) {
+            if (kAll || it < per_thread) {
                 uint4 hi, mid, lo;
-                split8(stage[it], hi, mid, lo);
+                split8(st_[it], hi, mid, lo);
                 uint16_t* d = dst + xslot[it];
                 *reinterpret_cast<uint4*>(d) = hi;
                 *reinterpret_cast<uint4*>(d + plane_elems) = mid;
@@ -350,8 +405,8 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
         }
 #pragma unroll
         for (int it = 0; it < kMaxWItems; ++it) {
-            if (it < wper_thread) {
-                *reinterpret_cast<u32x4_t*>(dst + wofs + wslot[it]) = wstage[it];
+            if (kAll || it < wper_thread) {
+                *reinterpret_cast<u32x4_t*>(dst + wofs + wslot[it]) = wst_[it];
             }
         }
     };
@@ -360,8 +415,8 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     int pbase[Cfg::FC];
 #pragma unroll
     for (int j = 0; j < Cfg::FC; ++j) {
-        int oh, ow, pi;
-        tile_pixel<Cfg>(g, q0, oh0, ow0, wq * Cfg::WQ + j * 32 + (lane & 31), oh, ow, pi);
+        int oh, ow, pi, im;
+        tile_pixel<Cfg>(g, q0, oh0, ow0, wq * Cfg::WQ + j * 32 + (lane & 31), oh, ow, pi, im);
         pbase[j] = pi * kPix;
     }
     // this lane's weight rows (fragment rows) inside the chunk's word table
@@ -375,16 +430,21 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    load_chunk(cb);
-    store_chunk(0);
+    // K groups: both chunks' loads in flight before the first is stored
+    // (host-checked: exactly two chunks, KG = 2)
+    Stage stage2;
+    WStage wstage2;
+    load_chunk(cb, stage, wstage);
+    if constexpr (Cfg::KG > 1) load_chunk(cb + 1, stage2, wstage2);
+    store_chunk(0, stage, wstage);
     // [BM] multipliers, [BM] addends after the buffer(s)
     float* epi_lds = reinterpret_cast<float*>(lds + (g.single ? 1 : 2) * buf_elems);
     if (tid < Cfg::BM) {
-        epi_lds[tid] = epi.alpha * raw_scale;
+        epi_lds[tid] = epi.alpha * (epi.scale ? raw_scale : 1.0f);
         epi_lds[Cfg::BM + tid] = raw_bias;
     }
-    if (cb + 1 < ce) load_chunk(cb + 1);
-    if constexpr (Cfg::KG > 1) store_chunk(1);  // both chunks (host-checked: exactly KG = 2)
+    if constexpr (Cfg::KG > 1) store_chunk(1, stage2, wstage2);
+    else if (cb + 1 < ce) load_chunk(cb + 1, stage, wstage);
     __syncthreads();
 
     const int kg = lane >> 5;
@@ -496,8 +556,8 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
         }
         if (Cfg::KG == 1 && ch + 1 < ce) {
             if (g.single) __syncthreads();  // every wave is done reading the buffer
-            store_chunk(g.single ? 0 : (ch + 1 - cb) & 1);
-            if (ch + 2 < ce) load_chunk(ch + 2);
+            store_chunk(g.single ? 0 : (ch + 1 - cb) & 1, stage, wstage);
+            if (ch + 2 < ce) load_chunk(ch + 2, stage, wstage);
         }
         __syncthreads();
     }
@@ -544,18 +604,21 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     const uint32_t plane = pool ? static_cast<uint32_t>(g.PH * g.PW) : static_cast<uint32_t>(g.OH * g.OW);
     const uint32_t plane4 = plane * 4;
     const int64_t obase = (static_cast<int64_t>(n) * g.M + m0) * plane;
-    const uint32_t obytes = static_cast<uint32_t>(g.M - m0) * plane4;
+    // stacked tiles address every image's planes from channel m0 of image 0
+    // (host-checked: M is a multiple of BM, so rows never pass M, and the
+    // batch's output stays under 2^31 bytes)
+    const uint32_t obytes = static_cast<uint32_t>((g.linear == 2 ? g.N * g.M : g.M) - m0) * plane4;
     const __amdgpu_buffer_rsrc_t y_rs = make_rsrc(epi.y + obase, obytes);
     const int rlane = wm * Cfg::WM + 4 * (lane >> 5);  // row of register 0 of fragment 0, from m0
     uint32_t voff[Cfg::FC];
 #pragma unroll
     for (int j = 0; j < Cfg::FC; ++j) {
-        int oh, ow, pi;
-        const bool valid = tile_pixel<Cfg>(g, q0, oh0, ow0, wq * Cfg::WQ + j * 32 + (lane & 31), oh, ow, pi);
+        int oh, ow, pi, im;
+        const bool valid = tile_pixel<Cfg>(g, q0, oh0, ow0, wq * Cfg::WQ + j * 32 + (lane & 31), oh, ow, pi, im);
         const uint32_t pix = pool ? static_cast<uint32_t>((oh >> 1) * g.PW + (ow >> 1))
                                   : static_cast<uint32_t>(oh * g.OW + ow);
         const bool keep = valid && (!pool || (lane & 3) == 0);
-        voff[j] = keep ? static_cast<uint32_t>(rlane) * plane4 + pix * 4 : kOutside;
+        voff[j] = keep ? (static_cast<uint32_t>(im) * g.M + rlane) * plane4 + pix * 4 : kOutside;
     }
     if (epi.partial) {
         // split-K (never with the pool, host-checked): raw sums of this
@@ -775,7 +838,7 @@ int64_t conv_weight_bytes(int weights, const tbn_conv2d_desc* d) {
 
 struct TileChoice {
     int cfg;     // index into the PatchCfg menu
-    int linear;  // 1: linear tiles, 0: 2-D tiles
+    int linear;  // 2: stacked linear tiles, 1: linear tiles, 0: 2-D tiles
     int TH, TW, BM, NT;
     int single;  // 1: one LDS buffer
     int kg;      // K groups of waves (PatchCfg::KG)
@@ -787,10 +850,55 @@ size_t lds_bytes(const PatchGeom& g, int BM, bool ternary) {
     return (g.single ? 1 : 2) * buf + 2 * sizeof(float) * BM;  // buffer(s) + epilogue factors
 }
 
+// Tiles of one launch (per split): stacked tiles cover the whole batch.
+int64_t patch_tiles(const PatchGeom& g) { return static_cast<int64_t>(g.linear == 2 ? 1 : g.N) * g.tiles_img; }
+
+// Stacked tiles apply to stride-1 convs whose channels fill whole chunks (a
+// chunk never reads past C into the next image), whose output channels fill
+// whole BM tiles, without the fused pool, with ph <= (kh-1)*dh (then a later
+// pixel of a tile never sits on an earlier virtual row), and whose batch
+// input and output fit 31-bit offsets.
+bool stacked_ok(const PatchGeom& g, int BM) {
+    const int64_t in_bytes = static_cast<int64_t>(g.N) * g.C * g.H * g.W * 4;
+    const int64_t out_bytes = static_cast<int64_t>(g.N) * g.M * g.OH * g.OW * 4;
+    return g.sh == 1 && g.sw == 1 && g.C % kChunk == 0 && g.M % BM == 0 && !g.pool && g.ph <= (g.kh - 1) * g.dh &&
+           in_bytes < (int64_t(1) << 31) && out_bytes < (int64_t(1) << 31);
+}
+
+// The tile-dependent dividers (blocks_split and the split's divider are set
+// at launch, once the channel tile is known).
+void set_dividers(PatchGeom& g) {
+    g.div_patch = make_udiv(static_cast<uint32_t>(g.PHi * g.PWi));
+    g.div_pwi = make_udiv(static_cast<uint32_t>(g.PWi));
+    g.div_img = make_udiv(static_cast<uint32_t>(std::max(1, g.tiles_img)));
+    g.div_tw = make_udiv(static_cast<uint32_t>(std::max(1, g.tiles_w)));
+    g.div_ow = make_udiv(static_cast<uint32_t>(std::max(1, g.OW)));
+    g.div_pw = make_udiv(static_cast<uint32_t>(std::max(1, g.PW)));
+    g.div_plane = make_udiv(static_cast<uint32_t>(std::max(1, g.OH * g.OW)));
+    g.div_vpitch = make_udiv(static_cast<uint32_t>(std::max(1, g.vpitch)));
+}
+
 void fill_patch(PatchGeom& g, const TileChoice& c) {
     g.linear = c.linear;
     g.single = c.single;
     g.rowperm = 0;
+    g.vpitch = g.H + g.ph;
+    if (c.linear == 2) {
+        // a run of QT pixels spans at most `rows` output rows and crosses at
+        // most `bounds` image boundaries, each of which skips vpitch - OH
+        // virtual rows more than a row step
+        const int QT = c.TH * c.TW;
+        const int plane = g.OH * g.OW;
+        g.tiles_img = static_cast<int>((static_cast<int64_t>(g.N) * plane + QT - 1) / QT);
+        const int rows = (g.OW - 1 + QT - 1) / g.OW + 1;
+        const int bounds = (plane - 1 + QT - 1) / plane;
+        g.tiles_h = g.tiles_w = 0;
+        g.psh = g.psw = g.poh = g.pow_ = 1;
+        g.PHi = rows - 1 + bounds * std::max(0, g.vpitch - g.OH) + (g.kh - 1) * g.dh + 1;
+        g.PWi = g.W + 2 * g.pw;
+        set_dividers(g);
+        return;
+    }
     int rows, cols;  // output rows / columns one tile's pixels span (at most)
     if (c.linear) {
         const int per = g.pool ? c.TH * c.TW / 4 : c.TH * c.TW;
@@ -820,11 +928,7 @@ void fill_patch(PatchGeom& g, const TileChoice& c) {
     g.pow_ = compact ? 1 : g.sw;
     g.PHi = compact ? rows : (rows - 1) * g.sh + (g.kh - 1) * g.dh + 1;
     g.PWi = compact ? cols : (cols - 1) * g.sw + (g.kw - 1) * g.dw + 1;
-    const auto magic = [](int64_t d) -> uint32_t {
-        return d <= 1 ? 0u : static_cast<uint32_t>(((int64_t(1) << 32) + d - 1) / d);
-    };
-    g.mul_patch = magic(static_cast<int64_t>(g.PHi) * g.PWi);
-    g.mul_pwi = magic(g.PWi);
+    set_dividers(g);
     g.rowperm = (!c.linear && !g.pool && c.TH == 8 && c.TW == 8 && g.PWi % 4 == 2) ? 1 : 0;
 }
 
@@ -854,14 +958,21 @@ constexpr TileChoice choice(int cfg, int linear, int single = 0) {
 }
 
 // The TBN_TUNE_CONV_TILE control forces one tile: id = cfg for linear tiles,
-// 16 + cfg for 2-D tiles, plus 32 for the one-buffer variants.
+// 16 + cfg for 2-D tiles, plus 32 for the one-buffer variants, plus 64 for
+// stacked tiles.
 int tile_override() { return tbn_hip::tuning(TBN_TUNE_CONV_TILE); }
+int tile_id(const TileChoice& c) { return (c.linear == 1 ? c.cfg : c.linear == 0 ? 16 + c.cfg : 64 + c.cfg) + 32 * c.single; }
 
 // In preference order (linear tiles store whole 128-byte pixel runs; larger
 // tiles do more MFMA per decoded weight word), the first tile whose patch fits
 // the LDS and the staging registers and that gives >= 240 blocks; otherwise
 // the feasible tile with the most blocks.
-constexpr TileChoice kMenu[] = {choice<P0>(0, 1), choice<P1>(1, 1), choice<P2>(2, 1), choice<P3>(3, 1),
+constexpr TileChoice kMenu[] = {// stacked linear tiles (stride 1): output runs of whole 4*QT-byte spans
+                                choice<P0>(0, 2), choice<P1>(1, 2), choice<P2>(2, 2), choice<P3>(3, 2),
+                                choice<P7>(7, 2), choice<P8>(8, 2), choice<P9>(9, 2), choice<P11>(11, 2),
+                                choice<P12>(12, 2), choice<P13>(13, 2), choice<P15>(15, 2), choice<P0>(0, 2, 1),
+                                choice<P1>(1, 2, 1), choice<P2>(2, 2, 1), choice<P3>(3, 2, 1),
+                                choice<P0>(0, 1), choice<P1>(1, 1), choice<P2>(2, 1), choice<P3>(3, 1),
                                 choice<P4>(4, 1), choice<P7>(7, 1), choice<P8>(8, 1), choice<P0>(0, 0),
                                 choice<P1>(1, 0), choice<P2>(2, 0), choice<P3>(3, 0), choice<P4>(4, 0),
                                 choice<P5>(5, 0), choice<P6>(6, 0), choice<P7>(7, 0), choice<P8>(8, 0),
@@ -886,6 +997,7 @@ bool two_group_shape(const PatchGeom& g) { return g.chunks == 2 && g.taps == 9 &
 
 bool tile_fits(const PatchGeom& g, const TileChoice& c, PatchGeom& t) {
     if ((c.kg == 2) != two_group_shape(g)) return false;
+    if (c.linear == 2 && !stacked_ok(g, c.BM)) return false;
     t = g;
     fill_patch(t, c);
     const size_t bufs = lds_bytes(t, c.BM, true) - 2 * sizeof(float) * c.BM;
@@ -900,7 +1012,7 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
     int64_t best_blocks = -1;
     const int forced = tile_override();
     for (const auto& c : kMenu) {
-        const int id = (c.linear ? c.cfg : 16 + c.cfg) + 32 * c.single;
+        const int id = tile_id(c);
         if (forced >= 0 && id != forced) continue;
         if (forced < 0) {
             if (g.M <= 32 && c.BM != 32) continue;
@@ -909,7 +1021,7 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
         }
         PatchGeom t;
         if (!tile_fits(g, c, t)) continue;
-        const int64_t blocks = static_cast<int64_t>(t.N) * t.tiles_img * ((g.M + c.BM - 1) / c.BM);
+        const int64_t blocks = patch_tiles(t) * ((g.M + c.BM - 1) / c.BM);
         if (forced >= 0 || blocks >= 240) {
             out = c;
             g = t;
@@ -939,7 +1051,9 @@ int launch_patch_taps(const float* x, const PatchGeom& g, const uint8_t* w, int6
         attr_set = true;
     }
     PatchGeom gl = g;
-    gl.blocks_split = static_cast<int>(static_cast<int64_t>(g.N) * g.tiles_img * ((g.M + Cfg::BM - 1) / Cfg::BM));
+    gl.blocks_split = static_cast<int>(patch_tiles(g) * ((g.M + Cfg::BM - 1) / Cfg::BM));
+    gl.div_split = make_udiv(static_cast<uint32_t>(gl.blocks_split));
+    gl.div_mt = make_udiv(static_cast<uint32_t>((g.M + Cfg::BM - 1) / Cfg::BM));
     const int64_t blocks = static_cast<int64_t>(gl.blocks_split) * g.splits;
     hipLaunchKernelGGL((conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI>), dim3(static_cast<unsigned>(blocks)),
                        dim3(Cfg::NT), lds, s, x, gl, w, col_bytes, m_alloc, epi);
@@ -953,6 +1067,10 @@ int launch_patch_items(const float* x, const PatchGeom& g, const uint8_t* w, int
     const int wper_thread = (Cfg::BM / (TERNARY ? 2 : 4) * g.taps + Cfg::NT - 1) / Cfg::NT;
     if (per_thread > 8 || wper_thread > 4 || (Cfg::KG > 1 && per_thread > 4))
         return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for the staging registers");
+    if constexpr (TAPS > 0) {
+        if (per_thread <= 1) return launch_patch_taps<Cfg, TERNARY, TAPS, 1>(x, g, w, col_bytes, m_alloc, epi, s);
+        if (per_thread <= 2) return launch_patch_taps<Cfg, TERNARY, TAPS, 2>(x, g, w, col_bytes, m_alloc, epi, s);
+    }
     if (per_thread <= 4) return launch_patch_taps<Cfg, TERNARY, TAPS, 4>(x, g, w, col_bytes, m_alloc, epi, s);
     if constexpr (Cfg::KG > 1) return TBN_INVALID_SHAPE;  // not reached (checked above)
     else return launch_patch_taps<Cfg, TERNARY, TAPS, 8>(x, g, w, col_bytes, m_alloc, epi, s);
@@ -1248,7 +1366,7 @@ int conv_patch_dispatch(int weights, const float* x, const tbn_conv2d_desc* desc
     }
     if (rc) return rc;
     // one counter per tile of a split
-    const int64_t tiles = static_cast<int64_t>(g.N) * g.tiles_img * ((g.M + tc.BM - 1) / tc.BM);
+    const int64_t tiles = patch_tiles(g) * ((g.M + tc.BM - 1) / tc.BM);
     if (tiles > tbn_hip::kWorkspaceCounters) e.counters = nullptr;
     rc = weights == TBN_WEIGHTS_TERNARY ? dispatch_patch<true>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, e, s)
                                         : dispatch_patch<false>(tc.cfg, x, g, conv_weights, col_bytes, m_alloc, e, s);
@@ -1379,7 +1497,8 @@ int tbn_hip_conv2d_kernel_name(int weights, const tbn_conv2d_desc* desc, int fla
     if (rc) return rc;
     // the launch's template arguments, as launch_patch / launch_patch_items pick them
     const int taps = (g.kh == 3 && g.kw == 3) ? 9 : 0;
-    const int maxi = (4 * g.PHi * g.PWi + tc.NT - 1) / tc.NT <= 4 ? 4 : 8;
+    const int per_thread = (4 * g.PHi * g.PWi + tc.NT - 1) / tc.NT;
+    const int maxi = taps && per_thread <= 1 ? 1 : taps && per_thread <= 2 ? 2 : per_thread <= 4 ? 4 : 8;
     std::snprintf(name, len, "conv_patch_kernel<PatchCfg<%d, %d, %d, %d, %d, %d>, %s, %d, %d>", tc.BM, tc.TH, tc.TW,
                   tc.WM, tc.WQ, tc.kg, weights == TBN_WEIGHTS_TERNARY ? "true" : "false", taps, maxi);
     return tbn_hip::ok();

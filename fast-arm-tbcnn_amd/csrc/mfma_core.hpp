@@ -183,6 +183,19 @@ inline FastDiv make_fastdiv(uint32_t d) {
     return f;
 }
 
+// n / d for every 0 <= n < 2^31 and d >= 1, without a branch: with
+// m = floor((2^32 - 1) / d), umulhi(n, m) > n/d - n/2^32 > n/d - 1/2, so it is
+// q or q - 1, and the remainder test adds the missing one (d = 1 included).
+struct UDiv {
+    uint32_t m, d;
+};
+inline UDiv make_udiv(uint32_t d) { return UDiv{0xFFFFFFFFu / (d ? d : 1u), d ? d : 1u}; }
+__device__ __forceinline__ int udiv(int n, UDiv v) {
+    uint32_t q = __umulhi(static_cast<uint32_t>(n), v.m);
+    q += (static_cast<uint32_t>(n) - q * v.d) >= v.d ? 1u : 0u;
+    return static_cast<int>(q);
+}
+
 // ---------------------------------------------------------------------------
 // Buffer resources and the split-K finish
 // ---------------------------------------------------------------------------

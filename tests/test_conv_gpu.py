@@ -405,12 +405,21 @@ def test_conv_patch_split_k_residual_and_ternary(dev, orc):
 @pytest.mark.parametrize("case", [(2, 64, 14, 14, 128, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_RELU),
                                   (3, 96, 12, 10, 64, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_MAXPOOL2X2),
                                   (2, 256, 7, 7, 96, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_BIAS_THEN_SCALE),
-                                  (2, 64, 15, 13, 64, 1, 1, (2, 2), (0, 0), (1, 1), 0)])
+                                  (2, 64, 15, 13, 64, 1, 1, (2, 2), (0, 0), (1, 1), 0),
+                                  # stacked tiles: runs across image boundaries (7x9 images
+                                  # smaller than a tile), dilation with the full zero band,
+                                  # no padding, a 5x5 kernel, a 1x1 kernel, many chunks
+                                  (5, 64, 7, 9, 64, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_RELU),
+                                  (2, 32, 9, 11, 128, 3, 3, (1, 1), (2, 2), (2, 2), 0),
+                                  (3, 32, 10, 10, 64, 3, 3, (1, 1), (0, 0), (1, 1), tbn_hip.EPI_RELU),
+                                  (2, 32, 11, 12, 64, 5, 5, (1, 1), (2, 1), (1, 1), 0),
+                                  (3, 96, 6, 13, 128, 1, 1, (1, 1), (0, 0), (1, 1), tbn_hip.EPI_RELU),
+                                  (2, 256, 14, 14, 128, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_BIAS_THEN_SCALE)])
 def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
-    """Each tile of the menu (forced with the conv-tile control: linear and 2-D tiles,
-    with two LDS buffers or one) sums every output in the same order, so all
-    feasible tiles give bit-identical outputs; one of them is checked against
-    the float64 oracle."""
+    """Each tile of the menu (forced with the conv-tile control: linear, 2-D
+    and stacked tiles, with two LDS buffers or one) sums every output in the
+    same order, so all feasible tiles give bit-identical outputs; one of them
+    is checked against the float64 oracle."""
     N, C, H, W, M, kh, kw, stride, pad, dil, flags = case
     rng = np.random.default_rng(C * 17 + M)
     x = rng.standard_normal((N, C, H, W)).astype(np.float32)
@@ -429,7 +438,7 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
     tbn_hip.call("tbn_hip_pack_conv_weights", tbn_hip.WEIGHTS_BINARY, P(packed), K_pad, N_pad, d, P(cw), None)
     dx, ds, db = to_dev(x), to_dev(scale), to_dev(bias)
     outs = {}
-    for tile in range(64):
+    for tile in range(128):
         with tbn_hip.tuning(tbn_hip.TUNE_CONV_TILE, tile):
             y = empty(oshape, torch.float32)
             y.fill_(np.nan)
@@ -443,7 +452,9 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
     two_groups = (C + 31) // 32 == 2 and kh * kw == 9  # two K groups of waves: no one-buffer tiles
     assert len(outs) >= 2, sorted(outs)
     if not two_groups:
-        assert any(t >= 32 for t in outs) and any(t < 32 for t in outs), sorted(outs)
+        assert any(32 <= t < 64 or t >= 96 for t in outs) and any(t < 32 or 64 <= t < 96 for t in outs), sorted(outs)
+    stacked = stride == (1, 1) and C % 32 == 0 and M % 64 == 0 and not flags & tbn_hip.EPI_MAXPOOL2X2
+    assert any(t >= 64 for t in outs) == stacked, sorted(outs)
     first = next(iter(outs.values()))
     for tile, y in outs.items():
         assert np.array_equal(y, first), f"tile {tile} differs"
