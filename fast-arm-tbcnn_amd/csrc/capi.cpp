@@ -168,6 +168,21 @@ int check_launch(const char* what) {
     return fail(TBN_RUNTIME_ERROR, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+int cu_count() {
+    static std::mutex mu;
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!cached[dev]) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        cached[dev] = cus;
+    }
+    return cached[dev];
+}
+
 }  // namespace tbn_hip
 
 extern "C" {

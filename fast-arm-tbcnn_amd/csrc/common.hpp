@@ -35,6 +35,10 @@ void release_workspace(void* ptr, bool temporary, hipStream_t s);
 // Current value of a tuning control (TBN_TUNE_*), the environment read once.
 int tuning(int option);
 
+// Compute units of the current device (cached per device; 256 if the query
+// fails).
+int cu_count();
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 }  // namespace tbn_hip

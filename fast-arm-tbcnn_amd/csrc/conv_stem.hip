@@ -418,21 +418,6 @@ __global__ void __launch_bounds__(64 * kWaves) stem_conv_kernel(const float* __r
     }
 }
 
-int stem_cu_count() {
-    static std::mutex mu;
-    static int cached[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    std::lock_guard<std::mutex> lock(mu);
-    if (!cached[dev]) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-        cached[dev] = cus;
-    }
-    return cached[dev];
-}
-
 using Stem7x7 = StemShape<3, 7, 7, 2, 2, 4, 16>;  // the ResNet stem: 4 x 16 conv pixels per wave
 using Stem7x7Pool = StemShape<3, 7, 7, 2, 2, 2 * kPoolTH + 1, 2 * kPoolTW + 1>;  // with the 3x3/2 pool
 static_assert(Stem7x7Pool::WBUF >= kTWords, "the pool's staging table fits the wave's buffer");
@@ -490,7 +475,7 @@ int launch_stem(const float* x, const StemGeom& g, const float* w, const float* 
         if (e != hipSuccess) return fail(TBN_RUNTIME_ERROR, std::string("hipFuncSetAttribute: ") + hipGetErrorString(e));
         attr_set = true;
     }
-    const int blocks = static_cast<int>(std::min<int64_t>(ceil_div(g.tiles, kWaves), stem_cu_count()));
+    const int blocks = static_cast<int>(std::min<int64_t>(ceil_div(g.tiles, kWaves), tbn_hip::cu_count()));
     hipLaunchKernelGGL((stem_conv_kernel<S, POOL>), dim3(blocks), dim3(64 * kWaves), S::LDS, s, x, g, w, bias, y);
     return check_launch(POOL ? "conv2d_f32 (stem + 3x3/2 max pool)" : "conv2d_f32 (stem)");
 }
