@@ -72,6 +72,12 @@ struct PatchGeom {
     // split-K over blocks: split s takes chunks [s * cps, min(chunks, (s + 1) * cps))
     // and writes raw sums; blocks_split = blocks of one split
     int splits, cps, blocks_split;
+    // the summation order is fixed by the shape: the chunks form groups of
+    // gchunks, each summed from zero, the group sums added in group order.
+    // Split-K runs one group per block; fold (splits == 1, groups > 1) runs
+    // all groups in one block and adds their sums in the same order, so both
+    // give the same bits and the batch may choose between them.
+    int gchunks, fold;
     // 1: one LDS buffer (the next chunk waits in the staging registers and is
     // stored after a barrier), for twice the blocks per CU; 0: two buffers
     int single;
@@ -217,7 +223,7 @@ __host__ __device__ inline int patch_buffer_elems(int patch, int words, int word
 // patch items a thread stages per chunk (4 or 8, the launch picks the smaller
 // that fits): the staging registers live through the whole K loop, and 8
 // items (64 VGPRs) would cost a wave per SIMD on shapes that need 2.
-template <class Cfg, bool TERNARY, int TAPS, int MAXI>
+template <class Cfg, bool TERNARY, int TAPS, int MAXI, bool FOLD = false>
 __global__ void __launch_bounds__(Cfg::NT)
 conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __restrict__ wbits, int64_t col_bytes,
                   int m_alloc, PatchEpi epi) {
@@ -451,6 +457,13 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     const int kg = lane >> 5;
     uint32_t ones;
     asm volatile("v_mov_b32 %0, 0x3f803f80" : "=v"(ones));
+    // FOLD: the sums of the finished chunk groups
+    f32x16_t hold[FOLD ? Cfg::FR : 1][FOLD ? Cfg::FC : 1];
+    bool held = false;
+    int in_group = 0;
+    (void)hold;
+    (void)held;
+    (void)in_group;
     // patch offset of tap (r, s): (r*dh*PWi + s*dw) * kPix
     const int tap_ds = g.dw * kPix;
     const int tap_dr = g.dh * g.PWi * kPix;
@@ -555,12 +568,38 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                 s = next_s;
             }
         }
+        if constexpr (FOLD) {
+            // a group ends: its sum joins the earlier groups' (in group order)
+            if (++in_group == g.gchunks && ch + 1 < ce) {
+                in_group = 0;
+#pragma unroll
+                for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+                    for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            hold[f][j][e] = held ? hold[f][j][e] + acc[f][j][e] : acc[f][j][e];
+                            acc[f][j][e] = 0.0f;
+                        }
+                held = true;
+            }
+        }
         if (Cfg::KG == 1 && ch + 1 < ce) {
             if (g.single) __syncthreads();  // every wave is done reading the buffer
             store_chunk(g.single ? 0 : (ch + 1 - cb) & 1, stage, wstage);
             if (ch + 2 < ce) load_chunk(ch + 2, stage, wstage);
         }
         __syncthreads();
+    }
+    if constexpr (FOLD) {
+        if (held) {
+#pragma unroll
+            for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+                for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) acc[f][j][e] = hold[f][j][e] + acc[f][j][e];
+        }
     }
     if constexpr (Cfg::KG > 1) {
         // group 1 hands its sums to group 0 through the (now free) patch
@@ -1386,6 +1425,14 @@ PipeGrid pipe_grid(const PatchGeom& g, int BM) {
 
 bool tile_fits(const PatchGeom& g, const TileChoice& c, PatchGeom& t) {
     if ((c.kg == 2) != two_group_shape(g)) return false;
+    if (g.fold) {
+        // the folded K loop: 3x3 taps, one K group, at most two staging items
+        if (c.pipe || c.kg != 1 || g.taps != 9) return false;
+        t = g;
+        fill_patch(t, c);
+        return lds_bytes(t, c.BM, true) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= 2 * c.NT &&
+               c.BM * t.taps <= 8 * c.NT;
+    }
     if (c.pipe) {
         // both chunks of a tile's patch staged by 256 helper threads, at most
         // four items each; no fused pool, no K split (two_group_shape)
@@ -1437,13 +1484,13 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
     return true;
 }
 
-template <class Cfg, bool TERNARY, int TAPS, int MAXI>
+template <class Cfg, bool TERNARY, int TAPS, int MAXI, bool FOLD = false>
 int launch_patch_taps(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
                       const PatchEpi& epi, hipStream_t s) {
     const size_t lds = lds_bytes(g, Cfg::BM, TERNARY);
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI, FOLD>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
         if (e != hipSuccess) return tbn_hip::fail(TBN_RUNTIME_ERROR, std::string("hipFuncSetAttribute: ") +
                                                                          hipGetErrorString(e));
@@ -1454,7 +1501,7 @@ int launch_patch_taps(const float* x, const PatchGeom& g, const uint8_t* w, int6
     gl.div_split = make_udiv(static_cast<uint32_t>(gl.blocks_split));
     gl.div_mt = make_udiv(static_cast<uint32_t>((g.M + Cfg::BM - 1) / Cfg::BM));
     const int64_t blocks = static_cast<int64_t>(gl.blocks_split) * g.splits;
-    hipLaunchKernelGGL((conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI, FOLD>), dim3(static_cast<unsigned>(blocks)),
                        dim3(Cfg::NT), lds, s, x, gl, w, col_bytes, m_alloc, epi);
     return tbn_hip::check_launch(TERNARY ? "conv2d_f32_ternary (patch)" : "conv2d_f32_binary (patch)");
 }
@@ -1466,6 +1513,14 @@ int launch_patch_items(const float* x, const PatchGeom& g, const uint8_t* w, int
     const int wper_thread = (Cfg::BM / (TERNARY ? 2 : 4) * g.taps + Cfg::NT - 1) / Cfg::NT;
     if (per_thread > 8 || wper_thread > 4 || (Cfg::KG > 1 && per_thread > 4))
         return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for the staging registers");
+    if (g.fold) {
+        // all chunk groups in one block (3x3, one K group of waves, small patches)
+        if constexpr (TAPS > 0 && Cfg::KG == 1) {
+            if (per_thread <= 1) return launch_patch_taps<Cfg, TERNARY, TAPS, 1, true>(x, g, w, col_bytes, m_alloc, epi, s);
+            if (per_thread <= 2) return launch_patch_taps<Cfg, TERNARY, TAPS, 2, true>(x, g, w, col_bytes, m_alloc, epi, s);
+        }
+        return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for a folded K loop");
+    }
     if constexpr (TAPS > 0) {
         if (per_thread <= 1) return launch_patch_taps<Cfg, TERNARY, TAPS, 1>(x, g, w, col_bytes, m_alloc, epi, s);
         if (per_thread <= 2) return launch_patch_taps<Cfg, TERNARY, TAPS, 2>(x, g, w, col_bytes, m_alloc, epi, s);
@@ -1714,10 +1769,27 @@ int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
     }
     // a forced count (TBN_TUNE_CONV_SPLITS) applies to unpooled convs only:
     // the split partials hold unpooled planes
-    if (!g.pool && tbn_hip::tuning(TBN_TUNE_CONV_SPLITS) > 0) splits = tbn_hip::tuning(TBN_TUNE_CONV_SPLITS);
+    const bool forced = !g.pool && tbn_hip::tuning(TBN_TUNE_CONV_SPLITS) > 0;
+    if (forced) splits = tbn_hip::tuning(TBN_TUNE_CONV_SPLITS);
     g.single = 0;
-    g.cps = (g.chunks + splits - 1) / splits;
-    g.splits = (g.chunks + g.cps - 1) / g.cps;
+    g.pipe = 0;
+    g.gchunks = (g.chunks + splits - 1) / splits;
+    const int groups = (g.chunks + g.gchunks - 1) / g.gchunks;
+    // The batch decides how the groups run: when the unsplit 8 x 8 tiles of
+    // 64 channels already fill the chip, one block runs all groups (fold) and
+    // no partial sums go through memory; else one block per group.  Both sum
+    // in the same order, so a sample's bits do not depend on its batch.
+    const int64_t unsplit = static_cast<int64_t>(g.N) * ((g.OH + 7) / 8) * ((g.OW + 7) / 8) * ((g.M + 63) / 64);
+    g.fold = !forced && groups > 1 && g.taps == 9 && unsplit >= 256 ? 1 : 0;
+    if (g.fold) {
+        PatchGeom t = g;
+        t.cps = g.chunks;
+        t.splits = 1;
+        TileChoice c;
+        if (!choose_tile(t, c)) g.fold = 0;  // no tile takes the folded loop: split instead
+    }
+    g.cps = g.fold ? g.chunks : g.gchunks;
+    g.splits = g.fold ? 1 : groups;
     g.blocks_split = 0;
     return TBN_SUCCESS;
 }
@@ -1956,8 +2028,9 @@ int tbn_hip_conv2d_kernel_name(int weights, const tbn_conv2d_desc* desc, int fla
     const int taps = (g.kh == 3 && g.kw == 3) ? 9 : 0;
     const int per_thread = (4 * g.PHi * g.PWi + tc.NT - 1) / tc.NT;
     const int maxi = taps && per_thread <= 1 ? 1 : taps && per_thread <= 2 ? 2 : per_thread <= 4 ? 4 : 8;
-    std::snprintf(name, len, "conv_patch_kernel<PatchCfg<%d, %d, %d, %d, %d, %d>, %s, %d, %d>", tc.BM, tc.TH, tc.TW,
-                  tc.WM, tc.WQ, tc.kg, weights == TBN_WEIGHTS_TERNARY ? "true" : "false", taps, maxi);
+    std::snprintf(name, len, "conv_patch_kernel<PatchCfg<%d, %d, %d, %d, %d, %d>, %s, %d, %d, %s>", tc.BM, tc.TH,
+                  tc.TW, tc.WM, tc.WQ, tc.kg, weights == TBN_WEIGHTS_TERNARY ? "true" : "false", taps, maxi,
+                  g.fold ? "true" : "false");
     return tbn_hip::ok();
 }
 

@@ -546,6 +546,65 @@ def test_conv_pipelined_matches_patch_kernel(dev, case):
     rm.assert_within_tolerance(want, ref, K, np.abs(x).max() * 1.5)
 
 
+@pytest.mark.parametrize("case", [(32, 512, 7, 7, 512, False, True), (128, 256, 7, 7, 128, True, True),
+                                  (128, 300, 7, 6, 96, False, False)], ids=["stage4", "ternary_res", "ragged"])
+def test_conv_folded_groups_match_split_k(dev, case):
+    """Deep layers sum their chunks in groups whose order the shape fixes.
+    With enough images the groups run in one block (folded), with few they
+    run split over blocks: every image gets the same bits at batch N as at
+    batch 2, and the same bits as the forced split of the same batch."""
+    import ctypes
+    N, C, H, W, M, ternary, with_res = case
+    rng = np.random.default_rng(C + M + H)
+    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
+    scale = rng.uniform(0.5, 1.5, M).astype(np.float32)
+    bias = (rng.standard_normal(M) * 0.01).astype(np.float32)
+    res = rng.standard_normal((N, M, H, W)).astype(np.float32) if with_res else None
+    K = C * 9
+    if ternary:
+        kind = tbn_hip.WEIGHTS_TERNARY
+        wt = rng.integers(-1, 2, (M, K)).astype(np.int8)
+        K_pad, N_pad = (K + 31) // 32 * 32, M
+        packed = empty(M * K_pad // 4, torch.uint8)
+        tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(wt)), K, M, tbn_hip.LAYOUT_NK, K_pad, M, P(packed), None)
+        wref = wt.reshape(M, C, 3, 3).astype(np.float32)
+    else:
+        kind = tbn_hip.WEIGHTS_BINARY
+        wbytes = (rng.random((M, C, 3, 3)) < 0.5).astype(np.uint8)
+        packed, K_pad, N_pad = pack_conv_weights(wbytes, M, K)
+        wref = np.where(wbytes == 1, 1.0, -1.0).astype(np.float32)
+
+    def run(n):
+        d = tbn_hip.conv_desc(n, C, H, W, M, 3, 3, 1, 1, 1, 1)
+        wb = ctypes.c_int64()
+        tbn_hip.call("tbn_hip_conv_weights_bytes", kind, d, ctypes.byref(wb))
+        cw = empty(wb.value, torch.uint8)
+        tbn_hip.call("tbn_hip_pack_conv_weights", kind, P(packed), K_pad, N_pad, d, P(cw), None)
+        y = empty((n, M, H, W), torch.float32)
+        y.fill_(np.nan)
+        dr = to_dev(res[:n]) if with_res else None
+        tbn_hip.call("tbn_hip_conv2d_f32_prepacked", kind, P(to_dev(x[:n])), d, P(cw), P(to_dev(scale)), 1.0,
+                     P(to_dev(bias)), P(dr) if with_res else None, tbn_hip.EPI_RELU, P(y), None)
+        name = ctypes.create_string_buffer(200)
+        tbn_hip.call("tbn_hip_conv2d_kernel_name", kind, d, tbn_hip.EPI_RELU, int(with_res), name, 200)
+        return host(y), name.value.decode()
+
+    big, big_name = run(N)
+    small, small_name = run(2)
+    assert big_name.endswith(", true>"), big_name       # folded: one block runs every group
+    assert small_name.endswith(", false>"), small_name  # split over blocks
+    assert np.array_equal(big[:2], small)
+    with tbn_hip.tuning(tbn_hip.TUNE_CONV_SPLITS, 2):
+        forced, _ = run(N)
+    if C // 32 * 9 // 2 >= 36 and M * H * W * 2 <= 1 << 16:  # the rule's own split is 2 here
+        assert np.array_equal(big, forced)
+    ref = conv_ref(x, wref, scale, 1.0, bias, (1, 1), (1, 1), (1, 1), 0)
+    if with_res:
+        ref = ref + res
+    ref = np.maximum(ref, 0.0)
+    rm.assert_within_tolerance(big, ref, K, np.abs(x).max() * 1.5)
+
+
 def _prepacked_setup(case, seed):
     import ctypes
     N, C, H, W, M, kh, kw, stride, pad, dil, flags = case

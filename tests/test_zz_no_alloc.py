@@ -81,13 +81,17 @@ def test_noalloc_conv_matches_allocating_entry_point(dev):
 
 
 def test_noalloc_conv_rejects_oversize_scratch(dev):
-    # 256 images x 512 x 7 x 7 with 2 K splits: 51 MB of partial sums > 16 MiB
+    # 256 images x 512 x 7 x 7 with 2 K splits forced (the batch alone would
+    # run its chunk groups in one block, with no partial sums): 51 MB of
+    # partial sums > 16 MiB
     d = tbn_hip.conv_desc(256, 512, 7, 7, 512, 3, 3, 1, 1, 1, 1)
     x = empty((256, 512, 7, 7), torch.float32)
     y = empty((256, 512, 7, 7), torch.float32)
     K_pad, N_pad = tbn_hip.padded_dims(512 * 9, 512)
     packed = empty(N_pad * K_pad // 8, torch.uint8)
-    rc = tbn_hip.lib().tbn_hip_conv2d_f32_quantized_noalloc(tbn_hip.WEIGHTS_BINARY, P(x), d, P(packed), K_pad, N_pad,
-                                                            None, 1.0, None, None, 0, P(y), None)
+    with tbn_hip.tuning(tbn_hip.TUNE_CONV_SPLITS, 2):
+        rc = tbn_hip.lib().tbn_hip_conv2d_f32_quantized_noalloc(tbn_hip.WEIGHTS_BINARY, P(x), d, P(packed), K_pad,
+                                                                N_pad, None, 1.0, None, None, 0, P(y), None)
+        msg = tbn_hip.last_error()  # before the control's reset clears it
     assert rc == tbn_hip.INVALID_SHAPE
-    assert "scratch" in tbn_hip.last_error()
+    assert "scratch" in msg
