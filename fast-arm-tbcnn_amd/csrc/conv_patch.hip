@@ -437,21 +437,33 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    // K groups: both chunks' loads in flight before the first is stored
-    // (host-checked: exactly two chunks, KG = 2)
+    // KG = 2: K group k sums the cpg chunks [cb + k * cpg, cb + (k + 1) * cpg)
+    // from zero (host-checked: the block's range is two equal runs, each one
+    // chunk group: a two-chunk layer, or a folded pair of groups).  Every
+    // thread stages both runs, run k's chunk i into buffer k + 2 (i & 1), so
+    // the groups advance together between the block's barriers.
+    const int cpg = (ce - cb) / Cfg::KG;
+    const int nbuf = g.single ? 1 : (Cfg::KG > 1 && cpg > 1 ? 4 : 2);
     Stage stage2;
     WStage wstage2;
     load_chunk(cb, stage, wstage);
-    if constexpr (Cfg::KG > 1) load_chunk(cb + 1, stage2, wstage2);
+    if constexpr (Cfg::KG > 1) load_chunk(cb + cpg, stage2, wstage2);
     store_chunk(0, stage, wstage);
     // [BM] multipliers, [BM] addends after the buffer(s)
-    float* epi_lds = reinterpret_cast<float*>(lds + (g.single ? 1 : 2) * buf_elems);
+    float* epi_lds = reinterpret_cast<float*>(lds + nbuf * buf_elems);
     if (tid < Cfg::BM) {
         epi_lds[tid] = epi.alpha * (epi.scale ? raw_scale : 1.0f);
         epi_lds[Cfg::BM + tid] = raw_bias;
     }
-    if constexpr (Cfg::KG > 1) store_chunk(1, stage2, wstage2);
-    else if (cb + 1 < ce) load_chunk(cb + 1, stage, wstage);
+    if constexpr (Cfg::KG > 1) {
+        store_chunk(1, stage2, wstage2);
+        if (cpg > 1) {
+            load_chunk(cb + 1, stage, wstage);
+            load_chunk(cb + cpg + 1, stage2, wstage2);
+        }
+    } else if (cb + 1 < ce) {
+        load_chunk(cb + 1, stage, wstage);
+    }
     __syncthreads();
 
     const int kg = lane >> 5;
@@ -467,8 +479,9 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     // patch offset of tap (r, s): (r*dh*PWi + s*dw) * kPix
     const int tap_ds = g.dw * kPix;
     const int tap_dr = g.dh * g.PWi * kPix;
-    for (int ch = cb + kgrp; ch < ce; ch += Cfg::KG) {
-        const uint16_t* cur = lds + (g.single ? 0 : ((ch - cb) & 1)) * buf_elems;
+    for (int i = 0; i < cpg; ++i) {
+        const int ch = cb + kgrp * cpg + i;
+        const uint16_t* cur = lds + (g.single ? 0 : Cfg::KG > 1 ? kgrp + 2 * (i & 1) : (i & 1)) * buf_elems;
         auto read_b = [&](int toff, int kk, u32x4_t (&b)[3][Cfg::FC]) {
 #pragma unroll
             for (int p = 0; p < 3; ++p)
@@ -568,7 +581,7 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                 s = next_s;
             }
         }
-        if constexpr (FOLD) {
+        if constexpr (FOLD && Cfg::KG == 1) {
             // a group ends: its sum joins the earlier groups' (in group order)
             if (++in_group == g.gchunks && ch + 1 < ce) {
                 in_group = 0;
@@ -588,6 +601,15 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
             if (g.single) __syncthreads();  // every wave is done reading the buffer
             store_chunk(g.single ? 0 : (ch + 1 - cb) & 1, stage, wstage);
             if (ch + 2 < ce) load_chunk(ch + 2, stage, wstage);
+        }
+        if (Cfg::KG > 1 && i + 1 < cpg) {
+            // both runs' next chunks into the buffers read one step ago
+            store_chunk(2 * ((i + 1) & 1), stage, wstage);
+            store_chunk(1 + 2 * ((i + 1) & 1), stage2, wstage2);
+            if (i + 2 < cpg) {
+                load_chunk(cb + i + 2, stage, wstage);
+                load_chunk(cb + cpg + i + 2, stage2, wstage2);
+            }
         }
         __syncthreads();
     }
@@ -1236,12 +1258,14 @@ struct TileChoice {
     int pipe;    // 1: conv_pipe_kernel (cfg indexes the PipeCfg menu)
 };
 
-size_t lds_bytes(const PatchGeom& g, int BM, bool ternary) {
+size_t lds_bytes(const PatchGeom& g, int BM, bool ternary, int kg = 1) {
     if (g.pipe)  // two patch buffers, two hand-over buffers, epilogue factors
         return 2 * static_cast<size_t>(pipe_buffer_elems(g.PHi * g.PWi)) * 2 + 2 * kPipeAccFloats * sizeof(float) +
                2 * sizeof(float) * BM;
     const size_t buf = static_cast<size_t>(patch_buffer_elems(g.PHi * g.PWi, BM * g.taps, ternary ? 4 : 2)) * 2;
-    return (g.single ? 1 : 2) * buf + 2 * sizeof(float) * BM;  // buffer(s) + epilogue factors
+    // two K groups over runs of more than one chunk: two buffers per run
+    const int nbuf = g.single ? 1 : (kg > 1 && g.cps > kg ? 4 : 2);
+    return nbuf * buf + 2 * sizeof(float) * BM;  // buffer(s) + epilogue factors
 }
 
 // Tiles of one launch (per split): stacked tiles cover the whole batch.
@@ -1424,15 +1448,21 @@ PipeGrid pipe_grid(const PatchGeom& g, int BM) {
 }
 
 bool tile_fits(const PatchGeom& g, const TileChoice& c, PatchGeom& t) {
-    if ((c.kg == 2) != two_group_shape(g)) return false;
     if (g.fold) {
-        // the folded K loop: 3x3 taps, one K group, at most two staging items
-        if (c.pipe || c.kg != 1 || g.taps != 9) return false;
+        // the folded K loop: 3x3 taps, at most two staging items; one K group
+        // summing the groups in turn, or (exactly two equal groups) two K
+        // groups of waves, one per group, whose sums are added in group order
+        const bool pair = g.chunks == 2 * g.gchunks;
+        if (c.pipe || g.taps != 9 || (c.kg != 1 && !(c.kg == 2 && pair))) return false;
+        if (c.linear == 2 && !stacked_ok(g, c.BM)) return false;
         t = g;
         fill_patch(t, c);
-        return lds_bytes(t, c.BM, true) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= 2 * c.NT &&
-               c.BM * t.taps <= 8 * c.NT;
+        const size_t bufs = lds_bytes(t, c.BM, true, c.kg) - 2 * sizeof(float) * c.BM;
+        const bool red_fits = c.kg == 1 || static_cast<size_t>(c.BM) * c.TH * c.TW * 4 <= bufs;
+        return lds_bytes(t, c.BM, true, c.kg) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= 2 * c.NT &&
+               c.BM * t.taps <= 8 * c.NT && red_fits && !c.single;
     }
+    if ((c.kg == 2) != two_group_shape(g)) return false;
     if (c.pipe) {
         // both chunks of a tile's patch staged by 256 helper threads, at most
         // four items each; no fused pool, no K split (two_group_shape)
@@ -1445,10 +1475,10 @@ bool tile_fits(const PatchGeom& g, const TileChoice& c, PatchGeom& t) {
     if (c.linear == 2 && !stacked_ok(g, c.BM)) return false;
     t = g;
     fill_patch(t, c);
-    const size_t bufs = lds_bytes(t, c.BM, true) - 2 * sizeof(float) * c.BM;
+    const size_t bufs = lds_bytes(t, c.BM, true, c.kg) - 2 * sizeof(float) * c.BM;
     const bool red_fits = c.kg == 1 || static_cast<size_t>(c.BM) * c.TH * c.TW * 4 <= bufs;
     const int stage_items = c.kg == 1 ? 8 : 4;  // staging registers per thread (MAXI)
-    return lds_bytes(t, c.BM, true) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= stage_items * c.NT &&
+    return lds_bytes(t, c.BM, true, c.kg) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= stage_items * c.NT &&
            c.BM * t.taps <= 8 * c.NT && red_fits && (c.kg == 1 || !c.single);
 }
 
@@ -1487,7 +1517,7 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
 template <class Cfg, bool TERNARY, int TAPS, int MAXI, bool FOLD = false>
 int launch_patch_taps(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
                       const PatchEpi& epi, hipStream_t s) {
-    const size_t lds = lds_bytes(g, Cfg::BM, TERNARY);
+    const size_t lds = lds_bytes(g, Cfg::BM, TERNARY, Cfg::KG);
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI, FOLD>),
@@ -1514,8 +1544,9 @@ int launch_patch_items(const float* x, const PatchGeom& g, const uint8_t* w, int
     if (per_thread > 8 || wper_thread > 4 || (Cfg::KG > 1 && per_thread > 4))
         return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for the staging registers");
     if (g.fold) {
-        // all chunk groups in one block (3x3, one K group of waves, small patches)
-        if constexpr (TAPS > 0 && Cfg::KG == 1) {
+        // all chunk groups in one block (3x3, small patches): one K group of
+        // waves taking the groups in turn, or two taking one group each
+        if constexpr (TAPS > 0) {
             if (per_thread <= 1) return launch_patch_taps<Cfg, TERNARY, TAPS, 1, true>(x, g, w, col_bytes, m_alloc, epi, s);
             if (per_thread <= 2) return launch_patch_taps<Cfg, TERNARY, TAPS, 2, true>(x, g, w, col_bytes, m_alloc, epi, s);
         }

@@ -4,6 +4,8 @@ Reference semantics (mode F32): the reference's fp32 conv2d (conv2d.cpp:78-192)
 applied to the dequantized weights s[m]*sign(w), i.e. y = s*acc + b
 (conv2d_binary_with_scales order, conv2d.cpp:319-369), then ReLU / MaxPool.
 Tolerance: rel-L2 <= 1e-5, max-abs <= 1e-4*sqrt(K)*max|x|*max|s|."""
+import re
+
 import numpy as np
 import pytest
 import torch
@@ -598,6 +600,19 @@ def test_conv_folded_groups_match_split_k(dev, case):
         forced, _ = run(N)
     if C // 32 * 9 // 2 >= 36 and M * H * W * 2 <= 1 << 16:  # the rule's own split is 2 here
         assert np.array_equal(big, forced)
+        # every tile gives these bits, folded or split; two equal chunk groups
+        # also run on tiles with two K groups of waves, one group each
+        pair = re.compile(r"PatchCfg<\d+, \d+, \d+, \d+, \d+, 2>, (true|false), 9, \d, true>$")
+        pairs = 0
+        for tile in range(128):
+            with tbn_hip.tuning(tbn_hip.TUNE_CONV_TILE, tile):
+                try:
+                    y_t, name_t = run(N)
+                except tbn_hip.TbnError:
+                    continue
+            assert np.array_equal(y_t, big), (tile, name_t)
+            pairs += bool(pair.search(name_t))
+        assert pairs >= 1
     ref = conv_ref(x, wref, scale, 1.0, bias, (1, 1), (1, 1), (1, 1), 0)
     if with_res:
         ref = ref + res
