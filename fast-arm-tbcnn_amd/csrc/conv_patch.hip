@@ -87,6 +87,9 @@ struct PatchGeom {
     // disjoint LDS banks
     int rowperm;
     int pipe;  // 1: laid out for conv_pipe_kernel (2-D tiles, both chunks per buffer)
+    // 1: the launch also computes the 1x1 projection of the same input from
+    // the centre tap (conv_patch_kernel<..., PROJ = true>)
+    int proj;
 };
 
 // Buffer resource (gfx9 word 3: raw dword addressing) over `bytes` from base;
@@ -209,6 +212,14 @@ struct PatchEpi {
     // split-K with tile counters (zero on entry, left zero): the last block of
     // each tile adds the splits and runs the epilogue; null: a reduce kernel does
     int* counters;
+    // the fused 1x1 projection (PROJ): its conv-layout words [chunk][m], its
+    // output (the conv's shape) and epilogue (scale, alpha, bias, flags)
+    const uint8_t* proj_w;
+    float* proj_y;
+    const float* proj_scale;
+    float proj_alpha;
+    const float* proj_bias;
+    int proj_flags;
 };
 
 // bf16 elements of one LDS buffer: three planes of patch + 1 pixel records
@@ -223,7 +234,14 @@ __host__ __device__ inline int patch_buffer_elems(int patch, int words, int word
 // patch items a thread stages per chunk (4 or 8, the launch picks the smaller
 // that fits): the staging registers live through the whole K loop, and 8
 // items (64 VGPRs) would cost a wave per SIMD on shapes that need 2.
-template <class Cfg, bool TERNARY, int TAPS, int MAXI, bool FOLD = false>
+// PROJ (3x3 taps, pad 1, one K split; host-checked): the launch also computes
+// the 1x1 stride-s pad-0 projection of the same input, whose pixel is the 3x3
+// window's centre: its K steps are the centre tap's pixel fragments times
+// its own weight words (a table after the conv's in each chunk buffer),
+// summed chunk after chunk, k-slice after k-slice, hi / mid / lo, as the 1x1
+// conv sums them alone, so both give the same bits.  One K group of waves
+// only: two groups would split the chunks between them.
+template <class Cfg, bool TERNARY, int TAPS, int MAXI, bool FOLD = false, bool PROJ = false>
 __global__ void __launch_bounds__(Cfg::NT)
 conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __restrict__ wbits, int64_t col_bytes,
                   int m_alloc, PatchEpi epi) {
@@ -235,7 +253,9 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     const int patch = g.PHi * g.PWi;
     const int plane_elems = (patch + 1) * kPix;
     const int wofs = 3 * plane_elems;                  // weight words after the planes
-    const int buf_elems = patch_buffer_elems(patch, Cfg::BM * g.taps, kWordHalves);
+    // PROJ: the projection's BM words after the conv's table and its spare
+    const int pofs = patch_buffer_elems(patch, Cfg::BM * g.taps, kWordHalves);
+    const int buf_elems = pofs + (PROJ ? Cfg::BM * kWordHalves : 0);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -373,9 +393,19 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     // other kernels stage per_thread / wper_thread items.
     constexpr bool kAll = TAPS > 0;
     using Stage = float[kMaxItems][8];
-    using WStage = u32x4_t[kMaxWItems];
+    // PROJ: one more 16-byte item, the projection words of kWPI channels
+    // (threads below kGroupsM; a row past m_alloc loads 0)
+    using WStage = u32x4_t[kMaxWItems + (PROJ ? 1 : 0)];
     Stage stage;
     WStage wstage;
+    const uint32_t pchunk = static_cast<uint32_t>(m_alloc) * kWordBytes;  // projection words per chunk
+    const __amdgpu_buffer_rsrc_t p_rs =
+        make_rsrc(PROJ ? epi.proj_w : nullptr, PROJ ? static_cast<uint64_t>(pchunk) * g.chunks : 0);
+    const uint32_t poff = tid < kGroupsM && m0 + tid * kWPI < m_alloc
+                              ? static_cast<uint32_t>(m0 + tid * kWPI) * kWordBytes
+                              : kOutside;
+    (void)p_rs;
+    (void)poff;
 
     auto load_chunk = [&](int ch, Stage& st_, WStage& wst_) {
         const uint32_t cofs = static_cast<uint32_t>(ch * kChunk) * HW4;
@@ -396,6 +426,9 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                                               __builtin_amdgcn_raw_buffer_load_b128(w_rs, woff[it] + wofs_ch, 0, 0));
             }
         }
+        if constexpr (PROJ)
+            wst_[kMaxWItems] = __builtin_bit_cast(
+                u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(p_rs, poff + static_cast<uint32_t>(ch) * pchunk, 0, 0));
     };
     auto store_chunk = [&](int b, Stage& st_, WStage& wst_) {
         uint16_t* dst = lds + b * buf_elems;
@@ -415,6 +448,9 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
             if (kAll || it < wper_thread) {
                 *reinterpret_cast<u32x4_t*>(dst + wofs + wslot[it]) = wst_[it];
             }
+        }
+        if constexpr (PROJ) {
+            if (tid < kGroupsM) *reinterpret_cast<u32x4_t*>(dst + pofs + tid * kWPI * kWordHalves) = wst_[kMaxWItems];
         }
     };
 
@@ -436,6 +472,18 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
         for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+    // PROJ: the projection's sums (one K group of waves, host-checked)
+    f32x16_t accp[PROJ ? Cfg::FR : 1][PROJ ? Cfg::FC : 1];
+    static_assert(!PROJ || Cfg::KG == 1, "a fused projection runs on one K group");
+    if constexpr (PROJ) {
+#pragma unroll
+        for (int i = 0; i < Cfg::FR; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) accp[i][j][e] = 0.0f;
+    }
+    (void)accp;
 
     // KG = 2: K group k sums the cpg chunks [cb + k * cpg, cb + (k + 1) * cpg)
     // from zero (host-checked: the block's range is two equal runs, each one
@@ -510,6 +558,16 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                     if (TERNARY) wr[f][tap] = *reinterpret_cast<const uint2*>(src);
                     else wr[f][tap] = make_uint2(*reinterpret_cast<const uint32_t*>(src), 0u);
                 }
+            uint2 pwr[PROJ ? Cfg::FR : 1];
+            if constexpr (PROJ) {
+#pragma unroll
+                for (int f = 0; f < Cfg::FR; ++f) {
+                    const uint16_t* src = cur + pofs + (wrow + f * 32) * kWordHalves;
+                    if (TERNARY) pwr[f] = *reinterpret_cast<const uint2*>(src);
+                    else pwr[f] = make_uint2(*reinterpret_cast<const uint32_t*>(src), 0u);
+                }
+            }
+            (void)pwr;
             // software pipeline over the 2*TAPS steps (tap, kk): step t+1's
             // pixel fragments are read from LDS and its weight fragments decoded
             // while step t's MFMAs run; the scheduling barriers keep each
@@ -525,6 +583,21 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
                 if (t + 1 < 2 * TAPS) read_b((nt / 3) * tap_dr + (nt % 3) * tap_ds, nk, bnext);
                 __builtin_amdgcn_sched_barrier(0);
                 mfma_step(acur, bcur);
+                if constexpr (PROJ) {
+                    // the centre tap's two k-slices (tap 4 = (1, 1)) are the
+                    // projection's K steps for this chunk
+                    if (t == 8 || t == 9) {
+                        u32x4_t ap[Cfg::FR];
+#pragma unroll
+                        for (int f = 0; f < Cfg::FR; ++f) ap[f] = weight_frag<TERNARY>(pwr[f], t & 1, kg, ones);
+#pragma unroll
+                        for (int p = 0; p < 3; ++p)
+#pragma unroll
+                            for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+                                for (int j = 0; j < Cfg::FC; ++j) accp[f][j] = mfma32(ap[f], bcur[p][j], accp[f][j]);
+                    }
+                }
                 if (t + 1 < 2 * TAPS) {
 #pragma unroll
                     for (int f = 0; f < Cfg::FR; ++f) anext[f] = weight_frag<TERNARY>(wr[f][nt], nk, kg, ones);
@@ -655,6 +728,14 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
             for (int j = 0; j < Cfg::FC; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[f][j][e] *= 0.5f;
+        if constexpr (PROJ) {
+#pragma unroll
+            for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+                for (int j = 0; j < Cfg::FC; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) accp[f][j][e] *= 0.5f;
+        }
     }
 
     // ---- epilogue: scale, bias, residual, ReLU, optional 2x2 max pool ----
@@ -726,6 +807,39 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
         }
         // ready for the next launch on this workspace
         if (tid == 0) __hip_atomic_store(epi.counters + bid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if constexpr (PROJ) {
+        // the projection's epilogue (never pooled, no residual, no split;
+        // host-checked): its factors formed as the conv's are, then
+        // v = (acc + a) * s + b and an optional ReLU, into the same pixels
+        const __amdgpu_buffer_rsrc_t py_rs = make_rsrc(epi.proj_y + obase, obytes);
+        const __amdgpu_buffer_rsrc_t ps_rs =
+            make_rsrc(epi.proj_scale, epi.proj_scale ? static_cast<uint64_t>(g.M) * 4 : 0);
+        const __amdgpu_buffer_rsrc_t pb_rs =
+            make_rsrc(epi.proj_bias, epi.proj_bias ? static_cast<uint64_t>(g.M) * 4 : 0);
+        const bool pbts = (epi.proj_flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
+        const bool prelu = (epi.proj_flags & TBN_EPI_RELU) != 0;
+#pragma unroll
+        for (int f = 0; f < Cfg::FR; ++f)
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {
+                const int r = wm * Cfg::WM + f * 32 + 8 * e4 + 4 * (lane >> 5);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t mo = static_cast<uint32_t>(min(m0 + r + i, g.M - 1)) * 4;
+                    const float sc = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ps_rs, mo, 0, 0));
+                    const float bi = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pb_rs, mo, 0, 0));
+                    const float mm = epi.proj_alpha * (epi.proj_scale ? sc : 1.0f);
+                    const float a = pbts ? bi : 0.0f, b = pbts ? 0.0f : bi;
+#pragma unroll
+                    for (int j = 0; j < Cfg::FC; ++j) {
+                        float v = (accp[f][j][4 * e4 + i] + a) * mm + b;
+                        if (prelu) v = v > 0.0f ? v : 0.0f;
+                        __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), py_rs,
+                                                              voff[j] + (f * 32 + 8 * e4 + i) * plane4, 0, 0);
+                    }
+                }
+            }
     }
     // v' = (v + a) * s + b with (a, b) = (bias, 0) for bias-then-scale, else (0, bias)
     const bool bts = (epi.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
@@ -1262,7 +1376,9 @@ size_t lds_bytes(const PatchGeom& g, int BM, bool ternary, int kg = 1) {
     if (g.pipe)  // two patch buffers, two hand-over buffers, epilogue factors
         return 2 * static_cast<size_t>(pipe_buffer_elems(g.PHi * g.PWi)) * 2 + 2 * kPipeAccFloats * sizeof(float) +
                2 * sizeof(float) * BM;
-    const size_t buf = static_cast<size_t>(patch_buffer_elems(g.PHi * g.PWi, BM * g.taps, ternary ? 4 : 2)) * 2;
+    // (a fused projection's words follow the conv's table)
+    const size_t buf =
+        static_cast<size_t>(patch_buffer_elems(g.PHi * g.PWi, BM * g.taps, ternary ? 4 : 2) + (g.proj ? BM * (ternary ? 4 : 2) : 0)) * 2;
     // two K groups over runs of more than one chunk: two buffers per run
     const int nbuf = g.single ? 1 : (kg > 1 && g.cps > kg ? 4 : 2);
     return nbuf * buf + 2 * sizeof(float) * BM;  // buffer(s) + epilogue factors
@@ -1447,7 +1563,27 @@ PipeGrid pipe_grid(const PatchGeom& g, int BM) {
     return p;
 }
 
+// The tiles built with a fused projection (launch_patch_items): 8 x 8
+// tiles on one K group of waves (two groups would sum the projection's
+// chunks in group order, not in the 1x1 conv's, so two-chunk layers, which
+// take two groups, run their projection apart), not the pipelined kernel, at
+// most four staging items per thread.  Measured: the fused pair takes
+// ResNet-18's stride-2 stage-3 / stage-4 pairs from 31.5 / 39 us to 27.2 /
+// 33 us at batch 32; its stage-2 pair (two chunks) on the two-group tiles
+// measured 52 us against 35 us apart.
+bool proj_tile_ok(const PatchGeom& g, const TileChoice& c, const PatchGeom& t) {
+    const bool cfg_ok = c.cfg == 1 || c.cfg == 3 || c.cfg == 9;
+    return cfg_ok && c.kg == 1 && !c.pipe && g.taps == 9 && 4 * t.PHi * t.PWi <= 4 * c.NT;
+}
+
+bool tile_fits_base(const PatchGeom& g, const TileChoice& c, PatchGeom& t);
+
 bool tile_fits(const PatchGeom& g, const TileChoice& c, PatchGeom& t) {
+    if (!tile_fits_base(g, c, t)) return false;
+    return !g.proj || proj_tile_ok(g, c, t);
+}
+
+bool tile_fits_base(const PatchGeom& g, const TileChoice& c, PatchGeom& t) {
     if (g.fold) {
         // the folded K loop: 3x3 taps, at most two staging items; one K group
         // summing the groups in turn, or (exactly two equal groups) two K
@@ -1514,13 +1650,13 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
     return true;
 }
 
-template <class Cfg, bool TERNARY, int TAPS, int MAXI, bool FOLD = false>
+template <class Cfg, bool TERNARY, int TAPS, int MAXI, bool FOLD = false, bool PROJ = false>
 int launch_patch_taps(const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes, int m_alloc,
                       const PatchEpi& epi, hipStream_t s) {
     const size_t lds = lds_bytes(g, Cfg::BM, TERNARY, Cfg::KG);
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI, FOLD>),
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI, FOLD, PROJ>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
         if (e != hipSuccess) return tbn_hip::fail(TBN_RUNTIME_ERROR, std::string("hipFuncSetAttribute: ") +
                                                                          hipGetErrorString(e));
@@ -1531,7 +1667,7 @@ int launch_patch_taps(const float* x, const PatchGeom& g, const uint8_t* w, int6
     gl.div_split = make_udiv(static_cast<uint32_t>(gl.blocks_split));
     gl.div_mt = make_udiv(static_cast<uint32_t>((g.M + Cfg::BM - 1) / Cfg::BM));
     const int64_t blocks = static_cast<int64_t>(gl.blocks_split) * g.splits;
-    hipLaunchKernelGGL((conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI, FOLD>), dim3(static_cast<unsigned>(blocks)),
+    hipLaunchKernelGGL((conv_patch_kernel<Cfg, TERNARY, TAPS, MAXI, FOLD, PROJ>), dim3(static_cast<unsigned>(blocks)),
                        dim3(Cfg::NT), lds, s, x, gl, w, col_bytes, m_alloc, epi);
     return tbn_hip::check_launch(TERNARY ? "conv2d_f32_ternary (patch)" : "conv2d_f32_binary (patch)");
 }
@@ -1543,6 +1679,23 @@ int launch_patch_items(const float* x, const PatchGeom& g, const uint8_t* w, int
     const int wper_thread = (Cfg::BM / (TERNARY ? 2 : 4) * g.taps + Cfg::NT - 1) / Cfg::NT;
     if (per_thread > 8 || wper_thread > 4 || (Cfg::KG > 1 && per_thread > 4))
         return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for the staging registers");
+    if (g.proj) {
+        // with the fused projection (the tiles proj_tile_ok admits)
+        constexpr bool kProj =
+            std::is_same<Cfg, P1>::value || std::is_same<Cfg, P3>::value || std::is_same<Cfg, P9>::value;
+        if constexpr (TAPS > 0 && kProj) {
+            if (g.fold) {
+                if (per_thread <= 2)
+                    return launch_patch_taps<Cfg, TERNARY, TAPS, 2, true, true>(x, g, w, col_bytes, m_alloc, epi, s);
+            } else {
+                if (per_thread <= 2)
+                    return launch_patch_taps<Cfg, TERNARY, TAPS, 2, false, true>(x, g, w, col_bytes, m_alloc, epi, s);
+                if (per_thread <= 4)
+                    return launch_patch_taps<Cfg, TERNARY, TAPS, 4, false, true>(x, g, w, col_bytes, m_alloc, epi, s);
+            }
+        }
+        return tbn_hip::fail(TBN_INVALID_SHAPE, "this conv tile does not take a fused projection");
+    }
     if (g.fold) {
         // all chunk groups in one block (3x3, small patches): one K group of
         // waves taking the groups in turn, or two taking one group each
@@ -1656,8 +1809,8 @@ int run_choice(const TileChoice& c, const float* x, const PatchGeom& g, const ui
 // k-slice, hi/mid/lo), so the choice never changes results.
 
 struct PlanKey {
-    int64_t v[16];
-    bool operator<(const PlanKey& o) const { return std::lexicographical_compare(v, v + 16, o.v, o.v + 16); }
+    int64_t v[17];
+    bool operator<(const PlanKey& o) const { return std::lexicographical_compare(v, v + 17, o.v, o.v + 17); }
 };
 
 std::mutex& plan_mutex() {
@@ -1671,7 +1824,7 @@ std::map<PlanKey, int>& plan_cache() {
 
 PlanKey plan_key(const tbn_conv2d_desc* d, bool ternary, const PatchEpi& epi) {
     return PlanKey{{d->n, d->c, d->h, d->w, d->m, d->kh, d->kw, d->sh, d->sw, d->ph, d->pw, d->dh, d->dw,
-                    ternary ? 1 : 0, epi.flags, epi.residual ? 1 : 0}};
+                    ternary ? 1 : 0, epi.flags, epi.residual ? 1 : 0, epi.proj_y ? 1 : 0}};
 }
 
 template <bool TERNARY>
@@ -1804,6 +1957,7 @@ int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
     if (forced) splits = tbn_hip::tuning(TBN_TUNE_CONV_SPLITS);
     g.single = 0;
     g.pipe = 0;
+    g.proj = 0;
     g.gchunks = (g.chunks + splits - 1) / splits;
     const int groups = (g.chunks + g.gchunks - 1) / g.gchunks;
     // The batch decides how the groups run: when the unsplit 8 x 8 tiles of
@@ -1901,6 +2055,56 @@ int conv_patch_run(int weights, const float* x, const tbn_conv2d_desc* desc, con
         if (!scratch) tbn_hip::release_workspace(part, temporary, s);
     }
     return rc;
+}
+
+// A 3x3 pad-1 conv and the 1x1 pad-0 projection of its input at the same
+// stride and channel count in one launch (conv_patch_kernel<..., PROJ>).
+// mode 0 runs, 1 times the tiles that take the pair and caches the fastest,
+// 2 only answers whether this geometry pairs.  TBN_NOT_IMPLEMENTED: the pair
+// does not fuse here (K split over blocks, no tile takes it); the caller
+// then runs the two convs, which give the same bits.
+int conv_patch_pair_run(int weights, const float* x, const tbn_conv2d_desc* desc, const uint8_t* conv_weights,
+                        const float* scale, float alpha, const float* bias, const float* residual, int flags,
+                        float* y, const uint8_t* proj_weights, const float* proj_scale, float proj_alpha,
+                        const float* proj_bias, int proj_flags, float* proj_y, int mode, hipStream_t s) {
+    TBN_REQUIRE(weights == TBN_WEIGHTS_BINARY || weights == TBN_WEIGHTS_TERNARY, TBN_INVALID_ARGUMENT,
+                "unknown weights kind");
+    TBN_REQUIRE(mode >= 0 && mode <= 2, TBN_INVALID_ARGUMENT, "mode must be 0 (run), 1 (tune) or 2 (query)");
+    constexpr int kFlags = TBN_EPI_RELU | TBN_EPI_BIAS_THEN_SCALE;
+    TBN_REQUIRE((flags & ~kFlags) == 0 && (proj_flags & ~kFlags) == 0, TBN_INVALID_ARGUMENT,
+                "a fused pair takes ReLU and bias-then-scale epilogues only");
+    TBN_REQUIRE(desc != nullptr, TBN_INVALID_ARGUMENT, "null pointer");
+    if (desc->kh != 3 || desc->kw != 3 || desc->ph != 1 || desc->pw != 1 || desc->dh != 1 || desc->dw != 1 ||
+        desc->sh != desc->sw)
+        return tbn_hip::fail(TBN_NOT_IMPLEMENTED, "only a 3x3 pad-1 conv pairs with the 1x1 projection of its input");
+    PatchGeom g;
+    int rc = make_patch_geom(desc, flags, g);
+    if (rc) return rc;
+    if (g.splits != 1)
+        return tbn_hip::fail(TBN_NOT_IMPLEMENTED, "a conv that splits K over blocks runs apart from its projection");
+    g.proj = 1;
+    TileChoice tc;
+    {
+        PatchGeom t = g;
+        if (!choose_tile(t, tc)) return tbn_hip::fail(TBN_NOT_IMPLEMENTED, "no conv tile takes this pair");
+    }
+    if (mode == 2 || g.VH == 0 || g.VW == 0 || g.N == 0) return tbn_hip::ok();
+    TBN_REQUIRE(x && conv_weights && y && proj_weights && proj_y, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_REQUIRE(reinterpret_cast<uintptr_t>(conv_weights) % 8 == 0 && reinterpret_cast<uintptr_t>(proj_weights) % 8 == 0,
+                TBN_INVALID_ARGUMENT, "conv weights must be 8-byte aligned");
+    if (mode == 1) {
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        TBN_REQUIRE(hipStreamIsCapturing(s, &st) == hipSuccess && st == hipStreamCaptureStatusNone,
+                    TBN_INVALID_ARGUMENT, "conv tuning waits for the stream and cannot run under stream capture");
+        if (tbn_hip::tuning(TBN_TUNE_CONV_TILE) >= 0) return tbn_hip::ok();  // a forced tile: nothing to choose
+    }
+    TBN_DEVICE_GUARD();
+    const int64_t Kc = static_cast<int64_t>(g.chunks) * g.taps * kChunk;
+    const int64_t col_bytes = Kc / (weights == TBN_WEIGHTS_BINARY ? 8 : 4);
+    const int m_alloc = int((desc->m + 7) / 8 * 8);
+    PatchEpi epi{y, scale, alpha, bias, residual, flags, nullptr, nullptr,
+                 proj_weights, proj_y, proj_scale, proj_alpha, proj_bias, proj_flags};
+    return conv_patch_dispatch(weights, x, desc, g, conv_weights, col_bytes, m_alloc, epi, s, mode == 1, nullptr);
 }
 
 int conv_patch_dispatch(int weights, const float* x, const tbn_conv2d_desc* desc, PatchGeom& g,
@@ -2034,6 +2238,15 @@ int tbn_hip_conv2d_f32_prepacked(int weights, const float* x, const tbn_conv2d_d
                                  const float* residual, int flags, float* y, tbn_stream_t stream) {
     return conv_patch_run(weights, x, desc, conv_weights, scale, alpha, bias, residual, flags, y,
                           tbn_hip::stream_of(stream));
+}
+
+int tbn_hip_conv2d_f32_prepacked_pair(int weights, const float* x, const tbn_conv2d_desc* desc,
+                                      const uint8_t* conv_weights, const float* scale, float alpha, const float* bias,
+                                      const float* residual, int flags, float* y, const uint8_t* proj_weights,
+                                      const float* proj_scale, float proj_alpha, const float* proj_bias,
+                                      int proj_flags, float* proj_y, int mode, tbn_stream_t stream) {
+    return conv_patch_pair_run(weights, x, desc, conv_weights, scale, alpha, bias, residual, flags, y, proj_weights,
+                               proj_scale, proj_alpha, proj_bias, proj_flags, proj_y, mode, tbn_hip::stream_of(stream));
 }
 
 int tbn_hip_conv2d_kernel_name(int weights, const tbn_conv2d_desc* desc, int flags, int has_residual, char* name,

@@ -120,6 +120,8 @@ _SIGNATURES = {
     "tbn_hip_conv_weights_bytes": ([_I32, ctypes.POINTER(ConvDesc), ctypes.POINTER(ctypes.c_int64)], _I32),
     "tbn_hip_pack_conv_weights": ([_I32, _P, _I64, _I64, ctypes.POINTER(ConvDesc), _P, _P], _I32),
     "tbn_hip_conv2d_f32_prepacked": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P, _P], _I32),
+    "tbn_hip_conv2d_f32_prepacked_pair": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P,
+                                           _P, _P, _F32, _P, _I32, _P, _I32, _P], _I32),
     "tbn_hip_conv2d_tune_prepacked": ([_I32, _P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _P, _P],
                                       _I32),
     "tbn_hip_conv2d_kernel_name": ([_I32, ctypes.POINTER(ConvDesc), _I32, _I32, ctypes.c_char_p, ctypes.c_size_t],

@@ -211,6 +211,8 @@ struct Op {
     int workspace = -1;              // value id of the op's transient workspace (grouped conv slices,
                                      // a TBN Gemm's fp4 activation rows)
     bool tbn = false;                // TBN arithmetic (ternarized activations, integer products)
+    int pair = -1;                   // a 1x1 projection of the same input run in this conv's launch
+    bool paired = false;             // this projection runs in its pair's launch (at the pair's position)
     int64_t tbn_scratch = 0;         // bytes of a TBN conv's record scratch (0: the fused kernel needs none)
     const Tensor* tbn_w = nullptr;   // its fp4 weights: TBN conv layout, or [N_pad, K_pad / 2] rows
     const float* scale = nullptr;  // per-channel scale (device)
@@ -1057,6 +1059,56 @@ struct TBNModel::Session::Impl {
         return -1;
     }
 
+    // ---- fused projection pairs ---------------------------------------------------------
+
+    int weights_kind(const Op& op) const {
+        return op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY : TBN_WEIGHTS_TERNARY;
+    }
+
+    // A prepacked quantized conv with a k x k kernel, pad (k - 1) / 2,
+    // dilation 1, equal strides, one group, no pool, no run-time bias.
+    bool pairable(const Op& op, int64_t k) const {
+        const tbn_conv2d_desc& d = op.desc;
+        return !op.dead && !op.paired && op.kind == OpKind::ConvQuant && op.groups == 1 && !op.tbn && op.conv_w &&
+               op.pw && op.bias_value < 0 && d.kh == k && d.kw == k && d.ph == (k - 1) / 2 && d.pw == (k - 1) / 2 &&
+               d.dh == 1 && d.dw == 1 && d.sh == d.sw &&
+               (op.flags & ~(TBN_EPI_RELU | TBN_EPI_BIAS_THEN_SCALE)) == 0;
+    }
+
+    // A ResNet downsampling block reads its input twice: the first 3x3 conv
+    // (stride s, pad 1) and the 1x1 stride-s projection shortcut to the same
+    // channel count.  When the library takes the pair
+    // (tbn_hip_conv2d_f32_prepacked_pair, mode 2) both run in the 3x3 conv's
+    // launch with the bits of the two launches; the projection's output is
+    // then written at the conv's position, which the memory plan takes as its
+    // definition.  Every reader of that output must come after the conv.
+    void pair_projections() {
+        for (size_t a = 0; a < ops.size(); ++a) {
+            Op& conv = ops[a];
+            if (!pairable(conv, 3)) continue;
+            for (size_t p = 0; p < ops.size(); ++p) {
+                Op& proj = ops[p];
+                if (p == a || !pairable(proj, 1) || proj.residual >= 0 || proj.in[0] != conv.in[0] ||
+                    proj.desc.m != conv.desc.m || proj.desc.sh != conv.desc.sh ||
+                    weights_kind(proj) != weights_kind(conv))
+                    continue;
+                bool later = true;
+                for (int r : readers(proj.out))
+                    if (r <= static_cast<int>(a)) later = false;
+                if (!later || is_output(proj.out)) continue;
+                if (tbn_hip_conv2d_f32_prepacked_pair(weights_kind(conv), nullptr, &conv.desc, nullptr, nullptr, 1.0f,
+                                                      nullptr, nullptr, conv.flags, nullptr, nullptr, nullptr, 1.0f,
+                                                      nullptr, proj.flags, nullptr, 2, nullptr) != TBN_SUCCESS) {
+                    (void)tbn_hip_last_error();  // not taken: the two convs run apart
+                    continue;
+                }
+                conv.pair = static_cast<int>(p);
+                proj.paired = true;
+                break;
+            }
+        }
+    }
+
     // ---- memory planning -------------------------------------------------------------
 
     int root(int v) const {
@@ -1078,6 +1130,12 @@ struct TBNModel::Session::Impl {
                 values[ops[i].workspace].last = i;
             }
         }
+        // a paired projection's output is written in its conv's launch
+        for (int i = 0; i < nops; ++i)
+            if (!ops[i].dead && ops[i].pair >= 0) {
+                Value& v = values[root(ops[ops[i].pair].out)];
+                v.def = std::min(v.def, i);
+            }
         for (const auto& name : graph->outputs) {
             auto it = value_id.find(name);
             TBN_CHECK(it != value_id.end(), RuntimeError, "Output '" + name + "' was not produced");
@@ -1146,11 +1204,12 @@ struct TBNModel::Session::Impl {
         }
         for (const auto& node : graph->nodes) lower(node);
         fuse();
+        pair_projections();
         plan_memory();
         tune_convs();
         launches = 0;
         for (const auto& op : ops)
-            if (!op.dead && op.kind != OpKind::View)
+            if (!op.dead && !op.paired && op.kind != OpKind::View)
                 launches += op.groups > 1 && op.kind != OpKind::ConvDepthwise ? op.groups * (op.desc.n == 1 ? 1 : 3) : 1;
         planned = true;
         plan_quant = quant;
@@ -1170,7 +1229,17 @@ struct TBNModel::Session::Impl {
             st != hipStreamCaptureStatusNone)
             return;
         for (auto& op : ops) {
-            if (op.dead || op.kind != OpKind::ConvQuant || op.groups > 1 || !op.conv_w) continue;
+            if (op.dead || op.paired || op.kind != OpKind::ConvQuant || op.groups > 1 || !op.conv_w) continue;
+            if (op.pair >= 0) {
+                const Op& pr = ops[op.pair];
+                check_status(tbn_hip_conv2d_f32_prepacked_pair(
+                                 weights_kind(op), fp(op.in[0]), &op.desc, op.conv_w->typed_data<uint8_t>(), op.scale,
+                                 1.0f, bias_of(op), op.residual >= 0 ? fp(op.residual) : nullptr, op.flags, fp(op.out),
+                                 pr.conv_w->typed_data<uint8_t>(), pr.scale, 1.0f, bias_of(pr), pr.flags, fp(pr.out),
+                                 1, s),
+                             ("tuning node '" + op.node + "' with '" + pr.node + "'").c_str());
+                continue;
+            }
             check_status(tbn_hip_conv2d_tune_prepacked(
                              op.pw->kind == PackedWeights::Kind::Binary ? TBN_WEIGHTS_BINARY : TBN_WEIGHTS_TERNARY,
                              fp(op.in[0]), &op.desc, op.conv_w->typed_data<uint8_t>(), op.scale, 1.0f, bias_of(op),
@@ -1256,6 +1325,17 @@ struct TBNModel::Session::Impl {
                                                                   : nullptr,
                                                               fp(op.out), s),
                                  what.c_str());
+                    return;
+                }
+                if (op.paired) return;  // written by its pair's launch
+                if (op.pair >= 0) {
+                    const Op& pr = ops[op.pair];
+                    check_status(tbn_hip_conv2d_f32_prepacked_pair(
+                                     weights_kind(op), fp(op.in[0]), &op.desc, op.conv_w->typed_data<uint8_t>(),
+                                     op.scale, 1.0f, bias_of(op), op.residual >= 0 ? fp(op.residual) : nullptr,
+                                     op.flags, fp(op.out), pr.conv_w->typed_data<uint8_t>(), pr.scale, 1.0f,
+                                     bias_of(pr), pr.flags, fp(pr.out), 0, s),
+                                 (what + " with '" + pr.node + "'").c_str());
                     return;
                 }
                 if (op.conv_w) {

@@ -334,6 +334,24 @@ int tbn_hip_conv2d_f32_prepacked(int weights, const float* x, const tbn_conv2d_d
 int tbn_hip_conv2d_tune_prepacked(int weights, const float* x, const tbn_conv2d_desc* desc,
                                   const uint8_t* conv_weights, const float* scale, float alpha, const float* bias,
                                   const float* residual, int flags, float* y, tbn_stream_t stream);
+/* No counterpart in the reference, which runs the two Conv2D layers of a
+ * ResNet downsampling block one after the other (conv2d.cpp:319-369 each).
+ * One launch computes both the conv of tbn_hip_conv2d_f32_prepacked (desc:
+ * 3x3, pad 1, stride s in both directions, dilation 1; flags TBN_EPI_RELU /
+ * TBN_EPI_BIAS_THEN_SCALE; optional residual) and the 1x1 pad-0 stride-s
+ * conv of the same x to the same desc->m channels (proj_weights in the conv
+ * layout of that 1x1 desc, its own scale, alpha, bias and flags, no
+ * residual; proj_y has y's shape).  The projection is summed in the order
+ * the 1x1 conv uses alone, so both ways give the same bits.  mode: 0 runs,
+ * 1 tunes as tbn_hip_conv2d_tune_prepacked does (its own cache entry), 2 only
+ * checks that this geometry pairs (no pointer is read).  Returns
+ * TBN_NOT_IMPLEMENTED when it does not (another kernel size or padding, K
+ * split over blocks, no tile takes it): the caller then makes the two calls. */
+int tbn_hip_conv2d_f32_prepacked_pair(int weights, const float* x, const tbn_conv2d_desc* desc,
+                                      const uint8_t* conv_weights, const float* scale, float alpha, const float* bias,
+                                      const float* residual, int flags, float* y, const uint8_t* proj_weights,
+                                      const float* proj_scale, float proj_alpha, const float* proj_bias,
+                                      int proj_flags, float* proj_y, int mode, tbn_stream_t stream);
 /* No counterpart in the reference (a diagnostic for profiling).  Writes into
  * name (len bytes, NUL-terminated, truncated if short) the kernel, as a
  * profiler names it, that tbn_hip_conv2d_f32_prepacked runs for this

@@ -677,3 +677,110 @@ def test_conv_forced_splits_skip_pooled_convs(dev):
     assert np.array_equal(got_pooled, want_pooled)
     rm.assert_within_tolerance(got_pooled, pooled["ref"], pooled["K"], pooled["xmax"] * 1.5)
     rm.assert_within_tolerance(got_plain, plain["ref"], plain["K"], plain["xmax"] * 1.5)
+
+
+PAIR_CASES = [
+    # N, C, H, W, M, stride, ternary, flags, proj_flags, with_residual
+    (4, 128, 28, 28, 256, 2, False, tbn_hip.EPI_RELU, 0, False),      # four chunks in turn
+    (32, 256, 14, 14, 512, 2, False, tbn_hip.EPI_RELU, 0, False),     # chunk groups folded into one block
+    (2, 72, 20, 18, 72, 2, True, tbn_hip.EPI_RELU, tbn_hip.EPI_BIAS_THEN_SCALE, True),  # ternary, ragged C / M
+    (3, 96, 15, 13, 80, 1, False, tbn_hip.EPI_BIAS_THEN_SCALE, tbn_hip.EPI_RELU, True),  # stride 1
+]
+
+
+def _conv_layout(kind, rng, M, C, k):
+    """Random binary / ternary weights [M, C, k, k] in the conv layout of a k x k desc, and their values."""
+    import ctypes
+    K = C * k * k
+    if kind == tbn_hip.WEIGHTS_TERNARY:
+        wt = rng.integers(-1, 2, (M, K)).astype(np.int8)
+        K_pad, N_pad = (K + 31) // 32 * 32, M
+        packed = empty(M * K_pad // 4, torch.uint8)
+        tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(wt)), K, M, tbn_hip.LAYOUT_NK, K_pad, M, P(packed), None)
+        wref = wt.reshape(M, C, k, k).astype(np.float32)
+    else:
+        wbytes = (rng.random((M, C, k, k)) < 0.5).astype(np.uint8)
+        packed, K_pad, N_pad = pack_conv_weights(wbytes, M, K)
+        wref = np.where(wbytes == 1, 1.0, -1.0).astype(np.float32)
+
+    def layout(d):
+        wb = ctypes.c_int64()
+        tbn_hip.call("tbn_hip_conv_weights_bytes", kind, d, ctypes.byref(wb))
+        cw = empty(wb.value, torch.uint8)
+        tbn_hip.call("tbn_hip_pack_conv_weights", kind, P(packed), K_pad, N_pad, d, P(cw), None)
+        return cw
+    return layout, wref
+
+
+@pytest.mark.parametrize("case", PAIR_CASES, ids=["chunks", "folded", "ternary", "stride1"])
+def test_conv_pair_matches_separate_convs(dev, case):
+    """A 3x3 pad-1 conv and the 1x1 projection of its input in one launch give
+    the bits of the two separate calls, for the tuned tile and every tile that
+    takes the pair; the pair's projection is also within tolerance of float64."""
+    N, C, H, W, M, st, ternary, flags, pflags, with_res = case
+    kind = tbn_hip.WEIGHTS_TERNARY if ternary else tbn_hip.WEIGHTS_BINARY
+    rng = np.random.default_rng(N + C + M + st)
+    x = to_dev(rng.standard_normal((N, C, H, W)).astype(np.float32))
+    d3 = tbn_hip.conv_desc(N, C, H, W, M, 3, 3, st, st, 1, 1)
+    d1 = tbn_hip.conv_desc(N, C, H, W, M, 1, 1, st, st, 0, 0)
+    OH, OW = tbn_hip.conv_out_hw(d3)
+    assert (OH, OW) == tbn_hip.conv_out_hw(d1)
+    lay3, w3 = _conv_layout(kind, rng, M, C, 3)
+    lay1, w1 = _conv_layout(kind, rng, M, C, 1)
+    cw3, cw1 = lay3(d3), lay1(d1)
+    s3 = to_dev(rng.uniform(0.5, 1.5, M).astype(np.float32))
+    b3 = to_dev((rng.standard_normal(M) * 0.01).astype(np.float32))
+    s1 = rng.uniform(0.5, 1.5, M).astype(np.float32)
+    b1 = (rng.standard_normal(M) * 0.01).astype(np.float32)
+    res = to_dev(rng.standard_normal((N, M, OH, OW)).astype(np.float32)) if with_res else None
+
+    def separate():
+        y, py = empty((N, M, OH, OW), torch.float32), empty((N, M, OH, OW), torch.float32)
+        tbn_hip.call("tbn_hip_conv2d_f32_prepacked", kind, P(x), d3, P(cw3), P(s3), 1.0, P(b3), P(res), flags, P(y),
+                     None)
+        tbn_hip.call("tbn_hip_conv2d_f32_prepacked", kind, P(x), d1, P(cw1), P(to_dev(s1)), 0.5, P(to_dev(b1)), None,
+                     pflags, P(py), None)
+        return host(y), host(py)
+
+    def pair(mode=0):
+        y, py = empty((N, M, OH, OW), torch.float32), empty((N, M, OH, OW), torch.float32)
+        y.fill_(np.nan)
+        py.fill_(np.nan)
+        tbn_hip.call("tbn_hip_conv2d_f32_prepacked_pair", kind, P(x), d3, P(cw3), P(s3), 1.0, P(b3), P(res), flags,
+                     P(y), P(cw1), P(to_dev(s1)), 0.5, P(to_dev(b1)), pflags, P(py), mode, None)
+        return host(y), host(py)
+
+    tbn_hip.call("tbn_hip_conv2d_f32_prepacked_pair", kind, None, d3, None, None, 1.0, None, None, flags, None,
+                 None, None, 0.5, None, pflags, None, 2, None)  # pairs: no pointer read
+    want_y, want_p = separate()
+    got_y, got_p = pair()
+    assert np.array_equal(got_y, want_y) and np.array_equal(got_p, want_p)
+    pair(mode=1)  # tuned
+    got_y, got_p = pair()
+    assert np.array_equal(got_y, want_y) and np.array_equal(got_p, want_p)
+    ran = 0
+    for tile in range(128):
+        with tbn_hip.tuning(tbn_hip.TUNE_CONV_TILE, tile):
+            try:
+                got_y, got_p = pair()
+            except tbn_hip.TbnError:
+                continue
+        assert np.array_equal(got_y, want_y) and np.array_equal(got_p, want_p), tile
+        ran += 1
+    assert ran >= 1
+    ref = conv_ref(host(x), w1, s1, 0.5, b1, (st, st), (0, 0), (1, 1), pflags)
+    rm.assert_within_tolerance(want_p, ref, C, float(np.abs(host(x)).max()) * 1.5)
+
+
+def test_conv_pair_declines_split_and_other_shapes(dev):
+    """Geometries that split K over blocks (few images of a deep layer), take
+    two K groups (two chunks), or have another kernel size or padding return
+    TBN_NOT_IMPLEMENTED without work."""
+    for d in (tbn_hip.conv_desc(2, 256, 14, 14, 512, 3, 3, 2, 2, 1, 1),   # K split at batch 2
+              tbn_hip.conv_desc(4, 64, 56, 56, 128, 3, 3, 2, 2, 1, 1),    # two chunks
+              tbn_hip.conv_desc(2, 64, 16, 16, 64, 5, 5, 1, 1, 2, 2),     # 5x5
+              tbn_hip.conv_desc(2, 64, 16, 16, 64, 3, 3, 1, 1, 0, 0)):    # pad 0
+        with pytest.raises(tbn_hip.TbnError) as e:
+            tbn_hip.call("tbn_hip_conv2d_f32_prepacked_pair", tbn_hip.WEIGHTS_BINARY, None, d, None, None, 1.0, None,
+                         None, 0, None, None, None, 1.0, None, 0, None, 2, None)
+        assert e.value.code == tbn_hip.NOT_IMPLEMENTED
