@@ -2272,7 +2272,8 @@ int tbn_hip_conv2d_kernel_name(int weights, const tbn_conv2d_desc* desc, int fla
     const int taps = (g.kh == 3 && g.kw == 3) ? 9 : 0;
     const int per_thread = (4 * g.PHi * g.PWi + tc.NT - 1) / tc.NT;
     const int maxi = taps && per_thread <= 1 ? 1 : taps && per_thread <= 2 ? 2 : per_thread <= 4 ? 4 : 8;
-    std::snprintf(name, len, "conv_patch_kernel<PatchCfg<%d, %d, %d, %d, %d, %d>, %s, %d, %d, %s>", tc.BM, tc.TH,
+    // (the last argument, PROJ, is false: this is the conv without a fused projection)
+    std::snprintf(name, len, "conv_patch_kernel<PatchCfg<%d, %d, %d, %d, %d, %d>, %s, %d, %d, %s, false>", tc.BM, tc.TH,
                   tc.TW, tc.WM, tc.WQ, tc.kg, weights == TBN_WEIGHTS_TERNARY ? "true" : "false", taps, maxi,
                   g.fold ? "true" : "false");
     return tbn_hip::ok();

@@ -593,8 +593,8 @@ def test_conv_folded_groups_match_split_k(dev, case):
 
     big, big_name = run(N)
     small, small_name = run(2)
-    assert big_name.endswith(", true>"), big_name       # folded: one block runs every group
-    assert small_name.endswith(", false>"), small_name  # split over blocks
+    assert big_name.endswith(", true, false>"), big_name       # folded: one block runs every group
+    assert small_name.endswith(", false, false>"), small_name  # split over blocks
     assert np.array_equal(big[:2], small)
     with tbn_hip.tuning(tbn_hip.TUNE_CONV_SPLITS, 2):
         forced, _ = run(N)
@@ -602,7 +602,7 @@ def test_conv_folded_groups_match_split_k(dev, case):
         assert np.array_equal(big, forced)
         # every tile gives these bits, folded or split; two equal chunk groups
         # also run on tiles with two K groups of waves, one group each
-        pair = re.compile(r"PatchCfg<\d+, \d+, \d+, \d+, \d+, 2>, (true|false), 9, \d, true>$")
+        pair = re.compile(r"PatchCfg<\d+, \d+, \d+, \d+, \d+, 2>, (true|false), 9, \d, true, false>$")
         pairs = 0
         for tile in range(128):
             with tbn_hip.tuning(tbn_hip.TUNE_CONV_TILE, tile):
