@@ -86,7 +86,6 @@ struct PatchGeom {
     // (80-byte records) the two rows one 16-lane group reads then sit in
     // disjoint LDS banks
     int rowperm;
-    int pipe;  // 1: laid out for conv_pipe_kernel (2-D tiles, both chunks per buffer)
     // 1: the launch also computes the 1x1 projection of the same input from
     // the centre tap (conv_patch_kernel<..., PROJ = true>)
     int proj;
@@ -154,10 +153,9 @@ __device__ __forceinline__ bool tile_pixel(const PatchGeom& g, int q0, int row0,
     return valid;
 }
 
-// KG > 1: KG groups of waves, group g taking chunks g, g + KG, ... of the
-// block's K range into its own accumulators; the groups' sums are added in
-// group order at the end (used for two-chunk layers, both chunks staged at
-// once, so a block's compute runs in half the time on twice the waves).
+// KG = 2: two groups of waves, each summing one run of consecutive chunks
+// into its own accumulators, the two sums added in group order at the end:
+// the order of two folded chunk groups (conv_patch_kernel, make_patch_geom).
 template <int BM_, int TH_, int TW_, int WM_, int WQ_, int KG_ = 1>
 struct PatchCfg {
     static constexpr int BM = BM_, TH = TH_, TW = TW_, WM = WM_, WQ = WQ_, KG = KG_;
@@ -486,10 +484,10 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     (void)accp;
 
     // KG = 2: K group k sums the cpg chunks [cb + k * cpg, cb + (k + 1) * cpg)
-    // from zero (host-checked: the block's range is two equal runs, each one
-    // chunk group: a two-chunk layer, or a folded pair of groups).  Every
-    // thread stages both runs, run k's chunk i into buffer k + 2 (i & 1), so
-    // the groups advance together between the block's barriers.
+    // from zero (host-checked: the block's range is a folded pair of equal
+    // chunk groups).  Every thread stages both runs, run k's chunk i into
+    // buffer k + 2 (i & 1), so the groups advance together between the
+    // block's barriers.
     const int cpg = (ce - cb) / Cfg::KG;
     const int nbuf = g.single ? 1 : (Cfg::KG > 1 && cpg > 1 ? 4 : 2);
     Stage stage2;
@@ -903,356 +901,6 @@ conv_patch_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __res
     }
 }
 
-// ---------------------------------------------------------------------------
-// Pipelined patch conv for two-chunk 3x3 layers (33..64 input channels)
-// ---------------------------------------------------------------------------
-// A block of 8 waves owns BM output channels and a run of consecutive pixel
-// tiles of one channel tile.  Waves 0-3 (one per SIMD) only multiply: wave
-// (g, h) takes chunk g (K group g) and the 64-channel x 32-pixel part h of
-// every tile, with its 36 weight fragments (9 taps x 2 k-halves x 2 row
-// fragments) decoded to bf16 once per block and kept in registers, so its
-// inner loop is LDS fragment reads and MFMAs only.  Waves 4-7 (one per SIMD)
-// stage tile i+1's patch (its loads issued one phase earlier) and finish tile
-// i-1 (group sum, epilogue, stores) while waves 0-3 run tile i's MFMAs, so on
-// every SIMD one wave's VALU and memory work fills the other's MFMA gaps.
-// Each phase ends with one barrier; both roles pass the same number of them.
-// Every output is summed as the two-group patch kernel sums it (chunk g's
-// taps, k-halves and hi/mid/lo planes in that order into group g's
-// accumulator, then group 0 + group 1), so the two kernels give the same bits.
-template <int BM_, int TH_, int TW_>
-struct PipeCfg {
-    static constexpr int BM = BM_, TH = TH_, TW = TW_, QT = TH * TW;
-    static constexpr int WAVES_M = BM / 64, WAVES_Q = QT / 32;  // multiply waves of one K group
-    static_assert(WAVES_M * WAVES_Q == 2 && TH % 2 == 0 && TW % 2 == 0, "two 64 x 32 multiply waves per K group");
-    static constexpr int NT = 512;
-};
-
-// floats of one hand-over buffer: [group][h][fragment][e4][lane][4]
-constexpr int kPipeAccFloats = 2 * 2 * 2 * 4 * 64 * 4;
-
-__host__ __device__ inline int pipe_buffer_elems(int patch) { return 2 * 3 * (patch + 1) * kPix; }
-
-// First pixel tile (n, oh0, ow0) of pixel tile t of a 2-D tiling.
-template <class Cfg>
-__device__ __forceinline__ void pipe_tile_origin(const PatchGeom& g, int t, int& n, int& oh0, int& ow0) {
-    n = udiv(t, g.div_img);
-    const int st = t - n * g.tiles_img;
-    const int th = udiv(st, g.div_tw);
-    oh0 = th * Cfg::TH;
-    ow0 = (st - th * g.tiles_w) * Cfg::TW;
-}
-
-// MAXI: patch items (8 channels of one pixel) one helper thread stages per
-// tile, the smallest that covers both chunks' 8 * patch items.
-template <int ITEMS>
-struct PipeStager {
-    uint32_t cofs[ITEMS];
-    int pr[ITEMS], pc[ITEMS], slot[ITEMS];
-    bool inp[ITEMS];
-    float v[ITEMS][8];
-
-    // items idx, idx + stride, ...: (chunk, 8-channel group, patch pixel),
-    // chunk-major; an item past the patch writes the spare records
-    __device__ __forceinline__ void init(const PatchGeom& g, int idx, int stride, int patch, int chunk_elems,
-                                         uint32_t HW4) {
-#pragma unroll
-        for (int it = 0; it < ITEMS; ++it) {
-            const int item = idx + it * stride;
-            inp[it] = item < 8 * patch;
-            const int chunk = item >= 4 * patch ? 1 : 0;
-            const int rem = item - chunk * 4 * patch;
-            const int grp = udiv(rem, g.div_patch);
-            const int pp = rem - grp * patch;
-            pr[it] = udiv(pp, g.div_pwi);
-            pc[it] = pp - pr[it] * g.PWi;
-            cofs[it] = static_cast<uint32_t>(chunk * kChunk + grp * 8) * HW4;
-            slot[it] = inp[it] ? chunk * chunk_elems + pp * kPix + grp * 8 : patch * kPix;
-        }
-    }
-    // the patch of pixel tile (n, oh0, ow0): zero outside the image and for
-    // channels past C (the buffer range ends at image n's C planes)
-    __device__ __forceinline__ void load(const float* x, const PatchGeom& g, int n, int oh0, int ow0, uint32_t HW4) {
-        constexpr uint32_t kOutside = 0x80000000u;
-        const int ih0 = oh0 * g.sh - g.ph, iw0 = ow0 * g.sw - g.pw;
-        const __amdgpu_buffer_rsrc_t x_rs =
-            make_rsrc(x + static_cast<int64_t>(n) * g.C * g.H * g.W, static_cast<uint64_t>(g.C) * HW4);
-#pragma unroll
-        for (int it = 0; it < ITEMS; ++it) {
-            const int ih = ih0 + pr[it] * g.psh, iw = iw0 + pc[it] * g.psw;
-            const bool ok = inp[it] && static_cast<unsigned>(ih) < static_cast<unsigned>(g.H) &&
-                            static_cast<unsigned>(iw) < static_cast<unsigned>(g.W);
-            const uint32_t o = ok ? cofs[it] + static_cast<uint32_t>(ih * g.W + iw) * 4 : kOutside;
-#pragma unroll
-            for (int e = 0; e < 8; ++e)
-                v[it][e] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(x_rs, o + e * HW4, 0, 0));
-        }
-    }
-    // split into the three bf16 planes and write the pixel records
-    __device__ __forceinline__ void store(uint16_t* dst, int plane_elems) {
-#pragma unroll
-        for (int it = 0; it < ITEMS; ++it) {
-            uint4 hi, mid, lo;
-            split8(v[it], hi, mid, lo);
-            uint16_t* d = dst + slot[it];
-            *reinterpret_cast<uint4*>(d) = hi;
-            *reinterpret_cast<uint4*>(d + plane_elems) = mid;
-            *reinterpret_cast<uint4*>(d + 2 * plane_elems) = lo;
-        }
-    }
-};
-
-// Epilogue of one tile's outputs held by multiply-wave part h, fragment f,
-// registers 4*e4 .. 4*e4 + 3 for e4 in [E4A, E4A + E4N): group 0's sums +
-// group 1's from the hand-over buffer `hand`, the ternary halving, then
-// (v + a) * s + b, residual, ReLU and the store, as the patch kernel's
-// epilogue forms them.
-template <class Cfg, bool TERNARY, bool RELU, bool RES, int E4A, int E4N>
-__device__ __forceinline__ void pipe_epilogue(const PatchGeom& g, const PatchEpi& epi, const float* hand,
-                                              const float* epi_lds, int m0, int n, int oh0, int ow0, int h, int f,
-                                              int lane) {
-    constexpr uint32_t kOutside = 0x80000000u;
-    const int wm = Cfg::WAVES_M == 2 ? h : 0, wq = Cfg::WAVES_Q == 2 ? h : 0;
-    const uint32_t plane = static_cast<uint32_t>(g.OH * g.OW);
-    const uint32_t plane4 = plane * 4;
-    const uint32_t obytes = static_cast<uint32_t>(g.M - m0) * plane4;
-    const int rlane = wm * 64 + f * 32 + 4 * (lane >> 5);  // row of register 0, from m0
-    const bool bts = (epi.flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
-    int oh, ow, pi, im;
-    const bool valid = tile_pixel<Cfg>(g, 0, oh0, ow0, wq * 32 + (lane & 31), oh, ow, pi, im);
-    const uint32_t voff =
-        valid ? static_cast<uint32_t>(rlane) * plane4 + static_cast<uint32_t>(oh * g.OW + ow) * 4 : kOutside;
-    const int64_t obase = (static_cast<int64_t>(n) * g.M + m0) * plane;
-    const __amdgpu_buffer_rsrc_t y_rs = make_rsrc(epi.y + obase, obytes);
-    float res[E4N][4];
-    if constexpr (RES) {
-        const __amdgpu_buffer_rsrc_t r_rs = make_rsrc(epi.residual + obase, obytes);
-#pragma unroll
-        for (int k = 0; k < E4N; ++k)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-                res[k][q] = __builtin_bit_cast(
-                    float, __builtin_amdgcn_raw_buffer_load_b32(r_rs, voff + (8 * (E4A + k) + q) * plane4, 0, 0));
-    }
-    const float* a0 = hand + ((0 * 2 + h) * 2 + f) * (4 * 64 * 4) + lane * 4;
-    const float* a1 = hand + ((1 * 2 + h) * 2 + f) * (4 * 64 * 4) + lane * 4;
-#pragma unroll
-    for (int k = 0; k < E4N; ++k) {
-        const int e4 = E4A + k;
-        const float4 s0 = *reinterpret_cast<const float4*>(a0 + e4 * 256);
-        const float4 s1 = *reinterpret_cast<const float4*>(a1 + e4 * 256);
-        float acc[4] = {s0.x, s0.y, s0.z, s0.w};
-        const float add[4] = {s1.x, s1.y, s1.z, s1.w};
-        const int r = rlane + 8 * e4;
-        const float4 mv = *reinterpret_cast<const float4*>(epi_lds + r);
-        const float4 bv = *reinterpret_cast<const float4*>(epi_lds + Cfg::BM + r);
-        const float mm[4] = {mv.x, mv.y, mv.z, mv.w};
-        const float bb[4] = {bv.x, bv.y, bv.z, bv.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            acc[q] += add[q];
-            if constexpr (TERNARY) acc[q] *= 0.5f;  // the ternary weights went in as twice their value
-            const float a = bts ? bb[q] : 0.0f, b = bts ? 0.0f : bb[q];
-            float v = (acc[q] + a) * mm[q] + b;
-            if constexpr (RES) v += res[k][q];
-            if constexpr (RELU) v = v > 0.0f ? v : 0.0f;
-            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), y_rs, voff + (8 * e4 + q) * plane4,
-                                                  0, 0);
-        }
-    }
-}
-
-template <class Cfg, bool TERNARY, int E4A, int E4N>
-__device__ __forceinline__ void pipe_finish(const PatchGeom& g, const PatchEpi& epi, const float* hand,
-                                            const float* epi_lds, int m0, int t, int h, int f, int lane) {
-    int n, oh0, ow0;
-    pipe_tile_origin<Cfg>(g, t, n, oh0, ow0);
-    const bool relu = (epi.flags & TBN_EPI_RELU) != 0;
-    if (epi.residual) {
-        if (relu) pipe_epilogue<Cfg, TERNARY, true, true, E4A, E4N>(g, epi, hand, epi_lds, m0, n, oh0, ow0, h, f, lane);
-        else pipe_epilogue<Cfg, TERNARY, false, true, E4A, E4N>(g, epi, hand, epi_lds, m0, n, oh0, ow0, h, f, lane);
-    } else {
-        if (relu) pipe_epilogue<Cfg, TERNARY, true, false, E4A, E4N>(g, epi, hand, epi_lds, m0, n, oh0, ow0, h, f, lane);
-        else pipe_epilogue<Cfg, TERNARY, false, false, E4A, E4N>(g, epi, hand, epi_lds, m0, n, oh0, ow0, h, f, lane);
-    }
-}
-
-template <class Cfg, bool TERNARY, int MAXI>
-__global__ void __launch_bounds__(512)
-conv_pipe_kernel(const float* __restrict__ x, PatchGeom g, const uint8_t* __restrict__ wbits, int m_alloc,
-                 PatchEpi epi, int tiles_pix, int per_block, int blocks_pix) {
-    extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-    const int patch = g.PHi * g.PWi;
-    const int plane_elems = (patch + 1) * kPix;  // one plane of one chunk, with the spare record
-    const int chunk_elems = 3 * plane_elems;
-    const int buf_elems = 2 * chunk_elems;        // one tile's patch: both chunks
-    float* accbuf = reinterpret_cast<float*>(lds + 2 * buf_elems);
-    float* epi_lds = accbuf + 2 * kPipeAccFloats;  // [BM] multipliers, [BM] addends
-
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-
-    // block -> channel tile and its run of pixel tiles; consecutive logical
-    // blocks run on one XCD (blocks are dealt round-robin over the 8 XCDs), so
-    // neighbouring tiles' patches share that XCD's L2
-    int bid = static_cast<int>(blockIdx.x);
-    const int nblocks = static_cast<int>(gridDim.x);
-    if ((nblocks & 7) == 0) bid = (bid & 7) * (nblocks >> 3) + (bid >> 3);
-    const int mt = bid / blocks_pix;
-    const int t0 = (bid - mt * blocks_pix) * per_block;
-    const int nt = min(per_block, tiles_pix - t0);  // >= 1 (host-checked)
-    const int m0 = mt * Cfg::BM;
-    const uint32_t HW4 = static_cast<uint32_t>(g.H) * g.W * 4;
-    // the epilogue part of wave w and of wave w + 4 (the last tile's outputs
-    // are finished by both: registers 0..7 by the helper, 8..15 by the other)
-    const int eh = (wave & 3) >> 1, ef = wave & 1;
-
-    // phase -1: all 512 threads stage tile 0's patch (at most 2 items each)
-    PipeStager<MAXI <= 2 ? 1 : 2> first;
-    first.init(g, tid, 512, patch, chunk_elems, HW4);
-    auto load_first = [&]() __attribute__((always_inline)) {
-        int n, oh0, ow0;
-        pipe_tile_origin<Cfg>(g, t0, n, oh0, ow0);
-        first.load(x, g, n, oh0, ow0, HW4);
-    };
-
-    if (wave < 4) {
-        // ---- multiply waves ----
-        const int kgrp = wave >> 1, h = wave & 1;
-        const int wm = Cfg::WAVES_M == 2 ? h : 0, wq = Cfg::WAVES_Q == 2 ? h : 0;
-        const int kg = lane >> 5;
-        uint32_t ones;
-        asm volatile("v_mov_b32 %0, 0x3f803f80" : "=v"(ones));
-        // this lane's two weight rows, chunk kgrp, all nine taps (rows past
-        // the allocation read other words or zero: never stored)
-        constexpr uint32_t kWordBytes = TERNARY ? 8 : 4;
-        const __amdgpu_buffer_rsrc_t w_rs =
-            make_rsrc(wbits, static_cast<uint64_t>(m_alloc) * g.chunks * g.taps * kWordBytes);
-        uint2 wr[2][9];
-#pragma unroll
-        for (int f = 0; f < 2; ++f)
-#pragma unroll
-            for (int tap = 0; tap < 9; ++tap) {
-                const uint32_t row = static_cast<uint32_t>(m0 + wm * 64 + f * 32 + (lane & 31));
-                const uint32_t o = ((static_cast<uint32_t>(kgrp * 9 + tap)) * static_cast<uint32_t>(m_alloc) + row) *
-                                   kWordBytes;
-                if (TERNARY) {
-                    wr[f][tap] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(w_rs, o, 0, 0));
-                } else {
-                    wr[f][tap] = make_uint2(__builtin_amdgcn_raw_buffer_load_b32(w_rs, o, 0, 0), 0u);
-                }
-            }
-        // the patch loads after the weight words: the decode waits for the
-        // words only and runs while the patch is in flight
-        load_first();
-        u32x4_t A[9][2][2];
-#pragma unroll
-        for (int tap = 0; tap < 9; ++tap)
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                for (int f = 0; f < 2; ++f) A[tap][kk][f] = weight_frag<TERNARY>(wr[f][tap], kk, kg, ones);
-        first.store(lds, plane_elems);
-        // the decoded fragments are complete here, not recomputed after the
-        // barrier where they would delay the first tile's MFMAs
-#pragma unroll
-        for (int tap = 0; tap < 9; ++tap)
-#pragma unroll
-            for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-                for (int f = 0; f < 2; ++f) asm volatile("" : "+v"(A[tap][kk][f]));
-        __syncthreads();  // phase -1: tile 0's patch is staged
-
-        const int tap_ds = g.dw * kPix;
-        const int tap_dr = g.dh * g.PWi * kPix;
-        for (int i = 0; i < nt; ++i) {
-            int n, oh0, ow0;
-            pipe_tile_origin<Cfg>(g, t0 + i, n, oh0, ow0);
-            int oh, ow, pi, im;
-            tile_pixel<Cfg>(g, 0, oh0, ow0, wq * 32 + (lane & 31), oh, ow, pi, im);
-            const uint16_t* cur = lds + (i & 1) * buf_elems + kgrp * chunk_elems + pi * kPix + kg * 8;
-            auto read_b = [&](int s, u32x4_t (&b)[3]) __attribute__((always_inline)) {
-                const int tap = s >> 1, kk = s & 1;
-                const int toff = (tap / 3) * tap_dr + (tap % 3) * tap_ds + kk * 16;
-#pragma unroll
-                for (int p = 0; p < 3; ++p) b[p] = *reinterpret_cast<const u32x4_t*>(cur + p * plane_elems + toff);
-            };
-            f32x16_t acc[2];
-#pragma unroll
-            for (int f = 0; f < 2; ++f)
-#pragma unroll
-                for (int e = 0; e < 16; ++e) acc[f][e] = 0.0f;
-            // pixel fragments two K steps ahead
-            u32x4_t bq[3][3];
-            read_b(0, bq[0]);
-            read_b(1, bq[1]);
-#pragma unroll
-            for (int s = 0; s < 18; ++s) {
-                const int tap = s >> 1, kk = s & 1;
-                if (s + 2 < 18) read_b(s + 2, bq[(s + 2) % 3]);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int p = 0; p < 3; ++p)
-#pragma unroll
-                    for (int f = 0; f < 2; ++f) acc[f] = mfma32(A[tap][kk][f], bq[s % 3][p], acc[f]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            // hand both fragments to the helper waves: [group][h][fragment][e4][lane][4]
-            float* dst = accbuf + (i & 1) * kPipeAccFloats + ((kgrp * 2 + h) * 2) * (4 * 64 * 4) + lane * 4;
-#pragma unroll
-            for (int f = 0; f < 2; ++f)
-#pragma unroll
-                for (int e4 = 0; e4 < 4; ++e4)
-                    *reinterpret_cast<float4*>(dst + (f * 4 + e4) * 256) =
-                        make_float4(acc[f][4 * e4], acc[f][4 * e4 + 1], acc[f][4 * e4 + 2], acc[f][4 * e4 + 3]);
-            __syncthreads();  // phase i
-        }
-        // the last tile's registers 8..15 of part (eh, ef)
-        pipe_finish<Cfg, TERNARY, 2, 2>(g, epi, accbuf + ((nt - 1) & 1) * kPipeAccFloats, epi_lds, m0, t0 + nt - 1, eh,
-                                        ef, lane);
-        return;
-    }
-
-    // ---- helper waves: staging and epilogue ----
-    const int htid = tid - 256;
-    {
-        // per-channel epilogue factors (empty ranges for null pointers read 0)
-        const uint32_t mofs = static_cast<uint32_t>(min(m0 + min(htid, Cfg::BM - 1), g.M - 1)) * 4;
-        const __amdgpu_buffer_rsrc_t s_rs = make_rsrc(epi.scale, epi.scale ? static_cast<uint64_t>(g.M) * 4 : 0);
-        const __amdgpu_buffer_rsrc_t b_rs = make_rsrc(epi.bias, epi.bias ? static_cast<uint64_t>(g.M) * 4 : 0);
-        const float raw_scale = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s_rs, mofs, 0, 0));
-        const float raw_bias = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(b_rs, mofs, 0, 0));
-        if (htid < Cfg::BM) {
-            epi_lds[htid] = epi.alpha * (epi.scale ? raw_scale : 1.0f);
-            epi_lds[Cfg::BM + htid] = raw_bias;
-        }
-    }
-    load_first();
-    PipeStager<MAXI> next;
-    next.init(g, htid, 256, patch, chunk_elems, HW4);
-    auto load_next = [&](int t) __attribute__((always_inline)) {
-        int n, oh0, ow0;
-        pipe_tile_origin<Cfg>(g, t, n, oh0, ow0);
-        next.load(x, g, n, oh0, ow0, HW4);
-    };
-    if (nt > 1) load_next(t0 + 1);
-    first.store(lds, plane_elems);
-    __syncthreads();  // phase -1
-    for (int i = 0; i < nt; ++i) {
-        if (i + 1 < nt) {
-            next.store(lds + ((i + 1) & 1) * buf_elems, plane_elems);
-            if (i + 2 < nt) load_next(t0 + i + 2);
-        }
-        if (i >= 1)
-            pipe_finish<Cfg, TERNARY, 0, 4>(g, epi, accbuf + ((i - 1) & 1) * kPipeAccFloats, epi_lds, m0, t0 + i - 1,
-                                            eh, ef, lane);
-        __syncthreads();  // phase i
-    }
-    // the last tile's registers 0..7 of part (eh, ef)
-    pipe_finish<Cfg, TERNARY, 0, 2>(g, epi, accbuf + ((nt - 1) & 1) * kPipeAccFloats, epi_lds, m0, t0 + nt - 1, eh, ef,
-                                    lane);
-}
-
 // Split-K sum and epilogue: y = the kernel's epilogue applied to the splits'
 // raw sums added in split order (element i of the [N][M][OH * OW] output).
 __global__ void __launch_bounds__(256) conv_splitk_reduce_kernel(const float* __restrict__ partial, int splits,
@@ -1369,13 +1017,9 @@ struct TileChoice {
     int single;  // 1: one LDS buffer
     int kg;      // K groups of waves (PatchCfg::KG)
     int WM, WQ;  // wave tile (PatchCfg::WM, WQ)
-    int pipe;    // 1: conv_pipe_kernel (cfg indexes the PipeCfg menu)
 };
 
 size_t lds_bytes(const PatchGeom& g, int BM, bool ternary, int kg = 1) {
-    if (g.pipe)  // two patch buffers, two hand-over buffers, epilogue factors
-        return 2 * static_cast<size_t>(pipe_buffer_elems(g.PHi * g.PWi)) * 2 + 2 * kPipeAccFloats * sizeof(float) +
-               2 * sizeof(float) * BM;
     // (a fused projection's words follow the conv's table)
     const size_t buf =
         static_cast<size_t>(patch_buffer_elems(g.PHi * g.PWi, BM * g.taps, ternary ? 4 : 2) + (g.proj ? BM * (ternary ? 4 : 2) : 0)) * 2;
@@ -1413,7 +1057,6 @@ void set_dividers(PatchGeom& g) {
 }
 
 void fill_patch(PatchGeom& g, const TileChoice& c) {
-    g.pipe = c.pipe;
     g.linear = c.linear;
     g.single = c.single;
     g.rowperm = 0;
@@ -1480,7 +1123,7 @@ using P7 = PatchCfg<64, 8, 8, 64, 32>;    // 64 channels per wave: each pixel fr
 using P8 = PatchCfg<64, 8, 16, 64, 32>;
 using P9 = PatchCfg<128, 8, 8, 32, 32>;   // 8 waves: two per SIMD share a tile
 using P10 = PatchCfg<32, 14, 16, 32, 32>; // linear: 224 pixels, a whole 14 x 14 (or smaller) image, 7 waves
-// two K groups (layers of exactly two chunks, 33..64 input channels)
+// two K groups (a folded pair of chunk groups)
 using P11 = PatchCfg<128, 8, 8, 64, 32, 2>;
 using P12 = PatchCfg<64, 8, 8, 32, 32, 2>;
 using P13 = PatchCfg<64, 8, 16, 64, 32, 2>;
@@ -1489,27 +1132,14 @@ using P15 = PatchCfg<64, 8, 8, 64, 32, 2>;
 
 template <class Cfg>
 constexpr TileChoice choice(int cfg, int linear, int single = 0) {
-    return TileChoice{cfg, linear, Cfg::TH, Cfg::TW, Cfg::BM, Cfg::NT, single, Cfg::KG, Cfg::WM, Cfg::WQ, 0};
-}
-
-// The pipelined kernel's menu (two-chunk 3x3 layers): BM x (TH x TW) tiles
-// whose K group is two 64 x 32 multiply waves.
-using Q0 = PipeCfg<128, 2, 16>;  // two whole rows of images up to 16 wide: 4*OW-byte output runs
-using Q1 = PipeCfg<128, 4, 8>;
-using Q2 = PipeCfg<64, 8, 8>;
-using Q3 = PipeCfg<64, 4, 16>;
-
-template <class Cfg>
-constexpr TileChoice pipe_choice(int cfg) {
-    return TileChoice{cfg, 0, Cfg::TH, Cfg::TW, Cfg::BM, Cfg::NT, 0, 2, 64, 32, 1};
+    return TileChoice{cfg, linear, Cfg::TH, Cfg::TW, Cfg::BM, Cfg::NT, single, Cfg::KG, Cfg::WM, Cfg::WQ};
 }
 
 // The TBN_TUNE_CONV_TILE control forces one tile: id = cfg for linear tiles,
 // 16 + cfg for 2-D tiles, plus 32 for the one-buffer variants, plus 64 for
-// stacked tiles; 128 + cfg for the pipelined kernel's tiles.
+// stacked tiles.
 int tile_override() { return tbn_hip::tuning(TBN_TUNE_CONV_TILE); }
 int tile_id(const TileChoice& c) {
-    if (c.pipe) return 128 + c.cfg;
     return (c.linear == 1 ? c.cfg : c.linear == 0 ? 16 + c.cfg : 64 + c.cfg) + 32 * c.single;
 }
 
@@ -1536,44 +1166,17 @@ constexpr TileChoice kMenu[] = {// stacked linear tiles (stride 1): output runs 
                                 choice<P9>(9, 0, 1), choice<P10>(10, 1), choice<P10>(10, 1, 1),
                                 choice<P11>(11, 1), choice<P12>(12, 1), choice<P13>(13, 1), choice<P14>(14, 1),
                                 choice<P15>(15, 1), choice<P11>(11, 0), choice<P12>(12, 0), choice<P13>(13, 0),
-                                choice<P15>(15, 0),
-                                // the pipelined kernel: chosen by measurement or when forced
-                                pipe_choice<Q0>(0), pipe_choice<Q1>(1), pipe_choice<Q2>(2), pipe_choice<Q3>(3)};
-
-// A tile can run this geometry: its patch fits the LDS and the staging
-// registers (8 items per thread for the patch and for the weight words).
-// Layers of exactly two chunks (33..64 input channels), 3x3, one K split:
-// two K groups of waves.  Decided by the shape alone, and every tile of a
-// class sums in the same order, so the tile choice never changes a result.
-bool two_group_shape(const PatchGeom& g) { return g.chunks == 2 && g.taps == 9 && g.splits == 1; }
-
-// Blocks of a pipelined launch: about one per CU, each taking a run of
-// per_block consecutive pixel tiles of one channel tile.
-struct PipeGrid {
-    int tiles_pix, per_block, blocks_pix, blocks;
-};
-PipeGrid pipe_grid(const PatchGeom& g, int BM) {
-    PipeGrid p;
-    p.tiles_pix = g.N * g.tiles_img;
-    const int tiles_m = (g.M + BM - 1) / BM;
-    const int64_t total = static_cast<int64_t>(p.tiles_pix) * tiles_m;
-    p.per_block = static_cast<int>(std::max<int64_t>(1, tbn_hip::ceil_div(total, tbn_hip::cu_count())));
-    p.blocks_pix = static_cast<int>(tbn_hip::ceil_div(p.tiles_pix, p.per_block));
-    p.blocks = p.blocks_pix * tiles_m;
-    return p;
-}
+                                choice<P15>(15, 0)};
 
 // The tiles built with a fused projection (launch_patch_items): 8 x 8
-// tiles on one K group of waves (two groups would sum the projection's
-// chunks in group order, not in the 1x1 conv's, so two-chunk layers, which
-// take two groups, run their projection apart), not the pipelined kernel, at
-// most four staging items per thread.  Measured: the fused pair takes
+// tiles on one K group of waves (two groups, as folded chunk pairs take,
+// would sum the projection's chunks in group order, not in the 1x1 conv's),
+// at most four staging items per thread.  Measured: the fused pair takes
 // ResNet-18's stride-2 stage-3 / stage-4 pairs from 31.5 / 39 us to 27.2 /
-// 33 us at batch 32; its stage-2 pair (two chunks) on the two-group tiles
-// measured 52 us against 35 us apart.
+// 33 us at batch 32.
 bool proj_tile_ok(const PatchGeom& g, const TileChoice& c, const PatchGeom& t) {
     const bool cfg_ok = c.cfg == 1 || c.cfg == 3 || c.cfg == 9;
-    return cfg_ok && c.kg == 1 && !c.pipe && g.taps == 9 && 4 * t.PHi * t.PWi <= 4 * c.NT;
+    return cfg_ok && c.kg == 1 && g.taps == 9 && 4 * t.PHi * t.PWi <= 4 * c.NT;
 }
 
 bool tile_fits_base(const PatchGeom& g, const TileChoice& c, PatchGeom& t);
@@ -1589,7 +1192,7 @@ bool tile_fits_base(const PatchGeom& g, const TileChoice& c, PatchGeom& t) {
         // summing the groups in turn, or (exactly two equal groups) two K
         // groups of waves, one per group, whose sums are added in group order
         const bool pair = g.chunks == 2 * g.gchunks;
-        if (c.pipe || g.taps != 9 || (c.kg != 1 && !(c.kg == 2 && pair))) return false;
+        if (g.taps != 9 || (c.kg != 1 && !(c.kg == 2 && pair))) return false;
         if (c.linear == 2 && !stacked_ok(g, c.BM)) return false;
         t = g;
         fill_patch(t, c);
@@ -1598,24 +1201,14 @@ bool tile_fits_base(const PatchGeom& g, const TileChoice& c, PatchGeom& t) {
         return lds_bytes(t, c.BM, true, c.kg) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= 2 * c.NT &&
                c.BM * t.taps <= 8 * c.NT && red_fits && !c.single;
     }
-    if ((c.kg == 2) != two_group_shape(g)) return false;
-    if (c.pipe) {
-        // both chunks of a tile's patch staged by 256 helper threads, at most
-        // four items each; no fused pool, no K split (two_group_shape)
-        if (g.pool) return false;
-        t = g;
-        fill_patch(t, c);
-        return lds_bytes(t, c.BM, true) <= static_cast<size_t>(kMaxLds) && 8 * t.PHi * t.PWi <= 4 * 256 &&
-               static_cast<int64_t>(t.N) * t.tiles_img < (int64_t(1) << 30);
-    }
+    // two K groups of waves take folded chunk pairs only (above): every other
+    // conv sums its chunks in turn, on one K group, whatever the tile
+    if (c.kg != 1) return false;
     if (c.linear == 2 && !stacked_ok(g, c.BM)) return false;
     t = g;
     fill_patch(t, c);
-    const size_t bufs = lds_bytes(t, c.BM, true, c.kg) - 2 * sizeof(float) * c.BM;
-    const bool red_fits = c.kg == 1 || static_cast<size_t>(c.BM) * c.TH * c.TW * 4 <= bufs;
-    const int stage_items = c.kg == 1 ? 8 : 4;  // staging registers per thread (MAXI)
-    return lds_bytes(t, c.BM, true, c.kg) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= stage_items * c.NT &&
-           c.BM * t.taps <= 8 * c.NT && red_fits && (c.kg == 1 || !c.single);
+    return lds_bytes(t, c.BM, true) <= static_cast<size_t>(kMaxLds) && 4 * t.PHi * t.PWi <= 8 * c.NT &&
+           c.BM * t.taps <= 8 * c.NT;
 }
 
 bool choose_tile(PatchGeom& g, TileChoice& out) {
@@ -1625,7 +1218,6 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
     for (const auto& c : kMenu) {
         const int id = tile_id(c);
         if (forced >= 0 && id != forced) continue;
-        if (forced < 0 && c.pipe) continue;  // the pipelined kernel is taken by measurement
         if (forced < 0) {
             if (g.M <= 32 && c.BM != 32) continue;
             if (g.M > 32 && c.BM == 32) continue;
@@ -1633,7 +1225,7 @@ bool choose_tile(PatchGeom& g, TileChoice& out) {
         }
         PatchGeom t;
         if (!tile_fits(g, c, t)) continue;
-        const int64_t blocks = c.pipe ? pipe_grid(t, c.BM).blocks : patch_tiles(t) * ((g.M + c.BM - 1) / c.BM);
+        const int64_t blocks = patch_tiles(t) * ((g.M + c.BM - 1) / c.BM);
         if (forced >= 0 || blocks >= 240) {
             out = c;
             g = t;
@@ -1745,57 +1337,10 @@ int dispatch_patch(int id, const float* x, const PatchGeom& g, const uint8_t* w,
     }
 }
 
-template <class Cfg, bool TERNARY, int MAXI>
-int launch_pipe_items(const float* x, const PatchGeom& g, const uint8_t* w, int m_alloc, const PatchEpi& epi,
-                      hipStream_t s) {
-    const size_t lds = lds_bytes(g, Cfg::BM, TERNARY);
-    static bool attr_set = false;
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_pipe_kernel<Cfg, TERNARY, MAXI>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLds);
-        if (e != hipSuccess) return tbn_hip::fail(TBN_RUNTIME_ERROR, std::string("hipFuncSetAttribute: ") +
-                                                                         hipGetErrorString(e));
-        attr_set = true;
-    }
-    const PipeGrid p = pipe_grid(g, Cfg::BM);
-    hipLaunchKernelGGL((conv_pipe_kernel<Cfg, TERNARY, MAXI>), dim3(static_cast<unsigned>(p.blocks)), dim3(Cfg::NT),
-                       lds, s, x, g, w, m_alloc, epi, p.tiles_pix, p.per_block, p.blocks_pix);
-    return tbn_hip::check_launch(TERNARY ? "conv2d_f32_ternary (pipelined patch)" : "conv2d_f32_binary (pipelined patch)");
-}
-
-// Staging items per helper thread: the smallest of 2, 3, 4 that covers both
-// chunks' 8 * patch items.
-int pipe_items(const PatchGeom& g) { return std::max(2, (8 * g.PHi * g.PWi + 255) / 256); }
-
-template <class Cfg, bool TERNARY>
-int launch_pipe(const float* x, const PatchGeom& g, const uint8_t* w, int m_alloc, const PatchEpi& epi,
-                hipStream_t s) {
-    if (!g.pipe || g.splits != 1 || g.pool || epi.partial || g.chunks != 2 || g.taps != 9)
-        return tbn_hip::fail(TBN_INVALID_SHAPE, "the pipelined conv takes unpooled two-chunk 3x3 layers");
-    switch (pipe_items(g)) {
-        case 2: return launch_pipe_items<Cfg, TERNARY, 2>(x, g, w, m_alloc, epi, s);
-        case 3: return launch_pipe_items<Cfg, TERNARY, 3>(x, g, w, m_alloc, epi, s);
-        case 4: return launch_pipe_items<Cfg, TERNARY, 4>(x, g, w, m_alloc, epi, s);
-        default: return tbn_hip::fail(TBN_INVALID_SHAPE, "conv patch too large for the pipelined kernel");
-    }
-}
-
-template <bool TERNARY>
-int dispatch_pipe(int id, const float* x, const PatchGeom& g, const uint8_t* w, int m_alloc, const PatchEpi& epi,
-                  hipStream_t s) {
-    switch (id) {
-        case 0: return launch_pipe<Q0, TERNARY>(x, g, w, m_alloc, epi, s);
-        case 1: return launch_pipe<Q1, TERNARY>(x, g, w, m_alloc, epi, s);
-        case 2: return launch_pipe<Q2, TERNARY>(x, g, w, m_alloc, epi, s);
-        default: return launch_pipe<Q3, TERNARY>(x, g, w, m_alloc, epi, s);
-    }
-}
-
 // Launches the kernel of tile choice c (g laid out for it by fill_patch).
 template <bool TERNARY>
 int run_choice(const TileChoice& c, const float* x, const PatchGeom& g, const uint8_t* w, int64_t col_bytes,
                int m_alloc, const PatchEpi& epi, hipStream_t s) {
-    if (c.pipe) return dispatch_pipe<TERNARY>(c.cfg, x, g, w, m_alloc, epi, s);
     return dispatch_patch<TERNARY>(c.cfg, x, g, w, col_bytes, m_alloc, epi, s);
 }
 
@@ -1956,7 +1501,6 @@ int make_patch_geom(const tbn_conv2d_desc* d, int flags, PatchGeom& g) {
     const bool forced = !g.pool && tbn_hip::tuning(TBN_TUNE_CONV_SPLITS) > 0;
     if (forced) splits = tbn_hip::tuning(TBN_TUNE_CONV_SPLITS);
     g.single = 0;
-    g.pipe = 0;
     g.proj = 0;
     g.gchunks = (g.chunks + splits - 1) / splits;
     const int groups = (g.chunks + g.gchunks - 1) / g.gchunks;
@@ -2263,11 +1807,6 @@ int tbn_hip_conv2d_kernel_name(int weights, const tbn_conv2d_desc* desc, int fla
     TileChoice tc;
     rc = weights == TBN_WEIGHTS_TERNARY ? select_tile<true>(desc, g, epi, tc) : select_tile<false>(desc, g, epi, tc);
     if (rc) return rc;
-    if (tc.pipe) {
-        std::snprintf(name, len, "conv_pipe_kernel<PipeCfg<%d, %d, %d>, %s, %d>", tc.BM, tc.TH, tc.TW,
-                      weights == TBN_WEIGHTS_TERNARY ? "true" : "false", pipe_items(g));
-        return tbn_hip::ok();
-    }
     // the launch's template arguments, as launch_patch / launch_patch_items pick them
     const int taps = (g.kh == 3 && g.kw == 3) ? 9 : 0;
     const int per_thread = (4 * g.PHi * g.PWi + tc.NT - 1) / tc.NT;

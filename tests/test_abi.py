@@ -69,7 +69,7 @@ def test_conv_kernel_name_is_host_only():
     name = buf.value.decode()
     # 3x3 taps: the staging items per thread are the smallest of 1, 2, 4, 8 that covers the patch
     assert name.startswith("conv_patch_kernel<PatchCfg<") and re.search(r">, false, 9, [1248], false, false>$", name), name
-    assert name.count(",") == 10 and ", 2>" in name, name  # two chunks of 32 channels: two K groups
+    assert name.count(",") == 10 and ", 1>" in name, name  # two chunks of 32 channels, summed in turn
     assert lib.tbn_hip_conv2d_kernel_name(1, ctypes.byref(d), 0, 1, buf, len(buf)) == 0
     assert re.search(r">, true, 9, [1248], false, false>$", buf.value.decode()), buf.value.decode()
     d5 = tbn_hip.conv_desc(2, 96, 19, 23, 72, 5, 5, 1, 2, 2, 2)  # a 5x5 kernel: the any-size variant

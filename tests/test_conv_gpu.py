@@ -419,8 +419,8 @@ def test_conv_patch_split_k_residual_and_ternary(dev, orc):
                                   (2, 256, 14, 14, 128, 3, 3, (1, 1), (1, 1), (1, 1), tbn_hip.EPI_BIAS_THEN_SCALE)])
 def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
     """Each tile of the menu (forced with the conv-tile control: linear, 2-D
-    and stacked tiles, with two LDS buffers or one, and the pipelined kernel's
-    tiles) sums every output in the same order, so all feasible tiles give
+    and stacked tiles, with two LDS buffers or one) sums every output in the
+    same order, so all feasible tiles give
     bit-identical outputs; one of them is checked against the float64 oracle."""
     N, C, H, W, M, kh, kw, stride, pad, dil, flags = case
     rng = np.random.default_rng(C * 17 + M)
@@ -440,7 +440,7 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
     tbn_hip.call("tbn_hip_pack_conv_weights", tbn_hip.WEIGHTS_BINARY, P(packed), K_pad, N_pad, d, P(cw), None)
     dx, ds, db = to_dev(x), to_dev(scale), to_dev(bias)
     outs = {}
-    for tile in list(range(128)) + PIPE_TILES:
+    for tile in range(128):
         with tbn_hip.tuning(tbn_hip.TUNE_CONV_TILE, tile):
             y = empty(oshape, torch.float32)
             y.fill_(np.nan)
@@ -451,101 +451,16 @@ def test_conv_patch_every_tile_gives_the_same_bits(dev, orc, case):
                 continue  # this tile cannot hold the geometry
             assert rc == 0, tbn_hip.last_error()
             outs[tile] = host(y)
-    two_groups = (C + 31) // 32 == 2 and kh * kw == 9  # two K groups of waves: no one-buffer tiles
     assert len(outs) >= 2, sorted(outs)
-    if not two_groups:
-        assert any(32 <= t < 64 or t >= 96 for t in outs) and any(t < 32 or 64 <= t < 96 for t in outs), sorted(outs)
+    assert any(32 <= t < 64 or t >= 96 for t in outs) and any(t < 32 or 64 <= t < 96 for t in outs), sorted(outs)
     stacked = stride == (1, 1) and C % 32 == 0 and M % 64 == 0 and not flags & tbn_hip.EPI_MAXPOOL2X2
     assert any(64 <= t < 128 for t in outs) == stacked, sorted(outs)
-    pipelined = two_groups and not flags & tbn_hip.EPI_MAXPOOL2X2
-    assert any(t >= 128 for t in outs) == pipelined, sorted(outs)
     first = next(iter(outs.values()))
     for tile, y in outs.items():
         assert np.array_equal(y, first), f"tile {tile} differs"
     wsign = np.where(wbytes == 1, 1.0, -1.0).astype(np.float32)
     ref = conv_ref(x, wsign, scale, 1.0, bias, stride, pad, dil, flags)
     rm.assert_within_tolerance(first, ref, K, np.abs(x).max() * 1.5)
-
-
-# the pipelined kernel's tiles (conv-tile control ids 128 + menu index)
-PIPE_TILES = [128, 129, 130, 131]
-
-
-@pytest.mark.parametrize("case", [
-    # N, C, H, W, M, stride, pad, dil, flags, residual, ternary
-    (64, 64, 14, 14, 128, 1, 1, 1, tbn_hip.EPI_RELU, False, False),       # config 4
-    (32, 64, 28, 28, 128, 1, 1, 1, tbn_hip.EPI_RELU, True, False),        # four or more tiles per block
-    (3, 48, 13, 11, 96, 1, 1, 1, tbn_hip.EPI_BIAS_THEN_SCALE, False, True),  # partial chunk, ragged M, ternary
-    (4, 64, 28, 28, 72, 1, 1, 1, tbn_hip.EPI_RELU, True, True),           # M below a channel tile, ternary
-    (2, 40, 17, 9, 160, 1, 2, 2, 0, False, False),                        # dilation 2, two channel tiles
-    (9, 64, 56, 56, 64, 1, 1, 1, tbn_hip.EPI_RELU, True, False),          # ResNet stage 1 shape
-], ids=["cfg4", "deep", "ternary", "ragged_m", "dil2", "resnet1"])
-def test_conv_pipelined_matches_patch_kernel(dev, case):
-    """The pipelined kernel (multiply waves with register-held weights, helper
-    waves staging the next tile and finishing the previous one) gives the
-    patch kernel's bits on every tile of its menu: binary and ternary weights,
-    residual, bias-then-scale, partial input chunks, ragged channel counts,
-    stride and dilation, runs of many tiles per block; one output is checked
-    against the float64 oracle."""
-    import ctypes
-    N, C, H, W, M, st, pd, dl, flags, with_res, ternary = case
-    rng = np.random.default_rng(N * 7 + C + M)
-    x = rng.standard_normal((N, C, H, W)).astype(np.float32)
-    scale = rng.uniform(0.5, 1.5, M).astype(np.float32)
-    bias = (rng.standard_normal(M) * 0.01).astype(np.float32)
-    K = C * 9
-    d = tbn_hip.conv_desc(N, C, H, W, M, 3, 3, st, st, pd, pd, dl, dl)
-    OH, OW = tbn_hip.conv_out_hw(d)
-    res = rng.standard_normal((N, M, OH, OW)).astype(np.float32) if with_res else None
-    if ternary:
-        kind = tbn_hip.WEIGHTS_TERNARY
-        wt = rng.integers(-1, 2, (M, K)).astype(np.int8)
-        K_pad, N_pad = (K + 31) // 32 * 32, M
-        packed = empty(M * K_pad // 4, torch.uint8)
-        tbn_hip.call("tbn_hip_pack_ternary", P(to_dev(wt)), K, M, tbn_hip.LAYOUT_NK, K_pad, M, P(packed), None)
-        wref = wt.reshape(M, C, 3, 3).astype(np.float32)
-    else:
-        kind = tbn_hip.WEIGHTS_BINARY
-        wbytes = (rng.random((M, C, 3, 3)) < 0.5).astype(np.uint8)
-        packed, K_pad, N_pad = pack_conv_weights(wbytes, M, K)
-        wref = np.where(wbytes == 1, 1.0, -1.0).astype(np.float32)
-    wb = ctypes.c_int64()
-    tbn_hip.call("tbn_hip_conv_weights_bytes", kind, d, ctypes.byref(wb))
-    cw = empty(wb.value, torch.uint8)
-    tbn_hip.call("tbn_hip_pack_conv_weights", kind, P(packed), K_pad, N_pad, d, P(cw), None)
-    dx, ds, db = to_dev(x), to_dev(scale), to_dev(bias)
-    dr = to_dev(res) if with_res else None
-
-    def run():
-        y = empty((N, M, OH, OW), torch.float32)
-        y.fill_(np.nan)
-        rc = tbn_hip.lib().tbn_hip_conv2d_f32_prepacked(kind, P(dx), d, P(cw), P(ds), 1.0, P(db),
-                                                        P(dr) if with_res else None, flags, P(y), None)
-        return rc, y
-
-    rc, y = run()  # the static rule: the two-group patch kernel
-    assert rc == 0, tbn_hip.last_error()
-    want = host(y)
-    ran = []
-    for tile in PIPE_TILES:
-        with tbn_hip.tuning(tbn_hip.TUNE_CONV_TILE, tile):
-            rc, y = run()
-            if rc == tbn_hip.INVALID_SHAPE:
-                continue  # the patch does not fit this tile's buffers
-            assert rc == 0, tbn_hip.last_error()
-            name = ctypes.create_string_buffer(160)
-            assert tbn_hip.lib().tbn_hip_conv2d_kernel_name(kind, d, flags, int(with_res), name, 160) == 0
-            assert name.value.decode().startswith("conv_pipe_kernel<"), name.value
-            got = host(y)
-            assert np.array_equal(got, want), f"pipelined tile {tile} differs"
-            ran.append(tile)
-    assert ran and (dl > 1 or len(ran) >= 2), ran  # dilation leaves one tile's patch in the buffers
-    ref = conv_ref(x, wref, scale, 1.0, bias, (st, st), (pd, pd), (dl, dl), flags & tbn_hip.EPI_BIAS_THEN_SCALE)
-    if with_res:
-        ref = ref + res
-    if flags & tbn_hip.EPI_RELU:
-        ref = np.maximum(ref, 0.0)
-    rm.assert_within_tolerance(want, ref, K, np.abs(x).max() * 1.5)
 
 
 @pytest.mark.parametrize("case", [(32, 512, 7, 7, 512, False, True), (128, 256, 7, 7, 128, True, True),
@@ -681,6 +596,7 @@ def test_conv_forced_splits_skip_pooled_convs(dev):
 
 PAIR_CASES = [
     # N, C, H, W, M, stride, ternary, flags, proj_flags, with_residual
+    (4, 64, 56, 56, 128, 2, False, tbn_hip.EPI_RELU, 0, False),       # two chunks
     (4, 128, 28, 28, 256, 2, False, tbn_hip.EPI_RELU, 0, False),      # four chunks in turn
     (32, 256, 14, 14, 512, 2, False, tbn_hip.EPI_RELU, 0, False),     # chunk groups folded into one block
     (2, 72, 20, 18, 72, 2, True, tbn_hip.EPI_RELU, tbn_hip.EPI_BIAS_THEN_SCALE, True),  # ternary, ragged C / M
@@ -712,7 +628,7 @@ def _conv_layout(kind, rng, M, C, k):
     return layout, wref
 
 
-@pytest.mark.parametrize("case", PAIR_CASES, ids=["chunks", "folded", "ternary", "stride1"])
+@pytest.mark.parametrize("case", PAIR_CASES, ids=["two_chunks", "chunks", "folded", "ternary", "stride1"])
 def test_conv_pair_matches_separate_convs(dev, case):
     """A 3x3 pad-1 conv and the 1x1 projection of its input in one launch give
     the bits of the two separate calls, for the tuned tile and every tile that
@@ -773,11 +689,10 @@ def test_conv_pair_matches_separate_convs(dev, case):
 
 
 def test_conv_pair_declines_split_and_other_shapes(dev):
-    """Geometries that split K over blocks (few images of a deep layer), take
-    two K groups (two chunks), or have another kernel size or padding return
-    TBN_NOT_IMPLEMENTED without work."""
+    """Geometries that split K over blocks (few images of a deep layer) or
+    have another kernel size or padding return TBN_NOT_IMPLEMENTED without
+    work."""
     for d in (tbn_hip.conv_desc(2, 256, 14, 14, 512, 3, 3, 2, 2, 1, 1),   # K split at batch 2
-              tbn_hip.conv_desc(4, 64, 56, 56, 128, 3, 3, 2, 2, 1, 1),    # two chunks
               tbn_hip.conv_desc(2, 64, 16, 16, 64, 5, 5, 1, 1, 2, 2),     # 5x5
               tbn_hip.conv_desc(2, 64, 16, 16, 64, 3, 3, 1, 1, 0, 0)):    # pad 0
         with pytest.raises(tbn_hip.TbnError) as e:
