@@ -282,6 +282,126 @@ int launch_small_gemm(SmallGemm g, const GemmEpi& epi, hipStream_t s) {
     return tbn_hip::check_launch("gemm (small)");
 }
 
+// ---- many columns, moderate K (a classifier over a batch: 32 x 512 -> 1000) --
+// With K split over MFMA tiles such a product is mostly staging at small batch: each block
+// splits a 64 x 64 tile of both operands into bf16 planes for one 64-deep
+// slice of K, and a second launch adds the slices.  Here a block owns
+// kRowsR rows x kRowsC columns of C in one launch.  It stages chunks of up
+// to kRowsKC values of k of those rows of op(A) and columns of op(B) in LDS
+// as fp32 (every load of a chunk in flight before the first store; zeros
+// past the end), and kRowsS lanes compute each output: lane l runs an fp32
+// FMA chain over the 4-value groups l, l + kRowsS, ... of every chunk in
+// turn, and the lanes are added in a fixed butterfly.  The order depends on
+// K only, so a row's result does not depend on how many rows the call has.
+constexpr int kRowsR = 16, kRowsC = 4, kRowsS = 4, kRowsKC = 512;
+// rows 16 floats past the chunk: a wave's 16 distinct 16-byte reads (4 rows x
+// 4 lanes) fall on disjoint banks
+constexpr int kRowsPitch = kRowsKC + 16;
+static_assert(kRowsR * kRowsC * kRowsS == 256, "one output per kRowsS lanes of the block");
+
+struct RowsGemm {
+    const float* A;
+    int64_t a_row, a_k;  // element (m, k) at A[m*a_row + k*a_k]
+    const float* B;
+    int64_t b_k, b_col;  // element (k, n) of op(B) at B[k*b_k + n*b_col]
+    int M, N, K;
+    int a_vec, b_vec;    // k contiguous and 16-byte aligned rows: float4 loads
+};
+
+// From N and K only (not M), so a row's result never depends on the batch:
+// more than a small GEMM's columns, at most 4096 of them, and 256 <= K <= 4096.
+bool rows_gemm_fits(int64_t N, int64_t K) { return N > 64 && N <= 4096 && K >= 256 && K <= 4096; }
+
+// Stage a rows x kRowsKC chunk (k0 .. k0 + kl) of an operand into
+// dst[rows][kRowsPitch]; values past kl or past the last row are zero.  Every
+// load reads a clamped, in-range address and the value is dropped afterwards,
+// so all of a thread's loads are issued before the first wait.  Strided
+// operands walk the contiguous dimension across lanes.
+template <int ROWS>
+__device__ __forceinline__ void rows_stage(float (*dst)[kRowsPitch], const float* base, int64_t s_row, int64_t s_k,
+                                           int row0, int rows_valid, int k0, int kl, bool vec) {
+    const int tid = static_cast<int>(threadIdx.x);
+    if (vec) {  // s_k == 1, kl a multiple of 4, 16-byte aligned rows
+        constexpr int kGroups = ROWS * (kRowsKC / 4);
+        constexpr int kPer = (kGroups + 255) / 256;
+        float4 v[kPer];
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int gi = min(j * 256 + tid, kGroups - 1), rr = gi / (kRowsKC / 4), q = (gi % (kRowsKC / 4)) * 4;
+            const int row = min(row0 + rr, rows_valid - 1), qc = min(q, kl - 4);
+            v[j] = *reinterpret_cast<const float4*>(base + static_cast<int64_t>(row) * s_row + k0 + qc);
+        }
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) {
+            const int gi = j * 256 + tid, rr = gi / (kRowsKC / 4), q = (gi % (kRowsKC / 4)) * 4;
+            if (gi >= kGroups) continue;
+            if (row0 + rr >= rows_valid || q >= kl) v[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            *reinterpret_cast<float4*>(&dst[rr][q]) = v[j];
+        }
+        return;
+    }
+    constexpr int kElems = ROWS * kRowsKC;
+    constexpr int kBatch = 16;
+    const bool rows_fast = s_row == 1;  // consecutive rows adjacent in memory
+    for (int base_i = 0; base_i < kElems; base_i += 256 * kBatch) {
+        float v[kBatch];
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int i = min(base_i + j * 256 + tid, kElems - 1);
+            const int rr = rows_fast ? i % ROWS : i / kRowsKC, k = rows_fast ? i / ROWS : i % kRowsKC;
+            const int row = min(row0 + rr, rows_valid - 1), kk = min(k, kl - 1);
+            v[j] = base[static_cast<int64_t>(row) * s_row + static_cast<int64_t>(k0 + kk) * s_k];
+        }
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+            const int i = base_i + j * 256 + tid;
+            if (i >= kElems) continue;
+            const int rr = rows_fast ? i % ROWS : i / kRowsKC, k = rows_fast ? i / ROWS : i % kRowsKC;
+            dst[rr][k] = (row0 + rr < rows_valid && k < kl) ? v[j] : 0.0f;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256) rows_gemm_kernel(RowsGemm g, GemmEpi epi) {
+    __shared__ __align__(16) float as[kRowsR][kRowsPitch];
+    __shared__ __align__(16) float bs[kRowsC][kRowsPitch];
+    const int tiles_c = (g.N + kRowsC - 1) / kRowsC;
+    const int m0 = static_cast<int>(blockIdx.x) / tiles_c * kRowsR;
+    const int n0 = static_cast<int>(blockIdx.x) % tiles_c * kRowsC;
+    const int t = static_cast<int>(threadIdx.x), sl = t % kRowsS, o = t / kRowsS;
+    const int r = o / kRowsC, c = o % kRowsC;
+    float acc = 0.0f;
+    for (int k0 = 0; k0 < g.K; k0 += kRowsKC) {
+        const int kl = min(kRowsKC, g.K - k0);
+        __syncthreads();  // the previous chunk is no longer read
+        rows_stage<kRowsR>(as, g.A, g.a_row, g.a_k, m0, g.M, k0, kl, g.a_vec);
+        rows_stage<kRowsC>(bs, g.B, g.b_col, g.b_k, n0, g.N, k0, kl, g.b_vec);
+        __syncthreads();
+        const float* a = as[r];
+        const float* b = bs[c];
+        // every group of the chunk, zeros past kl included: fmaf(0, 0, acc)
+        // is acc (acc starts at +0 and a sum is never -0), and a fixed trip
+        // count lets the LDS reads of eight steps issue together
+#pragma unroll 8
+        for (int q = sl; q < kRowsKC / 4; q += kRowsS) {
+            const float4 a4 = *reinterpret_cast<const float4*>(a + 4 * q);
+            const float4 b4 = *reinterpret_cast<const float4*>(b + 4 * q);
+            acc = fmaf(a4.x, b4.x, acc);
+            acc = fmaf(a4.y, b4.y, acc);
+            acc = fmaf(a4.z, b4.z, acc);
+            acc = fmaf(a4.w, b4.w, acc);
+        }
+    }
+    for (int d = 1; d < kRowsS; d <<= 1) acc += __shfl_xor(acc, d);
+    const int m = m0 + r, n = n0 + c;
+    if (sl != 0 || m >= g.M || n >= g.N) return;
+    // GemmEpi's arithmetic for one element (no scale, no bias on this path)
+    float v = acc * epi.alpha + 0.0f;
+    if (epi.cin) v += epi.beta * (epi.cin_1d ? epi.cin[n] : epi.cin[static_cast<int64_t>(m) * g.N + n]);
+    if (epi.flags & TBN_EPI_RELU) v = v > 0.0f ? v : 0.0f;
+    epi.C[static_cast<int64_t>(m) * epi.ldc + n] = v;
+}
+
 template <class Cfg, class ColL>
 int launch_gemm(const float* A, int64_t lda, int M, int N, int K, const ColL& coll,
                 const GemmEpi& epi, hipStream_t stream, const char* what) {
@@ -443,6 +563,18 @@ int tbn_hip_gemm_f32(const float* A, const float* B, const float* Cin, int c_is_
         const SmallGemm sg{A, transA ? 1 : K, transA ? M : 1, B, transB ? 1 : N, transB ? K : 1,
                            static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), 0, 0, 0, 0};
         return launch_small_gemm<0>(sg, epi, tbn_hip::stream_of(stream));
+    }
+    if (rows_gemm_fits(N, K)) {
+        const bool kvec = K % 4 == 0;
+        const RowsGemm rg{A, transA ? 1 : K, transA ? M : 1, B, transB ? 1 : N, transB ? K : 1,
+                          static_cast<int>(M), static_cast<int>(N), static_cast<int>(K),
+                          !transA && kvec && reinterpret_cast<uintptr_t>(A) % 16 == 0,
+                          transB && kvec && reinterpret_cast<uintptr_t>(B) % 16 == 0};
+        const int64_t blocks = tbn_hip::ceil_div(M, kRowsR) * tbn_hip::ceil_div(N, kRowsC);
+        TBN_REQUIRE(blocks < (1LL << 31), TBN_INVALID_SHAPE, "too many column tiles");
+        hipLaunchKernelGGL(rows_gemm_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                           tbn_hip::stream_of(stream), rg, epi);
+        return tbn_hip::check_launch("gemm_f32 (rows)");
     }
     const int tiles_r = static_cast<int>(tbn_hip::ceil_div(M, Cfg::BR));
     const int tiles_c = static_cast<int>(tbn_hip::ceil_div(N, Cfg::BC));

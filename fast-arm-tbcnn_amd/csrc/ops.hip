@@ -135,7 +135,9 @@ __global__ void __launch_bounds__(256) global_pool_kernel(const float* __restric
                                                           int64_t hw, float* __restrict__ y) {
     // a block owns 64 consecutive planes (contiguous in memory); each chunk
     // of 64 positions of all 64 planes is staged through LDS with coalesced
-    // loads, then thread p adds its plane's values in memory order
+    // loads, all 16 of a thread's issued before the first store (one memory
+    // latency per chunk, not 16), then thread p adds its plane's values in
+    // memory order
     __shared__ float tile[64][65];
     const int64_t p0 = static_cast<int64_t>(blockIdx.x) * 64;
     const int np = static_cast<int>(planes - p0 < 64 ? planes - p0 : 64);
@@ -143,9 +145,16 @@ __global__ void __launch_bounds__(256) global_pool_kernel(const float* __restric
     float acc = MAX ? -INFINITY : 0.0f;
     for (int64_t c0 = 0; c0 < hw; c0 += 64) {
         const int cl = static_cast<int>(hw - c0 < 64 ? hw - c0 : 64);
-        for (int idx = tid; idx < np * 64; idx += 256) {
-            const int pl = idx >> 6, i = idx & 63;
-            if (i < cl) tile[pl][i] = x[(p0 + pl) * hw + c0 + i];
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int idx = j * 256 + tid, pl = idx >> 6, i = idx & 63;
+            v[j] = (pl < np && i < cl) ? x[(p0 + pl) * hw + c0 + i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int idx = j * 256 + tid;
+            tile[idx >> 6][idx & 63] = v[j];
         }
         __syncthreads();
         if (tid < np)

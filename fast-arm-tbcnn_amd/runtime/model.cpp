@@ -225,6 +225,7 @@ struct Op {
     bool transA = false, transB = false;
     const float* cin = nullptr;    // constant addend (device) or null
     int cin_value = -1;            // or an activation addend
+    const float* bt = nullptr;     // a constant fp32 B kept as [N, K] (the launch passes transB)
     int cin_1d = 0;
     int dyn_b = -1;                // quantized Gemm whose B is packed on every run
     // pooling / elementwise
@@ -315,6 +316,22 @@ struct TBNModel::Session::Impl {
 
     std::vector<float> host_floats(const std::string& name) const {
         return initializer(name).to_vector<float>();
+    }
+
+    // A constant [K, N] fp32 matrix stored once as [N, K]: every fp32 GEMM
+    // kernel reads a column of op(B) as consecutive k then (16-byte loads
+    // along k), and the product is the same.
+    const float* transposed_init(const std::string& name, int64_t K, int64_t N) {
+        const std::string key = name + "#T";
+        auto it = dev_init.find(key);
+        if (it == dev_init.end()) {
+            const std::vector<float> b = host_floats(name);
+            std::vector<float> t(b.size());
+            for (int64_t k = 0; k < K; ++k)
+                for (int64_t n = 0; n < N; ++n) t[n * K + k] = b[k * N + n];
+            it = dev_init.emplace(key, Tensor(Shape{N, K}, DataType::FLOAT32, t.data(), DeviceType::HIP)).first;
+        }
+        return it->second.typed_data<float>();
     }
 
     // Per-channel mean|w| computed on the device with the Session's sequential
@@ -723,6 +740,7 @@ struct TBNModel::Session::Impl {
             op.in.push_back(bi);
             TBN_CHECK(values[bi].dtype == DataType::FLOAT32 && values[ai].dtype == DataType::FLOAT32,
                       InvalidArgumentError, "gemm requires float32 inputs");
+            if (values[bi].is_const && !op.transB) op.bt = transposed_init(node.inputs[1], op.K, op.N);
         }
         if (ci >= 0 && op.beta != 0.0f) {
             if (values[ci].is_const) op.cin = const_f32(ci);
@@ -1387,8 +1405,9 @@ struct TBNModel::Session::Impl {
             }
             case OpKind::GemmF32: {
                 const float* cin = op.cin ? op.cin : (op.cin_value >= 0 ? fp(op.cin_value) : nullptr);
-                check_status(tbn_hip_gemm_f32(fp(op.in[0]), fp(op.in[1]), cin, op.cin_1d, op.M, op.K, op.N, op.alpha,
-                                              cin ? op.beta : 0.0f, op.transA, op.transB, op.flags, fp(op.out), s),
+                check_status(tbn_hip_gemm_f32(fp(op.in[0]), op.bt ? op.bt : fp(op.in[1]), cin, op.cin_1d, op.M, op.K,
+                                              op.N, op.alpha, cin ? op.beta : 0.0f, op.transA, op.bt ? 1 : op.transB,
+                                              op.flags, fp(op.out), s),
                              what.c_str());
                 return;
             }

@@ -362,13 +362,16 @@ def test_gemm_f32_matches_blocked_reference(dev, orc):
                                    np.abs(A).max() * np.abs(B).max())
 
 
-def test_gemm_f32_split_k(dev, orc):
-    """K split over blocks (K >= 512, N <= 4096): 2-D addend, ReLU, transposed
-    operands and a K that leaves a short last split; rows are bit-identical
-    whatever the number of rows (the split count depends on N and K only)."""
+def test_gemm_f32_rows_and_split_k(dev, orc):
+    """The many-columns kernel (64 < N <= 4096, 256 <= K <= 4096: k chunks of
+    512 staged as fp32, float4 or strided loads, a K that leaves a short last
+    chunk) and K split over MFMA blocks (K > 4096, a short last split): 2-D
+    addend, ReLU, transposed operands; rows are bit-identical whatever the
+    number of rows (the path and the split count depend on N and K only)."""
     rng = np.random.default_rng(22)
     for (M, K, N, ta, tb, relu) in [(33, 600, 70, True, False, True), (5, 1030, 257, False, True, False),
-                                     (64, 512, 1000, False, True, True)]:
+                                     (64, 512, 1000, False, True, True), (96, 520, 130, False, False, False),
+                                     (40, 4616, 70, False, True, True)]:
         A = rng.standard_normal((K, M) if ta else (M, K)).astype(np.float32)
         B = rng.standard_normal((N, K) if tb else (K, N)).astype(np.float32)
         c2 = rng.standard_normal((M, N)).astype(np.float32)
