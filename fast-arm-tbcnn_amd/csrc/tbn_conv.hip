@@ -75,6 +75,15 @@ struct TbnConvArgs {
     const float* residual;  // same layout as y, or null
     int flags;
     float lo, hi;
+    // the fused 1x1 projection (PROJ): its fp4 weights (the layout of the
+    // 1x1 stride-s pad-0 desc: one k-step per chunk), its output (y's shape)
+    // and epilogue (no residual, no pool)
+    const uint8_t* proj_w4;
+    float* proj_y;
+    const float* proj_scale;
+    float proj_alpha;
+    const float* proj_bias;
+    int proj_flags;
 };
 
 // Stand-ins for an absent scale (1) or bias (0), so the epilogue's loads
@@ -313,8 +322,15 @@ __device__ __forceinline__ void tile_pixel(const TbnGeom& g, int p, int& r, int&
 // arrives, together with its wave's weight fragments for the chunk's first
 // GF taps and (once) the epilogue's scale and bias.  Every tap is then one
 // MFMA k-step read from the same records.
-template <int FC, int IPT, int GF>
-__global__ void __launch_bounds__(256) tbn_conv_fused_kernel(TbnGeom g, TbnConvArgs a) {
+//
+// PROJ (a 3x3 pad-1 conv, GF = 9, host-checked): the 1x1 stride-s projection
+// of the same input reads the centre tap's records, so the centre tap's
+// pixel fragments also feed one MFMA with the projection's weights per
+// chunk, into a second set of accumulators, written by a second epilogue.
+// Every product and partial sum is an exact integer, so the result has the
+// bits of the 1x1 conv run alone.
+template <int FC, int IPT, int GF, bool PROJ>
+__device__ __forceinline__ void tbn_conv_fused_body(const TbnGeom& g, const TbnConvArgs& a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x;
     const int nt = 64 * g.WV;
@@ -374,11 +390,20 @@ __global__ void __launch_bounds__(256) tbn_conv_fused_kernel(TbnGeom g, TbnConvA
         buffer_range(a.x + static_cast<int64_t>(n) * g.C * g.H * g.W, static_cast<uint64_t>(g.C) * HW4, 0);
     const i32x4_t* wp = reinterpret_cast<const i32x4_t*>(a.w4) + static_cast<int64_t>(mfc) * g.ksteps * 64 + lane;
 
-    f32x16_t acc[FC];
+    f32x16_t acc[FC], accp[PROJ ? FC : 1];
 #pragma unroll
     for (int j = 0; j < FC; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
+    if constexpr (PROJ) {
+#pragma unroll
+        for (int j = 0; j < FC; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) accp[j][e] = 0.0f;
+    }
+    // the projection's weight fragment of each chunk (one k-step per chunk)
+    const i32x4_t* wpp =
+        PROJ ? reinterpret_cast<const i32x4_t*>(a.proj_w4) + static_cast<int64_t>(mfc) * g.chunks * 64 + lane : nullptr;
 
     for (int chunk = 0; chunk < g.chunks; ++chunk) {
         // the weights of the chunk's first GF taps (taps past the end: zero)
@@ -388,6 +413,8 @@ __global__ void __launch_bounds__(256) tbn_conv_fused_kernel(TbnGeom g, TbnConvA
             const bool live = active && u < g.taps;
             wr[u] = live ? wp[(chunk * g.taps + u) * 64] : i32x4_t{0, 0, 0, 0};
         }
+        i32x4_t wpr = i32x4_t{0, 0, 0, 0};
+        if constexpr (PROJ) wpr = active ? wpp[chunk * 64] : i32x4_t{0, 0, 0, 0};
         // the patch: item i = (channel group cg, patch pixel), pixels fastest
         // so one load reads consecutive pixels of a channel row; channels
         // past C fall beyond the resource and read zero
@@ -440,6 +467,13 @@ __global__ void __launch_bounds__(256) tbn_conv_fused_kernel(TbnGeom g, TbnConvA
                     for (int j = 0; j < FC; ++j) bf[j] = *reinterpret_cast<const i32x4_t*>(lds + rec[j] + toff);
 #pragma unroll
                     for (int j = 0; j < FC; ++j) acc[j] = mfma_f4(wr[u], bf[j], acc[j]);
+                    if constexpr (PROJ) {
+                        // tap 4 = (1, 1), the centre: the projection's input pixel
+                        if (u == 4 && t0 == 0) {
+#pragma unroll
+                            for (int j = 0; j < FC; ++j) accp[j] = mfma_f4(wpr, bf[j], accp[j]);
+                        }
+                    }
                 }
             }
         }
@@ -491,6 +525,41 @@ __global__ void __launch_bounds__(256) tbn_conv_fused_kernel(TbnGeom g, TbnConvA
             __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), y_rs, voff[j] + roff, 0, 0);
         }
     }
+    if constexpr (PROJ) {
+        // the projection's epilogue (no residual, no pool: host-checked), its
+        // factors loaded here rather than held through the K loop
+        const __amdgpu_buffer_rsrc_t py_rs = buffer_range(a.proj_y + img, static_cast<uint64_t>(g.M) * plane4, 0);
+        const float* psp = a.proj_scale ? a.proj_scale : kUnitScale;
+        const float* pbp = a.proj_bias ? a.proj_bias : kNoBias;
+        const int psmask = a.proj_scale ? -1 : 0, pbmask = a.proj_bias ? -1 : 0;
+        const bool pbts = (a.proj_flags & TBN_EPI_BIAS_THEN_SCALE) != 0;
+        const bool prelu = (a.proj_flags & TBN_EPI_RELU) != 0;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int mc = min(h4 + 8 * (e >> 2) + (e & 3), g.M - 1);
+            const float mult = a.proj_alpha * psp[mc & psmask], bb = pbp[mc & pbmask];
+            const uint32_t roff = (8 * (e >> 2) + (e & 3)) * plane4;
+#pragma unroll
+            for (int j = 0; j < FC; ++j) {
+                float v = epilogue_value(accp[j][e], mult, bb, pbts, false, 0.0f);
+                if (prelu) v = v > 0.0f ? v : 0.0f;
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), py_rs, voff[j] + roff, 0, 0);
+            }
+        }
+    }
+}
+
+template <int FC, int IPT, int GF>
+__global__ void __launch_bounds__(256) tbn_conv_fused_kernel(TbnGeom g, TbnConvArgs a) {
+    tbn_conv_fused_body<FC, IPT, GF, false>(g, a);
+}
+
+// The pair (PROJ): held to two waves per SIMD, the non-pair kernel's
+// occupancy; its own register demand would leave one.  Only tiles of one
+// pixel fragment per wave take it (with more, the cap spills).
+template <int FC, int IPT>
+__global__ void __launch_bounds__(256, 2) tbn_conv_pair_kernel(TbnGeom g, TbnConvArgs a) {
+    tbn_conv_fused_body<FC, IPT, 9, true>(g, a);
 }
 
 // K = 8 output dwords (8 channels) per thread: conv-layout fp4 weights from
@@ -648,6 +717,12 @@ template <int FC, int IPT>
 void launch_fused_g(const TbnGeom& g, const TbnConvArgs& a, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(g.fused_blocks())), block(64 * g.WV);
     const size_t lds = static_cast<size_t>(g.PR) * g.PC * kRec;
+    if constexpr (FC == 1) {
+        if (a.proj_w4) {  // host-checked: pairs take one pixel fragment per wave
+            hipLaunchKernelGGL((tbn_conv_pair_kernel<1, IPT>), grid, block, lds, s, g, a);
+            return;
+        }
+    }
     if (g.GF == 1) hipLaunchKernelGGL((tbn_conv_fused_kernel<FC, IPT, 1>), grid, block, lds, s, g, a);
     else hipLaunchKernelGGL((tbn_conv_fused_kernel<FC, IPT, 9>), grid, block, lds, s, g, a);
 }
@@ -739,6 +814,41 @@ int tbn_hip_conv2d_tbn_prepacked(const float* x, const tbn_conv2d_desc* desc, co
     rc = run_tbn_conv(g, a, static_cast<uint8_t*>(ws), s);
     tbn_hip::release_workspace(ws, temporary, s);
     return rc;
+}
+
+int tbn_hip_conv2d_tbn_prepacked_pair(const float* x, const tbn_conv2d_desc* desc, const uint8_t* w4,
+                                      const float* scale, float alpha, const float* bias, const float* residual,
+                                      int flags, float lo, float hi, float* y, const uint8_t* proj_w4,
+                                      const float* proj_scale, float proj_alpha, const float* proj_bias,
+                                      int proj_flags, float* proj_y, int mode, tbn_stream_t stream) {
+    TBN_REQUIRE(mode == 0 || mode == 2, TBN_INVALID_ARGUMENT, "mode must be 0 (run) or 2 (query)");
+    constexpr int kFlags = TBN_EPI_RELU | TBN_EPI_BIAS_THEN_SCALE;
+    TBN_REQUIRE((flags & ~kFlags) == 0 && (proj_flags & ~kFlags) == 0, TBN_INVALID_ARGUMENT,
+                "a fused TBN pair takes ReLU and bias-then-scale epilogues only");
+    TBN_REQUIRE(desc != nullptr, TBN_INVALID_ARGUMENT, "null pointer");
+    if (desc->kh != 3 || desc->kw != 3 || desc->ph != 1 || desc->pw != 1 || desc->dh != 1 || desc->dw != 1 ||
+        desc->sh != desc->sw)
+        return tbn_hip::fail(TBN_NOT_IMPLEMENTED, "only a 3x3 pad-1 conv pairs with the 1x1 projection of its input");
+    TbnGeom g;
+    int rc = make_tbn_geom(desc, flags, g);
+    if (rc) return rc;
+    if (!g.fused)
+        return tbn_hip::fail(TBN_NOT_IMPLEMENTED, "a TBN conv on the two-pass kernels runs apart from its projection");
+    if (g.FC != 1)
+        return tbn_hip::fail(TBN_NOT_IMPLEMENTED, "a TBN conv tile of several pixel fragments runs apart from its projection");
+    if (mode == 2 || g.N == 0) return tbn_hip::ok();
+    TBN_REQUIRE(x && w4 && y && proj_w4 && proj_y, TBN_INVALID_ARGUMENT, "null pointer");
+    TBN_REQUIRE(reinterpret_cast<uintptr_t>(w4) % 16 == 0 && reinterpret_cast<uintptr_t>(proj_w4) % 16 == 0,
+                TBN_INVALID_ARGUMENT, "w4 and proj_w4 must be 16-byte aligned");
+    TBN_DEVICE_GUARD();
+    TbnConvArgs a{x, w4, y, scale, alpha, bias, residual, flags, lo, hi};
+    a.proj_w4 = proj_w4;
+    a.proj_y = proj_y;
+    a.proj_scale = proj_scale;
+    a.proj_alpha = proj_alpha;
+    a.proj_bias = proj_bias;
+    a.proj_flags = proj_flags;
+    return run_tbn_fused(g, a, tbn_hip::stream_of(stream));
 }
 
 int tbn_hip_conv2d_tbn_kernel_name(const tbn_conv2d_desc* desc, int flags, char* name, size_t len) {

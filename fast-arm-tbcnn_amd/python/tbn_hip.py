@@ -115,6 +115,8 @@ _SIGNATURES = {
     "tbn_hip_tbn_conv_scratch_bytes": ([ctypes.POINTER(ConvDesc), ctypes.POINTER(ctypes.c_int64)], _I32),
     "tbn_hip_conv2d_tbn_prepacked": ([_P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _F32, _F32, _P, _P,
                                       _P], _I32),
+    "tbn_hip_conv2d_tbn_prepacked_pair": ([_P, ctypes.POINTER(ConvDesc), _P, _P, _F32, _P, _P, _I32, _F32, _F32, _P,
+                                           _P, _P, _F32, _P, _I32, _P, _I32, _P], _I32),
     "tbn_hip_conv2d_tbn_kernel_name": ([ctypes.POINTER(ConvDesc), _I32, ctypes.c_char_p, ctypes.c_size_t], _I32),
     "tbn_hip_gemm_kernel_name": ([_I32, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_char_p, ctypes.c_size_t], _I32),
     "tbn_hip_conv_weights_bytes": ([_I32, ctypes.POINTER(ConvDesc), ctypes.POINTER(ctypes.c_int64)], _I32),

@@ -1087,8 +1087,9 @@ struct TBNModel::Session::Impl {
     // dilation 1, equal strides, one group, no pool, no run-time bias.
     bool pairable(const Op& op, int64_t k) const {
         const tbn_conv2d_desc& d = op.desc;
-        return !op.dead && !op.paired && op.kind == OpKind::ConvQuant && op.groups == 1 && !op.tbn && op.conv_w &&
-               op.pw && op.bias_value < 0 && d.kh == k && d.kw == k && d.ph == (k - 1) / 2 && d.pw == (k - 1) / 2 &&
+        const bool weights = op.tbn ? op.tbn_w != nullptr : (op.conv_w != nullptr && op.pw != nullptr);
+        return !op.dead && !op.paired && op.kind == OpKind::ConvQuant && op.groups == 1 && weights &&
+               op.bias_value < 0 && d.kh == k && d.kw == k && d.ph == (k - 1) / 2 && d.pw == (k - 1) / 2 &&
                d.dh == 1 && d.dw == 1 && d.sh == d.sw &&
                (op.flags & ~(TBN_EPI_RELU | TBN_EPI_BIAS_THEN_SCALE)) == 0;
     }
@@ -1096,10 +1097,11 @@ struct TBNModel::Session::Impl {
     // A ResNet downsampling block reads its input twice: the first 3x3 conv
     // (stride s, pad 1) and the 1x1 stride-s projection shortcut to the same
     // channel count.  When the library takes the pair
-    // (tbn_hip_conv2d_f32_prepacked_pair, mode 2) both run in the 3x3 conv's
-    // launch with the bits of the two launches; the projection's output is
-    // then written at the conv's position, which the memory plan takes as its
-    // definition.  Every reader of that output must come after the conv.
+    // (tbn_hip_conv2d_f32_prepacked_pair, or tbn_hip_conv2d_tbn_prepacked_pair
+    // in TBN arithmetic, mode 2) both run in the 3x3 conv's launch with the
+    // bits of the two launches; the projection's output is then written at
+    // the conv's position, which the memory plan takes as its definition.
+    // Every reader of that output must come after the conv.
     void pair_projections() {
         for (size_t a = 0; a < ops.size(); ++a) {
             Op& conv = ops[a];
@@ -1107,16 +1109,22 @@ struct TBNModel::Session::Impl {
             for (size_t p = 0; p < ops.size(); ++p) {
                 Op& proj = ops[p];
                 if (p == a || !pairable(proj, 1) || proj.residual >= 0 || proj.in[0] != conv.in[0] ||
-                    proj.desc.m != conv.desc.m || proj.desc.sh != conv.desc.sh ||
-                    weights_kind(proj) != weights_kind(conv))
+                    proj.desc.m != conv.desc.m || proj.desc.sh != conv.desc.sh || proj.tbn != conv.tbn ||
+                    (!conv.tbn && weights_kind(proj) != weights_kind(conv)))
                     continue;
                 bool later = true;
                 for (int r : readers(proj.out))
                     if (r <= static_cast<int>(a)) later = false;
                 if (!later || is_output(proj.out)) continue;
-                if (tbn_hip_conv2d_f32_prepacked_pair(weights_kind(conv), nullptr, &conv.desc, nullptr, nullptr, 1.0f,
-                                                      nullptr, nullptr, conv.flags, nullptr, nullptr, nullptr, 1.0f,
-                                                      nullptr, proj.flags, nullptr, 2, nullptr) != TBN_SUCCESS) {
+                const int rc =
+                    conv.tbn ? tbn_hip_conv2d_tbn_prepacked_pair(nullptr, &conv.desc, nullptr, nullptr, 1.0f, nullptr,
+                                                                 nullptr, conv.flags, -0.1f, 0.1f, nullptr, nullptr,
+                                                                 nullptr, 1.0f, nullptr, proj.flags, nullptr, 2, nullptr)
+                             : tbn_hip_conv2d_f32_prepacked_pair(weights_kind(conv), nullptr, &conv.desc, nullptr,
+                                                                 nullptr, 1.0f, nullptr, nullptr, conv.flags, nullptr,
+                                                                 nullptr, nullptr, 1.0f, nullptr, proj.flags, nullptr,
+                                                                 2, nullptr);
+                if (rc != TBN_SUCCESS) {
                     (void)tbn_hip_last_error();  // not taken: the two convs run apart
                     continue;
                 }
@@ -1333,6 +1341,17 @@ struct TBNModel::Session::Impl {
                 return;
             case OpKind::ConvQuant:
                 if (op.groups > 1) return launch_grouped(op, s, what);
+                if (op.tbn && op.paired) return;  // written by its pair's launch
+                if (op.tbn && op.pair >= 0) {
+                    const Op& pr = ops[op.pair];
+                    check_status(tbn_hip_conv2d_tbn_prepacked_pair(
+                                     fp(op.in[0]), &op.desc, op.tbn_w->typed_data<uint8_t>(), op.scale, 1.0f,
+                                     bias_of(op), op.residual >= 0 ? fp(op.residual) : nullptr, op.flags, -0.1f, 0.1f,
+                                     fp(op.out), pr.tbn_w->typed_data<uint8_t>(), pr.scale, 1.0f, bias_of(pr),
+                                     pr.flags, fp(pr.out), 0, s),
+                                 (what + " with '" + pr.node + "'").c_str());
+                    return;
+                }
                 if (op.tbn) {
                     check_status(tbn_hip_conv2d_tbn_prepacked(fp(op.in[0]), &op.desc, op.tbn_w->typed_data<uint8_t>(),
                                                               op.scale, 1.0f, bias_of(op),

@@ -558,6 +558,24 @@ int tbn_hip_conv2d_tbn_prepacked(const float* x, const tbn_conv2d_desc* desc, co
                                  const float* scale, float alpha, const float* bias, const float* residual,
                                  int flags, float lo, float hi, uint8_t* scratch, float* y,
                                  tbn_stream_t stream);
+/* No counterpart in the reference, which runs the two Conv2D layers of a
+ * ResNet downsampling block one after the other (model.hpp:482-557 each).
+ * One launch computes both tbn_hip_conv2d_tbn_prepacked for desc (3x3, pad
+ * 1, stride s in both directions, dilation 1; flags TBN_EPI_RELU /
+ * TBN_EPI_BIAS_THEN_SCALE; optional residual) and the 1x1 pad-0 stride-s TBN
+ * conv of the same x, ternarized at the same (lo, hi), to the same desc->m
+ * channels (proj_w4 packed for that 1x1 desc, its own scale, alpha, bias and
+ * flags, no residual; proj_y has y's shape).  Every product and sum is an
+ * exact integer, so both outputs have the bits of the two separate calls.
+ * mode: 0 runs, 2 only checks that this geometry pairs (no pointer read).
+ * Returns TBN_NOT_IMPLEMENTED when it does not (another kernel size or
+ * padding, a geometry on the two-pass kernels, or a tile of several pixel
+ * fragments): the caller then makes the two calls.  Allocates nothing. */
+int tbn_hip_conv2d_tbn_prepacked_pair(const float* x, const tbn_conv2d_desc* desc, const uint8_t* w4,
+                                      const float* scale, float alpha, const float* bias, const float* residual,
+                                      int flags, float lo, float hi, float* y, const uint8_t* proj_w4,
+                                      const float* proj_scale, float proj_alpha, const float* proj_bias,
+                                      int proj_flags, float* proj_y, int mode, tbn_stream_t stream);
 /* No counterpart in the reference (a diagnostic for profiling): the conv
  * kernel tbn_hip_conv2d_tbn_prepacked runs for desc and flags, as a profiler
  * names it.  No GPU work. */

@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 import models
+import tbn_hip
 import onnx_proto as op
 import refmath as rm
 
@@ -126,8 +127,19 @@ def _resnet_tbn(tbn, orc, batch, check_oracle):
 
 def test_resnet18_tbn_batch2_bit_exact(dev, tbn, orc):
     s, outs = _resnet_tbn(tbn, orc, 2, True)
-    # stem(+relu+pool), 16 binary convs with relu or residual fused, 3 projections, gap, fc
-    assert s.planned_launches() == 1 + 16 + 3 + 1 + 1
+    # stem(+relu+pool), 16 binary convs with relu or residual fused, 3 projections, gap, fc; a projection
+    # runs in its block's first conv's launch where the library takes the pair
+    fused = 0
+    for c, hw in ((64, 56), (128, 28), (256, 14)):
+        d = tbn_hip.conv_desc(2, c, hw, hw, 2 * c, 3, 3, 2, 2, 1, 1)
+        try:
+            tbn_hip.call("tbn_hip_conv2d_tbn_prepacked_pair", None, d, None, None, 1.0, None, None, tbn_hip.EPI_RELU,
+                         -0.1, 0.1, None, None, None, 1.0, None, 0, None, 2, None)
+            fused += 1
+        except tbn_hip.TbnError as e:
+            assert e.code == tbn_hip.NOT_IMPLEMENTED
+    assert fused >= 1
+    assert s.planned_launches() == 1 + 16 + 3 + 1 + 1 - fused
 
 
 def test_resnet18_tbn_batch32_batch_invariant(dev, tbn):

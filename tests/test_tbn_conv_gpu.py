@@ -156,3 +156,67 @@ def test_tbn_conv_error_codes(dev):
         tbn_hip.call("tbn_hip_conv2d_tbn_prepacked", P(x), ctypes.byref(d), P(buf), None, 1.0, None, P(y),
                      RELU | POOL, -0.1, 0.1, P(buf), P(y), None)
     assert e.value.code == tbn_hip.INVALID_ARGUMENT
+
+
+TBN_PAIR_CASES = [
+    # N, C, H, W, M, stride, flags, proj_flags, residual
+    (4, 64, 56, 56, 128, 2, RELU, 0, False),        # ResNet stage 2's downsampling block
+    (2, 128, 28, 28, 256, 2, RELU | BTS, BTS, True),  # two chunks, bias-then-scale, residual on the conv
+    (3, 300, 9, 8, 40, 2, 0, RELU, False),          # ragged last chunk and M
+    (2, 96, 15, 13, 80, 1, RELU, RELU, True),       # stride 1
+]
+
+
+@pytest.mark.parametrize("case", TBN_PAIR_CASES, ids=["stage2", "bts_res", "ragged", "stride1"])
+def test_tbn_conv_pair_matches_separate_convs(dev, case):
+    """A 3x3 pad-1 TBN conv and the 1x1 TBN projection of its input in one
+    launch (tbn_hip_conv2d_tbn_prepacked_pair) give the bits of the two
+    separate calls: every product and sum is an exact integer."""
+    N, C, H, W, M, st, flags, pflags, with_res = case
+    rng = np.random.default_rng(N + C + M + st)
+    x = to_dev(threshold_input(rng, (N, C, H, W)))
+    d3 = tbn_hip.conv_desc(N, C, H, W, M, 3, 3, st, st, 1, 1)
+    d1 = tbn_hip.conv_desc(N, C, H, W, M, 1, 1, st, st, 0, 0)
+    OH, OW = tbn_hip.conv_out_hw(d3)
+    assert (OH, OW) == tbn_hip.conv_out_hw(d1)
+    w3 = pack_tbn_conv((rng.random((M, C, 3, 3)) < 0.5).astype(np.uint8), d3)
+    w1 = pack_tbn_conv((rng.random((M, C, 1, 1)) < 0.5).astype(np.uint8), d1)
+    s3 = to_dev(rng.uniform(0.5, 1.5, M).astype(np.float32))
+    b3 = to_dev(rng.standard_normal(M).astype(np.float32))
+    s1 = to_dev(rng.uniform(0.5, 1.5, M).astype(np.float32))
+    b1 = to_dev(rng.standard_normal(M).astype(np.float32))
+    res = to_dev(rng.standard_normal((N, M, OH, OW)).astype(np.float32)) if with_res else None
+    want_y = run_tbn_conv(x, d3, w3, s3, b3, res, flags, (N, M, OH, OW))
+    want_p = run_tbn_conv(x, d1, w1, s1, b1, None, pflags, (N, M, OH, OW))
+    tbn_hip.call("tbn_hip_conv2d_tbn_prepacked_pair", None, ctypes.byref(d3), None, None, 1.0, None, None, flags,
+                 tbn_ref.LO, tbn_ref.HI, None, None, None, 1.0, None, pflags, None, 2, None)  # pairs: no pointer read
+    y, py = empty((N, M, OH, OW), torch.float32), empty((N, M, OH, OW), torch.float32)
+    y.fill_(np.nan)
+    py.fill_(np.nan)
+    tbn_hip.call("tbn_hip_conv2d_tbn_prepacked_pair", P(x), ctypes.byref(d3), P(w3), P(s3), 1.0, P(b3), P(res),
+                 flags, tbn_ref.LO, tbn_ref.HI, P(y), P(w1), P(s1), 1.0, P(b1), pflags, P(py), 0, None)
+    assert np.array_equal(host(y).view(np.uint32), want_y.view(np.uint32))
+    assert np.array_equal(host(py).view(np.uint32), want_p.view(np.uint32))
+
+
+def test_tbn_conv_pair_declines(dev):
+    """Another kernel size or padding, a tile of two pixel fragments per wave
+    (ResNet's stride-1 stage-1 conv at batch 32), and a geometry forced onto
+    the two-pass kernels return TBN_NOT_IMPLEMENTED without work; a pooled
+    epilogue is an invalid request."""
+    d = tbn_hip.conv_desc(2, 64, 16, 16, 64, 3, 3, 2, 2, 1, 1)
+    for dd in (tbn_hip.conv_desc(2, 64, 16, 16, 64, 5, 5, 1, 1, 2, 2), tbn_hip.conv_desc(2, 64, 16, 16, 64, 3, 3, 1, 1, 0, 0),
+               tbn_hip.conv_desc(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1)):
+        with pytest.raises(tbn_hip.TbnError) as e:
+            tbn_hip.call("tbn_hip_conv2d_tbn_prepacked_pair", None, ctypes.byref(dd), None, None, 1.0, None, None, 0,
+                         tbn_ref.LO, tbn_ref.HI, None, None, None, 1.0, None, 0, None, 2, None)
+        assert e.value.code == tbn_hip.NOT_IMPLEMENTED
+    with tbn_hip.tuning(tbn_hip.TUNE_TBN_CONV, 2):
+        with pytest.raises(tbn_hip.TbnError) as e:
+            tbn_hip.call("tbn_hip_conv2d_tbn_prepacked_pair", None, ctypes.byref(d), None, None, 1.0, None, None, 0,
+                         tbn_ref.LO, tbn_ref.HI, None, None, None, 1.0, None, 0, None, 2, None)
+        assert e.value.code == tbn_hip.NOT_IMPLEMENTED
+    with pytest.raises(tbn_hip.TbnError) as e:
+        tbn_hip.call("tbn_hip_conv2d_tbn_prepacked_pair", None, ctypes.byref(d), None, None, 1.0, None, None,
+                     RELU | POOL, tbn_ref.LO, tbn_ref.HI, None, None, None, 1.0, None, 0, None, 2, None)
+    assert e.value.code == tbn_hip.INVALID_ARGUMENT
