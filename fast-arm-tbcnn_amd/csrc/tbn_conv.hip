@@ -549,8 +549,11 @@ __device__ __forceinline__ void tbn_conv_fused_body(const TbnGeom& g, const TbnC
     }
 }
 
+// Tiles of one pixel fragment with at most four staged items per thread
+// fit three waves per SIMD without spills (asked for explicitly: left alone
+// the compiler allocates for two); the rest keep the compiler's choice.
 template <int FC, int IPT, int GF>
-__global__ void __launch_bounds__(256) tbn_conv_fused_kernel(TbnGeom g, TbnConvArgs a) {
+__global__ void __launch_bounds__(256, (FC == 1 && IPT <= 4) ? 3 : 1) tbn_conv_fused_kernel(TbnGeom g, TbnConvArgs a) {
     tbn_conv_fused_body<FC, IPT, GF, false>(g, a);
 }
 
