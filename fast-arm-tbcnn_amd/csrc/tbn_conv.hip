@@ -549,17 +549,16 @@ __device__ __forceinline__ void tbn_conv_fused_body(const TbnGeom& g, const TbnC
     }
 }
 
-// Tiles of one pixel fragment with at most four staged items per thread
-// fit three waves per SIMD without spills (asked for explicitly: left alone
-// the compiler allocates for two); the rest keep the compiler's choice.
+// Tiles with at most four staged items per thread fit three waves per SIMD
+// without spills (asked for explicitly: left alone the compiler allocates
+// for two); eight items keep the compiler's choice.
 template <int FC, int IPT, int GF>
 __global__ void __launch_bounds__(256, (FC == 1 && IPT <= 4) ? 3 : 1) tbn_conv_fused_kernel(TbnGeom g, TbnConvArgs a) {
     tbn_conv_fused_body<FC, IPT, GF, false>(g, a);
 }
 
 // The pair (PROJ): held to two waves per SIMD, the non-pair kernel's
-// occupancy; its own register demand would leave one.  Only tiles of one
-// pixel fragment per wave take it (with more, the cap spills).
+// occupancy; its own register demand would leave one.
 template <int FC, int IPT>
 __global__ void __launch_bounds__(256, 2) tbn_conv_pair_kernel(TbnGeom g, TbnConvArgs a) {
     tbn_conv_fused_body<FC, IPT, 9, true>(g, a);
@@ -650,9 +649,13 @@ int make_tbn_geom(const tbn_conv2d_desc* d, int flags, TbnGeom& g) {
     TBN_REQUIRE((g.waves() + 3) / 4 < (1LL << 31), TBN_INVALID_SHAPE, "TBN conv: grid too large");
 
     // fused tile: staged pixels per thread bounded (IPT <= 8 items of 8
-    // channels), at most 4 pixel fragments; the score is the share of useful
-    // MFMA columns weighed by how well the grid fills the chip (512 blocks)
-    // and by the patch pixels staged per output pixel (the halo)
+    // channels), one pixel fragment (32 output pixels); the score is the
+    // share of useful MFMA columns weighed by how well the grid fills the
+    // chip (512 blocks) and by the patch pixels staged per output pixel (the
+    // halo).  Tiles of two to four fragments stage less halo per pixel, but
+    // hold more staging registers and run fewer waves per SIMD: measured
+    // slower on ResNet-18's stage-1 and stage-2 convs (26.6 -> 25.0 us and
+    // 20.2 -> 17.3 us with one fragment), so they are not offered.
     const int rows = g.pool ? 2 * g.YH : g.OH, cols = g.pool ? 2 * g.YW : g.OW;
     double best_score = -1.0;
     g.fused = 0;
@@ -662,7 +665,7 @@ int make_tbn_geom(const tbn_conv2d_desc* d, int flags, TbnGeom& g) {
             const int TC = g.pool ? (tc + 1) / 2 * 2 : tc;
             for (int tr = g.pool ? 2 : 1; tr <= rows; tr += g.pool ? 2 : 1) {
                 const int px = tr * TC;
-                if (px > 128) break;
+                if (px > 32) break;
                 const int PR = (tr - 1) * g.sh + (g.kh - 1) * g.dh + 1;
                 const int PC = (TC - 1) * g.sw + (g.kw - 1) * g.dw + 1;
                 if (static_cast<int64_t>(PR) * PC * 8 > 8LL * 64 * wv) break;
@@ -688,7 +691,6 @@ int make_tbn_geom(const tbn_conv2d_desc* d, int flags, TbnGeom& g) {
         const int ipt = (g.PR * g.PC * 8 + 64 * g.WV - 1) / (64 * g.WV);
         g.IPT = ipt <= 2 ? 2 : (ipt <= 4 ? 4 : 8);
         g.GF = g.taps == 1 ? 1 : 9;
-        g.FC = g.FC == 3 ? 4 : g.FC;
         const int variant = tbn_hip::tuning(TBN_TUNE_TBN_CONV);
         if (variant == 2 || g.fused_blocks() >= (1LL << 31) || d->c * d->h * d->w * 4 >= (1LL << 31) ||
             (d->c + 64 + 8) * d->h * d->w * 4 >= (1LL << 32) ||
@@ -716,31 +718,21 @@ void launch_conv_g(const TbnGeom& g, const TbnConvArgs& a, const uint8_t* xt, hi
     }
 }
 
-template <int FC, int IPT>
+// Tiles of one pixel fragment (make_tbn_geom), so FC = 1.
+template <int IPT>
 void launch_fused_g(const TbnGeom& g, const TbnConvArgs& a, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>(g.fused_blocks())), block(64 * g.WV);
     const size_t lds = static_cast<size_t>(g.PR) * g.PC * kRec;
-    if constexpr (FC == 1) {
-        if (a.proj_w4) {  // host-checked: pairs take one pixel fragment per wave
-            hipLaunchKernelGGL((tbn_conv_pair_kernel<1, IPT>), grid, block, lds, s, g, a);
-            return;
-        }
-    }
-    if (g.GF == 1) hipLaunchKernelGGL((tbn_conv_fused_kernel<FC, IPT, 1>), grid, block, lds, s, g, a);
-    else hipLaunchKernelGGL((tbn_conv_fused_kernel<FC, IPT, 9>), grid, block, lds, s, g, a);
-}
-
-template <int FC>
-void launch_fused_i(const TbnGeom& g, const TbnConvArgs& a, hipStream_t s) {
-    if (g.IPT == 2) launch_fused_g<FC, 2>(g, a, s);
-    else if (g.IPT == 4) launch_fused_g<FC, 4>(g, a, s);
-    else launch_fused_g<FC, 8>(g, a, s);
+    if (a.proj_w4) hipLaunchKernelGGL((tbn_conv_pair_kernel<1, IPT>), grid, block, lds, s, g, a);
+    else if (g.GF == 1) hipLaunchKernelGGL((tbn_conv_fused_kernel<1, IPT, 1>), grid, block, lds, s, g, a);
+    else hipLaunchKernelGGL((tbn_conv_fused_kernel<1, IPT, 9>), grid, block, lds, s, g, a);
 }
 
 int run_tbn_fused(const TbnGeom& g, const TbnConvArgs& a, hipStream_t s) {
-    if (g.FC == 1) launch_fused_i<1>(g, a, s);
-    else if (g.FC == 2) launch_fused_i<2>(g, a, s);
-    else launch_fused_i<4>(g, a, s);
+    TBN_REQUIRE(g.FC == 1, TBN_INVALID_SHAPE, "TBN conv tiles hold one pixel fragment");
+    if (g.IPT == 2) launch_fused_g<2>(g, a, s);
+    else if (g.IPT == 4) launch_fused_g<4>(g, a, s);
+    else launch_fused_g<8>(g, a, s);
     return tbn_hip::check_launch("conv2d_tbn (fused)");
 }
 
@@ -837,8 +829,6 @@ int tbn_hip_conv2d_tbn_prepacked_pair(const float* x, const tbn_conv2d_desc* des
     if (rc) return rc;
     if (!g.fused)
         return tbn_hip::fail(TBN_NOT_IMPLEMENTED, "a TBN conv on the two-pass kernels runs apart from its projection");
-    if (g.FC != 1)
-        return tbn_hip::fail(TBN_NOT_IMPLEMENTED, "a TBN conv tile of several pixel fragments runs apart from its projection");
     if (mode == 2 || g.N == 0) return tbn_hip::ok();
     TBN_REQUIRE(x && w4 && y && proj_w4 && proj_y, TBN_INVALID_ARGUMENT, "null pointer");
     TBN_REQUIRE(reinterpret_cast<uintptr_t>(w4) % 16 == 0 && reinterpret_cast<uintptr_t>(proj_w4) % 16 == 0,

@@ -569,8 +569,8 @@ int tbn_hip_conv2d_tbn_prepacked(const float* x, const tbn_conv2d_desc* desc, co
  * exact integer, so both outputs have the bits of the two separate calls.
  * mode: 0 runs, 2 only checks that this geometry pairs (no pointer read).
  * Returns TBN_NOT_IMPLEMENTED when it does not (another kernel size or
- * padding, a geometry on the two-pass kernels, or a tile of several pixel
- * fragments): the caller then makes the two calls.  Allocates nothing. */
+ * padding, or a geometry on the two-pass kernels): the caller then makes
+ * the two calls.  Allocates nothing. */
 int tbn_hip_conv2d_tbn_prepacked_pair(const float* x, const tbn_conv2d_desc* desc, const uint8_t* w4,
                                       const float* scale, float alpha, const float* bias, const float* residual,
                                       int flags, float lo, float hi, float* y, const uint8_t* proj_w4,

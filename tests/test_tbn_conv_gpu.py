@@ -200,13 +200,11 @@ def test_tbn_conv_pair_matches_separate_convs(dev, case):
 
 
 def test_tbn_conv_pair_declines(dev):
-    """Another kernel size or padding, a tile of two pixel fragments per wave
-    (ResNet's stride-1 stage-1 conv at batch 32), and a geometry forced onto
-    the two-pass kernels return TBN_NOT_IMPLEMENTED without work; a pooled
-    epilogue is an invalid request."""
+    """Another kernel size or padding, and a geometry forced onto the two-pass
+    kernels, return TBN_NOT_IMPLEMENTED without work; a pooled epilogue is an
+    invalid request."""
     d = tbn_hip.conv_desc(2, 64, 16, 16, 64, 3, 3, 2, 2, 1, 1)
-    for dd in (tbn_hip.conv_desc(2, 64, 16, 16, 64, 5, 5, 1, 1, 2, 2), tbn_hip.conv_desc(2, 64, 16, 16, 64, 3, 3, 1, 1, 0, 0),
-               tbn_hip.conv_desc(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1)):
+    for dd in (tbn_hip.conv_desc(2, 64, 16, 16, 64, 5, 5, 1, 1, 2, 2), tbn_hip.conv_desc(2, 64, 16, 16, 64, 3, 3, 1, 1, 0, 0)):
         with pytest.raises(tbn_hip.TbnError) as e:
             tbn_hip.call("tbn_hip_conv2d_tbn_prepacked_pair", None, ctypes.byref(dd), None, None, 1.0, None, None, 0,
                          tbn_ref.LO, tbn_ref.HI, None, None, None, 1.0, None, 0, None, 2, None)
