@@ -95,3 +95,31 @@ def test_fused_stem_pool_shape_rule():
         assert lib.tbn_hip_conv2d_f32_supported(ctypes.byref(d), pool) == tbn_hip.NOT_IMPLEMENTED
         assert "stem shape" in tbn_hip.last_error()
     assert lib.tbn_hip_conv2d_f32_supported(ctypes.byref(stem), 16) == tbn_hip.INVALID_ARGUMENT
+
+
+def test_tbn_conv_tiles_and_pair_query_are_host_only():
+    """TBN conv tiles hold one pixel fragment (the kernel name's first
+    argument), and the pair query (mode 2) answers without a GPU: ResNet-18's
+    stride-2 downsampling convs pair at batch 2 and 32; a 5x5 conv, a pad-0
+    3x3 conv and a geometry forced onto the two-pass kernels do not; a pooled
+    epilogue is rejected."""
+    lib = tbn_hip.lib()
+    buf = ctypes.create_string_buffer(160)
+    for d in (tbn_hip.conv_desc(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1), tbn_hip.conv_desc(32, 512, 7, 7, 512, 3, 3, 1, 1, 1, 1),
+              tbn_hip.conv_desc(1, 1, 28, 28, 6, 5, 5), tbn_hip.conv_desc(64, 64, 14, 14, 128, 3, 3, 1, 1, 1, 1)):
+        assert lib.tbn_hip_conv2d_tbn_kernel_name(ctypes.byref(d), tbn_hip.EPI_RELU, buf, len(buf)) == 0
+        assert buf.value.decode().startswith("tbn_conv_fused_kernel<1, "), buf.value.decode()
+
+    def pair(d, flags=tbn_hip.EPI_RELU):
+        return lib.tbn_hip_conv2d_tbn_prepacked_pair(None, ctypes.byref(d), None, None, ctypes.c_float(1.0), None, None,
+                                                     flags, ctypes.c_float(-0.1), ctypes.c_float(0.1), None, None, None,
+                                                     ctypes.c_float(1.0), None, 0, None, 2, None)
+    for n in (2, 32):
+        for c, hw in ((64, 56), (128, 28), (256, 14)):
+            assert pair(tbn_hip.conv_desc(n, c, hw, hw, 2 * c, 3, 3, 2, 2, 1, 1)) == 0, (n, c)
+    assert pair(tbn_hip.conv_desc(2, 64, 16, 16, 64, 5, 5, 1, 1, 2, 2)) == tbn_hip.NOT_IMPLEMENTED
+    assert pair(tbn_hip.conv_desc(2, 64, 16, 16, 64, 3, 3, 1, 1, 0, 0)) == tbn_hip.NOT_IMPLEMENTED
+    with tbn_hip.tuning(tbn_hip.TUNE_TBN_CONV, 2):
+        assert pair(tbn_hip.conv_desc(2, 64, 16, 16, 64, 3, 3, 2, 2, 1, 1)) == tbn_hip.NOT_IMPLEMENTED
+    assert pair(tbn_hip.conv_desc(2, 64, 16, 16, 64, 3, 3, 1, 1, 1, 1),
+                tbn_hip.EPI_RELU | tbn_hip.EPI_MAXPOOL2X2) == tbn_hip.INVALID_ARGUMENT
